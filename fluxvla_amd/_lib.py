@@ -1,0 +1,145 @@
+"""ctypes binding of libfluxvla_amd.so (the C ABI in include/fluxvla_amd.h).
+
+The library is loaded from the package directory.  There is no fallback: if
+the shared object is missing or a symbol is absent, importing the kernels
+raises, so nothing can silently run a CPU path in its place.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, 'libfluxvla_amd.so')
+
+c_i64 = ctypes.c_int64
+c_i32 = ctypes.c_int32
+c_f32 = ctypes.c_float
+c_vp = ctypes.c_void_p
+
+FVX_OK = 0
+FVX_ERR_NULL = -1
+FVX_ERR_SHAPE = -2
+FVX_ERR_ALIGN = -3
+FVX_ERR_LAUNCH = -4
+FVX_ERR_ARG = -5
+FVX_ERR_WORKSPACE = -6
+
+GEMM_PLAIN, GEMM_GEGLU, GEMM_QKV_ROPE, GEMM_EULER = 0, 1, 2, 3
+ACT_NONE, ACT_SILU, ACT_GELU_TANH = 0, 1, 2
+
+
+class GemmDesc(ctypes.Structure):
+    """Mirror of ``fvx_gemm_desc``."""
+    _fields_ = [
+        ('a', c_vp), ('lda', c_i64),
+        ('b', c_vp), ('ldb', c_i64),
+        ('b2', c_vp),
+        ('c', c_vp), ('ldc', c_i64),
+        ('m', c_i64), ('n', c_i64), ('k', c_i64),
+        ('bias', c_vp),
+        ('bias_f32', c_vp),
+        ('residual', c_vp), ('ldr', c_i64),
+        ('gate', c_vp), ('ldg', c_i64), ('gate_group', c_i64),
+        ('pos', c_vp), ('ldp', c_i64), ('pos_period', c_i64),
+        ('act', c_i32),
+        ('mode', c_i32),
+        ('rownorm', c_i32),
+        ('out_f32', c_i32),
+        ('rownorm_eps', c_f32),
+        ('dt', c_f32),
+        ('row_group', c_i64), ('row_group_stride', c_i64),
+        ('rope', c_vp),
+        ('positions', c_vp),
+        ('q_out', c_vp), ('ldq', c_i64),
+        ('k_out', c_vp), ('ldk', c_i64),
+        ('v_out', c_vp), ('ldv', c_i64),
+        ('n_q_heads', c_i32), ('head_dim', c_i32),
+        ('xt', c_vp), ('ldx', c_i64),
+        ('xt_bf16', c_vp), ('ldxb', c_i64),
+        ('workspace', c_vp), ('workspace_bytes', c_i64),
+        ('split_k', c_i32),
+        ('reserved', c_i32),
+    ]
+
+
+class AttnDesc(ctypes.Structure):
+    """Mirror of ``fvx_attn_desc``."""
+    _fields_ = [
+        ('q', c_vp), ('q_tok_stride', c_i64), ('q_head_stride', c_i64),
+        ('q_zs1', c_i64), ('q_zs2', c_i64),
+        ('k', c_vp), ('k_tok_stride', c_i64), ('k_zs1', c_i64),
+        ('k_zs2', c_i64),
+        ('v', c_vp), ('v_tok_stride', c_i64), ('v_zs1', c_i64),
+        ('v_zs2', c_i64),
+        ('o', c_vp), ('o_tok_stride', c_i64), ('o_head_stride', c_i64),
+        ('o_zs1', c_i64), ('o_zs2', c_i64),
+        ('kgrp', c_vp), ('kgrp_zs1', c_i64),
+        ('qgrp', c_vp), ('qgrp_zs1', c_i64),
+        ('sq', c_i64), ('sk', c_i64), ('heads', c_i64), ('head_dim', c_i64),
+        ('n_problems', c_i64), ('zdiv', c_i64),
+        ('scale', c_f32),
+        ('kv_splits', c_i32),
+        ('workspace', c_vp), ('workspace_bytes', c_i64),
+    ]
+
+
+# name -> (restype, argtypes); the exact set declared by include/fluxvla_amd.h
+SIGNATURES = {
+    'fvx_version': (c_i32, []),
+    'fvx_last_error': (ctypes.c_char_p, []),
+    'fvx_gemm_workspace_bytes': (c_i64, [ctypes.POINTER(GemmDesc)]),
+    'fvx_gemm': (c_i32, [ctypes.POINTER(GemmDesc), c_vp]),
+    'fvx_rms_norm_residual':
+    (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
+    'fvx_layer_norm': (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32,
+                               c_vp]),
+    'fvx_adarms_norm': (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+                                c_i64, c_f32, c_vp]),
+    'fvx_attention_workspace_bytes': (c_i64, [ctypes.POINTER(AttnDesc)]),
+    'fvx_attention': (c_i32, [ctypes.POINTER(AttnDesc), c_vp]),
+    'fvx_im2col_patches': (c_i32, [c_vp, c_i32, c_vp, c_i64, c_i64, c_i64,
+                                   c_i64, c_i64, c_f32, c_f32, c_vp]),
+    'fvx_embed_tokens': (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_f32,
+                                 c_i64, c_i64, c_vp]),
+    'fvx_copy_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64,
+                              c_i64, c_vp]),
+}
+
+_lib = None
+
+
+class FvxError(RuntimeError):
+    """A C-ABI entry point returned a non-zero fvx_status."""
+
+    def __init__(self, name, code, message):
+        super().__init__(f'{name} failed (status {code}): {message}')
+        self.code = code
+
+
+def load():
+    """Load the shared library (once) and bind every declared symbol."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f'{LIB_PATH} is not built; run `python -c "import '
+            '__graft_entry__ as g; g.build()"` (hipcc, gfx950) first')
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if the export is missing
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def call(name, *args):
+    """Call entry point ``name``; raise FvxError on a non-zero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != FVX_OK:
+        msg = lib.fvx_last_error().decode(errors='replace')
+        if rc in (FVX_ERR_SHAPE, FVX_ERR_ARG, FVX_ERR_NULL, FVX_ERR_ALIGN):
+            raise ValueError(f'{name}: {msg} (status {rc})')
+        raise FvxError(name, rc, msg)
+    return rc

@@ -1,0 +1,102 @@
+// Shared device helpers for the gfx950 kernels of libfluxvla_amd.
+//
+// Storage type for bf16 is a raw uint16_t; arithmetic is always fp32.
+// Conversions use round-to-nearest-even (the same rounding torch uses when it
+// casts fp32 -> bf16), so a kernel that rounds at the same point as the
+// reference's PyTorch path produces the same bits there.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fvx {
+
+typedef uint16_t bf16_t;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf2f(bf16_t v) {
+  return __uint_as_float(((uint32_t)v) << 16);
+}
+
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  // Round to nearest even; NaN stays NaN (quiet bit forced).
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+// 8 packed bf16 values (one 16-byte vector).
+struct __align__(16) bf16x8 {
+  uint32_t w[4];
+};
+
+__device__ __forceinline__ void unpack8(const bf16x8& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(v.w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(v.w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float* f) {
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    v.w[i] = (uint32_t)f2bf(f[2 * i]) | ((uint32_t)f2bf(f[2 * i + 1]) << 16);
+  return v;
+}
+
+__device__ __forceinline__ bf16x8 ld8(const bf16_t* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+__device__ __forceinline__ void st8(bf16_t* p, const bf16x8& v) {
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 v;
+  v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;
+  return v;
+}
+
+__device__ __forceinline__ bf16x8_t as_mfma(const bf16x8& v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// D(16x16, fp32) += A(16x32) * B(32x16), bf16 inputs.
+// Lane l supplies A row (l % 16) and B column (l % 16), each with 8 k-values
+// of the k-group (l / 16). D lane l holds column (l % 16), rows 4*(l/16)+j.
+__device__ __forceinline__ f32x4_t mfma16x16x32(const bf16x8& a,
+                                                const bf16x8& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_mfma(a), as_mfma(b), c, 0,
+                                                 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), written through the
+  // identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)).
+  const float k2 = 1.5957691216057308f;  // 2 * sqrt(2 / pi)
+  float u = k2 * (x + 0.044715f * x * x * x);
+  return x / (1.0f + __expf(-u));
+}
+
+__device__ __forceinline__ float silu(float x) {
+  return x / (1.0f + __expf(-x));
+}
+
+}  // namespace fvx

@@ -1,0 +1,255 @@
+// Row normalizations: fused residual + RMSNorm, LayerNorm, adaptive RMSNorm.
+//
+// Layout: one 64-lane wavefront per row, 4 rows per 256-thread workgroup.
+// Each lane moves 16-byte vectors (8 bf16) with a stride of 64 vectors, so a
+// wavefront reads 1 KiB contiguous per instruction; the row is held in fp32
+// registers between the reduction and the write, so HBM sees each input byte
+// once and each output byte once.  Reductions are wavefront shuffles only.
+#include "capi_util.h"
+#include "common.h"
+
+namespace fvx {
+
+constexpr int kRowsPerBlock = 4;
+constexpr int kMaxVec = 8;  // up to 64 lanes * 8 vectors * 8 = 4096 columns
+
+template <int NV>
+__global__ __launch_bounds__(256) void rms_norm_residual_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ res,
+    const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
+    bf16_t* __restrict__ res_out, int64_t rows, int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nvec = cols >> 3;
+  const bf16_t* xr = x + row * cols;
+  float h[NV][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      unpack8(ld8(xr + v * 8), h[i]);
+      if (res) {
+        float r[8];
+        unpack8(ld8(res + row * cols + v * 8), r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[i][e] += r[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += h[i][e] * h[i][e];
+    }
+  }
+  ss = wave_sum(ss);
+  const float f = rsqrtf(ss / (float)cols + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      if (res_out) st8(res_out + row * cols + v * 8, pack8(h[i]));
+      float y[8];
+      if (w) {
+        float wv[8];
+        unpack8(ld8(w + v * 8), wv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = h[i][e] * f * wv[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = h[i][e] * f;
+      }
+      st8(out + row * cols + v * 8, pack8(y));
+    }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void layer_norm_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+    const bf16_t* __restrict__ b, bf16_t* __restrict__ out, int64_t rows,
+    int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nvec = cols >> 3;
+  float h[NV][8];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      unpack8(ld8(x + row * cols + v * 8), h[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += h[i][e];
+    }
+  }
+  const float mean = wave_sum(s) / (float)cols;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        h[i][e] -= mean;
+        ss += h[i][e] * h[i][e];
+      }
+    }
+  }
+  const float inv = rsqrtf(wave_sum(ss) / (float)cols + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      float wv[8], bv[8], y[8];
+      unpack8(ld8(w + v * 8), wv);
+      unpack8(ld8(b + v * 8), bv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = h[i][e] * inv * wv[e] + bv[e];
+      st8(out + row * cols + v * 8, pack8(y));
+    }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void adarms_norm_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ style,
+    bf16_t* __restrict__ out, bf16_t* __restrict__ gate_out, int64_t rows,
+    int cols, int64_t rows_per_style, int64_t style_stride, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nvec = cols >> 3;
+  const bf16_t* st = style + (row / rows_per_style) * style_stride;
+  float h[NV][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      unpack8(ld8(x + row * cols + v * 8), h[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += h[i][e] * h[i][e];
+    }
+  }
+  const float f = rsqrtf(wave_sum(ss) / (float)cols + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      float sc[8], sh[8], y[8];
+      unpack8(ld8(st + v * 8), sc);
+      unpack8(ld8(st + cols + v * 8), sh);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = h[i][e] * f * (1.f + sc[e]) + sh[e];
+      st8(out + row * cols + v * 8, pack8(y));
+      if (gate_out)
+        st8(gate_out + row * cols + v * 8, ld8(st + 2 * cols + v * 8));
+    }
+  }
+}
+
+#define FVX_NV_DISPATCH(NV_RUNTIME, LAUNCH) \
+  switch (NV_RUNTIME) {                     \
+    case 1: LAUNCH(1); break;               \
+    case 2: LAUNCH(2); break;               \
+    case 3: LAUNCH(3); break;               \
+    case 4: LAUNCH(4); break;               \
+    case 5: LAUNCH(5); break;               \
+    case 6: LAUNCH(6); break;               \
+    case 7: LAUNCH(7); break;               \
+    default: LAUNCH(8); break;              \
+  }
+
+static int check_rows(const char* what, int64_t rows, int64_t cols) {
+  FVX_REQUIRE(rows >= 0, FVX_ERR_SHAPE, "%s: rows=%lld < 0", what,
+              (long long)rows);
+  FVX_REQUIRE(cols > 0 && cols % 8 == 0 && cols <= 64 * 8 * kMaxVec,
+              FVX_ERR_SHAPE,
+              "%s: cols=%lld must be a positive multiple of 8 and <= 4096",
+              what, (long long)cols);
+  return FVX_OK;
+}
+
+}  // namespace fvx
+
+using namespace fvx;
+
+extern "C" int fvx_rms_norm_residual(const void* x, const void* residual,
+                                     const void* weight, void* out,
+                                     void* residual_out, int64_t rows,
+                                     int64_t cols, float eps, void* stream) {
+  clear_error();
+  FVX_REQUIRE(x && out, FVX_ERR_NULL, "rms_norm_residual: x and out required");
+  int st = check_rows("rms_norm_residual", rows, cols);
+  if (st) return st;
+  FVX_REQUIRE(aligned16(x) && aligned16(out) && aligned16(residual) &&
+                  aligned16(weight) && aligned16(residual_out),
+              FVX_ERR_ALIGN, "rms_norm_residual: pointers must be 16B aligned");
+  if (rows == 0) return FVX_OK;
+  const int nv = (int)((cols / 8 + 63) / 64);
+  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  hipStream_t s = (hipStream_t)stream;
+#define L(NV)                                                               \
+  hipLaunchKernelGGL(rms_norm_residual_kernel<NV>, grid, dim3(256), 0, s,   \
+                     (const bf16_t*)x, (const bf16_t*)residual,             \
+                     (const bf16_t*)weight, (bf16_t*)out,                   \
+                     (bf16_t*)residual_out, rows, (int)cols, eps)
+  FVX_NV_DISPATCH(nv, L)
+#undef L
+  return launch_status("rms_norm_residual");
+}
+
+extern "C" int fvx_layer_norm(const void* x, const void* weight,
+                              const void* bias, void* out, int64_t rows,
+                              int64_t cols, float eps, void* stream) {
+  clear_error();
+  FVX_REQUIRE(x && weight && bias && out, FVX_ERR_NULL,
+              "layer_norm: x, weight, bias, out required");
+  int st = check_rows("layer_norm", rows, cols);
+  if (st) return st;
+  FVX_REQUIRE(aligned16(x) && aligned16(out) && aligned16(weight) &&
+                  aligned16(bias),
+              FVX_ERR_ALIGN, "layer_norm: pointers must be 16B aligned");
+  if (rows == 0) return FVX_OK;
+  const int nv = (int)((cols / 8 + 63) / 64);
+  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  hipStream_t s = (hipStream_t)stream;
+#define L(NV)                                                               \
+  hipLaunchKernelGGL(layer_norm_kernel<NV>, grid, dim3(256), 0, s,          \
+                     (const bf16_t*)x, (const bf16_t*)weight,               \
+                     (const bf16_t*)bias, (bf16_t*)out, rows, (int)cols, eps)
+  FVX_NV_DISPATCH(nv, L)
+#undef L
+  return launch_status("layer_norm");
+}
+
+extern "C" int fvx_adarms_norm(const void* x, const void* style, void* out,
+                               void* gate_out, int64_t rows, int64_t cols,
+                               int64_t rows_per_style, int64_t style_stride,
+                               float eps, void* stream) {
+  clear_error();
+  FVX_REQUIRE(x && style && out, FVX_ERR_NULL,
+              "adarms_norm: x, style, out required");
+  int st = check_rows("adarms_norm", rows, cols);
+  if (st) return st;
+  FVX_REQUIRE(rows_per_style > 0 && style_stride >= 3 * cols &&
+                  style_stride % 8 == 0,
+              FVX_ERR_SHAPE,
+              "adarms_norm: rows_per_style > 0 and style_stride >= 3*cols "
+              "(multiple of 8) required");
+  FVX_REQUIRE(aligned16(x) && aligned16(out) && aligned16(style) &&
+                  aligned16(gate_out),
+              FVX_ERR_ALIGN, "adarms_norm: pointers must be 16B aligned");
+  if (rows == 0) return FVX_OK;
+  const int nv = (int)((cols / 8 + 63) / 64);
+  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  hipStream_t s = (hipStream_t)stream;
+#define L(NV)                                                               \
+  hipLaunchKernelGGL(adarms_norm_kernel<NV>, grid, dim3(256), 0, s,         \
+                     (const bf16_t*)x, (const bf16_t*)style, (bf16_t*)out,  \
+                     (bf16_t*)gate_out, rows, (int)cols, rows_per_style,    \
+                     style_stride, eps)
+  FVX_NV_DISPATCH(nv, L)
+#undef L
+  return launch_status("adarms_norm");
+}

@@ -1,0 +1,393 @@
+"""Torch-facing wrappers of the C ABI.
+
+Each function takes torch tensors that already live on the GPU, checks dtype,
+device and contiguity on the host, builds the C descriptor from raw pointers
+and enqueues on ``torch.cuda.current_stream()``.  Nothing here allocates
+unless the caller omits an ``out=`` tensor, so calls with preallocated
+outputs are safe inside HIP graph capture.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import AttnDesc, GemmDesc
+
+BF16 = torch.bfloat16
+
+# Split-K / split-KV workspace: one per device, zero-filled once.  Kernels
+# leave their arrival counters at zero, so the buffer is reusable by every
+# later call on the same stream.
+WORKSPACE_BYTES = 64 << 20
+_workspaces = {}
+
+
+def workspace(device=None):
+    dev = torch.device('cuda', torch.cuda.current_device()
+                       if device is None else torch.device(device).index)
+    ws = _workspaces.get(dev.index)
+    if ws is None:
+        ws = torch.zeros(WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
+        _workspaces[dev.index] = ws
+    return ws
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check(t, name, dtype=BF16, contiguous=True, allow_none=False):
+    if t is None:
+        if allow_none:
+            return
+        raise ValueError(f'{name} is required')
+    if not t.is_cuda:
+        raise ValueError(f'{name} must be a CUDA (HIP) tensor')
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f'{name} must be {dtype}, got {t.dtype}')
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f'{name} must be contiguous')
+
+
+def _rows_ld(t, name):
+    """(rows, leading dim) of a 2-D view with unit column stride."""
+    if t.dim() < 2:
+        raise ValueError(f'{name} must be at least 2-D')
+    if t.stride(-1) != 1:
+        raise ValueError(f'{name} must have unit stride in its last dim')
+    t2 = t if t.dim() == 2 else t.reshape(-1, t.shape[-1])
+    return t2.shape[0], t2.stride(0)
+
+
+# ---------------------------------------------------------------------------
+# Norms
+# ---------------------------------------------------------------------------
+def rms_norm_residual(x, residual=None, weight=None, eps=1e-6, out=None,
+                      residual_out=None):
+    """h = x (+ residual); residual_out = bf16(h);
+    out = bf16(h * rsqrt(mean(h^2) + eps) * weight).  Returns (out, residual_out)."""
+    _check(x, 'x')
+    _check(residual, 'residual', allow_none=True)
+    _check(weight, 'weight', allow_none=True)
+    cols = x.shape[-1]
+    rows = x.numel() // cols
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, 'out')
+    if residual_out is not None:
+        _check(residual_out, 'residual_out')
+    if residual is not None and residual.shape != x.shape:
+        raise ValueError('residual must have the shape of x')
+    if weight is not None and weight.numel() != cols:
+        raise ValueError('weight must have x.shape[-1] elements')
+    _lib.call('fvx_rms_norm_residual', _ptr(x), _ptr(residual), _ptr(weight),
+              _ptr(out), _ptr(residual_out), rows, cols, float(eps),
+              _stream())
+    return out, residual_out
+
+
+def layer_norm(x, weight, bias, eps=1e-6, out=None):
+    _check(x, 'x')
+    _check(weight, 'weight')
+    _check(bias, 'bias')
+    cols = x.shape[-1]
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, 'out')
+    _lib.call('fvx_layer_norm', _ptr(x), _ptr(weight), _ptr(bias), _ptr(out),
+              x.numel() // cols, cols, float(eps), _stream())
+    return out
+
+
+def adarms_norm(x, style, out=None, gate_out=None, rows_per_style=None,
+                eps=1e-6):
+    """style rows [scale | shift | gate] (bf16, 3*cols wide), one per
+    ``rows_per_style`` rows of x (default: one style row for all rows)."""
+    _check(x, 'x')
+    cols = x.shape[-1]
+    rows = x.numel() // cols
+    _check(style, 'style', contiguous=False)
+    srows, sld = _rows_ld(style.view(-1, style.shape[-1]), 'style')
+    if rows_per_style is None:
+        rows_per_style = max(rows, 1)
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, 'out')
+    _check(gate_out, 'gate_out', allow_none=True)
+    _lib.call('fvx_adarms_norm', _ptr(x), _ptr(style), _ptr(out),
+              _ptr(gate_out), rows, cols, int(rows_per_style), sld,
+              float(eps), _stream())
+    return out, gate_out
+
+
+# ---------------------------------------------------------------------------
+# GEMM family
+# ---------------------------------------------------------------------------
+def _gemm_desc(a, w):
+    _check(a, 'a', contiguous=False)
+    _check(w, 'weight', contiguous=False)
+    m, lda = _rows_ld(a, 'a')
+    n, ldb = _rows_ld(w, 'weight')
+    k = a.shape[-1]
+    if w.shape[-1] != k:
+        raise ValueError(
+            f'weight must be [out_features, in_features={k}] (nn.Linear '
+            f'layout), got {tuple(w.shape)}')
+    d = GemmDesc()
+    d.a, d.lda, d.b, d.ldb = a.data_ptr(), lda, w.data_ptr(), ldb
+    d.m, d.n, d.k = m, n, k
+    d.gate_group = 1
+    ws = workspace(a.device)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+    return d
+
+
+def _run_gemm(d):
+    _lib.call('fvx_gemm', ctypes.byref(d), _stream())
+
+
+def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
+         gate=None, gate_group=1, pos=None, pos_period=0, act=_lib.ACT_NONE,
+         rownorm_eps=None, out_f32=False, row_group=0, row_group_stride=0,
+         split_k=0):
+    """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order."""
+    d = _gemm_desc(a, weight)
+    if out is None:
+        out = torch.empty(*a.shape[:-1], d.n,
+                          dtype=torch.float32 if out_f32 else BF16,
+                          device=a.device)
+    _check(out, 'out', dtype=torch.float32 if out_f32 else BF16,
+           contiguous=False)
+    _, d.ldc = _rows_ld(out, 'out')
+    d.c = out.data_ptr()
+    if bias is not None:
+        _check(bias, 'bias')
+        d.bias = bias.data_ptr()
+    if bias_f32 is not None:
+        _check(bias_f32, 'bias_f32', dtype=torch.float32)
+        d.bias_f32 = bias_f32.data_ptr()
+    if residual is not None:
+        _check(residual, 'residual', contiguous=False)
+        _, d.ldr = _rows_ld(residual, 'residual')
+        d.residual = residual.data_ptr()
+    if gate is not None:
+        _check(gate, 'gate', contiguous=False)
+        _, d.ldg = _rows_ld(gate, 'gate')
+        d.gate, d.gate_group = gate.data_ptr(), gate_group
+    if pos is not None:
+        _check(pos, 'pos', contiguous=False)
+        _, d.ldp = _rows_ld(pos, 'pos')
+        d.pos, d.pos_period = pos.data_ptr(), pos_period or pos.shape[0]
+    d.act, d.mode, d.out_f32 = int(act), _lib.GEMM_PLAIN, int(bool(out_f32))
+    if rownorm_eps is not None:
+        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    d.row_group, d.row_group_stride = row_group, row_group_stride
+    d.split_k = split_k
+    _run_gemm(d)
+    return out
+
+
+def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0):
+    """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T)."""
+    d = _gemm_desc(a, gate_w)
+    _check(up_w, 'up_w', contiguous=False)
+    if tuple(up_w.shape) != tuple(gate_w.shape) or up_w.stride() != gate_w.stride():
+        raise ValueError('up_w must match gate_w in shape and strides')
+    d.b2 = up_w.data_ptr()
+    if out is None:
+        out = torch.empty(*a.shape[:-1], d.n, dtype=BF16, device=a.device)
+    _check(out, 'out', contiguous=False)
+    _, d.ldc = _rows_ld(out, 'out')
+    d.c, d.mode = out.data_ptr(), _lib.GEMM_GEGLU
+    if rownorm_eps is not None:
+        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    d.split_k = split_k
+    _run_gemm(d)
+    return out
+
+
+def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
+                  head_dim, rownorm_eps=None, row_group=0, row_group_stride=0,
+                  split_k=0):
+    """[q|k|v] = a @ w_qkv^T with pair-interleaved RoPE on q and k.
+
+    rope: fp32 [max_pos, head_dim/2, 2] (cos, sin); positions: int32 [M].
+    k_out / v_out rows are remapped with (row_group, row_group_stride)."""
+    d = _gemm_desc(a, w_qkv)
+    _check(rope, 'rope', dtype=torch.float32)
+    _check(positions, 'positions', dtype=torch.int32)
+    if positions.numel() < d.m:
+        raise ValueError('positions must have one entry per row of a')
+    for t, nm in ((q_out, 'q_out'), (k_out, 'k_out'), (v_out, 'v_out')):
+        _check(t, nm, contiguous=False)
+    d.mode = _lib.GEMM_QKV_ROPE
+    d.rope, d.positions = rope.data_ptr(), positions.data_ptr()
+    d.q_out, d.ldq = q_out.data_ptr(), _rows_ld(q_out, 'q_out')[1]
+    d.k_out, d.ldk = k_out.data_ptr(), _rows_ld(k_out, 'k_out')[1]
+    d.v_out, d.ldv = v_out.data_ptr(), _rows_ld(v_out, 'v_out')[1]
+    d.n_q_heads, d.head_dim = n_q_heads, head_dim
+    if rownorm_eps is not None:
+        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    d.row_group, d.row_group_stride = row_group, row_group_stride
+    d.split_k = split_k
+    _run_gemm(d)
+
+
+def gemm_euler(a, weight, bias, xt, dt, xt_bf16=None, rownorm_eps=None,
+               split_k=0):
+    """v = a @ weight^T + bias; xt += dt * v (fp32, in place); xt_bf16 mirrors."""
+    d = _gemm_desc(a, weight)
+    _check(xt, 'xt', dtype=torch.float32, contiguous=False)
+    d.mode = _lib.GEMM_EULER
+    d.xt, d.ldx = xt.data_ptr(), _rows_ld(xt, 'xt')[1]
+    if xt_bf16 is not None:
+        _check(xt_bf16, 'xt_bf16', contiguous=False)
+        d.xt_bf16, d.ldxb = xt_bf16.data_ptr(), _rows_ld(xt_bf16, 'xt_bf16')[1]
+    if bias is not None:
+        _check(bias, 'bias')
+        d.bias = bias.data_ptr()
+    d.dt = float(dt)
+    if rownorm_eps is not None:
+        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    d.split_k = split_k
+    _run_gemm(d)
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+def attention_desc(q, k, v, o, *, sq, sk, heads, head_dim, n_problems=1,
+                   zdiv=1, q_tok_stride, q_head_stride, q_zs=(0, 0),
+                   k_tok_stride, k_zs=(0, 0), v_tok_stride, v_zs=(0, 0),
+                   o_tok_stride, o_head_stride, o_zs=(0, 0), kgrp=None,
+                   qgrp=None, kgrp_zs=0, qgrp_zs=0, scale=None, kv_splits=0):
+    for t, nm in ((q, 'q'), (k, 'k'), (v, 'v'), (o, 'o')):
+        _check(t, nm, contiguous=False)
+    d = AttnDesc()
+    d.q, d.q_tok_stride, d.q_head_stride = q.data_ptr(), q_tok_stride, q_head_stride
+    d.q_zs1, d.q_zs2 = q_zs
+    d.k, d.k_tok_stride = k.data_ptr(), k_tok_stride
+    d.k_zs1, d.k_zs2 = k_zs
+    d.v, d.v_tok_stride = v.data_ptr(), v_tok_stride
+    d.v_zs1, d.v_zs2 = v_zs
+    d.o, d.o_tok_stride, d.o_head_stride = o.data_ptr(), o_tok_stride, o_head_stride
+    d.o_zs1, d.o_zs2 = o_zs
+    if (kgrp is None) != (qgrp is None):
+        raise ValueError('kgrp and qgrp must be given together')
+    if kgrp is not None:
+        _check(kgrp, 'kgrp', dtype=torch.int32)
+        _check(qgrp, 'qgrp', dtype=torch.int32)
+        d.kgrp, d.qgrp = kgrp.data_ptr(), qgrp.data_ptr()
+        d.kgrp_zs1, d.qgrp_zs1 = kgrp_zs, qgrp_zs
+    d.sq, d.sk, d.heads, d.head_dim = sq, sk, heads, head_dim
+    d.n_problems, d.zdiv = n_problems, zdiv
+    d.scale = float(head_dim ** -0.5 if scale is None else scale)
+    d.kv_splits = kv_splits
+    ws = workspace(q.device)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+    return d
+
+
+def run_attention(d):
+    _lib.call('fvx_attention', ctypes.byref(d), _stream())
+
+
+def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0):
+    """Batched multi-query attention.
+
+    q: [B, Sq, H, D] (or [B, Sq, H*D]); k, v: [B, Sk, D] (row stride may
+    exceed D, e.g. a cache slice); o like q.  kgrp: int32 [B, Sk], qgrp:
+    int32 [B, Sq] (visible iff kgrp[j] <= qgrp[i])."""
+    B, Sq = q.shape[0], q.shape[1]
+    D = k.shape[-1]
+    H = (q.shape[2] if q.dim() == 4 else q.shape[2] // D)
+    Sk = k.shape[1]
+    d = attention_desc(
+        q, k, v, o, sq=Sq, sk=Sk, heads=H, head_dim=D, n_problems=B, zdiv=1,
+        q_tok_stride=q.stride(1), q_head_stride=D, q_zs=(q.stride(0), 0),
+        k_tok_stride=k.stride(1), k_zs=(k.stride(0), 0),
+        v_tok_stride=v.stride(1), v_zs=(v.stride(0), 0),
+        o_tok_stride=o.stride(1), o_head_stride=D, o_zs=(o.stride(0), 0),
+        kgrp=kgrp, qgrp=qgrp,
+        kgrp_zs=(kgrp.stride(0) if kgrp is not None else 0),
+        qgrp_zs=(qgrp.stride(0) if qgrp is not None else 0), scale=scale,
+        kv_splits=kv_splits)
+    run_attention(d)
+    return o
+
+
+def mha_packed_qkv(qkv, out, n_views, seq, heads, head_dim, scale=None,
+                   kv_splits=0):
+    """Bidirectional MHA over packed [n_views * seq, 3 * heads * head_dim]
+    (SigLIP): out [n_views * seq, heads * head_dim]."""
+    hid = heads * head_dim
+    ld = qkv.stride(0)
+    d = attention_desc(
+        qkv, qkv[:, hid:], qkv[:, 2 * hid:], out, sq=seq, sk=seq, heads=1,
+        head_dim=head_dim, n_problems=n_views * heads, zdiv=heads,
+        q_tok_stride=ld, q_head_stride=0, q_zs=(seq * ld, head_dim),
+        k_tok_stride=ld, k_zs=(seq * ld, head_dim),
+        v_tok_stride=ld, v_zs=(seq * ld, head_dim),
+        o_tok_stride=out.stride(0), o_head_stride=0,
+        o_zs=(seq * out.stride(0), head_dim), scale=scale,
+        kv_splits=kv_splits)
+    run_attention(d)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Data movement
+# ---------------------------------------------------------------------------
+def im2col_patches(images, patch, k_pad, out=None, scale=1.0, shift=0.0):
+    """images [N, 3, H, W] (bf16 or fp32) -> [N * (H/p) * (W/p), k_pad] bf16."""
+    _check(images, 'images', dtype=None)
+    if images.dtype not in (BF16, torch.float32):
+        raise ValueError('images must be bf16 or fp32')
+    n, c, h, w = images.shape
+    if c != 3:
+        raise ValueError('images must have 3 channels')
+    rows = n * (h // patch) * (w // patch)
+    if out is None:
+        out = torch.empty(rows, k_pad, dtype=BF16, device=images.device)
+    _check(out, 'out')
+    _lib.call('fvx_im2col_patches', _ptr(images),
+              int(images.dtype == torch.float32), _ptr(out), n, h, w, patch,
+              k_pad, float(scale), float(shift), _stream())
+    return out
+
+
+def embed_tokens(table, ids, out, scale=1.0, row_group=0, row_group_stride=0):
+    _check(table, 'table')
+    _check(ids, 'ids', dtype=torch.int64)
+    _check(out, 'out', contiguous=False)
+    _lib.call('fvx_embed_tokens', _ptr(table), _ptr(ids), _ptr(out),
+              ids.numel(), table.shape[1], table.shape[0], float(scale),
+              row_group, row_group_stride, _stream())
+    return out
+
+
+def copy_rows(src, dst, row_group=0, dst_group_stride=0):
+    _check(src, 'src', contiguous=False)
+    _check(dst, 'dst', contiguous=False)
+    rows, sld = _rows_ld(src, 'src')
+    _, dld = _rows_ld(dst, 'dst')
+    _lib.call('fvx_copy_rows', _ptr(src), sld, _ptr(dst), dld, rows,
+              src.shape[-1], row_group, dst_group_stride, _stream())
+    return dst
+
+
+def rope_table(max_pos, head_dim, theta=10000.0, device=None):
+    """fp32 [max_pos, head_dim/2, 2] (cos, sin) of pos * inv_freq, with
+    inv_freq = 1 / theta^(2i/head_dim) evaluated in fp32 as the HF Gemma
+    rotary embedding does (condition_gemma.py:246-260)."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64)
+                           .float() / head_dim))
+    pos = torch.arange(max_pos, dtype=torch.float32)
+    ph = pos[:, None] * inv[None, :]
+    t = torch.stack([torch.cos(ph), torch.sin(ph)], dim=-1).contiguous()
+    return t.to(device) if device is not None else t
+

@@ -1,0 +1,205 @@
+/*
+ * fluxvla_amd.h -- C ABI of libfluxvla_amd.so, the MI355X (gfx950) kernels of
+ * FluxVLA's PI0 / PI0.5 fused inference path.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensors are device pointers (HIP), row-major, 16-byte aligned.
+ *     bf16 storage is raw 16-bit (torch.bfloat16 bit pattern).
+ *   - Weight matrices are [out_features, in_features] (the nn.Linear layout):
+ *     the reduction dimension is contiguous, which is what the MFMA operand
+ *     fetch wants.  The reference's prepare hooks emit [in, out] instead
+ *     (fluxvla/models/backbones/llms/condition_gemma_inference.py:91-105).
+ *   - `stream` is a hipStream_t (0 = legacy default stream).  Nothing here
+ *     synchronizes, allocates or frees: every entry point is safe inside HIP
+ *     graph capture and only enqueues kernels.
+ *   - Every entry point returns 0 on success or a negative fvx_status code
+ *     without launching anything; fvx_last_error() then describes the
+ *     problem (thread-local).  Nothing aborts the process.
+ *   - Split-K GEMMs and split-KV attention need a workspace: `workspace`
+ *     must be device memory that was zero-filled once before its first use;
+ *     kernels leave it zeroed where it matters (the arrival counters) so it
+ *     can be reused by the next call on the same stream.  Passing a NULL
+ *     workspace is allowed and selects the single-pass kernels.
+ */
+#ifndef FLUXVLA_AMD_H_
+#define FLUXVLA_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum fvx_status {
+  FVX_OK = 0,
+  FVX_ERR_NULL = -1,      /* a required pointer is NULL */
+  FVX_ERR_SHAPE = -2,     /* a size is out of the supported range */
+  FVX_ERR_ALIGN = -3,     /* pointer / leading dimension not 16B aligned */
+  FVX_ERR_LAUNCH = -4,    /* the HIP launch itself failed */
+  FVX_ERR_ARG = -5,       /* an enum / flag argument is invalid */
+  FVX_ERR_WORKSPACE = -6, /* workspace too small for the requested split */
+};
+
+/* GEMM epilogue modes. */
+enum fvx_gemm_mode {
+  FVX_GEMM_PLAIN = 0, /* out = epilogue(A @ B^T) */
+  FVX_GEMM_GEGLU = 1, /* out = gelu_tanh(A @ B^T) * (A @ B2^T) */
+  FVX_GEMM_QKV_ROPE = 2, /* split into Q/K/V, rotate Q and K pairs */
+  FVX_GEMM_EULER = 3, /* v = A @ B^T + bias; xt += dt * v (fp32) */
+};
+
+enum fvx_act { FVX_ACT_NONE = 0, FVX_ACT_SILU = 1, FVX_ACT_GELU_TANH = 2 };
+
+/*
+ * One GEMM launch: acc[m][n] = sum_k A[m][k] * B[n][k] (fp32 accumulate),
+ * followed by the fused epilogue, applied in this order:
+ *   v = acc
+ *   v *= rsqrt(mean_k(A[m][k]^2) + rownorm_eps)      if rownorm
+ *   v += bias[n] (bf16) ; v += bias_f32[n] (fp32)    if given
+ *   v = act(v)
+ *   v *= gate[(m / gate_group) * ldg + n]            if gate
+ *   v += residual[orow(m) * ldr + n]                 if residual (may alias c)
+ *   v += pos[(m % pos_period) * ldp + n]             if pos
+ *   c[orow(m) * ldc + n] = bf16(v)  (fp32 if out_f32)
+ * where orow(m) = (m / row_group) * row_group_stride + m % row_group
+ * (identity when row_group == 0).
+ */
+typedef struct fvx_gemm_desc {
+  const void* a; int64_t lda;      /* [M, K] bf16 */
+  const void* b; int64_t ldb;      /* [N, K] bf16 */
+  const void* b2;                  /* GEGLU: up weight, same shape as b */
+  void* c; int64_t ldc;            /* [M, N] output */
+  int64_t m, n, k;
+  const void* bias;                /* [N] bf16 or NULL */
+  const float* bias_f32;           /* [N] fp32 or NULL */
+  const void* residual; int64_t ldr;
+  const void* gate; int64_t ldg; int64_t gate_group;
+  const void* pos; int64_t ldp; int64_t pos_period;
+  int32_t act;                     /* fvx_act */
+  int32_t mode;                    /* fvx_gemm_mode */
+  int32_t rownorm;                 /* 1: apply the per-row RMS factor of A */
+  int32_t out_f32;                 /* 1: c is fp32 */
+  float rownorm_eps;
+  float dt;                        /* EULER step */
+  int64_t row_group, row_group_stride;
+  /* QKV_ROPE: columns [0, nq*hd) -> q, [nq*hd, nq*hd+hd) -> k, next hd -> v.
+   * Q and K columns are in pair-interleaved order (2i, 2i+1) = (x_i,
+   * x_{i+hd/2}); rope[(pos * hd/2 + i) * 2 + {0,1}] = {cos, sin}. */
+  const float* rope;
+  const int32_t* positions;        /* [M] rope position per row */
+  void* q_out; int64_t ldq;
+  void* k_out; int64_t ldk;        /* rows remapped by orow() */
+  void* v_out; int64_t ldv;        /* rows remapped by orow() */
+  int32_t n_q_heads, head_dim;
+  /* EULER: xt[m*ldx + n] += dt * v ; xt_bf16 mirrors it in bf16 */
+  float* xt; int64_t ldx;
+  void* xt_bf16; int64_t ldxb;
+  /* split-K workspace (may be NULL) */
+  void* workspace; int64_t workspace_bytes;
+  int32_t split_k;                 /* 0 = choose automatically */
+  int32_t reserved;
+} fvx_gemm_desc;
+
+/* Library identity / diagnostics. */
+int fvx_version(void);
+const char* fvx_last_error(void);
+/* Number of fp32 workspace bytes fvx_gemm needs for the given problem
+ * (0 if it will run single-pass). */
+int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d);
+
+/* General GEMM with fused epilogue (all matmul_* entry points below are thin
+ * wrappers around it). */
+int fvx_gemm(const fvx_gemm_desc* d, void* stream);
+
+/*
+ * Fused residual-add + RMSNorm.  Replaces GemmaRMSNorm.forward followed by
+ * the residual add (fluxvla/models/backbones/llms/condition_gemma.py:75-116,
+ * :319-337) and the weight-less rms_norm_kernel
+ * (fluxvla/ops/triton/norm_triton_ops.py:317-332).
+ *   h = x (+ residual, fp32 add)            residual may be NULL
+ *   residual_out = bf16(h)                  residual_out may be NULL
+ *   out = bf16(h * rsqrt(mean(h^2) + eps) * weight)   weight may be NULL (=1)
+ * The Gemma (1 + w) scale is passed pre-folded in `weight`.
+ */
+int fvx_rms_norm_residual(const void* x, const void* residual,
+                          const void* weight, void* out, void* residual_out,
+                          int64_t rows, int64_t cols, float eps, void* stream);
+
+/* LayerNorm with affine (SigLIP).  Replaces layer_norm_small_kernel
+ * (fluxvla/ops/triton/norm_triton_ops.py:90-125). */
+int fvx_layer_norm(const void* x, const void* weight, const void* bias,
+                   void* out, int64_t rows, int64_t cols, float eps,
+                   void* stream);
+
+/* Adaptive RMSNorm (PI0.5).  Replaces adarms_norm_kernel
+ * (fluxvla/ops/triton/norm_triton_ops.py:355-395):
+ *   style row s = row / rows_per_style holds [scale | shift | gate] (bf16)
+ *   out = bf16(rms(x) * (1 + scale) + shift);  gate_out = gate (may be NULL) */
+int fvx_adarms_norm(const void* x, const void* style, void* out,
+                    void* gate_out, int64_t rows, int64_t cols,
+                    int64_t rows_per_style, int64_t style_stride, float eps,
+                    void* stream);
+
+/*
+ * Fused multi-query attention: softmax(Q K^T * scale + mask) V, flash-style
+ * (online softmax, fp32 statistics).  Replaces matmul_abT_scale +
+ * softmax_kernel_masklen / softmax_kernel_prefix_suffix + matmul_small
+ * (fluxvla/ops/triton/attention_triton_ops.py:5-146,
+ * fluxvla/ops/atomic_ops.py:209-221) and the SigLIP SDPA call
+ * (fluxvla/ops/atomic_ops.py:65-76).
+ *
+ * One problem z (z < n_problems) has sq query tokens x heads query rows and
+ * sk keys; query row r is token r / heads, head r % heads (all heads share
+ * the problem's single K/V head).  Pointer offsets of problem z are
+ * (z / zdiv) * zs1 + (z % zdiv) * zs2 elements, per tensor.
+ * Mask: key j is visible to query token t iff kgrp[j] <= qgrp[t]; NULL
+ * kgrp/qgrp means no mask.  This encodes make_att_2d_masks
+ * (fluxvla/engines/utils/model_utils.py:77-95): kgrp = pad ? cumsum(att) :
+ * INT32_MAX, qgrp = cumsum(att).  Rows that see no key produce zeros.
+ * kv_splits > 1 splits the key range across workgroups (needs workspace).
+ */
+typedef struct fvx_attn_desc {
+  const void* q; int64_t q_tok_stride, q_head_stride, q_zs1, q_zs2;
+  const void* k; int64_t k_tok_stride, k_zs1, k_zs2;
+  const void* v; int64_t v_tok_stride, v_zs1, v_zs2;
+  void* o; int64_t o_tok_stride, o_head_stride, o_zs1, o_zs2;
+  const int32_t* kgrp; int64_t kgrp_zs1;
+  const int32_t* qgrp; int64_t qgrp_zs1;
+  int64_t sq, sk, heads, head_dim, n_problems, zdiv;
+  float scale;
+  int32_t kv_splits;
+  void* workspace; int64_t workspace_bytes;
+} fvx_attn_desc;
+
+int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d);
+int fvx_attention(const fvx_attn_desc* d, void* stream);
+
+/*
+ * SigLIP patch im2col: images [n_img, 3, H, W] (bf16 or fp32 per
+ * `in_f32`) -> patches [n_img * (H/p) * (W/p), k_pad] bf16, column order
+ * (channel, ky, kx) (the Conv2d weight flattening), zero-filled from 3*p*p
+ * up to k_pad.  Optional affine: value * in_scale + in_shift.
+ */
+int fvx_im2col_patches(const void* images, int in_f32, void* patches,
+                       int64_t n_img, int64_t height, int64_t width,
+                       int64_t patch, int64_t k_pad, float in_scale,
+                       float in_shift, void* stream);
+
+/* Token embedding gather: out[orow(i)] = bf16(table[ids[i]] * scale). */
+int fvx_embed_tokens(const void* table, const int64_t* ids, void* out,
+                     int64_t n_tokens, int64_t dim, int64_t vocab,
+                     float scale, int64_t row_group, int64_t row_group_stride,
+                     void* stream);
+
+/* Row copy: dst[(i / row_group) * dst_group_stride + i % row_group] =
+ * src[(i / src_group) * src_group_stride ...] for bf16 rows of `cols`.  Used
+ * to place the per-chunk state token in front of the action tokens. */
+int fvx_copy_rows(const void* src, int64_t src_ld, void* dst, int64_t dst_ld,
+                  int64_t rows, int64_t cols, int64_t row_group,
+                  int64_t dst_group_stride, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLUXVLA_AMD_H_ */

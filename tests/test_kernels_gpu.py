@@ -1,0 +1,369 @@
+"""Parity of every HIP kernel against an fp32 reference of the same op.
+
+References are computed on the CPU in fp32 (float64 where noted) from the
+same bf16 inputs the kernel sees.  Bar (from the north star): each bf16 op
+has max relative error <= 1e-2, measured as max|out - ref| / max|ref|.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2
+
+
+def rel_err(out, ref):
+    out = out.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    return ((out - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(shape, seed, std=1.0, mean=0.0):
+    return (torch.randn(shape, generator=gen(seed)) * std + mean).to(
+        torch.bfloat16)
+
+
+@pytest.fixture(scope='module')
+def K():
+    from fluxvla_amd import kernels
+    kernels._lib.load()
+    return kernels
+
+
+# ---------------------------------------------------------------------------
+# Norms
+# ---------------------------------------------------------------------------
+def test_rms_norm_residual_config1(K, cuda):
+    """Config 1: x, residual [1024, 2048] ~N(0,1), w ~N(1, 0.02), eps 1e-6."""
+    announce('rms_norm_residual [1024,2048]')
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1024, 2048, generator=g).bfloat16()
+    res = torch.randn(1024, 2048, generator=g).bfloat16()
+    w = (torch.randn(2048, generator=g) * 0.02 + 1.0).bfloat16()
+    y, r = K.rms_norm_residual(x.to(cuda), res.to(cuda), w.to(cuda), 1e-6,
+                               residual_out=torch.empty_like(x, device=cuda))
+    h = x.float() + res.float()
+    ref_y = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
+    assert rel_err(y, ref_y) <= REL_TOL
+    assert rel_err(r, h) <= REL_TOL
+    # residual_out is exactly bf16(x + res) (one rounding of an exact sum)
+    assert torch.equal(r.cpu(), h.bfloat16())
+
+
+@pytest.mark.parametrize('rows,cols', [(51, 1024), (816, 2048), (7, 1152)])
+def test_rms_norm_plain(K, cuda, rows, cols):
+    announce(f'rms_norm plain [{rows},{cols}]')
+    x = randn((rows, cols), 1)
+    y, _ = K.rms_norm_residual(x.to(cuda), None, None, 1e-6)
+    xf = x.float()
+    ref = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert rel_err(y, ref) <= REL_TOL
+
+
+def test_layer_norm(K, cuda):
+    announce('layer_norm [768,1152]')
+    x = randn((768, 1152), 2, std=3.0, mean=0.5)
+    w = randn((1152,), 3, std=0.1, mean=1.0)
+    b = randn((1152,), 4, std=0.1)
+    y = K.layer_norm(x.to(cuda), w.to(cuda), b.to(cuda), 1e-6)
+    ref = F.layer_norm(x.float(), (1152,), w.float(), b.float(), 1e-6)
+    assert rel_err(y, ref) <= REL_TOL
+
+
+def test_adarms_norm(K, cuda):
+    announce('adarms_norm [100,1024] 2 styles')
+    x = randn((100, 1024), 5)
+    style = randn((2, 3072), 6, std=0.2)
+    y = torch.empty(100, 1024, dtype=torch.bfloat16, device=cuda)
+    gt = torch.empty_like(y)
+    K.adarms_norm(x.to(cuda), style.to(cuda), y, gt, rows_per_style=50)
+    xf = x.float()
+    n = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    st = style.float().repeat_interleave(50, 0)
+    ref = n * (1 + st[:, :1024]) + st[:, 1024:2048]
+    assert rel_err(y, ref) <= REL_TOL
+    assert torch.equal(gt.cpu(), style[:, 2048:].repeat_interleave(50, 0))
+
+
+# ---------------------------------------------------------------------------
+# GEMM family
+# ---------------------------------------------------------------------------
+GEMM_SHAPES = [
+    # (M, N, K): skinny (M <= 64) and tiled, ragged edges included
+    (51, 2560, 1024), (50, 1024, 32), (1, 1024, 1024), (64, 4304, 1152),
+    (816, 2560, 2048), (768, 4304, 1152), (768, 1152, 4304), (200, 640, 96),
+    (129, 136, 72),
+]
+
+
+@pytest.mark.parametrize('m,n,k', GEMM_SHAPES)
+def test_gemm_plain_bias_act(K, cuda, m, n, k):
+    announce(f'gemm plain m={m} n={n} k={k}')
+    a = randn((m, k), 10)
+    w = randn((n, k), 11, std=0.02)
+    b = randn((n,), 12, std=0.5)
+    ref = a.float() @ w.float().t()
+    out = K.gemm(a.to(cuda), w.to(cuda))
+    assert rel_err(out, ref) <= REL_TOL
+    out = K.gemm(a.to(cuda), w.to(cuda), bias=b.to(cuda), act=2)
+    assert rel_err(out, F.gelu(ref + b.float(), approximate='tanh')) <= REL_TOL
+    out = K.gemm(a.to(cuda), w.to(cuda), bias=b.to(cuda), act=1)
+    assert rel_err(out, F.silu(ref + b.float())) <= REL_TOL
+
+
+@pytest.mark.parametrize('m', [51, 816])
+def test_gemm_residual_gate_inplace(K, cuda, m):
+    announce(f'gemm residual/gate in place m={m}')
+    n, k = 1024, 2048
+    a = randn((m, k), 20)
+    w = randn((n, k), 21, std=0.02)
+    res = randn((m, n), 22)
+    gate = randn((m, n), 23, std=0.5)
+    ref = a.float() @ w.float().t()
+    x = res.clone().to(cuda)
+    K.gemm(a.to(cuda), w.to(cuda), out=x, residual=x)
+    assert rel_err(x, res.float() + ref) <= REL_TOL
+    x = res.clone().to(cuda)
+    K.gemm(a.to(cuda), w.to(cuda), out=x, residual=x, gate=gate.to(cuda))
+    assert rel_err(x, res.float() + ref * gate.float()) <= REL_TOL
+
+
+def test_gemm_split_deterministic(K, cuda):
+    """Split-K partials are reduced in a fixed order: bitwise repeatable,
+    and equal (to rounding) to the single-pass kernel."""
+    announce('gemm split-k determinism')
+    a = randn((51, 4096), 30).to(cuda)
+    w = randn((1024, 4096), 31, std=0.02).to(cuda)
+    o1 = K.gemm(a, w)
+    o2 = K.gemm(a, w)
+    o3 = K.gemm(a, w, split_k=1)
+    assert torch.equal(o1, o2)
+    assert rel_err(o1, o3.float()) <= 4e-3
+
+
+def test_gemm_pos_rowgroup_f32(K, cuda):
+    announce('gemm pos/row_group/out_f32')
+    m, n, k = 768, 1152, 640
+    a = randn((m, k), 40)
+    w = randn((n, k), 41, std=0.02)
+    b = randn((n,), 42)
+    pos = randn((256, n), 43)
+    ref = a.float() @ w.float().t() + b.float() + pos.float().repeat(3, 1)
+    out = K.gemm(a.to(cuda), w.to(cuda), bias=b.to(cuda), pos=pos.to(cuda),
+                 pos_period=256)
+    assert rel_err(out, ref) <= REL_TOL
+    # row remap: rows [256 g + r] -> [300 g + r] of a taller buffer
+    big = torch.zeros(900, n, dtype=torch.float32, device=cuda)
+    K.gemm(a.to(cuda), w.to(cuda), out=big, bias=b.to(cuda), pos=pos.to(cuda),
+           pos_period=256, out_f32=True, row_group=256, row_group_stride=300)
+    got = big.view(3, 300, n)[:, :256].reshape(768, n)
+    assert rel_err(got, ref) <= REL_TOL
+    assert big.view(3, 300, n)[:, 256:].abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize('m,n,k', [(51, 4096, 1024), (816, 16384, 2048),
+                                   (100, 4096, 1024)])
+def test_gemm_geglu_rownorm(K, cuda, m, n, k):
+    announce(f'gemm geglu rownorm m={m} n={n} k={k}')
+    x = randn((m, k), 50, std=2.0)
+    wg = randn((n, k), 51, std=0.02)
+    wu = randn((n, k), 52, std=0.02)
+    out = K.gemm_geglu(x.to(cuda), wg.to(cuda), wu.to(cuda), rownorm_eps=1e-6)
+    xf = x.float()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = F.gelu(xn @ wg.float().t(), approximate='tanh') * (xn @ wu.float().t())
+    assert rel_err(out, ref) <= REL_TOL
+
+
+def rope_ref(x, pos, hd, theta=10000.0):
+    """Rotate-half RoPE on [rows, heads, hd] at integer positions (fp64)."""
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.float64) / hd))
+    ph = pos.double()[:, None] * inv[None, :]
+    cos = torch.cat([ph.cos(), ph.cos()], -1)[:, None, :]
+    sin = torch.cat([ph.sin(), ph.sin()], -1)[:, None, :]
+    x1, x2 = x[..., :hd // 2], x[..., hd // 2:]
+    rot = torch.cat([-x2, x1], -1)
+    return x * cos + rot * sin
+
+
+def interleave_perm(hd):
+    """Row permutation that puts rotate-half pair (i, i + hd/2) at (2i, 2i+1)
+    (condition_gemma_inference.py:46-63)."""
+    idx = torch.arange(hd).view(2, hd // 2).t().reshape(-1)
+    return idx
+
+
+@pytest.mark.parametrize('m,k,start', [(51, 1024, 816), (816, 2048, 0)])
+def test_gemm_qkv_rope(K, cuda, m, k, start):
+    announce(f'gemm qkv_rope m={m} k={k}')
+    nq, hd = 8, 256
+    x = randn((m, k), 60, std=1.5)
+    wq = randn((nq * hd, k), 61, std=0.02)
+    wk = randn((hd, k), 62, std=0.02)
+    wv = randn((hd, k), 63, std=0.02)
+    perm = interleave_perm(hd)
+    wq_p = wq.view(nq, hd, k)[:, perm].reshape(nq * hd, k)
+    wk_p = wk[perm]
+    w = torch.cat([wq_p, wk_p, wv], 0).contiguous()
+    pos = torch.arange(start, start + m, dtype=torch.int32)
+    rope = K.rope_table(start + m + 8, hd, device=cuda)
+    q = torch.empty(m, nq * hd, dtype=torch.bfloat16, device=cuda)
+    kk = torch.zeros(m + 10, hd, dtype=torch.bfloat16, device=cuda)
+    vv = torch.zeros(m + 10, hd, dtype=torch.bfloat16, device=cuda)
+    K.gemm_qkv_rope(x.to(cuda), w.to(cuda), rope, pos.to(cuda), q, kk[5:],
+                    vv[5:], nq, hd, rownorm_eps=1e-6)
+    xf = x.double()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    rq = rope_ref((xn @ wq.double().t()).view(m, nq, hd), pos, hd)
+    rk = rope_ref((xn @ wk.double().t()).view(m, 1, hd), pos, hd)
+    rv = xn @ wv.double().t()
+    got_q = q.cpu().view(m, nq, hd)[:, :, torch.argsort(perm)]
+    got_k = kk[5:5 + m].cpu()[:, torch.argsort(perm)]
+    assert rel_err(got_q, rq) <= REL_TOL
+    assert rel_err(got_k, rk.view(m, hd)) <= REL_TOL
+    assert rel_err(vv[5:5 + m], rv) <= REL_TOL
+    assert kk[:5].abs().max().item() == 0.0
+    assert kk[5 + m:].abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize('m', [50, 400])
+def test_gemm_euler(K, cuda, m):
+    announce(f'gemm euler m={m}')
+    x = randn((m, 1024), 70, std=2.0)
+    w = randn((32, 1024), 71, std=0.02)
+    b = randn((32,), 72, std=0.1)
+    xt0 = torch.randn(m, 32, generator=gen(73))
+    xt = xt0.clone().to(cuda)
+    xtb = torch.empty(m, 32, dtype=torch.bfloat16, device=cuda)
+    K.gemm_euler(x.to(cuda), w.to(cuda), b.to(cuda), xt, -0.1, xt_bf16=xtb,
+                 rownorm_eps=1e-6)
+    xf = x.float()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    v = xn @ w.float().t() + b.float()
+    ref = xt0 - 0.1 * v
+    assert (xt.cpu() - ref).abs().max().item() <= 2e-3
+    assert torch.equal(xtb.cpu(), xt.cpu().bfloat16())
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+def sdpa_ref(q, k, v, mask=None, scale=None):
+    """q [B, H, Sq, D], k/v [B, 1, Sk, D] fp32 on CPU; mask [B, Sq, Sk]."""
+    k = k.expand(-1, q.shape[1], -1, -1)
+    v = v.expand(-1, q.shape[1], -1, -1)
+    am = None if mask is None else mask[:, None]
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=am, scale=scale)
+
+
+@pytest.mark.parametrize('splits', [0, 1])
+def test_attention_prefix_mqa(K, cuda, splits):
+    announce(f'attention prefix mqa 816 splits={splits}')
+    S, H, D = 816, 8, 256
+    q = randn((1, S, H, D), 80)
+    k = randn((1, S, D), 81)
+    v = randn((1, S, D), 82)
+    o = torch.empty(1, S, H, D, dtype=torch.bfloat16, device=cuda)
+    K.mqa_attention(q.to(cuda), k.to(cuda), v.to(cuda), o, kv_splits=splits)
+    ref = sdpa_ref(q.float().transpose(1, 2), k.float()[:, None],
+                   v.float()[:, None]).transpose(1, 2)
+    assert rel_err(o, ref) <= REL_TOL
+
+
+def test_attention_prefix_padded(K, cuda):
+    """Padded keys (pad mask) are invisible: kgrp = INT32_MAX there."""
+    announce('attention prefix padded')
+    S, H, D = 300, 8, 256
+    pad = torch.ones(S, dtype=torch.bool)
+    pad[200:256] = False  # a missing camera block in the middle
+    pad[290:] = False     # prompt padding
+    q = randn((1, S, H, D), 83)
+    k = randn((1, S, D), 84)
+    v = randn((1, S, D), 85)
+    kgrp = torch.where(pad, 0, 2**31 - 1).to(torch.int32)[None]
+    qgrp = torch.zeros(1, S, dtype=torch.int32)
+    o = torch.empty(1, S, H, D, dtype=torch.bfloat16, device=cuda)
+    K.mqa_attention(q.to(cuda), k.to(cuda), v.to(cuda), o, kgrp.to(cuda),
+                    qgrp.to(cuda))
+    mask = pad[None, None, :].expand(1, S, S)
+    ref = sdpa_ref(q.float().transpose(1, 2), k.float()[:, None],
+                   v.float()[:, None], mask).transpose(1, 2)
+    assert rel_err(o[:, pad], ref[:, pad]) <= REL_TOL
+
+
+@pytest.mark.parametrize('splits', [0, 1, 5])
+def test_attention_decode_block_causal(K, cuda, splits):
+    """PI0 suffix: state token sees prefix + itself, actions see all."""
+    announce(f'attention decode block-causal splits={splits}')
+    P, Ssuf, H, D = 816, 51, 8, 256
+    T = P + Ssuf
+    q = randn((1, Ssuf, H, D), 90)
+    cache_k = randn((1, T + 13, D), 91)
+    cache_v = randn((1, T + 13, D), 92)
+    att = torch.tensor([1, 1] + [0] * 49)
+    cum = torch.cumsum(att, 0).to(torch.int32)
+    kgrp = torch.cat([torch.zeros(P, dtype=torch.int32), cum])[None]
+    qgrp = cum[None]
+    o = torch.empty(1, Ssuf, H, D, dtype=torch.bfloat16, device=cuda)
+    kc, vc = cache_k.to(cuda), cache_v.to(cuda)
+    K.mqa_attention(q.to(cuda), kc[:, :T], vc[:, :T], o, kgrp.to(cuda),
+                    qgrp.to(cuda), kv_splits=splits)
+    mask = torch.ones(1, Ssuf, T, dtype=torch.bool)
+    mask[0, 0, P + 1:] = False
+    ref = sdpa_ref(q.float().transpose(1, 2), cache_k[:, :T].float()[:, None],
+                   cache_v[:, :T].float()[:, None], mask).transpose(1, 2)
+    assert rel_err(o, ref) <= REL_TOL
+
+
+def test_attention_siglip_packed(K, cuda):
+    announce('attention siglip packed hd=72')
+    nv, S, H, D = 3, 256, 16, 72
+    qkv = randn((nv * S, 3 * H * D), 95)
+    out = torch.empty(nv * S, H * D, dtype=torch.bfloat16, device=cuda)
+    K.mha_packed_qkv(qkv.to(cuda), out, nv, S, H, D)
+    t = qkv.float().view(nv, S, 3, H, D).permute(2, 0, 3, 1, 4)
+    ref = F.scaled_dot_product_attention(t[0], t[1], t[2])
+    ref = ref.transpose(1, 2).reshape(nv * S, H * D)
+    assert rel_err(out, ref) <= REL_TOL
+
+
+# ---------------------------------------------------------------------------
+# Data movement
+# ---------------------------------------------------------------------------
+def test_im2col_and_patch_embed(K, cuda):
+    announce('im2col + patch embed gemm')
+    imgs = torch.rand(3, 3, 224, 224, generator=gen(100)) * 2 - 1
+    w = randn((1152, 3, 14, 14), 101, std=0.02)
+    b = randn((1152,), 102, std=0.1)
+    kpad = 592
+    wp = torch.zeros(1152, kpad, dtype=torch.bfloat16)
+    wp[:, :588] = w.view(1152, -1)
+    patches = K.im2col_patches(imgs.to(cuda), 14, kpad)
+    out = K.gemm(patches, wp.to(cuda), bias=b.to(cuda))
+    ref = F.conv2d(imgs.bfloat16().float(), w.float(), b.float(), stride=14)
+    ref = ref.flatten(2).transpose(1, 2).reshape(768, 1152)
+    assert rel_err(out, ref) <= REL_TOL
+
+
+def test_embed_tokens_and_copy_rows(K, cuda):
+    announce('embed tokens / copy rows')
+    table = randn((1000, 2048), 110)
+    ids = torch.randint(0, 1000, (2, 48), generator=gen(111))
+    out = torch.zeros(2, 100, 2048, dtype=torch.bfloat16, device=cuda)
+    K.embed_tokens(table.to(cuda), ids.to(cuda), out.view(-1, 2048)[52:],
+                   scale=2048 ** 0.5, row_group=48, row_group_stride=100)
+    ref = (table[ids].float() * 2048 ** 0.5).bfloat16()
+    assert torch.equal(out[:, 52:].cpu(), ref)
+    src = randn((2, 64), 112)
+    dst = torch.zeros(2, 10, 64, dtype=torch.bfloat16, device=cuda)
+    K.copy_rows(src.to(cuda), dst.view(-1, 64), row_group=1,
+                dst_group_stride=10)
+    assert torch.equal(dst[:, 0].cpu(), src)
+    assert dst[:, 1:].abs().max().item() == 0.0
