@@ -471,7 +471,7 @@ static int validate(const GemmArgs& d) {
                   FVX_ERR_NULL,
                   "gemm(qkv_rope): rope, positions, q_out, k_out, v_out "
                   "required");
-      FVX_REQUIRE(d.head_dim > 0 && d.head_dim % 2 == 0 && d.n_q_heads > 0 &&
+      FVX_REQUIRE(d.head_dim > 0 && d.head_dim % 2 == 0 && d.n_q_heads >= 0 &&
                       d.n == (int64_t)(d.n_q_heads + 2) * d.head_dim,
                   FVX_ERR_SHAPE,
                   "gemm(qkv_rope): n must be (n_q_heads + 2) * head_dim with "

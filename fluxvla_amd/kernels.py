@@ -279,8 +279,10 @@ def attention_desc(q, k, v, o, *, sq, sk, heads, head_dim, n_problems=1,
     if (kgrp is None) != (qgrp is None):
         raise ValueError('kgrp and qgrp must be given together')
     if kgrp is not None:
-        _check(kgrp, 'kgrp', dtype=torch.int32)
-        _check(qgrp, 'qgrp', dtype=torch.int32)
+        _check(kgrp, 'kgrp', dtype=torch.int32, contiguous=False)
+        _check(qgrp, 'qgrp', dtype=torch.int32, contiguous=False)
+        if kgrp.stride(-1) != 1 or qgrp.stride(-1) != 1:
+            raise ValueError('kgrp and qgrp need unit stride along tokens')
         d.kgrp, d.qgrp = kgrp.data_ptr(), qgrp.data_ptr()
         d.kgrp_zs1, d.qgrp_zs1 = kgrp_zs, qgrp_zs
     d.sq, d.sk, d.heads, d.head_dim = sq, sk, heads, head_dim

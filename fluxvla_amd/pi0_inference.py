@@ -1,0 +1,518 @@
+"""PI0 / PI0.5 action-chunk inference on MI355X.
+
+Host-side mirror of the reference's fused inference model
+(fluxvla/models/vlas/pi05_flowmatching_inference.py:329-656): weight
+preparation hooks, static buffers, one pipeline function per stage
+(vision_encoder / transformer_encoder / transformer_decoder, :22-312) and
+one HIP graph per batch size that replays the whole chunk (:469-512).  Unlike
+the reference fast path it covers PI0 (state token, block-causal suffix) as
+well as PI0.5 (adaRMS), batches > 1, and follows the reference's PyTorch
+path where the Triton path departs from it (suffix RoPE positions start at
+sum(prefix_pad) as in pi0_flowmatching.py:817-819; SigLIP LayerNorm eps is
+the config's 1e-6).
+
+Every op runs as a HIP kernel from libfluxvla_amd.so; torch is used for
+buffers, the stream and graph capture, and to stage the request's inputs.
+"""
+import math
+
+import torch
+
+from . import kernels as K
+from ._lib import ACT_GELU_TANH, ACT_SILU
+from .config import PI0Config
+
+BF16 = torch.bfloat16
+INT32_MAX = 2**31 - 1
+VIS = 'vision_backbone.vision.vision_model'
+
+
+# ---------------------------------------------------------------------------
+# Weight preparation hooks
+# ---------------------------------------------------------------------------
+def interleave_rows(head_dim):
+    """Row order that places rotate-half pair (i, i + d/2) at (2i, 2i + 1),
+    the same layout condition_gemma_inference.py:46-63 produces, so RoPE is a
+    rotation of adjacent columns inside the GEMM epilogue.  Applied to both Q
+    and K it leaves Q K^T unchanged."""
+    return torch.arange(head_dim).view(2, head_dim // 2).t().reshape(-1)
+
+
+def prepare_siglip(sd, cfg: PI0Config, device):
+    """SigLIPViTBackboneInference.prepare_triton counterpart
+    (fluxvla/models/visions/siglip_vit_inference.py:10-101): conv weight
+    flattened in (c, ky, kx) order and zero-padded to a multiple of 8
+    columns; Q|K|V stacked with their biases; weights stay [out, in]."""
+    vh, kp = cfg.vit_hidden, cfg.patch_k_pad
+    pw = torch.zeros(vh, kp, dtype=BF16)
+    pw[:, :cfg.patch_k] = sd[f'{VIS}.embeddings.patch_embedding.weight'].reshape(vh, -1)
+    w = {
+        'patch_w': pw,
+        'patch_b': sd[f'{VIS}.embeddings.patch_embedding.bias'],
+        'pos_emb': sd[f'{VIS}.embeddings.position_embedding.weight'],
+        'post_ln_w': sd[f'{VIS}.post_layernorm.weight'],
+        'post_ln_b': sd[f'{VIS}.post_layernorm.bias'],
+    }
+    layers = []
+    for i in range(cfg.vit_layers):
+        pre = f'{VIS}.encoder.layers.{i}'
+        a = f'{pre}.self_attn'
+        layers.append({
+            'ln1_w': sd[f'{pre}.layer_norm1.weight'],
+            'ln1_b': sd[f'{pre}.layer_norm1.bias'],
+            'qkv_w': torch.cat([sd[f'{a}.q_proj.weight'], sd[f'{a}.k_proj.weight'],
+                                sd[f'{a}.v_proj.weight']], 0),
+            'qkv_b': torch.cat([sd[f'{a}.q_proj.bias'], sd[f'{a}.k_proj.bias'],
+                                sd[f'{a}.v_proj.bias']], 0),
+            'o_w': sd[f'{a}.out_proj.weight'],
+            'o_b': sd[f'{a}.out_proj.bias'],
+            'ln2_w': sd[f'{pre}.layer_norm2.weight'],
+            'ln2_b': sd[f'{pre}.layer_norm2.bias'],
+            'fc1_w': sd[f'{pre}.mlp.fc1.weight'],
+            'fc1_b': sd[f'{pre}.mlp.fc1.bias'],
+            'fc2_w': sd[f'{pre}.mlp.fc2.weight'],
+            'fc2_b': sd[f'{pre}.mlp.fc2.bias'],
+        })
+    w['layers'] = layers
+    return _to(w, device)
+
+
+def prepare_gemma(sd, cfg: PI0Config, role, device):
+    """ConditionGemmaInferenceModel.prepare_triton counterpart
+    (condition_gemma_inference.py:65-170).  For plain-RMSNorm layers the
+    Gemma (1 + w) scale is folded into the following Q/K/V (input norm) and
+    gate/up (post-attention norm) weights in fp32 before the single bf16
+    rounding (:85-101); the expert's final norm is folded into
+    action_out_proj.  Q/K rows go to pair-interleaved order.  adaRMS layers
+    (PI0.5 expert) keep their dense modulation weights instead."""
+    prefix = 'llm_backbone' if role == 'llm' else 'llm_expert'
+    n = cfg.llm_layers if role == 'llm' else cfg.exp_layers
+    adarms = role == 'expert' and cfg.pi05
+    H, D = cfg.heads, cfg.head_dim
+    perm = interleave_rows(D)
+    layers = []
+    for i in range(n):
+        pre = f'{prefix}.layers.{i}'
+        wq = sd[f'{pre}.self_attn.q_proj.weight'].float()
+        wk = sd[f'{pre}.self_attn.k_proj.weight'].float()
+        wv = sd[f'{pre}.self_attn.v_proj.weight'].float()
+        wg = sd[f'{pre}.mlp.gate_proj.weight'].float()
+        wu = sd[f'{pre}.mlp.up_proj.weight'].float()
+        L = {}
+        if adarms:
+            for nm, key in (('attn', 'input_layernorm'),
+                            ('ffn', 'post_attention_layernorm')):
+                L[f'{nm}_mod_w'] = sd[f'{pre}.{key}.dense.weight']
+                L[f'{nm}_mod_b'] = sd[f'{pre}.{key}.dense.bias']
+        else:
+            s_in = 1.0 + sd[f'{pre}.input_layernorm.weight'].float()
+            s_post = 1.0 + sd[f'{pre}.post_attention_layernorm.weight'].float()
+            wq, wk, wv = wq * s_in, wk * s_in, wv * s_in
+            wg, wu = wg * s_post, wu * s_post
+        wq = wq.view(H, D, -1)[:, perm].reshape(H * D, -1)
+        wk = wk[perm]
+        L['qkv_w'] = torch.cat([wq, wk, wv], 0).to(BF16)
+        L['o_w'] = sd[f'{pre}.self_attn.o_proj.weight']
+        L['gate_w'] = wg.to(BF16)
+        L['up_w'] = wu.to(BF16)
+        L['down_w'] = sd[f'{pre}.mlp.down_proj.weight']
+        layers.append(L)
+    w = {'layers': layers}
+    if role == 'llm':
+        w['embed'] = sd['llm_backbone.embed_tokens.weight']
+    elif adarms:
+        w['final_mod_w'] = sd['llm_expert.norm.dense.weight']
+        w['final_mod_b'] = sd['llm_expert.norm.dense.bias']
+    else:
+        w['final_scale'] = 1.0 + sd['llm_expert.norm.weight'].float()
+    return _to(w, device)
+
+
+def prepare_projector(sd, prefix, device):
+    """LinearProjectorInference.prepare_triton counterpart
+    (linear_projector_inference.py:8-14): weight [out, in] and bias."""
+    return _to({'w': sd[f'{prefix}.projector.weight'],
+                'b': sd[f'{prefix}.projector.bias']}, device)
+
+
+def _to(obj, device):
+    if isinstance(obj, dict):
+        return {k: _to(v, device) for k, v in obj.items()}
+    if isinstance(obj, list):
+        return [_to(v, device) for v in obj]
+    if isinstance(obj, torch.Tensor):
+        return obj.to(device).contiguous()
+    return obj
+
+
+def euler_times(num_steps):
+    """fp32 time values of the reference Euler loop
+    (pi0_flowmatching.py:642-649): t = 1, t += dt while t >= -dt/2."""
+    dt = torch.tensor(-1.0 / num_steps, dtype=torch.float32)
+    t = torch.tensor(1.0, dtype=torch.float32)
+    out = []
+    while t >= -dt / 2:
+        out.append(float(t))
+        t = t + dt
+    return out, float(dt)
+
+
+def sinusoid(times, dim, min_period=4e-3, max_period=4.0):
+    """create_sinusoidal_pos_embedding (model_utils.py:40-68), fp32, for the
+    input-independent per-step time embeddings."""
+    fraction = torch.linspace(0.0, 1.0, dim // 2, dtype=torch.float32)
+    period = min_period * (max_period / min_period)**fraction
+    x = torch.tensor(times, dtype=torch.float32)[:, None] * (
+        1.0 / period * 2 * math.pi)
+    return torch.cat([torch.sin(x), torch.cos(x)], dim=-1)
+
+
+# ---------------------------------------------------------------------------
+# The inference model
+# ---------------------------------------------------------------------------
+class PI0Inference:
+    """Static-buffer, graph-replayed PI0 / PI0.5 action-chunk inference.
+
+    ``predict_action`` keeps the reference signature
+    (pi0_flowmatching.py:702-715) and returns the denoised chunk
+    [B, n_action_steps, max_action_dim] in fp32.
+    """
+
+    def __init__(self, cfg: PI0Config, state_dict, device='cuda',
+                 max_batch=1, use_graph=True):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.use_graph = use_graph
+        self.max_batch = max_batch
+        K.workspace(self.device)
+        self.prepare_triton_inference(state_dict)
+        self._graphs = {}
+        self._bufs = {}
+
+    # -- weight prep (prepare_triton_inference, :596-656) --------------------
+    @torch.no_grad()
+    def prepare_triton_inference(self, sd):
+        cfg, dev = self.cfg, self.device
+        self.vis = prepare_siglip(sd, cfg, dev)
+        self.llm = prepare_gemma(sd, cfg, 'llm', dev)
+        self.exp = prepare_gemma(sd, cfg, 'expert', dev)
+        self.proj = prepare_projector(sd, 'projector', dev)
+        self.act_in = prepare_projector(sd, 'action_in_proj', dev)
+        out = prepare_projector(sd, 'action_out_proj', dev)
+        if not cfg.pi05:
+            # final expert RMSNorm (1 + w) folded into action_out_proj
+            out['w'] = (out['w'].float() *
+                        self.exp.pop('final_scale')[None]).to(BF16)
+        self.act_out = out
+        self.times, self.dt = euler_times(cfg.num_steps)
+        temb = sinusoid(self.times, cfg.proj_width).to(BF16).to(dev)
+        w = cfg.proj_width
+        if cfg.pi05:
+            tin = prepare_projector(sd, 'time_mlp_in', dev)
+            tout = prepare_projector(sd, 'time_mlp_out', dev)
+            h = K.gemm(temb, tin['w'], bias=tin['b'], act=ACT_SILU)
+            self.cond = K.gemm(h, tout['w'], bias=tout['b'], act=ACT_SILU)
+            # adaRMS style rows depend only on (step, layer): precomputed once
+            styles = []
+            for L in self.exp['layers']:
+                styles.append(K.gemm(self.cond, L['attn_mod_w'],
+                                     bias=L['attn_mod_b']))
+                styles.append(K.gemm(self.cond, L['ffn_mod_w'],
+                                     bias=L['ffn_mod_b']))
+            styles.append(K.gemm(self.cond, self.exp['final_mod_w'],
+                                 bias=self.exp['final_mod_b']))
+            # [steps, 2 * layers + 1, 3 * width]
+            self.styles = torch.stack(styles, 1).contiguous()
+        else:
+            self.state = prepare_projector(sd, 'state_proj', dev)
+            mi = prepare_projector(sd, 'action_time_mlp_in', dev)
+            mo = prepare_projector(sd, 'action_time_mlp_out', dev)
+            # cat([action_emb, time_emb]) @ W^T = action_emb @ Wa^T +
+            # time_emb @ Wt^T: the time half is a per-step fp32 bias.
+            self.mlp_in_a = mi['w'][:, :w].contiguous()
+            wt = mi['w'][:, w:].contiguous()
+            self.step_bias = K.gemm(temb, wt, bias=mi['b'], out_f32=True)
+            self.mlp_out = mo
+        self.rope = K.rope_table(cfg.prefix_len + cfg.suffix_len + 8,
+                                 cfg.head_dim, cfg.rope_theta, device=dev)
+        torch.cuda.synchronize(dev)
+
+    # -- static buffers (_init_buffers, :356-442) ----------------------------
+    def _buffers(self, B):
+        if B in self._bufs:
+            return self._bufs[B]
+        cfg, dev = self.cfg, self.device
+        S, Ss, D = cfg.prefix_len, cfg.suffix_len, cfg.head_dim
+        T = S + Ss
+        nimg = B * cfg.n_views
+        nv_tok = nimg * cfg.num_patches
+        e = lambda *s, dt=BF16: torch.zeros(*s, dtype=dt, device=dev)  # noqa
+        b = {
+            'images': e(B, 3 * cfg.n_views, cfg.image_size, cfg.image_size,
+                        dt=torch.float32),
+            'ids': e(B, cfg.max_prompt_len, dt=torch.int64),
+            'patches': e(nv_tok, cfg.patch_k_pad),
+            'vis_x': e(nv_tok, cfg.vit_hidden),
+            'vis_xn': e(nv_tok, cfg.vit_hidden),
+            'vis_qkv': e(nv_tok, 3 * cfg.vit_hidden),
+            'vis_ctx': e(nv_tok, cfg.vit_hidden),
+            'vis_h': e(nv_tok, cfg.vit_mlp),
+            'pre_x': e(B, S, cfg.llm_hidden),
+            'pre_q': e(B, S, cfg.heads * D),
+            'pre_ctx': e(B, S, cfg.heads * D),
+            'pre_h': e(B * S, cfg.llm_mlp),
+            'kc': e(cfg.exp_layers, B, T, D),
+            'vc': e(cfg.exp_layers, B, T, D),
+            'pos_pre': e(B * S, dt=torch.int32),
+            'pos_suf': e(B * Ss, dt=torch.int32),
+            'kgrp': e(B, T, dt=torch.int32),
+            'qgrp_pre': e(B, S, dt=torch.int32),
+            'qgrp_suf': e(B, Ss, dt=torch.int32),
+            'ex_x': e(B, Ss, cfg.exp_hidden),
+            'ex_xn': e(B, Ss, cfg.exp_hidden),
+            'ex_gate': e(B, Ss, cfg.exp_hidden),
+            'ex_q': e(B, Ss, cfg.heads * D),
+            'ex_ctx': e(B, Ss, cfg.heads * D),
+            'ex_h': e(B * Ss, cfg.exp_mlp),
+            'act_h1': e(B * cfg.n_action_steps, cfg.proj_width),
+            'act_h2': e(B * cfg.n_action_steps, cfg.proj_width),
+            'states': e(B, cfg.state_dim),
+            'state_emb': e(B, cfg.proj_width),
+            'xt': e(B, cfg.n_action_steps, cfg.max_action_dim,
+                    dt=torch.float32),
+            'xt_bf16': e(B, cfg.n_action_steps, cfg.max_action_dim),
+        }
+        self._bufs[B] = b
+        return b
+
+    # -- pipeline ------------------------------------------------------------
+    def vision_encoder(self, b, B):
+        """SigLIP per view + projector into the prefix rows
+        (pi05_flowmatching_inference.py:22-66, 69-84)."""
+        cfg, V = self.cfg, self.vis
+        nimg = B * cfg.n_views
+        imgs = b['images'].view(nimg, 3, cfg.image_size, cfg.image_size)
+        K.im2col_patches(imgs, cfg.patch, cfg.patch_k_pad, out=b['patches'])
+        x, xn = b['vis_x'], b['vis_xn']
+        K.gemm(b['patches'], V['patch_w'], out=x, bias=V['patch_b'],
+               pos=V['pos_emb'], pos_period=cfg.num_patches)
+        for L in V['layers']:
+            K.layer_norm(x, L['ln1_w'], L['ln1_b'], cfg.vit_eps, out=xn)
+            K.gemm(xn, L['qkv_w'], out=b['vis_qkv'], bias=L['qkv_b'])
+            K.mha_packed_qkv(b['vis_qkv'], b['vis_ctx'], nimg,
+                             cfg.num_patches, cfg.vit_heads, cfg.vit_head_dim)
+            K.gemm(b['vis_ctx'], L['o_w'], out=x, bias=L['o_b'], residual=x)
+            K.layer_norm(x, L['ln2_w'], L['ln2_b'], cfg.vit_eps, out=xn)
+            K.gemm(xn, L['fc1_w'], out=b['vis_h'], bias=L['fc1_b'],
+                   act=ACT_GELU_TANH)
+            K.gemm(b['vis_h'], L['fc2_w'], out=x, bias=L['fc2_b'], residual=x)
+        K.layer_norm(x, V['post_ln_w'], V['post_ln_b'], cfg.vit_eps, out=xn)
+        n_img_tok = cfg.n_views * cfg.num_patches
+        K.gemm(xn, self.proj['w'], out=b['pre_x'].view(-1, cfg.llm_hidden),
+               bias=self.proj['b'], row_group=n_img_tok,
+               row_group_stride=cfg.prefix_len)
+
+    def transformer_encoder(self, b, B):
+        """Gemma-2B prefix: fills the K/V cache rows [0, S) of every layer
+        (pi05_flowmatching_inference.py:69-152).  The last layer stops after
+        its K/V: its outputs feed nothing."""
+        cfg, W = self.cfg, self.llm
+        S, D, hid = cfg.prefix_len, cfg.head_dim, cfg.llm_hidden
+        T = S + cfg.suffix_len
+        n_img_tok = cfg.n_views * cfg.num_patches
+        x = b['pre_x'].view(B * S, hid)
+        K.embed_tokens(W['embed'], b['ids'],
+                       b['pre_x'].view(-1, hid)[n_img_tok:],
+                       scale=math.sqrt(hid), row_group=cfg.max_prompt_len,
+                       row_group_stride=S)
+        n = len(W['layers'])
+        for i, L in enumerate(W['layers']):
+            kc, vc = b['kc'][i], b['vc'][i]
+            last = i == n - 1
+            wqkv = L['qkv_w'][cfg.heads * D:] if last else L['qkv_w']
+            K.gemm_qkv_rope(x, wqkv, self.rope, b['pos_pre'],
+                            b['pre_q'].view(B * S, -1),
+                            kc.view(B * T, D), vc.view(B * T, D),
+                            0 if last else cfg.heads, D,
+                            rownorm_eps=cfg.rms_eps, row_group=S,
+                            row_group_stride=T)
+            if last:
+                break
+            K.mqa_attention(b['pre_q'], kc[:, :S], vc[:, :S], b['pre_ctx'],
+                            kgrp=b['kgrp'][:, :S], qgrp=b['qgrp_pre'])
+            K.gemm(b['pre_ctx'].view(B * S, -1), L['o_w'], out=x, residual=x)
+            K.gemm_geglu(x, L['gate_w'], L['up_w'], out=b['pre_h'],
+                         rownorm_eps=cfg.rms_eps)
+            K.gemm(b['pre_h'], L['down_w'], out=x, residual=x)
+
+    def _expert_layer_pi0(self, b, B, i, L):
+        cfg = self.cfg
+        S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
+        T = S + Ss
+        x = b['ex_x'].view(B * Ss, hid)
+        kc, vc = b['kc'][i], b['vc'][i]
+        K.gemm_qkv_rope(x, L['qkv_w'], self.rope, b['pos_suf'],
+                        b['ex_q'].view(B * Ss, -1), kc.view(B * T, D)[S:],
+                        vc.view(B * T, D)[S:], cfg.heads, D,
+                        rownorm_eps=cfg.rms_eps, row_group=Ss,
+                        row_group_stride=T)
+        K.mqa_attention(b['ex_q'], kc, vc, b['ex_ctx'], kgrp=b['kgrp'],
+                        qgrp=b['qgrp_suf'])
+        K.gemm(b['ex_ctx'].view(B * Ss, -1), L['o_w'], out=x, residual=x)
+        K.gemm_geglu(x, L['gate_w'], L['up_w'], out=b['ex_h'],
+                     rownorm_eps=cfg.rms_eps)
+        K.gemm(b['ex_h'], L['down_w'], out=x, residual=x)
+
+    def _expert_layer_pi05(self, b, B, i, L, step):
+        cfg = self.cfg
+        S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
+        T = S + Ss
+        x = b['ex_x'].view(B * Ss, hid)
+        xn, gate = b['ex_xn'].view(B * Ss, hid), b['ex_gate'].view(B * Ss, hid)
+        kc, vc = b['kc'][i], b['vc'][i]
+        st = self.styles[step]
+        K.adarms_norm(x, st[2 * i:2 * i + 1], out=xn, gate_out=gate,
+                      eps=cfg.rms_eps)
+        K.gemm_qkv_rope(xn, L['qkv_w'], self.rope, b['pos_suf'],
+                        b['ex_q'].view(B * Ss, -1), kc.view(B * T, D)[S:],
+                        vc.view(B * T, D)[S:], cfg.heads, D, row_group=Ss,
+                        row_group_stride=T)
+        K.mqa_attention(b['ex_q'], kc, vc, b['ex_ctx'], kgrp=b['kgrp'],
+                        qgrp=b['qgrp_suf'])
+        K.gemm(b['ex_ctx'].view(B * Ss, -1), L['o_w'], out=x, residual=x,
+               gate=gate)
+        K.adarms_norm(x, st[2 * i + 1:2 * i + 2], out=xn, gate_out=gate,
+                      eps=cfg.rms_eps)
+        K.gemm_geglu(xn, L['gate_w'], L['up_w'], out=b['ex_h'])
+        K.gemm(b['ex_h'], L['down_w'], out=x, residual=x, gate=gate)
+
+    def transformer_decoder(self, b, B):
+        """The Euler loop of the action expert
+        (pi05_flowmatching_inference.py:155-312 / pi0_flowmatching.py:
+        642-649, 787-831): suffix embedding, expert layers against the
+        cached prefix K/V, final norm + action_out_proj + Euler update fused
+        in one GEMM epilogue."""
+        cfg = self.cfg
+        Ss, na, hid = cfg.suffix_len, cfg.n_action_steps, cfg.exp_hidden
+        x3 = b['ex_x']
+        xt_b = b['xt_bf16'].view(B * na, -1)
+        if not cfg.pi05:
+            K.gemm(b['states'], self.state['w'], out=b['state_emb'],
+                   bias=self.state['b'])
+        for step in range(len(self.times)):
+            if cfg.pi05:
+                K.gemm(xt_b, self.act_in['w'], out=x3.view(B * Ss, hid),
+                       bias=self.act_in['b'])
+            else:
+                K.gemm(xt_b, self.act_in['w'], out=b['act_h1'],
+                       bias=self.act_in['b'])
+                K.gemm(b['act_h1'], self.mlp_in_a, out=b['act_h2'],
+                       bias_f32=self.step_bias[step], act=ACT_SILU)
+                K.gemm(b['act_h2'], self.mlp_out['w'],
+                       out=x3.view(B * Ss, hid)[1:], bias=self.mlp_out['b'],
+                       row_group=na, row_group_stride=Ss)
+                K.copy_rows(b['state_emb'], x3.view(B * Ss, hid),
+                            row_group=1, dst_group_stride=Ss)
+            for i, L in enumerate(self.exp['layers']):
+                if cfg.pi05:
+                    self._expert_layer_pi05(b, B, i, L, step)
+                else:
+                    self._expert_layer_pi0(b, B, i, L)
+            lead = Ss - na
+            for s in range(B):
+                a = x3[s, lead:]
+                if cfg.pi05:
+                    xn = b['ex_xn'][s, lead:]
+                    st = self.styles[step, -1:]
+                    K.adarms_norm(a, st, out=xn, eps=cfg.rms_eps)
+                    a, rn = xn, None
+                else:
+                    rn = cfg.rms_eps
+                K.gemm_euler(a, self.act_out['w'], self.act_out['b'],
+                             b['xt'][s], self.dt, xt_bf16=b['xt_bf16'][s],
+                             rownorm_eps=rn)
+
+    def _run(self, B):
+        b = self._buffers(B)
+        self.vision_encoder(b, B)
+        self.transformer_encoder(b, B)
+        self.transformer_decoder(b, B)
+
+    # -- request staging (_triton_forward, :486-512) ---------------------------
+    @torch.no_grad()
+    def _stage(self, b, images, lang_tokens, states, img_masks, lang_masks,
+               noise):
+        cfg = self.cfg
+        B = images.shape[0]
+        dev = self.device
+        b['images'].copy_(images, non_blocking=True)
+        L = lang_tokens.shape[1]
+        if L > cfg.max_prompt_len:
+            raise ValueError(f'prompt of {L} tokens exceeds max_prompt_len='
+                             f'{cfg.max_prompt_len}')
+        b['ids'].zero_()
+        b['ids'][:, :L].copy_(lang_tokens, non_blocking=True)
+        if img_masks is None:
+            img_masks = torch.ones(B, cfg.n_views, dtype=torch.bool,
+                                   device=dev)
+        if lang_masks is None:
+            lang_masks = torch.ones(B, L, dtype=torch.bool, device=dev)
+        lm = torch.zeros(B, cfg.max_prompt_len, dtype=torch.bool, device=dev)
+        lm[:, :L] = lang_masks.to(dev).bool()
+        pad = torch.cat([img_masks.to(dev).bool().repeat_interleave(
+            cfg.num_patches, dim=1), lm], dim=1)
+        # make_att_2d_masks over [prefix (att 0) | suffix (att pattern)]
+        na = cfg.n_action_steps
+        satt = [1] + [0] * (na - 1) if cfg.pi05 else [1, 1] + [0] * (na - 1)
+        scum = torch.cumsum(torch.tensor(satt, dtype=torch.int32), 0).to(dev)
+        kg_pre = torch.where(pad, 0, INT32_MAX).to(torch.int32)
+        b['kgrp'].copy_(torch.cat([kg_pre, scum[None].expand(B, -1)], 1))
+        b['qgrp_suf'].copy_(scum[None].expand(B, -1))
+        b['qgrp_pre'].zero_()
+        b['pos_pre'].copy_((torch.cumsum(pad.int(), 1) - 1).view(-1))
+        off = pad.int().sum(1, keepdim=True)
+        b['pos_suf'].copy_((off + torch.arange(cfg.suffix_len, device=dev,
+                                               dtype=torch.int32)).view(-1))
+        if not cfg.pi05:
+            b['states'].copy_(states.to(dev, BF16), non_blocking=True)
+        b['xt'].copy_(noise, non_blocking=True)
+        b['xt_bf16'].copy_(noise, non_blocking=True)
+
+    def _capture(self, B):
+        g = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream(device=self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream):
+            self._run(B)  # warm-up on the capture stream
+            torch.cuda.synchronize(self.device)
+            g.capture_begin()
+            self._run(B)
+            g.capture_end()
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        torch.cuda.synchronize(self.device)
+        return g
+
+    @torch.no_grad()
+    def predict_action(self, images, lang_tokens, states, img_masks=None,
+                       lang_masks=None, past_key_values=None, noise=None,
+                       *args, **kwargs):
+        cfg = self.cfg
+        B = images.shape[0]
+        if B > self.max_batch:
+            raise ValueError(f'batch {B} > max_batch {self.max_batch}')
+        if noise is None:
+            noise = torch.randn(B, cfg.n_action_steps, cfg.max_action_dim,
+                                device=self.device)
+        b = self._buffers(B)
+        self._stage(b, images, lang_tokens, states, img_masks, lang_masks,
+                    noise)
+        if self.use_graph:
+            g = self._graphs.get(B)
+            if g is None:
+                g = self._graphs[B] = self._capture(B)
+                self._stage(b, images, lang_tokens, states, img_masks,
+                            lang_masks, noise)
+            g.replay()
+        else:
+            self._run(B)
+        return b['xt'].clone()

@@ -82,7 +82,8 @@ typedef struct fvx_gemm_desc {
   float rownorm_eps;
   float dt;                        /* EULER step */
   int64_t row_group, row_group_stride;
-  /* QKV_ROPE: columns [0, nq*hd) -> q, [nq*hd, nq*hd+hd) -> k, next hd -> v.
+  /* QKV_ROPE: columns [0, nq*hd) -> q, [nq*hd, nq*hd+hd) -> k, next hd -> v
+   * (n_q_heads may be 0: K/V only, e.g. the last prefix layer).
    * Q and K columns are in pair-interleaved order (2i, 2i+1) = (x_i,
    * x_{i+hd/2}); rope[(pos * hd/2 + i) * 2 + {0,1}] = {cos, sin}. */
   const float* rope;
@@ -191,9 +192,10 @@ int fvx_embed_tokens(const void* table, const int64_t* ids, void* out,
                      float scale, int64_t row_group, int64_t row_group_stride,
                      void* stream);
 
-/* Row copy: dst[(i / row_group) * dst_group_stride + i % row_group] =
- * src[(i / src_group) * src_group_stride ...] for bf16 rows of `cols`.  Used
- * to place the per-chunk state token in front of the action tokens. */
+/* Row copy of bf16 rows of `cols` elements: dst row orow(i) = src row i,
+ * orow(i) = (i / row_group) * dst_group_stride + i % row_group (identity
+ * when row_group == 0).  Used to place the per-chunk state token in front of
+ * each sample's action tokens. */
 int fvx_copy_rows(const void* src, int64_t src_ld, void* dst, int64_t dst_ld,
                   int64_t rows, int64_t cols, int64_t row_group,
                   int64_t dst_group_stride, void* stream);
