@@ -57,7 +57,7 @@ class GemmDesc(ctypes.Structure):
         ('xt_bf16', c_vp), ('ldxb', c_i64),
         ('workspace', c_vp), ('workspace_bytes', c_i64),
         ('split_k', c_i32),
-        ('reserved', c_i32),
+        ('v_transposed', c_i32),
     ]
 
 
@@ -70,6 +70,7 @@ class AttnDesc(ctypes.Structure):
         ('k_zs2', c_i64),
         ('v', c_vp), ('v_tok_stride', c_i64), ('v_zs1', c_i64),
         ('v_zs2', c_i64),
+        ('v_d_stride', c_i64),
         ('o', c_vp), ('o_tok_stride', c_i64), ('o_head_stride', c_i64),
         ('o_zs1', c_i64), ('o_zs2', c_i64),
         ('kgrp', c_vp), ('kgrp_zs1', c_i64),

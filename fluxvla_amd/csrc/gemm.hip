@@ -33,8 +33,6 @@ namespace fvx {
 
 typedef fvx_gemm_desc GemmArgs;
 
-constexpr int kMaxCounters = 4096;  // arrival counters at workspace start
-constexpr int64_t kCounterBytes = kMaxCounters * 4;
 
 __device__ __forceinline__ int64_t out_row(const GemmArgs& p, int64_t m) {
   return p.row_group > 0
@@ -45,14 +43,14 @@ __device__ __forceinline__ int64_t out_row(const GemmArgs& p, int64_t m) {
 // Epilogue for one MFMA output fragment: rows row0 + j (j < 4) of column n.
 // v: main accumulator, u: GEGLU up accumulator, pv: value of column n ^ 1
 // (QKV_ROPE partner), rs: per-row RMS factors (used when p.rownorm).
-template <int MODE>
+template <int MODE, int NR = 4>
 __device__ __forceinline__ void epilogue4(const GemmArgs& p, int64_t row0,
                                           int64_t n, const float* v,
                                           const float* u, const float* pv,
                                           const float* rs) {
   if (n >= p.n) return;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NR; ++j) {
     const int64_t m = row0 + j;
     if (m >= p.m) break;
     const float r = p.rownorm ? rs[j] : 1.f;
@@ -75,6 +73,11 @@ __device__ __forceinline__ void epilogue4(const GemmArgs& p, int64_t row0,
           ((bf16_t*)p.q_out)[m * p.ldq + n] = f2bf(x);
         else
           ((bf16_t*)p.k_out)[out_row(p, m) * p.ldk + (n - qcols)] = f2bf(x);
+      } else if (p.v_transposed) {
+        // V^T cache: [group][head_dim][ldv], tokens contiguous
+        const int64_t b = p.row_group > 0 ? m / p.row_group : 0;
+        const int64_t t = p.row_group > 0 ? m % p.row_group : m;
+        ((bf16_t*)p.v_out)[(b * hd + (n - qcols - hd)) * p.ldv + t] = f2bf(x);
       } else {
         ((bf16_t*)p.v_out)[out_row(p, m) * p.ldv + (n - qcols - hd)] = f2bf(x);
       }
@@ -254,130 +257,117 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs p, int m_tiles,
 }
 
 // ---------------------------------------------------------------------------
-// Skinny (M <= 64) split-K weight-streaming kernel
+// Skinny (M <= 64) weight-streaming kernels
 // ---------------------------------------------------------------------------
-constexpr int kSkinnyBN = 64;  // 4 waves x 16 columns
-constexpr int kSkinnyU = 4;    // k-steps of 32 in flight per wave
-
-template <int NB>
-__host__ __device__ constexpr int64_t skinny_part_floats() {
-  return (int64_t)4 * NB * 4 * 64 * 4;  // waves * NB * mfrags * lanes * 4
-}
+// gemm_skinny_kernel: a workgroup owns 64 output columns (4 waves x 16) and a
+// K range of at most kSkinnyKc.  Each wave first issues every weight
+// fragment load of its range (up to 8 x 16 B per lane per weight matrix, so
+// ~32-64 KiB per CU are in flight -- what HBM latency needs), then the whole
+// workgroup stages the 64 x Kc activation slab once in LDS, where all four
+// waves read their A fragments (activation traffic = weight traffic / 1.25
+// instead of 4x when every wave fetched its own copy).
+//
+// With one K range (splits == 1) the epilogue runs in place.  Otherwise the
+// fp32 partial tile and the partial row sums of squares go to the workspace
+// with plain stores, and gemm_skinny_reduce_kernel -- the next kernel on the
+// stream, so the partials are visible without any fence -- adds the splits
+// in order and runs the epilogue (deterministic).
+constexpr int kSkinnyKc = 256;
+constexpr int kSkinnyLDA = kSkinnyKc + 8;  // LDS pitch: conflict-free frag reads
 
 template <int MODE>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
                                                           int64_t kchunk) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int KS = kSkinnyKc / 32;  // k-steps per workgroup (max)
+  __shared__ __align__(16) bf16_t sA[64 * kSkinnyLDA];
+  __shared__ float s_ss[64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
   const int ntile = blockIdx.x, split = blockIdx.y;
   const int64_t M = p.m, N = p.n, K = p.k;
-  const int64_t n = (int64_t)ntile * kSkinnyBN + wave * 16 + fr;
+  const int64_t n = (int64_t)ntile * 64 + wave * 16 + fr;
   const bool nval = n < N;
   const int64_t kb = (int64_t)split * kchunk;
   const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
+  const int nks = (int)((ke - kb + 31) / 32);
 
-  const bf16_t* A = (const bf16_t*)p.a;
+  // 1. weight fragments for the whole K range, all loads in flight
   const bf16_t* Bp[2] = {(const bf16_t*)p.b + (nval ? n : 0) * p.ldb,
                          (const bf16_t*)(NB == 2 ? p.b2 : p.b) +
                              (nval ? n : 0) * p.ldb};
-  const bf16_t* Ap[4];
-  bool mval[4];
+  bf16x8 bw[KS][NB];
 #pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    const int64_t r = f * 16 + fr;
-    mval[f] = r < M;
-    Ap[f] = A + (mval[f] ? r : 0) * p.lda;
+  for (int t = 0; t < KS; ++t) {
+    const int64_t kk = kb + 32 * t + 8 * g;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      bw[t][b] = (t < nks && kk < ke && nval) ? ld8(Bp[b] + kk) : zero8();
   }
-
-  f32x4_t acc[NB][4];
-  float ss[4];
+  // 2. activation slab [64 x Kc] -> LDS (zero rows >= M / columns >= ke)
+  const bf16_t* A = (const bf16_t*)p.a;
+  constexpr int ACH = 64 * (kSkinnyKc / 8) / 256;  // 16 B chunks per thread
+  float ssp[ACH];
 #pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    ss[f] = 0.f;
+  for (int c = 0; c < ACH; ++c) {
+    const int i = tid + 256 * c;
+    const int r = i / (kSkinnyKc / 8), ck = i % (kSkinnyKc / 8);
+    const int64_t kk = kb + ck * 8;
+    const bf16x8 v = (r < M && kk < ke) ? ld8(A + r * p.lda + kk) : zero8();
+    st8(&sA[r * kSkinnyLDA + ck * 8], v);
+    ssp[c] = p.rownorm ? sumsq8(v) : 0.f;
+  }
+  // row sums: the 32 chunks of a row sit in 32 consecutive threads
+  if (p.rownorm) {
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) {
+      float v = ssp[c];
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, 64);
+      ssp[c] = v;
+    }
+  }
+  if (p.rownorm && (tid & 31) == 0) {
+#pragma unroll
+    for (int c = 0; c < ACH; ++c) s_ss[(tid + 256 * c) / 32] = ssp[c];
+  }
+  __syncthreads();
+
+  // 3. MFMA over the K range
+  f32x4_t acc[NB][4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-
-  for (int64_t k0 = kb; k0 < ke; k0 += 32 * kSkinnyU) {
-    bf16x8 a[kSkinnyU][4], bw[kSkinnyU][NB];
 #pragma unroll
-    for (int u = 0; u < kSkinnyU; ++u) {
-      const int64_t kk = k0 + 32 * u + 8 * g;
-      const bool kin = kk < ke;
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-        bw[u][b] = (kin && nval) ? ld8(Bp[b] + kk) : zero8();
-#pragma unroll
-      for (int f = 0; f < 4; ++f)
-        a[u][f] = (kin && mval[f]) ? ld8(Ap[f] + kk) : zero8();
-    }
-#pragma unroll
-    for (int u = 0; u < kSkinnyU; ++u)
+  for (int t = 0; t < KS; ++t) {
+    if (t < nks) {
 #pragma unroll
       for (int f = 0; f < 4; ++f) {
-        if (p.rownorm) ss[f] += sumsq8(a[u][f]);
+        const bf16x8 a = ld8(&sA[(f * 16 + fr) * kSkinnyLDA + 32 * t + 8 * g]);
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-          acc[b][f] = mfma16x16x32(a[u][f], bw[u][b], acc[b][f]);
+        for (int b = 0; b < NB; ++b) acc[b][f] = mfma16x16x32(a, bw[t][b], acc[b][f]);
       }
-  }
-  // Row sums of squares for rows f*16 + fr: reduce over the 4 k-groups.
-#pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    ss[f] += __shfl_xor(ss[f], 16, 64);
-    ss[f] += __shfl_xor(ss[f], 32, 64);
+    }
   }
 
   if (splits > 1) {
-    float* ws = (float*)((char*)p.workspace + kCounterBytes);
-    unsigned* counters = (unsigned*)p.workspace;
-    const int64_t tile_floats = skinny_part_floats<NB>() + 64;
-    float* part = ws + ((int64_t)ntile * splits + split) * tile_floats;
+    // partials: [NB][split][64 rows][N] fp32, then [split][64] row sums
+    float* ws = (float*)p.workspace;
+    const int64_t plane = (int64_t)splits * 64 * N;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int f = 0; f < 4; ++f)
-        *(f32x4_t*)(part + (((wave * NB + b) * 4 + f) * 64 + lane) * 4) =
-            acc[b][f];
-    if (wave == 0 && g == 0) {
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
-        part[skinny_part_floats<NB>() + f * 16 + fr] = ss[f];
-    }
-    __threadfence();
-    __syncthreads();
-    __shared__ unsigned s_last;
-    if (threadIdx.x == 0) {
-      const unsigned prev = atomicAdd(&counters[ntile], 1u);
-      s_last = (prev == (unsigned)(splits - 1)) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    // Last arrival: reduce all splits in split order.
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      ss[f] = 0.f;
-#pragma unroll
-      for (int b = 0; b < NB; ++b) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int s = 0; s < splits; ++s) {
-      const float* q = ws + ((int64_t)ntile * splits + s) * tile_floats;
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          const f32x4_t t = __builtin_nontemporal_load(
-              (const f32x4_t*)(q + (((wave * NB + b) * 4 + f) * 64 + lane) * 4));
-          acc[b][f] += t;
-        }
-#pragma unroll
-      for (int f = 0; f < 4; ++f)
-        ss[f] += __builtin_nontemporal_load(q + skinny_part_floats<NB>() + f * 16 + fr);
-    }
-    if (threadIdx.x == 0) counters[ntile] = 0u;
+        for (int j = 0; j < 4; ++j)
+          if (nval && f * 16 + 4 * g + j < M)
+            ws[b * plane + ((int64_t)split * 64 + f * 16 + 4 * g + j) * N + n] =
+                acc[b][f][j];
+    if (ntile == 0 && tid < 64) ws[NB * plane + split * 64 + tid] = s_ss[tid];
+    return;
   }
 
   // Epilogue: lane holds column n, rows f*16 + 4g + j.
@@ -385,10 +375,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
   for (int f = 0; f < 4; ++f) {
     float rs[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float s = __shfl(ss[f], 4 * g + j, 64);
-      rs[j] = rsqrtf(s / (float)K + p.rownorm_eps);
-    }
+    for (int j = 0; j < 4; ++j)
+      rs[j] = p.rownorm ? rsqrtf(s_ss[f * 16 + 4 * g + j] / (float)K + p.rownorm_eps)
+                        : 1.f;
     float v[4], u[4], pv[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -398,6 +387,48 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
     }
     epilogue4<MODE>(p, (int64_t)f * 16 + 4 * g, n, v, u, pv, rs);
   }
+}
+
+// Sum of the split partials + epilogue.  Thread t of block (x, y): column
+// 64 x + t % 64, row 4 y + t / 64; the loads of all splits are issued before
+// the adds (one memory latency) and added in split order (deterministic).
+constexpr int kSkinnyMaxSplits = 64;
+
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(GemmArgs p,
+                                                                 int splits) {
+  constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
+  constexpr int UN = 16;  // loads in flight per pass
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t N = p.n, K = p.k;
+  const int64_t n = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t row = (int64_t)blockIdx.y * 4 + (tid >> 6);
+  const bool ok = n < N && row < p.m;
+  const float* ws = (const float*)p.workspace;
+  const int64_t plane = (int64_t)splits * 64 * N;
+  float v = 0.f, u = 0.f, ss = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += UN) {
+    float t[NB][UN], q[UN];
+#pragma unroll
+    for (int i = 0; i < UN; ++i) {
+      const int s = s0 + i;
+      const bool in = ok && s < splits;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        t[b][i] = in ? ws[b * plane + ((int64_t)s * 64 + row) * N + n] : 0.f;
+      q[i] = (in && p.rownorm) ? ws[NB * plane + s * 64 + row] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < UN; ++i) {
+      v += t[0][i];
+      u += t[NB - 1][i];
+      ss += q[i];
+    }
+  }
+  float rs[1] = {p.rownorm ? rsqrtf(ss / (float)K + p.rownorm_eps) : 1.f};
+  float vv[1] = {v}, uu[1] = {u};
+  float pv[1] = {(MODE == FVX_GEMM_QKV_ROPE) ? __shfl_xor(v, 1, 64) : 0.f};
+  if (ok) epilogue4<MODE, 1>(p, row, n, vv, uu, pv, rs);
 }
 
 // ---------------------------------------------------------------------------
@@ -411,25 +442,22 @@ struct SkinnyPlan {
 static SkinnyPlan plan_skinny(const GemmArgs& d) {
   SkinnyPlan s;
   const int nb = d.mode == FVX_GEMM_GEGLU ? 2 : 1;
-  s.n_tiles = (int)((d.n + kSkinnyBN - 1) / kSkinnyBN);
-  int splits = d.split_k;
-  if (splits <= 0) {
-    const int target = 512;  // workgroups: 2 per CU on 256 CUs
-    splits = (target + s.n_tiles - 1) / s.n_tiles;
-    if (splits > 16) splits = 16;
+  s.n_tiles = (int)((d.n + 63) / 64);
+  int64_t kchunk;
+  if (d.split_k > 0) {
+    kchunk = (d.k + d.split_k - 1) / d.split_k;
+    kchunk = (kchunk + 31) / 32 * 32;
+  } else {
+    // 256-wide K ranges when that already gives ~200+ workgroups, else 128
+    kchunk = s.n_tiles * ((d.k + kSkinnyKc - 1) / kSkinnyKc) >= 200 ? 256 : 128;
   }
-  int64_t kchunk = (d.k + splits - 1) / splits;
-  kchunk = (kchunk + 127) / 128 * 128;  // whole unrolled k-iterations
-  if (kchunk < 128) kchunk = 128;
-  splits = (int)((d.k + kchunk - 1) / kchunk);
-  if (splits < 1) splits = 1;
-  s.splits = splits;
-  s.kchunk = splits == 1 ? d.k : kchunk;
-  const int64_t tile_floats =
-      (nb == 2 ? skinny_part_floats<2>() : skinny_part_floats<1>()) + 64;
-  s.ws_bytes = splits > 1 ? kCounterBytes + (int64_t)s.n_tiles * splits *
-                                                tile_floats * 4
-                          : 0;
+  if (kchunk > kSkinnyKc) kchunk = kSkinnyKc;
+  if (kchunk < 32) kchunk = 32;
+  s.splits = (int)((d.k + kchunk - 1) / kchunk);
+  s.kchunk = kchunk;
+  s.ws_bytes = s.splits > 1
+                   ? ((int64_t)nb * s.splits * 64 * d.n + (int64_t)s.splits * 64) * 4
+                   : 0;
   return s;
 }
 
@@ -511,15 +539,13 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (d.m <= 64) {
     SkinnyPlan sp = plan_skinny(d);
-    if (sp.splits > 1 && (!d.workspace || d.workspace_bytes < sp.ws_bytes ||
-                          sp.n_tiles > kMaxCounters)) {
-      FVX_REQUIRE(d.split_k <= 1, FVX_ERR_WORKSPACE,
-                  "gemm: split_k=%d needs %lld workspace bytes, got %lld",
-                  d.split_k, (long long)sp.ws_bytes,
-                  (long long)d.workspace_bytes);
-      sp.splits = 1;
-      sp.kchunk = d.k;
-    }
+    if (sp.splits > 1 && (!d.workspace || d.workspace_bytes < sp.ws_bytes))
+      return set_error(FVX_ERR_WORKSPACE,
+                       "gemm: m=%lld n=%lld k=%lld needs %lld workspace bytes "
+                       "for %d K ranges, got %lld",
+                       (long long)d.m, (long long)d.n, (long long)d.k,
+                       (long long)sp.ws_bytes, sp.splits,
+                       (long long)d.workspace_bytes);
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "gemm: workspace must be 16B aligned");
     dim3 grid((unsigned)sp.n_tiles, (unsigned)sp.splits);
@@ -528,7 +554,15 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
                      sp.splits, sp.kchunk)
     FVX_MODE_DISPATCH(d.mode, L)
 #undef L
-    return launch_status("gemm(skinny)");
+    int st2 = launch_status("gemm(skinny)");
+    if (st2 || sp.splits == 1) return st2;
+#define L(MODE)                                                            \
+  hipLaunchKernelGGL(gemm_skinny_reduce_kernel<MODE>,                      \
+                     dim3(sp.n_tiles, (unsigned)((d.m + 3) / 4)), dim3(256), \
+                     0, s, d, sp.splits)
+    FVX_MODE_DISPATCH(d.mode, L)
+#undef L
+    return launch_status("gemm(skinny reduce)");
   }
   // Big tiles: 128x128 when that fills the GPU, else 64-row tiles.
   const int64_t mt128 = (d.m + 127) / 128, nt128 = (d.n + 127) / 128;

@@ -212,11 +212,14 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0):
 
 def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
                   head_dim, rownorm_eps=None, row_group=0, row_group_stride=0,
-                  split_k=0):
+                  split_k=0, v_ld=None):
     """[q|k|v] = a @ w_qkv^T with pair-interleaved RoPE on q and k.
 
     rope: fp32 [max_pos, head_dim/2, 2] (cos, sin); positions: int32 [M].
-    k_out / v_out rows are remapped with (row_group, row_group_stride)."""
+    k_out rows are remapped with (row_group, row_group_stride).  v_out is
+    row-major like k_out, or -- with ``v_ld`` given -- the transposed value
+    cache: element (m, d) at v_out[(m // row_group * head_dim + d) * v_ld +
+    m % row_group] (v_out may be a view offset to the first token column)."""
     d = _gemm_desc(a, w_qkv)
     _check(rope, 'rope', dtype=torch.float32)
     _check(positions, 'positions', dtype=torch.int32)
@@ -228,7 +231,10 @@ def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
     d.rope, d.positions = rope.data_ptr(), positions.data_ptr()
     d.q_out, d.ldq = q_out.data_ptr(), _rows_ld(q_out, 'q_out')[1]
     d.k_out, d.ldk = k_out.data_ptr(), _rows_ld(k_out, 'k_out')[1]
-    d.v_out, d.ldv = v_out.data_ptr(), _rows_ld(v_out, 'v_out')[1]
+    if v_ld is None:
+        d.v_out, d.ldv = v_out.data_ptr(), _rows_ld(v_out, 'v_out')[1]
+    else:
+        d.v_out, d.ldv, d.v_transposed = v_out.data_ptr(), int(v_ld), 1
     d.n_q_heads, d.head_dim = n_q_heads, head_dim
     if rownorm_eps is not None:
         d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
@@ -264,7 +270,8 @@ def attention_desc(q, k, v, o, *, sq, sk, heads, head_dim, n_problems=1,
                    zdiv=1, q_tok_stride, q_head_stride, q_zs=(0, 0),
                    k_tok_stride, k_zs=(0, 0), v_tok_stride, v_zs=(0, 0),
                    o_tok_stride, o_head_stride, o_zs=(0, 0), kgrp=None,
-                   qgrp=None, kgrp_zs=0, qgrp_zs=0, scale=None, kv_splits=0):
+                   qgrp=None, kgrp_zs=0, qgrp_zs=0, scale=None, kv_splits=0,
+                   v_d_stride=0):
     for t, nm in ((q, 'q'), (k, 'k'), (v, 'v'), (o, 'o')):
         _check(t, nm, contiguous=False)
     d = AttnDesc()
@@ -274,6 +281,7 @@ def attention_desc(q, k, v, o, *, sq, sk, heads, head_dim, n_problems=1,
     d.k_zs1, d.k_zs2 = k_zs
     d.v, d.v_tok_stride = v.data_ptr(), v_tok_stride
     d.v_zs1, d.v_zs2 = v_zs
+    d.v_d_stride = v_d_stride
     d.o, d.o_tok_stride, d.o_head_stride = o.data_ptr(), o_tok_stride, o_head_stride
     d.o_zs1, d.o_zs2 = o_zs
     if (kgrp is None) != (qgrp is None):
@@ -298,21 +306,27 @@ def run_attention(d):
     _lib.call('fvx_attention', ctypes.byref(d), _stream())
 
 
-def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0):
+def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
+                  v_transposed=False):
     """Batched multi-query attention.
 
-    q: [B, Sq, H, D] (or [B, Sq, H*D]); k, v: [B, Sk, D] (row stride may
-    exceed D, e.g. a cache slice); o like q.  kgrp: int32 [B, Sk], qgrp:
-    int32 [B, Sq] (visible iff kgrp[j] <= qgrp[i])."""
+    q: [B, Sq, H, D] (or [B, Sq, H*D]); k: [B, Sk, D] (row stride may exceed
+    D, e.g. a cache slice); v: [B, Sk, D], or with ``v_transposed`` the value
+    cache [B, D, T >= Sk] (keys contiguous); o like q.  kgrp: int32 [B, Sk],
+    qgrp: int32 [B, Sq] (visible iff kgrp[j] <= qgrp[i])."""
     B, Sq = q.shape[0], q.shape[1]
     D = k.shape[-1]
     H = (q.shape[2] if q.dim() == 4 else q.shape[2] // D)
     Sk = k.shape[1]
+    if v_transposed and (v.shape[1] != D or v.stride(2) != 1):
+        raise ValueError('transposed v must be [B, D, T] with unit key stride')
     d = attention_desc(
         q, k, v, o, sq=Sq, sk=Sk, heads=H, head_dim=D, n_problems=B, zdiv=1,
         q_tok_stride=q.stride(1), q_head_stride=D, q_zs=(q.stride(0), 0),
         k_tok_stride=k.stride(1), k_zs=(k.stride(0), 0),
-        v_tok_stride=v.stride(1), v_zs=(v.stride(0), 0),
+        v_tok_stride=0 if v_transposed else v.stride(1),
+        v_zs=(v.stride(0), 0),
+        v_d_stride=v.stride(1) if v_transposed else 0,
         o_tok_stride=o.stride(1), o_head_stride=D, o_zs=(o.stride(0), 0),
         kgrp=kgrp, qgrp=qgrp,
         kgrp_zs=(kgrp.stride(0) if kgrp is not None else 0),

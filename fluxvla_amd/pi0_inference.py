@@ -237,13 +237,20 @@ class PI0Inference:
                                  cfg.head_dim, cfg.rope_theta, device=dev)
         torch.cuda.synchronize(dev)
 
+    @property
+    def kv_len(self):
+        """Token capacity of the K/V caches: prefix + suffix, rounded up to a
+        multiple of 8 (16-byte rows of the transposed value cache)."""
+        n = self.cfg.prefix_len + self.cfg.suffix_len
+        return (n + 7) // 8 * 8
+
     # -- static buffers (_init_buffers, :356-442) ----------------------------
     def _buffers(self, B):
         if B in self._bufs:
             return self._bufs[B]
         cfg, dev = self.cfg, self.device
         S, Ss, D = cfg.prefix_len, cfg.suffix_len, cfg.head_dim
-        T = S + Ss
+        T = self.kv_len
         nimg = B * cfg.n_views
         nv_tok = nimg * cfg.num_patches
         e = lambda *s, dt=BF16: torch.zeros(*s, dtype=dt, device=dev)  # noqa
@@ -261,11 +268,13 @@ class PI0Inference:
             'pre_q': e(B, S, cfg.heads * D),
             'pre_ctx': e(B, S, cfg.heads * D),
             'pre_h': e(B * S, cfg.llm_mlp),
+            # K cache [layer][batch][token][dim] (pair-interleaved dims);
+            # V cache transposed [layer][batch][dim][token]
             'kc': e(cfg.exp_layers, B, T, D),
-            'vc': e(cfg.exp_layers, B, T, D),
+            'vc': e(cfg.exp_layers, B, D, T),
             'pos_pre': e(B * S, dt=torch.int32),
             'pos_suf': e(B * Ss, dt=torch.int32),
-            'kgrp': e(B, T, dt=torch.int32),
+            'kgrp': e(B, S + Ss, dt=torch.int32),
             'qgrp_pre': e(B, S, dt=torch.int32),
             'qgrp_suf': e(B, Ss, dt=torch.int32),
             'ex_x': e(B, Ss, cfg.exp_hidden),
@@ -318,7 +327,7 @@ class PI0Inference:
         its K/V: its outputs feed nothing."""
         cfg, W = self.cfg, self.llm
         S, D, hid = cfg.prefix_len, cfg.head_dim, cfg.llm_hidden
-        T = S + cfg.suffix_len
+        T = self.kv_len
         n_img_tok = cfg.n_views * cfg.num_patches
         x = b['pre_x'].view(B * S, hid)
         K.embed_tokens(W['embed'], b['ids'],
@@ -332,14 +341,14 @@ class PI0Inference:
             wqkv = L['qkv_w'][cfg.heads * D:] if last else L['qkv_w']
             K.gemm_qkv_rope(x, wqkv, self.rope, b['pos_pre'],
                             b['pre_q'].view(B * S, -1),
-                            kc.view(B * T, D), vc.view(B * T, D),
-                            0 if last else cfg.heads, D,
-                            rownorm_eps=cfg.rms_eps, row_group=S,
-                            row_group_stride=T)
+                            kc.view(B * T, D), vc, 0 if last else cfg.heads,
+                            D, rownorm_eps=cfg.rms_eps, row_group=S,
+                            row_group_stride=T, v_ld=T)
             if last:
                 break
-            K.mqa_attention(b['pre_q'], kc[:, :S], vc[:, :S], b['pre_ctx'],
-                            kgrp=b['kgrp'][:, :S], qgrp=b['qgrp_pre'])
+            K.mqa_attention(b['pre_q'], kc[:, :S], vc, b['pre_ctx'],
+                            kgrp=b['kgrp'][:, :S], qgrp=b['qgrp_pre'],
+                            v_transposed=True)
             K.gemm(b['pre_ctx'].view(B * S, -1), L['o_w'], out=x, residual=x)
             K.gemm_geglu(x, L['gate_w'], L['up_w'], out=b['pre_h'],
                          rownorm_eps=cfg.rms_eps)
@@ -348,16 +357,16 @@ class PI0Inference:
     def _expert_layer_pi0(self, b, B, i, L):
         cfg = self.cfg
         S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
-        T = S + Ss
+        T = self.kv_len
         x = b['ex_x'].view(B * Ss, hid)
         kc, vc = b['kc'][i], b['vc'][i]
         K.gemm_qkv_rope(x, L['qkv_w'], self.rope, b['pos_suf'],
                         b['ex_q'].view(B * Ss, -1), kc.view(B * T, D)[S:],
-                        vc.view(B * T, D)[S:], cfg.heads, D,
+                        vc[:, :, S:], cfg.heads, D,
                         rownorm_eps=cfg.rms_eps, row_group=Ss,
-                        row_group_stride=T)
-        K.mqa_attention(b['ex_q'], kc, vc, b['ex_ctx'], kgrp=b['kgrp'],
-                        qgrp=b['qgrp_suf'])
+                        row_group_stride=T, v_ld=T)
+        K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
+                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True)
         K.gemm(b['ex_ctx'].view(B * Ss, -1), L['o_w'], out=x, residual=x)
         K.gemm_geglu(x, L['gate_w'], L['up_w'], out=b['ex_h'],
                      rownorm_eps=cfg.rms_eps)
@@ -366,7 +375,7 @@ class PI0Inference:
     def _expert_layer_pi05(self, b, B, i, L, step):
         cfg = self.cfg
         S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
-        T = S + Ss
+        T = self.kv_len
         x = b['ex_x'].view(B * Ss, hid)
         xn, gate = b['ex_xn'].view(B * Ss, hid), b['ex_gate'].view(B * Ss, hid)
         kc, vc = b['kc'][i], b['vc'][i]
@@ -375,10 +384,10 @@ class PI0Inference:
                       eps=cfg.rms_eps)
         K.gemm_qkv_rope(xn, L['qkv_w'], self.rope, b['pos_suf'],
                         b['ex_q'].view(B * Ss, -1), kc.view(B * T, D)[S:],
-                        vc.view(B * T, D)[S:], cfg.heads, D, row_group=Ss,
-                        row_group_stride=T)
-        K.mqa_attention(b['ex_q'], kc, vc, b['ex_ctx'], kgrp=b['kgrp'],
-                        qgrp=b['qgrp_suf'])
+                        vc[:, :, S:], cfg.heads, D, row_group=Ss,
+                        row_group_stride=T, v_ld=T)
+        K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
+                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True)
         K.gemm(b['ex_ctx'].view(B * Ss, -1), L['o_w'], out=x, residual=x,
                gate=gate)
         K.adarms_norm(x, st[2 * i + 1:2 * i + 2], out=xn, gate_out=gate,

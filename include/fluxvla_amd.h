@@ -90,7 +90,7 @@ typedef struct fvx_gemm_desc {
   const int32_t* positions;        /* [M] rope position per row */
   void* q_out; int64_t ldq;
   void* k_out; int64_t ldk;        /* rows remapped by orow() */
-  void* v_out; int64_t ldv;        /* rows remapped by orow() */
+  void* v_out; int64_t ldv;        /* rows remapped by orow(), or V^T: */
   int32_t n_q_heads, head_dim;
   /* EULER: xt[m*ldx + n] += dt * v ; xt_bf16 mirrors it in bf16 */
   float* xt; int64_t ldx;
@@ -98,7 +98,10 @@ typedef struct fvx_gemm_desc {
   /* split-K workspace (may be NULL) */
   void* workspace; int64_t workspace_bytes;
   int32_t split_k;                 /* 0 = choose automatically */
-  int32_t reserved;
+  /* QKV_ROPE with v_transposed: V is written transposed, element (m, d) at
+   * v_out[((m / row_group) * head_dim + d) * ldv + m % row_group] (the
+   * [batch][head_dim][tokens] value-cache layout the attention reads). */
+  int32_t v_transposed;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */
@@ -157,12 +160,20 @@ int fvx_adarms_norm(const void* x, const void* style, void* out,
  * kgrp/qgrp means no mask.  This encodes make_att_2d_masks
  * (fluxvla/engines/utils/model_utils.py:77-95): kgrp = pad ? cumsum(att) :
  * INT32_MAX, qgrp = cumsum(att).  Rows that see no key produce zeros.
- * kv_splits > 1 splits the key range across workgroups (needs workspace).
+ * kv_splits > 1 splits the key range across workgroups (needs workspace);
+ * the split partials are merged by a second kernel on the same stream.
+ * Decode-shaped problems (at most 512 query rows per problem) with a
+ * transposed value cache run a barrier-free kernel in which every wave owns
+ * 16 query rows and one key range.
  */
 typedef struct fvx_attn_desc {
   const void* q; int64_t q_tok_stride, q_head_stride, q_zs1, q_zs2;
   const void* k; int64_t k_tok_stride, k_zs1, k_zs2;
   const void* v; int64_t v_tok_stride, v_zs1, v_zs2;
+  /* v_d_stride > 0: V is stored transposed (the value cache), element
+   * (key j, dim d) at v[d * v_d_stride + j]; v_tok_stride is then unused.
+   * Needs sk <= v_d_stride and v_d_stride % 8 == 0. */
+  int64_t v_d_stride;
   void* o; int64_t o_tok_stride, o_head_stride, o_zs1, o_zs2;
   const int32_t* kgrp; int64_t kgrp_zs1;
   const int32_t* qgrp; int64_t qgrp_zs1;

@@ -201,8 +201,9 @@ def interleave_perm(hd):
 
 
 @pytest.mark.parametrize('m,k,start', [(51, 1024, 816), (816, 2048, 0)])
-def test_gemm_qkv_rope(K, cuda, m, k, start):
-    announce(f'gemm qkv_rope m={m} k={k}')
+@pytest.mark.parametrize('vt', [False, True])
+def test_gemm_qkv_rope(K, cuda, m, k, start, vt):
+    announce(f'gemm qkv_rope m={m} k={k} v_transposed={vt}')
     nq, hd = 8, 256
     x = randn((m, k), 60, std=1.5)
     wq = randn((nq * hd, k), 61, std=0.02)
@@ -217,8 +218,13 @@ def test_gemm_qkv_rope(K, cuda, m, k, start):
     q = torch.empty(m, nq * hd, dtype=torch.bfloat16, device=cuda)
     kk = torch.zeros(m + 10, hd, dtype=torch.bfloat16, device=cuda)
     vv = torch.zeros(m + 10, hd, dtype=torch.bfloat16, device=cuda)
+    vtc = torch.zeros(hd, m + 24, dtype=torch.bfloat16, device=cuda)
     K.gemm_qkv_rope(x.to(cuda), w.to(cuda), rope, pos.to(cuda), q, kk[5:],
-                    vv[5:], nq, hd, rownorm_eps=1e-6)
+                    vtc[:, 8:] if vt else vv[5:], nq, hd, rownorm_eps=1e-6,
+                    v_ld=m + 24 if vt else None)
+    if vt:
+        assert vtc[:, :8].abs().max().item() == 0.0
+        vv[5:5 + m] = vtc[:, 8:8 + m].t()
     xf = x.double()
     xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
     rq = rope_ref((xn @ wq.double().t()).view(m, nq, hd), pos, hd)
@@ -264,14 +270,22 @@ def sdpa_ref(q, k, v, mask=None, scale=None):
 
 
 @pytest.mark.parametrize('splits', [0, 1])
-def test_attention_prefix_mqa(K, cuda, splits):
-    announce(f'attention prefix mqa 816 splits={splits}')
+@pytest.mark.parametrize('vt', [False, True])
+def test_attention_prefix_mqa(K, cuda, splits, vt):
+    announce(f'attention prefix mqa 816 splits={splits} v_transposed={vt}')
     S, H, D = 816, 8, 256
     q = randn((1, S, H, D), 80)
     k = randn((1, S, D), 81)
     v = randn((1, S, D), 82)
     o = torch.empty(1, S, H, D, dtype=torch.bfloat16, device=cuda)
-    K.mqa_attention(q.to(cuda), k.to(cuda), v.to(cuda), o, kv_splits=splits)
+    if vt:  # value cache [B, D, T] with spare token columns
+        vv = torch.zeros(1, D, S + 56, dtype=torch.bfloat16)
+        vv[:, :, :S] = v.transpose(1, 2)
+        K.mqa_attention(q.to(cuda), k.to(cuda), vv.to(cuda), o,
+                        kv_splits=splits, v_transposed=True)
+    else:
+        K.mqa_attention(q.to(cuda), k.to(cuda), v.to(cuda), o,
+                        kv_splits=splits)
     ref = sdpa_ref(q.float().transpose(1, 2), k.float()[:, None],
                    v.float()[:, None]).transpose(1, 2)
     assert rel_err(o, ref) <= REL_TOL
@@ -299,24 +313,34 @@ def test_attention_prefix_padded(K, cuda):
 
 
 @pytest.mark.parametrize('splits', [0, 1, 5])
-def test_attention_decode_block_causal(K, cuda, splits):
-    """PI0 suffix: state token sees prefix + itself, actions see all."""
-    announce(f'attention decode block-causal splits={splits}')
+@pytest.mark.parametrize('vt', [False, True])
+@pytest.mark.parametrize('batch', [1, 3])
+def test_attention_decode_block_causal(K, cuda, splits, vt, batch):
+    """PI0 suffix: state token sees prefix + itself, actions see all.  With a
+    transposed value cache this runs the barrier-free decode kernel."""
+    announce(f'attention decode block-causal splits={splits} vt={vt} '
+             f'batch={batch}')
     P, Ssuf, H, D = 816, 51, 8, 256
     T = P + Ssuf
-    q = randn((1, Ssuf, H, D), 90)
-    cache_k = randn((1, T + 13, D), 91)
-    cache_v = randn((1, T + 13, D), 92)
+    Ta = T + 13 if not vt else 872
+    q = randn((batch, Ssuf, H, D), 90)
+    cache_k = randn((batch, Ta, D), 91)
+    cache_v = randn((batch, Ta, D), 92)
     att = torch.tensor([1, 1] + [0] * 49)
     cum = torch.cumsum(att, 0).to(torch.int32)
-    kgrp = torch.cat([torch.zeros(P, dtype=torch.int32), cum])[None]
-    qgrp = cum[None]
-    o = torch.empty(1, Ssuf, H, D, dtype=torch.bfloat16, device=cuda)
-    kc, vc = cache_k.to(cuda), cache_v.to(cuda)
-    K.mqa_attention(q.to(cuda), kc[:, :T], vc[:, :T], o, kgrp.to(cuda),
-                    qgrp.to(cuda), kv_splits=splits)
-    mask = torch.ones(1, Ssuf, T, dtype=torch.bool)
-    mask[0, 0, P + 1:] = False
+    kgrp = torch.cat([torch.zeros(P, dtype=torch.int32), cum])[None].repeat(
+        batch, 1)
+    kgrp[-1, 100:140] = 2**31 - 1  # padded prefix keys in the last sample
+    qgrp = cum[None].repeat(batch, 1)
+    o = torch.empty(batch, Ssuf, H, D, dtype=torch.bfloat16, device=cuda)
+    kc = cache_k.to(cuda)
+    if vt:
+        vc = cache_v.transpose(1, 2).contiguous().to(cuda)
+    else:
+        vc = cache_v.to(cuda)[:, :T]
+    K.mqa_attention(q.to(cuda), kc[:, :T], vc, o, kgrp.to(cuda),
+                    qgrp.to(cuda), kv_splits=splits, v_transposed=vt)
+    mask = (kgrp[:, None, :] <= qgrp[:, :, None])
     ref = sdpa_ref(q.float().transpose(1, 2), cache_k[:, :T].float()[:, None],
                    cache_v[:, :T].float()[:, None], mask).transpose(1, 2)
     assert rel_err(o, ref) <= REL_TOL

@@ -81,7 +81,7 @@ def test_prefix_kv_cache_matches_oracle(models, cuda):
     S = cfg.prefix_len
     for i, (k, v) in enumerate(kvs):
         gk = b['kc'][i, 0, :S].cpu()[:, inv]
-        gv = b['vc'][i, 0, :S].cpu()
+        gv = b['vc'][i, 0, :, :S].t().cpu()
         assert rel_err(gk, k[0, 0]) <= 1e-2, f'layer {i} K'
         assert rel_err(gv, v[0, 0]) <= 1e-2, f'layer {i} V'
 
