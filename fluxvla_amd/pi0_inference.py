@@ -167,6 +167,54 @@ def sinusoid(times, dim, min_period=4e-3, max_period=4.0):
     return torch.cat([torch.sin(x), torch.cos(x)], dim=-1)
 
 
+def suffix_att_pattern(cfg: PI0Config):
+    """Suffix attention-mask pattern: PI0 [1, 1, 0 x 49] (state block, then
+    the action block; pi0_flowmatching.py:274-313), PI0.5 [1, 0 x 49]
+    (pi05_flowmatching.py:112-120)."""
+    na = cfg.n_action_steps
+    return [1] + [0] * (na - 1) if cfg.pi05 else [1, 1] + [0] * (na - 1)
+
+
+def attention_groups(prefix_pad, suffix_att):
+    """The prefix/suffix masks as the kernels consume them.
+
+    make_att_2d_masks (model_utils.py:77-95) over [prefix (att all 0) |
+    suffix] lets query token i see key j iff cumsum(att)[j] <= cumsum(att)[i]
+    and both are valid; denoise_step shows every suffix row all valid prefix
+    keys (pi0_flowmatching.py:802-813).  So with
+        kgrp[j] = cumsum(att)[j] if key j is valid else INT32_MAX
+        qgrp[i] = cumsum(att)[i]
+    key j is visible to valid query i iff kgrp[j] <= qgrp[i].  Positions
+    follow the PyTorch path: prefix cumsum(pad) - 1, suffix sum(prefix_pad)
+    + cumsum(suffix_pad) - 1 (pi0_flowmatching.py:729-730, 817-819).
+
+    prefix_pad: bool [B, S]; suffix_att: int/bool [Ss] (all suffix tokens
+    valid).  Returns int32 kgrp [B, S + Ss], qgrp_prefix [B, S],
+    qgrp_suffix [B, Ss], pos_prefix [B, S], pos_suffix [B, Ss]."""
+    B, S = prefix_pad.shape
+    dev = prefix_pad.device
+    pad = prefix_pad.bool()
+    scum = torch.cumsum(torch.as_tensor(suffix_att, dtype=torch.int32,
+                                        device=dev), 0).to(torch.int32)
+    Ss = scum.numel()
+    kg_pre = torch.where(pad, 0, INT32_MAX).to(torch.int32)
+    kgrp = torch.cat([kg_pre, scum[None].expand(B, Ss)], dim=1)
+    qgrp_pre = torch.zeros(B, S, dtype=torch.int32, device=dev)
+    qgrp_suf = scum[None].expand(B, Ss).contiguous()
+    pos_pre = (torch.cumsum(pad.int(), 1) - 1).to(torch.int32)
+    off = pad.int().sum(1, keepdim=True)
+    pos_suf = (off + torch.arange(Ss, device=dev, dtype=torch.int32)).to(
+        torch.int32)
+    return kgrp, qgrp_pre, qgrp_suf, pos_pre, pos_suf
+
+
+def prefix_pad_mask(img_masks, lang_masks, num_patches):
+    """embed_prefix pad mask (pi0_flowmatching.py:216-247): each camera's
+    mask repeated over its patches, then the prompt mask."""
+    return torch.cat([img_masks.bool().repeat_interleave(num_patches, dim=1),
+                      lang_masks.bool()], dim=1)
+
+
 # ---------------------------------------------------------------------------
 # The inference model
 # ---------------------------------------------------------------------------
@@ -468,20 +516,14 @@ class PI0Inference:
             lang_masks = torch.ones(B, L, dtype=torch.bool, device=dev)
         lm = torch.zeros(B, cfg.max_prompt_len, dtype=torch.bool, device=dev)
         lm[:, :L] = lang_masks.to(dev).bool()
-        pad = torch.cat([img_masks.to(dev).bool().repeat_interleave(
-            cfg.num_patches, dim=1), lm], dim=1)
-        # make_att_2d_masks over [prefix (att 0) | suffix (att pattern)]
-        na = cfg.n_action_steps
-        satt = [1] + [0] * (na - 1) if cfg.pi05 else [1, 1] + [0] * (na - 1)
-        scum = torch.cumsum(torch.tensor(satt, dtype=torch.int32), 0).to(dev)
-        kg_pre = torch.where(pad, 0, INT32_MAX).to(torch.int32)
-        b['kgrp'].copy_(torch.cat([kg_pre, scum[None].expand(B, -1)], 1))
-        b['qgrp_suf'].copy_(scum[None].expand(B, -1))
-        b['qgrp_pre'].zero_()
-        b['pos_pre'].copy_((torch.cumsum(pad.int(), 1) - 1).view(-1))
-        off = pad.int().sum(1, keepdim=True)
-        b['pos_suf'].copy_((off + torch.arange(cfg.suffix_len, device=dev,
-                                               dtype=torch.int32)).view(-1))
+        pad = prefix_pad_mask(img_masks.to(dev), lm, cfg.num_patches)
+        kgrp, qg_pre, qg_suf, pos_pre, pos_suf = attention_groups(
+            pad, suffix_att_pattern(cfg))
+        b['kgrp'].copy_(kgrp)
+        b['qgrp_pre'].copy_(qg_pre)
+        b['qgrp_suf'].copy_(qg_suf)
+        b['pos_pre'].copy_(pos_pre.view(-1))
+        b['pos_suf'].copy_(pos_suf.view(-1))
         if not cfg.pi05:
             b['states'].copy_(states.to(dev, BF16), non_blocking=True)
         b['xt'].copy_(noise, non_blocking=True)

@@ -1,0 +1,107 @@
+"""Host-side logic of the product path, checked on the CPU against the
+oracle: weight preparation (norm folds, pair-interleaved Q/K rows, QKV
+stacking, patch-weight flattening), the per-step time tables, and the
+library's refusal to run without its HIP shared object."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from fluxvla_amd import pi0_inference as P
+from fluxvla_amd.config import tiny
+from fluxvla_amd.weights import make_state_dict
+from oracle import pi0_oracle as O
+
+
+@pytest.fixture(scope='module')
+def small():
+    cfg = tiny(vit_hidden=64, vit_heads=4, vit_layers=1, vit_mlp=96,
+               llm_hidden=64, llm_mlp=96, heads=4, head_dim=16, llm_layers=1,
+               exp_hidden=32, exp_mlp=48, exp_layers=1, image_size=28,
+               patch=14, proj_width=32, max_prompt_len=4)
+    sd = {k: v for k, v in make_state_dict(cfg, seed=21).items()}
+    return cfg, sd
+
+
+@pytest.mark.parametrize('role', ['llm', 'expert'])
+def test_gemma_prep_equals_norm_then_linear(small, role):
+    """x @ qkv_w'^T * rms(x) == [q | k | v](gemma_rms_norm(x)) with Q/K in
+    pair-interleaved order; gate/up likewise with the post-attn norm."""
+    cfg, sd = small
+    W = P.prepare_gemma(sd, cfg, role, 'cpu')
+    pre = ('llm_backbone' if role == 'llm' else 'llm_expert') + '.layers.0'
+    hid = cfg.llm_hidden if role == 'llm' else cfg.exp_hidden
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(5, hid, generator=g)
+    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.rms_eps)
+    L = W['layers'][0]
+    got = (x @ L['qkv_w'].float().t()) * r
+    xn = O.gemma_rms_norm(x, sd[f'{pre}.input_layernorm.weight'], cfg.rms_eps)
+    q = O.linear(xn, sd[f'{pre}.self_attn.q_proj.weight'])
+    k = O.linear(xn, sd[f'{pre}.self_attn.k_proj.weight'])
+    v = O.linear(xn, sd[f'{pre}.self_attn.v_proj.weight'])
+    perm = P.interleave_rows(cfg.head_dim)
+    q = q.view(5, cfg.heads, cfg.head_dim)[:, :, perm].reshape(5, -1)
+    want = torch.cat([q, k[:, perm], v], 1)
+    assert torch.allclose(got, want, atol=2e-2 * want.abs().max().item())
+    xn2 = O.gemma_rms_norm(x, sd[f'{pre}.post_attention_layernorm.weight'],
+                           cfg.rms_eps)
+    got_g = (x @ L['gate_w'].float().t()) * r
+    want_g = O.linear(xn2, sd[f'{pre}.mlp.gate_proj.weight'])
+    assert torch.allclose(got_g, want_g, atol=2e-2 * want_g.abs().max().item())
+
+
+def test_final_norm_fold_into_action_out(small):
+    cfg, sd = small
+    W = P.prepare_gemma(sd, cfg, 'expert', 'cpu')
+    w_out = (sd['action_out_proj.projector.weight'].float() *
+             W['final_scale'][None])
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(3, cfg.exp_hidden, generator=g)
+    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.rms_eps)
+    got = (x @ w_out.t()) * r
+    want = O.linear(O.gemma_rms_norm(x, sd['llm_expert.norm.weight'],
+                                     cfg.rms_eps),
+                    sd['action_out_proj.projector.weight'])
+    assert torch.allclose(got, want, atol=1e-4)
+
+
+def test_siglip_patch_weight_order(small):
+    """im2col column order (c, ky, kx) against conv2d."""
+    cfg, sd = small
+    V = P.prepare_siglip(sd, cfg, 'cpu')
+    g = torch.Generator().manual_seed(3)
+    img = torch.rand(2, 3, 28, 28, generator=g)
+    p = cfg.patch
+    cols = F.unfold(img, p, stride=p).transpose(1, 2)  # (c, ky, kx) order
+    cols = F.pad(cols, (0, cfg.patch_k_pad - cfg.patch_k))
+    got = cols @ V['patch_w'].float().t() + V['patch_b'].float()
+    w = sd[f'{P.VIS}.embeddings.patch_embedding.weight'].float()
+    ref = F.conv2d(img, w, V['patch_b'].float(), stride=p)
+    ref = ref.flatten(2).transpose(1, 2)
+    assert torch.allclose(got, ref, atol=1e-4)
+    L = V['layers'][0]
+    assert L['qkv_w'].shape == (3 * cfg.vit_hidden, cfg.vit_hidden)
+
+
+def test_time_tables_match_oracle():
+    ts, dt = P.euler_times(10)
+    assert ts == O.euler_times(10)
+    assert dt == float(torch.tensor(-0.1, dtype=torch.float32))
+    emb = P.sinusoid(ts, 64)
+    ref = O.sinusoidal_pos_embedding(torch.tensor(ts), 64, 4e-3, 4.0)
+    assert torch.equal(emb, ref)
+
+
+def test_kv_len_is_vector_aligned():
+    cfg = tiny()
+    obj = P.PI0Inference.__new__(P.PI0Inference)
+    obj.cfg = cfg
+    assert obj.kv_len % 8 == 0 and obj.kv_len >= cfg.prefix_len + cfg.suffix_len
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from fluxvla_amd import _lib
+    monkeypatch.setattr(_lib, 'LIB_PATH', str(tmp_path / 'absent.so'))
+    monkeypatch.setattr(_lib, '_lib', None)
+    with pytest.raises(ImportError, match='not built'):
+        _lib.load()

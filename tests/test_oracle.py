@@ -1,0 +1,347 @@
+"""Pins of the CPU oracle (oracle/pi0_oracle.py) -- each check is chosen so a
+plausible mistake (dropped term, wrong sign/index, transposed operand) fails:
+
+* the reference's own input fixtures (tests/golden/reference_masks.npz,
+  copied from test/data/models/vlas/pi0{,5}) for prefix/suffix mask
+  assembly and the 2-D attention mask;
+* library routines: HF transformers' GemmaDecoderLayer / GemmaRMSNorm /
+  GemmaRotaryEmbedding and SiglipVisionModel (random init, same weights),
+  torch scaled_dot_product_attention;
+* invariants and closed forms: RoPE relative-position property, attention
+  mask zeroing, adaRMS reduction, Euler loop with a constant velocity,
+  brute-force mask rule on tiny inputs.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from fluxvla_amd.config import PI0Config, tiny
+from fluxvla_amd.weights import make_inputs, make_state_dict
+from oracle import pi0_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), 'golden',
+                      'reference_masks.npz')
+
+
+@pytest.fixture(scope='module')
+def golden():
+    return dict(np.load(GOLDEN, allow_pickle=False))
+
+
+# ---------------------------------------------------------------------------
+# masks and positions
+# ---------------------------------------------------------------------------
+def brute_force_2d(pad, att):
+    """The mask rule stated in the reference (model_utils.py:77-95 after
+    big_vision): i sees j iff j is not in a later block than i and both are
+    valid; blocks start where att == 1.  Loops, no cumsum."""
+    B, S = pad.shape
+    out = torch.zeros(B, S, S, dtype=torch.bool)
+    for b in range(B):
+        block = []
+        cur = 0
+        for j in range(S):
+            cur += int(att[b, j])
+            block.append(cur)
+        for i in range(S):
+            for j in range(S):
+                out[b, i, j] = (block[j] <= block[i] and bool(pad[b, i])
+                                and bool(pad[b, j]))
+    return out
+
+
+def test_make_att_2d_masks_brute_force():
+    g = torch.Generator().manual_seed(0)
+    pad = torch.rand(3, 13, generator=g) > 0.2
+    att = torch.rand(3, 13, generator=g) > 0.6
+    assert torch.equal(O.make_att_2d_masks(pad, att), brute_force_2d(pad, att))
+
+
+def test_prefix_pad_mask_from_reference_fixture(golden):
+    """pi05 fixture: img_masks [1,1,0] (missing third camera) + 200-token
+    prompt masks -> the stored prefix_pad_masks (968 = 3 * 256 + 200)."""
+    from fluxvla_amd.pi0_inference import prefix_pad_mask
+    img = torch.from_numpy(golden['pi05_img_masks'])
+    lang = torch.from_numpy(golden['pi05_lang_masks'])
+    want = torch.from_numpy(golden['pi05_prefix_pad_masks']).bool()
+    assert torch.equal(prefix_pad_mask(img, lang, 256), want)
+    # the oracle's embed_prefix builds the same mask (pi0_flowmatching.py
+    # :216-247); run its mask logic on the fixture shapes
+    B = img.shape[0]
+    pads = [img[:, i:i + 1].expand(B, 256) for i in range(img.shape[1])]
+    assert torch.equal(torch.cat(pads + [lang], 1), want)
+
+
+def test_suffix_patterns_match_reference_fixtures(golden):
+    from fluxvla_amd.pi0_inference import suffix_att_pattern
+    pi0 = torch.from_numpy(golden['pi0_suffix_att_masks'])
+    pi05 = torch.from_numpy(golden['pi05_suffix_att_masks']).bool()
+    cfg0 = PI0Config()
+    cfg5 = PI0Config(pi05=True, n_action_steps=pi05.shape[1])
+    assert pi0.shape[1] == cfg0.suffix_len
+    for row in pi0:
+        assert row.int().tolist() == suffix_att_pattern(cfg0)
+    for row in pi05:
+        assert row.int().tolist() == suffix_att_pattern(cfg5)
+    # and the oracle's embed_suffix emits the same patterns
+    cfg = tiny()
+    sd = make_state_dict(cfg.scaled(vit_layers=0, llm_layers=0, exp_layers=0))
+    x = torch.zeros(2, cfg.n_action_steps, cfg.max_action_dim)
+    _, _, att, _ = O.embed_suffix(sd, cfg, torch.zeros(2, 32), x,
+                                  torch.tensor([0.5, 0.5]))
+    assert torch.equal(att, pi0)
+
+
+@pytest.mark.parametrize('which', ['pi0', 'pi05'])
+def test_kernel_mask_encoding_equals_2d_mask(golden, which):
+    """Product encoding kgrp[j] <= qgrp[i] == the oracle's full 2-D mask of
+    denoise_step (prefix pad 2-D | suffix block mask) on the reference's
+    own masks, and the prefix mask for valid query rows; positions equal
+    cumsum-based position ids."""
+    from fluxvla_amd.pi0_inference import attention_groups
+    ppad = torch.from_numpy(golden[f'{which}_prefix_pad_masks']).bool()
+    patt = torch.from_numpy(golden[f'{which}_prefix_att_masks']).bool()
+    spad = torch.from_numpy(golden[f'{which}_suffix_pad_masks']).bool()
+    satt = torch.from_numpy(golden[f'{which}_suffix_att_masks']).bool()
+    assert not patt.any()
+    B, S = ppad.shape
+    Ss = spad.shape[1]
+    kgrp, qg_pre, qg_suf, pos_pre, pos_suf = attention_groups(
+        ppad, satt[0].int().tolist())
+    # suffix rows (denoise_step, pi0_flowmatching.py:796-813)
+    full = torch.cat([ppad[:, None, :].expand(B, Ss, S),
+                      O.make_att_2d_masks(spad, satt)], dim=2)
+    enc = kgrp[:, None, :] <= qg_suf[:, :, None]
+    assert torch.equal(enc, full)
+    # prefix rows, valid queries (predict_action :728-730)
+    pm = O.make_att_2d_masks(ppad, patt)
+    enc_p = kgrp[:, None, :S] <= qg_pre[:, :, None]
+    assert torch.equal(enc_p & ppad[:, :, None], pm)
+    assert torch.equal(pos_pre.long(), torch.cumsum(ppad.long(), 1) - 1)
+    want_suf = ppad.sum(-1, keepdim=True) + torch.cumsum(spad.long(), 1) - 1
+    assert torch.equal(pos_suf.long(), want_suf)
+
+
+# ---------------------------------------------------------------------------
+# Gemma: against HF transformers' Gemma modules (library routine)
+# ---------------------------------------------------------------------------
+def _small_gemma_cfg():
+    return tiny(llm_hidden=64, llm_mlp=96, heads=4, head_dim=16,
+                llm_layers=2)
+
+
+def _hf_gemma(cfg):
+    from transformers import GemmaConfig
+    from transformers.models.gemma.modeling_gemma import (
+        GemmaDecoderLayer, GemmaRMSNorm, GemmaRotaryEmbedding)
+    hc = GemmaConfig(hidden_size=cfg.llm_hidden,
+                     intermediate_size=cfg.llm_mlp,
+                     num_attention_heads=cfg.heads, num_key_value_heads=1,
+                     head_dim=cfg.head_dim, num_hidden_layers=cfg.llm_layers,
+                     vocab_size=16, rms_norm_eps=cfg.rms_eps,
+                     rope_theta=cfg.rope_theta,
+                     hidden_act='gelu_pytorch_tanh',
+                     hidden_activation='gelu_pytorch_tanh',
+                     attention_dropout=0.0)
+    hc._attn_implementation = 'eager'
+    layers = [GemmaDecoderLayer(hc, i) for i in range(cfg.llm_layers)]
+    return hc, layers, GemmaRMSNorm(cfg.llm_hidden, eps=cfg.rms_eps), \
+        GemmaRotaryEmbedding(hc)
+
+
+def test_gemma_layers_match_hf():
+    cfg = _small_gemma_cfg()
+    sd = {k: v.float() for k, v in make_state_dict(cfg, seed=3).items()
+          if k.startswith('llm_backbone.')}
+    hc, layers, norm, rot = _hf_gemma(cfg)
+    for i, layer in enumerate(layers):
+        pre = f'llm_backbone.layers.{i}.'
+        layer.load_state_dict({k[len(pre):]: v for k, v in sd.items()
+                               if k.startswith(pre)})
+    norm.load_state_dict({'weight': sd['llm_backbone.norm.weight']})
+    g = torch.Generator().manual_seed(1)
+    B, S = 2, 11
+    x = torch.randn(B, S, cfg.llm_hidden, generator=g)
+    pad = torch.ones(B, S, dtype=torch.bool)
+    pad[1, 8:] = False
+    att = torch.zeros(B, S, dtype=torch.bool)
+    att[:, 5] = True  # two blocks: bidirectional inside, causal across
+    mask = O.make_att_2d_masks(pad, att)
+    pos = torch.cumsum(pad.long(), 1) - 1
+    got, kvs = O.gemma_model(sd, 'llm_backbone', cfg.llm_layers, x, pos, mask,
+                             cfg)
+    add = torch.zeros(B, 1, S, S).masked_fill(~mask[:, None], O.BF16_MIN)
+    h = x
+    with torch.no_grad():
+        pe = rot(h, pos)
+        for layer in layers:
+            out = layer(h, attention_mask=add, position_ids=pos,
+                        position_embeddings=pe)
+            h = out[0] if isinstance(out, tuple) else out
+        ref = norm(h)
+    valid = pad[:, :, None].expand_as(ref)
+    err = (got - ref)[valid].abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item()
+    # the KV of layer 0 is the rotated K / plain V of the normed input
+    assert kvs[0][0].shape == (B, 1, S, cfg.head_dim)
+
+
+def test_rope_relative_position_and_norm():
+    """<R(p) q, R(p') k> depends only on p - p'; rotations keep norms."""
+    D = 32
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(1, 1, 1, D, generator=g)
+    k = torch.randn(1, 1, 1, D, generator=g)
+
+    def dot(p, pk):
+        cq, sq = O.rope_cos_sin(torch.tensor([[p]]), D, 10000.0)
+        ck, sk = O.rope_cos_sin(torch.tensor([[pk]]), D, 10000.0)
+        rq, _ = O.apply_rope(q, q, cq, sq)
+        rk, _ = O.apply_rope(k, k, ck, sk)
+        return (rq * rk).sum().item(), rq.norm().item()
+
+    a, na = dot(7, 3)
+    b, nb = dot(107, 103)
+    assert abs(a - b) < 1e-3
+    assert abs(na - q.norm().item()) < 1e-4
+
+
+def test_interleaved_rope_layout_preserves_scores():
+    """Permuting Q/K rows to pair-interleaved order (the kernels' layout,
+    condition_gemma_inference.py:46-63) leaves Q K^T unchanged."""
+    from fluxvla_amd.pi0_inference import interleave_rows
+    D = 16
+    perm = interleave_rows(D)
+    assert sorted(perm.tolist()) == list(range(D))
+    # pair (i, i + D/2) lands on (2i, 2i + 1)
+    for i in range(D // 2):
+        assert perm[2 * i].item() == i and perm[2 * i + 1].item() == i + D // 2
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(5, D, generator=g)
+    k = torch.randn(7, D, generator=g)
+    assert torch.allclose(q @ k.t(), q[:, perm] @ k[:, perm].t(), atol=1e-6)
+
+
+def test_attention_matches_sdpa_and_masks_zero():
+    g = torch.Generator().manual_seed(4)
+    B, H, Sq, Sk, D = 2, 4, 5, 9, 16
+    q = torch.randn(B, H, Sq, D, generator=g)
+    k = torch.randn(B, 1, Sk, D, generator=g)
+    v = torch.randn(B, 1, Sk, D, generator=g)
+    mask = torch.rand(B, Sq, Sk, generator=g) > 0.3
+    mask[:, :, 0] = True
+    got = O.attention(q, k, v, mask, D**-0.5)
+    ref = F.scaled_dot_product_attention(
+        q, k.expand(-1, H, -1, -1), v.expand(-1, H, -1, -1),
+        attn_mask=mask[:, None])
+    assert torch.allclose(got, ref, atol=1e-5)
+    # perturbing masked values changes nothing
+    v2 = v.clone()
+    v2[~mask.any(1)[:, None, :, None].expand_as(v2)] += 100.0
+    assert torch.allclose(O.attention(q, k, v2, mask, D**-0.5), got,
+                          atol=1e-5)
+
+
+def test_adarms_reduces_to_plain_rms():
+    """Zero modulation -> plain RMSNorm with w = 0 (condition_gemma.py:70)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 4, 16, generator=g)
+    cond = torch.randn(3, 8, generator=g)
+    y, gate = O.ada_rms_norm(x, cond, torch.zeros(48, 8), torch.zeros(48),
+                             1e-6)
+    assert torch.allclose(y, O.gemma_rms_norm(x, torch.zeros(16), 1e-6))
+    assert gate.abs().max().item() == 0.0
+    # and RMSNorm output has unit RMS when w = 0
+    r = O.gemma_rms_norm(x, torch.zeros(16), 0.0)
+    assert torch.allclose(r.pow(2).mean(-1), torch.ones(3, 4), atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# SigLIP: against HF transformers' SiglipVisionModel
+# ---------------------------------------------------------------------------
+def test_siglip_tower_matches_hf():
+    from transformers import SiglipVisionConfig, SiglipVisionModel
+    cfg = tiny(vit_hidden=64, vit_heads=4, vit_layers=2, vit_mlp=96,
+               image_size=28, patch=14)
+    sd = make_state_dict(cfg.scaled(llm_layers=0, exp_layers=0), seed=6)
+    sd = {k: v.float() for k, v in sd.items()}
+    hc = SiglipVisionConfig(hidden_size=64, intermediate_size=96,
+                            num_attention_heads=4, num_hidden_layers=2,
+                            image_size=28, patch_size=14, layer_norm_eps=1e-6,
+                            hidden_act='gelu_pytorch_tanh',
+                            attention_dropout=0.0)
+    hc._attn_implementation = 'eager'
+    model = SiglipVisionModel(hc).eval()
+    # transformers 4.53.2 (the reference's pin) nests the tower under
+    # `vision_model.`; 5.x does not -- accept whichever this install uses.
+    nested = any(k.startswith('vision_model.') for k in model.state_dict())
+    pre = 'vision_backbone.vision.' + ('' if nested else 'vision_model.')
+    hf_sd = {k[len(pre):]: v for k, v in sd.items() if k.startswith(pre)}
+    missing, unexpected = model.load_state_dict(hf_sd, strict=False)
+    assert not unexpected
+    assert all('head' in m or 'position_ids' in m for m in missing), missing
+    g = torch.Generator().manual_seed(7)
+    px = torch.rand(2, 3, 28, 28, generator=g) * 2 - 1
+    with torch.no_grad():
+        ref = model(pixel_values=px).last_hidden_state
+    got = O.siglip_tower(sd, px, cfg)
+    assert (got - ref).abs().max().item() <= 1e-4 * ref.abs().max().item()
+
+
+# ---------------------------------------------------------------------------
+# time embedding and the Euler loop
+# ---------------------------------------------------------------------------
+def test_sinusoidal_embedding_closed_form():
+    d = 16
+    e0 = O.sinusoidal_pos_embedding(torch.tensor([0.0]), d, 4e-3, 4.0)
+    assert torch.allclose(e0[0, :8], torch.zeros(8))
+    assert torch.allclose(e0[0, 8:], torch.ones(8))
+    # the slowest component has period max_period: sin(2 pi t / 4)
+    t = torch.tensor([0.5])
+    e = O.sinusoidal_pos_embedding(t, d, 4e-3, 4.0)
+    assert abs(e[0, 7].item() - math.sin(2 * math.pi * 0.5 / 4.0)) < 1e-6
+    assert abs(e[0, 0].item() - math.sin(2 * math.pi * 0.5 / 4e-3)) < 1e-3
+
+
+@pytest.mark.parametrize('n', [1, 2, 3, 7, 10, 16, 25])
+def test_euler_schedule(n):
+    """Exactly n steps, starting at t = 1, ending near 1/n, decreasing."""
+    from fluxvla_amd.pi0_inference import euler_times
+    ts = O.euler_times(n)
+    assert len(ts) == n and ts[0] == 1.0
+    assert abs(ts[-1] - 1.0 / n) < 1e-5
+    assert all(a > b for a, b in zip(ts, ts[1:]))
+    assert euler_times(n)[0] == ts
+
+
+def test_predict_action_constant_velocity():
+    """Zero expert weights and zero action_out weight make v = bias for
+    every step: the loop then returns noise - bias (sum of dt = -1)."""
+    cfg = tiny(vit_layers=1, llm_layers=1, exp_layers=1)
+    sd = make_state_dict(cfg, seed=8)
+    for k in list(sd):
+        if k.startswith('llm_expert.') or k == 'action_out_proj.projector.weight':
+            sd[k] = torch.zeros_like(sd[k])
+    inp = make_inputs(cfg, batch=1, seed=9)
+    out = O.predict_action(sd, cfg, inp['images'], inp['lang_tokens'],
+                           inp['states'], noise=inp['noise'], num_steps=4)
+    bias = sd['action_out_proj.projector.bias'].float()
+    assert torch.allclose(out, inp['noise'] - bias, atol=1e-5)
+
+
+def test_one_step_equals_single_denoise():
+    cfg = tiny(vit_layers=1, llm_layers=1, exp_layers=1)
+    sd = make_state_dict(cfg, seed=10)
+    inp = make_inputs(cfg, batch=1, seed=11)
+    out = O.predict_action(sd, cfg, inp['images'], inp['lang_tokens'],
+                           inp['states'], noise=inp['noise'], num_steps=1)
+    kvs, pad = O.prefix_forward(sd, cfg, inp['images'], inp['lang_tokens'],
+                                torch.ones(1, 3, dtype=torch.bool),
+                                torch.ones(1, 48, dtype=torch.bool))
+    v = O.denoise_step(sd, cfg, inp['states'], pad, kvs, inp['noise'],
+                       torch.tensor([1.0]))
+    assert torch.allclose(out, inp['noise'] - v, atol=1e-5)
