@@ -34,6 +34,18 @@ def log(msg):
     print(f'[bench] {msg}', file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE passes (counter-calibrated)."""
+    import re
+    path = os.path.join(ROOT, 'profiles', 'prefix_geglu_gemm_traffic.md')
+    try:
+        m = re.search(r'traffic_bytes_per_launch:\s*(\d+)', open(path).read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def time_dominant_kernel(model, iters=20):
     """Prefix GeGLU GEMM (M=816, K=2048, N=16384 x 2 weights, rownorm):
     the largest single kernel of the chunk.  Times `iters` back-to-back
@@ -68,10 +80,40 @@ def time_dominant_kernel(model, iters=20):
         'peak': PEAK_BF16_TFLOPS,
         'unit': 'TFLOP/s',
         'frac': round(achieved / PEAK_BF16_TFLOPS, 4),
-        'traffic': None,
+        'traffic': measured_traffic(),
+        'traffic_unit': 'bytes/launch (rocprofv3 FETCH_SIZE + WRITE_SIZE)',
         'avg_us': round(us, 2),
         'flops_per_launch': flops,
     }
+
+
+def kernel_only(iters=10):
+    """The dominant kernel alone at its chunk shape (random operands), then
+    a plain 256 MiB device copy: the short program the rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE passes run (the copy calibrates the counters:
+    it fetches and writes exactly 256 MiB)."""
+    import torch
+
+    from fluxvla_amd import kernels as K
+    from fluxvla_amd.config import PI0
+    cfg = PI0
+    dev = torch.device('cuda', 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    M, Kd, N = cfg.prefix_len, cfg.llm_hidden, cfg.llm_mlp
+    x = torch.randn(M, Kd, device=dev, generator=g).bfloat16()
+    wg = (torch.randn(N, Kd, device=dev, generator=g) * 0.02).bfloat16()
+    wu = (torch.randn(N, Kd, device=dev, generator=g) * 0.02).bfloat16()
+    h = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    for _ in range(iters):
+        K.gemm_geglu(x, wg, wu, out=h, rownorm_eps=cfg.rms_eps)
+    torch.cuda.synchronize()
+    src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f'kernel-only: {iters} x gemm_geglu M={M} N={N}x2 K={Kd}; '
+        '3 x copy 256 MiB')
 
 
 def cpu_baseline(sd_gpu, cfg, inp, gpu_out):
@@ -109,12 +151,19 @@ def main():
     ap.add_argument('--batch', type=int, default=1)
     ap.add_argument('--no-cpu', action='store_true',
                     help='skip the CPU oracle baseline')
+    ap.add_argument('--kernel-only', action='store_true',
+                    help='run only the dominant kernel + a calibration copy '
+                    '(for rocprofv3 --pmc passes)')
     args = ap.parse_args()
     if args.gpus != 1:
         print('bench.py: this build runs on one GPU; multi-GPU figures are '
               'not part of it (the path shards by request, see DESIGN.md)',
               file=sys.stderr)
         sys.exit(2)
+
+    if args.kernel_only:
+        kernel_only()
+        return
 
     import torch
 

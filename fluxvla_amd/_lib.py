@@ -97,8 +97,8 @@ SIGNATURES = {
                                 c_i64, c_f32, c_vp]),
     'fvx_attention_workspace_bytes': (c_i64, [ctypes.POINTER(AttnDesc)]),
     'fvx_attention': (c_i32, [ctypes.POINTER(AttnDesc), c_vp]),
-    'fvx_im2col_patches': (c_i32, [c_vp, c_i32, c_vp, c_i64, c_i64, c_i64,
-                                   c_i64, c_i64, c_f32, c_f32, c_vp]),
+    'fvx_im2col_patches': (c_i32, [c_vp, c_i32, c_i32, c_vp, c_i64, c_i64,
+                                   c_i64, c_i64, c_i64, c_f32, c_f32, c_vp]),
     'fvx_embed_tokens': (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_f32,
                                  c_i64, c_i64, c_vp]),
     'fvx_copy_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64,

@@ -24,7 +24,8 @@ void clear_error() { g_err[0] = 0; }
 // (c * P + ky) * P + kx; one thread per output element pair is too fine, so
 // each thread builds 8 consecutive columns of one patch row.
 __global__ void im2col_kernel(const void* __restrict__ img, int in_f32,
-                              bf16_t* __restrict__ out, int64_t n_img, int H,
+                              int chlast, bf16_t* __restrict__ out,
+                              int64_t n_img, int H,
                               int W, int P, int k_pad, float scale,
                               float shift) {
   const int gw = W / P, gh = H / P;
@@ -45,8 +46,9 @@ __global__ void im2col_kernel(const void* __restrict__ img, int in_f32,
     if (col < kreal) {
       const int c = col / (P * P), rem = col % (P * P);
       const int ky = rem / P, kx = rem % P;
-      const int64_t off =
-          ((im * 3 + c) * H + (int64_t)(py * P + ky)) * W + px * P + kx;
+      const int64_t y = py * P + ky, xx = px * P + kx;
+      const int64_t off = chlast ? ((im * H + y) * W + xx) * 3 + c
+                                 : ((im * 3 + c) * H + y) * W + xx;
       const float x = in_f32 ? ((const float*)img)[off]
                              : bf2f(((const bf16_t*)img)[off]);
       v[e] = x * scale + shift;
@@ -99,9 +101,9 @@ extern "C" int fvx_version(void) { return 1; }
 extern "C" const char* fvx_last_error(void) { return g_err; }
 
 extern "C" int fvx_im2col_patches(const void* images, int in_f32,
-                                  void* patches, int64_t n_img,
-                                  int64_t height, int64_t width,
-                                  int64_t patch, int64_t k_pad,
+                                  int channels_last, void* patches,
+                                  int64_t n_img, int64_t height,
+                                  int64_t width, int64_t patch, int64_t k_pad,
                                   float in_scale, float in_shift,
                                   void* stream) {
   clear_error();
@@ -119,7 +121,8 @@ extern "C" int fvx_im2col_patches(const void* images, int in_f32,
   if (total == 0) return FVX_OK;
   hipLaunchKernelGGL(im2col_kernel, dim3((unsigned)((total + 255) / 256)),
                      dim3(256), 0, (hipStream_t)stream, images, in_f32,
-                     (bf16_t*)patches, n_img, (int)height, (int)width,
+                     channels_last ? 1 : 0, (bf16_t*)patches, n_img,
+                     (int)height, (int)width,
                      (int)patch, (int)k_pad, in_scale, in_shift);
   return launch_status("im2col_patches");
 }

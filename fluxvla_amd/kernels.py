@@ -358,12 +358,17 @@ def mha_packed_qkv(qkv, out, n_views, seq, heads, head_dim, scale=None,
 # ---------------------------------------------------------------------------
 # Data movement
 # ---------------------------------------------------------------------------
-def im2col_patches(images, patch, k_pad, out=None, scale=1.0, shift=0.0):
-    """images [N, 3, H, W] (bf16 or fp32) -> [N * (H/p) * (W/p), k_pad] bf16."""
+def im2col_patches(images, patch, k_pad, out=None, scale=1.0, shift=0.0,
+                   channels_last=False):
+    """images [N, 3, H, W] (or [N, H, W, 3] with channels_last; bf16 or
+    fp32) -> [N * (H/p) * (W/p), k_pad] bf16, columns (c, ky, kx)."""
     _check(images, 'images', dtype=None)
     if images.dtype not in (BF16, torch.float32):
         raise ValueError('images must be bf16 or fp32')
-    n, c, h, w = images.shape
+    if channels_last:
+        n, h, w, c = images.shape
+    else:
+        n, c, h, w = images.shape
     if c != 3:
         raise ValueError('images must have 3 channels')
     rows = n * (h // patch) * (w // patch)
@@ -371,8 +376,9 @@ def im2col_patches(images, patch, k_pad, out=None, scale=1.0, shift=0.0):
         out = torch.empty(rows, k_pad, dtype=BF16, device=images.device)
     _check(out, 'out')
     _lib.call('fvx_im2col_patches', _ptr(images),
-              int(images.dtype == torch.float32), _ptr(out), n, h, w, patch,
-              k_pad, float(scale), float(shift), _stream())
+              int(images.dtype == torch.float32), int(bool(channels_last)),
+              _ptr(out), n, h, w, patch, k_pad, float(scale), float(shift),
+              _stream())
     return out
 
 

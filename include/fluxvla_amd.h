@@ -187,15 +187,17 @@ int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d);
 int fvx_attention(const fvx_attn_desc* d, void* stream);
 
 /*
- * SigLIP patch im2col: images [n_img, 3, H, W] (bf16 or fp32 per
- * `in_f32`) -> patches [n_img * (H/p) * (W/p), k_pad] bf16, column order
- * (channel, ky, kx) (the Conv2d weight flattening), zero-filled from 3*p*p
- * up to k_pad.  Optional affine: value * in_scale + in_shift.
+ * SigLIP patch im2col: images [n_img, 3, H, W] (or [n_img, H, W, 3] with
+ * channels_last; bf16 or fp32 per `in_f32`) -> patches
+ * [n_img * (H/p) * (W/p), k_pad] bf16, column order (channel, ky, kx) (the
+ * Conv2d weight flattening), zero-filled from 3*p*p up to k_pad.  Optional
+ * affine: value * in_scale + in_shift.  Replaces the patch gather of
+ * conv2d_embed_res (fluxvla/ops/atomic_ops.py:34-53).
  */
-int fvx_im2col_patches(const void* images, int in_f32, void* patches,
-                       int64_t n_img, int64_t height, int64_t width,
-                       int64_t patch, int64_t k_pad, float in_scale,
-                       float in_shift, void* stream);
+int fvx_im2col_patches(const void* images, int in_f32, int channels_last,
+                       void* patches, int64_t n_img, int64_t height,
+                       int64_t width, int64_t patch, int64_t k_pad,
+                       float in_scale, float in_shift, void* stream);
 
 /* Token embedding gather: out[orow(i)] = bf16(table[ids[i]] * scale). */
 int fvx_embed_tokens(const void* table, const int64_t* ids, void* out,

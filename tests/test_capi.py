@@ -113,8 +113,8 @@ def test_norm_and_attention_reject_bad_arguments():
 
 def test_data_movement_rejects_bad_arguments():
     lib = _lib.load()
-    assert lib.fvx_im2col_patches(4096, 0, 4096, 1, 224, 224, 14, 580, 1.0,
-                                  0.0, None) == _lib.FVX_ERR_SHAPE
+    assert lib.fvx_im2col_patches(4096, 0, 0, 4096, 1, 224, 224, 14, 580,
+                                  1.0, 0.0, None) == _lib.FVX_ERR_SHAPE
     assert lib.fvx_embed_tokens(4096, None, 4096, 1, 8, 8, 1.0, 0, 0,
                                 None) == _lib.FVX_ERR_NULL
     assert lib.fvx_copy_rows(4096, 8, 4096, 8, 1, 12, 0, 0,
