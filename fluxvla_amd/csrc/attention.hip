@@ -17,9 +17,10 @@
 // in.  K/V rows past the key range are zero-filled; masked scores are -inf
 // and never produce NaN (a row that has seen no visible key yet keeps a zero
 // reference).  With kv_splits > 1 each split writes (O, m, l) partials to a
-// workspace and the last workgroup of a row block merges them in split
-// order (deterministic) -- used for the decode-shaped action-expert
-// attention (408 query rows against the 867-key prefix+suffix cache).
+// workspace and a merge kernel, the next kernel on the stream, combines them
+// in split order (deterministic).  The decode-shaped action-expert attention
+// (408 query rows against the 867-key prefix+suffix cache) runs the
+// barrier-free attn_decode_kernel further below.
 #include <math.h>
 
 #include "capi_util.h"

@@ -15,12 +15,15 @@
 //  * gemm_skinny_kernel<MODE>: M <= 64 (the bs=1 action expert, M=50/51).
 //    The op is a weight stream: each wave owns 16 output columns and pulls
 //    its weight rows straight from HBM as MFMA B fragments (16 contiguous
-//    bytes per lane, no LDS); the 64xK activation slab is re-read from L1/L2.
-//    The K range is split over blockIdx.y so that >= 2 workgroups per CU
-//    stream weights; partial tiles go to an fp32 workspace and the last
-//    workgroup to arrive for an n-tile (arrival counter, device-scope fences)
-//    reduces them in a fixed order -- deterministic -- and runs the epilogue,
-//    then re-arms its counter to zero for the next call / graph replay.
+//    bytes per lane); the activation slab is staged once per workgroup in
+//    LDS.  K is split over blockIdx.y in ranges of <= 256 so that ~256+
+//    workgroups stream weights; fp32 partials go to a workspace and
+//    gemm_skinny_reduce_kernel, the next kernel on the stream, sums them in
+//    split order (deterministic) and runs the epilogue.  (A single-kernel
+//    variant in which the last workgroup to arrive reduced the partials
+//    behind device-scope fences cost 30-40 us per GEMM on MI355X: the
+//    agent-scope release/acquire writes back and invalidates the per-XCD
+//    L2.)
 //
 // Per-row RMSNorm ("rownorm") is fused: the kernel that streams A also
 // accumulates sum(A[m][:]^2) and scales the accumulator by
@@ -392,7 +395,6 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
 // Sum of the split partials + epilogue.  Thread t of block (x, y): column
 // 64 x + t % 64, row 4 y + t / 64; the loads of all splits are issued before
 // the adds (one memory latency) and added in split order (deterministic).
-constexpr int kSkinnyMaxSplits = 64;
 
 template <int MODE>
 __global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(GemmArgs p,

@@ -15,9 +15,9 @@ from ._lib import AttnDesc, GemmDesc
 
 BF16 = torch.bfloat16
 
-# Split-K / split-KV workspace: one per device, zero-filled once.  Kernels
-# leave their arrival counters at zero, so the buffer is reusable by every
-# later call on the same stream.
+# Split-K / split-KV workspace (fp32 partials), one per device, allocated
+# before any graph capture.  Every split op reduces its partials with a
+# second kernel on the same stream, so consecutive calls share it.
 WORKSPACE_BYTES = 64 << 20
 _workspaces = {}
 

@@ -15,11 +15,13 @@
  *   - Every entry point returns 0 on success or a negative fvx_status code
  *     without launching anything; fvx_last_error() then describes the
  *     problem (thread-local).  Nothing aborts the process.
- *   - Split-K GEMMs and split-KV attention need a workspace: `workspace`
- *     must be device memory that was zero-filled once before its first use;
- *     kernels leave it zeroed where it matters (the arrival counters) so it
- *     can be reused by the next call on the same stream.  Passing a NULL
- *     workspace is allowed and selects the single-pass kernels.
+ *   - Split-K GEMMs and split-KV attention need a device workspace for
+ *     their fp32 partials (size from fvx_gemm_workspace_bytes /
+ *     fvx_attention_workspace_bytes; no initial contents needed).  The
+ *     partials are reduced by a second kernel on the same stream, so calls
+ *     on one stream may share one workspace; calls overlapping on different
+ *     streams must not.  A NULL or too small workspace is an error
+ *     (FVX_ERR_WORKSPACE) whenever the problem needs a split.
  */
 #ifndef FLUXVLA_AMD_H_
 #define FLUXVLA_AMD_H_
@@ -107,8 +109,9 @@ typedef struct fvx_gemm_desc {
 /* Library identity / diagnostics. */
 int fvx_version(void);
 const char* fvx_last_error(void);
-/* Number of fp32 workspace bytes fvx_gemm needs for the given problem
- * (0 if it will run single-pass). */
+/* Workspace bytes fvx_gemm needs for the given problem (0 if it runs in
+ * one pass).  M <= 64 problems split K in ranges of at most 256; split_k > 0
+ * requests a range length of ceil(K / split_k) (still capped at 256). */
 int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d);
 
 /* General GEMM with fused epilogue (all matmul_* entry points below are thin

@@ -105,3 +105,43 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, '_lib', None)
     with pytest.raises(ImportError, match='not built'):
         _lib.load()
+
+
+def _reference_style_cfg(type_name, pi05):
+    """A model dict shaped like the reference's PI0 / PI0.5 configs (the
+    keys build_vla_from_cfg reads), with the PI0 dimensions."""
+    gemma = dict(type='ConditionGemmaModel', head_dim=256, hidden_size=2048,
+                 intermediate_size=16384, num_attention_heads=8,
+                 num_hidden_layers=18, num_key_value_heads=1,
+                 rms_norm_eps=1e-06, rope_theta=10000.0, vocab_size=257152)
+    expert = dict(gemma, hidden_size=1024, intermediate_size=4096,
+                  use_adarms=pi05, adarms_cond_dim=1024 if pi05 else None)
+    cfg = dict(type=type_name, llm_backbone=gemma, llm_expert=expert,
+               vision_backbone=dict(
+                   type='SigLIPViTBackbone', vision_backbone_id='siglip_224',
+                   vision_config=dict(hidden_size=1152, image_size=224,
+                                      intermediate_size=4304,
+                                      layer_norm_eps=1e-06,
+                                      num_attention_heads=16,
+                                      num_hidden_layers=27, patch_size=14)),
+               proj_width=1024, n_action_steps=50, max_action_dim=32)
+    if not pi05:
+        cfg['state_proj'] = dict(type='LinearProjector', in_dim=32,
+                                 out_dim=1024)
+    return cfg
+
+
+@pytest.mark.parametrize('name,pi05', [('PI0FlowMatching', False),
+                                       ('PI05FlowMatchingInference', True)])
+def test_registry_reads_reference_configs(name, pi05):
+    from fluxvla_amd.config import PI0Config
+    from fluxvla_amd.registry import VLAS, config_from_reference
+    cfg = config_from_reference(_reference_style_cfg(name, pi05))
+    assert name in VLAS
+    assert cfg == PI0Config(pi05=pi05)
+
+
+def test_registry_rejects_unknown_type():
+    from fluxvla_amd.registry import build_vla_from_cfg
+    with pytest.raises(KeyError, match='not a registered'):
+        build_vla_from_cfg(dict(type='OpenVLA'), {}, device='cpu')
