@@ -73,7 +73,7 @@ def time_dominant_kernel(model, iters=20):
     flops = 2.0 * M * N * Kd * 2
     achieved = flops / (us * 1e-6) / 1e12
     return {
-        'kernel': 'gemm_tile_kernel<128,128,GEGLU> (prefix gate/up, '
+        'kernel': 'gemm_tile_kernel<128,64,GEGLU> (prefix gate/up, '
                   f'M={M} N={N}x2 K={Kd})',
         'bound': 'mfma',
         'achieved': round(achieved, 2),

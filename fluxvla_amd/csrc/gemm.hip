@@ -18,7 +18,7 @@
 //    bytes per lane); the activation slab is staged once per workgroup in
 //    LDS.  K is split over blockIdx.y in ranges of <= 256 so that ~256+
 //    workgroups stream weights; fp32 partials go to a workspace and
-//    gemm_skinny_reduce_kernel, the next kernel on the stream, sums them in
+//    gemm_partial_reduce_kernel, the next kernel on the stream, sums them in
 //    split order (deterministic) and runs the epilogue.  (A single-kernel
 //    variant in which the last workgroup to arrive reduced the partials
 //    behind device-scope fences cost 30-40 us per GEMM on MI355X: the
@@ -121,68 +121,102 @@ __device__ __forceinline__ float sumsq8(const bf16x8& v) {
 }
 
 // ---------------------------------------------------------------------------
-// Big-tile kernel
+// Tiled kernel (M > 64)
 // ---------------------------------------------------------------------------
+// 256 threads = 2 x 2 waves; block tile BM x BN (GEGLU: BN columns of each
+// of the two weights).  K moves through a 2-stage LDS ring in 64-wide slabs
+// with ONE barrier per slab: while slab t feeds the MFMAs, slab t+1 (already
+// in registers) is written to the other LDS stage and slab t+2's global
+// loads are issued.  LDS rows are XOR-swizzled (see the loader) so neither
+// the staging writes nor the fragment reads conflict.  <= 256 registers and
+// <= 64 KiB of LDS keep two workgroups per CU.  With
+// splits > 1 the K range is split over blockIdx.y and fp32 partials go to
+// the workspace for gemm_partial_reduce_kernel.
 template <int BM, int BN, int MODE>
-__global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs p, int m_tiles,
-                                                        int n_tiles) {
+constexpr int tile_min_blocks() {
+  // two workgroups per CU when the 2-stage ring fits twice in 160 KiB
+  return (2 * (BM + (MODE == FVX_GEMM_GEGLU ? 2 : 1) * BN) * 64 * 2 <= 80 * 1024 &&
+          MODE != FVX_GEMM_QKV_ROPE) ? 2 : 1;
+}
+
+template <int BM, int BN, int MODE>
+__global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_tile_kernel(GemmArgs p,
+                                                           int m_tiles,
+                                                           int n_tiles,
+                                                           int splits,
+                                                           int64_t kchunk) {
   constexpr int BK = 64;
-  constexpr int LD = BK + 8;  // LDS row pitch (bf16): 144 B, conflict-free reads
+  constexpr int LD = BK;  // 128-byte rows, XOR-swizzled chunks (see loader)
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int FM = WM / 16, FN = WN / 16;
   constexpr int AI = BM / 32, BI = BN / 32;
-  __shared__ __align__(16) bf16_t sA[BM * LD];
-  __shared__ __align__(16) bf16_t sB[NB][BN * LD];
+  constexpr int STAGE = BM * LD + NB * BN * LD;  // bf16 elements per stage
+  __shared__ __align__(16) bf16_t smem[2 * STAGE];
   __shared__ float sRow[BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // XCD-aware tile order (see file comment).
+  // XCD-aware tile order: consecutive tile ids (the M tiles of one weight
+  // panel, m fastest) land on one XCD and share its L2.
   const int nblk = m_tiles * n_tiles;
   int bid = blockIdx.x;
   if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
+  const int split = blockIdx.y;
   const int64_t m0 = (int64_t)m_tile * BM, n0 = (int64_t)n_tile * BN;
+  const int64_t M = p.m, N = p.n, K = p.k;
+  const int64_t kb = (int64_t)split * kchunk;
+  const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
+  const int nk = (int)((ke - kb + BK - 1) / BK);
 
   const bf16_t* A = (const bf16_t*)p.a;
   const bf16_t* Bm[2] = {(const bf16_t*)p.b, (const bf16_t*)p.b2};
-  const int64_t M = p.m, N = p.n, K = p.k;
 
+  // Loader: 8 consecutive lanes move one 128-byte row slab (coalesced).
+  // LDS rows have no padding; chunk c of row r lives at chunk position
+  // c ^ ((r >> 1) & 7).  With 64 banks and 16 lanes per LDS cycle, the
+  // loader's 16 lanes (rows 2j, 2j+1, all chunks) and a fragment read's 16
+  // lanes (16 consecutive rows, one chunk) both land on 16 distinct 4-bank
+  // groups: no bank conflicts on either side.
   const int lrow = tid >> 3, lchk = tid & 7;
-  bf16x8 ra[AI], rb[NB][BI];
+  // Two register sets: slab t is loaded into set t & 1 two slabs before it
+  // is written to LDS, so its global latency overlaps two slabs of MFMAs.
+  bf16x8 ra[2][AI], rb[2][NB][BI];
   float ss[AI];
 #pragma unroll
   for (int i = 0; i < AI; ++i) ss[i] = 0.f;
 
-  auto gload = [&](int64_t k0) {
-    const int64_t kk = k0 + lchk * 8;
-    const bool kin = kk < K;
+  auto gload = [&](int t, int set) {
+    const int64_t kk = kb + (int64_t)t * BK + lchk * 8;
+    const bool kin = t < nk && kk < ke;
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
       const int64_t r = m0 + lrow + 32 * i;
-      ra[i] = (kin && r < M) ? ld8(A + r * p.lda + kk) : zero8();
+      ra[set][i] = (kin && r < M) ? ld8(A + r * p.lda + kk) : zero8();
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int i = 0; i < BI; ++i) {
         const int64_t c = n0 + lrow + 32 * i;
-        rb[b][i] = (kin && c < N) ? ld8(Bm[b] + c * p.ldb + kk) : zero8();
+        rb[set][b][i] = (kin && c < N) ? ld8(Bm[b] + c * p.ldb + kk) : zero8();
       }
   };
-  auto swrite = [&]() {
+  const int wpos = (lchk ^ ((lrow >> 1) & 7)) * 8;  // same for rows lrow + 32 i
+  auto swrite = [&](int buf, int set) {
+    bf16_t* sa = smem + buf * STAGE;
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
-      st8(&sA[(lrow + 32 * i) * LD + lchk * 8], ra[i]);
-      if (p.rownorm) ss[i] += sumsq8(ra[i]);
+      st8(&sa[(lrow + 32 * i) * LD + wpos], ra[set][i]);
+      if (p.rownorm) ss[i] += sumsq8(ra[set][i]);
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int i = 0; i < BI; ++i)
-        st8(&sB[b][(lrow + 32 * i) * LD + lchk * 8], rb[b][i]);
+        st8(&sa[BM * LD + (b * BN + lrow + 32 * i) * LD + wpos], rb[set][b][i]);
   };
 
   f32x4_t acc[NB][FM][FN];
@@ -193,24 +227,23 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs p, int m_tiles,
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[b][i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = (int)((K + BK - 1) / BK);
-  gload(0);
-  swrite();
-  __syncthreads();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) gload((int64_t)(kt + 1) * BK);
+  auto compute = [&](int buf) {
+    const bf16_t* sa = smem + buf * STAGE;
+    const bf16_t* sb = sa + BM * LD;
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
       bf16x8 af[FM], bfr[NB][FN];
+      // rows here are (multiple of 16) + fr, so (row >> 1) & 7 == fr >> 1
+      const int rpos = ((4 * ks + (lane >> 4)) ^ ((fr >> 1) & 7)) * 8;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = ld8(&sA[(wm * WM + i * 16 + fr) * LD + ks * 32 + fk]);
+        af[i] = ld8(&sa[(wm * WM + i * 16 + fr) * LD + rpos]);
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          bfr[b][j] = ld8(&sB[b][(wn * WN + j * 16 + fr) * LD + ks * 32 + fk]);
+          bfr[b][j] = ld8(&sb[(b * BN + wn * WN + j * 16 + fr) * LD + rpos]);
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -219,23 +252,62 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs p, int m_tiles,
           for (int j = 0; j < FN; ++j)
             acc[b][i][j] = mfma16x16x32(af[i], bfr[b][j], acc[b][i][j]);
     }
-    __syncthreads();
-    if (kt + 1 < nk) {
-      swrite();
-      __syncthreads();
+  };
+
+  // slab t: loaded into register set t&1, written to LDS stage t&1.
+  gload(0, 0);
+  gload(1, 1);
+  if (nk > 0) swrite(0, 0);
+  gload(2, 0);
+  __syncthreads();
+  for (int t = 0; t < nk; t += 2) {
+    compute(0);                          // slab t
+    if (t + 1 < nk) {
+      swrite(1, 1);                      // slab t+1
+      gload(t + 3, 1);
     }
+    __syncthreads();
+    if (t + 1 >= nk) break;
+    compute(1);                          // slab t+1
+    if (t + 2 < nk) {
+      swrite(0, 0);                      // slab t+2
+      gload(t + 4, 0);
+    }
+    __syncthreads();
   }
 
+  // Row sums of squares of this K range: 8 consecutive lanes share a row.
   if (p.rownorm) {
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
-      float s = ss[i];
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      s += __shfl_xor(s, 4, 64);
-      if (lchk == 0) sRow[lrow + 32 * i] = rsqrtf(s / (float)K + p.rownorm_eps);
+      float s2 = ss[i];
+      s2 += __shfl_xor(s2, 1, 64);
+      s2 += __shfl_xor(s2, 2, 64);
+      s2 += __shfl_xor(s2, 4, 64);
+      if (lchk == 0) sRow[lrow + 32 * i] = s2;
     }
     __syncthreads();
+  }
+
+  if (splits > 1) {
+    float* ws = (float*)p.workspace;
+    const int64_t plane = (int64_t)splits * M * N;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t n = n0 + wn * WN + j * 16 + fr;
+          const int64_t r0 = m0 + wm * WM + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n < N && r0 + e < M)
+              ws[b * plane + ((int64_t)split * M + r0 + e) * N + n] = acc[b][i][j][e];
+        }
+    if (n_tile == 0 && p.rownorm && tid < BM && m0 + tid < M)
+      ws[NB * plane + (int64_t)split * M + m0 + tid] = sRow[tid];
+    return;
   }
 
 #pragma unroll
@@ -243,7 +315,8 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs p, int m_tiles,
     const int lr0 = wm * WM + i * 16 + 4 * (lane >> 4);
     float rs[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) rs[j] = p.rownorm ? sRow[lr0 + j] : 1.f;
+    for (int j = 0; j < 4; ++j)
+      rs[j] = p.rownorm ? rsqrtf(sRow[lr0 + j] / (float)K + p.rownorm_eps) : 1.f;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int64_t n = n0 + wn * WN + j * 16 + fr;
@@ -272,7 +345,7 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs p, int m_tiles,
 //
 // With one K range (splits == 1) the epilogue runs in place.  Otherwise the
 // fp32 partial tile and the partial row sums of squares go to the workspace
-// with plain stores, and gemm_skinny_reduce_kernel -- the next kernel on the
+// with plain stores, and gemm_partial_reduce_kernel -- the next kernel on the
 // stream, so the partials are visible without any fence -- adds the splits
 // in order and runs the epilogue (deterministic).
 constexpr int kSkinnyKc = 256;
@@ -357,9 +430,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
   }
 
   if (splits > 1) {
-    // partials: [NB][split][64 rows][N] fp32, then [split][64] row sums
+    // partials: [NB][split][M rows][N] fp32, then [split][M] row sums
     float* ws = (float*)p.workspace;
-    const int64_t plane = (int64_t)splits * 64 * N;
+    const int64_t plane = (int64_t)splits * M * N;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -367,9 +440,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (nval && f * 16 + 4 * g + j < M)
-            ws[b * plane + ((int64_t)split * 64 + f * 16 + 4 * g + j) * N + n] =
+            ws[b * plane + ((int64_t)split * M + f * 16 + 4 * g + j) * N + n] =
                 acc[b][f][j];
-    if (ntile == 0 && tid < 64) ws[NB * plane + split * 64 + tid] = s_ss[tid];
+    if (ntile == 0 && p.rownorm && tid < M) ws[NB * plane + split * M + tid] = s_ss[tid];
     return;
   }
 
@@ -392,13 +465,13 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
   }
 }
 
-// Sum of the split partials + epilogue.  Thread t of block (x, y): column
-// 64 x + t % 64, row 4 y + t / 64; the loads of all splits are issued before
-// the adds (one memory latency) and added in split order (deterministic).
-
+// Sum of the split partials of either GEMM kernel + epilogue.  Thread t of
+// block (x, y): column 64 x + t % 64, row 4 y + t / 64; the loads of 16
+// splits are issued before their adds (one memory latency per 16), added in
+// split order (deterministic).
 template <int MODE>
-__global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(GemmArgs p,
-                                                                 int splits) {
+__global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
+                                                                  int splits) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
   constexpr int UN = 16;  // loads in flight per pass
   const int tid = threadIdx.x, lane = tid & 63;
@@ -407,7 +480,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(GemmArgs p,
   const int64_t row = (int64_t)blockIdx.y * 4 + (tid >> 6);
   const bool ok = n < N && row < p.m;
   const float* ws = (const float*)p.workspace;
-  const int64_t plane = (int64_t)splits * 64 * N;
+  const int64_t M = p.m;
+  const int64_t plane = (int64_t)splits * M * N;
   float v = 0.f, u = 0.f, ss = 0.f;
   for (int s0 = 0; s0 < splits; s0 += UN) {
     float t[NB][UN], q[UN];
@@ -417,8 +491,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(GemmArgs p,
       const bool in = ok && s < splits;
 #pragma unroll
       for (int b = 0; b < NB; ++b)
-        t[b][i] = in ? ws[b * plane + ((int64_t)s * 64 + row) * N + n] : 0.f;
-      q[i] = (in && p.rownorm) ? ws[NB * plane + s * 64 + row] : 0.f;
+        t[b][i] = in ? ws[b * plane + ((int64_t)s * M + row) * N + n] : 0.f;
+      q[i] = (in && p.rownorm) ? ws[NB * plane + (int64_t)s * M + row] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < UN; ++i) {
@@ -458,7 +532,7 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
   s.splits = (int)((d.k + kchunk - 1) / kchunk);
   s.kchunk = kchunk;
   s.ws_bytes = s.splits > 1
-                   ? ((int64_t)nb * s.splits * 64 * d.n + (int64_t)s.splits * 64) * 4
+                   ? ((int64_t)nb * s.splits * d.m * d.n + (int64_t)s.splits * d.m) * 4
                    : 0;
   return s;
 }
@@ -519,9 +593,19 @@ static int validate(const GemmArgs& d) {
 using namespace fvx;
 
 extern "C" int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d) {
-  if (!d || d->m > 64 || d->m <= 0) return 0;
-  return plan_skinny(*d).ws_bytes;
+  if (!d || d->m <= 0) return 0;
+  if (d->m <= 64) return plan_skinny(*d).ws_bytes;
+  // tiled path: at most 4 K splits of fp32 partials (+ row sums)
+  const int nb = d->mode == FVX_GEMM_GEGLU ? 2 : 1;
+  return ((int64_t)nb * 4 * d->m * d->n + 4 * d->m) * 4;
 }
+
+#define FVX_MODE_DISPATCH_NG(MODE_RT, LAUNCH)                 \
+  switch (MODE_RT) {                                          \
+    case FVX_GEMM_QKV_ROPE: LAUNCH(FVX_GEMM_QKV_ROPE); break; \
+    case FVX_GEMM_EULER: LAUNCH(FVX_GEMM_EULER); break;       \
+    default: LAUNCH(FVX_GEMM_PLAIN); break;                   \
+  }
 
 #define FVX_MODE_DISPATCH(MODE_RT, LAUNCH)         \
   switch (MODE_RT) {                               \
@@ -559,31 +643,70 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
     int st2 = launch_status("gemm(skinny)");
     if (st2 || sp.splits == 1) return st2;
 #define L(MODE)                                                            \
-  hipLaunchKernelGGL(gemm_skinny_reduce_kernel<MODE>,                      \
+  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                      \
                      dim3(sp.n_tiles, (unsigned)((d.m + 3) / 4)), dim3(256), \
                      0, s, d, sp.splits)
     FVX_MODE_DISPATCH(d.mode, L)
 #undef L
     return launch_status("gemm(skinny reduce)");
   }
-  // Big tiles: 128x128 when that fills the GPU, else 64-row tiles.
-  const int64_t mt128 = (d.m + 127) / 128, nt128 = (d.n + 127) / 128;
-  const bool big = mt128 * nt128 >= 256;
-  const int m_tiles = (int)(big ? mt128 : (d.m + 63) / 64);
-  const int n_tiles = (int)nt128;
-  dim3 grid((unsigned)(m_tiles * n_tiles));
-  if (big) {
-#define L(MODE)                                                              \
-  hipLaunchKernelGGL((gemm_tile_kernel<128, 128, MODE>), grid, dim3(256), 0, \
-                     s, d, m_tiles, n_tiles)
-    FVX_MODE_DISPATCH(d.mode, L)
+  // Tiled path: 128 x 128 tiles (GEGLU: 128 x 64 of each weight) when that
+  // gives >= 512 workgroups (two per CU), else 64 x 128.  Projections with a long K and
+  // too few tiles to fill 256 CUs split K.
+  const bool gg = d.mode == FVX_GEMM_GEGLU;
+  const int64_t mt128 = (d.m + 127) / 128, mt64 = (d.m + 63) / 64;
+  const int64_t ncols = gg ? 2 * d.n : d.n;  // output columns incl. both weights
+  int cfg;  // 1: 128x128, 2: 64x128  (128x256 needs >110 KiB of LDS: one
+            // workgroup per CU, measured 3-4x slower than two of 128x128)
+  if (mt128 * ((ncols + 127) / 128) >= 512) cfg = 1;
+  else cfg = 2;
+  const int bm = cfg == 2 ? 64 : 128;
+  const int bn = 128 / (gg ? 2 : 1);
+  const int m_tiles = (int)(cfg == 2 ? mt64 : mt128);
+  const int n_tiles = (int)((d.n + bn - 1) / bn);
+  const int tiles = m_tiles * n_tiles;
+  int splits = d.split_k > 0 ? d.split_k : 1;
+  if (d.split_k <= 0 && tiles < 160 && d.k >= 4096) {
+    splits = (int)((256 + tiles - 1) / tiles);
+    if (splits > 4) splits = 4;
+  }
+  int64_t kchunk = (d.k + splits - 1) / splits;
+  kchunk = (kchunk + 63) / 64 * 64;
+  splits = (int)((d.k + kchunk - 1) / kchunk);
+  const int nbm = gg ? 2 : 1;
+  const int64_t need = splits > 1 ? ((int64_t)nbm * splits * d.m * d.n + (int64_t)splits * d.m) * 4 : 0;
+  if (splits > 1 && (!d.workspace || d.workspace_bytes < need)) {
+    if (d.split_k > 1)
+      return set_error(FVX_ERR_WORKSPACE,
+                       "gemm: split_k=%d needs %lld workspace bytes, got %lld",
+                       d.split_k, (long long)need, (long long)d.workspace_bytes);
+    splits = 1;
+    kchunk = d.k;
+  }
+  dim3 grid((unsigned)tiles, (unsigned)splits);
+#define LT(BM_, BN_, MODE)                                                  \
+  hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, MODE>), grid, dim3(256), 0, \
+                     s, d, m_tiles, n_tiles, splits, kchunk)
+  if (gg) {
+    if (cfg == 1) LT(128, 64, FVX_GEMM_GEGLU);
+    else LT(64, 64, FVX_GEMM_GEGLU);
+  } else if (cfg == 1) {
+#define L(MODE) LT(128, 128, MODE)
+    FVX_MODE_DISPATCH_NG(d.mode, L)
 #undef L
   } else {
-#define L(MODE)                                                             \
-  hipLaunchKernelGGL((gemm_tile_kernel<64, 128, MODE>), grid, dim3(256), 0, \
-                     s, d, m_tiles, n_tiles)
-    FVX_MODE_DISPATCH(d.mode, L)
+#define L(MODE) LT(64, 128, MODE)
+    FVX_MODE_DISPATCH_NG(d.mode, L)
 #undef L
   }
-  return launch_status("gemm(tile)");
+#undef LT
+  int st3 = launch_status("gemm(tile)");
+  if (st3 || splits == 1) return st3;
+#define L(MODE)                                                            \
+  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                     \
+                     dim3((unsigned)((d.n + 63) / 64), (unsigned)((d.m + 3) / 4)), \
+                     dim3(256), 0, s, d, splits)
+  FVX_MODE_DISPATCH(d.mode, L)
+#undef L
+  return launch_status("gemm(reduce)");
 }
