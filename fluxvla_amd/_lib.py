@@ -58,6 +58,8 @@ class GemmDesc(ctypes.Structure):
         ('workspace', c_vp), ('workspace_bytes', c_i64),
         ('split_k', c_i32),
         ('v_transposed', c_i32),
+        ('a_frag', c_i32), ('b_frag', c_i32),
+        ('c_frag', c_vp),
     ]
 
 
@@ -101,6 +103,7 @@ SIGNATURES = {
                                    c_i64, c_i64, c_i64, c_f32, c_f32, c_vp]),
     'fvx_embed_tokens': (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_f32,
                                  c_i64, c_i64, c_vp]),
+    'fvx_pack_frag': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     'fvx_copy_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64,
                               c_i64, c_vp]),
 }

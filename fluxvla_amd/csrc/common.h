@@ -75,6 +75,15 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const bf16x8& a,
                                                  0, 0);
 }
 
+// Element offset of (row m, column k) of an M <= 64 operand in the
+// fragment-major layout [K / 32 steps][4 row blocks][64 lanes][8]: lane =
+// 16 g + m % 16 with g = (k % 32) / 8, so one 16x32 MFMA A fragment is one
+// contiguous 1 KiB block.
+__host__ __device__ __forceinline__ int64_t frag_offset(int64_t m, int64_t k) {
+  return (((k >> 5) * 4 + (m >> 4)) * 64 + ((k & 31) >> 3) * 16 + (m & 15)) * 8 +
+         (k & 7);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

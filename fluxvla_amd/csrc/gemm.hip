@@ -36,6 +36,11 @@ namespace fvx {
 
 typedef fvx_gemm_desc GemmArgs;
 
+// The first kCounterBytes of a GEMM workspace hold the per-column-tile
+// arrival counters of the split-K skinny kernel; fp32 partials follow.
+constexpr int kCounterBytes = 4096;
+constexpr int kMaxSkinnyTiles = kCounterBytes / 4;
+
 
 __device__ __forceinline__ int64_t out_row(const GemmArgs& p, int64_t m) {
   return p.row_group > 0
@@ -118,6 +123,216 @@ __device__ __forceinline__ float sumsq8(const bf16x8& v) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) s += f[e] * f[e];
   return s;
+}
+
+// ---------------------------------------------------------------------------
+// Row-chunk epilogue: output columns n .. n + 7 of one row m.
+//
+// epi_load issues every global read the epilogue needs (bias, residual, gate,
+// position table, Euler state, RoPE table) and epi_store computes and writes.
+// Callers run epi_load for all of their chunks before the first epi_store:
+// an in-place operand (residual == c, xt) may alias the output, so a read
+// issued after a store would wait for a full memory round trip per element.
+// `vec`: the chunk holds 8 columns and every operand is 16-byte aligned, so
+// each operand moves as one 16-byte (fp32: two) access; otherwise `cnt`
+// columns are handled one by one.
+// ---------------------------------------------------------------------------
+struct EpiIn {
+  bf16x8 res, gate, pos, bias;
+  float f0[8];  // bias_f32 (PLAIN, EULER) or RoPE (cos, sin) x 4 (QKV_ROPE)
+  float xt[8];  // EULER state
+};
+
+__device__ __forceinline__ void ld_f8(const float* src, bool vec, int cnt,
+                                      float* d) {
+  if (vec) {
+    const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      d[e] = a[e];
+      d[4 + e] = b[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = e < cnt ? src[e] : 0.f;
+  }
+}
+
+__device__ __forceinline__ bf16x8 ld_b8(const bf16_t* src, bool vec, int cnt) {
+  if (vec) return ld8(src);
+  bf16x8 v = zero8();
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (e < cnt) v.w[e >> 1] |= (uint32_t)src[e] << (16 * (e & 1));
+  return v;
+}
+
+__device__ __forceinline__ void st_b8(bf16_t* dst, const float* x, bool vec,
+                                      int cnt) {
+  if (vec) {
+    st8(dst, pack8(x));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < cnt) dst[e] = f2bf(x[e]);
+  }
+}
+
+__device__ __forceinline__ void st_f8(float* dst, const float* x, bool vec,
+                                      int cnt) {
+  if (vec) {
+    *(f32x4_t*)dst = f32x4_t{x[0], x[1], x[2], x[3]};
+    *(f32x4_t*)(dst + 4) = f32x4_t{x[4], x[5], x[6], x[7]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < cnt) dst[e] = x[e];
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
+                                         int64_t n, bool vec, int cnt,
+                                         EpiIn& in) {
+  if (MODE == FVX_GEMM_GEGLU) return;
+  if (MODE == FVX_GEMM_QKV_ROPE) {
+    const int hd = p.head_dim;
+    if (n < (int64_t)(p.n_q_heads + 1) * hd) {
+      const int64_t pos = p.positions[m];
+      ld_f8(p.rope + (pos * (hd >> 1) + ((n % hd) >> 1)) * 2, vec, cnt, in.f0);
+    }
+    return;
+  }
+  in.bias = p.bias ? ld_b8((const bf16_t*)p.bias + n, vec, cnt) : zero8();
+  if (p.bias_f32) {
+    ld_f8(p.bias_f32 + n, vec, cnt, in.f0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) in.f0[e] = 0.f;
+  }
+  if (MODE == FVX_GEMM_EULER) {
+    ld_f8(p.xt + m * p.ldx + n, vec, cnt, in.xt);
+    return;
+  }
+  in.gate = p.gate ? ld_b8((const bf16_t*)p.gate + (m / p.gate_group) * p.ldg + n,
+                           vec, cnt)
+                   : zero8();
+  in.res = p.residual ? ld_b8((const bf16_t*)p.residual + out_row(p, m) * p.ldr + n,
+                              vec, cnt)
+                      : zero8();
+  in.pos = p.pos ? ld_b8((const bf16_t*)p.pos + (m % p.pos_period) * p.ldp + n,
+                         vec, cnt)
+                 : zero8();
+}
+
+// v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
+template <int MODE>
+__device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
+                                          int64_t n, bool vec, int cnt,
+                                          const float* v, const float* u,
+                                          float r, const EpiIn& in) {
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = v[e] * r;
+  if (MODE == FVX_GEMM_GEGLU) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = gelu_tanh(x[e]) * (u[e] * r);
+    st_b8((bf16_t*)p.c + out_row(p, m) * p.ldc + n, x, vec, cnt);
+    if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, n), pack8(x));
+    return;
+  }
+  if (MODE == FVX_GEMM_QKV_ROPE) {
+    const int hd = p.head_dim;
+    const int64_t qcols = (int64_t)p.n_q_heads * hd;
+    if (n < qcols + hd) {
+      // pair (2i, 2i+1) = (x_i, x_{i+hd/2}) rotated by (cos, sin)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = x[2 * i], b = x[2 * i + 1];
+        const float c = in.f0[2 * i], s = in.f0[2 * i + 1];
+        x[2 * i] = a * c - b * s;
+        x[2 * i + 1] = b * c + a * s;
+      }
+      if (n < qcols)
+        st_b8((bf16_t*)p.q_out + m * p.ldq + n, x, vec, cnt);
+      else
+        st_b8((bf16_t*)p.k_out + out_row(p, m) * p.ldk + (n - qcols), x, vec,
+              cnt);
+    } else if (p.v_transposed) {
+      // V^T cache: [group][head_dim][ldv], tokens contiguous
+      const int64_t b = p.row_group > 0 ? m / p.row_group : 0;
+      const int64_t t = p.row_group > 0 ? m % p.row_group : m;
+      bf16_t* dst = (bf16_t*)p.v_out + (b * hd + (n - qcols - hd)) * p.ldv + t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e < cnt) dst[e * p.ldv] = f2bf(x[e]);
+    } else {
+      st_b8((bf16_t*)p.v_out + out_row(p, m) * p.ldv + (n - qcols - hd), x,
+            vec, cnt);
+    }
+    return;
+  }
+  float t[8];
+  unpack8(in.bias, t);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] += t[e] + in.f0[e];
+  if (MODE == FVX_GEMM_EULER) {
+    float nx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) nx[e] = in.xt[e] + p.dt * x[e];
+    st_f8(p.xt + m * p.ldx + n, nx, vec, cnt);
+    if (p.xt_bf16) st_b8((bf16_t*)p.xt_bf16 + m * p.ldxb + n, nx, vec, cnt);
+    return;
+  }
+  if (p.act == FVX_ACT_SILU) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = silu(x[e]);
+  } else if (p.act == FVX_ACT_GELU_TANH) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = gelu_tanh(x[e]);
+  }
+  if (p.gate) {
+    unpack8(in.gate, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= t[e];
+  }
+  if (p.residual) {
+    unpack8(in.res, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] += t[e];
+  }
+  if (p.pos) {
+    unpack8(in.pos, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] += t[e];
+  }
+  const int64_t orow = out_row(p, m);
+  if (p.out_f32)
+    st_f8((float*)p.c + orow * p.ldc + n, x, vec, cnt);
+  else
+    st_b8((bf16_t*)p.c + orow * p.ldc + n, x, vec, cnt);
+  if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, n), pack8(x));
+}
+
+// Host check: may the chunk epilogue use 16-byte accesses for full chunks?
+static bool epi_vec_ok(const GemmArgs& d) {
+  auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+  switch (d.mode) {
+    case FVX_GEMM_GEGLU:
+      return al(d.c) && d.ldc % 8 == 0;
+    case FVX_GEMM_QKV_ROPE:
+      return d.head_dim % 8 == 0 && al(d.rope) && al(d.q_out) &&
+             d.ldq % 8 == 0 && al(d.k_out) && d.ldk % 8 == 0 &&
+             (d.v_transposed || (al(d.v_out) && d.ldv % 8 == 0));
+    case FVX_GEMM_EULER:
+      return al(d.bias) && al(d.bias_f32) && al(d.xt) && d.ldx % 4 == 0 &&
+             (!d.xt_bf16 || (al(d.xt_bf16) && d.ldxb % 8 == 0));
+    default:
+      return al(d.c) && d.ldc % (d.out_f32 ? 4 : 8) == 0 && al(d.bias) &&
+             al(d.bias_f32) && (!d.gate || (al(d.gate) && d.ldg % 8 == 0)) &&
+             (!d.residual || (al(d.residual) && d.ldr % 8 == 0)) &&
+             (!d.pos || (al(d.pos) && d.ldp % 8 == 0));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -290,7 +505,7 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
   }
 
   if (splits > 1) {
-    float* ws = (float*)p.workspace;
+    float* ws = (float*)((char*)p.workspace + kCounterBytes);
     const int64_t plane = (int64_t)splits * M * N;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -335,134 +550,259 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
 // ---------------------------------------------------------------------------
 // Skinny (M <= 64) weight-streaming kernels
 // ---------------------------------------------------------------------------
-// gemm_skinny_kernel: a workgroup owns 64 output columns (4 waves x 16) and a
-// K range of at most kSkinnyKc.  Each wave first issues every weight
-// fragment load of its range (up to 8 x 16 B per lane per weight matrix, so
-// ~32-64 KiB per CU are in flight -- what HBM latency needs), then the whole
-// workgroup stages the 64 x Kc activation slab once in LDS, where all four
-// waves read their A fragments (activation traffic = weight traffic / 1.25
-// instead of 4x when every wave fetched its own copy).
+// gemm_skinny_kernel: M <= 64 (the bs=1 action expert, M = 50/51).  The op is
+// a weight stream.  A workgroup of 8 waves owns 16 output columns (GEGLU: 16
+// of each weight) and one K range of the split-K grid (blockIdx.y); wave w
+// takes the slice [w kw, (w + 1) kw) of that range.  Both MFMA operands come
+// straight from global memory: lane (fr, g) reads the 16 bytes at k = 32 t +
+// 8 g of weight row n0 + fr and of activation rows 16 f + fr (the activations
+// are a few hundred KB and stay L2-resident).  The slice moves through two
+// register sets of 4 MFMA steps (GEGLU: 2), the loads of the next set issued
+// before the MFMAs of the current one.  The waves' partial tiles and row sums of squares
+// meet in LDS and are added in wave order.
 //
-// With one K range (splits == 1) the epilogue runs in place.  Otherwise the
-// fp32 partial tile and the partial row sums of squares go to the workspace
-// with plain stores, and gemm_partial_reduce_kernel -- the next kernel on the
-// stream, so the partials are visible without any fence -- adds the splits
-// in order and runs the epilogue (deterministic).
-constexpr int kSkinnyKc = 256;
-constexpr int kSkinnyLDA = kSkinnyKc + 8;  // LDS pitch: conflict-free frag reads
+// With one K range 128 threads run the chunk epilogue at once.  Otherwise
+// every workgroup writes its fp32 partial tile (and row sums) with stores
+// that write through to the device-coherent level (sc1), waits for them to
+// complete, and bumps the arrival counter of its column tile; the last
+// workgroup of the tile to arrive re-reads the splits' partials with sc1
+// loads, adds them in split order (deterministic, whatever the arrival
+// order), runs the epilogue and resets the counter to zero for the next
+// call.  No device-scope fence is involved: the shared data never sits
+// dirty in a non-coherent L2, which is what a release/acquire pair would
+// have to write back and invalidate (tens of microseconds per GEMM here).
+constexpr int kSkWaves = 8;
+constexpr int kSkStep = 4;    // MFMA steps (of 32 k) per register set (GEGLU: 2)
+constexpr int kSkMaxSplits = 4;
+
+__host__ __device__ constexpr int skinny_block_floats(int nb) {
+  return nb * 64 * 16 + 64;  // [nb][64 rows][16 cols] + 64 row sums
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;  // buffer cache policy bit: write through / read at
+                          // the device-coherent level
+
+__device__ __forceinline__ void sc1_store8(__amdgpu_buffer_rsrc_t r, int off,
+                                           const float* x) {
+  __builtin_amdgcn_raw_buffer_store_b128(
+      u32x4_t{__float_as_uint(x[0]), __float_as_uint(x[1]),
+              __float_as_uint(x[2]), __float_as_uint(x[3])},
+      r, off, 0, kSc1);
+  __builtin_amdgcn_raw_buffer_store_b128(
+      u32x4_t{__float_as_uint(x[4]), __float_as_uint(x[5]),
+              __float_as_uint(x[6]), __float_as_uint(x[7])},
+      r, off + 16, 0, kSc1);
+}
+
+__device__ __forceinline__ void sc1_load8(__amdgpu_buffer_rsrc_t r, int off,
+                                          float* x) {
+  const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1);
+  const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, kSc1);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = __uint_as_float(a[e]);
+    x[4 + e] = __uint_as_float(b[e]);
+  }
+}
 
 template <int MODE>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs p,
+__global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
-                                                          int64_t kchunk) {
+                                                          int64_t kc,
+                                                          int vec_ok) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
-  constexpr int KS = kSkinnyKc / 32;  // k-steps per workgroup (max)
-  __shared__ __align__(16) bf16_t sA[64 * kSkinnyLDA];
-  __shared__ float s_ss[64];
+  constexpr int W = kSkWaves, S = kSkStep / NB;
+  __shared__ float sP[W][NB][64][16 + 1];
+  __shared__ float sS[W][64];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
-  const int ntile = blockIdx.x, split = blockIdx.y;
+  const int tile = blockIdx.x, split = blockIdx.y;
   const int64_t M = p.m, N = p.n, K = p.k;
-  const int64_t n = (int64_t)ntile * 64 + wave * 16 + fr;
+  const int64_t n0 = (int64_t)tile * 16;
+  const int64_t n = n0 + fr;
   const bool nval = n < N;
-  const int64_t kb = (int64_t)split * kchunk;
-  const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
-  const int nks = (int)((ke - kb + 31) / 32);
+  const int64_t kw = kc / W;  // multiple of 32
+  const int64_t kb = (int64_t)split * kc + wave * kw;
+  const int64_t ke0 = kb + kw, kend = (int64_t)(split + 1) * kc;
+  const int64_t ke = ke0 < K ? (ke0 < kend ? ke0 : kend) : K;
+  const int nst = kb < ke ? (int)((ke - kb + 31) / 32) : 0;
+  // Operand byte offsets: fragment (f, step ks) of A at a0 + ks * a_ks +
+  // f * a_f, of B at b0 + ks * b_ks (32-bit, through buffer resources).
+  // Fragment-major operands (a_frag / b_frag) hold each MFMA step as one
+  // contiguous 1 KiB block, so every wave load is fully coalesced; row-major
+  // ones give 16 rows x 64 B per load.
+  const uint32_t ks0 = (uint32_t)(kb >> 5);
+  uint32_t a0, a_ks, a_f, b0, b_ks;
+  if (p.a_frag) {
+    a0 = lane * 16;
+    a_ks = 4 * 64 * 16;
+    a_f = 64 * 16;
+  } else {
+    a0 = (uint32_t)(fr * p.lda + 8 * g) * 2;
+    a_ks = 64;
+    a_f = (uint32_t)(16 * p.lda * 2);
+  }
+  if (p.b_frag) {
+    b0 = (uint32_t)(((int64_t)tile * (K >> 5) * 64 + lane) * 16);
+    b_ks = 64 * 16;
+  } else {
+    b0 = (uint32_t)(((nval ? n : 0) * p.ldb + 8 * g) * 2);
+    b_ks = 64;
+  }
+  const bool bval = nval || p.b_frag;
+  const __amdgpu_buffer_rsrc_t ra_rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.a, 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb_rs[2] = {
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.b, 0, 0x7fffffff, 0x00020000),
+      __builtin_amdgcn_make_buffer_rsrc((void*)(NB == 2 ? p.b2 : p.b), 0, 0x7fffffff,
+                                        0x00020000)};
+  auto bld = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  };
 
-  // 1. weight fragments for the whole K range, all loads in flight
-  const bf16_t* Bp[2] = {(const bf16_t*)p.b + (nval ? n : 0) * p.ldb,
-                         (const bf16_t*)(NB == 2 ? p.b2 : p.b) +
-                             (nval ? n : 0) * p.ldb};
-  bf16x8 bw[KS][NB];
+  bf16x8 ra[2][S][4], rb[2][S][NB];
+  auto load = [&](int t0, int set) {
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const int64_t kk = kb + 32 * t + 8 * g;
+    for (int t = 0; t < S; ++t) {
+      const uint32_t ks = ks0 + t0 + t;
+      const bool kin = kb + 32 * (t0 + t) + 8 * g < ke;
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
-      bw[t][b] = (t < nks && kk < ke && nval) ? ld8(Bp[b] + kk) : zero8();
+      for (int b = 0; b < NB; ++b)
+        rb[set][t][b] = (kin && bval) ? bld(rb_rs[b], b0 + ks * b_ks) : zero8();
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const bool rin = p.a_frag || f * 16 + fr < M;
+        ra[set][t][f] = (kin && rin) ? bld(ra_rs, a0 + ks * a_ks + f * a_f) : zero8();
+      }
+    }
+  };
+  f32x4_t acc[NB][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int set) {
+#pragma unroll
+    for (int t = 0; t < S; ++t)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        if (p.rownorm) ss[f] += sumsq8(ra[set][t][f]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          acc[b][f] = mfma16x16x32(ra[set][t][f], rb[set][t][b], acc[b][f]);
+      }
+  };
+  if (nst > 0) load(0, 0);
+  for (int t0 = 0; t0 < nst; t0 += 2 * S) {
+    if (t0 + S < nst) load(t0 + S, 1);
+    compute(0);
+    if (t0 + S >= nst) break;
+    if (t0 + 2 * S < nst) load(t0 + 2 * S, 0);
+    compute(1);
   }
-  // 2. activation slab [64 x Kc] -> LDS (zero rows >= M / columns >= ke)
-  const bf16_t* A = (const bf16_t*)p.a;
-  constexpr int ACH = 64 * (kSkinnyKc / 8) / 256;  // 16 B chunks per thread
-  float ssp[ACH];
+
+  // wave partials -> LDS; lane holds column fr, rows 16 f + 4 g + j
 #pragma unroll
-  for (int c = 0; c < ACH; ++c) {
-    const int i = tid + 256 * c;
-    const int r = i / (kSkinnyKc / 8), ck = i % (kSkinnyKc / 8);
-    const int64_t kk = kb + ck * 8;
-    const bf16x8 v = (r < M && kk < ke) ? ld8(A + r * p.lda + kk) : zero8();
-    st8(&sA[r * kSkinnyLDA + ck * 8], v);
-    ssp[c] = p.rownorm ? sumsq8(v) : 0.f;
-  }
-  // row sums: the 32 chunks of a row sit in 32 consecutive threads
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sP[wave][b][f * 16 + 4 * g + j][fr] = acc[b][f][j];
   if (p.rownorm) {
 #pragma unroll
-    for (int c = 0; c < ACH; ++c) {
-      float v = ssp[c];
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, 64);
-      ssp[c] = v;
+    for (int f = 0; f < 4; ++f) {
+      float v = ss[f];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (g == 0) sS[wave][f * 16 + fr] = v;
     }
-  }
-  if (p.rownorm && (tid & 31) == 0) {
-#pragma unroll
-    for (int c = 0; c < ACH; ++c) s_ss[(tid + 256 * c) / 32] = ssp[c];
   }
   __syncthreads();
 
-  // 3. MFMA over the K range
-  f32x4_t acc[NB][4];
+  // thread t < 128: row t / 2, columns n0 + 8 (t % 2) .. + 7
+  const int row = (tid >> 1) & 63, half = tid & 1;
+  const int64_t ncol = n0 + 8 * half;
+  const int cnt = (int)(N - ncol < 8 ? N - ncol : 8);
+  const bool mine = tid < 128 && row < M && cnt > 0;
+  float v[8], u[8], rsum = 0.f;
 #pragma unroll
-  for (int f = 0; f < 4; ++f)
+  for (int e = 0; e < 8; ++e) v[e] = u[e] = 0.f;
+  if (mine) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < W; ++w) {
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    if (t < nks) {
-#pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        const bf16x8 a = ld8(&sA[(f * 16 + fr) * kSkinnyLDA + 32 * t + 8 * g]);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[b][f] = mfma16x16x32(a, bw[t][b], acc[b][f]);
+      for (int e = 0; e < 8; ++e) {
+        v[e] += sP[w][0][row][8 * half + e];
+        if (NB == 2) u[e] += sP[w][NB - 1][row][8 * half + e];
       }
+      if (p.rownorm) rsum += sS[w][row];
     }
   }
 
   if (splits > 1) {
-    // partials: [NB][split][M rows][N] fp32, then [split][M] row sums
-    float* ws = (float*)p.workspace;
-    const int64_t plane = (int64_t)splits * M * N;
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int f = 0; f < 4; ++f)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (nval && f * 16 + 4 * g + j < M)
-            ws[b * plane + ((int64_t)split * M + f * 16 + 4 * g + j) * N + n] =
-                acc[b][f][j];
-    if (ntile == 0 && p.rownorm && tid < M) ws[NB * plane + split * M + tid] = s_ss[tid];
-    return;
-  }
-
-  // Epilogue: lane holds column n, rows f*16 + 4g + j.
-#pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    float rs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      rs[j] = p.rownorm ? rsqrtf(s_ss[f * 16 + 4 * g + j] / (float)K + p.rownorm_eps)
-                        : 1.f;
-    float v[4], u[4], pv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = acc[0][f][e];
-      u[e] = acc[NB - 1][f][e];
-      pv[e] = (MODE == FVX_GEMM_QKV_ROPE) ? __shfl_xor(v[e], 1, 64) : 0.f;
+    // partial block of (tile, split): [NB][64][16] floats, then 64 row sums
+    constexpr int BLK = skinny_block_floats(NB);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (char*)p.workspace + kCounterBytes, 0, 0x7fffffff, 0x00020000);
+    const int base = (tile * splits + split) * BLK * 4;
+    if (mine) {
+      sc1_store8(rs, base + (row * 16 + 8 * half) * 4, v);
+      if (NB == 2) sc1_store8(rs, base + ((64 + row) * 16 + 8 * half) * 4, u);
+      if (p.rownorm && half == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(rsum), rs,
+                                              base + (NB * 1024 + row) * 4, 0, kSc1);
     }
-    epilogue4<MODE>(p, (int64_t)f * 16 + 4 * g, n, v, u, pv, rs);
+    // every store of this workgroup completes before it is counted
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t* ctr = (uint32_t*)p.workspace + tile;
+      const uint32_t old =
+          __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old == (uint32_t)(splits - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last || !mine) return;
+    // last arrival: every split's loads in flight, added in split order
+    float tv[kSkMaxSplits][8], tu[kSkMaxSplits][8], tr[kSkMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kSkMaxSplits; ++s) {
+      if (s < splits) {
+        const int bs = (tile * splits + s) * BLK * 4;
+        sc1_load8(rs, bs + (row * 16 + 8 * half) * 4, tv[s]);
+        if (NB == 2) sc1_load8(rs, bs + ((64 + row) * 16 + 8 * half) * 4, tu[s]);
+        tr[s] = p.rownorm ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                rs, bs + (NB * 1024 + row) * 4, 0, kSc1))
+                          : 0.f;
+      }
+    }
+    rsum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = u[e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < kSkMaxSplits; ++s) {
+      if (s < splits) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[e] += tv[s][e];
+          if (NB == 2) u[e] += tu[s][e];
+        }
+        rsum += tr[s];
+      }
+    }
   }
+  if (!mine) return;
+  const bool vec = vec_ok && cnt == 8;
+  EpiIn in;
+  epi_load<MODE>(p, row, ncol, vec, cnt, in);
+  const float r = p.rownorm ? rsqrtf(rsum / (float)K + p.rownorm_eps) : 1.f;
+  epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in);
 }
 
 // Sum of the split partials of either GEMM kernel + epilogue.  Thread t of
@@ -479,7 +819,7 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
   const int64_t n = (int64_t)blockIdx.x * 64 + lane;
   const int64_t row = (int64_t)blockIdx.y * 4 + (tid >> 6);
   const bool ok = n < N && row < p.m;
-  const float* ws = (const float*)p.workspace;
+  const float* ws = (const float*)((const char*)p.workspace + kCounterBytes);
   const int64_t M = p.m;
   const int64_t plane = (int64_t)splits * M * N;
   float v = 0.f, u = 0.f, ss = 0.f;
@@ -512,29 +852,51 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
 // ---------------------------------------------------------------------------
 struct SkinnyPlan {
   int n_tiles, splits;
-  int64_t kchunk, ws_bytes;
+  int64_t kc, ws_bytes;
 };
 
+// 16-column tiles over the whole K.  A split of K costs a round trip through
+// the device-coherent level (~4 us measured), so K is split only when one
+// workgroup would otherwise stream more than ~400 KB of operands (64
+// activation rows + 16 NB weight rows per k), and never beyond 256
+// workgroups.  Ranges are multiples of 8 waves x 32 k.
 static SkinnyPlan plan_skinny(const GemmArgs& d) {
   SkinnyPlan s;
   const int nb = d.mode == FVX_GEMM_GEGLU ? 2 : 1;
-  s.n_tiles = (int)((d.n + 63) / 64);
-  int64_t kchunk;
-  if (d.split_k > 0) {
-    kchunk = (d.k + d.split_k - 1) / d.split_k;
-    kchunk = (kchunk + 31) / 32 * 32;
-  } else {
-    // 256-wide K ranges when that already gives ~200+ workgroups, else 128
-    kchunk = s.n_tiles * ((d.k + kSkinnyKc - 1) / kSkinnyKc) >= 200 ? 256 : 128;
+  s.n_tiles = (int)((d.n + 15) / 16);
+  const int64_t unit = 32 * kSkWaves;
+  const int64_t max_splits = (d.k + unit - 1) / unit;
+  int64_t sp = d.split_k;
+  if (sp <= 0) {
+    const int64_t bytes = (64 + 16 * nb) * d.k * 2;
+    sp = (bytes + 400 * 1024 - 1) / (400 * 1024);
+    const int64_t cap = 256 / s.n_tiles;
+    if (sp > cap) sp = cap;
   }
-  if (kchunk > kSkinnyKc) kchunk = kSkinnyKc;
-  if (kchunk < 32) kchunk = 32;
-  s.splits = (int)((d.k + kchunk - 1) / kchunk);
-  s.kchunk = kchunk;
-  s.ws_bytes = s.splits > 1
-                   ? ((int64_t)nb * s.splits * d.m * d.n + (int64_t)s.splits * d.m) * 4
-                   : 0;
+  if (sp > kSkMaxSplits) sp = kSkMaxSplits;
+  if (sp > max_splits) sp = max_splits;
+  if (sp < 1) sp = 1;
+  int64_t kc = (d.k + sp - 1) / sp;
+  kc = (kc + unit - 1) / unit * unit;
+  s.splits = (int)((d.k + kc - 1) / kc);
+  s.kc = kc;
+  s.ws_bytes = s.splits > 1 ? kCounterBytes + (int64_t)s.n_tiles * s.splits *
+                                                   skinny_block_floats(nb) * 4
+                             : 0;
   return s;
+}
+
+// The skinny kernel serves M <= 64 while its arrival counters fit the
+// counter area and its partial offsets fit 31 bits; anything else is tiled.
+static bool use_skinny(const GemmArgs& d) {
+  if (d.m > 64) return false;
+  const SkinnyPlan s = plan_skinny(d);
+  // operand byte offsets are 32-bit
+  const int64_t a_bytes = d.a_frag ? (d.k / 32) * 4 * 1024 : 64 * d.lda * 2;
+  const int64_t b_bytes = d.b_frag ? (int64_t)s.n_tiles * 16 * d.k * 2
+                                   : (int64_t)s.n_tiles * 16 * d.ldb * 2;
+  return s.n_tiles <= kMaxSkinnyTiles && s.ws_bytes < ((int64_t)1 << 31) &&
+         a_bytes < ((int64_t)1 << 31) && b_bytes < ((int64_t)1 << 31);
 }
 
 static int validate(const GemmArgs& d) {
@@ -585,6 +947,22 @@ static int validate(const GemmArgs& d) {
       FVX_REQUIRE(d.xt, FVX_ERR_NULL, "gemm(euler): xt required");
       break;
   }
+  if (d.a_frag || d.b_frag || d.c_frag) {
+    FVX_REQUIRE(d.m <= 64 && use_skinny(d), FVX_ERR_ARG,
+                "gemm: fragment-major operands need m <= 64 (m=%lld)",
+                (long long)d.m);
+    FVX_REQUIRE(!(d.a_frag || d.b_frag) || d.k % 32 == 0, FVX_ERR_SHAPE,
+                "gemm: fragment-major A/B need k %% 32 == 0 (k=%lld)",
+                (long long)d.k);
+    FVX_REQUIRE(!d.b_frag || d.n % 16 == 0, FVX_ERR_SHAPE,
+                "gemm: fragment-major B needs n %% 16 == 0 (n=%lld)",
+                (long long)d.n);
+    FVX_REQUIRE(!d.c_frag || ((d.mode == FVX_GEMM_PLAIN || d.mode == FVX_GEMM_GEGLU) &&
+                              !d.out_f32 && d.n % 32 == 0 && aligned16(d.c_frag)),
+                FVX_ERR_ARG,
+                "gemm: c_frag needs PLAIN/GEGLU bf16 output, n %% 32 == 0 and a "
+                "16B-aligned buffer");
+  }
   return FVX_OK;
 }
 
@@ -594,10 +972,10 @@ using namespace fvx;
 
 extern "C" int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d) {
   if (!d || d->m <= 0) return 0;
-  if (d->m <= 64) return plan_skinny(*d).ws_bytes;
+  if (use_skinny(*d)) return plan_skinny(*d).ws_bytes;
   // tiled path: at most 4 K splits of fp32 partials (+ row sums)
   const int nb = d->mode == FVX_GEMM_GEGLU ? 2 : 1;
-  return ((int64_t)nb * 4 * d->m * d->n + 4 * d->m) * 4;
+  return kCounterBytes + ((int64_t)nb * 4 * d->m * d->n + 4 * d->m) * 4;
 }
 
 #define FVX_MODE_DISPATCH_NG(MODE_RT, LAUNCH)                 \
@@ -623,7 +1001,7 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
   if (st) return st;
   if (d.m == 0) return FVX_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (d.m <= 64) {
+  if (use_skinny(d)) {
     SkinnyPlan sp = plan_skinny(d);
     if (sp.splits > 1 && (!d.workspace || d.workspace_bytes < sp.ws_bytes))
       return set_error(FVX_ERR_WORKSPACE,
@@ -635,20 +1013,13 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "gemm: workspace must be 16B aligned");
     dim3 grid((unsigned)sp.n_tiles, (unsigned)sp.splits);
+    const int vec_ok = epi_vec_ok(d) ? 1 : 0;
 #define L(MODE)                                                          \
-  hipLaunchKernelGGL(gemm_skinny_kernel<MODE>, grid, dim3(256), 0, s, d, \
-                     sp.splits, sp.kchunk)
+  hipLaunchKernelGGL(gemm_skinny_kernel<MODE>, grid, dim3(64 * kSkWaves), \
+                     0, s, d, sp.splits, sp.kc, vec_ok)
     FVX_MODE_DISPATCH(d.mode, L)
 #undef L
-    int st2 = launch_status("gemm(skinny)");
-    if (st2 || sp.splits == 1) return st2;
-#define L(MODE)                                                            \
-  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                      \
-                     dim3(sp.n_tiles, (unsigned)((d.m + 3) / 4)), dim3(256), \
-                     0, s, d, sp.splits)
-    FVX_MODE_DISPATCH(d.mode, L)
-#undef L
-    return launch_status("gemm(skinny reduce)");
+    return launch_status("gemm(skinny)");
   }
   // Tiled path: 128 x 128 tiles (GEGLU: 128 x 64 of each weight) when that
   // gives >= 512 workgroups (two per CU), else 64 x 128.  Projections with a long K and
@@ -674,7 +1045,9 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
   kchunk = (kchunk + 63) / 64 * 64;
   splits = (int)((d.k + kchunk - 1) / kchunk);
   const int nbm = gg ? 2 : 1;
-  const int64_t need = splits > 1 ? ((int64_t)nbm * splits * d.m * d.n + (int64_t)splits * d.m) * 4 : 0;
+  const int64_t need = splits > 1 ? kCounterBytes + ((int64_t)nbm * splits * d.m * d.n +
+                                                     (int64_t)splits * d.m) * 4
+                                   : 0;
   if (splits > 1 && (!d.workspace || d.workspace_bytes < need)) {
     if (d.split_k > 1)
       return set_error(FVX_ERR_WORKSPACE,

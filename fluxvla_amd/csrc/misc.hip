@@ -92,6 +92,18 @@ __global__ void copy_rows_kernel(const bf16_t* __restrict__ src,
   st8(dst + orow * dst_ld + c, ld8(src + r * src_ld + c));
 }
 
+// Row-major [m <= 64, k] -> fragment-major (frag_offset); one thread per
+// 8-column chunk.
+__global__ void pack_frag_kernel(const bf16_t* __restrict__ src, int64_t src_ld,
+                                 bf16_t* __restrict__ dst, int64_t rows,
+                                 int64_t cols) {
+  const int64_t vpr = cols / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * vpr) return;
+  const int64_t r = idx / vpr, c = (idx % vpr) * 8;
+  st8(dst + frag_offset(r, c), ld8(src + r * src_ld + c));
+}
+
 }  // namespace fvx
 
 using namespace fvx;
@@ -166,4 +178,22 @@ extern "C" int fvx_copy_rows(const void* src, int64_t src_ld, void* dst,
                      src_ld, (bf16_t*)dst, dst_ld, rows, (int)cols, row_group,
                      dst_group_stride);
   return launch_status("copy_rows");
+}
+
+extern "C" int fvx_pack_frag(const void* src, int64_t src_ld, void* dst,
+                             int64_t rows, int64_t cols, void* stream) {
+  clear_error();
+  FVX_REQUIRE(src && dst, FVX_ERR_NULL, "pack_frag: src and dst required");
+  FVX_REQUIRE(rows >= 0 && rows <= 64 && cols > 0 && cols % 32 == 0 &&
+                  src_ld % 8 == 0 && src_ld >= cols,
+              FVX_ERR_SHAPE,
+              "pack_frag: need rows <= 64, cols %% 32 == 0, src_ld %% 8 == 0");
+  FVX_REQUIRE(aligned16(src) && aligned16(dst), FVX_ERR_ALIGN,
+              "pack_frag: pointers must be 16B aligned");
+  const int64_t total = rows * (cols / 8);
+  if (total == 0) return FVX_OK;
+  hipLaunchKernelGGL(pack_frag_kernel, dim3((unsigned)((total + 255) / 256)),
+                     dim3(256), 0, (hipStream_t)stream, (const bf16_t*)src,
+                     src_ld, (bf16_t*)dst, rows, cols);
+  return launch_status("pack_frag");
 }

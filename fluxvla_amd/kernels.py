@@ -15,20 +15,26 @@ from ._lib import AttnDesc, GemmDesc
 
 BF16 = torch.bfloat16
 
-# Split-K / split-KV workspace (fp32 partials), one per device, allocated
-# before any graph capture.  Every split op reduces its partials with a
-# second kernel on the same stream, so consecutive calls share it.
+# Split-K / split-KV workspaces (fp32 partials), one pair per device,
+# allocated zero-filled before any graph capture.  The GEMM keeps per-tile
+# arrival counters in the first 4 KiB of its workspace (zero before the first
+# call, left zero by every call), so attention partials go to a buffer of
+# their own.  Calls on one stream share them.
 WORKSPACE_BYTES = 64 << 20
+ATTN_WORKSPACE_BYTES = 32 << 20
 _workspaces = {}
 
 
-def workspace(device=None):
+def workspace(device=None, kind='gemm'):
+    """The per-device ``kind`` ('gemm' or 'attn') workspace."""
     dev = torch.device('cuda', torch.cuda.current_device()
                        if device is None else torch.device(device).index)
-    ws = _workspaces.get(dev.index)
+    key = (dev.index, kind)
+    ws = _workspaces.get(key)
     if ws is None:
-        ws = torch.zeros(WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
-        _workspaces[dev.index] = ws
+        size = WORKSPACE_BYTES if kind == 'gemm' else ATTN_WORKSPACE_BYTES
+        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+        _workspaces[key] = ws
     return ws
 
 
@@ -125,25 +131,117 @@ def adarms_norm(x, style, out=None, gate_out=None, rows_per_style=None,
 
 
 # ---------------------------------------------------------------------------
+# Fragment-major operands (M <= 64 GEMMs): each 16x32 MFMA operand block is
+# one contiguous 1 KiB, so the skinny GEMM streams them with fully coalesced
+# loads (fvx_gemm_desc.a_frag / b_frag / c_frag).
+# ---------------------------------------------------------------------------
+class FragA:
+    """Activations [m <= 64, k] in the fragment-major layout: a bf16 buffer
+    of 64 * k elements, element (r, c) at frag_offset(r, c)."""
+
+    def __init__(self, buf, m, k):
+        if m > 64 or k % 32 or buf.numel() < 64 * k:
+            raise ValueError(f'FragA needs m <= 64, k % 32 == 0 and 64*k '
+                             f'elements (m={m}, k={k}, numel={buf.numel()})')
+        self.buf, self.m, self.k = buf, m, k
+
+    @staticmethod
+    def empty(k, device):
+        return FragA(torch.zeros(64 * k, dtype=BF16, device=device), 64, k)
+
+    def rows(self, m):
+        return FragA(self.buf, m, self.k)
+
+
+class FragB:
+    """A weight [n, k] (nn.Linear layout) in the fragment-major layout
+    [n/16][k/32][4][16][8]; n % 16 == 0, k % 32 == 0."""
+
+    def __init__(self, buf, n, k):
+        self.buf, self.n, self.k = buf, n, k
+
+    @staticmethod
+    def pack(w):
+        n, k = w.shape
+        if n % 16 or k % 32:
+            raise ValueError(f'FragB needs n % 16 == 0 and k % 32 == 0, got '
+                             f'{tuple(w.shape)}')
+        buf = (w.reshape(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4)
+               .contiguous().view(-1))
+        return FragB(buf, n, k)
+
+
+def pack_frag_a_ref(a):
+    """Torch restatement of the FragA layout (tests): [m <= 64, k] ->
+    64 * k elements; rows >= m are zero."""
+    m, k = a.shape
+    full = torch.zeros(64, k, dtype=a.dtype, device=a.device)
+    full[:m] = a
+    return (full.view(4, 16, k // 32, 4, 8).permute(2, 0, 3, 1, 4)
+            .contiguous().view(-1))
+
+
+def pack_frag(src, dst):
+    """Row-major [m <= 64, k] -> FragA ``dst`` (device kernel)."""
+    _check(src, 'src', contiguous=False)
+    rows, sld = _rows_ld(src, 'src')
+    _check(dst.buf, 'dst')
+    if dst.k != src.shape[-1]:
+        raise ValueError('pack_frag: k mismatch')
+    _lib.call('fvx_pack_frag', _ptr(src), sld, _ptr(dst.buf), rows,
+              src.shape[-1], _stream())
+    return dst
+
+
+# ---------------------------------------------------------------------------
 # GEMM family
 # ---------------------------------------------------------------------------
 def _gemm_desc(a, w):
-    _check(a, 'a', contiguous=False)
-    _check(w, 'weight', contiguous=False)
-    m, lda = _rows_ld(a, 'a')
-    n, ldb = _rows_ld(w, 'weight')
-    k = a.shape[-1]
-    if w.shape[-1] != k:
+    d = GemmDesc()
+    if isinstance(a, FragA):
+        _check(a.buf, 'a')
+        m, lda, k = a.m, a.k, a.k
+        d.a, d.a_frag, dev = a.buf.data_ptr(), 1, a.buf.device
+    else:
+        _check(a, 'a', contiguous=False)
+        m, lda = _rows_ld(a, 'a')
+        k = a.shape[-1]
+        d.a, dev = a.data_ptr(), a.device
+    if isinstance(w, FragB):
+        _check(w.buf, 'weight')
+        n, ldb, kw = w.n, w.k, w.k
+        d.b, d.b_frag = w.buf.data_ptr(), 1
+    else:
+        _check(w, 'weight', contiguous=False)
+        n, ldb = _rows_ld(w, 'weight')
+        kw = w.shape[-1]
+        d.b = w.data_ptr()
+    if kw != k:
         raise ValueError(
             f'weight must be [out_features, in_features={k}] (nn.Linear '
-            f'layout), got {tuple(w.shape)}')
-    d = GemmDesc()
-    d.a, d.lda, d.b, d.ldb = a.data_ptr(), lda, w.data_ptr(), ldb
+            f'layout), got in_features={kw}')
+    d.lda, d.ldb = lda, ldb
     d.m, d.n, d.k = m, n, k
     d.gate_group = 1
-    ws = workspace(a.device)
+    ws = workspace(dev)
     d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
     return d
+
+
+def _lead_shape(a):
+    return (a.m,) if isinstance(a, FragA) else tuple(a.shape[:-1])
+
+
+def _device(a):
+    return a.buf.device if isinstance(a, FragA) else a.device
+
+
+def _set_c_frag(d, c_frag):
+    if c_frag is not None:
+        if c_frag.k != d.n:
+            raise ValueError('c_frag must have k == n of the GEMM')
+        _check(c_frag.buf, 'c_frag')
+        d.c_frag = c_frag.buf.data_ptr()
 
 
 def _run_gemm(d):
@@ -153,13 +251,15 @@ def _run_gemm(d):
 def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
          gate=None, gate_group=1, pos=None, pos_period=0, act=_lib.ACT_NONE,
          rownorm_eps=None, out_f32=False, row_group=0, row_group_stride=0,
-         split_k=0):
-    """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order."""
+         split_k=0, c_frag=None):
+    """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order.
+    ``a`` may be a FragA and ``weight`` a FragB; ``c_frag`` (a FragA with
+    k == n) also receives the output in the fragment-major layout."""
     d = _gemm_desc(a, weight)
     if out is None:
-        out = torch.empty(*a.shape[:-1], d.n,
+        out = torch.empty(*_lead_shape(a), d.n,
                           dtype=torch.float32 if out_f32 else BF16,
-                          device=a.device)
+                          device=_device(a))
     _check(out, 'out', dtype=torch.float32 if out_f32 else BF16,
            contiguous=False)
     _, d.ldc = _rows_ld(out, 'out')
@@ -187,25 +287,34 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
         d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
     d.row_group, d.row_group_stride = row_group, row_group_stride
     d.split_k = split_k
+    _set_c_frag(d, c_frag)
     _run_gemm(d)
     return out
 
 
-def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0):
+def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
+               c_frag=None):
     """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T)."""
     d = _gemm_desc(a, gate_w)
-    _check(up_w, 'up_w', contiguous=False)
-    if tuple(up_w.shape) != tuple(gate_w.shape) or up_w.stride() != gate_w.stride():
-        raise ValueError('up_w must match gate_w in shape and strides')
-    d.b2 = up_w.data_ptr()
+    if isinstance(gate_w, FragB):
+        if not isinstance(up_w, FragB) or (up_w.n, up_w.k) != (gate_w.n, gate_w.k):
+            raise ValueError('up_w must be a FragB shaped like gate_w')
+        _check(up_w.buf, 'up_w')
+        d.b2 = up_w.buf.data_ptr()
+    else:
+        _check(up_w, 'up_w', contiguous=False)
+        if tuple(up_w.shape) != tuple(gate_w.shape) or up_w.stride() != gate_w.stride():
+            raise ValueError('up_w must match gate_w in shape and strides')
+        d.b2 = up_w.data_ptr()
     if out is None:
-        out = torch.empty(*a.shape[:-1], d.n, dtype=BF16, device=a.device)
+        out = torch.empty(*_lead_shape(a), d.n, dtype=BF16, device=_device(a))
     _check(out, 'out', contiguous=False)
     _, d.ldc = _rows_ld(out, 'out')
     d.c, d.mode = out.data_ptr(), _lib.GEMM_GEGLU
     if rownorm_eps is not None:
         d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
     d.split_k = split_k
+    _set_c_frag(d, c_frag)
     _run_gemm(d)
     return out
 
@@ -297,7 +406,7 @@ def attention_desc(q, k, v, o, *, sq, sk, heads, head_dim, n_problems=1,
     d.n_problems, d.zdiv = n_problems, zdiv
     d.scale = float(head_dim ** -0.5 if scale is None else scale)
     d.kv_splits = kv_splits
-    ws = workspace(q.device)
+    ws = workspace(q.device, 'attn')
     d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
     return d
 

@@ -233,6 +233,7 @@ class PI0Inference:
         self.use_graph = use_graph
         self.max_batch = max_batch
         K.workspace(self.device)
+        K.workspace(self.device, 'attn')
         self.prepare_triton_inference(state_dict)
         self._graphs = {}
         self._bufs = {}
@@ -283,7 +284,25 @@ class PI0Inference:
             self.mlp_out = mo
         self.rope = K.rope_table(cfg.prefix_len + cfg.suffix_len + 8,
                                  cfg.head_dim, cfg.rope_theta, device=dev)
+        self._prepare_frag_weights()
         torch.cuda.synchronize(dev)
+
+    def _prepare_frag_weights(self):
+        """Fragment-major copies of the action-expert weights for the M <= 64
+        (bs=1) skinny GEMMs: every weight load becomes one coalesced 1 KiB
+        block per wave.  The row-major originals stay for batched calls."""
+        F = K.FragB.pack
+        self.exp_f = []
+        for L in self.exp['layers']:
+            self.exp_f.append({nm: F(L[nm]) for nm in
+                               ('qkv_w', 'o_w', 'gate_w', 'up_w', 'down_w')})
+        self.act_out_f = F(self.act_out['w'])
+        if self.cfg.pi05:
+            self.act_in_f = F(self.act_in['w'])
+        else:
+            self.act_in_f = F(self.act_in['w'])
+            self.mlp_in_a_f = F(self.mlp_in_a)
+            self.mlp_out_f = F(self.mlp_out['w'])
 
     @property
     def kv_len(self):
@@ -331,6 +350,11 @@ class PI0Inference:
             'ex_q': e(B, Ss, cfg.heads * D),
             'ex_ctx': e(B, Ss, cfg.heads * D),
             'ex_h': e(B * Ss, cfg.exp_mlp),
+            # fragment-major copies of x, the attention output and the GeGLU
+            # output for the bs=1 skinny GEMMs (M = suffix_len <= 64)
+            'ex_xf': K.FragA.empty(cfg.exp_hidden, dev),
+            'ex_ctxf': K.FragA.empty(cfg.heads * D, dev),
+            'ex_hf': K.FragA.empty(cfg.exp_mlp, dev),
             'act_h1': e(B * cfg.n_action_steps, cfg.proj_width),
             'act_h2': e(B * cfg.n_action_steps, cfg.proj_width),
             'states': e(B, cfg.state_dim),
@@ -402,7 +426,39 @@ class PI0Inference:
                          rownorm_eps=cfg.rms_eps)
             K.gemm(b['pre_h'], L['down_w'], out=x, residual=x)
 
+    def _frag_ok(self, B):
+        """bs=1 expert GEMMs (M = suffix_len <= 64) run fragment-major."""
+        return B * self.cfg.suffix_len <= 64
+
+    def _expert_layer_pi0_frag(self, b, i, L):
+        """_expert_layer_pi0 at bs=1 with fragment-major operands: x, the
+        attention output and the GeGLU output are kept in the layout of the
+        skinny GEMM's A fragments (the epilogues write it next to the
+        row-major x)."""
+        cfg = self.cfg
+        S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
+        T = self.kv_len
+        Lf = self.exp_f[i]
+        x = b['ex_x'].view(Ss, hid)
+        xf = b['ex_xf'].rows(Ss)
+        ctxf, hf = b['ex_ctxf'].rows(Ss), b['ex_hf'].rows(Ss)
+        kc, vc = b['kc'][i], b['vc'][i]
+        K.gemm_qkv_rope(xf, Lf['qkv_w'], self.rope, b['pos_suf'],
+                        b['ex_q'].view(Ss, -1), kc.view(T, D)[S:],
+                        vc[:, :, S:], cfg.heads, D,
+                        rownorm_eps=cfg.rms_eps, row_group=Ss,
+                        row_group_stride=T, v_ld=T)
+        K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
+                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True)
+        K.pack_frag(b['ex_ctx'].view(Ss, -1), ctxf)
+        K.gemm(ctxf, Lf['o_w'], out=x, residual=x, c_frag=xf)
+        K.gemm_geglu(xf, Lf['gate_w'], Lf['up_w'], out=b['ex_h'],
+                     rownorm_eps=cfg.rms_eps, c_frag=hf)
+        K.gemm(hf, Lf['down_w'], out=x, residual=x, c_frag=xf)
+
     def _expert_layer_pi0(self, b, B, i, L):
+        if self._frag_ok(B):
+            return self._expert_layer_pi0_frag(b, i, L)
         cfg = self.cfg
         S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
         T = self.kv_len
@@ -453,23 +509,28 @@ class PI0Inference:
         Ss, na, hid = cfg.suffix_len, cfg.n_action_steps, cfg.exp_hidden
         x3 = b['ex_x']
         xt_b = b['xt_bf16'].view(B * na, -1)
+        fr = self._frag_ok(B)
+        w_in = self.act_in_f if fr else self.act_in['w']
         if not cfg.pi05:
             K.gemm(b['states'], self.state['w'], out=b['state_emb'],
                    bias=self.state['b'])
+            w_mi = self.mlp_in_a_f if fr else self.mlp_in_a
+            w_mo = self.mlp_out_f if fr else self.mlp_out['w']
         for step in range(len(self.times)):
             if cfg.pi05:
-                K.gemm(xt_b, self.act_in['w'], out=x3.view(B * Ss, hid),
+                K.gemm(xt_b, w_in, out=x3.view(B * Ss, hid),
                        bias=self.act_in['b'])
             else:
-                K.gemm(xt_b, self.act_in['w'], out=b['act_h1'],
-                       bias=self.act_in['b'])
-                K.gemm(b['act_h1'], self.mlp_in_a, out=b['act_h2'],
+                K.gemm(xt_b, w_in, out=b['act_h1'], bias=self.act_in['b'])
+                K.gemm(b['act_h1'], w_mi, out=b['act_h2'],
                        bias_f32=self.step_bias[step], act=ACT_SILU)
-                K.gemm(b['act_h2'], self.mlp_out['w'],
+                K.gemm(b['act_h2'], w_mo,
                        out=x3.view(B * Ss, hid)[1:], bias=self.mlp_out['b'],
                        row_group=na, row_group_stride=Ss)
                 K.copy_rows(b['state_emb'], x3.view(B * Ss, hid),
                             row_group=1, dst_group_stride=Ss)
+                if fr:
+                    K.pack_frag(x3.view(Ss, hid), b['ex_xf'].rows(Ss))
             for i, L in enumerate(self.exp['layers']):
                 if cfg.pi05:
                     self._expert_layer_pi05(b, B, i, L, step)
@@ -485,7 +546,7 @@ class PI0Inference:
                     a, rn = xn, None
                 else:
                     rn = cfg.rms_eps
-                K.gemm_euler(a, self.act_out['w'], self.act_out['b'],
+                K.gemm_euler(a, self.act_out_f, self.act_out['b'],
                              b['xt'][s], self.dt, xt_bf16=b['xt_bf16'][s],
                              rownorm_eps=rn)
 

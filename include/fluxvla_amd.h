@@ -17,11 +17,14 @@
  *     problem (thread-local).  Nothing aborts the process.
  *   - Split-K GEMMs and split-KV attention need a device workspace for
  *     their fp32 partials (size from fvx_gemm_workspace_bytes /
- *     fvx_attention_workspace_bytes; no initial contents needed).  The
- *     partials are reduced by a second kernel on the same stream, so calls
- *     on one stream may share one workspace; calls overlapping on different
- *     streams must not.  A NULL or too small workspace is an error
- *     (FVX_ERR_WORKSPACE) whenever the problem needs a split.
+ *     fvx_attention_workspace_bytes).  Attention needs no initial contents.
+ *     A GEMM workspace holds per-tile arrival counters in its first 4 KiB:
+ *     zero them once before the first fvx_gemm call that uses the buffer;
+ *     every call leaves them zero again.  Keep attention partials out of a
+ *     GEMM workspace.  Calls on one stream may share a workspace; calls
+ *     overlapping on different streams must not.  A NULL or too small
+ *     workspace is an error (FVX_ERR_WORKSPACE) whenever the problem needs a
+ *     split.
  */
 #ifndef FLUXVLA_AMD_H_
 #define FLUXVLA_AMD_H_
@@ -104,6 +107,17 @@ typedef struct fvx_gemm_desc {
    * v_out[((m / row_group) * head_dim + d) * ldv + m % row_group] (the
    * [batch][head_dim][tokens] value-cache layout the attention reads). */
   int32_t v_transposed;
+  /* Fragment-major operands (M <= 64, K % 32 == 0; one MFMA operand step
+   * per contiguous 1 KiB block, so every wave load is fully coalesced):
+   *   a_frag: element (m, k) of A at ((k/32 * 4 + m/16) * 64
+   *           + (k%32)/8 * 16 + m%16) * 8 + k%8  (rows >= M are ignored)
+   *   b_frag: element (n, k) of B (and b2) at (((n/16) * (K/32) + k/32) * 64
+   *           + (k%32)/8 * 16 + n%16) * 8 + k%8  (needs N % 16 == 0)
+   *   c_frag: PLAIN / GEGLU with M <= 64 and N % 32 == 0: the bf16 output
+   *           is also written there in the a_frag layout (K' = N), ready
+   *           as the A operand of the next skinny GEMM. */
+  int32_t a_frag, b_frag;
+  void* c_frag;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */
@@ -215,6 +229,14 @@ int fvx_embed_tokens(const void* table, const int64_t* ids, void* out,
 int fvx_copy_rows(const void* src, int64_t src_ld, void* dst, int64_t dst_ld,
                   int64_t rows, int64_t cols, int64_t row_group,
                   int64_t dst_group_stride, void* stream);
+
+/*
+ * Row-major [rows <= 64, cols] bf16 -> the fragment-major A layout of
+ * fvx_gemm_desc.a_frag (cols % 32 == 0).  No counterpart in the reference:
+ * it re-lays an activation that no fused epilogue wrote in that layout.
+ */
+int fvx_pack_frag(const void* src, int64_t src_ld, void* dst, int64_t rows,
+                  int64_t cols, void* stream);
 
 #ifdef __cplusplus
 }

@@ -145,3 +145,25 @@ def test_registry_rejects_unknown_type():
     from fluxvla_amd.registry import build_vla_from_cfg
     with pytest.raises(KeyError, match='not a registered'):
         build_vla_from_cfg(dict(type='OpenVLA'), {}, device='cpu')
+
+
+def test_fragment_major_layouts():
+    """FragA / FragB packing puts element (r, c) where the kernels'
+    frag_offset formula says: ((c/32 * 4 + r/16) * 64 + (c%32)/8 * 16 +
+    r%16) * 8 + c%8 for A, and the same with the 16-row tile index leading
+    for B."""
+    import torch
+    from fluxvla_amd import kernels as K
+    m, k = 37, 96
+    a = torch.arange(m * k, dtype=torch.float32).view(m, k)
+    pa = K.pack_frag_a_ref(a)
+    for r, c in [(0, 0), (5, 9), (16, 31), (36, 95), (20, 40)]:
+        off = ((c // 32 * 4 + r // 16) * 64 + (c % 32) // 8 * 16 + r % 16) * 8 + c % 8
+        assert pa[off].item() == a[r, c].item()
+    n = 48
+    w = torch.arange(n * k, dtype=torch.float32).view(n, k)
+    pb = K.FragB.pack(w).buf
+    for r, c in [(0, 0), (5, 9), (16, 31), (47, 95), (33, 70)]:
+        off = (((r // 16) * (k // 32) + c // 32) * 64 + (c % 32) // 8 * 16 +
+               r % 16) * 8 + c % 8
+        assert pb[off].item() == w[r, c].item()

@@ -148,6 +148,82 @@ def test_gemm_split_deterministic(K, cuda):
     assert rel_err(o1, o3.float()) <= 4e-3
 
 
+@pytest.mark.parametrize('m,n,k', [(51, 1000, 1000), (7, 1004, 744),
+                                   (64, 72, 4096), (33, 520, 264)])
+def test_gemm_skinny_ragged(K, cuda, m, n, k):
+    """M <= 64: partial column tiles, a partial last K range, N % 8 != 0 (the
+    element-wise epilogue) and an output row stride that is not a multiple
+    of 8 (element-wise stores everywhere), with bias + residual in place."""
+    announce(f'gemm skinny ragged m={m} n={n} k={k}')
+    a = randn((m, k), 24)
+    w = randn((n, k), 25, std=0.02)
+    b = randn((n,), 26, std=0.5)
+    res = randn((m, n), 27)
+    ref = a.float() @ w.float().t() + b.float() + res.float()
+    x = res.clone().to(cuda)
+    K.gemm(a.to(cuda), w.to(cuda), out=x, bias=b.to(cuda), residual=x)
+    assert rel_err(x, ref) <= REL_TOL
+    wide = torch.zeros(m, n + 3, dtype=torch.bfloat16, device=cuda)
+    wide[:, :n] = res.to(cuda)
+    K.gemm(a.to(cuda), w.to(cuda), out=wide[:, :n], bias=b.to(cuda),
+           residual=wide[:, :n])
+    assert rel_err(wide[:, :n], ref) <= REL_TOL
+    assert wide[:, n:].abs().max().item() == 0.0
+
+
+def test_gemm_split_counters_left_zero(K, cuda):
+    """The split-K arrival counters (first 4 KiB of the GEMM workspace) are
+    zero after every call, so back-to-back calls of different shapes and
+    modes each see a clean start; repeated calls are bitwise equal."""
+    announce('gemm split counters')
+    ws = K.workspace(cuda)
+    a = randn((51, 2048), 28).to(cuda)
+    w1 = randn((1024, 2048), 29, std=0.02).to(cuda)
+    w2 = randn((4096, 2048), 31, std=0.02).to(cuda)
+    outs = []
+    for _ in range(3):
+        outs.append(K.gemm(a, w1))
+        K.gemm_geglu(a, w2, w1.repeat(4, 1).contiguous(), rownorm_eps=1e-6)
+        assert ws[:4096].count_nonzero().item() == 0
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+@pytest.mark.parametrize('m,n,k', [(51, 2560, 1024), (51, 1024, 4096),
+                                   (50, 32, 1024), (17, 1024, 32)])
+def test_gemm_fragment_major_operands(K, cuda, m, n, k):
+    """FragA / FragB operands feed the MFMAs the same fragments in the same
+    k order as row-major ones: the outputs are bitwise equal.  c_frag holds
+    the output in the FragA layout (rows < m)."""
+    announce(f'gemm fragment-major m={m} n={n} k={k}')
+    a = randn((m, k), 32).to(cuda)
+    w = randn((n, k), 33, std=0.02).to(cuda)
+    b = randn((n,), 34, std=0.5).to(cuda)
+    res = randn((m, n), 35).to(cuda)
+    af = K.FragA.empty(k, cuda).rows(m)
+    K.pack_frag(a, af)
+    ref_pack = K.pack_frag_a_ref(a.cpu())
+    mask = K.pack_frag_a_ref(torch.ones(m, k, dtype=torch.bfloat16)) != 0
+    assert torch.equal(af.buf.cpu()[mask], ref_pack[mask])
+    wf = K.FragB.pack(w)
+    x0 = res.clone()
+    K.gemm(a, w, out=x0, bias=b, residual=x0)
+    for aa, ww in ((af, w), (a, wf), (af, wf)):
+        x1 = res.clone()
+        cf = K.FragA.empty(n, cuda).rows(m) if n % 32 == 0 else None
+        K.gemm(aa, ww, out=x1, bias=b, residual=x1, c_frag=cf)
+        assert torch.equal(x0, x1)
+        if cf is not None:
+            assert torch.equal(cf.buf.cpu()[K.pack_frag_a_ref(
+                torch.ones(m, n, dtype=torch.bfloat16)) != 0],
+                K.pack_frag_a_ref(x1.cpu())[K.pack_frag_a_ref(
+                    torch.ones(m, n, dtype=torch.bfloat16)) != 0])
+    if n % 16 == 0 and k >= 256:
+        g0 = K.gemm_geglu(a, w, w.flip(0).contiguous(), rownorm_eps=1e-6)
+        g1 = K.gemm_geglu(af, wf, K.FragB.pack(w.flip(0).contiguous()),
+                          rownorm_eps=1e-6)
+        assert torch.equal(g0, g1)
+
+
 def test_gemm_pos_rowgroup_f32(K, cuda):
     announce('gemm pos/row_group/out_f32')
     m, n, k = 768, 1152, 640
