@@ -82,6 +82,7 @@ class AttnDesc(ctypes.Structure):
         ('scale', c_f32),
         ('kv_splits', c_i32),
         ('workspace', c_vp), ('workspace_bytes', c_i64),
+        ('o_frag', c_vp),
     ]
 
 

@@ -47,6 +47,7 @@ __device__ __forceinline__ void store_rows(const fvx_attn_desc& p, bf16_t* O,
 // Zero the elements e >= valid of an 8-key vector (keys past the range).
 __device__ __forceinline__ bf16x8 mask_keys(bf16x8 v, int64_t valid) {
   if (valid >= 8) return v;
+  if (valid <= 0) return zero8();
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     if (2 * w >= valid) v.w[w] = 0u;
@@ -65,6 +66,7 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
   constexpr int ND = HDV / 16;   // 16-wide d chunks of the output
   __shared__ __align__(16) bf16_t sK[kKeyTile * LDK];
   __shared__ __align__(16) bf16_t sVt[HDV * LDV];
+  __shared__ int32_t sG[kKeyTile];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
@@ -95,13 +97,17 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
   const int64_t qtok = qval ? qrow / heads : 0;
   const int64_t qhead = qval ? qrow % heads : 0;
   const int32_t qg = (qgrp && qval) ? qgrp[qtok] : 0;
+  // Branch-free loads through buffer views (an out-of-range offset reads
+  // zero), so that every load of a batch is in flight at once.
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+      Q, (uint32_t)(((p.sq - 1) * p.q_tok_stride + (heads - 1) * p.q_head_stride + HD) * 2));
   bf16x8 qf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int d = 32 * s + 8 * g;
-    qf[s] = (qval && d < HD)
-                ? ld8(Q + qtok * p.q_tok_stride + qhead * p.q_head_stride + d)
-                : zero8();
+    qf[s] = bload8(rq, (qval && d < HD) ? (uint32_t)((qtok * p.q_tok_stride +
+                                                      qhead * p.q_head_stride + d) * 2)
+                                        : kOOB);
   }
 
   const float sc = p.scale * kLog2e;
@@ -115,27 +121,35 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
   const int kchunks = HD / 8;
   const int tile_chunks = kKeyTile * kchunks;
   // Register prefetch of the next K/V tile: CH 16-byte chunks per thread.
+  // Keys >= kend read as zero (K, row-major V: outside the buffer view; V^T:
+  // masked when the tile is written to LDS).
   constexpr int CH = (kKeyTile * (HDP / 8) + 255) / 256;
+  const __amdgpu_buffer_rsrc_t rkc = make_rsrc(K, (uint32_t)(kend * p.k_tok_stride * 2));
+  const __amdgpu_buffer_rsrc_t rvc = make_rsrc(
+      V, (uint32_t)(p.v_d_stride > 0 ? HD * p.v_d_stride * 2 : kend * p.v_tok_stride * 2));
+  const __amdgpu_buffer_rsrc_t rgc =
+      make_rsrc(kgrp ? (const void*)kgrp : (const void*)K, kgrp ? (uint32_t)(kend * 4) : 0u);
   bf16x8 rk[CH], rv[CH];
+  int32_t rgp = 0;
   auto prefetch = [&](int64_t t0) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int i = tid + 256 * c;
-      rk[c] = zero8();
-      rv[c] = zero8();
-      if (i < tile_chunks) {
-        const int64_t jk = t0 + i / kchunks;  // K: key-major chunks
-        if (jk < kend) rk[c] = ld8(K + jk * p.k_tok_stride + (i % kchunks) * 8);
-        if (p.v_d_stride > 0) {
-          // V^T: chunk = 8 consecutive keys of one dim
-          const int64_t j8 = t0 + (i % 4) * 8;
-          if (j8 < kend) rv[c] = mask_keys(ld8(V + (i / 4) * p.v_d_stride + j8), kend - j8);
-        } else {
-          const int64_t jv = t0 + i % kKeyTile;  // V: key-minor chunks
-          if (jv < kend) rv[c] = ld8(V + jv * p.v_tok_stride + (i / kKeyTile) * 8);
-        }
+      const bool in = i < tile_chunks;
+      const int64_t jk = t0 + i / kchunks;  // K: key-major chunks
+      rk[c] = bload8(rkc, in ? (uint32_t)((jk * p.k_tok_stride + (i % kchunks) * 8) * 2) : kOOB);
+      if (p.v_d_stride > 0) {
+        // V^T: chunk = 8 consecutive keys of one dim
+        const int64_t j8 = t0 + (i % 4) * 8;
+        rv[c] = bload8(rvc, in ? (uint32_t)(((i / 4) * p.v_d_stride + j8) * 2) : kOOB);
+      } else {
+        const int64_t jv = t0 + i % kKeyTile;  // V: key-minor chunks
+        rv[c] = bload8(rvc, in ? (uint32_t)((jv * p.v_tok_stride + (i / kKeyTile) * 8) * 2)
+                               : kOOB);
       }
     }
+    if (kgrp && tid < kKeyTile)
+      rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)((t0 + tid) * 4), 0, 0);
   };
   if (kbeg < kend) prefetch(kbeg);
 
@@ -147,7 +161,8 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
       if (i < tile_chunks) {
         st8(&sK[(i / kchunks) * LDK + (i % kchunks) * 8], rk[c]);
         if (p.v_d_stride > 0) {
-          st8(&sVt[(i / 4) * LDV + (i % 4) * 8], rv[c]);
+          st8(&sVt[(i / 4) * LDV + (i % 4) * 8],
+              mask_keys(rv[c], kend - (t0 + (i % 4) * 8)));
         } else {
           const bf16_t* ve = (const bf16_t*)&rv[c];
           const int key = i % kKeyTile, c8 = i / kKeyTile;
@@ -156,6 +171,7 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
         }
       }
     }
+    if (kgrp && tid < kKeyTile) sG[tid] = rgp;
     __syncthreads();
     if (t0 + kKeyTile < kend) prefetch(t0 + kKeyTile);
 
@@ -172,7 +188,7 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
       for (int e = 0; e < 4; ++e) {
         const int64_t j = t0 + kf * 16 + 4 * g + e;
         bool vis = j < kend;
-        if (vis && kgrp) vis = kgrp[j] <= qg;
+        if (vis && kgrp) vis = sG[kf * 16 + 4 * g + e] <= qg;
         s[kf][e] = vis ? acc[e] * sc : -INFINITY;
       }
     }
@@ -323,28 +339,63 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(fvx_attn_desc p,
 }
 
 // ---------------------------------------------------------------------------
-// Decode-shaped attention: no LDS, no barriers.  Work item = one wave =
-// (problem z, 16 query rows, key range).  K comes straight from the cache as
-// the A operand of S^T = K Q^T, with the rows of each 16-key fragment mapped
-// to keys 8 * (i / 4) + 4 * kf + i % 4: lane group g then holds the 8
-// consecutive keys 8g .. 8g + 7 of the 32-key tile, so its probabilities are
-// a ready A operand of P V and the transposed value cache gives the B
-// operand in one 16-byte load per 16 output dims.  The next tile's K loads
-// are issued before the softmax and its V loads before the next QK^T.
+// Decode-shaped attention: the action expert's 408 query rows (51 tokens x 8
+// heads) against the ~870-key prefix + suffix cache.  Per-CU load throughput
+// decides this kernel, so every global load is fully coalesced: a workgroup
+// of 4 waves owns 64 query rows and one key range, and copies Q once and
+// then 64-key tiles of K (32 KB contiguous) and of the transposed value
+// cache (256 rows of 128 B) into LDS; the next tile is prefetched into
+// registers while the current one feeds the MFMAs.  Each wave computes
+// S^T = K Q^T for its 16 query rows.  K rows sit in LDS in the order that
+// leaves lane group g holding keys 8g .. 8g+7 of each 32-key step (row of
+// key 32s + 8a + 4h + b is 32s + 16h + 4a + b), so the probabilities are the
+// A operand of O += P V with no shuffle, and each 16-row fragment read is 16
+// consecutive LDS rows (conflict-free).  Online-softmax statistics are fp32.
+// The O tile is transposed through LDS so that partials (and, without a
+// split, the output) move as 16-byte row chunks; attn_decode_merge_kernel
+// combines split partials in split order (deterministic).  Both can write
+// the output also in the fragment-major A layout of the o-projection.
 // ---------------------------------------------------------------------------
-constexpr int64_t kDecPF = 16 * 64 * 4 + 2 * 16;  // partial floats per item
+constexpr int kDecKT = 64;                    // keys per tile
+constexpr int kDecQP = 256 + 8;               // LDS pitch (elements), Q / K rows
+constexpr int kDecVP = kDecKT + 8;            // LDS pitch (elements), V^T rows
+constexpr int kDecOP = 256 + 4;               // LDS pitch (floats), O rows
+constexpr int64_t kDecPF = 64 * 256 + 2 * 64;  // partial floats per workgroup
+constexpr int kDecLDS = (64 * kDecQP + 256 * kDecVP) * 2;
+
+__device__ __forceinline__ int dec_krow(int jl) {
+  // LDS row of tile key jl = 32 s + 8 a + 4 h + b
+  return (jl & ~31) + ((jl >> 2) & 1) * 16 + ((jl >> 3) & 3) * 4 + (jl & 3);
+}
+
+// One output chunk: 8 dims of query row r (token r / heads) of problem z.
+__device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int64_t z,
+                                          int64_t r, int d0, const float* v) {
+  const int64_t tok = r / p.heads, h = r % p.heads;
+  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
+  bf16_t* O = (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2;
+  const bf16x8 b = pack8(v);
+  st8(O + tok * p.o_tok_stride + h * p.o_head_stride + d0, b);
+  if (p.o_frag)
+    st8((bf16_t*)p.o_frag + frag_offset(z * p.sq + tok, h * 256 + d0), b);
+}
 
 __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
-                                                          int n_rb, int splits,
-                                                          int64_t kps,
-                                                          int n_items) {
-  constexpr int HD = 256, NS = HD / 32, ND = HD / 16;
-  const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= n_items) return;  // whole wave
+                                                          int n_rg, int splits,
+                                                          int64_t kps) {
+  constexpr int HD = 256;
+  __shared__ __align__(16) unsigned char smem[kDecLDS];
+  __shared__ int32_t sG[kDecKT];
+  __shared__ float sM[64], sL[64];
+  bf16_t* sQK = (bf16_t*)smem;                      // Q, then K tiles
+  bf16_t* sV = (bf16_t*)smem + 64 * kDecQP;         // V^T tiles
+  float* sO = (float*)smem;                         // O rows at the end
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
-  const int rb = item % n_rb, split = (item / n_rb) % splits;
-  const int z = item / (n_rb * splits);
+  const int rg = blockIdx.x % n_rg;
+  const int split = (blockIdx.x / n_rg) % splits;
+  const int64_t z = blockIdx.x / (n_rg * splits);
   const int64_t heads = p.heads, R = p.sq * heads;
   const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
@@ -352,71 +403,103 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   const bf16_t* Vt = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
   const int32_t* kgrp = p.kgrp ? p.kgrp + zb * p.kgrp_zs1 : nullptr;
   const int32_t* qgrp = p.qgrp ? p.qgrp + zb * p.qgrp_zs1 : nullptr;
-
-  const int64_t qrow = (int64_t)rb * 16 + fr;
-  const bool qval = qrow < R;
-  const int64_t qtok = qval ? qrow / heads : 0, qhead = qval ? qrow % heads : 0;
-  const int32_t qg = (qgrp && qval) ? qgrp[qtok] : 0;
-  bf16x8 qf[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s)
-    qf[s] = qval ? ld8(Q + qtok * p.q_tok_stride + qhead * p.q_head_stride +
-                       32 * s + 8 * g)
-                 : zero8();
-
   const int64_t kbeg = (int64_t)split * kps;
   const int64_t kend = (kbeg + kps < p.sk) ? kbeg + kps : p.sk;
-  const int krow = 8 * (fr >> 2) + (fr & 3);  // tile row of this lane (kf=0)
-  bf16x8 kr[2][NS], vr[ND];
-  auto load_k = [&](int64_t t0) {
+
+  // Buffer views: rows past the range read as zero (K: keys >= kend; V^T:
+  // the last row's tail; Q: rows >= R get an out-of-range offset).
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+      Q, (uint32_t)(((p.sq - 1) * p.q_tok_stride + (heads - 1) * p.q_head_stride + HD) * 2));
+  const __amdgpu_buffer_rsrc_t rkc = make_rsrc(K, (uint32_t)(kend * p.k_tok_stride * 2));
+  const __amdgpu_buffer_rsrc_t rvc = make_rsrc(Vt, (uint32_t)(HD * p.v_d_stride * 2));
+  const __amdgpu_buffer_rsrc_t rgc =
+      make_rsrc(kgrp ? (const void*)kgrp : (const void*)Q, kgrp ? (uint32_t)(kend * 4) : 0u);
+
+  // Q rows of this group (32 16-byte chunks per row) and the first K/V tile
+  // are requested together; Q goes through LDS into VGPRs.
+  bf16x8 rqv[8];
 #pragma unroll
-    for (int kf = 0; kf < 2; ++kf) {
-      const int64_t j = t0 + krow + 4 * kf;
+  for (int u = 0; u < 8; ++u) {
+    const int c = tid + 256 * u, i = c >> 5, ck = c & 31;
+    const int r = rg * 64 + i;
+    rqv[u] = bload8(rq, r < R ? (uint32_t)(((r / (int)heads) * p.q_tok_stride +
+                                            (r % (int)heads) * p.q_head_stride + ck * 8) * 2)
+                              : kOOB);
+  }
+
+  // Next-tile prefetch: unconditional buffer loads (all in flight at once);
+  // V keys past kend are zeroed when the tile is written to LDS.
+  bf16x8 rk[8], rv[8];
+  int32_t rgp = 0;
+  auto prefetch = [&](int64_t t0) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        kr[kf][s] = j < kend ? ld8(K + j * p.k_tok_stride + 32 * s + 8 * g) : zero8();
+    for (int u = 0; u < 8; ++u) {
+      const int c = tid + 256 * u;
+      const int64_t j = t0 + (c >> 5);  // K: 32 chunks per key row
+      rk[u] = bload8(rkc, (uint32_t)((j * p.k_tok_stride + (c & 31) * 8) * 2));
+      const int64_t j8 = t0 + (c & 7) * 8;  // V^T: 8 chunks per dim row
+      rv[u] = bload8(rvc, (uint32_t)(((int64_t)(c >> 3) * p.v_d_stride + j8) * 2));
     }
+    if (kgrp && tid < kDecKT)
+      rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)((t0 + tid) * 4), 0, 0);
   };
-  auto load_v = [&](int64_t t0) {
-    const int64_t j8 = t0 + 8 * g;
+
+  if (kbeg < kend) prefetch(kbeg);
+  const int64_t qrow = (int64_t)rg * 64 + wave * 16 + fr;
+  const int32_t qg = (qgrp && qrow < R) ? qgrp[qrow / heads] : 0;
 #pragma unroll
-    for (int df = 0; df < ND; ++df)
-      vr[df] = j8 < kend ? mask_keys(ld8(Vt + (df * 16 + fr) * p.v_d_stride + j8),
-                                     kend - j8)
-                         : zero8();
-  };
+  for (int u = 0; u < 8; ++u) {
+    const int c = tid + 256 * u;
+    st8(&sQK[(c >> 5) * kDecQP + (c & 31) * 8], rqv[u]);
+  }
+  __syncthreads();
+  bf16x8 qf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) qf[s] = ld8(&sQK[(wave * 16 + fr) * kDecQP + 32 * s + 8 * g]);
 
   const float sc = p.scale * kLog2e;
   float m_run = -INFINITY, l_run = 0.f;
-  f32x4_t o[ND];
+  f32x4_t o[16];
 #pragma unroll
-  for (int i = 0; i < ND; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (kbeg < kend) {
-    load_k(kbeg);
-    load_v(kbeg);
-  }
-  for (int64_t t0 = kbeg; t0 < kend; t0 += kKeyTile) {
-    float s[8];
+  for (int i = 0; i < 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int64_t t0 = kbeg; t0 < kend; t0 += kDecKT) {
+    __syncthreads();  // previous tile (or the Q copy) fully read
 #pragma unroll
-    for (int kf = 0; kf < 2; ++kf) {
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ss = 0; ss < NS; ++ss) acc = mfma16x16x32(kr[kf][ss], qf[ss], acc);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) s[4 * kf + e] = acc[e];
+    for (int u = 0; u < 8; ++u) {
+      const int c = tid + 256 * u;
+      st8(&sQK[dec_krow(c >> 5) * kDecQP + (c & 31) * 8], rk[u]);
+      st8(&sV[(c >> 3) * kDecVP + (c & 7) * 8],
+          mask_keys(rv[u], kend - (t0 + (c & 7) * 8)));
     }
-    const bool more = t0 + kKeyTile < kend;
-    if (more) load_k(t0 + kKeyTile);
-    // lane group g holds keys t0 + 8g + e
+    if (kgrp && tid < kDecKT) sG[tid] = rgp;
+    __syncthreads();
+    if (t0 + kDecKT < kend) prefetch(t0 + kDecKT);
+
+    // S^T for keys t0 + 32 s + 8 g + e (e = 4 h + j), query row qrow
+    float sv[2][8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < 8; ++ds)
+          acc = mfma16x16x32(ld8(&sQK[(32 * s + 16 * h + fr) * kDecQP + 32 * ds + 8 * g]),
+                             qf[ds], acc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sv[s][4 * h + j] = acc[j];
+      }
     float tmax = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int64_t j = t0 + 8 * g + e;
-      bool vis = j < kend;
-      if (vis && kgrp) vis = kgrp[j] <= qg;
-      s[e] = vis ? s[e] * sc : -INFINITY;
-      tmax = fmaxf(tmax, s[e]);
-    }
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int jl = 32 * s + 8 * g + e;
+        bool vis = t0 + jl < kend;
+        if (vis && kgrp) vis = sG[jl] <= qg;
+        sv[s][e] = vis ? sv[s][e] * sc : -INFINITY;
+        tmax = fmaxf(tmax, sv[s][e]);
+      }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
@@ -424,102 +507,121 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     const float alpha = exp2f(m_run - m_ref);
     float psum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      s[e] = exp2f(s[e] - m_ref);
-      psum += s[e];
-    }
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sv[s][e] = exp2f(sv[s][e] - m_ref);
+        psum += sv[s][e];
+      }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    const bf16x8 pa = pack8(s);
     float al[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) al[j] = __shfl(alpha, 4 * g + j, 64);
 #pragma unroll
-    for (int df = 0; df < ND; ++df) {
+    for (int df = 0; df < 16; ++df)
 #pragma unroll
       for (int j = 0; j < 4; ++j) o[df][j] *= al[j];
-      o[df] = mfma16x16x32(pa, vr[df], o[df]);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const bf16x8 pa = pack8(sv[s]);
+#pragma unroll
+      for (int df = 0; df < 16; ++df)
+        o[df] = mfma16x16x32(pa, ld8(&sV[(16 * df + fr) * kDecVP + 32 * s + 8 * g]), o[df]);
     }
-    if (more) load_v(t0 + kKeyTile);
   }
 
-  if (splits > 1) {
-    float* part = (float*)p.workspace + (int64_t)item * kDecPF;
+  // O rows (lane: rows 16 wave + 4 g + j, dim 16 df + fr) -> LDS row-major
+  __syncthreads();
 #pragma unroll
-    for (int df = 0; df < ND; ++df) *(f32x4_t*)(part + (df * 64 + lane) * 4) = o[df];
-    if (g == 0) {
-      part[ND * 64 * 4 + fr] = m_run;
-      part[ND * 64 * 4 + 16 + fr] = l_run;
-    }
-    return;
+  for (int df = 0; df < 16; ++df)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sO[(wave * 16 + 4 * g + j) * kDecOP + 16 * df + fr] = o[df][j];
+  if (g == 0) {
+    sM[wave * 16 + fr] = m_run;
+    sL[wave * 16 + fr] = l_run;
   }
-  bf16_t* O = (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2;
-  store_rows<ND>(p, O, (int64_t)rb * 16 + 4 * g, R, heads, HD, fr, g, o, l_run);
+  __syncthreads();
+  float* part = splits > 1 ? (float*)p.workspace +
+                                 (((int64_t)z * n_rg + rg) * splits + split) * kDecPF
+                           : nullptr;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int c = tid + 256 * u, i = c >> 5, d0 = (c & 31) * 8;
+    const int64_t r = (int64_t)rg * 64 + i;
+    if (r >= R) continue;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = sO[i * kDecOP + d0 + e];
+    if (part) {
+      *(f32x4_t*)(part + i * 256 + d0) = f32x4_t{v[0], v[1], v[2], v[3]};
+      *(f32x4_t*)(part + i * 256 + d0 + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+    } else {
+      const float l = sL[i];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] *= inv;
+      dec_store(p, z, r, d0, v);
+    }
+  }
+  if (part && tid < 64) {
+    part[64 * 256 + tid] = sM[tid];
+    part[64 * 256 + 64 + tid] = sL[tid];
+  }
+  (void)HD;
 }
 
-// Merge of the decode partials: one thread per (problem, 16-row block,
-// output fragment float4) = 4 rows x 1 dim; every split's loads of a batch
-// of 8 are issued before the running-max merge, applied in split order.
+// Merge of the decode partials: one thread per (problem, query row, 8 dims);
+// every split's loads are issued before the running-max merge, which is
+// applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
-    fvx_attn_desc p, int n_rb, int splits) {
-  constexpr int ND = 16;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t n_blk = (int64_t)p.n_problems * n_rb;
-  if (gid >= n_blk * ND * 64) return;
-  const int64_t blk = gid / (ND * 64);
-  const int fi = (int)(gid % (ND * 64));
-  const int df = fi / 64, lane = fi % 64, fr = lane & 15, g = lane >> 4;
-  const int z = (int)(blk / n_rb), rb = (int)(blk % n_rb);
-  // item index of split s: rb + n_rb * (s + splits * z)
-  float M[4], L[4];
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    M[j] = -INFINITY;
-    L[j] = 0.f;
-  }
-  for (int s0 = 0; s0 < splits; s0 += 8) {
-    f32x4_t ov[8], mv[8], lv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (s0 + i < splits) {
-        const float* part =
-            (const float*)p.workspace +
-            ((int64_t)rb + (int64_t)n_rb * (s0 + i + (int64_t)splits * z)) * kDecPF;
-        ov[i] = *(const f32x4_t*)(part + (df * 64 + lane) * 4);
-        mv[i] = *(const f32x4_t*)(part + ND * 64 * 4 + 4 * g);
-        lv[i] = *(const f32x4_t*)(part + ND * 64 * 4 + 16 + 4 * g);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (s0 + i < splits) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float mn = fmaxf(M[j], mv[i][j]);
-          const float mr = (mn == -INFINITY) ? 0.f : mn;
-          const float a = exp2f(M[j] - mr), b = exp2f(mv[i][j] - mr);
-          acc[j] = acc[j] * a + ov[i][j] * b;
-          L[j] = L[j] * a + lv[i][j] * b;
-          M[j] = mn;
-        }
-      }
-    }
-  }
-  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
-  bf16_t* O = (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2;
+    fvx_attn_desc p, int n_rg, int splits) {
   const int64_t R = p.sq * p.heads;
-  const int d = df * 16 + fr;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (int64_t)p.n_problems * R * 32) return;
+  const int d0 = (int)(gid & 31) * 8;
+  const int64_t zr = gid >> 5;
+  const int64_t z = zr / R, r = zr % R;
+  const int64_t rg = r / 64, i = r % 64;
+  const float* base = (const float*)p.workspace + ((z * n_rg + rg) * splits) * kDecPF;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
+  float acc[8], M = -INFINITY, L = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t r = (int64_t)rb * 16 + 4 * g + j;
-    if (r >= R) break;
-    const int64_t tok = r / p.heads, h = r % p.heads;
-    O[tok * p.o_tok_stride + h * p.o_head_stride + d] =
-        f2bf(L[j] > 0.f ? acc[j] / L[j] : 0.f);
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    f32x4_t a[8], b[8];
+    float mv[8], lv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      // splits past the end read as zero (out of the buffer view)
+      const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
+      a[u] = bload4f(rw, off + (uint32_t)(i * 256 + d0) * 4);
+      b[u] = bload4f(rw, off + (uint32_t)(i * 256 + d0 + 4) * 4);
+      mv[u] = bload1f(rw, off + (uint32_t)(64 * 256 + i) * 4);
+      lv[u] = bload1f(rw, off + (uint32_t)(64 * 256 + 64 + i) * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s0 + u < splits) {
+        const float mn = fmaxf(M, mv[u]);
+        const float mr = (mn == -INFINITY) ? 0.f : mn;
+        const float wa = exp2f(M - mr), wb = exp2f(mv[u] - mr);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] = acc[e] * wa + a[u][e] * wb;
+          acc[4 + e] = acc[4 + e] * wa + b[u][e] * wb;
+        }
+        L = L * wa + lv[u] * wb;
+        M = mn;
+      }
+    }
   }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] *= inv;
+  dec_store(p, z, r, d0, acc);
 }
 
 struct AttnPlan {
@@ -567,14 +669,18 @@ static bool use_decode(const fvx_attn_desc& d) {
   return d.v_d_stride > 0 && d.head_dim == 256 && d.sq * d.heads <= 512;
 }
 
+// 64-row groups x key ranges of whole 64-key tiles; by default about 128
+// workgroups.
 static DecodePlan plan_decode(const fvx_attn_desc& d) {
   DecodePlan a;
-  a.n_rb = (int)((d.sq * d.heads + 15) / 16);
-  int splits = d.kv_splits;
-  if (splits <= 0) splits = (int)((d.sk + 95) / 96);  // ~3 key tiles per wave
+  a.n_rb = (int)((d.sq * d.heads + 63) / 64);
+  const int64_t tiles = (d.sk + kDecKT - 1) / kDecKT;
+  int64_t splits = d.kv_splits;
+  if (splits <= 0) splits = (128 + (int64_t)a.n_rb * d.n_problems - 1) /
+                            ((int64_t)a.n_rb * d.n_problems);
+  if (splits > tiles) splits = tiles;
   if (splits < 1) splits = 1;
-  int64_t kps = (d.sk + splits - 1) / splits;
-  kps = (kps + kKeyTile - 1) / kKeyTile * kKeyTile;
+  const int64_t kps = (tiles + splits - 1) / splits * kDecKT;
   a.splits = (int)((d.sk + kps - 1) / kps);
   a.kps = kps;
   a.n_items = (int)(a.n_rb * a.splits * d.n_problems);
@@ -619,6 +725,12 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
               FVX_ERR_SHAPE,
               "attention: a transposed V needs head_dim 256, v_d_stride %% 8 "
               "== 0 and sk <= v_d_stride");
+  FVX_REQUIRE(!d.o_frag || (use_decode(d) && d.n_problems * d.sq <= 64 &&
+                             d.o_head_stride % 8 == 0 && d.o_tok_stride % 8 == 0 &&
+                             aligned16(d.o) && aligned16(d.o_frag)),
+              FVX_ERR_ARG,
+              "attention: o_frag needs the decode path (transposed V, head_dim "
+              "256), n_problems * sq <= 64 and 16B-aligned outputs");
   if (d.sq == 0 || d.n_problems == 0) return FVX_OK;
   FVX_REQUIRE(d.sk > 0, FVX_ERR_SHAPE, "attention: sk must be > 0");
   hipStream_t s = (hipStream_t)stream;
@@ -631,11 +743,11 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
                        (long long)d.workspace_bytes);
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "attention: workspace must be 16B aligned");
-    hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)((a.n_items + 3) / 4)),
-                       dim3(256), 0, s, d, a.n_rb, a.splits, a.kps, a.n_items);
+    hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)a.n_items), dim3(256),
+                       0, s, d, a.n_rb, a.splits, a.kps);
     int st = launch_status("attention(decode)");
     if (st || a.splits == 1) return st;
-    const int64_t threads = (int64_t)d.n_problems * a.n_rb * 16 * 64;
+    const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 32;
     hipLaunchKernelGGL(attn_decode_merge_kernel,
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                        d, a.n_rb, a.splits);

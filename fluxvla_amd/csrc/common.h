@@ -75,6 +75,34 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const bf16x8& a,
                                                  0, 0);
 }
 
+// Raw buffer access: loads at byte offsets >= `bytes` return zero without
+// touching memory, so a guarded load needs no branch (a branch around each
+// load makes the compiler wait for it at the join, serializing the loads).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                            uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           (int)bytes, 0x00020000);
+}
+
+constexpr uint32_t kOOB = 0x80000000u;  // an offset beyond any buffer here
+
+__device__ __forceinline__ bf16x8 bload8(__amdgpu_buffer_rsrc_t r,
+                                         uint32_t off) {
+  return __builtin_bit_cast(bf16x8,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ f32x4_t bload4f(__amdgpu_buffer_rsrc_t r,
+                                           uint32_t off) {
+  return __builtin_bit_cast(f32x4_t,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float bload1f(__amdgpu_buffer_rsrc_t r,
+                                         uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
 // Element offset of (row m, column k) of an M <= 64 operand in the
 // fragment-major layout [K / 32 steps][4 row blocks][64 lanes][8]: lane =
 // 16 g + m % 16 with g = (k % 32) / 8, so one 16x32 MFMA A fragment is one

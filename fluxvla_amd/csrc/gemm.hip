@@ -143,30 +143,6 @@ struct EpiIn {
   float xt[8];  // EULER state
 };
 
-__device__ __forceinline__ void ld_f8(const float* src, bool vec, int cnt,
-                                      float* d) {
-  if (vec) {
-    const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      d[e] = a[e];
-      d[4 + e] = b[e];
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) d[e] = e < cnt ? src[e] : 0.f;
-  }
-}
-
-__device__ __forceinline__ bf16x8 ld_b8(const bf16_t* src, bool vec, int cnt) {
-  if (vec) return ld8(src);
-  bf16x8 v = zero8();
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    if (e < cnt) v.w[e >> 1] |= (uint32_t)src[e] << (16 * (e & 1));
-  return v;
-}
-
 __device__ __forceinline__ void st_b8(bf16_t* dst, const float* x, bool vec,
                                       int cnt) {
   if (vec) {
@@ -190,39 +166,74 @@ __device__ __forceinline__ void st_f8(float* dst, const float* x, bool vec,
   }
 }
 
+// Buffer-view reads for the epilogue: a NULL operand gets an empty view (all
+// reads return zero) and no load sits behind a branch, so the compiler can
+// keep every load of a batch in flight (a branch around a load makes it
+// wait for that load at the join).
+__device__ __forceinline__ uint32_t rec_bytes(int64_t b) {
+  return b > 0x7fffffff ? 0x7fffffffu : (uint32_t)b;
+}
+
+__device__ __forceinline__ bf16x8 bl_b8(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                        bool vec) {
+  if (vec) return bload8(r, off);
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    v.w[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off + 4 * i, 0, 0) |
+             ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off + 4 * i + 2, 0, 0) << 16);
+  return v;
+}
+
+__device__ __forceinline__ void bl_f8(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                      bool vec, float* d) {
+  if (vec) {
+    const f32x4_t a = bload4f(r, off), b = bload4f(r, off + 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      d[e] = a[e];
+      d[4 + e] = b[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = bload1f(r, off + 4 * e);
+  }
+}
+
 template <int MODE>
 __device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
                                          int64_t n, bool vec, int cnt,
                                          EpiIn& in) {
+  (void)cnt;
   if (MODE == FVX_GEMM_GEGLU) return;
   if (MODE == FVX_GEMM_QKV_ROPE) {
     const int hd = p.head_dim;
-    if (n < (int64_t)(p.n_q_heads + 1) * hd) {
-      const int64_t pos = p.positions[m];
-      ld_f8(p.rope + (pos * (hd >> 1) + ((n % hd) >> 1)) * 2, vec, cnt, in.f0);
-    }
+    const bool rot = n < (int64_t)(p.n_q_heads + 1) * hd;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.positions, rec_bytes(p.m * 4));
+    const int64_t pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (uint32_t)(m * 4), 0, 0);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.rope, 0x7fffffffu);
+    bl_f8(rr, rot ? (uint32_t)((pos * (hd >> 1) + ((n % hd) >> 1)) * 8) : kOOB, vec,
+          in.f0);
     return;
   }
-  in.bias = p.bias ? ld_b8((const bf16_t*)p.bias + n, vec, cnt) : zero8();
-  if (p.bias_f32) {
-    ld_f8(p.bias_f32 + n, vec, cnt, in.f0);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) in.f0[e] = 0.f;
-  }
+  const int64_t N = p.n;
+  in.bias = bl_b8(make_rsrc(p.bias, p.bias ? rec_bytes(N * 2) : 0u), (uint32_t)(n * 2), vec);
+  bl_f8(make_rsrc(p.bias_f32, p.bias_f32 ? rec_bytes(N * 4) : 0u), (uint32_t)(n * 4), vec,
+        in.f0);
   if (MODE == FVX_GEMM_EULER) {
-    ld_f8(p.xt + m * p.ldx + n, vec, cnt, in.xt);
+    bl_f8(make_rsrc(p.xt, rec_bytes(p.m * p.ldx * 4)), (uint32_t)((m * p.ldx + n) * 4), vec,
+          in.xt);
     return;
   }
-  in.gate = p.gate ? ld_b8((const bf16_t*)p.gate + (m / p.gate_group) * p.ldg + n,
-                           vec, cnt)
-                   : zero8();
-  in.res = p.residual ? ld_b8((const bf16_t*)p.residual + out_row(p, m) * p.ldr + n,
-                              vec, cnt)
-                      : zero8();
-  in.pos = p.pos ? ld_b8((const bf16_t*)p.pos + (m % p.pos_period) * p.ldp + n,
-                         vec, cnt)
-                 : zero8();
+  const int64_t gg = p.gate_group > 0 ? p.gate_group : 1;
+  in.gate = bl_b8(make_rsrc(p.gate, p.gate ? rec_bytes((p.m + gg - 1) / gg * p.ldg * 2) : 0u),
+                  (uint32_t)(((m / gg) * p.ldg + n) * 2), vec);
+  in.res = bl_b8(make_rsrc(p.residual,
+                           p.residual ? rec_bytes((out_row(p, p.m - 1) + 1) * p.ldr * 2) : 0u),
+                 (uint32_t)((out_row(p, m) * p.ldr + n) * 2), vec);
+  const int64_t pp = p.pos_period > 0 ? p.pos_period : 1;
+  in.pos = bl_b8(make_rsrc(p.pos, p.pos ? rec_bytes(pp * p.ldp * 2) : 0u),
+                 (uint32_t)(((m % pp) * p.ldp + n) * 2), vec);
 }
 
 // v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
@@ -403,21 +414,27 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
 #pragma unroll
   for (int i = 0; i < AI; ++i) ss[i] = 0.f;
 
+  // Buffer views of this tile's A rows and B rows: rows past M / N read as
+  // zero, and a slab past the K range gets an out-of-view offset, so every
+  // load is unconditional (no branch, hence no conservative wait at a join:
+  // the next slabs' loads stay in flight under the MFMAs).
+  const int64_t a_rows = (M - m0 < BM) ? M - m0 : BM;
+  const int64_t b_rows = (N - n0 < BN) ? N - n0 : BN;
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + m0 * p.lda, (uint32_t)(a_rows * p.lda * 2));
+  const __amdgpu_buffer_rsrc_t rB[2] = {
+      make_rsrc(Bm[0] + n0 * p.ldb, (uint32_t)(b_rows * p.ldb * 2)),
+      make_rsrc((NB == 2 ? Bm[1] : Bm[0]) + n0 * p.ldb, (uint32_t)(b_rows * p.ldb * 2))};
   auto gload = [&](int t, int set) {
     const int64_t kk = kb + (int64_t)t * BK + lchk * 8;
     const bool kin = t < nk && kk < ke;
 #pragma unroll
-    for (int i = 0; i < AI; ++i) {
-      const int64_t r = m0 + lrow + 32 * i;
-      ra[set][i] = (kin && r < M) ? ld8(A + r * p.lda + kk) : zero8();
-    }
+    for (int i = 0; i < AI; ++i)
+      ra[set][i] = bload8(rA, kin ? (uint32_t)(((lrow + 32 * i) * p.lda + kk) * 2) : kOOB);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int i = 0; i < BI; ++i) {
-        const int64_t c = n0 + lrow + 32 * i;
-        rb[set][b][i] = (kin && c < N) ? ld8(Bm[b] + c * p.ldb + kk) : zero8();
-      }
+      for (int i = 0; i < BI; ++i)
+        rb[set][b][i] = bload8(rB[b], kin ? (uint32_t)(((lrow + 32 * i) * p.ldb + kk) * 2) : kOOB);
   };
   const int wpos = (lchk ^ ((lrow >> 1) & 7)) * 8;  // same for rows lrow + 32 i
   auto swrite = [&](int buf, int set) {
@@ -557,7 +574,7 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
 // straight from global memory: lane (fr, g) reads the 16 bytes at k = 32 t +
 // 8 g of weight row n0 + fr and of activation rows 16 f + fr (the activations
 // are a few hundred KB and stay L2-resident).  The slice moves through two
-// register sets of 4 MFMA steps (GEGLU: 2), the loads of the next set issued
+// register sets of 3 MFMA steps (GEGLU: 2), the loads of the next set issued
 // before the MFMAs of the current one.  The waves' partial tiles and row sums of squares
 // meet in LDS and are added in wave order.
 //
@@ -572,7 +589,7 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
 // dirty in a non-coherent L2, which is what a release/acquire pair would
 // have to write back and invalidate (tens of microseconds per GEMM here).
 constexpr int kSkWaves = 8;
-constexpr int kSkStep = 4;    // MFMA steps (of 32 k) per register set (GEGLU: 2)
+constexpr int kSkStep = 3;    // MFMA steps (of 32 k) per register set (GEGLU: 2)
 constexpr int kSkMaxSplits = 4;
 
 __host__ __device__ constexpr int skinny_block_floats(int nb) {
@@ -612,7 +629,7 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
                                                           int64_t kc,
                                                           int vec_ok) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
-  constexpr int W = kSkWaves, S = kSkStep / NB;
+  constexpr int W = kSkWaves, S = NB == 2 ? 2 : kSkStep;
   __shared__ float sP[W][NB][64][16 + 1];
   __shared__ float sS[W][64];
   __shared__ int s_last;
@@ -653,17 +670,15 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
     b_ks = 64;
   }
   const bool bval = nval || p.b_frag;
-  const __amdgpu_buffer_rsrc_t ra_rs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)p.a, 0, 0x7fffffff, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rb_rs[2] = {
-      __builtin_amdgcn_make_buffer_rsrc((void*)p.b, 0, 0x7fffffff, 0x00020000),
-      __builtin_amdgcn_make_buffer_rsrc((void*)(NB == 2 ? p.b2 : p.b), 0, 0x7fffffff,
-                                        0x00020000)};
+  const __amdgpu_buffer_rsrc_t ra_rs = make_rsrc(p.a, 0x7fffffffu);
+  const __amdgpu_buffer_rsrc_t rb_rs[2] = {make_rsrc(p.b, 0x7fffffffu),
+                                           make_rsrc(NB == 2 ? p.b2 : p.b, 0x7fffffffu)};
   auto bld = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   };
 
   bf16x8 ra[2][S][4], rb[2][S][NB];
+  // unconditional loads: a masked-out fragment gets an offset past the view
   auto load = [&](int t0, int set) {
 #pragma unroll
     for (int t = 0; t < S; ++t) {
@@ -671,11 +686,11 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
       const bool kin = kb + 32 * (t0 + t) + 8 * g < ke;
 #pragma unroll
       for (int b = 0; b < NB; ++b)
-        rb[set][t][b] = (kin && bval) ? bld(rb_rs[b], b0 + ks * b_ks) : zero8();
+        rb[set][t][b] = bld(rb_rs[b], (kin && bval) ? b0 + ks * b_ks : kOOB);
 #pragma unroll
       for (int f = 0; f < 4; ++f) {
         const bool rin = p.a_frag || f * 16 + fr < M;
-        ra[set][t][f] = (kin && rin) ? bld(ra_rs, a0 + ks * a_ks + f * a_f) : zero8();
+        ra[set][t][f] = bld(ra_rs, (kin && rin) ? a0 + ks * a_ks + f * a_f : kOOB);
       }
     }
   };
@@ -697,6 +712,16 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
       }
   };
   if (nst > 0) load(0, 0);
+  // The epilogue's reads (residual, gate, bias, RoPE table, Euler state) do
+  // not depend on the product: issue them now so that their latency hides
+  // under the K loop.  Thread t < 128 owns row t / 2, columns n0 + 8 (t % 2).
+  const int row = (tid >> 1) & 63, half = tid & 1;
+  const int64_t ncol = n0 + 8 * half;
+  const int cnt = (int)(N - ncol < 8 ? N - ncol : 8);
+  const bool mine = tid < 128 && row < M && cnt > 0;
+  const bool vec = vec_ok && cnt == 8;
+  EpiIn in;
+  if (mine) epi_load<MODE>(p, row, ncol, vec, cnt, in);
   for (int t0 = 0; t0 < nst; t0 += 2 * S) {
     if (t0 + S < nst) load(t0 + S, 1);
     compute(0);
@@ -724,10 +749,6 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
   __syncthreads();
 
   // thread t < 128: row t / 2, columns n0 + 8 (t % 2) .. + 7
-  const int row = (tid >> 1) & 63, half = tid & 1;
-  const int64_t ncol = n0 + 8 * half;
-  const int cnt = (int)(N - ncol < 8 ? N - ncol : 8);
-  const bool mine = tid < 128 && row < M && cnt > 0;
   float v[8], u[8], rsum = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = u[e] = 0.f;
@@ -798,9 +819,6 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
     }
   }
   if (!mine) return;
-  const bool vec = vec_ok && cnt == 8;
-  EpiIn in;
-  epi_load<MODE>(p, row, ncol, vec, cnt, in);
   const float r = p.rownorm ? rsqrtf(rsum / (float)K + p.rownorm_eps) : 1.f;
   epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in);
 }
@@ -822,6 +840,9 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
   const float* ws = (const float*)((const char*)p.workspace + kCounterBytes);
   const int64_t M = p.m;
   const int64_t plane = (int64_t)splits * M * N;
+  // unconditional loads through a view of the partials (masked: past it)
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(ws, rec_bytes((NB * plane + (int64_t)splits * M) * 4));
   float v = 0.f, u = 0.f, ss = 0.f;
   for (int s0 = 0; s0 < splits; s0 += UN) {
     float t[NB][UN], q[UN];
@@ -831,8 +852,10 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
       const bool in = ok && s < splits;
 #pragma unroll
       for (int b = 0; b < NB; ++b)
-        t[b][i] = in ? ws[b * plane + ((int64_t)s * M + row) * N + n] : 0.f;
-      q[i] = (in && p.rownorm) ? ws[NB * plane + (int64_t)s * M + row] : 0.f;
+        t[b][i] = bload1f(rw, in ? (uint32_t)((b * plane + ((int64_t)s * M + row) * N + n) * 4)
+                                 : kOOB);
+      q[i] = bload1f(rw, (in && p.rownorm) ? (uint32_t)((NB * plane + (int64_t)s * M + row) * 4)
+                                           : kOOB);
     }
 #pragma unroll
     for (int i = 0; i < UN; ++i) {
@@ -1036,8 +1059,12 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
   const int m_tiles = (int)(cfg == 2 ? mt64 : mt128);
   const int n_tiles = (int)((d.n + bn - 1) / bn);
   const int tiles = m_tiles * n_tiles;
+  // Split K when the tiles cannot fill the CUs twice over and K is long:
+  // more workgroups per CU hide the memory latency of the K loop.
   int splits = d.split_k > 0 ? d.split_k : 1;
-  if (d.split_k <= 0 && tiles < 160 && d.k >= 4096) {
+  if (d.split_k <= 0 && d.k >= 8192 && tiles < 512) {
+    splits = 4;
+  } else if (d.split_k <= 0 && tiles < 160 && d.k >= 4096) {
     splits = (int)((256 + tiles - 1) / tiles);
     if (splits > 4) splits = 4;
   }

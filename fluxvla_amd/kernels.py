@@ -416,13 +416,15 @@ def run_attention(d):
 
 
 def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
-                  v_transposed=False):
+                  v_transposed=False, o_frag=None):
     """Batched multi-query attention.
 
     q: [B, Sq, H, D] (or [B, Sq, H*D]); k: [B, Sk, D] (row stride may exceed
     D, e.g. a cache slice); v: [B, Sk, D], or with ``v_transposed`` the value
     cache [B, D, T >= Sk] (keys contiguous); o like q.  kgrp: int32 [B, Sk],
-    qgrp: int32 [B, Sq] (visible iff kgrp[j] <= qgrp[i])."""
+    qgrp: int32 [B, Sq] (visible iff kgrp[j] <= qgrp[i]).  ``o_frag`` (a
+    FragA with k = H*D, decode path only) also receives the output in the
+    fragment-major layout, ready as the o-projection's A operand."""
     B, Sq = q.shape[0], q.shape[1]
     D = k.shape[-1]
     H = (q.shape[2] if q.dim() == 4 else q.shape[2] // D)
@@ -441,6 +443,11 @@ def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
         kgrp_zs=(kgrp.stride(0) if kgrp is not None else 0),
         qgrp_zs=(qgrp.stride(0) if qgrp is not None else 0), scale=scale,
         kv_splits=kv_splits)
+    if o_frag is not None:
+        if o_frag.k != H * D:
+            raise ValueError('o_frag must have k == heads * head_dim')
+        _check(o_frag.buf, 'o_frag')
+        d.o_frag = o_frag.buf.data_ptr()
     run_attention(d)
     return o
 

@@ -449,8 +449,8 @@ class PI0Inference:
                         rownorm_eps=cfg.rms_eps, row_group=Ss,
                         row_group_stride=T, v_ld=T)
         K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
-                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True)
-        K.pack_frag(b['ex_ctx'].view(Ss, -1), ctxf)
+                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True,
+                        o_frag=ctxf)
         K.gemm(ctxf, Lf['o_w'], out=x, residual=x, c_frag=xf)
         K.gemm_geglu(xf, Lf['gate_w'], Lf['up_w'], out=b['ex_h'],
                      rownorm_eps=cfg.rms_eps, c_frag=hf)

@@ -180,8 +180,8 @@ int fvx_adarms_norm(const void* x, const void* style, void* out,
  * kv_splits > 1 splits the key range across workgroups (needs workspace);
  * the split partials are merged by a second kernel on the same stream.
  * Decode-shaped problems (at most 512 query rows per problem) with a
- * transposed value cache run a barrier-free kernel in which every wave owns
- * 16 query rows and one key range.
+ * transposed value cache run a kernel in which a workgroup owns 64 query
+ * rows and a key range of 64-key tiles staged through LDS.
  */
 typedef struct fvx_attn_desc {
   const void* q; int64_t q_tok_stride, q_head_stride, q_zs1, q_zs2;
@@ -198,6 +198,11 @@ typedef struct fvx_attn_desc {
   float scale;
   int32_t kv_splits;
   void* workspace; int64_t workspace_bytes;
+  /* Decode path only (transposed V, head_dim 256, n_problems * sq <= 64):
+   * if non-NULL, the output is also written in the fragment-major A layout
+   * of fvx_gemm_desc.a_frag, row z * sq + token, column head * 256 + d --
+   * the A operand of the o-projection. */
+  void* o_frag;
 } fvx_attn_desc;
 
 int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d);

@@ -388,12 +388,13 @@ def test_attention_prefix_padded(K, cuda):
     assert rel_err(o[:, pad], ref[:, pad]) <= REL_TOL
 
 
-@pytest.mark.parametrize('splits', [0, 1, 5])
+@pytest.mark.parametrize('splits', [0, 1, 5, 14])
 @pytest.mark.parametrize('vt', [False, True])
 @pytest.mark.parametrize('batch', [1, 3])
 def test_attention_decode_block_causal(K, cuda, splits, vt, batch):
     """PI0 suffix: state token sees prefix + itself, actions see all.  With a
-    transposed value cache this runs the barrier-free decode kernel."""
+    transposed value cache this runs the LDS-tiled decode kernel (and, at
+    batch 1, also writes the fragment-major copy of the output)."""
     announce(f'attention decode block-causal splits={splits} vt={vt} '
              f'batch={batch}')
     P, Ssuf, H, D = 816, 51, 8, 256
@@ -414,12 +415,19 @@ def test_attention_decode_block_causal(K, cuda, splits, vt, batch):
         vc = cache_v.transpose(1, 2).contiguous().to(cuda)
     else:
         vc = cache_v.to(cuda)[:, :T]
+    of = K.FragA.empty(H * D, cuda).rows(Ssuf) if vt and batch == 1 else None
     K.mqa_attention(q.to(cuda), kc[:, :T], vc, o, kgrp.to(cuda),
-                    qgrp.to(cuda), kv_splits=splits, v_transposed=vt)
+                    qgrp.to(cuda), kv_splits=splits, v_transposed=vt,
+                    o_frag=of)
     mask = (kgrp[:, None, :] <= qgrp[:, :, None])
     ref = sdpa_ref(q.float().transpose(1, 2), cache_k[:, :T].float()[:, None],
                    cache_v[:, :T].float()[:, None], mask).transpose(1, 2)
     assert rel_err(o, ref) <= REL_TOL
+    if of is not None:
+        valid = K.pack_frag_a_ref(torch.ones(Ssuf, H * D,
+                                             dtype=torch.bfloat16)) != 0
+        assert torch.equal(of.buf.cpu()[valid],
+                           K.pack_frag_a_ref(o.view(Ssuf, H * D).cpu())[valid])
 
 
 def test_attention_siglip_packed(K, cuda):
