@@ -359,7 +359,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(fvx_attn_desc p,
 constexpr int kDecKT = 64;                    // keys per tile
 constexpr int kDecQP = 256 + 8;               // LDS pitch (elements), Q / K rows
 constexpr int kDecVP = kDecKT + 8;            // LDS pitch (elements), V^T rows
-constexpr int kDecOP = 256 + 4;               // LDS pitch (floats), O rows
+constexpr int kDecOT = 64 + 4;                // LDS pitch (floats), O by dim
 constexpr int64_t kDecPF = 64 * 256 + 2 * 64;  // partial floats per workgroup
 constexpr int kDecLDS = (64 * kDecQP + 256 * kDecVP) * 2;
 
@@ -517,13 +517,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    float al[4];
+    if (t0 != kbeg) {  // O is still zero on the first tile
+      float al[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) al[j] = __shfl(alpha, 4 * g + j, 64);
+      for (int j = 0; j < 4; ++j) al[j] = __shfl(alpha, 4 * g + j, 64);
 #pragma unroll
-    for (int df = 0; df < 16; ++df)
+      for (int df = 0; df < 16; ++df)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[df][j] *= al[j];
+        for (int j = 0; j < 4; ++j) o[df][j] *= al[j];
+    }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const bf16x8 pa = pack8(sv[s]);
@@ -533,12 +535,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     }
   }
 
-  // O rows (lane: rows 16 wave + 4 g + j, dim 16 df + fr) -> LDS row-major
+  // O (lane: rows 16 wave + 4 g + j, dim 16 df + fr) -> LDS, dim-major so
+  // that each lane writes its 4 rows as one 16-byte store
   __syncthreads();
 #pragma unroll
   for (int df = 0; df < 16; ++df)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sO[(wave * 16 + 4 * g + j) * kDecOP + 16 * df + fr] = o[df][j];
+    *(f32x4_t*)&sO[(16 * df + fr) * kDecOT + wave * 16 + 4 * g] = o[df];
   if (g == 0) {
     sM[wave * 16 + fr] = m_run;
     sL[wave * 16 + fr] = l_run;
@@ -549,12 +551,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
                            : nullptr;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const int c = tid + 256 * u, i = c >> 5, d0 = (c & 31) * 8;
-    const int64_t r = (int64_t)rg * 64 + i;
+    const int c = tid + 256 * u, i = c & 63, d0 = (c >> 6) * 8;
+    const int r = rg * 64 + i;
     if (r >= R) continue;
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = sO[i * kDecOP + d0 + e];
+    for (int e = 0; e < 8; ++e) v[e] = sO[(d0 + e) * kDecOT + i];
     if (part) {
       *(f32x4_t*)(part + i * 256 + d0) = f32x4_t{v[0], v[1], v[2], v[3]};
       *(f32x4_t*)(part + i * 256 + d0 + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
@@ -574,8 +576,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
 }
 
 // Merge of the decode partials: one thread per (problem, query row, 8 dims);
-// every split's loads are issued before the running-max merge, which is
-// applied in split order.
+// the loads of up to 16 splits are issued before the running-max merge,
+// which is applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
     fvx_attn_desc p, int n_rg, int splits) {
   const int64_t R = p.sq * p.heads;
@@ -590,11 +592,11 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
   float acc[8], M = -INFINITY, L = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += 8) {
-    f32x4_t a[8], b[8];
-    float mv[8], lv[8];
+  for (int s0 = 0; s0 < splits; s0 += 16) {
+    f32x4_t a[16], b[16];
+    float mv[16], lv[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 16; ++u) {
       // splits past the end read as zero (out of the buffer view)
       const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
       a[u] = bload4f(rw, off + (uint32_t)(i * 256 + d0) * 4);
@@ -603,7 +605,7 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
       lv[u] = bload1f(rw, off + (uint32_t)(64 * 256 + 64 + i) * 4);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 16; ++u) {
       if (s0 + u < splits) {
         const float mn = fmaxf(M, mv[u]);
         const float mr = (mn == -INFINITY) ? 0.f : mn;

@@ -19,12 +19,18 @@ __device__ __forceinline__ float bf2f(bf16_t v) {
   return __uint_as_float(((uint32_t)v) << 16);
 }
 
+// fp32 -> bf16 with round-to-nearest-even (NaN stays a quiet NaN): gfx950's
+// v_cvt_pk_bf16_f32, two values per instruction.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
 __device__ __forceinline__ bf16_t f2bf(float f) {
-  // Round to nearest even; NaN stays NaN (quiet bit forced).
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+  return __builtin_bit_cast(bf16_t, (__bf16)f);
 }
 
 // 8 packed bf16 values (one 16-byte vector).
@@ -43,8 +49,7 @@ __device__ __forceinline__ void unpack8(const bf16x8& v, float* f) {
 __device__ __forceinline__ bf16x8 pack8(const float* f) {
   bf16x8 v;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    v.w[i] = (uint32_t)f2bf(f[2 * i]) | ((uint32_t)f2bf(f[2 * i + 1]) << 16);
+  for (int i = 0; i < 4; ++i) v.w[i] = f2bf2(f[2 * i], f[2 * i + 1]);
   return v;
 }
 

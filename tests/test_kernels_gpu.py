@@ -224,6 +224,20 @@ def test_gemm_fragment_major_operands(K, cuda, m, n, k):
         assert torch.equal(g0, g1)
 
 
+@pytest.mark.parametrize('m', [40, 96])
+def test_bf16_rounding_matches_torch(K, cuda, m):
+    """The kernels' fp32 -> bf16 conversion rounds to nearest even, as
+    torch's cast does: the bf16 output of a GEMM equals torch's cast of the
+    same GEMM's fp32 output bit for bit (outputs span ~12 binades)."""
+    announce(f'bf16 rounding m={m}')
+    a = randn((m, 256), 36, std=4.0).to(cuda)
+    scale = torch.logspace(-6, 6, 512, base=2.0).bfloat16()[:, None]
+    w = (randn((512, 256), 37) * scale).bfloat16().to(cuda)
+    o32 = K.gemm(a, w, out_f32=True)
+    o16 = K.gemm(a, w)
+    assert torch.equal(o16.cpu(), o32.cpu().bfloat16())
+
+
 def test_gemm_pos_rowgroup_f32(K, cuda):
     announce('gemm pos/row_group/out_f32')
     m, n, k = 768, 1152, 640
