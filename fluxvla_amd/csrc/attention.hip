@@ -368,62 +368,81 @@ __device__ __forceinline__ int dec_krow(int jl) {
   return (jl & ~31) + ((jl >> 2) & 1) * 16 + ((jl >> 3) & 3) * 4 + (jl & 3);
 }
 
-// One output chunk: 8 dims of query row r (token r / heads) of problem z.
-__device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int64_t z,
-                                          int64_t r, int d0, const float* v) {
-  const int64_t tok = r / p.heads, h = r % p.heads;
+// Query row r of a problem is (token r / heads, head r % heads); `hs` is
+// log2(heads) when heads is a power of two (shifts instead of divisions).
+__device__ __forceinline__ int row_tok(int r, int heads, int hs) {
+  return hs >= 0 ? r >> hs : r / heads;
+}
+
+// One output chunk: `n` (4 or 8) dims d0.. of query row r of problem z,
+// row-major and, if requested, fragment-major for the o-projection.
+template <int NE>
+__device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int z, int r,
+                                          int d0, int hs, const float* v) {
+  const int heads = (int)p.heads;
+  const int tok = row_tok(r, heads, hs), h = r - tok * heads;
   const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
   bf16_t* O = (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2;
-  const bf16x8 b = pack8(v);
-  st8(O + tok * p.o_tok_stride + h * p.o_head_stride + d0, b);
-  if (p.o_frag)
-    st8((bf16_t*)p.o_frag + frag_offset(z * p.sq + tok, h * 256 + d0), b);
+  bf16_t* dst = O + (int64_t)tok * p.o_tok_stride + (int64_t)h * p.o_head_stride + d0;
+  bf16_t* fdst = p.o_frag ? (bf16_t*)p.o_frag + frag_offset((int64_t)z * p.sq + tok,
+                                                            h * 256 + d0)
+                          : nullptr;
+  if (NE == 8) {
+    const bf16x8 b = pack8(v);
+    st8(dst, b);
+    if (fdst) st8(fdst, b);
+  } else {
+    const uint2 b = {f2bf2(v[0], v[1]), f2bf2(v[2], v[3])};
+    *(uint2*)dst = b;
+    if (fdst) *(uint2*)fdst = b;
+  }
 }
 
 __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
                                                           int n_rg, int splits,
-                                                          int64_t kps) {
+                                                          int kps, int hs) {
   constexpr int HD = 256;
   __shared__ __align__(16) unsigned char smem[kDecLDS];
-  __shared__ int32_t sG[kDecKT];
+  __shared__ __align__(16) int32_t sG[kDecKT];
   __shared__ float sM[64], sL[64];
   bf16_t* sQK = (bf16_t*)smem;                      // Q, then K tiles
   bf16_t* sV = (bf16_t*)smem + 64 * kDecQP;         // V^T tiles
-  float* sO = (float*)smem;                         // O rows at the end
+  float* sO = (float*)smem;                         // O by dim at the end
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
   const int rg = blockIdx.x % n_rg;
   const int split = (blockIdx.x / n_rg) % splits;
-  const int64_t z = blockIdx.x / (n_rg * splits);
-  const int64_t heads = p.heads, R = p.sq * heads;
+  const int z = blockIdx.x / (n_rg * splits);
+  const int heads = (int)p.heads, R = (int)p.sq * heads;
   const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
   const bf16_t* K = (const bf16_t*)p.k + zb * p.k_zs1 + zh * p.k_zs2;
   const bf16_t* Vt = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
   const int32_t* kgrp = p.kgrp ? p.kgrp + zb * p.kgrp_zs1 : nullptr;
   const int32_t* qgrp = p.qgrp ? p.qgrp + zb * p.qgrp_zs1 : nullptr;
-  const int64_t kbeg = (int64_t)split * kps;
-  const int64_t kend = (kbeg + kps < p.sk) ? kbeg + kps : p.sk;
+  const int kbeg = split * kps;
+  const int kend = kbeg + kps < (int)p.sk ? kbeg + kps : (int)p.sk;
+  const int qts = (int)p.q_tok_stride, qhs = (int)p.q_head_stride;
+  const int kts = (int)p.k_tok_stride, vds = (int)p.v_d_stride;
 
   // Buffer views: rows past the range read as zero (K: keys >= kend; V^T:
   // the last row's tail; Q: rows >= R get an out-of-range offset).
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(
-      Q, (uint32_t)(((p.sq - 1) * p.q_tok_stride + (heads - 1) * p.q_head_stride + HD) * 2));
-  const __amdgpu_buffer_rsrc_t rkc = make_rsrc(K, (uint32_t)(kend * p.k_tok_stride * 2));
-  const __amdgpu_buffer_rsrc_t rvc = make_rsrc(Vt, (uint32_t)(HD * p.v_d_stride * 2));
+  const __amdgpu_buffer_rsrc_t rq =
+      make_rsrc(Q, (uint32_t)(((int)p.sq - 1) * qts + (heads - 1) * qhs + HD) * 2);
+  const __amdgpu_buffer_rsrc_t rkc = make_rsrc(K, (uint32_t)kend * kts * 2);
+  const __amdgpu_buffer_rsrc_t rvc = make_rsrc(Vt, (uint32_t)HD * vds * 2);
   const __amdgpu_buffer_rsrc_t rgc =
-      make_rsrc(kgrp ? (const void*)kgrp : (const void*)Q, kgrp ? (uint32_t)(kend * 4) : 0u);
+      make_rsrc(kgrp ? (const void*)kgrp : (const void*)Q, kgrp ? (uint32_t)kend * 4 : 0u);
 
   // Q rows of this group (32 16-byte chunks per row) and the first K/V tile
   // are requested together; Q goes through LDS into VGPRs.
   bf16x8 rqv[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const int c = tid + 256 * u, i = c >> 5, ck = c & 31;
-    const int r = rg * 64 + i;
-    rqv[u] = bload8(rq, r < R ? (uint32_t)(((r / (int)heads) * p.q_tok_stride +
-                                            (r % (int)heads) * p.q_head_stride + ck * 8) * 2)
+    const int c = tid + 256 * u, r = rg * 64 + (c >> 5);
+    const int tok = row_tok(r, heads, hs);
+    rqv[u] = bload8(rq, r < R ? (uint32_t)(tok * qts + (r - tok * heads) * qhs + (c & 31) * 8) * 2
                               : kOOB);
   }
 
@@ -431,22 +450,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   // V keys past kend are zeroed when the tile is written to LDS.
   bf16x8 rk[8], rv[8];
   int32_t rgp = 0;
-  auto prefetch = [&](int64_t t0) {
+  auto prefetch = [&](int t0) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int c = tid + 256 * u;
-      const int64_t j = t0 + (c >> 5);  // K: 32 chunks per key row
-      rk[u] = bload8(rkc, (uint32_t)((j * p.k_tok_stride + (c & 31) * 8) * 2));
-      const int64_t j8 = t0 + (c & 7) * 8;  // V^T: 8 chunks per dim row
-      rv[u] = bload8(rvc, (uint32_t)(((int64_t)(c >> 3) * p.v_d_stride + j8) * 2));
+      rk[u] = bload8(rkc, (uint32_t)((t0 + (c >> 5)) * kts + (c & 31) * 8) * 2);
+      rv[u] = bload8(rvc, (uint32_t)((c >> 3) * vds + t0 + (c & 7) * 8) * 2);
     }
     if (kgrp && tid < kDecKT)
-      rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)((t0 + tid) * 4), 0, 0);
+      rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)(t0 + tid) * 4, 0, 0);
   };
 
   if (kbeg < kend) prefetch(kbeg);
-  const int64_t qrow = (int64_t)rg * 64 + wave * 16 + fr;
-  const int32_t qg = (qgrp && qrow < R) ? qgrp[qrow / heads] : 0;
+  const int qrow = rg * 64 + wave * 16 + fr;
+  const int32_t qg = (qgrp && qrow < R) ? qgrp[row_tok(qrow, heads, hs)] : 0;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int c = tid + 256 * u;
@@ -462,14 +479,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   f32x4_t o[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int64_t t0 = kbeg; t0 < kend; t0 += kDecKT) {
+  for (int t0 = kbeg; t0 < kend; t0 += kDecKT) {
     __syncthreads();  // previous tile (or the Q copy) fully read
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int c = tid + 256 * u;
       st8(&sQK[dec_krow(c >> 5) * kDecQP + (c & 31) * 8], rk[u]);
-      st8(&sV[(c >> 3) * kDecVP + (c & 7) * 8],
-          mask_keys(rv[u], kend - (t0 + (c & 7) * 8)));
+      st8(&sV[(c >> 3) * kDecVP + (c & 7) * 8], mask_keys(rv[u], kend - (t0 + (c & 7) * 8)));
     }
     if (kgrp && tid < kDecKT) sG[tid] = rgp;
     __syncthreads();
@@ -491,15 +507,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
       }
     float tmax = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < 2; ++s) {
+      int32_t gk[8];
+      if (kgrp) {
+        const int4 a = *(const int4*)&sG[32 * s + 8 * g];
+        const int4 b = *(const int4*)&sG[32 * s + 8 * g + 4];
+        gk[0] = a.x; gk[1] = a.y; gk[2] = a.z; gk[3] = a.w;
+        gk[4] = b.x; gk[5] = b.y; gk[6] = b.z; gk[7] = b.w;
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int jl = 32 * s + 8 * g + e;
-        bool vis = t0 + jl < kend;
-        if (vis && kgrp) vis = sG[jl] <= qg;
+        bool vis = t0 + 32 * s + 8 * g + e < kend;
+        if (kgrp) vis = vis && gk[e] <= qg;
         sv[s][e] = vis ? sv[s][e] * sc : -INFINITY;
         tmax = fmaxf(tmax, sv[s][e]);
       }
+    }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
@@ -565,42 +588,38 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
       const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] *= inv;
-      dec_store(p, z, r, d0, v);
+      dec_store<8>(p, z, r, d0, hs, v);
     }
   }
   if (part && tid < 64) {
     part[64 * 256 + tid] = sM[tid];
     part[64 * 256 + 64 + tid] = sL[tid];
   }
-  (void)HD;
 }
 
-// Merge of the decode partials: one thread per (problem, query row, 8 dims);
+// Merge of the decode partials: one thread per (problem, query row, 4 dims);
 // the loads of up to 16 splits are issued before the running-max merge,
 // which is applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
-    fvx_attn_desc p, int n_rg, int splits) {
-  const int64_t R = p.sq * p.heads;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)p.n_problems * R * 32) return;
-  const int d0 = (int)(gid & 31) * 8;
-  const int64_t zr = gid >> 5;
-  const int64_t z = zr / R, r = zr % R;
-  const int64_t rg = r / 64, i = r % 64;
-  const float* base = (const float*)p.workspace + ((z * n_rg + rg) * splits) * kDecPF;
+    fvx_attn_desc p, int n_rg, int splits, int hs) {
+  const int R = (int)(p.sq * p.heads);
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (int)p.n_problems * R * 64) return;
+  const int d0 = (gid & 63) * 4;
+  const int zr = gid >> 6;
+  const int z = zr / R, r = zr % R;
+  const int rg = r >> 6, i = r & 63;
+  const float* base = (const float*)p.workspace + (((int64_t)z * n_rg + rg) * splits) * kDecPF;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
-  float acc[8], M = -INFINITY, L = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f}, M = -INFINITY, L = 0.f;
   for (int s0 = 0; s0 < splits; s0 += 16) {
-    f32x4_t a[16], b[16];
+    f32x4_t a[16];
     float mv[16], lv[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       // splits past the end read as zero (out of the buffer view)
       const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
       a[u] = bload4f(rw, off + (uint32_t)(i * 256 + d0) * 4);
-      b[u] = bload4f(rw, off + (uint32_t)(i * 256 + d0 + 4) * 4);
       mv[u] = bload1f(rw, off + (uint32_t)(64 * 256 + i) * 4);
       lv[u] = bload1f(rw, off + (uint32_t)(64 * 256 + 64 + i) * 4);
     }
@@ -611,10 +630,7 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
         const float mr = (mn == -INFINITY) ? 0.f : mn;
         const float wa = exp2f(M - mr), wb = exp2f(mv[u] - mr);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[e] = acc[e] * wa + a[u][e] * wb;
-          acc[4 + e] = acc[4 + e] * wa + b[u][e] * wb;
-        }
+        for (int e = 0; e < 4; ++e) acc[e] = acc[e] * wa + a[u][e] * wb;
         L = L * wa + lv[u] * wb;
         M = mn;
       }
@@ -622,8 +638,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] *= inv;
-  dec_store(p, z, r, d0, acc);
+  for (int e = 0; e < 4; ++e) acc[e] *= inv;
+  dec_store<4>(p, z, r, d0, hs, acc);
 }
 
 struct AttnPlan {
@@ -668,11 +684,16 @@ struct DecodePlan {
 };
 
 static bool use_decode(const fvx_attn_desc& d) {
-  return d.v_d_stride > 0 && d.head_dim == 256 && d.sq * d.heads <= 512;
+  // (its operand offsets are 32-bit)
+  const int64_t lim = (int64_t)1 << 30;
+  return d.v_d_stride > 0 && d.head_dim == 256 && d.sq * d.heads <= 512 &&
+         d.sq * d.q_tok_stride + d.heads * d.q_head_stride < lim &&
+         d.sk * d.k_tok_stride < lim && 256 * d.v_d_stride < lim;
 }
 
 // 64-row groups x key ranges of whole 64-key tiles; by default about 128
-// workgroups.
+// workgroups (one tile each for the action expert: measured faster than two
+// tiles per workgroup with half the partials to merge).
 static DecodePlan plan_decode(const fvx_attn_desc& d) {
   DecodePlan a;
   a.n_rb = (int)((d.sq * d.heads + 63) / 64);
@@ -745,14 +766,15 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
                        (long long)d.workspace_bytes);
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "attention: workspace must be 16B aligned");
+    const int hs = (d.heads & (d.heads - 1)) == 0 ? __builtin_ctzll((uint64_t)d.heads) : -1;
     hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)a.n_items), dim3(256),
-                       0, s, d, a.n_rb, a.splits, a.kps);
+                       0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
     int st = launch_status("attention(decode)");
     if (st || a.splits == 1) return st;
-    const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 32;
+    const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 64;
     hipLaunchKernelGGL(attn_decode_merge_kernel,
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                       d, a.n_rb, a.splits);
+                       d, a.n_rb, a.splits, hs);
     return launch_status("attention(decode merge)");
   }
   AttnPlan a = plan_attn(d);
