@@ -116,12 +116,15 @@ __device__ __forceinline__ void epilogue4(const GemmArgs& p, int64_t row0,
   }
 }
 
+// sum of squares of 8 bf16 values: four v_dot2c_f32_bf16 (fp32 accumulate)
 __device__ __forceinline__ float sumsq8(const bf16x8& v) {
-  float f[8];
-  unpack8(v, f);
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
   float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s += f[e] * f[e];
+  for (int i = 0; i < 4; ++i) {
+    const bf16x2v h = __builtin_bit_cast(bf16x2v, v.w[i]);
+    s = __builtin_amdgcn_fdot2_f32_bf16(h, h, s, false);
+  }
   return s;
 }
 
@@ -424,17 +427,23 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
   const __amdgpu_buffer_rsrc_t rB[2] = {
       make_rsrc(Bm[0] + n0 * p.ldb, (uint32_t)(b_rows * p.ldb * 2)),
       make_rsrc((NB == 2 ? Bm[1] : Bm[0]) + n0 * p.ldb, (uint32_t)(b_rows * p.ldb * 2))};
+  // per-thread byte offsets of slab 0 (rows lrow + 32 i, chunk lchk); slab t
+  // adds 2 t BK bytes
+  const uint32_t lda2 = (uint32_t)p.lda * 2, ldb2 = (uint32_t)p.ldb * 2;
+  const uint32_t offA0 = (uint32_t)lrow * lda2 + (uint32_t)(kb + lchk * 8) * 2;
+  const uint32_t offB0 = (uint32_t)lrow * ldb2 + (uint32_t)(kb + lchk * 8) * 2;
+  const int kin_end = (int)(ke - kb - lchk * 8);  // slab t is in range iff t BK < kin_end
   auto gload = [&](int t, int set) {
-    const int64_t kk = kb + (int64_t)t * BK + lchk * 8;
-    const bool kin = t < nk && kk < ke;
+    const bool kin = t < nk && t * BK < kin_end;
+    const uint32_t dk = (uint32_t)t * (BK * 2);
 #pragma unroll
     for (int i = 0; i < AI; ++i)
-      ra[set][i] = bload8(rA, kin ? (uint32_t)(((lrow + 32 * i) * p.lda + kk) * 2) : kOOB);
+      ra[set][i] = bload8(rA, kin ? offA0 + dk + (uint32_t)(32 * i) * lda2 : kOOB);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int i = 0; i < BI; ++i)
-        rb[set][b][i] = bload8(rB[b], kin ? (uint32_t)(((lrow + 32 * i) * p.ldb + kk) * 2) : kOOB);
+        rb[set][b][i] = bload8(rB[b], kin ? offB0 + dk + (uint32_t)(32 * i) * ldb2 : kOOB);
   };
   const int wpos = (lchk ^ ((lrow >> 1) & 7)) * 8;  // same for rows lrow + 32 i
   auto swrite = [&](int buf, int set) {
@@ -442,7 +451,7 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
       st8(&sa[(lrow + 32 * i) * LD + wpos], ra[set][i]);
-      if (p.rownorm) ss[i] += sumsq8(ra[set][i]);
+      ss[i] += sumsq8(ra[set][i]);  // unconditional: no branch in the loop
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -486,25 +495,24 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
     }
   };
 
-  // slab t: loaded into register set t&1, written to LDS stage t&1.
+  // slab t: loaded into register set t&1, written to LDS stage t&1.  The
+  // loop body has no branches: slabs past nk load as zeros (out-of-view
+  // offsets) and add nothing, so every half-step issues the same loads and
+  // the compiler's wait counts stay exact (any conditional load makes it
+  // wait for every load in flight, which undoes the prefetch).
   gload(0, 0);
   gload(1, 1);
-  if (nk > 0) swrite(0, 0);
+  swrite(0, 0);
   gload(2, 0);
   __syncthreads();
   for (int t = 0; t < nk; t += 2) {
     compute(0);                          // slab t
-    if (t + 1 < nk) {
-      swrite(1, 1);                      // slab t+1
-      gload(t + 3, 1);
-    }
+    swrite(1, 1);                        // slab t+1
+    gload(t + 3, 1);
     __syncthreads();
-    if (t + 1 >= nk) break;
     compute(1);                          // slab t+1
-    if (t + 2 < nk) {
-      swrite(0, 0);                      // slab t+2
-      gload(t + 4, 0);
-    }
+    swrite(0, 0);                        // slab t+2
+    gload(t + 4, 0);
     __syncthreads();
   }
 
