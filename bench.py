@@ -11,6 +11,11 @@ plus one HIP graph replay.
 Also reported on the same JSON line:
   roofline      the dominant kernel (prefix GeGLU GEMM, MFMA-bound) timed live
                 with HIP events on the stream it runs on;
+  kernels       the same for every main kernel of the chunk (and the C1
+                RMSNorm+residual op), HBM-bound ones over distinct operand
+                sets so that they do not run from the memory-side cache;
+  phases        C2 (one expert layer, bs=1) and C3 (prefix prefill, bs=1)
+                as HIP graphs of the chunk's kernels;
   cpu_baseline  the CPU oracle (fp32 restatement of the reference's eager
                 PyTorch path) timed on this host for one chunk;
   parity        max abs error of the GPU chunk vs that CPU chunk.
@@ -87,6 +92,196 @@ def time_dominant_kernel(model, iters=20):
     }
 
 
+def _graph_time_us(fn, reps=20):
+    """Average us per replay of a HIP graph holding one call of ``fn``."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        fn()
+        torch.cuda.synchronize()
+        g.capture_begin()
+        fn()
+        g.capture_end()
+    torch.cuda.current_stream().wait_stream(st)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
+        enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / reps
+
+
+def _launch_time_us(calls, reps, min_calls=16):
+    """Average us per call: ``calls`` (distinct operand sets, so HBM-bound
+    kernels are not served from the 256 MB memory-side cache; repeated to
+    at least ``min_calls``) captured back to back in one HIP graph and
+    replayed ``reps`` times between HIP events.  The graph keeps host launch
+    overhead out of the figure; the ~1.6 us a kernel boundary costs inside a
+    graph stays in it."""
+    seq = list(calls) * max(1, -(-min_calls // len(calls)))
+
+    def run():
+        for c in seq:
+            c()
+    return _graph_time_us(run, reps) / len(seq)
+
+
+def _row(name, shape, bound, work, us):
+    if bound == 'hbm':
+        achieved = work / (us * 1e-6) / 1e9
+        peak, unit = PEAK_HBM_GBS, 'GB/s'
+    else:
+        achieved = work / (us * 1e-6) / 1e12
+        peak, unit = PEAK_BF16_TFLOPS, 'TFLOP/s'
+    return {'kernel': name, 'shape': shape, 'bound': bound,
+            'avg_us': round(us, 2), 'achieved': round(achieved, 1),
+            'peak': peak, 'unit': unit, 'frac': round(achieved / peak, 4),
+            'work': work}
+
+
+def kernel_table(model):
+    """Per-kernel rooflines at the chunk's shapes (algorithmic bytes or
+    flops per launch / average launch time).  M = 51 GEMMs, norms and the
+    decode attention are judged against HBM, M >= 768 GEMMs and prefill
+    attention against bf16 MFMA.  HBM-bound kernels cycle through distinct
+    operand sets (C1: 32 sets, 537 MB; expert: the 18 layers' weights,
+    623 MB) so that the figures are HBM, not memory-side-cache, figures."""
+    import torch
+
+    from fluxvla_amd import kernels as K
+    cfg, dev = model.cfg, model.device
+    rows = []
+    # C1: fused RMSNorm + residual, [1024, 2048]
+    g = torch.Generator(device=dev).manual_seed(0)
+    sets = []
+    for _ in range(32):
+        x = torch.randn(1024, 2048, device=dev, generator=g).bfloat16()
+        r = torch.randn(1024, 2048, device=dev, generator=g).bfloat16()
+        sets.append((x, r, torch.empty_like(x), torch.empty_like(x)))
+    w = (torch.randn(2048, device=dev, generator=g) * 0.02 + 1).bfloat16()
+    calls = [lambda s=s: K.rms_norm_residual(s[0], s[1], w, 1e-6, out=s[2],
+                                             residual_out=s[3])
+             for s in sets]
+    nbytes = 4 * 1024 * 2048 * 2 + 2048 * 2
+    rows.append(_row('rms_norm_residual_kernel (C1)', '[1024, 2048]', 'hbm',
+                     nbytes, _launch_time_us(calls, 10)))
+    rows.append(_row('rms_norm_residual_kernel (C1, cache-resident)',
+                     '[1024, 2048]', 'hbm', nbytes,
+                     _launch_time_us(calls[:1], 20, min_calls=32)))
+    del sets, calls
+
+    # action expert at bs=1, fragment-major operands as in the chunk
+    b = model._bufs[1]
+    S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
+    T = model.kv_len
+    x = b['ex_x'].view(Ss, hid)
+    xf, ctxf, hf = (b['ex_xf'].rows(Ss), b['ex_ctxf'].rows(Ss),
+                    b['ex_hf'].rows(Ss))
+    H, mlp = cfg.heads, cfg.exp_mlp
+    qkv, oc, ggl, dn, att = [], [], [], [], []
+    for i, Lf in enumerate(model.exp_f):
+        kc, vc = b['kc'][i], b['vc'][i]
+        qkv.append(lambda Lf=Lf, kc=kc, vc=vc: K.gemm_qkv_rope(
+            xf, Lf['qkv_w'], model.rope, b['pos_suf'], b['ex_q'].view(Ss, -1),
+            kc.view(T, D)[S:], vc[:, :, S:], H, D, rownorm_eps=cfg.rms_eps,
+            row_group=Ss, row_group_stride=T, v_ld=T))
+        att.append(lambda kc=kc, vc=vc: K.mqa_attention(
+            b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'], kgrp=b['kgrp'],
+            qgrp=b['qgrp_suf'], v_transposed=True, o_frag=ctxf))
+        oc.append(lambda Lf=Lf: K.gemm(ctxf, Lf['o_w'], out=x, residual=x,
+                                       c_frag=xf))
+        ggl.append(lambda Lf=Lf: K.gemm_geglu(xf, Lf['gate_w'], Lf['up_w'],
+                                              out=b['ex_h'],
+                                              rownorm_eps=cfg.rms_eps,
+                                              c_frag=hf))
+        dn.append(lambda Lf=Lf: K.gemm(hf, Lf['down_w'], out=x, residual=x,
+                                       c_frag=xf))
+    nq = (H + 2) * D
+    for name, calls, N, Kd, nb, extra in (
+            ('gemm_skinny_kernel<QKV_ROPE> (expert)', qkv, nq, hid, 1, 0),
+            ('gemm_skinny_kernel<PLAIN> o-proj (expert)', oc, hid, H * D, 1,
+             Ss * hid * 2),
+            ('gemm_skinny_kernel<GEGLU> (expert)', ggl, mlp, hid, 2, 0),
+            ('gemm_skinny_kernel<PLAIN> down (expert)', dn, hid, mlp, 1,
+             Ss * hid * 2)):
+        work = nb * N * Kd * 2 + Ss * Kd * 2 + Ss * N * 2 + extra
+        rows.append(_row(name, f'M={Ss} N={N}{"x2" if nb == 2 else ""} K={Kd}',
+                         'hbm', work, _launch_time_us(calls, 5)))
+    T_keys = S + Ss
+    work = T_keys * D * 2 * 2 + 2 * Ss * H * D * 2
+    rows.append(_row('attn_decode_kernel + merge (expert)',
+                     f'{Ss * H} query rows x {T_keys} keys', 'hbm', work,
+                     _launch_time_us(att, 5)))
+
+    # prefix (M = 816) and SigLIP (M = 768) GEMMs, prefill attention: MFMA
+    L = model.llm['layers'][0]
+    px = b['pre_x'].view(-1, cfg.llm_hidden)
+    M = px.shape[0]
+    kc0, vc0 = b['kc'][0], b['vc'][0]
+    pre = [
+        ('gemm_tile_kernel<QKV_ROPE> (prefix)', lambda: K.gemm_qkv_rope(
+            px, L['qkv_w'], model.rope, b['pos_pre'], b['pre_q'].view(M, -1),
+            kc0.view(T, D), vc0, H, D, rownorm_eps=cfg.rms_eps, row_group=S,
+            row_group_stride=T, v_ld=T), 2 * M * nq * cfg.llm_hidden),
+        ('gemm_tile_kernel<PLAIN> o-proj (prefix)', lambda: K.gemm(
+            b['pre_ctx'].view(M, -1), L['o_w'], out=b['pre_h'][:, :cfg.llm_hidden],
+            residual=px), 2 * M * cfg.llm_hidden * H * D),
+        ('gemm_tile_kernel<GEGLU> (prefix)', lambda: K.gemm_geglu(
+            px, L['gate_w'], L['up_w'], out=b['pre_h'], rownorm_eps=cfg.rms_eps),
+         4 * M * cfg.llm_mlp * cfg.llm_hidden),
+        ('gemm_tile_kernel<PLAIN> down, split-K 4 (prefix)', lambda: K.gemm(
+            b['pre_h'], L['down_w'], out=b['pre_q'].view(M, -1)[:, :cfg.llm_hidden],
+            residual=px), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
+        ('attn_kernel<256,256> + merge (prefix)', lambda: K.mqa_attention(
+            b['pre_q'], kc0[:, :S], vc0, b['pre_ctx'], kgrp=b['kgrp'][:, :S],
+            qgrp=b['qgrp_pre'], v_transposed=True), 4 * H * S * S * D),
+    ]
+    V = model.vis['layers'][0]
+    vx, vxn = b['vis_x'], b['vis_xn']
+    Mv, vh = vx.shape
+    nimg = Mv // cfg.num_patches
+    pre += [
+        ('gemm_tile_kernel<PLAIN> qkv+bias (SigLIP)', lambda: K.gemm(
+            vxn, V['qkv_w'], out=b['vis_qkv'], bias=V['qkv_b']),
+         2 * Mv * 3 * vh * vh),
+        ('gemm_tile_kernel<PLAIN> o-proj+bias+res, split-K 3 (SigLIP)',
+         lambda: K.gemm(b['vis_ctx'], V['o_w'], out=vxn, bias=V['o_b'],
+                        residual=vx), 2 * Mv * vh * vh),
+        ('gemm_tile_kernel<PLAIN> fc1+bias+gelu (SigLIP)', lambda: K.gemm(
+            vxn, V['fc1_w'], out=b['vis_h'], bias=V['fc1_b'], act=2),
+         2 * Mv * cfg.vit_mlp * vh),
+        ('gemm_tile_kernel<PLAIN> fc2+bias+res (SigLIP)', lambda: K.gemm(
+            b['vis_h'], V['fc2_w'], out=vxn, bias=V['fc2_b'], residual=vx),
+         2 * Mv * vh * cfg.vit_mlp),
+        ('attn_kernel<96,80> (SigLIP)', lambda: K.mha_packed_qkv(
+            b['vis_qkv'], b['vis_ctx'], nimg, cfg.num_patches, cfg.vit_heads,
+            cfg.vit_head_dim),
+         4 * nimg * cfg.vit_heads * cfg.num_patches ** 2 * cfg.vit_head_dim),
+    ]
+    for name, fn, flops in pre:
+        rows.append(_row(name, '', 'mfma', flops, _launch_time_us([fn], 10)))
+    return rows
+
+
+def phase_times(model):
+    """C2 (one expert layer, one flow step, bs=1) and C3 (prefix prefill,
+    bs=1) as HIP graphs of the chunk's own kernels."""
+    b = model._bufs[1]
+    c3 = _graph_time_us(lambda: (model.vision_encoder(b, 1),
+                                 model.transformer_encoder(b, 1)), reps=10)
+    L = model.exp['layers'][0]
+    c2 = _graph_time_us(lambda: model._expert_layer_pi0(b, 1, 0, L), reps=50)
+    return {'C2_expert_layer_bs1_us': round(c2, 2),
+            'C3_prefix_prefill_bs1_ms': round(c3 / 1000.0, 3)}
+
+
 def kernel_only(iters=10):
     """The dominant kernel alone at its chunk shape (random operands), then
     a plain 256 MiB device copy: the short program the rocprofv3 --pmc
@@ -151,6 +346,9 @@ def main():
     ap.add_argument('--batch', type=int, default=1)
     ap.add_argument('--no-cpu', action='store_true',
                     help='skip the CPU oracle baseline')
+    ap.add_argument('--no-table', action='store_true',
+                    help='skip the per-kernel roofline table and the C2/C3 '
+                    'phase times')
     ap.add_argument('--kernel-only', action='store_true',
                     help='run only the dominant kernel + a calibration copy '
                     '(for rocprofv3 --pmc passes)')
@@ -210,6 +408,16 @@ def main():
     if roof:
         log(f"dominant kernel {roof['avg_us']} us, {roof['achieved']} TFLOP/s")
 
+    table, phases = None, None
+    if B == 1 and not args.no_table:
+        log('per-kernel rooflines and C2/C3 phase times')
+        table = kernel_table(model)
+        phases = phase_times(model)
+        for r in table:
+            log(f"  {r['kernel']:56s} {r['avg_us']:9.2f} us "
+                f"{r['achieved']:8.1f} {r['unit']} ({100 * r['frac']:.1f} %)")
+        log(f'  {phases}')
+
     cpu, err = (None, None)
     if not args.no_cpu and B == 1:
         log('timing the CPU oracle (one chunk)')
@@ -243,6 +451,8 @@ def main():
             'median_event_ms': round(per[len(per) // 2], 3),
         },
         'roofline': roof,
+        'kernels': table,
+        'phases': phases,
         'cpu_baseline': cpu,
         'parity': None if err is None else {
             'chunk_max_abs_err_vs_cpu_oracle': err, 'tolerance': 2e-2},

@@ -13,6 +13,14 @@ namespace fvx {
 constexpr int kRowsPerBlock = 4;
 constexpr int kMaxVec = 8;  // up to 64 lanes * 8 vectors * 8 = 4096 columns
 
+// All of a row's loads (and the per-column weights) are issued before any
+// is used, through buffer views: a vector past the row end or of an absent
+// operand reads zero without a branch (a load behind a branch makes the
+// compiler wait for it at the join, serializing the loads).
+__device__ __forceinline__ uint32_t vec_off(int v, int nvec, int64_t base) {
+  return v < nvec ? (uint32_t)((base + (int64_t)v * 8) * 2) : kOOB;
+}
+
 template <int NV>
 __global__ __launch_bounds__(256) void rms_norm_residual_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ res,
@@ -22,22 +30,29 @@ __global__ __launch_bounds__(256) void rms_norm_residual_kernel(
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nvec = cols >> 3;
-  const bf16_t* xr = x + row * cols;
+  const uint32_t rb = (uint32_t)cols * 2;  // views of this row only
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * cols, rb);
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(res ? res + row * cols : x, res ? rb : 0u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w ? w : x, w ? (uint32_t)cols * 2 : 0u);
+  bf16x8 xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    xv[i] = bload8(rx, vec_off(v, nvec, 0));
+    rv[i] = bload8(rr, vec_off(v, nvec, 0));
+    wv[i] = bload8(rw, vec_off(v, nvec, 0));
+  }
   float h[NV][8];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int v = lane + 64 * i;
-    if (v < nvec) {
-      unpack8(ld8(xr + v * 8), h[i]);
-      if (res) {
-        float r[8];
-        unpack8(ld8(res + row * cols + v * 8), r);
+    float r[8];
+    unpack8(xv[i], h[i]);
+    unpack8(rv[i], r);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) h[i][e] += r[e];
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += h[i][e] * h[i][e];
+    for (int e = 0; e < 8; ++e) {
+      h[i][e] += r[e];
+      ss += h[i][e] * h[i][e];
     }
   }
   ss = wave_sum(ss);
@@ -47,16 +62,10 @@ __global__ __launch_bounds__(256) void rms_norm_residual_kernel(
     const int v = lane + 64 * i;
     if (v < nvec) {
       if (res_out) st8(res_out + row * cols + v * 8, pack8(h[i]));
-      float y[8];
-      if (w) {
-        float wv[8];
-        unpack8(ld8(w + v * 8), wv);
+      float y[8], wf[8];
+      unpack8(wv[i], wf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = h[i][e] * f * wv[e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = h[i][e] * f;
-      }
+      for (int e = 0; e < 8; ++e) y[e] = h[i][e] * f * (w ? wf[e] : 1.f);
       st8(out + row * cols + v * 8, pack8(y));
     }
   }
@@ -71,28 +80,34 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nvec = cols >> 3;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * cols, (uint32_t)cols * 2);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)cols * 2);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(b, (uint32_t)cols * 2);
+  bf16x8 xv[NV], wv[NV], bv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    xv[i] = bload8(rx, vec_off(v, nvec, 0));
+    wv[i] = bload8(rw, vec_off(v, nvec, 0));
+    bv[i] = bload8(rb, vec_off(v, nvec, 0));
+  }
   float h[NV][8];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int v = lane + 64 * i;
-    if (v < nvec) {
-      unpack8(ld8(x + row * cols + v * 8), h[i]);
+    unpack8(xv[i], h[i]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += h[i][e];
-    }
+    for (int e = 0; e < 8; ++e) s += h[i][e];
   }
   const float mean = wave_sum(s) / (float)cols;
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int v = lane + 64 * i;
-    if (v < nvec) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        h[i][e] -= mean;
-        ss += h[i][e] * h[i][e];
-      }
+    for (int e = 0; e < 8; ++e) {
+      h[i][e] -= mean;
+      if (v < nvec) ss += h[i][e] * h[i][e];
     }
   }
   const float inv = rsqrtf(wave_sum(ss) / (float)cols + eps);
@@ -100,11 +115,11 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(
   for (int i = 0; i < NV; ++i) {
     const int v = lane + 64 * i;
     if (v < nvec) {
-      float wv[8], bv[8], y[8];
-      unpack8(ld8(w + v * 8), wv);
-      unpack8(ld8(b + v * 8), bv);
+      float wf[8], bf[8], y[8];
+      unpack8(wv[i], wf);
+      unpack8(bv[i], bf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = h[i][e] * inv * wv[e] + bv[e];
+      for (int e = 0; e < 8; ++e) y[e] = h[i][e] * inv * wf[e] + bf[e];
       st8(out + row * cols + v * 8, pack8(y));
     }
   }
@@ -119,17 +134,25 @@ __global__ __launch_bounds__(256) void adarms_norm_kernel(
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nvec = cols >> 3;
-  const bf16_t* st = style + (row / rows_per_style) * style_stride;
+  const int64_t so = (row / rows_per_style) * style_stride;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * cols, (uint32_t)cols * 2);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(style + so, (uint32_t)cols * 6);
+  bf16x8 xv[NV], scv[NV], shv[NV], gv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    xv[i] = bload8(rx, vec_off(v, nvec, 0));
+    scv[i] = bload8(rs, vec_off(v, nvec, 0));
+    shv[i] = bload8(rs, vec_off(v, nvec, cols));
+    gv[i] = bload8(rs, vec_off(v, nvec, 2 * cols));
+  }
   float h[NV][8];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int v = lane + 64 * i;
-    if (v < nvec) {
-      unpack8(ld8(x + row * cols + v * 8), h[i]);
+    unpack8(xv[i], h[i]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss += h[i][e] * h[i][e];
-    }
+    for (int e = 0; e < 8; ++e) ss += h[i][e] * h[i][e];
   }
   const float f = rsqrtf(wave_sum(ss) / (float)cols + eps);
 #pragma unroll
@@ -137,13 +160,12 @@ __global__ __launch_bounds__(256) void adarms_norm_kernel(
     const int v = lane + 64 * i;
     if (v < nvec) {
       float sc[8], sh[8], y[8];
-      unpack8(ld8(st + v * 8), sc);
-      unpack8(ld8(st + cols + v * 8), sh);
+      unpack8(scv[i], sc);
+      unpack8(shv[i], sh);
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] = h[i][e] * f * (1.f + sc[e]) + sh[e];
       st8(out + row * cols + v * 8, pack8(y));
-      if (gate_out)
-        st8(gate_out + row * cols + v * 8, ld8(st + 2 * cols + v * 8));
+      if (gate_out) st8(gate_out + row * cols + v * 8, gv[i]);
     }
   }
 }
