@@ -78,7 +78,7 @@ def time_dominant_kernel(model, iters=20):
     flops = 2.0 * M * N * Kd * 2
     achieved = flops / (us * 1e-6) / 1e12
     return {
-        'kernel': 'gemm_tile_kernel<128,64,GEGLU> (prefix gate/up, '
+        'kernel': 'gemm_tile_kernel<256,256,GEGLU> (prefix gate/up, '
                   f'M={M} N={N}x2 K={Kd})',
         'bound': 'mfma',
         'achieved': round(achieved, 2),
@@ -226,17 +226,17 @@ def kernel_table(model):
     M = px.shape[0]
     kc0, vc0 = b['kc'][0], b['vc'][0]
     pre = [
-        ('gemm_tile_kernel<QKV_ROPE> (prefix)', lambda: K.gemm_qkv_rope(
+        ('gemm_tile_kernel<64,128,QKV_ROPE> (prefix)', lambda: K.gemm_qkv_rope(
             px, L['qkv_w'], model.rope, b['pos_pre'], b['pre_q'].view(M, -1),
             kc0.view(T, D), vc0, H, D, rownorm_eps=cfg.rms_eps, row_group=S,
             row_group_stride=T, v_ld=T), 2 * M * nq * cfg.llm_hidden),
-        ('gemm_tile_kernel<PLAIN> o-proj (prefix)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> o-proj (prefix)', lambda: K.gemm(
             b['pre_ctx'].view(M, -1), L['o_w'], out=b['pre_h'][:, :cfg.llm_hidden],
             residual=px), 2 * M * cfg.llm_hidden * H * D),
-        ('gemm_tile_kernel<GEGLU> (prefix)', lambda: K.gemm_geglu(
+        ('gemm_tile_kernel<256,256,GEGLU> (prefix)', lambda: K.gemm_geglu(
             px, L['gate_w'], L['up_w'], out=b['pre_h'], rownorm_eps=cfg.rms_eps),
          4 * M * cfg.llm_mlp * cfg.llm_hidden),
-        ('gemm_tile_kernel<PLAIN> down, split-K 4 (prefix)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> down, split-K 2 (prefix)', lambda: K.gemm(
             b['pre_h'], L['down_w'], out=b['pre_q'].view(M, -1)[:, :cfg.llm_hidden],
             residual=px), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
         ('attn_kernel<256,256> + merge (prefix)', lambda: K.mqa_attention(
@@ -248,16 +248,16 @@ def kernel_table(model):
     Mv, vh = vx.shape
     nimg = Mv // cfg.num_patches
     pre += [
-        ('gemm_tile_kernel<PLAIN> qkv+bias (SigLIP)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> qkv+bias (SigLIP)', lambda: K.gemm(
             vxn, V['qkv_w'], out=b['vis_qkv'], bias=V['qkv_b']),
          2 * Mv * 3 * vh * vh),
-        ('gemm_tile_kernel<PLAIN> o-proj+bias+res, split-K 3 (SigLIP)',
+        ('gemm_tile_kernel<64,128,PLAIN> o-proj+bias+res (SigLIP)',
          lambda: K.gemm(b['vis_ctx'], V['o_w'], out=vxn, bias=V['o_b'],
                         residual=vx), 2 * Mv * vh * vh),
-        ('gemm_tile_kernel<PLAIN> fc1+bias+gelu (SigLIP)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> fc1+bias+gelu (SigLIP)', lambda: K.gemm(
             vxn, V['fc1_w'], out=b['vis_h'], bias=V['fc1_b'], act=2),
          2 * Mv * cfg.vit_mlp * vh),
-        ('gemm_tile_kernel<PLAIN> fc2+bias+res (SigLIP)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> fc2+bias+res, split-K 4 (SigLIP)', lambda: K.gemm(
             b['vis_h'], V['fc2_w'], out=vxn, bias=V['fc2_b'], residual=vx),
          2 * Mv * vh * cfg.vit_mlp),
         ('attn_kernel<96,80> (SigLIP)', lambda: K.mha_packed_qkv(

@@ -80,6 +80,18 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const bf16x8& a,
                                                  0, 0);
 }
 
+// D(32x32, fp32) += A(32x16) * B(16x32), bf16 inputs.
+// Lane l supplies A row (l % 32) and B column (l % 32), each with the 8
+// k-values 8 (l / 32) .. + 7.  D lane l holds column (l % 32), rows
+// 8 (r / 4) + 4 (l / 32) + r % 4 for r = 0..15.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16_t mfma32x32x16(const bf16x8& a,
+                                                 const bf16x8& b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_mfma(a), as_mfma(b), c, 0,
+                                                 0, 0);
+}
+
 // Raw buffer access: loads at byte offsets >= `bytes` return zero without
 // touching memory, so a guarded load needs no branch (a branch around each
 // load makes the compiler wait for it at the join, serializing the loads).
@@ -90,6 +102,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
 }
 
 constexpr uint32_t kOOB = 0x80000000u;  // an offset beyond any buffer here
+
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4 ...
+// lds): lane l's bytes land at LDS address lds + 16 l (wave-uniform `lds`,
+// passed in M0).  An out-of-view offset writes zeros.  Issued through inline
+// asm: the compiler then does not treat every later LDS read as dependent on
+// the load (it would wait for all loads in flight, i.e. for the prefetch),
+// so the caller must wait for the load with s_waitcnt vmcnt before reading.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4_t make_rsrc4(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_char_t*)p;
+}
+
+__device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds,
+                                           uint32_t off) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(off), "s"(rsrc)
+               : "memory");
+}
 
 __device__ __forceinline__ bf16x8 bload8(__amdgpu_buffer_rsrc_t r,
                                          uint32_t off) {

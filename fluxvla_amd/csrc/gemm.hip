@@ -352,40 +352,70 @@ static bool epi_vec_ok(const GemmArgs& d) {
 // ---------------------------------------------------------------------------
 // Tiled kernel (M > 64)
 // ---------------------------------------------------------------------------
-// 256 threads = 2 x 2 waves; block tile BM x BN (GEGLU: BN columns of each
-// of the two weights).  K moves through a 2-stage LDS ring in 64-wide slabs
-// with ONE barrier per slab: while slab t feeds the MFMAs, slab t+1 (already
-// in registers) is written to the other LDS stage and slab t+2's global
-// loads are issued.  LDS rows are XOR-swizzled (see the loader) so neither
-// the staging writes nor the fragment reads conflict.  <= 256 registers and
-// <= 64 KiB of LDS keep two workgroups per CU.  With
-// splits > 1 the K range is split over blockIdx.y and fp32 partials go to
-// the workspace for gemm_partial_reduce_kernel.
-template <int BM, int BN, int MODE>
-constexpr int tile_min_blocks() {
-  // two workgroups per CU when the 2-stage ring fits twice in 160 KiB
-  return (2 * (BM + (MODE == FVX_GEMM_GEGLU ? 2 : 1) * BN) * 64 * 2 <= 80 * 1024 &&
-          MODE != FVX_GEMM_QKV_ROPE) ? 2 : 1;
+// WGM x WGN waves own a BM x BN output tile.  GEGLU tiles hold BN / 2
+// columns of each weight, and wave wn holds the gate and the up accumulators
+// of the same output columns, so the GeGLU product needs no exchange.  Each
+// wave computes a (BM / WGM) x (BN / WGN) sub-tile with
+// v_mfma_f32_32x32x16_bf16 (on MI355X it sustains ~1.4x the rate of the
+// 16x16x32 form).
+//
+// K moves through a STAGES-deep LDS ring in 64-wide slabs fetched with
+// buffer_load_dwordx4 ... lds: the data goes from L2 straight into LDS (no
+// staging registers, no ds_write).  One wave instruction moves 8 rows of 128
+// bytes; lane l fetches row l / 8, 16-byte chunk (l % 8) ^ ((row >> 1) & 7),
+// so the LDS image is XOR-swizzled and both the fetch and the fragment reads
+// (16 consecutive rows of one chunk per 16 lanes) are free of bank
+// conflicts.  One barrier per slab: at slab t each wave waits for its own
+// loads of slab t, the barrier publishes everyone's and frees the stage of
+// slab t - 1, which then receives slab t + STAGES - 1.  Loads of slabs past
+// the K range use out-of-view offsets (zeros), so the loop has no branch
+// around a load.
+//
+// Per-row sums of squares for the fused RMSNorm are taken from the A
+// fragments as they feed the MFMAs.  The epilogue moves each wave's 32-row
+// blocks through LDS so that every lane finishes 8 consecutive columns of a
+// row with 16-byte accesses.  With splits > 1 the K range is split over
+// blockIdx.y and fp32 partials go to the workspace for
+// gemm_partial_reduce_kernel.
+template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE>
+struct TileCfg {
+  static constexpr int NW = WGM * WGN, NT = 64 * NW;
+  static constexpr int NB = MODE == FVX_GEMM_GEGLU ? 2 : 1;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;  // WN counts both weights
+  static constexpr int FM = WM / 32, FN = WN / 32;
+  static constexpr int ROWS = BM + BN;                // LDS rows per stage
+  static constexpr int STAGE_BYTES = ROWS * 128;
+  static constexpr int LPW = ROWS / (8 * NW);         // loads per wave per slab
+  static constexpr int WNO = WN / NB;                 // output columns per wave
+  static constexpr int ELD = WN + 4;                  // epilogue scratch stride
+  static constexpr int EPI_BYTES = NW * 32 * ELD * 4;
+  static constexpr int LDS_BYTES =
+      STAGES * STAGE_BYTES > EPI_BYTES ? STAGES * STAGE_BYTES : EPI_BYTES;
+  static_assert(BM % (32 * WGM) == 0 && BN % (32 * NB * WGN) == 0, "tile");
+  static_assert(ROWS % (8 * NW) == 0 && STAGES >= 2, "loader");
+  static_assert(NT >= BM, "row sums");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  // s_waitcnt: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int MODE>
-__global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_tile_kernel(GemmArgs p,
-                                                           int m_tiles,
-                                                           int n_tiles,
-                                                           int splits,
-                                                           int64_t kchunk) {
-  constexpr int BK = 64;
-  constexpr int LD = BK;  // 128-byte rows, XOR-swizzled chunks (see loader)
-  constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int FM = WM / 16, FN = WN / 16;
-  constexpr int AI = BM / 32, BI = BN / 32;
-  constexpr int STAGE = BM * LD + NB * BN * LD;  // bf16 elements per stage
-  __shared__ __align__(16) bf16_t smem[2 * STAGE];
+template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
+    GemmArgs p, int m_tiles, int n_tiles, int splits, int64_t kchunk,
+    int vec_ok) {
+  typedef TileCfg<BM, BN, WGM, WGN, STAGES, MODE> C;
+  constexpr int NB = C::NB, WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
+  constexpr int LPW = C::LPW, WNO = C::WNO, ELD = C::ELD;
+  __shared__ __align__(16) char smem[C::LDS_BYTES];
   __shared__ float sRow[BM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
 
   // XCD-aware tile order: consecutive tile ids (the M tiles of one weight
   // panel, m fastest) land on one XCD and share its L2.
@@ -394,180 +424,183 @@ __global__ __launch_bounds__(256, (tile_min_blocks<BM, BN, MODE>())) void gemm_t
   if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
   const int split = blockIdx.y;
-  const int64_t m0 = (int64_t)m_tile * BM, n0 = (int64_t)n_tile * BN;
   const int64_t M = p.m, N = p.n, K = p.k;
+  const int64_t m0 = (int64_t)m_tile * BM, n0 = (int64_t)n_tile * (BN / NB);
   const int64_t kb = (int64_t)split * kchunk;
   const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
-  const int nk = (int)((ke - kb + BK - 1) / BK);
+  const int nk = (int)((ke - kb + 63) / 64);
 
-  const bf16_t* A = (const bf16_t*)p.a;
-  const bf16_t* Bm[2] = {(const bf16_t*)p.b, (const bf16_t*)p.b2};
-
-  // Loader: 8 consecutive lanes move one 128-byte row slab (coalesced).
-  // LDS rows have no padding; chunk c of row r lives at chunk position
-  // c ^ ((r >> 1) & 7).  With 64 banks and 16 lanes per LDS cycle, the
-  // loader's 16 lanes (rows 2j, 2j+1, all chunks) and a fragment read's 16
-  // lanes (16 consecutive rows, one chunk) both land on 16 distinct 4-bank
-  // groups: no bank conflicts on either side.
-  const int lrow = tid >> 3, lchk = tid & 7;
-  // Two register sets: slab t is loaded into set t & 1 two slabs before it
-  // is written to LDS, so its global latency overlaps two slabs of MFMAs.
-  bf16x8 ra[2][AI], rb[2][NB][BI];
-  float ss[AI];
-#pragma unroll
-  for (int i = 0; i < AI; ++i) ss[i] = 0.f;
-
-  // Buffer views of this tile's A rows and B rows: rows past M / N read as
-  // zero, and a slab past the K range gets an out-of-view offset, so every
-  // load is unconditional (no branch, hence no conservative wait at a join:
-  // the next slabs' loads stay in flight under the MFMAs).
+  // Buffer views of the tile's A rows and B rows: rows past M / N read zero.
   const int64_t a_rows = (M - m0 < BM) ? M - m0 : BM;
-  const int64_t b_rows = (N - n0 < BN) ? N - n0 : BN;
-  const __amdgpu_buffer_rsrc_t rA = make_rsrc(A + m0 * p.lda, (uint32_t)(a_rows * p.lda * 2));
-  const __amdgpu_buffer_rsrc_t rB[2] = {
-      make_rsrc(Bm[0] + n0 * p.ldb, (uint32_t)(b_rows * p.ldb * 2)),
-      make_rsrc((NB == 2 ? Bm[1] : Bm[0]) + n0 * p.ldb, (uint32_t)(b_rows * p.ldb * 2))};
-  // per-thread byte offsets of slab 0 (rows lrow + 32 i, chunk lchk); slab t
-  // adds 2 t BK bytes
+  const int64_t b_rows = (N - n0 < BN / NB) ? N - n0 : BN / NB;
   const uint32_t lda2 = (uint32_t)p.lda * 2, ldb2 = (uint32_t)p.ldb * 2;
-  const uint32_t offA0 = (uint32_t)lrow * lda2 + (uint32_t)(kb + lchk * 8) * 2;
-  const uint32_t offB0 = (uint32_t)lrow * ldb2 + (uint32_t)(kb + lchk * 8) * 2;
-  const int kin_end = (int)(ke - kb - lchk * 8);  // slab t is in range iff t BK < kin_end
-  auto gload = [&](int t, int set) {
-    const bool kin = t < nk && t * BK < kin_end;
-    const uint32_t dk = (uint32_t)t * (BK * 2);
+  const i32x4_t rA =
+      make_rsrc4((const bf16_t*)p.a + m0 * p.lda, (uint32_t)(a_rows * lda2));
+  const i32x4_t rB0 =
+      make_rsrc4((const bf16_t*)p.b + n0 * p.ldb, (uint32_t)(b_rows * ldb2));
+  const i32x4_t rB1 =
+      make_rsrc4((const bf16_t*)(NB == 2 ? p.b2 : p.b) + n0 * p.ldb,
+                 (uint32_t)(b_rows * ldb2));
+
+  // Load i of this wave fills LDS rows R0 = (wave LPW + i) 8 .. + 7 of a
+  // stage: A rows first, then BN / NB rows of each weight.
+  const int lr = lane >> 3, lc = lane & 7;
+  uint32_t voff[LPW];
+  int kmax[LPW];  // slab t of load i is in range iff 64 t < kmax[i]
+  i32x4_t rsel[LPW];
 #pragma unroll
-    for (int i = 0; i < AI; ++i)
-      ra[set][i] = bload8(rA, kin ? offA0 + dk + (uint32_t)(32 * i) * lda2 : kOOB);
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int i = 0; i < BI; ++i)
-        rb[set][b][i] = bload8(rB[b], kin ? offB0 + dk + (uint32_t)(32 * i) * ldb2 : kOOB);
-  };
-  const int wpos = (lchk ^ ((lrow >> 1) & 7)) * 8;  // same for rows lrow + 32 i
-  auto swrite = [&](int buf, int set) {
-    bf16_t* sa = smem + buf * STAGE;
-#pragma unroll
-    for (int i = 0; i < AI; ++i) {
-      st8(&sa[(lrow + 32 * i) * LD + wpos], ra[set][i]);
-      ss[i] += sumsq8(ra[set][i]);  // unconditional: no branch in the loop
+  for (int i = 0; i < LPW; ++i) {
+    const int R0 = (wave * LPW + i) * 8, R = R0 + lr;
+    const int gc = lc ^ ((R >> 1) & 7);
+    const uint32_t kofs = (uint32_t)(kb + gc * 8) * 2;
+    if (R0 < BM) {
+      rsel[i] = rA;
+      voff[i] = (uint32_t)R * lda2 + kofs;
+    } else {
+      // 8-row groups never straddle the two weights' regions (BN / NB % 8 == 0)
+      const int br0 = R0 - BM;
+      rsel[i] = br0 < BN / NB ? rB0 : rB1;
+      voff[i] = (uint32_t)(br0 % (BN / NB) + lr) * ldb2 + kofs;
     }
+    kmax[i] = (int)(ke - kb) - gc * 8;
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * LPW * 1024);
+  auto issue = [&](int t, int stage) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int i = 0; i < BI; ++i)
-        st8(&sa[BM * LD + (b * BN + lrow + 32 * i) * LD + wpos], rb[set][b][i]);
+    for (int i = 0; i < LPW; ++i)
+      load_lds16(rsel[i], lds0 + stage * C::STAGE_BYTES + i * 1024,
+                 64 * t < kmax[i] ? voff[i] + (uint32_t)t * 128 : kOOB);
   };
 
-  f32x4_t acc[NB][FM][FN];
+  f32x16_t acc[FM][FN];
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[b][i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  float ss[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) ss[i] = 0.f;
 
-  const int fr = lane & 15, fk = (lane >> 4) * 8;
-  auto compute = [&](int buf) {
-    const bf16_t* sa = smem + buf * STAGE;
-    const bf16_t* sb = sa + BM * LD;
+  // LDS row of B fragment j of this wave (GEGLU: gate blocks, then up)
+  auto brow = [&](int j) {
+    if (NB == 2)
+      return j < FN / 2 ? BM + wn * (WN / 2) + 32 * j
+                        : BM + BN / 2 + wn * (WN / 2) + 32 * (j - FN / 2);
+    return BM + wn * WN + 32 * j;
+  };
+  // rows of a fragment are (multiple of 32) + lane % 32: swizzle (lane >> 1) & 7
+  const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
+  auto compute = [&](int stage) {
+    const char* s = smem + stage * C::STAGE_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      bf16x8 af[FM], bfr[NB][FN];
-      // rows here are (multiple of 16) + fr, so (row >> 1) & 7 == fr >> 1
-      const int rpos = ((4 * ks + (lane >> 4)) ^ ((fr >> 1) & 7)) * 8;
+    for (int ks = 0; ks < 4; ++ks) {
+      const int cpos = ((2 * ks + hk) ^ sw) * 16;
+      bf16x8 af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = ld8(&sa[(wm * WM + i * 16 + fr) * LD + rpos]);
+        af[i] = *(const bf16x8*)(s + (wm * WM + 32 * i + fr) * 128 + cpos);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          bfr[b][j] = ld8(&sb[(b * BN + wn * WN + j * 16 + fr) * LD + rpos]);
+      for (int i = 0; i < FM; ++i) {
+        ss[i] += sumsq8(af[i]);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[b][i][j] = mfma16x16x32(af[i], bfr[b][j], acc[b][i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+      }
     }
   };
 
-  // slab t: loaded into register set t&1, written to LDS stage t&1.  The
-  // loop body has no branches: slabs past nk load as zeros (out-of-view
-  // offsets) and add nothing, so every half-step issues the same loads and
-  // the compiler's wait counts stay exact (any conditional load makes it
-  // wait for every load in flight, which undoes the prefetch).
-  gload(0, 0);
-  gload(1, 1);
-  swrite(0, 0);
-  gload(2, 0);
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
+  for (int t0 = 0; t0 < nk; t0 += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+      const int t = t0 + s;
+      if (t >= nk) break;
+      wait_vmcnt<LPW * (STAGES - 2)>();  // this wave's loads of slab t landed
+      __syncthreads();                   // everyone's, and slab t-1 is consumed
+      issue(t + STAGES - 1, (s + STAGES - 1) % STAGES);
+      compute(s);
+    }
+  }
+  // Loads past the end may still be in flight into the ring: drain them
+  // before the ring becomes epilogue scratch.
+  wait_vmcnt<0>();
+
+  // Row sums of squares: lanes l and l ^ 32 hold the two k halves of row
+  // l % 32 of block i (waves with wn > 0 computed the same sums).
+  if (wn == 0) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const float s2 = ss[i] + __shfl_xor(ss[i], 32, 64);
+      if (lane < 32) sRow[wm * WM + 32 * i + lane] = s2;
+    }
+  }
   __syncthreads();
-  for (int t = 0; t < nk; t += 2) {
-    compute(0);                          // slab t
-    swrite(1, 1);                        // slab t+1
-    gload(t + 3, 1);
-    __syncthreads();
-    compute(1);                          // slab t+1
-    swrite(0, 0);                        // slab t+2
-    gload(t + 4, 0);
-    __syncthreads();
-  }
 
-  // Row sums of squares of this K range: 8 consecutive lanes share a row.
-  if (p.rownorm) {
-#pragma unroll
-    for (int i = 0; i < AI; ++i) {
-      float s2 = ss[i];
-      s2 += __shfl_xor(s2, 1, 64);
-      s2 += __shfl_xor(s2, 2, 64);
-      s2 += __shfl_xor(s2, 4, 64);
-      if (lchk == 0) sRow[lrow + 32 * i] = s2;
-    }
-    __syncthreads();
-  }
+  float* ws = (float*)((char*)p.workspace + kCounterBytes);
+  const int64_t plane = (int64_t)splits * M * N;
+  if (splits > 1 && n_tile == 0 && tid < BM && m0 + tid < M)
+    ws[NB * plane + (int64_t)split * M + m0 + tid] = sRow[tid];
 
-  if (splits > 1) {
-    float* ws = (float*)((char*)p.workspace + kCounterBytes);
-    const int64_t plane = (int64_t)splits * M * N;
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int64_t n = n0 + wn * WN + j * 16 + fr;
-          const int64_t r0 = m0 + wm * WM + i * 16 + 4 * (lane >> 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n < N && r0 + e < M)
-              ws[b * plane + ((int64_t)split * M + r0 + e) * N + n] = acc[b][i][j][e];
-        }
-    if (n_tile == 0 && p.rownorm && tid < BM && m0 + tid < M)
-      ws[NB * plane + (int64_t)split * M + m0 + tid] = sRow[tid];
-    return;
-  }
-
+  // Epilogue: each 32-row block of the wave's sub-tile goes through the
+  // wave's own LDS scratch [32][ELD] fp32 (GEGLU: gate columns, then up).
+  float* scr = (float*)smem + wave * 32 * ELD;
+  constexpr int CH = WNO / 8;               // 8-column chunks per row
+  constexpr int ITEMS = 32 * CH / 64;       // chunks per lane per block
+  constexpr int EB = ITEMS < 4 ? ITEMS : 4; // chunks whose loads fly together
+  const int64_t nw0 = n0 + wn * WNO;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const int lr0 = wm * WM + i * 16 + 4 * (lane >> 4);
-    float rs[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      rs[j] = p.rownorm ? rsqrtf(sRow[lr0 + j] / (float)K + p.rownorm_eps) : 1.f;
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t n = n0 + wn * WN + j * 16 + fr;
-      float v[4], u[4], pv[4];
+      for (int r = 0; r < 16; ++r)
+        scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * ELD + 32 * j + fr] = acc[i][j][r];
+    const int64_t rb = m0 + wm * WM + 32 * i;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = acc[0][i][j][e];
-        u[e] = acc[NB - 1][i][j][e];
-        pv[e] = (MODE == FVX_GEMM_QKV_ROPE) ? __shfl_xor(v[e], 1, 64) : 0.f;
+    for (int e0 = 0; e0 < ITEMS; e0 += EB) {
+      EpiIn in[EB];
+      if (splits == 1) {
+#pragma unroll
+        for (int e = 0; e < EB; ++e) {
+          const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
+          const int64_t nn = nw0 + 8 * ch;
+          const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+          epi_load<MODE>(p, rb + row, nn, vec_ok && cnt == 8, cnt, in[e]);
+        }
       }
-      epilogue4<MODE>(p, m0 + lr0, n, v, u, pv, rs);
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
+        const int64_t m = rb + row, nn = nw0 + 8 * ch;
+        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+        if (m >= M || cnt <= 0) continue;
+        float v[8], u[8];
+        const float* sv = scr + row * ELD + 8 * ch;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          v[x] = sv[x];
+          u[x] = NB == 2 ? sv[WNO + x] : 0.f;
+        }
+        if (splits > 1) {
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            float* dst = ws + b * plane + ((int64_t)split * M + m) * N + nn;
+#pragma unroll
+            for (int x = 0; x < 8; ++x)
+              if (x < cnt) dst[x] = b ? u[x] : v[x];
+          }
+          continue;
+        }
+        const float r = p.rownorm
+                            ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps)
+                            : 1.f;
+        epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e]);
+      }
     }
   }
 }
@@ -997,18 +1030,6 @@ static int validate(const GemmArgs& d) {
   return FVX_OK;
 }
 
-}  // namespace fvx
-
-using namespace fvx;
-
-extern "C" int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d) {
-  if (!d || d->m <= 0) return 0;
-  if (use_skinny(*d)) return plan_skinny(*d).ws_bytes;
-  // tiled path: at most 4 K splits of fp32 partials (+ row sums)
-  const int nb = d->mode == FVX_GEMM_GEGLU ? 2 : 1;
-  return kCounterBytes + ((int64_t)nb * 4 * d->m * d->n + 4 * d->m) * 4;
-}
-
 #define FVX_MODE_DISPATCH_NG(MODE_RT, LAUNCH)                 \
   switch (MODE_RT) {                                          \
     case FVX_GEMM_QKV_ROPE: LAUNCH(FVX_GEMM_QKV_ROPE); break; \
@@ -1023,6 +1044,109 @@ extern "C" int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d) {
     case FVX_GEMM_QKV_ROPE: LAUNCH(FVX_GEMM_QKV_ROPE); break; \
     default: LAUNCH(FVX_GEMM_EULER); break;                   \
   }
+
+// Tile configurations: {BM, BN (all weights' columns), waves M x N, stages}.
+//   0: 128 x 128, 2 x 2 waves of 64 x 64, 2 stages (64 KiB of LDS)
+//   1: 256 x 256, 2 x 4 waves of 128 x 64, 2 stages (128 KiB: one workgroup
+//      of 8 waves per CU; half the L2 traffic per flop of config 0)
+//   2:  64 x 128, 2 x 2 waves of 32 x 64, 2 stages (48 KiB)
+// Measured on MI355X (us; bs=1 chunk shapes, configs 0 / 1 / 2):
+//   prefix GeGLU 816 x 16384 x2 x 2048   158 / 151 / 154
+//   prefix QKV   816 x 2560 x 2048        39 /  84 /  27
+//   prefix O     816 x 2048 x 2048        37 /  82 /  24
+//   SigLIP fc1   768 x 4304 x 1152        34 /  69 /  23
+//   SigLIP o     768 x 1152 x 1152        25 /  58 /  15
+// The small projections gain from the extra workgroups of config 2 more
+// than they lose to its higher LDS traffic per flop.
+static const int kTileBM[] = {128, 256, 64};
+static const int kTileBN[] = {128, 256, 128};
+constexpr int kTileCfgs = 3;
+
+struct TilePlan {
+  int cfg, splits;
+};
+
+// Config 1 for GeGLU projections that still give >= 256 of its tiles, else
+// config 2.  A long K (>= 4096) with fewer than 256 tiles is split
+// (ceil(384 / tiles), at most 4: prefix down projection 2, SigLIP fc2 4);
+// with a shorter K the partials cost more than the idle CUs.
+static TilePlan plan_tile(const GemmArgs& d) {
+  TilePlan t;
+  const bool gg = d.mode == FVX_GEMM_GEGLU;
+  t.cfg = (gg && ((d.m + 255) / 256) * ((d.n + 127) / 128) >= 256) ? 1 : 2;
+  const int64_t bm = kTileBM[t.cfg], bn = kTileBN[t.cfg] / (gg ? 2 : 1);
+  const int64_t tiles = ((d.m + bm - 1) / bm) * ((d.n + bn - 1) / bn);
+  t.splits = 1;
+  if (d.split_k > 0) {
+    t.splits = d.split_k;
+  } else if (tiles < 256 && d.k >= 4096) {
+    t.splits = (int)((384 + tiles - 1) / tiles);
+    if (t.splits > 4) t.splits = 4;
+  }
+  return t;
+}
+
+static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
+  FVX_REQUIRE(cfg >= 0 && cfg < kTileCfgs, FVX_ERR_ARG, "gemm: bad tile config %d", cfg);
+  const bool gg = d.mode == FVX_GEMM_GEGLU;
+  const int bm = kTileBM[cfg], bn = kTileBN[cfg] / (gg ? 2 : 1);
+  const int m_tiles = (int)((d.m + bm - 1) / bm);
+  const int n_tiles = (int)((d.n + bn - 1) / bn);
+  if (splits < 1) splits = 1;
+  int64_t kchunk = (d.k + splits - 1) / splits;
+  kchunk = (kchunk + 63) / 64 * 64;
+  splits = (int)((d.k + kchunk - 1) / kchunk);
+  const int nbm = gg ? 2 : 1;
+  const int64_t need = splits > 1 ? kCounterBytes + ((int64_t)nbm * splits * d.m * d.n +
+                                                     (int64_t)splits * d.m) * 4
+                                   : 0;
+  if (splits > 1 && (!d.workspace || d.workspace_bytes < need)) {
+    if (d.split_k > 1)
+      return set_error(FVX_ERR_WORKSPACE,
+                       "gemm: split_k=%d needs %lld workspace bytes, got %lld",
+                       d.split_k, (long long)need, (long long)d.workspace_bytes);
+    splits = 1;
+    kchunk = d.k;
+  }
+  FVX_REQUIRE(splits == 1 || aligned16(d.workspace), FVX_ERR_ALIGN,
+              "gemm: workspace must be 16B aligned");
+  const int vec_ok = epi_vec_ok(d) ? 1 : 0;
+  dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
+#define LT(BM_, BN_, WGM_, WGN_, ST_, MODE)                                       \
+  hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE>), grid,   \
+                     dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits,   \
+                     kchunk, vec_ok)
+#define LCFG(MODE)                                \
+  if (cfg == 0) LT(128, 128, 2, 2, 2, MODE);      \
+  else if (cfg == 1) LT(256, 256, 2, 4, 2, MODE); \
+  else LT(64, 128, 2, 2, 2, MODE);
+  FVX_MODE_DISPATCH(d.mode, LCFG)
+#undef LCFG
+#undef LT
+  int st3 = launch_status("gemm(tile)");
+  if (st3 || splits == 1) return st3;
+#define L(MODE)                                                            \
+  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                     \
+                     dim3((unsigned)((d.n + 63) / 64), (unsigned)((d.m + 3) / 4)), \
+                     dim3(256), 0, s, d, splits)
+  FVX_MODE_DISPATCH(d.mode, L)
+#undef L
+  return launch_status("gemm(reduce)");
+}
+
+}  // namespace fvx
+
+using namespace fvx;
+
+extern "C" int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d) {
+  if (!d || d->m <= 0) return 0;
+  if (use_skinny(*d)) return plan_skinny(*d).ws_bytes;
+  // tiled path: fp32 partials (+ row sums) of every K split
+  const int64_t sp = plan_tile(*d).splits;
+  if (sp <= 1) return 0;
+  const int nb = d->mode == FVX_GEMM_GEGLU ? 2 : 1;
+  return kCounterBytes + ((int64_t)nb * sp * d->m * d->n + sp * d->m) * 4;
+}
 
 extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
   clear_error();
@@ -1052,69 +1176,6 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
 #undef L
     return launch_status("gemm(skinny)");
   }
-  // Tiled path: 128 x 128 tiles (GEGLU: 128 x 64 of each weight) when that
-  // gives >= 512 workgroups (two per CU), else 64 x 128.  Projections with a long K and
-  // too few tiles to fill 256 CUs split K.
-  const bool gg = d.mode == FVX_GEMM_GEGLU;
-  const int64_t mt128 = (d.m + 127) / 128, mt64 = (d.m + 63) / 64;
-  const int64_t ncols = gg ? 2 * d.n : d.n;  // output columns incl. both weights
-  int cfg;  // 1: 128x128, 2: 64x128  (128x256 needs >110 KiB of LDS: one
-            // workgroup per CU, measured 3-4x slower than two of 128x128)
-  if (mt128 * ((ncols + 127) / 128) >= 512) cfg = 1;
-  else cfg = 2;
-  const int bm = cfg == 2 ? 64 : 128;
-  const int bn = 128 / (gg ? 2 : 1);
-  const int m_tiles = (int)(cfg == 2 ? mt64 : mt128);
-  const int n_tiles = (int)((d.n + bn - 1) / bn);
-  const int tiles = m_tiles * n_tiles;
-  // Split K when the tiles cannot fill the CUs twice over and K is long:
-  // more workgroups per CU hide the memory latency of the K loop.
-  int splits = d.split_k > 0 ? d.split_k : 1;
-  if (d.split_k <= 0 && d.k >= 8192 && tiles < 512) {
-    splits = 4;
-  } else if (d.split_k <= 0 && tiles < 160 && d.k >= 4096) {
-    splits = (int)((256 + tiles - 1) / tiles);
-    if (splits > 4) splits = 4;
-  }
-  int64_t kchunk = (d.k + splits - 1) / splits;
-  kchunk = (kchunk + 63) / 64 * 64;
-  splits = (int)((d.k + kchunk - 1) / kchunk);
-  const int nbm = gg ? 2 : 1;
-  const int64_t need = splits > 1 ? kCounterBytes + ((int64_t)nbm * splits * d.m * d.n +
-                                                     (int64_t)splits * d.m) * 4
-                                   : 0;
-  if (splits > 1 && (!d.workspace || d.workspace_bytes < need)) {
-    if (d.split_k > 1)
-      return set_error(FVX_ERR_WORKSPACE,
-                       "gemm: split_k=%d needs %lld workspace bytes, got %lld",
-                       d.split_k, (long long)need, (long long)d.workspace_bytes);
-    splits = 1;
-    kchunk = d.k;
-  }
-  dim3 grid((unsigned)tiles, (unsigned)splits);
-#define LT(BM_, BN_, MODE)                                                  \
-  hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, MODE>), grid, dim3(256), 0, \
-                     s, d, m_tiles, n_tiles, splits, kchunk)
-  if (gg) {
-    if (cfg == 1) LT(128, 64, FVX_GEMM_GEGLU);
-    else LT(64, 64, FVX_GEMM_GEGLU);
-  } else if (cfg == 1) {
-#define L(MODE) LT(128, 128, MODE)
-    FVX_MODE_DISPATCH_NG(d.mode, L)
-#undef L
-  } else {
-#define L(MODE) LT(64, 128, MODE)
-    FVX_MODE_DISPATCH_NG(d.mode, L)
-#undef L
-  }
-#undef LT
-  int st3 = launch_status("gemm(tile)");
-  if (st3 || splits == 1) return st3;
-#define L(MODE)                                                            \
-  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                     \
-                     dim3((unsigned)((d.n + 63) / 64), (unsigned)((d.m + 3) / 4)), \
-                     dim3(256), 0, s, d, splits)
-  FVX_MODE_DISPATCH(d.mode, L)
-#undef L
-  return launch_status("gemm(reduce)");
+  TilePlan tp = plan_tile(d);
+  return run_tile(d, tp.cfg, tp.splits, s);
 }
