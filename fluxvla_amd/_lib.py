@@ -60,6 +60,8 @@ class GemmDesc(ctypes.Structure):
         ('v_transposed', c_i32),
         ('a_frag', c_i32), ('b_frag', c_i32),
         ('c_frag', c_vp),
+        ('b_fp8', c_i32),
+        ('b_scale', c_vp), ('b2_scale', c_vp),
     ]
 
 

@@ -92,6 +92,85 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(const bf16x8& a,
                                                  0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// fp8 (OCP e4m3fn, max 448) with power-of-two block scales (E8M0)
+// ---------------------------------------------------------------------------
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
+
+// E8M0 exponent e (scale 2^(e - 127)) of a block whose largest magnitude has
+// bf16 bits `amax`: the smallest power of two with amax / 2^(e-127) <= 448.
+// amax = (1 + m/128) 2^(E-127) with E its exponent field; 448 = 1.75 2^8, so
+// e = E - 8, one more when m > 96 (1 + m/128 > 1.75).  Clamped to [1, 254].
+__device__ __forceinline__ int e8m0_for_amax(uint32_t amax) {
+  const int E = (int)((amax >> 7) & 0xff), m = (int)(amax & 0x7f);
+  int e = E - 8 + (m > 96 ? 1 : 0);
+  return e < 1 ? 1 : (e > 254 ? 254 : e);
+}
+
+// Quantize the 32 bf16 values of four 8-vectors (one MFMA lane's share of a
+// row's k step) to e4m3, q = fp8(x / 2^(e-127)), round to nearest even
+// (v_cvt_scalef32_pk_fp8_bf16).  The scale is shared by all lanes holding
+// the same row of the step (the lanes l ^ X1 [^ X2]): the block-scaled MFMAs
+// apply a lane's scale to 16-byte halves of other lanes of its row, so one
+// scale per (row, step) is what keeps the product exact whatever that
+// assignment is.  No value can overflow (see e8m0_for_amax).  Returns the
+// packed bytes in k order; *e8 receives the E8M0 exponent.
+template <int X1, int X2>
+__device__ __forceinline__ i32x8_t quant_fp8x32(const bf16x8* v, int* e8) {
+  uint32_t mx = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = v[i].w[j] & 0x7fff7fffu;
+      const uint32_t a = w & 0xffffu, b = w >> 16;
+      mx = a > mx ? a : mx;
+      mx = b > mx ? b : mx;
+    }
+  uint32_t o = (uint32_t)__shfl_xor((int)mx, X1, 64);
+  mx = o > mx ? o : mx;
+  if (X2) {
+    o = (uint32_t)__shfl_xor((int)mx, X2, 64);
+    mx = o > mx ? o : mx;
+  }
+  const int e = e8m0_for_amax(mx);
+  const float scale = __uint_as_float((uint32_t)e << 23);
+  i32x8_t q;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      i16x2_t r = {0, 0};
+      r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(
+          r, __builtin_bit_cast(bf16x2_t, v[i].w[2 * j]), scale, false);
+      r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(
+          r, __builtin_bit_cast(bf16x2_t, v[i].w[2 * j + 1]), scale, true);
+      q[2 * i + j] = __builtin_bit_cast(int, r);
+    }
+  *e8 = e;
+  return q;
+}
+
+// D(16x16) += A(16x128) * B(128x16), e4m3 inputs with E8M0 block scales:
+// lane l holds 32 k-values of A row (l % 16) and of B column (l % 16) (the
+// same k positions in A and B), scaled by 2^(sa - 127) and 2^(sb - 127).
+__device__ __forceinline__ f32x4_t mfma16x16x128_f8(const i32x8_t& a, int sa,
+                                                   const i32x8_t& b, int sb,
+                                                   f32x4_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa,
+                                                          0, sb);
+}
+
+// D(32x32) += A(32x64) * B(64x32), e4m3 with E8M0 block scales; lane l holds
+// 32 k-values of A row (l % 32) / B column (l % 32); D as in mfma32x32x16.
+__device__ __forceinline__ f32x16_t mfma32x32x64_f8(const i32x8_t& a, int sa,
+                                                    const i32x8_t& b, int sb,
+                                                    f32x16_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa,
+                                                         0, sb);
+}
+
 // Raw buffer access: loads at byte offsets >= `bytes` return zero without
 // touching memory, so a guarded load needs no branch (a branch around each
 // load makes the compiler wait for it at the join, serializing the loads).

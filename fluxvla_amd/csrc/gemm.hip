@@ -377,13 +377,18 @@ static bool epi_vec_ok(const GemmArgs& d) {
 // row with 16-byte accesses.  With splits > 1 the K range is split over
 // blockIdx.y and fp32 partials go to the workspace for
 // gemm_partial_reduce_kernel.
-template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE>
+template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8>
 struct TileCfg {
   static constexpr int NW = WGM * WGN, NT = 64 * NW;
   static constexpr int NB = MODE == FVX_GEMM_GEGLU ? 2 : 1;
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // WN counts both weights
   static constexpr int FM = WM / 32, FN = WN / 32;
-  static constexpr int ROWS = BM + BN;                // LDS rows per stage
+  // bf16: slabs of 64 k, one 128-byte LDS row per A and B row.  F8 (e4m3
+  // weights): slabs of 128 k, A rows split into two 128-byte half rows (k
+  // 0..63 then 64..127), B rows of 128 fp8 bytes.
+  static constexpr int BK = F8 ? 128 : 64;
+  static constexpr int AROWS = F8 ? 2 * BM : BM;
+  static constexpr int ROWS = AROWS + BN;             // LDS rows per stage
   static constexpr int STAGE_BYTES = ROWS * 128;
   static constexpr int LPW = ROWS / (8 * NW);         // loads per wave per slab
   static constexpr int WNO = WN / NB;                 // output columns per wave
@@ -403,13 +408,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE>
+template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     GemmArgs p, int m_tiles, int n_tiles, int splits, int64_t kchunk,
     int vec_ok) {
-  typedef TileCfg<BM, BN, WGM, WGN, STAGES, MODE> C;
+  typedef TileCfg<BM, BN, WGM, WGN, STAGES, MODE, F8> C;
   constexpr int NB = C::NB, WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
-  constexpr int LPW = C::LPW, WNO = C::WNO, ELD = C::ELD;
+  constexpr int LPW = C::LPW, WNO = C::WNO, ELD = C::ELD, BK = C::BK;
+  constexpr int AROWS = C::AROWS;
   __shared__ __align__(16) char smem[C::LDS_BYTES];
   __shared__ float sRow[BM];
 
@@ -428,48 +434,55 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   const int64_t m0 = (int64_t)m_tile * BM, n0 = (int64_t)n_tile * (BN / NB);
   const int64_t kb = (int64_t)split * kchunk;
   const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
-  const int nk = (int)((ke - kb + 63) / 64);
+  const int nk = (int)((ke - kb + BK - 1) / BK);
 
   // Buffer views of the tile's A rows and B rows: rows past M / N read zero.
   const int64_t a_rows = (M - m0 < BM) ? M - m0 : BM;
   const int64_t b_rows = (N - n0 < BN / NB) ? N - n0 : BN / NB;
-  const uint32_t lda2 = (uint32_t)p.lda * 2, ldb2 = (uint32_t)p.ldb * 2;
+  const uint32_t lda2 = (uint32_t)p.lda * 2, ldb2 = (uint32_t)p.ldb * (F8 ? 1 : 2);
   const i32x4_t rA =
       make_rsrc4((const bf16_t*)p.a + m0 * p.lda, (uint32_t)(a_rows * lda2));
   const i32x4_t rB0 =
-      make_rsrc4((const bf16_t*)p.b + n0 * p.ldb, (uint32_t)(b_rows * ldb2));
+      make_rsrc4((const char*)p.b + n0 * ldb2, (uint32_t)(b_rows * ldb2));
   const i32x4_t rB1 =
-      make_rsrc4((const bf16_t*)(NB == 2 ? p.b2 : p.b) + n0 * p.ldb,
+      make_rsrc4((const char*)(NB == 2 ? p.b2 : p.b) + n0 * ldb2,
                  (uint32_t)(b_rows * ldb2));
 
   // Load i of this wave fills LDS rows R0 = (wave LPW + i) 8 .. + 7 of a
-  // stage: A rows first, then BN / NB rows of each weight.
+  // stage: A rows (F8: half rows) first, then BN / NB rows of each weight.
+  // Either way a slab advances 128 bytes along a B row and 2 BK along an A
+  // row; a 16-byte chunk spans 8 k of A and 8 (F8: 16) k of B.
   const int lr = lane >> 3, lc = lane & 7;
   uint32_t voff[LPW];
-  int kmax[LPW];  // slab t of load i is in range iff 64 t < kmax[i]
+  int kmax[LPW];  // slab t of load i is in range iff BK t < kmax[i]
+  bool isa[LPW];
   i32x4_t rsel[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
     const int R0 = (wave * LPW + i) * 8, R = R0 + lr;
     const int gc = lc ^ ((R >> 1) & 7);
-    const uint32_t kofs = (uint32_t)(kb + gc * 8) * 2;
-    if (R0 < BM) {
+    isa[i] = R0 < AROWS;
+    if (R0 < AROWS) {
+      const int hk = R0 / BM;  // F8: which 64-k half of the slab
       rsel[i] = rA;
-      voff[i] = (uint32_t)R * lda2 + kofs;
+      voff[i] = (uint32_t)(R0 % BM + lr) * lda2 + (uint32_t)(kb + hk * 64 + gc * 8) * 2;
+      kmax[i] = (int)(ke - kb) - hk * 64 - gc * 8;
     } else {
       // 8-row groups never straddle the two weights' regions (BN / NB % 8 == 0)
-      const int br0 = R0 - BM;
+      const int br0 = R0 - AROWS;
+      const int kc = F8 ? 16 : 8;
       rsel[i] = br0 < BN / NB ? rB0 : rB1;
-      voff[i] = (uint32_t)(br0 % (BN / NB) + lr) * ldb2 + kofs;
+      voff[i] = (uint32_t)(br0 % (BN / NB) + lr) * ldb2 +
+                (uint32_t)(kb + gc * kc) * (F8 ? 1 : 2);
+      kmax[i] = (int)(ke - kb) - gc * kc;
     }
-    kmax[i] = (int)(ke - kb) - gc * 8;
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * LPW * 1024);
   auto issue = [&](int t, int stage) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i)
       load_lds16(rsel[i], lds0 + stage * C::STAGE_BYTES + i * 1024,
-                 64 * t < kmax[i] ? voff[i] + (uint32_t)t * 128 : kOOB);
+                 BK * t < kmax[i] ? voff[i] + (uint32_t)t * (isa[i] ? 2 * BK : 128) : kOOB);
   };
 
   f32x16_t acc[FM][FN];
@@ -486,14 +499,51 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   // LDS row of B fragment j of this wave (GEGLU: gate blocks, then up)
   auto brow = [&](int j) {
     if (NB == 2)
-      return j < FN / 2 ? BM + wn * (WN / 2) + 32 * j
-                        : BM + BN / 2 + wn * (WN / 2) + 32 * (j - FN / 2);
-    return BM + wn * WN + 32 * j;
+      return j < FN / 2 ? AROWS + wn * (WN / 2) + 32 * j
+                        : AROWS + BN / 2 + wn * (WN / 2) + 32 * (j - FN / 2);
+    return AROWS + wn * WN + 32 * j;
   };
   // rows of a fragment are (multiple of 32) + lane % 32: swizzle (lane >> 1) & 7
   const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
   auto compute = [&](int stage) {
     const char* s = smem + stage * C::STAGE_BYTES;
+    if (F8) {
+      // two 64-k steps; lane (fr, hk) takes k = 64 ks + 32 hk .. + 31: A as
+      // four bf16 chunks of half row ks (quantized here with one scale per
+      // row and step), B as two fp8 chunks
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        i32x8_t aq[FM], bq[FN];
+        int ae[FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const char* row = s + (ks * BM + wm * WM + 32 * i + fr) * 128;
+          bf16x8 av[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) av[c] = *(const bf16x8*)(row + (((4 * hk + c) ^ sw) * 16));
+#pragma unroll
+          for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
+          aq[i] = quant_fp8x32<32, 0>(av, &ae[i]);  // (row, 64-k step) scale
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const char* row = s + (brow(j) + fr) * 128;
+          const bf16x8 b0 = *(const bf16x8*)(row + (((4 * ks + 2 * hk) ^ sw) * 16));
+          const bf16x8 b1 = *(const bf16x8*)(row + (((4 * ks + 2 * hk + 1) ^ sw) * 16));
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            bq[j][x] = (int)b0.w[x];
+            bq[j][4 + x] = (int)b1.w[x];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = mfma32x32x64_f8(aq[i], ae[i], bq[j], 127, acc[i][j]);
+      }
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int cpos = ((2 * ks + hk) ^ sw) * 16;
@@ -586,6 +636,18 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
           v[x] = sv[x];
           u[x] = NB == 2 ? sv[WNO + x] : 0.f;
         }
+        if (F8) {  // per-output-channel weight scales
+          float w0[8], w1[8];
+          const bool sv8 = vec_ok && cnt == 8;
+          bl_f8(make_rsrc(p.b_scale, rec_bytes(N * 4)), (uint32_t)(nn * 4), sv8, w0);
+          bl_f8(make_rsrc(NB == 2 ? p.b2_scale : p.b_scale, rec_bytes(N * 4)),
+                (uint32_t)(nn * 4), sv8, w1);
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            v[x] *= w0[x];
+            u[x] *= w1[x];
+          }
+        }
         if (splits > 1) {
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
@@ -664,13 +726,14 @@ __device__ __forceinline__ void sc1_load8(__amdgpu_buffer_rsrc_t r, int off,
   }
 }
 
-template <int MODE>
+template <int MODE, bool F8>
 __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
                                                           int64_t kc,
                                                           int vec_ok) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
-  constexpr int W = kSkWaves, S = NB == 2 ? 2 : kSkStep;
+  // F8: one register set = one 128-k step of the fp8 MFMA (4 A blocks of 32)
+  constexpr int W = kSkWaves, S = F8 ? 4 : (NB == 2 ? 2 : kSkStep);
   __shared__ float sP[W][NB][64][16 + 1];
   __shared__ float sS[W][64];
   __shared__ int s_last;
@@ -703,7 +766,12 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
     a_ks = 64;
     a_f = (uint32_t)(16 * p.lda * 2);
   }
-  if (p.b_frag) {
+  if (F8) {
+    // fp8 fragment-major: one 2 KiB block per (16 columns, 128 k), 32 B per
+    // lane; b_ks counts 32-k steps (a block spans four)
+    b0 = (uint32_t)(((int64_t)tile * (K >> 7) * 64 + lane) * 32);
+    b_ks = 512;
+  } else if (p.b_frag) {
     b0 = (uint32_t)(((int64_t)tile * (K >> 5) * 64 + lane) * 16);
     b_ks = 64 * 16;
   } else {
@@ -726,8 +794,12 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
       const uint32_t ks = ks0 + t0 + t;
       const bool kin = kb + 32 * (t0 + t) + 8 * g < ke;
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-        rb[set][t][b] = bld(rb_rs[b], (kin && bval) ? b0 + ks * b_ks : kOOB);
+      for (int b = 0; b < NB; ++b) {
+        if (!F8)
+          rb[set][t][b] = bld(rb_rs[b], (kin && bval) ? b0 + ks * b_ks : kOOB);
+        else if (t < 2)  // the step's 32 fp8 bytes: two 16-byte halves
+          rb[set][t][b] = bld(rb_rs[b], kin ? b0 + (ks0 + t0) * b_ks + 16 * t : kOOB);
+      }
 #pragma unroll
       for (int f = 0; f < 4; ++f) {
         const bool rin = p.a_frag || f * 16 + fr < M;
@@ -742,6 +814,31 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
     for (int f = 0; f < 4; ++f) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float ss[4] = {0.f, 0.f, 0.f, 0.f};
   auto compute = [&](int set) {
+    if (F8) {
+      // lane (fr, g) holds k = 32 t + 8 g + j of row 16 f + fr: quantize the
+      // row's 128 values of the step with one power-of-two scale, one fp8
+      // MFMA per row block
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const bf16x8 av[4] = {ra[set][0][f], ra[set][1][f], ra[set][2][f], ra[set][3][f]};
+        if (p.rownorm)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) ss[f] += sumsq8(av[t]);
+        int e8;  // one scale per (row, 128-k step): lanes fr + 16 g, g = 0..3
+        const i32x8_t aq = quant_fp8x32<16, 32>(av, &e8);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          i32x8_t bq;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            bq[i] = (int)rb[set][0][b].w[i];
+            bq[4 + i] = (int)rb[set][1][b].w[i];
+          }
+          acc[b][f] = mfma16x16x128_f8(aq, e8, bq, 127, acc[b][f]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < S; ++t)
 #pragma unroll
@@ -763,6 +860,12 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
   const bool vec = vec_ok && cnt == 8;
   EpiIn in;
   if (mine) epi_load<MODE>(p, row, ncol, vec, cnt, in);
+  float wsc[8], wsc2[8];  // fp8 per-channel weight scales of the 8 columns
+  if (F8) {
+    bl_f8(make_rsrc(p.b_scale, rec_bytes(N * 4)), (uint32_t)(ncol * 4), vec, wsc);
+    bl_f8(make_rsrc(NB == 2 ? p.b2_scale : p.b_scale, rec_bytes(N * 4)), (uint32_t)(ncol * 4),
+          vec, wsc2);
+  }
   for (int t0 = 0; t0 < nst; t0 += 2 * S) {
     if (t0 + S < nst) load(t0 + S, 1);
     compute(0);
@@ -861,6 +964,13 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
   }
   if (!mine) return;
   const float r = p.rownorm ? rsqrtf(rsum / (float)K + p.rownorm_eps) : 1.f;
+  if (F8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] *= wsc[e];
+      u[e] *= wsc2[e];
+    }
+  }
   epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in);
 }
 
@@ -928,11 +1038,11 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
   SkinnyPlan s;
   const int nb = d.mode == FVX_GEMM_GEGLU ? 2 : 1;
   s.n_tiles = (int)((d.n + 15) / 16);
-  const int64_t unit = 32 * kSkWaves;
+  const int64_t unit = (d.b_fp8 ? 128 : 32) * kSkWaves;
   const int64_t max_splits = (d.k + unit - 1) / unit;
   int64_t sp = d.split_k;
   if (sp <= 0) {
-    const int64_t bytes = (64 + 16 * nb) * d.k * 2;
+    const int64_t bytes = (64 * 2 + 16 * nb * (d.b_fp8 ? 1 : 2)) * d.k;
     sp = (bytes + 400 * 1024 - 1) / (400 * 1024);
     const int64_t cap = 256 / s.n_tiles;
     if (sp > cap) sp = cap;
@@ -954,10 +1064,11 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
 // counter area and its partial offsets fit 31 bits; anything else is tiled.
 static bool use_skinny(const GemmArgs& d) {
   if (d.m > 64) return false;
+  if (d.b_fp8 && !d.b_frag) return false;  // fp8 skinny reads fragment-major B
   const SkinnyPlan s = plan_skinny(d);
   // operand byte offsets are 32-bit
   const int64_t a_bytes = d.a_frag ? (d.k / 32) * 4 * 1024 : 64 * d.lda * 2;
-  const int64_t b_bytes = d.b_frag ? (int64_t)s.n_tiles * 16 * d.k * 2
+  const int64_t b_bytes = d.b_frag ? (int64_t)s.n_tiles * 16 * d.k * (d.b_fp8 ? 1 : 2)
                                    : (int64_t)s.n_tiles * 16 * d.ldb * 2;
   return s.n_tiles <= kMaxSkinnyTiles && s.ws_bytes < ((int64_t)1 << 31) &&
          a_bytes < ((int64_t)1 << 31) && b_bytes < ((int64_t)1 << 31);
@@ -1011,6 +1122,15 @@ static int validate(const GemmArgs& d) {
       FVX_REQUIRE(d.xt, FVX_ERR_NULL, "gemm(euler): xt required");
       break;
   }
+  if (d.b_fp8) {
+    FVX_REQUIRE(d.b_scale && (d.mode != FVX_GEMM_GEGLU || d.b2_scale), FVX_ERR_NULL,
+                "gemm(fp8): b_scale (and b2_scale for GEGLU) required");
+    FVX_REQUIRE(aligned16(d.b_scale) && aligned16(d.b2_scale), FVX_ERR_ALIGN,
+                "gemm(fp8): weight scales must be 16B aligned");
+    FVX_REQUIRE(d.k % 128 == 0 && d.ldb % 16 == 0, FVX_ERR_SHAPE,
+                "gemm(fp8): needs k %% 128 == 0 and ldb %% 16 == 0 (k=%lld ldb=%lld)",
+                (long long)d.k, (long long)d.ldb);
+  }
   if (d.a_frag || d.b_frag || d.c_frag) {
     FVX_REQUIRE(d.m <= 64 && use_skinny(d), FVX_ERR_ARG,
                 "gemm: fragment-major operands need m <= 64 (m=%lld)",
@@ -1062,6 +1182,8 @@ static const int kTileBM[] = {128, 256, 64};
 static const int kTileBN[] = {128, 256, 128};
 constexpr int kTileCfgs = 3;
 
+static int tile_bm(int cfg, int fp8) { return cfg == 1 && fp8 ? 128 : kTileBM[cfg]; }
+
 struct TilePlan {
   int cfg, splits;
 };
@@ -1074,7 +1196,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   TilePlan t;
   const bool gg = d.mode == FVX_GEMM_GEGLU;
   t.cfg = (gg && ((d.m + 255) / 256) * ((d.n + 127) / 128) >= 256) ? 1 : 2;
-  const int64_t bm = kTileBM[t.cfg], bn = kTileBN[t.cfg] / (gg ? 2 : 1);
+  const int64_t bm = tile_bm(t.cfg, d.b_fp8), bn = kTileBN[t.cfg] / (gg ? 2 : 1);
   const int64_t tiles = ((d.m + bm - 1) / bm) * ((d.n + bn - 1) / bn);
   t.splits = 1;
   if (d.split_k > 0) {
@@ -1089,12 +1211,13 @@ static TilePlan plan_tile(const GemmArgs& d) {
 static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   FVX_REQUIRE(cfg >= 0 && cfg < kTileCfgs, FVX_ERR_ARG, "gemm: bad tile config %d", cfg);
   const bool gg = d.mode == FVX_GEMM_GEGLU;
-  const int bm = kTileBM[cfg], bn = kTileBN[cfg] / (gg ? 2 : 1);
+  const int bm = tile_bm(cfg, d.b_fp8), bn = kTileBN[cfg] / (gg ? 2 : 1);
   const int m_tiles = (int)((d.m + bm - 1) / bm);
   const int n_tiles = (int)((d.n + bn - 1) / bn);
   if (splits < 1) splits = 1;
+  const int64_t bk = d.b_fp8 ? 128 : 64;
   int64_t kchunk = (d.k + splits - 1) / splits;
-  kchunk = (kchunk + 63) / 64 * 64;
+  kchunk = (kchunk + bk - 1) / bk * bk;
   splits = (int)((d.k + kchunk - 1) / kchunk);
   const int nbm = gg ? 2 : 1;
   const int64_t need = splits > 1 ? kCounterBytes + ((int64_t)nbm * splits * d.m * d.n +
@@ -1112,14 +1235,22 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
               "gemm: workspace must be 16B aligned");
   const int vec_ok = epi_vec_ok(d) ? 1 : 0;
   dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
-#define LT(BM_, BN_, WGM_, WGN_, ST_, MODE)                                       \
-  hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE>), grid,   \
-                     dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits,   \
+#define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_)                                   \
+  hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_>), grid,  \
+                     dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits,      \
                      kchunk, vec_ok)
-#define LCFG(MODE)                                \
-  if (cfg == 0) LT(128, 128, 2, 2, 2, MODE);      \
-  else if (cfg == 1) LT(256, 256, 2, 4, 2, MODE); \
-  else LT(64, 128, 2, 2, 2, MODE);
+  // fp8 tiles hold 128-k slabs (bf16 A rows of 256 bytes): config 1 becomes
+  // 128 x 256 to stay within the LDS
+#define LCFG(MODE)                                                   \
+  if (d.b_fp8) {                                                     \
+    if (cfg == 0) LT(128, 128, 2, 2, 2, MODE, true);                 \
+    else if (cfg == 1) LT(128, 256, 2, 4, 2, MODE, true);            \
+    else LT(64, 128, 2, 2, 2, MODE, true);                           \
+  } else {                                                           \
+    if (cfg == 0) LT(128, 128, 2, 2, 2, MODE, false);                \
+    else if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false);           \
+    else LT(64, 128, 2, 2, 2, MODE, false);                          \
+  }
   FVX_MODE_DISPATCH(d.mode, LCFG)
 #undef LCFG
 #undef LT
@@ -1169,9 +1300,13 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
                 "gemm: workspace must be 16B aligned");
     dim3 grid((unsigned)sp.n_tiles, (unsigned)sp.splits);
     const int vec_ok = epi_vec_ok(d) ? 1 : 0;
-#define L(MODE)                                                          \
-  hipLaunchKernelGGL(gemm_skinny_kernel<MODE>, grid, dim3(64 * kSkWaves), \
-                     0, s, d, sp.splits, sp.kc, vec_ok)
+#define L(MODE)                                                                 \
+  if (d.b_fp8)                                                                   \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true>), grid, dim3(64 * kSkWaves), \
+                       0, s, d, sp.splits, sp.kc, vec_ok);                       \
+  else                                                                           \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false>), grid, dim3(64 * kSkWaves), \
+                       0, s, d, sp.splits, sp.kc, vec_ok)
     FVX_MODE_DISPATCH(d.mode, L)
 #undef L
     return launch_status("gemm(skinny)");

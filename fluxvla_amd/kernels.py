@@ -171,6 +171,52 @@ class FragB:
         return FragB(buf, n, k)
 
 
+class Fp8Weight:
+    """An nn.Linear weight [n, k] quantized to OCP e4m3fn (max 448) with one
+    fp32 scale per output channel: W[j] ~= scale[j] * e4m3(data[j]),
+    scale[j] = max_i |W[j, i]| / 448.  ``data`` is uint8, row-major
+    ([n, k], ldb = k bytes) or, with ``frag``, in the fp8 fragment-major
+    layout of fvx_gemm_desc (one 16 x 128 MFMA operand per 2 KiB; needs
+    n % 16 == 0 and k % 128 == 0) for the M <= 64 skinny GEMM."""
+
+    def __init__(self, data, scale, n, k, frag=False):
+        self.data, self.scale, self.n, self.k, self.frag = data, scale, n, k, frag
+
+    @staticmethod
+    def quantize(w):
+        n, k = w.shape
+        wf = w.float()
+        s = (wf.abs().amax(1) / 448.0).clamp_min(torch.finfo(torch.float32).tiny)
+        q = (wf / s[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+        return Fp8Weight(q.contiguous(), s.contiguous(), n, k)
+
+    def dequantize(self):
+        """fp32 [n, k] (row-major weights only)."""
+        if self.frag:
+            raise ValueError('dequantize needs the row-major layout')
+        return (self.data.view(torch.float8_e4m3fn).float() *
+                self.scale[:, None])
+
+    def rows(self, start, end=None):
+        """Output channels [start, end) (row-major weights only)."""
+        if self.frag:
+            raise ValueError('rows() needs the row-major layout')
+        end = self.n if end is None else end
+        return Fp8Weight(self.data[start:end], self.scale[start:end],
+                         end - start, self.k)
+
+    def pack_frag(self):
+        """Fragment-major copy: byte (n, k) of block (n/16, k/128) at lane
+        16 g + n%16, position 8 t + j, where k%128 = 32 t + 8 g + j."""
+        n, k = self.n, self.k
+        if n % 16 or k % 128:
+            raise ValueError(f'fp8 fragment-major weights need n % 16 == 0 '
+                             f'and k % 128 == 0, got {(n, k)}')
+        buf = (self.data.view(n // 16, 16, k // 128, 4, 4, 8)
+               .permute(0, 2, 4, 1, 3, 5).contiguous().view(-1))
+        return Fp8Weight(buf, self.scale, n, k, frag=True)
+
+
 def pack_frag_a_ref(a):
     """Torch restatement of the FragA layout (tests): [m <= 64, k] ->
     64 * k elements; rows >= m are zero."""
@@ -211,6 +257,13 @@ def _gemm_desc(a, w):
         _check(w.buf, 'weight')
         n, ldb, kw = w.n, w.k, w.k
         d.b, d.b_frag = w.buf.data_ptr(), 1
+    elif isinstance(w, Fp8Weight):
+        _check(w.data, 'weight', dtype=torch.uint8, contiguous=not w.frag)
+        _check(w.scale, 'weight scale', dtype=torch.float32)
+        n, kw = w.n, w.k
+        ldb = w.k if w.frag else w.data.stride(0)
+        d.b, d.b_frag, d.b_fp8 = w.data.data_ptr(), int(w.frag), 1
+        d.b_scale = w.scale.data_ptr()
     else:
         _check(w, 'weight', contiguous=False)
         n, ldb = _rows_ld(w, 'weight')
@@ -296,7 +349,14 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
                c_frag=None):
     """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T)."""
     d = _gemm_desc(a, gate_w)
-    if isinstance(gate_w, FragB):
+    if isinstance(gate_w, Fp8Weight):
+        if (not isinstance(up_w, Fp8Weight) or up_w.frag != gate_w.frag or
+                (up_w.n, up_w.k) != (gate_w.n, gate_w.k) or
+                (not up_w.frag and up_w.data.stride() != gate_w.data.stride())):
+            raise ValueError('up_w must be an Fp8Weight laid out like gate_w')
+        _check(up_w.scale, 'up_w scale', dtype=torch.float32)
+        d.b2, d.b2_scale = up_w.data.data_ptr(), up_w.scale.data_ptr()
+    elif isinstance(gate_w, FragB):
         if not isinstance(up_w, FragB) or (up_w.n, up_w.k) != (gate_w.n, gate_w.k):
             raise ValueError('up_w must be a FragB shaped like gate_w')
         _check(up_w.buf, 'up_w')

@@ -128,6 +128,22 @@ def prepare_gemma(sd, cfg: PI0Config, role, device):
     return _to(w, device)
 
 
+LINEARS = ('qkv_w', 'o_w', 'gate_w', 'up_w', 'down_w')
+
+
+def quantize_linears(w):
+    """fp8 variant (PI0.5 config 5): every linear layer of a Gemma tower
+    (Q|K|V, O, gate, up, down) as OCP e4m3fn with one fp32 scale per output
+    channel, s = max|W[j]| / 448, taken after the (1 + w) fold and the Q/K
+    interleave, so the quantized weight is exactly the one the GEMM applies.
+    The reference has no fp8 path; the activations stay bf16 and the GEMM
+    kernels quantize them per row and k step on the fly."""
+    for L in w['layers']:
+        for nm in LINEARS:
+            L[nm] = K.Fp8Weight.quantize(L[nm])
+    return w
+
+
 def prepare_projector(sd, prefix, device):
     """LinearProjectorInference.prepare_triton counterpart
     (linear_projector_inference.py:8-14): weight [out, in] and bias."""
@@ -227,11 +243,15 @@ class PI0Inference:
     """
 
     def __init__(self, cfg: PI0Config, state_dict, device='cuda',
-                 max_batch=1, use_graph=True):
+                 max_batch=1, use_graph=True, weight_dtype='bf16'):
+        if weight_dtype not in ('bf16', 'fp8'):
+            raise ValueError(f"weight_dtype must be 'bf16' or 'fp8', got "
+                             f'{weight_dtype!r}')
         self.cfg = cfg
         self.device = torch.device(device)
         self.use_graph = use_graph
         self.max_batch = max_batch
+        self.weight_dtype = weight_dtype
         K.workspace(self.device)
         K.workspace(self.device, 'attn')
         self.prepare_triton_inference(state_dict)
@@ -245,6 +265,9 @@ class PI0Inference:
         self.vis = prepare_siglip(sd, cfg, dev)
         self.llm = prepare_gemma(sd, cfg, 'llm', dev)
         self.exp = prepare_gemma(sd, cfg, 'expert', dev)
+        if self.weight_dtype == 'fp8':
+            quantize_linears(self.llm)
+            quantize_linears(self.exp)
         self.proj = prepare_projector(sd, 'projector', dev)
         self.act_in = prepare_projector(sd, 'action_in_proj', dev)
         out = prepare_projector(sd, 'action_out_proj', dev)
@@ -292,10 +315,12 @@ class PI0Inference:
         (bs=1) skinny GEMMs: every weight load becomes one coalesced 1 KiB
         block per wave.  The row-major originals stay for batched calls."""
         F = K.FragB.pack
+
+        def frag(w):
+            return w.pack_frag() if isinstance(w, K.Fp8Weight) else F(w)
         self.exp_f = []
         for L in self.exp['layers']:
-            self.exp_f.append({nm: F(L[nm]) for nm in
-                               ('qkv_w', 'o_w', 'gate_w', 'up_w', 'down_w')})
+            self.exp_f.append({nm: frag(L[nm]) for nm in LINEARS})
         self.act_out_f = F(self.act_out['w'])
         if self.cfg.pi05:
             self.act_in_f = F(self.act_in['w'])
@@ -410,7 +435,10 @@ class PI0Inference:
         for i, L in enumerate(W['layers']):
             kc, vc = b['kc'][i], b['vc'][i]
             last = i == n - 1
-            wqkv = L['qkv_w'][cfg.heads * D:] if last else L['qkv_w']
+            wqkv = L['qkv_w']
+            if last:
+                wqkv = (wqkv.rows(cfg.heads * D) if isinstance(wqkv, K.Fp8Weight)
+                        else wqkv[cfg.heads * D:])
             K.gemm_qkv_rope(x, wqkv, self.rope, b['pos_pre'],
                             b['pre_q'].view(B * S, -1),
                             kc.view(B * T, D), vc, 0 if last else cfg.heads,
@@ -478,6 +506,8 @@ class PI0Inference:
 
     def _expert_layer_pi05(self, b, B, i, L, step):
         cfg = self.cfg
+        if self._frag_ok(B):
+            L = self.exp_f[i]  # fragment-major weights for the skinny GEMMs
         S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
         T = self.kv_len
         x = b['ex_x'].view(B * Ss, hid)

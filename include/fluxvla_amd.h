@@ -118,6 +118,21 @@ typedef struct fvx_gemm_desc {
    *           as the A operand of the next skinny GEMM. */
   int32_t a_frag, b_frag;
   void* c_frag;
+  /* fp8 weights (PI0.5 quantized variant; no counterpart in the reference,
+   * which has no fp8 path): b (and b2) hold OCP e4m3fn bytes with one fp32
+   * scale per output channel, W[n][k] = b_scale[n] * e4m3(b[n][k]).  The
+   * activations stay bf16 in memory; the kernels quantize each 32-wide k
+   * block of an A row to e4m3 with its own power-of-two scale on the fly and
+   * run the block-scaled fp8 MFMA.  ldb counts bytes.  K % 128 == 0.
+   *   b_frag with b_fp8: element (n, k) at byte
+   *     ((n/16) * (K/128) + k/128) * 2048 + ((k%128)/8 % 4 * 16 + n%16) * 32
+   *     + (k%128)/32 * 8 + k%8
+   *   (one 16x128 MFMA operand per contiguous 2 KiB; lane (n%16, g) holds
+   *   k = 32t + 8g + j, t = 0..3, j = 0..7, the k positions the fragment-major
+   *   A gives that lane). */
+  int32_t b_fp8;
+  const float* b_scale;            /* [N] */
+  const float* b2_scale;           /* [N], GEGLU up weight */
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */

@@ -1,0 +1,189 @@
+"""fp8 (e4m3) weight GEMMs: the PI0.5 quantized-weight variant.
+
+The reference has no fp8 path, so the kernels are pinned two ways:
+
+* exactly, against a float64 restatement of what they compute: the weight
+  dequantized from its e4m3 bytes and per-channel scale, and the A values of
+  each row and MFMA k step (64 values in the tiled kernel, 128 in the skinny
+  one) quantized to e4m3 under one power-of-two scale 2^(e - 127),
+  e = E - 8 + (mantissa > 96) from the block maximum's bf16 exponent E and
+  7-bit mantissa (the smallest power of two that keeps the block within
+  448).  The bar is the bf16 op bar, max relative error <= 1e-2 (what
+  remains is fp32 accumulation and the bf16 output rounding);
+* by the rounding bound of e4m3 against the unquantized bf16 activations:
+  |out - a @ Wq^T| <= 2^-4 (|a| @ |Wq|^T) elementwise (3 mantissa bits give a
+  relative rounding error of at most 2^-4 for every quantized value), which
+  a wrong block layout or scale convention would violate by orders of
+  magnitude.
+
+One scale per (row, step) rather than per 32 values: the block-scaled MFMAs
+apply a lane's scale to 16-byte halves held by other lanes of the same row
+(measured on gfx950), so a scale shared by the row's lanes is the choice that
+makes the product exact without depending on that assignment.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2
+
+
+def rel_err(out, ref):
+    out = out.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return ((out - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+def randn(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(torch.bfloat16)
+
+
+@pytest.fixture(scope='module')
+def K():
+    from fluxvla_amd import kernels
+    kernels._lib.load()
+    return kernels
+
+
+def block_ids(k, skinny):
+    kk = torch.arange(k)
+    return kk // 128 if skinny else kk // 64
+
+
+def quant_a_ref(a, skinny):
+    """float64 values the kernel multiplies: a (bf16 [m, k]) with every
+    block (row, k step) quantized to e4m3 under its power-of-two scale."""
+    m, k = a.shape
+    bid = block_ids(k, skinny)
+    nb = int(bid.max()) + 1
+    bits = a.view(torch.int16).int() & 0x7FFF           # |a| bf16 bits
+    amax = torch.zeros(m, nb, dtype=torch.int32)
+    amax.scatter_reduce_(1, bid.expand(m, k), bits, 'amax')
+    E, mant = (amax >> 7) & 0xFF, amax & 0x7F
+    e = (E - 8 + (mant > 96).int()).clamp(1, 254)
+    scale = torch.pow(2.0, (e - 127).double())          # [m, nb]
+    sc = scale.gather(1, bid.expand(m, k))
+    q = (a.double() / sc).float().to(torch.float8_e4m3fn).double()
+    return q * sc
+
+
+def fp8_weight(K, w, cuda, frag=False):
+    fw = K.Fp8Weight.quantize(w.to(cuda))
+    wq = fw.dequantize().double().cpu()
+    return (fw.pack_frag() if frag else fw), wq
+
+
+def check_bound(out, a, wq, ref_extra=None):
+    """e4m3 rounding bound against the unquantized activations."""
+    exact = a.double() @ wq.t()
+    bound = (a.double().abs() @ wq.abs().t()) * 2.0**-4
+    out = out.detach().double().cpu()
+    if ref_extra is not None:
+        out = out - ref_extra
+    # 1e-2 of the output scale covers the bf16 rounding of the stored result
+    slack = 1e-2 * exact.abs().max()
+    assert ((out - exact).abs() <= bound + slack).all()
+
+
+@pytest.mark.parametrize('m,n,k', [(300, 384, 512), (816, 640, 2048),
+                                   (129, 256, 128)])
+def test_fp8_gemm_tile(K, cuda, m, n, k):
+    announce(f'fp8 gemm tile m={m} n={n} k={k}')
+    a = randn((m, k), 100, std=1.5)
+    fw, wq = fp8_weight(K, randn((n, k), 101, std=0.02), cuda)
+    bias = randn((n,), 102, std=0.5)
+    res = randn((m, n), 103)
+    out = K.gemm(a.to(cuda), fw, bias=bias.to(cuda), residual=res.to(cuda))
+    extra = bias.double() + res.double()
+    ref = quant_a_ref(a, skinny=False) @ wq.t() + extra
+    assert rel_err(out, ref) <= REL_TOL
+    check_bound(out, a, wq, ref_extra=extra)
+
+
+@pytest.mark.parametrize('m,n,k', [(51, 2560, 1024), (50, 1024, 2048),
+                                   (51, 1024, 4096), (1, 256, 128)])
+def test_fp8_gemm_skinny_frag(K, cuda, m, n, k):
+    announce(f'fp8 gemm skinny m={m} n={n} k={k}')
+    a = randn((m, k), 110, std=1.5)
+    fw, wq = fp8_weight(K, randn((n, k), 111, std=0.02), cuda, frag=True)
+    af = K.pack_frag(a.to(cuda), K.FragA.empty(k, cuda).rows(m))
+    res = randn((m, n), 112)
+    out = K.gemm(af, fw, residual=res.to(cuda))
+    ref = quant_a_ref(a, skinny=True) @ wq.t() + res.double()
+    assert rel_err(out, ref) <= REL_TOL
+    check_bound(out, a, wq, ref_extra=res.double())
+
+
+@pytest.mark.parametrize('m,skinny', [(51, True), (200, False)])
+def test_fp8_gemm_geglu_rownorm(K, cuda, m, skinny):
+    announce(f'fp8 gemm geglu rownorm m={m} skinny={skinny}')
+    n, k = 512, 1024
+    a = randn((m, k), 120, std=2.0)
+    gw, gq = fp8_weight(K, randn((n, k), 121, std=0.02), cuda, frag=skinny)
+    uw, uq = fp8_weight(K, randn((n, k), 122, std=0.02), cuda, frag=skinny)
+    ad = a.to(cuda)
+    if skinny:
+        ad = K.pack_frag(ad, K.FragA.empty(k, cuda).rows(m))
+    out = K.gemm_geglu(ad, gw, uw, rownorm_eps=1e-6)
+    aq = quant_a_ref(a, skinny=skinny)
+    r = torch.rsqrt(a.double().pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = F.gelu((aq @ gq.t()) * r, approximate='tanh') * ((aq @ uq.t()) * r)
+    assert rel_err(out, ref) <= REL_TOL
+
+
+def test_fp8_quantization_edge_blocks(K, cuda):
+    """Blocks at the scale boundaries: a block maximum with mantissa 96 and
+    97 (exactly 448 2^s and just above), all-zero rows, tiny and huge
+    magnitudes; the restatement must agree to fp32 accumulation."""
+    announce('fp8 gemm edge blocks')
+    m, n, k = 96, 128, 256
+    a = randn((m, k), 130)
+    a[0] = 0.0
+    a[1, :32] = 1.75                    # 1.75 = 1 + 96/128: e = E - 8
+    a[2, :32] = 1.7578125               # 1 + 97/128: e = E - 7
+    a[3] = randn((k,), 131) * 1e-30
+    a[4] = randn((k,), 132) * 1e30
+    a[5, 5] = 448.0
+    fw, wq = fp8_weight(K, randn((n, k), 133, std=0.05), cuda)
+    out = K.gemm(a.to(cuda), fw, out_f32=True)
+    aq = quant_a_ref(a, skinny=False)
+    ref = aq @ wq.t()
+    mass = aq.abs() @ wq.abs().t()      # sum of |products| per output
+    got = out.double().cpu()
+    # fp32 output, each row against its own scale.  The fp8 MFMA adds a
+    # step's products at a precision set by the largest of them: next to the
+    # 448 of row 5 the others lose low-order bits (measured ~1e-4 of the
+    # row's mass), far below any layout or scale mistake (a factor of 2).
+    for row in range(m):
+        scale = mass[row].max().item()
+        if scale == 0.0:
+            assert got[row].abs().max().item() == 0.0
+        else:
+            assert (got[row] - ref[row]).abs().max().item() <= 1e-3 * scale
+
+
+def test_fp8_weight_quantization_and_layout(K, cuda):
+    """Fp8Weight: per-channel scale = max|row| / 448 (the largest entry of
+    every row maps to 448 exactly), dequantization error within e4m3's
+    half-ulp, and the fragment-major packing is a permutation of the bytes
+    placing (n, k) where fvx_gemm_desc documents it."""
+    announce('fp8 weight quantization and packing')
+    w = randn((64, 256), 140, std=0.03)
+    fw = K.Fp8Weight.quantize(w.to(cuda))
+    assert torch.allclose(fw.scale.cpu(), w.float().abs().amax(1) / 448.0)
+    wd = fw.dequantize().cpu()
+    assert ((wd - w.float()).abs() <= 2.0**-4 * w.float().abs() +
+            fw.scale.cpu()[:, None] * 2.0**-10).all()
+    q = fw.data.cpu()
+    assert (q.view(torch.float8_e4m3fn).float().abs().amax(1) == 448.0).all()
+    fb = fw.pack_frag().data.cpu()
+    n, kk = torch.meshgrid(torch.arange(64), torch.arange(256), indexing='ij')
+    r = kk % 128
+    pos = (((n // 16) * 2 + kk // 128) * 2048 + ((r // 8) % 4 * 16 + n % 16) * 32
+           + (r // 32) * 8 + kk % 8)
+    assert torch.equal(fb[pos.reshape(-1)].view(64, 256), q)

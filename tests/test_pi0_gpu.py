@@ -125,3 +125,77 @@ def test_eager_equals_graph(cuda):
         a2 = g.predict_action(*args, noise=inp['noise'].to(cuda))
         assert torch.equal(a, a2)
         assert torch.equal(a, c)
+
+
+# ---------------------------------------------------------------------------
+# fp8 e4m3 weights (PI0.5 quantized variant)
+# ---------------------------------------------------------------------------
+FP8_CHUNK_ATOL = 5e-2
+
+
+def dequantized_state_dict(sd, cfg, m):
+    """The state dict whose fp32 forward is the model the fp8 pipeline runs:
+    every quantized linear replaced by its dequantized weight (scale *
+    e4m3 bytes, read back from the GPU model), with the preparation's
+    (1 + w) fold and Q/K interleave undone, so the oracle's own norms and
+    RoPE apply to it unchanged."""
+    from fluxvla_amd.pi0_inference import interleave_rows
+    H, D = cfg.heads, cfg.head_dim
+    inv = torch.argsort(interleave_rows(D))
+    out = dict(sd)
+    for role, prefix, W in (('llm', 'llm_backbone', m.llm),
+                            ('expert', 'llm_expert', m.exp)):
+        adarms = role == 'expert' and cfg.pi05
+        for i, L in enumerate(W['layers']):
+            pre = f'{prefix}.layers.{i}'
+            dq = {nm: L[nm].dequantize().cpu() for nm in
+                  ('qkv_w', 'o_w', 'gate_w', 'up_w', 'down_w')}
+            qkv = dq['qkv_w']
+            wq = qkv[:H * D].view(H, D, -1)[:, inv].reshape(H * D, -1)
+            wk, wv = qkv[H * D:H * D + D][inv], qkv[H * D + D:]
+            wg, wu = dq['gate_w'], dq['up_w']
+            if not adarms:
+                s_in = 1.0 + sd[f'{pre}.input_layernorm.weight'].float()
+                s_post = 1.0 + sd[f'{pre}.post_attention_layernorm.weight'].float()
+                wq, wk, wv = wq / s_in, wk / s_in, wv / s_in
+                wg, wu = wg / s_post, wu / s_post
+            out[f'{pre}.self_attn.q_proj.weight'] = wq
+            out[f'{pre}.self_attn.k_proj.weight'] = wk
+            out[f'{pre}.self_attn.v_proj.weight'] = wv
+            out[f'{pre}.self_attn.o_proj.weight'] = dq['o_w']
+            out[f'{pre}.mlp.gate_proj.weight'] = wg
+            out[f'{pre}.mlp.up_proj.weight'] = wu
+            out[f'{pre}.mlp.down_proj.weight'] = dq['down_w']
+    return out
+
+
+@pytest.mark.parametrize('pi05', [True, False])
+def test_fp8_chunk_matches_oracle(cuda, pi05):
+    """fp8 weights in every Gemma-2B and action-expert linear layer: the
+    chunk within 5e-2 of the fp32 oracle run with the dequantized weights
+    (the bar the north star sets for fp8 weights), at bs 1 (skinny
+    fragment-major GEMMs) and 2 (tiled)."""
+    from fluxvla_amd.pi0_inference import PI0Inference
+    cfg = tiny(pi05=pi05)
+    sd = make_state_dict(cfg, seed=0)
+    m = PI0Inference(cfg, sd, device='cuda', max_batch=2, weight_dtype='fp8')
+    sdq = dequantized_state_dict(sd, cfg, m)
+    for batch in (1, 2):
+        announce(f'fp8 chunk pi05={pi05} batch={batch}')
+        inp = make_inputs(cfg, batch=batch, seed=13)
+        ref = O.predict_action(sdq, cfg, inp['images'], inp['lang_tokens'],
+                               inp['states'], inp['img_masks'],
+                               inp['lang_masks'], inp['noise'])
+        got = m.predict_action(inp['images'].to(cuda),
+                               inp['lang_tokens'].to(cuda),
+                               inp['states'].to(cuda),
+                               inp['img_masks'].to(cuda),
+                               inp['lang_masks'].to(cuda),
+                               noise=inp['noise'].to(cuda)).cpu()
+        err = (got - ref).abs().max().item()
+        ref_bf16 = O.predict_action(sd, cfg, inp['images'], inp['lang_tokens'],
+                                    inp['states'], inp['img_masks'],
+                                    inp['lang_masks'], inp['noise'])
+        print(f'fp8 chunk max abs err {err:.3e} vs dequantized-weight oracle, '
+              f'{(got - ref_bf16).abs().max().item():.3e} vs bf16-weight oracle')
+        assert err <= FP8_CHUNK_ATOL
