@@ -338,6 +338,89 @@ def cpu_baseline(sd_gpu, cfg, inp, gpu_out):
     }, err
 
 
+def time_chunks(model, cfg, batch, seed, warmup=2, steps=5):
+    """Median HIP-event ms of ``steps`` graph-replayed chunks at ``batch``
+    (inputs staged in HBM first, as for the headline figure)."""
+    import torch
+
+    from fluxvla_amd.weights import make_inputs
+    dev = model.device
+    inp = {k: v.to(dev) for k, v in make_inputs(cfg, batch=batch,
+                                                seed=seed).items()}
+
+    def step():
+        return model.predict_action(inp['images'], inp['lang_tokens'],
+                                    inp['states'], inp['img_masks'],
+                                    inp['lang_masks'], noise=inp['noise'])
+    for _ in range(warmup):
+        out = step()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(steps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = step()
+        e1.record()
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1))
+    return sorted(per)[len(per) // 2], out, inp
+
+
+def other_configs(pi0_model, dev, parity=True):
+    """BASELINE configs 4 (PI0 at bs 8) and 5 (PI0.5 with fp8 e4m3 weights
+    in every Gemma-2B and expert linear, bs 1 / 8 / 32), plus PI0.5 bf16 at
+    bs 1 for reference.  Each: ms per chunk (median of 5 graph replays) and
+    actions/s.  With ``parity``, the full-size fp8 PI0.5 bs=1 chunk against
+    the CPU oracle run on the dequantized weights (bar 5e-2)."""
+    import torch
+
+    from fluxvla_amd.config import PI0, PI05
+    from fluxvla_amd.pi0_inference import PI0Inference
+    from fluxvla_amd.weights import make_state_dict
+    rows = []
+
+    def row(name, model_name, weights, batch, ms, cfg):
+        r = {'config': name, 'model': model_name, 'weights': weights,
+             'batch': batch, 'ms_per_chunk': round(ms, 3),
+             'actions_per_s': round(batch * cfg.n_action_steps / ms * 1e3, 1)}
+        log(f'  {name} {model_name} {weights} bs={batch}: {ms:.3f} ms/chunk')
+        rows.append(r)
+
+    ms, _, _ = time_chunks(pi0_model, PI0, 8, seed=21)
+    row('C4', 'PI0', 'bf16', 8, ms, PI0)
+    sd5 = make_state_dict(PI05, seed=0, device=dev)
+    ref = PI0Inference(PI05, sd5, device=dev, max_batch=1)
+    ms, _, _ = time_chunks(ref, PI05, 1, seed=22)
+    row('C5-ref', 'PI0.5', 'bf16', 1, ms, PI05)
+    del ref
+    torch.cuda.empty_cache()
+    fp8 = PI0Inference(PI05, sd5, device=dev, max_batch=32, weight_dtype='fp8')
+    parity_res = None
+    for batch in (1, 8, 32):
+        ms, out, inp = time_chunks(fp8, PI05, batch, seed=23)
+        row('C5', 'PI0.5', 'fp8_e4m3', batch, ms, PI05)
+        if batch == 1 and parity:
+            from oracle import pi0_oracle
+            torch.set_num_threads(len(os.sched_getaffinity(0)))
+            sdq = fp8.dequantized_state_dict({k: v.cpu() for k, v in sd5.items()})
+            cin = {k: v.cpu() for k, v in inp.items()}
+            t0 = time.perf_counter()
+            r = pi0_oracle.predict_action(sdq, PI05, cin['images'],
+                                          cin['lang_tokens'], cin['states'],
+                                          cin['img_masks'], cin['lang_masks'],
+                                          cin['noise'])
+            err = (out.cpu() - r).abs().max().item()
+            log(f'  C5 fp8 bs=1 chunk vs CPU oracle (dequantized weights): '
+                f'max abs err {err:.3e} ({time.perf_counter() - t0:.1f} s CPU)')
+            parity_res = {'chunk_max_abs_err_vs_cpu_oracle_dequantized': err,
+                          'tolerance': 5e-2}
+            del sdq
+    del fp8, sd5
+    torch.cuda.empty_cache()
+    return rows, parity_res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -349,6 +432,9 @@ def main():
     ap.add_argument('--no-table', action='store_true',
                     help='skip the per-kernel roofline table and the C2/C3 '
                     'phase times')
+    ap.add_argument('--no-configs', action='store_true',
+                    help='skip the other BASELINE configs (PI0 bs 8, PI0.5 '
+                    'fp8 bs 1/8/32)')
     ap.add_argument('--kernel-only', action='store_true',
                     help='run only the dominant kernel + a calibration copy '
                     '(for rocprofv3 --pmc passes)')
@@ -375,7 +461,7 @@ def main():
     log('generating weights on the GPU')
     sd = make_state_dict(cfg, seed=0, device=dev)
     log('preparing model')
-    model = PI0Inference(cfg, sd, device=dev, max_batch=B)
+    model = PI0Inference(cfg, sd, device=dev, max_batch=max(B, 8))
     inp = make_inputs(cfg, batch=B, seed=1)
     dinp = {k: v.to(dev) for k, v in inp.items()}
 
@@ -425,6 +511,11 @@ def main():
         log(f"cpu {cpu['value']} ms on {cpu['cores']} threads; gpu vs cpu "
             f'max abs err {err:.3e}')
 
+    configs, fp8_parity = None, None
+    if B == 1 and not args.no_configs:
+        log('other BASELINE configs')
+        configs, fp8_parity = other_configs(model, dev, parity=not args.no_cpu)
+
     res = {
         'metric': METRIC,
         'value': round(ms, 3),
@@ -456,6 +547,8 @@ def main():
         'cpu_baseline': cpu,
         'parity': None if err is None else {
             'chunk_max_abs_err_vs_cpu_oracle': err, 'tolerance': 2e-2},
+        'configs': configs,
+        'fp8_parity': fp8_parity,
     }
     print(json.dumps(res), flush=True)
 

@@ -329,6 +329,44 @@ class PI0Inference:
             self.mlp_in_a_f = F(self.mlp_in_a)
             self.mlp_out_f = F(self.mlp_out['w'])
 
+    def dequantized_state_dict(self, sd):
+        """fp8 models: the state dict whose fp32 forward is the model the
+        fp8 pipeline runs -- every quantized linear replaced by its
+        dequantized weight (scale * e4m3 bytes, read back from the device),
+        with the preparation's (1 + w) fold and Q/K interleave undone, so a
+        reference implementation's own norms and RoPE apply to it unchanged.
+        Tensors are fp32 on the CPU; the other entries are those of ``sd``."""
+        if self.weight_dtype != 'fp8':
+            raise ValueError('dequantized_state_dict needs an fp8 model')
+        cfg = self.cfg
+        H, D = cfg.heads, cfg.head_dim
+        inv = torch.argsort(interleave_rows(D))
+        out = dict(sd)
+        for role, prefix, W in (('llm', 'llm_backbone', self.llm),
+                                ('expert', 'llm_expert', self.exp)):
+            adarms = role == 'expert' and cfg.pi05
+            for i, L in enumerate(W['layers']):
+                pre = f'{prefix}.layers.{i}'
+                dq = {nm: L[nm].dequantize().cpu() for nm in LINEARS}
+                qkv = dq['qkv_w']
+                wq = qkv[:H * D].view(H, D, -1)[:, inv].reshape(H * D, -1)
+                wk, wv = qkv[H * D:H * D + D][inv], qkv[H * D + D:]
+                wg, wu = dq['gate_w'], dq['up_w']
+                if not adarms:
+                    s_in = 1.0 + sd[f'{pre}.input_layernorm.weight'].float().cpu()
+                    s_post = 1.0 + sd[
+                        f'{pre}.post_attention_layernorm.weight'].float().cpu()
+                    wq, wk, wv = wq / s_in, wk / s_in, wv / s_in
+                    wg, wu = wg / s_post, wu / s_post
+                out[f'{pre}.self_attn.q_proj.weight'] = wq
+                out[f'{pre}.self_attn.k_proj.weight'] = wk
+                out[f'{pre}.self_attn.v_proj.weight'] = wv
+                out[f'{pre}.self_attn.o_proj.weight'] = dq['o_w']
+                out[f'{pre}.mlp.gate_proj.weight'] = wg
+                out[f'{pre}.mlp.up_proj.weight'] = wu
+                out[f'{pre}.mlp.down_proj.weight'] = dq['down_w']
+        return out
+
     @property
     def kv_len(self):
         """Token capacity of the K/V caches: prefix + suffix, rounded up to a

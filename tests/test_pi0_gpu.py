@@ -133,42 +133,6 @@ def test_eager_equals_graph(cuda):
 FP8_CHUNK_ATOL = 5e-2
 
 
-def dequantized_state_dict(sd, cfg, m):
-    """The state dict whose fp32 forward is the model the fp8 pipeline runs:
-    every quantized linear replaced by its dequantized weight (scale *
-    e4m3 bytes, read back from the GPU model), with the preparation's
-    (1 + w) fold and Q/K interleave undone, so the oracle's own norms and
-    RoPE apply to it unchanged."""
-    from fluxvla_amd.pi0_inference import interleave_rows
-    H, D = cfg.heads, cfg.head_dim
-    inv = torch.argsort(interleave_rows(D))
-    out = dict(sd)
-    for role, prefix, W in (('llm', 'llm_backbone', m.llm),
-                            ('expert', 'llm_expert', m.exp)):
-        adarms = role == 'expert' and cfg.pi05
-        for i, L in enumerate(W['layers']):
-            pre = f'{prefix}.layers.{i}'
-            dq = {nm: L[nm].dequantize().cpu() for nm in
-                  ('qkv_w', 'o_w', 'gate_w', 'up_w', 'down_w')}
-            qkv = dq['qkv_w']
-            wq = qkv[:H * D].view(H, D, -1)[:, inv].reshape(H * D, -1)
-            wk, wv = qkv[H * D:H * D + D][inv], qkv[H * D + D:]
-            wg, wu = dq['gate_w'], dq['up_w']
-            if not adarms:
-                s_in = 1.0 + sd[f'{pre}.input_layernorm.weight'].float()
-                s_post = 1.0 + sd[f'{pre}.post_attention_layernorm.weight'].float()
-                wq, wk, wv = wq / s_in, wk / s_in, wv / s_in
-                wg, wu = wg / s_post, wu / s_post
-            out[f'{pre}.self_attn.q_proj.weight'] = wq
-            out[f'{pre}.self_attn.k_proj.weight'] = wk
-            out[f'{pre}.self_attn.v_proj.weight'] = wv
-            out[f'{pre}.self_attn.o_proj.weight'] = dq['o_w']
-            out[f'{pre}.mlp.gate_proj.weight'] = wg
-            out[f'{pre}.mlp.up_proj.weight'] = wu
-            out[f'{pre}.mlp.down_proj.weight'] = dq['down_w']
-    return out
-
-
 @pytest.mark.parametrize('pi05', [True, False])
 def test_fp8_chunk_matches_oracle(cuda, pi05):
     """fp8 weights in every Gemma-2B and action-expert linear layer: the
@@ -179,7 +143,7 @@ def test_fp8_chunk_matches_oracle(cuda, pi05):
     cfg = tiny(pi05=pi05)
     sd = make_state_dict(cfg, seed=0)
     m = PI0Inference(cfg, sd, device='cuda', max_batch=2, weight_dtype='fp8')
-    sdq = dequantized_state_dict(sd, cfg, m)
+    sdq = m.dequantized_state_dict(sd)
     for batch in (1, 2):
         announce(f'fp8 chunk pi05={pi05} batch={batch}')
         inp = make_inputs(cfg, batch=batch, seed=13)
