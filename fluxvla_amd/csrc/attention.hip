@@ -340,24 +340,29 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(fvx_attn_desc p,
 
 // ---------------------------------------------------------------------------
 // Decode-shaped attention: the action expert's 408 query rows (51 tokens x 8
-// heads) against the ~870-key prefix + suffix cache.  Per-CU load throughput
-// decides this kernel, so every global load is fully coalesced: a workgroup
-// of 4 waves owns 64 query rows and one key range, and copies Q once and
-// then 64-key tiles of K (32 KB contiguous) and of the transposed value
-// cache (256 rows of 128 B) into LDS; the next tile is prefetched into
-// registers while the current one feeds the MFMAs.  Each wave computes
-// S^T = K Q^T for its 16 query rows.  K rows sit in LDS in the order that
-// leaves lane group g holding keys 8g .. 8g+7 of each 32-key step (row of
-// key 32s + 8a + 4h + b is 32s + 16h + 4a + b), so the probabilities are the
-// A operand of O += P V with no shuffle, and each 16-row fragment read is 16
-// consecutive LDS rows (conflict-free).  Online-softmax statistics are fp32.
-// The O tile is transposed through LDS so that partials (and, without a
-// split, the output) move as 16-byte row chunks; attn_decode_merge_kernel
-// combines split partials in split order (deterministic).  Both can write
-// the output also in the fragment-major A layout of the o-projection.
+// heads) against the ~870-key prefix + suffix cache, in ONE kernel.
+//
+// A workgroup of 4 waves owns 64 query rows and one key range of 64-key
+// tiles (about 100 workgroups).  Q fragments go straight from memory into
+// VGPRs; K and the transposed value cache are copied tile by tile into LDS
+// with fully coalesced loads, the next tile prefetched into registers.  Each
+// wave computes S^T = K Q^T for its 16 query rows.  K rows sit in LDS in the
+// order that leaves lane group g holding keys 8g .. 8g+7 of each 32-key step
+// (row of key 32s + 8a + 4h + b is 32s + 16h + 4a + b), so the probabilities
+// are the A operand of O += P V with no shuffle.  Fragments are read from LDS
+// in batches ahead of their MFMAs (the four S chains advance together), so
+// the MFMAs do not wait on one LDS round trip each.  Online-softmax
+// statistics are fp32.
+//
+// With several key ranges each workgroup writes its partial (O, m, l) and
+// attn_decode_merge_kernel, the next kernel on the stream, combines them in
+// split order (deterministic).  (Merging inside this kernel -- partials
+// written through to the device-coherent level, a per-row-group arrival
+// counter, every split merging a share of the rows -- measured slower: the
+// write-through stores of ~6 MB of partials alone took ~9 us.)
 // ---------------------------------------------------------------------------
 constexpr int kDecKT = 64;                    // keys per tile
-constexpr int kDecQP = 256 + 8;               // LDS pitch (elements), Q / K rows
+constexpr int kDecQP = 256 + 8;               // LDS pitch (elements), K rows
 constexpr int kDecVP = kDecKT + 8;            // LDS pitch (elements), V^T rows
 constexpr int kDecOT = 64 + 4;                // LDS pitch (floats), O by dim
 constexpr int64_t kDecPF = 64 * 256 + 2 * 64;  // partial floats per workgroup
@@ -405,7 +410,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   __shared__ __align__(16) unsigned char smem[kDecLDS];
   __shared__ __align__(16) int32_t sG[kDecKT];
   __shared__ float sM[64], sL[64];
-  bf16_t* sQK = (bf16_t*)smem;                      // Q, then K tiles
+  bf16_t* sQK = (bf16_t*)smem;                      // K tiles
   bf16_t* sV = (bf16_t*)smem + 64 * kDecQP;         // V^T tiles
   float* sO = (float*)smem;                         // O by dim at the end
 
@@ -435,16 +440,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   const __amdgpu_buffer_rsrc_t rgc =
       make_rsrc(kgrp ? (const void*)kgrp : (const void*)Q, kgrp ? (uint32_t)kend * 4 : 0u);
 
-  // Q rows of this group (32 16-byte chunks per row) and the first K/V tile
-  // are requested together; Q goes through LDS into VGPRs.
-  bf16x8 rqv[8];
+  // Q fragments of this wave's 16 rows straight into VGPRs: lane (fr, g)
+  // holds dims 32 ds + 8 g .. + 7 of row qrow (the B operand of S^T).
+  const int qrow = rg * 64 + wave * 16 + fr;
+  const int qtok = row_tok(qrow, heads, hs);
+  const uint32_t qoff = (uint32_t)(qtok * qts + (qrow - qtok * heads) * qhs + 8 * g) * 2;
+  bf16x8 qf[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int c = tid + 256 * u, r = rg * 64 + (c >> 5);
-    const int tok = row_tok(r, heads, hs);
-    rqv[u] = bload8(rq, r < R ? (uint32_t)(tok * qts + (r - tok * heads) * qhs + (c & 31) * 8) * 2
-                              : kOOB);
-  }
+  for (int ds = 0; ds < 8; ++ds) qf[ds] = bload8(rq, qrow < R ? qoff + 64 * ds : kOOB);
 
   // Next-tile prefetch: unconditional buffer loads (all in flight at once);
   // V keys past kend are zeroed when the tile is written to LDS.
@@ -457,22 +460,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
       rk[u] = bload8(rkc, (uint32_t)((t0 + (c >> 5)) * kts + (c & 31) * 8) * 2);
       rv[u] = bload8(rvc, (uint32_t)((c >> 3) * vds + t0 + (c & 7) * 8) * 2);
     }
-    if (kgrp && tid < kDecKT)
-      rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)(t0 + tid) * 4, 0, 0);
+    rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)(t0 + (tid & 63)) * 4, 0, 0);
   };
-
-  if (kbeg < kend) prefetch(kbeg);
-  const int qrow = rg * 64 + wave * 16 + fr;
-  const int32_t qg = (qgrp && qrow < R) ? qgrp[row_tok(qrow, heads, hs)] : 0;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int c = tid + 256 * u;
-    st8(&sQK[(c >> 5) * kDecQP + (c & 31) * 8], rqv[u]);
-  }
-  __syncthreads();
-  bf16x8 qf[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) qf[s] = ld8(&sQK[(wave * 16 + fr) * kDecQP + 32 * s + 8 * g]);
+  prefetch(kbeg);
+  const int32_t qg = (qgrp && qrow < R) ? qgrp[qtok] : 0;
 
   const float sc = p.scale * kLog2e;
   float m_run = -INFINITY, l_run = 0.f;
@@ -480,31 +471,54 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
 #pragma unroll
   for (int i = 0; i < 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   for (int t0 = kbeg; t0 < kend; t0 += kDecKT) {
-    __syncthreads();  // previous tile (or the Q copy) fully read
+    __syncthreads();  // previous tile fully read
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int c = tid + 256 * u;
       st8(&sQK[dec_krow(c >> 5) * kDecQP + (c & 31) * 8], rk[u]);
       st8(&sV[(c >> 3) * kDecVP + (c & 7) * 8], mask_keys(rv[u], kend - (t0 + (c & 7) * 8)));
     }
-    if (kgrp && tid < kDecKT) sG[tid] = rgp;
+    if (tid < kDecKT) sG[tid] = rgp;
     __syncthreads();
     if (t0 + kDecKT < kend) prefetch(t0 + kDecKT);
 
-    // S^T for keys t0 + 32 s + 8 g + e (e = 4 h + j), query row qrow
+    // S^T for keys t0 + 32 s + 8 g + e (e = 4 h + j), query row qrow.  The
+    // four 16-key chains c = 2 s + h advance together (each MFMA's
+    // accumulator was written four MFMAs earlier); their K fragments are read
+    // in two halves of the head dimension, the second half's reads in flight
+    // under the first half's MFMAs.
     float sv[2][8];
+    {
+      f32x4_t acc[4];
+      bf16x8 kf[2][4][4];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int c = 0; c < 4; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      for (int hv = 0; hv < 2; ++hv)
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds)
-          acc = mfma16x16x32(ld8(&sQK[(32 * s + 16 * h + fr) * kDecQP + 32 * ds + 8 * g]),
-                             qf[ds], acc);
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sv[s][4 * h + j] = acc[j];
-      }
+          for (int d = 0; d < 4; ++d)
+            kf[hv][c][d] = ld8(&sQK[(16 * c + fr) * kDecQP + 32 * (4 * hv + d) + 8 * g]);
+      // keep the reads ahead of the MFMAs (the scheduler would otherwise sink
+      // each read next to its MFMA: one LDS round trip per MFMA)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int hv = 0; hv < 2; ++hv)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[c] = mfma16x16x32(kf[hv][c][d], qf[4 * hv + d], acc[c]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sv[c >> 1][4 * (c & 1) + j] = acc[c][j];
+    }
+    // the first step's V fragments load under the softmax
+    bf16x8 vf[2][16];
+#pragma unroll
+    for (int df = 0; df < 16; ++df) vf[0][df] = ld8(&sV[(16 * df + fr) * kDecVP + 8 * g]);
+    __builtin_amdgcn_sched_barrier(0);
     float tmax = -INFINITY;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -550,11 +564,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
         for (int j = 0; j < 4; ++j) o[df][j] *= al[j];
     }
 #pragma unroll
+    for (int df = 0; df < 16; ++df) vf[1][df] = ld8(&sV[(16 * df + fr) * kDecVP + 32 + 8 * g]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
     for (int s = 0; s < 2; ++s) {
       const bf16x8 pa = pack8(sv[s]);
 #pragma unroll
-      for (int df = 0; df < 16; ++df)
-        o[df] = mfma16x16x32(pa, ld8(&sV[(16 * df + fr) * kDecVP + 32 * s + 8 * g]), o[df]);
+      for (int df = 0; df < 16; ++df) o[df] = mfma16x16x32(pa, vf[s][df], o[df]);
     }
   }
 
@@ -569,33 +585,38 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     sL[wave * 16 + fr] = l_run;
   }
   __syncthreads();
-  float* part = splits > 1 ? (float*)p.workspace +
-                                 (((int64_t)z * n_rg + rg) * splits + split) * kDecPF
-                           : nullptr;
+  if (splits == 1) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = tid + 256 * u, i = c & 63, d0 = (c >> 6) * 8;
+      const int r = rg * 64 + i;
+      if (r >= R) continue;
+      const float l = sL[i];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = sO[(d0 + e) * kDecOT + i] * inv;
+      dec_store<8>(p, z, r, d0, hs, v);
+    }
+    return;
+  }
+
+  float* part = (float*)p.workspace + (((int64_t)z * n_rg + rg) * splits + split) * kDecPF;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int c = tid + 256 * u, i = c & 63, d0 = (c >> 6) * 8;
-    const int r = rg * 64 + i;
-    if (r >= R) continue;
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = sO[(d0 + e) * kDecOT + i];
-    if (part) {
-      *(f32x4_t*)(part + i * 256 + d0) = f32x4_t{v[0], v[1], v[2], v[3]};
-      *(f32x4_t*)(part + i * 256 + d0 + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
-    } else {
-      const float l = sL[i];
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] *= inv;
-      dec_store<8>(p, z, r, d0, hs, v);
-    }
+    *(f32x4_t*)(part + i * 256 + d0) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *(f32x4_t*)(part + i * 256 + d0 + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
   }
-  if (part && tid < 64) {
+  if (tid < 64) {
     part[64 * 256 + tid] = sM[tid];
     part[64 * 256 + 64 + tid] = sL[tid];
   }
 }
+
 
 // Merge of the decode partials: one thread per (problem, query row, 4 dims);
 // the loads of up to 16 splits are issued before the running-max merge,
@@ -698,15 +719,15 @@ static DecodePlan plan_decode(const fvx_attn_desc& d) {
   DecodePlan a;
   a.n_rb = (int)((d.sq * d.heads + 63) / 64);
   const int64_t tiles = (d.sk + kDecKT - 1) / kDecKT;
+  const int64_t groups = (int64_t)a.n_rb * d.n_problems;
   int64_t splits = d.kv_splits;
-  if (splits <= 0) splits = (128 + (int64_t)a.n_rb * d.n_problems - 1) /
-                            ((int64_t)a.n_rb * d.n_problems);
+  if (splits <= 0) splits = (128 + groups - 1) / groups;
   if (splits > tiles) splits = tiles;
   if (splits < 1) splits = 1;
   const int64_t kps = (tiles + splits - 1) / splits * kDecKT;
   a.splits = (int)((d.sk + kps - 1) / kps);
   a.kps = kps;
-  a.n_items = (int)(a.n_rb * a.splits * d.n_problems);
+  a.n_items = (int)(groups * a.splits);
   a.ws_bytes = a.splits > 1 ? (int64_t)a.n_items * kDecPF * 4 : 0;
   return a;
 }
@@ -716,6 +737,38 @@ extern "C" int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d) {
     return 0;
   if (use_decode(*d)) return plan_decode(*d).ws_bytes;
   return plan_attn(*d).ws_bytes;
+}
+
+static int run_generic(const fvx_attn_desc& d, hipStream_t s) {
+  AttnPlan a = plan_attn(d);
+  if (a.splits > 1 && (!d.workspace || d.workspace_bytes < a.ws_bytes)) {
+    FVX_REQUIRE(d.kv_splits <= 1, FVX_ERR_WORKSPACE,
+                "attention: kv_splits=%d needs %lld workspace bytes, got %lld",
+                d.kv_splits, (long long)a.ws_bytes,
+                (long long)d.workspace_bytes);
+    a.splits = 1;
+    a.kps = ((d.sk + kKeyTile - 1) / kKeyTile) * kKeyTile;
+  }
+  FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
+              "attention: workspace must be 16B aligned");
+  dim3 grid((unsigned)a.n_row_blocks, (unsigned)a.splits,
+            (unsigned)d.n_problems);
+  if (a.hdp == 256)
+    hipLaunchKernelGGL((attn_kernel<256, 256>), grid, dim3(256), 0, s, d,
+                       a.n_row_blocks, a.splits, a.kps);
+  else
+    hipLaunchKernelGGL((attn_kernel<96, 80>), grid, dim3(256), 0, s, d,
+                       a.n_row_blocks, a.splits, a.kps);
+  int st = launch_status("attention");
+  if (st || a.splits == 1) return st;
+  dim3 mgrid((unsigned)a.n_row_blocks, 1u, (unsigned)d.n_problems);
+  if (a.hdp == 256)
+    hipLaunchKernelGGL((attn_merge_kernel<256, 256>), mgrid, dim3(256), 0, s,
+                       d, a.n_row_blocks, a.splits);
+  else
+    hipLaunchKernelGGL((attn_merge_kernel<96, 80>), mgrid, dim3(256), 0, s, d,
+                       a.n_row_blocks, a.splits);
+  return launch_status("attention");
 }
 
 extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
@@ -777,33 +830,5 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
                        d, a.n_rb, a.splits, hs);
     return launch_status("attention(decode merge)");
   }
-  AttnPlan a = plan_attn(d);
-  if (a.splits > 1 && (!d.workspace || d.workspace_bytes < a.ws_bytes)) {
-    FVX_REQUIRE(d.kv_splits <= 1, FVX_ERR_WORKSPACE,
-                "attention: kv_splits=%d needs %lld workspace bytes, got %lld",
-                d.kv_splits, (long long)a.ws_bytes,
-                (long long)d.workspace_bytes);
-    a.splits = 1;
-    a.kps = ((d.sk + kKeyTile - 1) / kKeyTile) * kKeyTile;
-  }
-  FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
-              "attention: workspace must be 16B aligned");
-  dim3 grid((unsigned)a.n_row_blocks, (unsigned)a.splits,
-            (unsigned)d.n_problems);
-  if (a.hdp == 256)
-    hipLaunchKernelGGL((attn_kernel<256, 256>), grid, dim3(256), 0, s, d,
-                       a.n_row_blocks, a.splits, a.kps);
-  else
-    hipLaunchKernelGGL((attn_kernel<96, 80>), grid, dim3(256), 0, s, d,
-                       a.n_row_blocks, a.splits, a.kps);
-  int st = launch_status("attention");
-  if (st || a.splits == 1) return st;
-  dim3 mgrid((unsigned)a.n_row_blocks, 1u, (unsigned)d.n_problems);
-  if (a.hdp == 256)
-    hipLaunchKernelGGL((attn_merge_kernel<256, 256>), mgrid, dim3(256), 0, s,
-                       d, a.n_row_blocks, a.splits);
-  else
-    hipLaunchKernelGGL((attn_merge_kernel<96, 80>), mgrid, dim3(256), 0, s, d,
-                       a.n_row_blocks, a.splits);
-  return launch_status("attention");
+  return run_generic(d, s);
 }
