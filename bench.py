@@ -236,7 +236,7 @@ def kernel_table(model):
         ('gemm_tile_kernel<256,256,GEGLU> (prefix)', lambda: K.gemm_geglu(
             px, L['gate_w'], L['up_w'], out=b['pre_h'], rownorm_eps=cfg.rms_eps),
          4 * M * cfg.llm_mlp * cfg.llm_hidden),
-        ('gemm_tile_kernel<64,128,PLAIN> down, split-K 2 (prefix)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> down (prefix)', lambda: K.gemm(
             b['pre_h'], L['down_w'], out=b['pre_q'].view(M, -1)[:, :cfg.llm_hidden],
             residual=px), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
         ('attn_kernel<256,256> + merge (prefix)', lambda: K.mqa_attention(
@@ -257,7 +257,7 @@ def kernel_table(model):
         ('gemm_tile_kernel<64,128,PLAIN> fc1+bias+gelu (SigLIP)', lambda: K.gemm(
             vxn, V['fc1_w'], out=b['vis_h'], bias=V['fc1_b'], act=2),
          2 * Mv * cfg.vit_mlp * vh),
-        ('gemm_tile_kernel<64,128,PLAIN> fc2+bias+res, split-K 4 (SigLIP)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> fc2+bias+res, split-K 2 (SigLIP)', lambda: K.gemm(
             b['vis_h'], V['fc2_w'], out=vxn, bias=V['fc2_b'], residual=vx),
          2 * Mv * vh * cfg.vit_mlp),
         ('attn_kernel<96,80> (SigLIP)', lambda: K.mha_packed_qkv(

@@ -707,7 +707,7 @@ struct DecodePlan {
 static bool use_decode(const fvx_attn_desc& d) {
   // (its operand offsets are 32-bit)
   const int64_t lim = (int64_t)1 << 30;
-  return d.v_d_stride > 0 && d.head_dim == 256 && d.sq * d.heads <= 512 &&
+  return d.v_d_stride > 0 && d.head_dim == 256 &&
          d.sq * d.q_tok_stride + d.heads * d.q_head_stride < lim &&
          d.sk * d.k_tok_stride < lim && 256 * d.v_d_stride < lim;
 }

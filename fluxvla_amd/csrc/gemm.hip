@@ -544,21 +544,30 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
       }
       return;
     }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    // k step ks + 1's fragments are read before step ks's MFMAs are issued
+    // (two register sets), so each step's LDS latency hides under the
+    // previous step's MFMAs
+    bf16x8 af[2][FM], bfr[2][FN];
+    auto rd = [&](int ks, int b) {
       const int cpos = ((2 * ks + hk) ^ sw) * 16;
-      bf16x8 af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = *(const bf16x8*)(s + (wm * WM + 32 * i + fr) * 128 + cpos);
+        af[b][i] = *(const bf16x8*)(s + (wm * WM + 32 * i + fr) * 128 + cpos);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
+        bfr[b][j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int b = ks & 1;
+      if (ks < 3) rd(ks + 1, b ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        ss[i] += sumsq8(af[i]);
+        ss[i] += sumsq8(af[b][i]);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
       }
     }
   };
@@ -1166,19 +1175,23 @@ static int validate(const GemmArgs& d) {
   }
 
 // Tile configurations: {BM, BN (all weights' columns), waves M x N, stages}.
-//   0: 128 x 128, 2 x 2 waves of 64 x 64, 2 stages (64 KiB of LDS)
+//   0:  64 x 128, 2 x 2 waves of 32 x 64,  2 stages (48 KiB of LDS: two
+//       workgroups per CU)
 //   1: 256 x 256, 2 x 4 waves of 128 x 64, 2 stages (128 KiB: one workgroup
-//      of 8 waves per CU; half the L2 traffic per flop of config 0)
-//   2:  64 x 128, 2 x 2 waves of 32 x 64, 2 stages (48 KiB)
-// Measured on MI355X (us; bs=1 chunk shapes, configs 0 / 1 / 2):
-//   prefix GeGLU 816 x 16384 x2 x 2048   158 / 151 / 154
-//   prefix QKV   816 x 2560 x 2048        39 /  84 /  27
-//   prefix O     816 x 2048 x 2048        37 /  82 /  24
-//   SigLIP fc1   768 x 4304 x 1152        34 /  69 /  23
-//   SigLIP o     768 x 1152 x 1152        25 /  58 /  15
-// The small projections gain from the extra workgroups of config 2 more
-// than they lose to its higher LDS traffic per flop.
-static const int kTileBM[] = {128, 256, 64};
+//      of 8 waves per CU; half the L2 traffic per flop of a 128 x 128 tile)
+//   2:  64 x 128 with 4 stages (96 KiB, one workgroup per CU: three slabs in
+//       flight instead of one, for grids that leave CUs free anyway)
+// Measured on MI355X (us; bs=1 chunk shapes):
+//   prefix GeGLU 816 x 16384 x2 x 2048   128x128: 158, 1: 151 (0: 154)
+//   prefix QKV   816 x 2560 x 2048   (260 tiles)   0: 26.2   2: 37.4
+//   prefix O     816 x 2048 x 2048   (208 tiles)   0: 23.7   2: 19.9
+//   SigLIP fc1   768 x 4304 x 1152   (408 tiles)   0: 23.4   2: 30.4
+//   SigLIP fc2   768 x 1152 x 4304   (108 tiles)   0 split 4: 37.6, 2 split 2: 33.6
+//   bs=8 QKV     408 x 2560 x 1024   (140 tiles)   0: 16.5   2: 14.1
+// Small tiles win on these shapes: the extra workgroups hide more latency
+// than they cost in LDS traffic per flop; deeper rings win only when the
+// grid leaves CUs idle.
+static const int kTileBM[] = {64, 256, 64};
 static const int kTileBN[] = {128, 256, 128};
 constexpr int kTileCfgs = 3;
 
@@ -1188,23 +1201,20 @@ struct TilePlan {
   int cfg, splits;
 };
 
-// Config 1 for GeGLU projections that still give >= 256 of its tiles, else
-// config 2.  A long K (>= 4096) with fewer than 256 tiles is split
-// (ceil(384 / tiles), at most 4: prefix down projection 2, SigLIP fc2 4);
-// with a shorter K the partials cost more than the idle CUs.
+// Config 1 for GeGLU projections that still give >= 256 of its tiles; else
+// 64 x 128 tiles, with the 4-stage ring (config 2) when they number <= 256.
+// A long K (>= 4096) with fewer than 128 tiles is split in two (SigLIP fc2);
+// with more tiles the partials cost more than the idle CUs.
 static TilePlan plan_tile(const GemmArgs& d) {
   TilePlan t;
   const bool gg = d.mode == FVX_GEMM_GEGLU;
-  t.cfg = (gg && ((d.m + 255) / 256) * ((d.n + 127) / 128) >= 256) ? 1 : 2;
-  const int64_t bm = tile_bm(t.cfg, d.b_fp8), bn = kTileBN[t.cfg] / (gg ? 2 : 1);
-  const int64_t tiles = ((d.m + bm - 1) / bm) * ((d.n + bn - 1) / bn);
+  const int64_t bn = 128 / (gg ? 2 : 1);
+  const int64_t tiles = ((d.m + 63) / 64) * ((d.n + bn - 1) / bn);
+  if (gg && ((d.m + 255) / 256) * ((d.n + 127) / 128) >= 256) t.cfg = 1;
+  else t.cfg = tiles <= 256 ? 2 : 0;
   t.splits = 1;
-  if (d.split_k > 0) {
-    t.splits = d.split_k;
-  } else if (tiles < 256 && d.k >= 4096) {
-    t.splits = (int)((384 + tiles - 1) / tiles);
-    if (t.splits > 4) t.splits = 4;
-  }
+  if (d.split_k > 0) t.splits = d.split_k;
+  else if (t.cfg != 1 && tiles < 128 && d.k >= 4096) t.splits = 2;
   return t;
 }
 
@@ -1243,12 +1253,12 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   // 128 x 256 to stay within the LDS
 #define LCFG(MODE)                                                   \
   if (d.b_fp8) {                                                     \
-    if (cfg == 0) LT(128, 128, 2, 2, 2, MODE, true);                 \
-    else if (cfg == 1) LT(128, 256, 2, 4, 2, MODE, true);            \
+    if (cfg == 1) LT(128, 256, 2, 4, 2, MODE, true);                 \
+    else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, true);             \
     else LT(64, 128, 2, 2, 2, MODE, true);                           \
   } else {                                                           \
-    if (cfg == 0) LT(128, 128, 2, 2, 2, MODE, false);                \
-    else if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false);           \
+    if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false);                \
+    else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false);            \
     else LT(64, 128, 2, 2, 2, MODE, false);                          \
   }
   FVX_MODE_DISPATCH(d.mode, LCFG)
