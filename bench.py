@@ -239,7 +239,7 @@ def kernel_table(model):
         ('gemm_tile_kernel<64,128,PLAIN> down (prefix)', lambda: K.gemm(
             b['pre_h'], L['down_w'], out=b['pre_q'].view(M, -1)[:, :cfg.llm_hidden],
             residual=px), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
-        ('attn_kernel<256,256> + merge (prefix)', lambda: K.mqa_attention(
+        ('attn_decode_kernel + merge (prefix)', lambda: K.mqa_attention(
             b['pre_q'], kc0[:, :S], vc0, b['pre_ctx'], kgrp=b['kgrp'][:, :S],
             qgrp=b['qgrp_pre'], v_transposed=True), 4 * H * S * S * D),
     ]
