@@ -339,39 +339,55 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(fvx_attn_desc p,
 }
 
 // ---------------------------------------------------------------------------
-// Decode-shaped attention: the action expert's 408 query rows (51 tokens x 8
-// heads) against the ~870-key prefix + suffix cache, in ONE kernel.
+// Head-dim-256 attention with a transposed value cache: the action expert's
+// 408 query rows (51 tokens x 8 heads) against the ~870-key prefix + suffix
+// cache, and the prefix prefill (6528 rows x 816 keys).
 //
-// A workgroup of 4 waves owns 64 query rows and one key range of 64-key
-// tiles (about 100 workgroups).  Q fragments go straight from memory into
-// VGPRs; K and the transposed value cache are copied tile by tile into LDS
-// with fully coalesced loads, the next tile prefetched into registers.  Each
-// wave computes S^T = K Q^T for its 16 query rows.  K rows sit in LDS in the
-// order that leaves lane group g holding keys 8g .. 8g+7 of each 32-key step
-// (row of key 32s + 8a + 4h + b is 32s + 16h + 4a + b), so the probabilities
-// are the A operand of O += P V with no shuffle.  Fragments are read from LDS
-// in batches ahead of their MFMAs (the four S chains advance together), so
-// the MFMAs do not wait on one LDS round trip each.  Online-softmax
-// statistics are fp32.
+// A workgroup of 4 waves owns 64 query rows and one key range, walked in
+// 64-key tiles.  The waves split each tile two ways:
+//   S^T = K Q^T   wave w takes keys 16 w .. 16 w + 15 of the tile for all 64
+//                 rows (the 64 rows' Q fragments stay in VGPRs for the whole
+//                 range);
+//   O += P V      wave w takes dims 64 w .. 64 w + 63 for all 64 rows.
+// Every byte moves from memory into LDS by the buffer unit (buffer_load ...
+// lds), 1 KiB of contiguous rows per wave instruction: a wave load that
+// gathers 16 rows x 64 B (the shape of an MFMA fragment) runs at a third of
+// that rate per CU.  Each wave loads exactly the K and V^T slices it reads
+// itself, so their arrival needs only the wave's own vmcnt, no barrier; a
+// two-stage ring keeps the next tile in flight.  LDS rows carry an XOR
+// swizzle of their 16-byte chunks (the load picks which global chunk lands
+// in each slot), so the fragment reads are conflict-free.
+//
+// Only the probabilities cross waves: each wave writes its 64 x 16 block of
+// P (bf16) and its per-row maxima to LDS and reads the whole 64 x 64 tile
+// back as the A operand of P V.  Every wave derives the same running
+// maximum from the exchanged maxima, so the per-wave row sums add up to the
+// softmax denominator at the end.  Two barriers per tile; the exchange
+// buffers alternate between tiles.  Online-softmax statistics are fp32.
 //
 // With several key ranges each workgroup writes its partial (O, m, l) and
 // attn_decode_merge_kernel, the next kernel on the stream, combines them in
 // split order (deterministic).  (Merging inside this kernel -- partials
 // written through to the device-coherent level, a per-row-group arrival
-// counter, every split merging a share of the rows -- measured slower: the
-// write-through stores of ~6 MB of partials alone took ~9 us.)
+// counter -- measured slower: the write-through stores of ~6 MB of partials
+// alone took ~9 us.)
 // ---------------------------------------------------------------------------
-constexpr int kDecKT = 64;                    // keys per tile
-constexpr int kDecQP = 256 + 8;               // LDS pitch (elements), K rows
-constexpr int kDecVP = kDecKT + 8;            // LDS pitch (elements), V^T rows
-constexpr int kDecOT = 64 + 4;                // LDS pitch (floats), O by dim
-constexpr int64_t kDecPF = 64 * 256 + 2 * 64;  // partial floats per workgroup
-constexpr int kDecLDS = (64 * kDecQP + 256 * kDecVP) * 2;
-
-__device__ __forceinline__ int dec_krow(int jl) {
-  // LDS row of tile key jl = 32 s + 8 a + 4 h + b
-  return (jl & ~31) + ((jl >> 2) & 1) * 16 + ((jl >> 3) & 3) * 4 + (jl & 3);
-}
+constexpr int kDecKT = 64;                      // keys per tile
+constexpr int kDecPP = kDecKT + 8;              // LDS pitch (elements), P rows
+constexpr int kDecOP = 256 + 4;                 // LDS pitch (floats), O rows
+constexpr int64_t kDecPF = 64 * 256 + 2 * 64;   // partial floats per workgroup
+// LDS map (bytes): two stages of [K tile 64 x 512 B | V^T tile 256 x 128 B]
+// (stage 1 first holds the Q rows), then P [2][64][kDecPP] bf16, the row
+// maxima [2][64][4] f32, the key groups [2][4 waves][64] and the query
+// groups [64]; at the end the O rows [64][kDecOP] f32 over the stages.
+constexpr int kDecStage = 64 * 512 + 256 * 128;
+constexpr int kDecOffP = 2 * kDecStage;
+constexpr int kDecOffM = kDecOffP + 2 * 64 * kDecPP * 2;
+constexpr int kDecOffG = kDecOffM + 2 * 64 * 4 * 4;
+constexpr int kDecOffQG = kDecOffG + 2 * 4 * 64 * 4;
+constexpr int kDecLDS = kDecOffQG + 64 * 4;
+static_assert(64 * kDecOP * 4 <= 2 * kDecStage, "O rows fit the stages");
+constexpr int kDecLoads = 17;  // DMA instructions per wave per tile
 
 // Query row r of a problem is (token r / heads, head r % heads); `hs` is
 // log2(heads) when heads is a power of two (shifts instead of divisions).
@@ -406,19 +422,20 @@ __device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int z, int r,
 __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
                                                           int n_rg, int splits,
                                                           int kps, int hs) {
-  constexpr int HD = 256;
+  constexpr int HD = 256, KT = kDecKT;
   __shared__ __align__(16) unsigned char smem[kDecLDS];
-  __shared__ __align__(16) int32_t sG[kDecKT];
-  __shared__ float sM[64], sL[64];
-  bf16_t* sQK = (bf16_t*)smem;                      // K tiles
-  bf16_t* sV = (bf16_t*)smem + 64 * kDecQP;         // V^T tiles
-  float* sO = (float*)smem;                         // O by dim at the end
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float sL[4][64], sM[64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, g = lane >> 4;
-  const int rg = blockIdx.x % n_rg;
-  const int split = (blockIdx.x / n_rg) % splits;
-  const int z = blockIdx.x / (n_rg * splits);
+  // XCD-aware order: consecutive items (the row groups of one key range)
+  // land on one XCD and share its L2 copy of the range's K / V tiles.
+  const int nb = (int)gridDim.x, q8 = nb >> 3, r8 = nb & 7;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
+  const int rg = item % n_rg;
+  const int split = (item / n_rg) % splits;
+  const int z = item / (n_rg * splits);
   const int heads = (int)p.heads, R = (int)p.sq * heads;
   const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
@@ -431,171 +448,236 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   const int qts = (int)p.q_tok_stride, qhs = (int)p.q_head_stride;
   const int kts = (int)p.k_tok_stride, vds = (int)p.v_d_stride;
 
-  // Buffer views: rows past the range read as zero (K: keys >= kend; V^T:
-  // the last row's tail; Q: rows >= R get an out-of-range offset).
-  const __amdgpu_buffer_rsrc_t rq =
-      make_rsrc(Q, (uint32_t)(((int)p.sq - 1) * qts + (heads - 1) * qhs + HD) * 2);
-  const __amdgpu_buffer_rsrc_t rkc = make_rsrc(K, (uint32_t)kend * kts * 2);
-  const __amdgpu_buffer_rsrc_t rvc = make_rsrc(Vt, (uint32_t)HD * vds * 2);
-  const __amdgpu_buffer_rsrc_t rgc =
-      make_rsrc(kgrp ? (const void*)kgrp : (const void*)Q, kgrp ? (uint32_t)kend * 4 : 0u);
+  // Buffer views: loads past them write zeros (K: keys >= kend; V^T: past
+  // its last row; Q: rows >= R get an out-of-range offset).  V^T keys past
+  // kend inside the view are zeroed after they are read.
+  const i32x4_t rq =
+      make_rsrc4(Q, (uint32_t)(((int)p.sq - 1) * qts + (heads - 1) * qhs + HD) * 2);
+  const i32x4_t rkc = make_rsrc4(K, (uint32_t)kend * kts * 2);
+  const i32x4_t rvc = make_rsrc4(Vt, (uint32_t)HD * vds * 2);
+  const i32x4_t rgc = make_rsrc4(kgrp ? (const void*)kgrp : (const void*)Q,
+                                 kgrp ? (uint32_t)kend * 4 : 0u);
+  const i32x4_t rqg = make_rsrc4(qgrp ? (const void*)qgrp : (const void*)Q,
+                                 qgrp ? (uint32_t)p.sq * 4 : 0u);
+  const uint32_t lbase = lds_addr(smem);
+  bf16_t* sP = (bf16_t*)(smem + kDecOffP);
+  float* sMx = (float*)(smem + kDecOffM);
+  const int32_t* sG = (const int32_t*)(smem + kDecOffG);
+  const int32_t* sQG = (const int32_t*)(smem + kDecOffQG);
 
-  // Q fragments of this wave's 16 rows straight into VGPRs: lane (fr, g)
-  // holds dims 32 ds + 8 g .. + 7 of row qrow (the B operand of S^T).
-  const int qrow = rg * 64 + wave * 16 + fr;
-  const int qtok = row_tok(qrow, heads, hs);
-  const uint32_t qoff = (uint32_t)(qtok * qts + (qrow - qtok * heads) * qhs + 8 * g) * 2;
-  bf16x8 qf[8];
+  // Tile t0 into stage st, this wave's slices: K keys t0 + 16 w + 2 i +
+  // (lane >> 5) (LDS slot lane & 31 of the key's 512-byte row holds global
+  // chunk slot ^ (key & 15)); V^T dims 64 w + 8 i + (lane >> 3) (slot lane
+  // & 7 of the dim's 128-byte row holds key chunk slot ^ ((dim >> 1) & 7));
+  // the groups of keys t0 + 16 w + lane, lane < 16.
+  auto issue = [&](int t0, int st) {
+    const uint32_t sb = lbase + st * kDecStage;
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) qf[ds] = bload8(rq, qrow < R ? qoff + 64 * ds : kOOB);
-
-  // Next-tile prefetch: unconditional buffer loads (all in flight at once);
-  // V keys past kend are zeroed when the tile is written to LDS.
-  bf16x8 rk[8], rv[8];
-  int32_t rgp = 0;
-  auto prefetch = [&](int t0) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int c = tid + 256 * u;
-      rk[u] = bload8(rkc, (uint32_t)((t0 + (c >> 5)) * kts + (c & 31) * 8) * 2);
-      rv[u] = bload8(rvc, (uint32_t)((c >> 3) * vds + t0 + (c & 7) * 8) * 2);
+    for (int i = 0; i < 8; ++i) {
+      const int kl = 16 * w + 2 * i + (lane >> 5);
+      const int ch = (lane & 31) ^ (kl & 15);
+      load_lds16(rkc, sb + (16 * w + 2 * i) * 512,
+                 (uint32_t)((t0 + kl) * kts + 8 * ch) * 2);
     }
-    rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)(t0 + (tid & 63)) * 4, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d = 64 * w + 8 * i + (lane >> 3);
+      const int ch = (lane & 7) ^ ((d >> 1) & 7);
+      load_lds16(rvc, sb + 64 * 512 + (64 * w + 8 * i) * 128,
+                 (uint32_t)(d * vds + t0 + 8 * ch) * 2);
+    }
+    load_lds4(rgc, lbase + kDecOffG + (st * 4 + w) * 256,
+              lane < 16 ? (uint32_t)(t0 + 16 * w + lane) * 4 : kOOB);
   };
-  prefetch(kbeg);
-  const int32_t qg = (qgrp && qrow < R) ? qgrp[qtok] : 0;
+
+  // Q rows 64 rg + 16 w + 2 i + (lane >> 5) into stage 1 (same swizzle as
+  // K), their tokens' query groups, then tile 0.
+  {
+    const uint32_t qb = lbase + kDecStage;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rl = 16 * w + 2 * i + (lane >> 5);
+      const int r = rg * 64 + rl;
+      const int tok = row_tok(r, heads, hs);
+      const int ch = (lane & 31) ^ (rl & 15);
+      load_lds16(rq, qb + (16 * w + 2 * i) * 512,
+                 r < R ? (uint32_t)(tok * qts + (r - tok * heads) * qhs + 8 * ch) * 2
+                       : kOOB);
+    }
+    if (w == 0) {
+      const int r = rg * 64 + lane;
+      load_lds4(rqg, lbase + kDecOffQG, r < R ? (uint32_t)row_tok(r, heads, hs) * 4 : kOOB);
+    }
+  }
+  issue(kbeg, 0);
+  wait_vmcnt<kDecLoads>();  // this wave's Q rows (and query groups) landed
+  __syncthreads();
+
+  // Q fragments (B operand of S^T): lane (fr, g) holds dims 32 ds + 8 g ..
+  // + 7 of row 16 rb + fr.
+  bf16x8 qf[4][8];
+  int32_t qg[4];
+  {
+    const bf16_t* sQ = (const bf16_t*)(smem + kDecStage);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds)
+        qf[rb][ds] = ld8(&sQ[(16 * rb + fr) * 256 + 8 * ((4 * ds + g) ^ fr)]);
+      qg[rb] = qgrp ? sQG[16 * rb + fr] : 0;
+    }
+  }
+  __syncthreads();  // stage 1 is free for tile 1
+  if (kbeg + KT < kend) issue(kbeg + KT, 1);
 
   const float sc = p.scale * kLog2e;
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4_t o[16];
+  float m_run[4], l_w[4];
+  f32x4_t o[4][4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int t0 = kbeg; t0 < kend; t0 += kDecKT) {
-    __syncthreads();  // previous tile fully read
+  for (int rb = 0; rb < 4; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_w[rb] = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int c = tid + 256 * u;
-      st8(&sQK[dec_krow(c >> 5) * kDecQP + (c & 31) * 8], rk[u]);
-      st8(&sV[(c >> 3) * kDecVP + (c & 7) * 8], mask_keys(rv[u], kend - (t0 + (c & 7) * 8)));
+    for (int b = 0; b < 4; ++b) o[rb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int t0 = kbeg, cs = 0; t0 < kend; t0 += KT, cs ^= 1) {
+    // this wave's slices of tile t0 have landed (the next tile's may not)
+    if (t0 + KT < kend)
+      wait_vmcnt<kDecLoads>();
+    else
+      wait_vmcnt<0>();
+    const unsigned char* stg = smem + cs * kDecStage;
+    const bf16_t* sK = (const bf16_t*)stg;
+    const bf16_t* sV = (const bf16_t*)(stg + 64 * 512);
+
+    // S^T: lane (fr, g) ends with keys t0 + 16 w + 4 g + j of row 16 rb + fr
+    bf16x8 kf[8];
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+      kf[ds] = ld8(&sK[(16 * w + fr) * 256 + 8 * ((4 * ds + g) ^ fr)]);
+    const int4 kgv = *(const int4*)&sG[(cs * 4 + w) * 64 + 4 * g];
+    const int32_t kgc[4] = {kgv.x, kgv.y, kgv.z, kgv.w};
+    f32x4_t s[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) s[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) s[rb] = mfma16x16x32(kf[ds], qf[rb][ds], s[rb]);
+
+    float sv[4][4], mx[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      mx[rb] = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bool vis = t0 + 16 * w + 4 * g + j < kend;
+        if (kgrp) vis = vis && kgc[j] <= qg[rb];
+        sv[rb][j] = vis ? s[rb][j] * sc : -INFINITY;
+        mx[rb] = fmaxf(mx[rb], sv[rb][j]);
+      }
+      mx[rb] = fmaxf(mx[rb], __shfl_xor(mx[rb], 16, 64));
+      mx[rb] = fmaxf(mx[rb], __shfl_xor(mx[rb], 32, 64));
     }
-    if (tid < kDecKT) sG[tid] = rgp;
+    float* mxb = sMx + cs * 256;
+    if (g == 0)
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) mxb[(16 * rb + fr) * 4 + w] = mx[rb];
     __syncthreads();
-    if (t0 + kDecKT < kend) prefetch(t0 + kDecKT);
 
-    // S^T for keys t0 + 32 s + 8 g + e (e = 4 h + j), query row qrow.  The
-    // four 16-key chains c = 2 s + h advance together (each MFMA's
-    // accumulator was written four MFMAs earlier); their K fragments are read
-    // in two halves of the head dimension, the second half's reads in flight
-    // under the first half's MFMAs.
-    float sv[2][8];
-    {
-      f32x4_t acc[4];
-      bf16x8 kf[2][4][4];
+    bf16_t* pb = sP + cs * 64 * kDecPP;
+    float alpha[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < 4; ++rb) {
+      const f32x4_t t = *(const f32x4_t*)&mxb[(16 * rb + fr) * 4];
+      const float m_new = fmaxf(m_run[rb], fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])));
+      const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+      alpha[rb] = exp2f(m_run[rb] - m_ref);
+      m_run[rb] = m_new;
+      float pv[4], ps = 0.f;
 #pragma unroll
-      for (int hv = 0; hv < 2; ++hv)
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-          for (int d = 0; d < 4; ++d)
-            kf[hv][c][d] = ld8(&sQK[(16 * c + fr) * kDecQP + 32 * (4 * hv + d) + 8 * g]);
-      // keep the reads ahead of the MFMAs (the scheduler would otherwise sink
-      // each read next to its MFMA: one LDS round trip per MFMA)
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int hv = 0; hv < 2; ++hv)
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[c] = mfma16x16x32(kf[hv][c][d], qf[4 * hv + d], acc[c]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sv[c >> 1][4 * (c & 1) + j] = acc[c][j];
+      for (int j = 0; j < 4; ++j) {
+        pv[j] = exp2f(sv[rb][j] - m_ref);
+        ps += pv[j];
+      }
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      l_w[rb] = l_w[rb] * alpha[rb] + ps;
+      *(uint2*)&pb[(16 * rb + fr) * kDecPP + 16 * w + 4 * g] =
+          uint2{f2bf2(pv[0], pv[1]), f2bf2(pv[2], pv[3])};
     }
-    // the first step's V fragments load under the softmax
-    bf16x8 vf[2][16];
-#pragma unroll
-    for (int df = 0; df < 16; ++df) vf[0][df] = ld8(&sV[(16 * df + fr) * kDecVP + 8 * g]);
-    __builtin_amdgcn_sched_barrier(0);
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      int32_t gk[8];
-      if (kgrp) {
-        const int4 a = *(const int4*)&sG[32 * s + 8 * g];
-        const int4 b = *(const int4*)&sG[32 * s + 8 * g + 4];
-        gk[0] = a.x; gk[1] = a.y; gk[2] = a.z; gk[3] = a.w;
-        gk[4] = b.x; gk[5] = b.y; gk[6] = b.z; gk[7] = b.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        bool vis = t0 + 32 * s + 8 * g + e < kend;
-        if (kgrp) vis = vis && gk[e] <= qg;
-        sv[s][e] = vis ? sv[s][e] * sc : -INFINITY;
-        tmax = fmaxf(tmax, sv[s][e]);
-      }
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_ref);
-    float psum = 0.f;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sv[s][e] = exp2f(sv[s][e] - m_ref);
-        psum += sv[s][e];
-      }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
     if (t0 != kbeg) {  // O is still zero on the first tile
-      float al[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) al[j] = __shfl(alpha, 4 * g + j, 64);
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int df = 0; df < 16; ++df)
+        for (int j = 0; j < 4; ++j) {
+          const float al = __shfl(alpha[rb], 4 * g + j, 64);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[df][j] *= al[j];
+          for (int b = 0; b < 4; ++b) o[rb][b][j] *= al;
+        }
     }
+    // V fragments (B operand of P V): dim 64 w + 16 b + fr, keys t0 + 32 c +
+    // 8 g .. + 7
+    bf16x8 vf[8];
 #pragma unroll
-    for (int df = 0; df < 16; ++df) vf[1][df] = ld8(&sV[(16 * df + fr) * kDecVP + 32 + 8 * g]);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const bf16x8 pa = pack8(sv[s]);
+      for (int b = 0; b < 4; ++b) {
+        const int d = 64 * w + 16 * b + fr;
+        vf[4 * c + b] = mask_keys(ld8(&sV[d * 64 + 8 * ((4 * c + g) ^ ((d >> 1) & 7))]),
+                                  kend - (t0 + 32 * c + 8 * g));
+      }
+    __syncthreads();
+
 #pragma unroll
-      for (int df = 0; df < 16; ++df) o[df] = mfma16x16x32(pa, vf[s][df], o[df]);
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const bf16x8 pa = ld8(&pb[(16 * rb + fr) * kDecPP + 32 * c + 8 * g]);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) o[rb][b] = mfma16x16x32(pa, vf[4 * c + b], o[rb][b]);
+      }
+    if (t0 + 2 * KT < kend) {
+      // this wave's reads of stage cs are done before the stage is refilled
+      __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 << 8) | (3 << 14));
+      issue(t0 + 2 * KT, cs);
     }
   }
 
-  // O (lane: rows 16 wave + 4 g + j, dim 16 df + fr) -> LDS, dim-major so
-  // that each lane writes its 4 rows as one 16-byte store
+  // per-wave row sums; O rows -> LDS (over the stages, once every wave is
+  // done with them), then row segments out
   __syncthreads();
-#pragma unroll
-  for (int df = 0; df < 16; ++df)
-    *(f32x4_t*)&sO[(16 * df + fr) * kDecOT + wave * 16 + 4 * g] = o[df];
   if (g == 0) {
-    sM[wave * 16 + fr] = m_run;
-    sL[wave * 16 + fr] = l_run;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      sL[w][16 * rb + fr] = l_w[rb];
+      if (w == 0) sM[16 * rb + fr] = m_run[rb];
+    }
   }
+  float* sO = (float*)smem;
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sO[(16 * rb + 4 * g + j) * kDecOP + 64 * w + 16 * b + fr] = o[rb][b][j];
   __syncthreads();
+  // thread item c: row c >> 5, dims 8 (c & 31) .. + 7 (a wave writes two
+  // whole rows)
   if (splits == 1) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int c = tid + 256 * u, i = c & 63, d0 = (c >> 6) * 8;
+      const int c = tid + 256 * u, i = c >> 5, d0 = (c & 31) * 8;
       const int r = rg * 64 + i;
       if (r >= R) continue;
-      const float l = sL[i];
+      const float l = ((sL[0][i] + sL[1][i]) + sL[2][i]) + sL[3][i];
       const float inv = l > 0.f ? 1.f / l : 0.f;
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = sO[(d0 + e) * kDecOT + i] * inv;
+      const f32x4_t a = *(const f32x4_t*)&sO[i * kDecOP + d0];
+      const f32x4_t b = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
+      float v[8] = {a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv,
+                    b[0] * inv, b[1] * inv, b[2] * inv, b[3] * inv};
       dec_store<8>(p, z, r, d0, hs, v);
     }
     return;
@@ -604,16 +686,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   float* part = (float*)p.workspace + (((int64_t)z * n_rg + rg) * splits + split) * kDecPF;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const int c = tid + 256 * u, i = c & 63, d0 = (c >> 6) * 8;
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = sO[(d0 + e) * kDecOT + i];
-    *(f32x4_t*)(part + i * 256 + d0) = f32x4_t{v[0], v[1], v[2], v[3]};
-    *(f32x4_t*)(part + i * 256 + d0 + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+    const int c = tid + 256 * u, i = c >> 5, d0 = (c & 31) * 8;
+    *(f32x4_t*)(part + i * 256 + d0) = *(const f32x4_t*)&sO[i * kDecOP + d0];
+    *(f32x4_t*)(part + i * 256 + d0 + 4) = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
   }
   if (tid < 64) {
     part[64 * 256 + tid] = sM[tid];
-    part[64 * 256 + 64 + tid] = sL[tid];
+    part[64 * 256 + 64 + tid] = ((sL[0][tid] + sL[1][tid]) + sL[2][tid]) + sL[3][tid];
   }
 }
 

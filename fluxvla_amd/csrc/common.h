@@ -214,6 +214,25 @@ __device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds,
                : "memory");
 }
 
+// 4 bytes per lane into LDS (buffer_load_dword ... lds): lane l's word lands
+// at lds + 4 l.
+__device__ __forceinline__ void load_lds4(i32x4_t rsrc, uint32_t lds,
+                                          uint32_t off) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(off), "s"(rsrc)
+               : "memory");
+}
+
+// Wait until at most N vector memory operations of this wave are in flight
+// (the LDS loads above are invisible to the compiler's own accounting).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  // s_waitcnt: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 __device__ __forceinline__ bf16x8 bload8(__amdgpu_buffer_rsrc_t r,
                                          uint32_t off) {
   return __builtin_bit_cast(bf16x8,

@@ -401,13 +401,6 @@ struct TileCfg {
   static_assert(NT >= BM, "row sums");
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  // s_waitcnt: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] at [15:14]
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     GemmArgs p, int m_tiles, int n_tiles, int splits, int64_t kchunk,
