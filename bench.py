@@ -52,9 +52,10 @@ def measured_traffic():
 
 
 def time_dominant_kernel(model, iters=20):
-    """Prefix GeGLU GEMM (M=816, K=2048, N=16384 x 2 weights, rownorm):
-    the largest single kernel of the chunk.  Times `iters` back-to-back
-    launches on the current stream with HIP events."""
+    """Prefix GeGLU GEMM (M=816, K=2048, N=16384 x 2 weights, rownorm with
+    the row sums handed over by the O projection, as in the chunk): the
+    largest single kernel of the chunk.  Times `iters` back-to-back launches
+    on the current stream with HIP events."""
     import torch
 
     from fluxvla_amd import kernels as K
@@ -63,14 +64,17 @@ def time_dominant_kernel(model, iters=20):
     L = model.llm['layers'][0]
     x = b['pre_x'].view(-1, cfg.llm_hidden)
     h = b['pre_h']
+    ss = b['pre_ss'][0]
     for _ in range(3):
-        K.gemm_geglu(x, L['gate_w'], L['up_w'], out=h, rownorm_eps=cfg.rms_eps)
+        K.gemm_geglu(x, L['gate_w'], L['up_w'], out=h, rownorm_eps=cfg.rms_eps,
+                     ss_in=ss)
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
         enable_timing=True)
     e0.record(s)
     for _ in range(iters):
-        K.gemm_geglu(x, L['gate_w'], L['up_w'], out=h, rownorm_eps=cfg.rms_eps)
+        K.gemm_geglu(x, L['gate_w'], L['up_w'], out=h, rownorm_eps=cfg.rms_eps,
+                     ss_in=ss)
     e1.record(s)
     e1.synchronize()
     us = e0.elapsed_time(e1) * 1000.0 / iters
@@ -78,7 +82,7 @@ def time_dominant_kernel(model, iters=20):
     flops = 2.0 * M * N * Kd * 2
     achieved = flops / (us * 1e-6) / 1e12
     return {
-        'kernel': 'gemm_tile_kernel<256,256,GEGLU> (prefix gate/up, '
+        'kernel': 'gemm_geglu_wide_kernel (prefix gate/up, '
                   f'M={M} N={N}x2 K={Kd})',
         'bound': 'mfma',
         'achieved': round(achieved, 2),
@@ -225,20 +229,23 @@ def kernel_table(model):
     px = b['pre_x'].view(-1, cfg.llm_hidden)
     M = px.shape[0]
     kc0, vc0 = b['kc'][0], b['vc'][0]
+    # as in the chunk: the residual GEMMs hand the row sums of squares of x
+    # to the next fused RMSNorm
+    ss_a, ss_b = b['pre_ss'][0], b['pre_ss'][1]
     pre = [
         ('gemm_tile_kernel<64,128,QKV_ROPE> (prefix)', lambda: K.gemm_qkv_rope(
             px, L['qkv_w'], model.rope, b['pos_pre'], b['pre_q'].view(M, -1),
             kc0.view(T, D), vc0, H, D, rownorm_eps=cfg.rms_eps, row_group=S,
-            row_group_stride=T, v_ld=T), 2 * M * nq * cfg.llm_hidden),
+            row_group_stride=T, v_ld=T, ss_in=ss_b), 2 * M * nq * cfg.llm_hidden),
         ('gemm_tile_kernel<64,128,PLAIN> o-proj (prefix)', lambda: K.gemm(
             b['pre_ctx'].view(M, -1), L['o_w'], out=b['pre_h'][:, :cfg.llm_hidden],
-            residual=px), 2 * M * cfg.llm_hidden * H * D),
-        ('gemm_tile_kernel<256,256,GEGLU> (prefix)', lambda: K.gemm_geglu(
-            px, L['gate_w'], L['up_w'], out=b['pre_h'], rownorm_eps=cfg.rms_eps),
-         4 * M * cfg.llm_mlp * cfg.llm_hidden),
+            residual=px, ss_out=ss_a), 2 * M * cfg.llm_hidden * H * D),
+        ('gemm_geglu_wide_kernel (prefix)', lambda: K.gemm_geglu(
+            px, L['gate_w'], L['up_w'], out=b['pre_h'], rownorm_eps=cfg.rms_eps,
+            ss_in=ss_a), 4 * M * cfg.llm_mlp * cfg.llm_hidden),
         ('gemm_tile_kernel<64,128,PLAIN> down (prefix)', lambda: K.gemm(
             b['pre_h'], L['down_w'], out=b['pre_q'].view(M, -1)[:, :cfg.llm_hidden],
-            residual=px), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
+            residual=px, ss_out=ss_b), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
         ('attn_decode_kernel + merge (prefix)', lambda: K.mqa_attention(
             b['pre_q'], kc0[:, :S], vc0, b['pre_ctx'], kgrp=b['kgrp'][:, :S],
             qgrp=b['qgrp_pre'], v_transposed=True), 4 * H * S * S * D),
@@ -299,8 +306,10 @@ def kernel_only(iters=10):
     wg = (torch.randn(N, Kd, device=dev, generator=g) * 0.02).bfloat16()
     wu = (torch.randn(N, Kd, device=dev, generator=g) * 0.02).bfloat16()
     h = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    # the row sums of squares the O projection hands over in the chunk
+    ss = x.float().view(M, -1, 64).pow(2).sum(-1).t().contiguous()
     for _ in range(iters):
-        K.gemm_geglu(x, wg, wu, out=h, rownorm_eps=cfg.rms_eps)
+        K.gemm_geglu(x, wg, wu, out=h, rownorm_eps=cfg.rms_eps, ss_in=ss)
     torch.cuda.synchronize()
     src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)

@@ -62,6 +62,7 @@ class GemmDesc(ctypes.Structure):
         ('c_frag', c_vp),
         ('b_fp8', c_i32),
         ('b_scale', c_vp), ('b2_scale', c_vp),
+        ('ss_out', c_vp), ('ss_in', c_vp), ('ss_ld', c_i64), ('ss_parts', c_i32),
     ]
 
 

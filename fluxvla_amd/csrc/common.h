@@ -214,6 +214,15 @@ __device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds,
                : "memory");
 }
 
+// load_lds16 with a scalar offset added to every lane's offset.
+__device__ __forceinline__ void load_lds16_so(i32x4_t rsrc, uint32_t lds,
+                                              uint32_t off, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(off), "s"(rsrc), "s"(soff)
+               : "memory");
+}
+
 // 4 bytes per lane into LDS (buffer_load_dword ... lds): lane l's word lands
 // at lds + 4 l.
 __device__ __forceinline__ void load_lds4(i32x4_t rsrc, uint32_t lds,
@@ -271,16 +280,24 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Compile-time flag for generic lambdas (a kernel path chosen once, outside
+// its loops).
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), written through the
   // identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)).
   const float k2 = 1.5957691216057308f;  // 2 * sqrt(2 / pi)
   float u = k2 * (x + 0.044715f * x * x * x);
-  return x / (1.0f + __expf(-u));
+  // hardware reciprocal (1 ulp) instead of the IEEE division sequence
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-u));
 }
 
 __device__ __forceinline__ float silu(float x) {
-  return x / (1.0f + __expf(-x));
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
 }  // namespace fvx

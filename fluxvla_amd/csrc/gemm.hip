@@ -240,11 +240,14 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
 }
 
 // v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
+// ssq (PLAIN, may be NULL): receives the sum of squares of the values as
+// stored (bf16-rounded unless out_f32) over the cnt columns.
 template <int MODE>
 __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
                                           int64_t n, bool vec, int cnt,
                                           const float* v, const float* u,
-                                          float r, const EpiIn& in) {
+                                          float r, const EpiIn& in,
+                                          float* ssq = nullptr) {
   float x[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = v[e] * r;
@@ -326,6 +329,38 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
   else
     st_b8((bf16_t*)p.c + orow * p.ldc + n, x, vec, cnt);
   if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, n), pack8(x));
+  if (ssq) {
+    float xr[8];
+    if (p.out_f32) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xr[e] = x[e];
+    } else {
+      unpack8(pack8(x), xr);
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < cnt) q += xr[e] * xr[e];
+    *ssq = q;
+  }
+}
+
+// Sum over the parts of a row's handed-over sums of squares (ss_in), all
+// loads in flight, added in part order; parts past the view read as zero.
+__device__ __forceinline__ float ss_in_row(const GemmArgs& p, int64_t m) {
+  const __amdgpu_buffer_rsrc_t r =
+      make_rsrc(p.ss_in, rec_bytes((int64_t)p.ss_parts * p.ss_ld * 4));
+  float s = 0.f;
+  for (int q0 = 0; q0 < p.ss_parts; q0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      t[u] = bload1f(r, q0 + u < p.ss_parts ? (uint32_t)(((int64_t)(q0 + u) * p.ss_ld + m) * 4)
+                                            : kOOB);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += t[u];
+  }
+  return s;
 }
 
 // Host check: may the chunk epilogue use 16-byte accesses for full chunks?
@@ -488,6 +523,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   float ss[FM];
 #pragma unroll
   for (int i = 0; i < FM; ++i) ss[i] = 0.f;
+  // the fused RMSNorm sums A's squares in the K loop unless they are handed
+  // over (ss_in)
+  const bool sum_a = p.rownorm && !p.ss_in;
 
   // LDS row of B fragment j of this wave (GEGLU: gate blocks, then up)
   auto brow = [&](int j) {
@@ -498,7 +536,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   };
   // rows of a fragment are (multiple of 32) + lane % 32: swizzle (lane >> 1) & 7
   const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
-  auto compute = [&](int stage) {
+  auto compute = [&](int stage, auto with_ss) {
+    constexpr bool SS = decltype(with_ss)::value;
     const char* s = smem + stage * C::STAGE_BYTES;
     if (F8) {
       // two 64-k steps; lane (fr, hk) takes k = 64 ks + 32 hk .. + 31: A as
@@ -514,8 +553,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
           bf16x8 av[4];
 #pragma unroll
           for (int c = 0; c < 4; ++c) av[c] = *(const bf16x8*)(row + (((4 * hk + c) ^ sw) * 16));
+          if (SS)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
+            for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
           aq[i] = quant_fp8x32<32, 0>(av, &ae[i]);  // (row, 64-k step) scale
         }
 #pragma unroll
@@ -558,7 +598,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        ss[i] += sumsq8(af[b][i]);
+        if (SS) ss[i] += sumsq8(af[b][i]);
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
       }
@@ -567,24 +607,36 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
-  for (int t0 = 0; t0 < nk; t0 += STAGES) {
+  // handed-over row sums: thread t < BM takes row m0 + t (these loads wait
+  // with the first slabs)
+  float ss_pre = 0.f;
+  if (p.rownorm && p.ss_in && tid < BM && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
+  auto k_loop = [&](auto with_ss) {
+    for (int t0 = 0; t0 < nk; t0 += STAGES) {
 #pragma unroll
-    for (int s = 0; s < STAGES; ++s) {
-      const int t = t0 + s;
-      if (t >= nk) break;
-      wait_vmcnt<LPW * (STAGES - 2)>();  // this wave's loads of slab t landed
-      __syncthreads();                   // everyone's, and slab t-1 is consumed
-      issue(t + STAGES - 1, (s + STAGES - 1) % STAGES);
-      compute(s);
+      for (int s = 0; s < STAGES; ++s) {
+        const int t = t0 + s;
+        if (t >= nk) break;
+        wait_vmcnt<LPW * (STAGES - 2)>();  // this wave's loads of slab t landed
+        __syncthreads();                   // everyone's, and slab t-1 is consumed
+        issue(t + STAGES - 1, (s + STAGES - 1) % STAGES);
+        compute(s, with_ss);
+      }
     }
-  }
+  };
+  if (sum_a)
+    k_loop(BoolC<true>{});
+  else
+    k_loop(BoolC<false>{});
   // Loads past the end may still be in flight into the ring: drain them
   // before the ring becomes epilogue scratch.
   wait_vmcnt<0>();
 
   // Row sums of squares: lanes l and l ^ 32 hold the two k halves of row
   // l % 32 of block i (waves with wn > 0 computed the same sums).
-  if (wn == 0) {
+  if (!sum_a) {
+    if (tid < BM) sRow[tid] = ss_pre;
+  } else if (wn == 0) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const float s2 = ss[i] + __shfl_xor(ss[i], 32, 64);
@@ -595,8 +647,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 
   float* ws = (float*)((char*)p.workspace + kCounterBytes);
   const int64_t plane = (int64_t)splits * M * N;
+  // (handed-over sums are complete: split 0 carries them)
   if (splits > 1 && n_tile == 0 && tid < BM && m0 + tid < M)
-    ws[NB * plane + (int64_t)split * M + m0 + tid] = sRow[tid];
+    ws[NB * plane + (int64_t)split * M + m0 + tid] = (p.ss_in && split) ? 0.f : sRow[tid];
 
   // Epilogue: each 32-row block of the wave's sub-tile goes through the
   // wave's own LDS scratch [32][ELD] fp32 (GEGLU: gate columns, then up).
@@ -630,7 +683,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
         const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
         const int64_t m = rb + row, nn = nw0 + 8 * ch;
         const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        if (m >= M || cnt <= 0) continue;
+        // ss_out: the 8 lanes of a row (CH == 8: one 64-column block per
+        // wave) add their sums of squares; the shuffles run in every lane
+        constexpr bool SSO = MODE == FVX_GEMM_PLAIN && WNO == 64;
+        float ssq = 0.f;
+        if (m < M && cnt > 0) {
         float v[8], u[8];
         const float* sv = scr + row * ELD + 8 * ch;
 #pragma unroll
@@ -658,13 +715,174 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
             for (int x = 0; x < 8; ++x)
               if (x < cnt) dst[x] = b ? u[x] : v[x];
           }
-          continue;
+          goto next_item;
         }
         const float r = p.rownorm
                             ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps)
                             : 1.f;
-        epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e]);
+        epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e],
+                        (SSO && p.ss_out) ? &ssq : nullptr);
+        }
+      next_item:
+        if (SSO && p.ss_out && splits == 1) {
+          ssq += __shfl_xor(ssq, 1, 64);
+          ssq += __shfl_xor(ssq, 2, 64);
+          ssq += __shfl_xor(ssq, 4, 64);
+          if (ch == 0 && m < M) p.ss_out[(nw0 / 64) * p.ss_ld + m] = ssq;
+        }
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gemm_geglu_wide_kernel: the wide GeGLU projection (Gemma-2B's gate/up over
+// the prefix: M ~ 800, N = 16384 per weight, K = 2048).  A 256 x 256 tile
+// (256 rows x 128 columns of each weight) for 4 waves; wave (wm, wn) owns
+// rows 128 wm .. + 127 and columns 64 wn .. + 63 of both weights, i.e. 16
+// 32x32 accumulators held in AGPRs, so 8 fragment reads from LDS feed 16
+// MFMAs (the 8-wave 128 x 64 split of gemm_tile_kernel needs 12 for 16).
+// Each wave loads one 128-row band of every slab by LDS DMA (waves 0, 1 the
+// A rows, 2 the gate rows, 3 the up rows): per load one VGPR offset, the
+// slab advance in the scalar offset, rows past the operand out of the
+// buffer view (zeros).  K moves in 64-wide slabs through a 2-stage ring
+// with one barrier per slab; K % 64 == 0.  LDS rows are 128 bytes with the
+// 16-byte chunk index XOR (row >> 1) & 7, as in gemm_tile_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kGwBM = 256, kGwBN = 128;  // rows; columns of each weight
+constexpr int kGwStage = 512 * 128;
+constexpr int kGwELD = 128 + 4;          // epilogue scratch stride (floats)
+
+template <bool SUM_A>  // fused RMSNorm sums A's squares here (else: ss_in or none)
+__global__ __launch_bounds__(256, 1) void gemm_geglu_wide_kernel(GemmArgs p, int m_tiles,
+                                                                 int n_tiles, int vec_ok) {
+  __shared__ __align__(16) char smem[2 * kGwStage];
+  __shared__ float sRow[kGwBM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // XCD-aware tile order (consecutive ids: the M tiles of one weight panel)
+  const int nblk = m_tiles * n_tiles;
+  int bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
+  const int64_t M = p.m, N = p.n, K = p.k;
+  const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * kGwBN;
+  const int nk = (int)(K / 64);
+
+  // this wave's band
+  const bool isa = wave < 2;
+  const int64_t r0 = isa ? m0 + 128 * wave : n0;
+  const int64_t rlim = (isa ? M : N) - r0;
+  const int64_t nrows = rlim <= 0 ? 0 : (rlim < 128 ? rlim : 128);
+  const uint32_t ld2 = (uint32_t)(isa ? p.lda : p.ldb) * 2;
+  const bf16_t* band = isa ? (const bf16_t*)p.a + r0 * p.lda
+                           : (const bf16_t*)(wave == 2 ? p.b : p.b2) + r0 * p.ldb;
+  const i32x4_t rs = make_rsrc4(band, (uint32_t)(nrows * ld2));
+  // load i: LDS rows 128 wave + 8 i + (lane >> 3), slot lane & 7 holds global
+  // chunk slot ^ (((8 i + (lane >> 3)) >> 1) & 7)
+  const int lr = lane >> 3, lc = lane & 7;
+  const uint32_t vo0 = (uint32_t)lr * ld2 + 16u * (uint32_t)(lc ^ (lr >> 1));
+  const uint32_t vo1 = (uint32_t)lr * ld2 + 16u * (uint32_t)(lc ^ (lr >> 1) ^ 4);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * 128 * 128);
+  auto issue = [&](int t, int stage) {
+    const uint32_t so = (uint32_t)t * 128u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      load_lds16_so(rs, lds0 + stage * kGwStage + i * 1024,
+                    ((i & 1) ? vo1 : vo0) + (uint32_t)(8 * i) * ld2, so);
+  };
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+  const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
+  auto compute = [&](int stage) {
+    const char* s = smem + stage * kGwStage;
+    bf16x8 af[2][4], bfr[2][4];
+    auto rd = [&](int ks, int b) {
+      const int cpos = ((2 * ks + hk) ^ sw) * 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[b][i] = *(const bf16x8*)(s + (wm * 128 + 32 * i + fr) * 128 + cpos);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)  // gate blocks, then up blocks
+        bfr[b][j] = *(const bf16x8*)(s + (256 + (j >> 1) * 128 + wn * 64 + 32 * (j & 1) + fr) * 128 +
+                                     cpos);
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int b = ks & 1;
+      if (ks < 3) rd(ks + 1, b ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (SUM_A) ss[i] += sumsq8(af[b][i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
+      }
+    }
+  };
+
+  issue(0, 0);
+  // handed-over row sums: thread t takes row m0 + t (waits with slab 0)
+  float ss_pre = 0.f;
+  if (!SUM_A && p.rownorm && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
+  for (int t = 0; t < nk; ++t) {
+    wait_vmcnt<0>();   // this wave's loads of slab t landed
+    __syncthreads();   // everyone's, and slab t - 1 is consumed
+    if (t + 1 < nk) issue(t + 1, (t + 1) & 1);
+    compute(t & 1);
+  }
+
+  // row sums of squares: lanes l and l ^ 32 hold the two k halves of row
+  // l % 32 of block i
+  if (!SUM_A) {
+    sRow[tid] = ss_pre;
+  } else if (wn == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float s2 = ss[i] + __shfl_xor(ss[i], 32, 64);
+      if (lane < 32) sRow[wm * 128 + 32 * i + lane] = s2;
+    }
+  }
+  __syncthreads();  // also: every wave is done with the ring
+
+  // each 32-row block through the wave's LDS scratch [32][kGwELD] (gate
+  // columns 0..63, up 64..127); lane item q: row q / 8, columns 8 (q % 8)
+  float* scr = (float*)smem + wave * 32 * kGwELD;
+  const int64_t nw0 = n0 + wn * 64;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * kGwELD + 32 * j + fr] = acc[i][j][r];
+    const int64_t rb = m0 + wm * 128 + 32 * i;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int q = lane + 64 * e, row = q >> 3, ch = q & 7;
+      const int64_t m = rb + row, nn = nw0 + 8 * ch;
+      const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+      if (m >= M || cnt <= 0) continue;
+      float v[8], u[8];
+      const float* sv = scr + row * kGwELD + 8 * ch;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        v[x] = sv[x];
+        u[x] = sv[64 + x];
+      }
+      const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
+      EpiIn in;
+      epi_store<FVX_GEMM_GEGLU>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in);
     }
   }
 }
@@ -1093,6 +1311,11 @@ static int validate(const GemmArgs& d) {
               d.mode);
   FVX_REQUIRE(d.act >= 0 && d.act <= 2, FVX_ERR_ARG, "gemm: bad act %d",
               d.act);
+  FVX_REQUIRE(!d.ss_out || (d.mode == FVX_GEMM_PLAIN && d.m > 64 && d.ss_ld >= d.m &&
+                            aligned16(d.ss_out)),
+              FVX_ERR_ARG, "gemm: ss_out needs mode PLAIN, m > 64 and ss_ld >= m");
+  FVX_REQUIRE(!d.ss_in || (d.rownorm && d.ss_parts > 0 && d.ss_ld >= d.m), FVX_ERR_ARG,
+              "gemm: ss_in needs rownorm, ss_parts > 0 and ss_ld >= m");
   FVX_REQUIRE(!d.rownorm || d.rownorm_eps >= 0.f, FVX_ERR_ARG,
               "gemm: rownorm_eps must be >= 0");
   FVX_REQUIRE(d.row_group >= 0, FVX_ERR_ARG, "gemm: row_group must be >= 0");
@@ -1206,6 +1429,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   if (gg && ((d.m + 255) / 256) * ((d.n + 127) / 128) >= 256) t.cfg = 1;
   else t.cfg = tiles <= 256 ? 2 : 0;
   t.splits = 1;
+  if (d.ss_out) return t;  // written by the one-pass epilogue
   if (d.split_k > 0) t.splits = d.split_k;
   else if (t.cfg != 1 && tiles < 128 && d.k >= 4096) t.splits = 2;
   return t;
@@ -1217,7 +1441,7 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   const int bm = tile_bm(cfg, d.b_fp8), bn = kTileBN[cfg] / (gg ? 2 : 1);
   const int m_tiles = (int)((d.m + bm - 1) / bm);
   const int n_tiles = (int)((d.n + bn - 1) / bn);
-  if (splits < 1) splits = 1;
+  if (splits < 1 || d.ss_out) splits = 1;  // ss_out is written by the one-pass epilogue
   const int64_t bk = d.b_fp8 ? 128 : 64;
   int64_t kchunk = (d.k + splits - 1) / splits;
   kchunk = (kchunk + bk - 1) / bk * bk;
@@ -1237,6 +1461,16 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   FVX_REQUIRE(splits == 1 || aligned16(d.workspace), FVX_ERR_ALIGN,
               "gemm: workspace must be 16B aligned");
   const int vec_ok = epi_vec_ok(d) ? 1 : 0;
+  if (gg && cfg == 1 && !d.b_fp8 && splits == 1 && d.k % 64 == 0) {
+    // same 256 x (2 x 128) tiling as config 1, 4 waves of 128 x 128
+    if (d.rownorm && !d.ss_in)
+      hipLaunchKernelGGL(gemm_geglu_wide_kernel<true>, dim3((unsigned)(m_tiles * n_tiles)),
+                         dim3(256), 0, s, d, m_tiles, n_tiles, vec_ok);
+    else
+      hipLaunchKernelGGL(gemm_geglu_wide_kernel<false>, dim3((unsigned)(m_tiles * n_tiles)),
+                         dim3(256), 0, s, d, m_tiles, n_tiles, vec_ok);
+    return launch_status("gemm(geglu wide)");
+  }
   dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
 #define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_)                                   \
   hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_>), grid,  \

@@ -301,13 +301,42 @@ def _run_gemm(d):
     _lib.call('fvx_gemm', ctypes.byref(d), _stream())
 
 
+def ss_parts(n):
+    """Parts of the row sums of squares a GEMM with n output columns hands
+    over (one per 64-column block)."""
+    return (n + 63) // 64
+
+
+def _set_ss(d, rownorm_eps, ss_in=None, ss_out=None):
+    """Row sums of squares handed between GEMMs: ``ss_out`` (fp32 [parts,
+    ld], parts = ss_parts(n)) receives the producer's per-block sums of its
+    squared bf16 outputs; ``ss_in`` (same layout, from the GEMM that wrote
+    this GEMM's A) replaces the fused RMSNorm's pass over A."""
+    if rownorm_eps is not None:
+        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    if ss_in is not None:
+        if rownorm_eps is None:
+            raise ValueError('ss_in needs rownorm_eps')
+        _check(ss_in, 'ss_in', dtype=torch.float32, contiguous=False)
+        if ss_in.dim() != 2 or ss_in.stride(1) != 1 or ss_in.shape[1] < d.m:
+            raise ValueError('ss_in must be [parts, >= m] with unit row stride')
+        d.ss_in, d.ss_parts, d.ss_ld = ss_in.data_ptr(), ss_in.shape[0], ss_in.stride(0)
+    if ss_out is not None:
+        _check(ss_out, 'ss_out', dtype=torch.float32, contiguous=False)
+        if (ss_out.dim() != 2 or ss_out.stride(1) != 1 or ss_out.shape[1] < d.m or
+                ss_out.shape[0] < ss_parts(d.n)):
+            raise ValueError(f'ss_out must be [>= {ss_parts(d.n)}, >= m] with unit row stride')
+        d.ss_out, d.ss_ld = ss_out.data_ptr(), ss_out.stride(0)
+
+
 def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
          gate=None, gate_group=1, pos=None, pos_period=0, act=_lib.ACT_NONE,
          rownorm_eps=None, out_f32=False, row_group=0, row_group_stride=0,
-         split_k=0, c_frag=None):
+         split_k=0, c_frag=None, ss_in=None, ss_out=None):
     """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order.
     ``a`` may be a FragA and ``weight`` a FragB; ``c_frag`` (a FragA with
-    k == n) also receives the output in the fragment-major layout."""
+    k == n) also receives the output in the fragment-major layout;
+    ``ss_in`` / ``ss_out``: see _set_ss."""
     d = _gemm_desc(a, weight)
     if out is None:
         out = torch.empty(*_lead_shape(a), d.n,
@@ -336,8 +365,7 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
         _, d.ldp = _rows_ld(pos, 'pos')
         d.pos, d.pos_period = pos.data_ptr(), pos_period or pos.shape[0]
     d.act, d.mode, d.out_f32 = int(act), _lib.GEMM_PLAIN, int(bool(out_f32))
-    if rownorm_eps is not None:
-        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    _set_ss(d, rownorm_eps, ss_in, ss_out)
     d.row_group, d.row_group_stride = row_group, row_group_stride
     d.split_k = split_k
     _set_c_frag(d, c_frag)
@@ -346,7 +374,7 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
 
 
 def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
-               c_frag=None):
+               c_frag=None, ss_in=None):
     """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T)."""
     d = _gemm_desc(a, gate_w)
     if isinstance(gate_w, Fp8Weight):
@@ -371,8 +399,7 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
     _check(out, 'out', contiguous=False)
     _, d.ldc = _rows_ld(out, 'out')
     d.c, d.mode = out.data_ptr(), _lib.GEMM_GEGLU
-    if rownorm_eps is not None:
-        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    _set_ss(d, rownorm_eps, ss_in)
     d.split_k = split_k
     _set_c_frag(d, c_frag)
     _run_gemm(d)
@@ -381,7 +408,7 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
 
 def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
                   head_dim, rownorm_eps=None, row_group=0, row_group_stride=0,
-                  split_k=0, v_ld=None):
+                  split_k=0, v_ld=None, ss_in=None):
     """[q|k|v] = a @ w_qkv^T with pair-interleaved RoPE on q and k.
 
     rope: fp32 [max_pos, head_dim/2, 2] (cos, sin); positions: int32 [M].
@@ -405,8 +432,7 @@ def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
     else:
         d.v_out, d.ldv, d.v_transposed = v_out.data_ptr(), int(v_ld), 1
     d.n_q_heads, d.head_dim = n_q_heads, head_dim
-    if rownorm_eps is not None:
-        d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    _set_ss(d, rownorm_eps, ss_in)
     d.row_group, d.row_group_stride = row_group, row_group_stride
     d.split_k = split_k
     _run_gemm(d)

@@ -398,6 +398,8 @@ class PI0Inference:
             'pre_q': e(B, S, cfg.heads * D),
             'pre_ctx': e(B, S, cfg.heads * D),
             'pre_h': e(B * S, cfg.llm_mlp),
+            # row sums of squares of x handed between prefix GEMMs
+            'pre_ss': e(2, K.ss_parts(cfg.llm_hidden), B * S, dt=torch.float32),
             # K cache [layer][batch][token][dim] (pair-interleaved dims);
             # V cache transposed [layer][batch][dim][token]
             'kc': e(cfg.exp_layers, B, T, D),
@@ -470,6 +472,9 @@ class PI0Inference:
                        scale=math.sqrt(hid), row_group=cfg.max_prompt_len,
                        row_group_stride=S)
         n = len(W['layers'])
+        # row sums of squares of x handed from the residual GEMMs to the
+        # next fused RMSNorm (O proj -> gate/up, down -> next QKV)
+        ss = b['pre_ss'] if B * S > 64 else [None, None]
         for i, L in enumerate(W['layers']):
             kc, vc = b['kc'][i], b['vc'][i]
             last = i == n - 1
@@ -481,16 +486,18 @@ class PI0Inference:
                             b['pre_q'].view(B * S, -1),
                             kc.view(B * T, D), vc, 0 if last else cfg.heads,
                             D, rownorm_eps=cfg.rms_eps, row_group=S,
-                            row_group_stride=T, v_ld=T)
+                            row_group_stride=T, v_ld=T,
+                            ss_in=ss[1] if i > 0 else None)
             if last:
                 break
             K.mqa_attention(b['pre_q'], kc[:, :S], vc, b['pre_ctx'],
                             kgrp=b['kgrp'][:, :S], qgrp=b['qgrp_pre'],
                             v_transposed=True)
-            K.gemm(b['pre_ctx'].view(B * S, -1), L['o_w'], out=x, residual=x)
+            K.gemm(b['pre_ctx'].view(B * S, -1), L['o_w'], out=x, residual=x,
+                   ss_out=ss[0])
             K.gemm_geglu(x, L['gate_w'], L['up_w'], out=b['pre_h'],
-                         rownorm_eps=cfg.rms_eps)
-            K.gemm(b['pre_h'], L['down_w'], out=x, residual=x)
+                         rownorm_eps=cfg.rms_eps, ss_in=ss[0])
+            K.gemm(b['pre_h'], L['down_w'], out=x, residual=x, ss_out=ss[1])
 
     def _frag_ok(self, B):
         """bs=1 expert GEMMs (M = suffix_len <= 64) run fragment-major."""

@@ -133,6 +133,18 @@ typedef struct fvx_gemm_desc {
   int32_t b_fp8;
   const float* b_scale;            /* [N] */
   const float* b2_scale;           /* [N], GEGLU up weight */
+  /* Row sums of squares handed from one GEMM to the next (no counterpart in
+   * the reference; it lets the fused RMSNorm of a rownorm GEMM skip its pass
+   * over A when A is the output of the previous GEMM):
+   *   ss_out (PLAIN, M > 64): ss_out[(n / 64) * ss_ld + m] = sum over the
+   *           64-column block of n of bf16(c[m][n'])^2 (ceil(N / 64) parts);
+   *   ss_in  (rownorm): the sum of squares of row m of A is taken as
+   *           ss_in[0 * ss_ld + m] + ... + ss_in[(ss_parts - 1) * ss_ld + m],
+   *           added in that order (deterministic). */
+  float* ss_out;
+  const float* ss_in;
+  int64_t ss_ld;
+  int32_t ss_parts;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */
