@@ -287,6 +287,21 @@ struct BoolC {
   static constexpr bool value = B;
 };
 
+// Compile-time loop: f(IntC<B>{}), ..., f(IntC<E - 1>{}).  Array indices
+// derived from the argument are constants before any optimization, so a
+// large register array indexed in the body stays in registers.
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(IntC<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), written through the
   // identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)).

@@ -240,14 +240,14 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
 }
 
 // v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
-// ssq (PLAIN, may be NULL): receives the sum of squares of the values as
+// want_ssq (PLAIN): ssq receives the sum of squares of the values as
 // stored (bf16-rounded unless out_f32) over the cnt columns.
 template <int MODE>
 __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
                                           int64_t n, bool vec, int cnt,
                                           const float* v, const float* u,
                                           float r, const EpiIn& in,
-                                          float* ssq = nullptr) {
+                                          bool want_ssq, float& ssq) {
   float x[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = v[e] * r;
@@ -329,7 +329,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
   else
     st_b8((bf16_t*)p.c + orow * p.ldc + n, x, vec, cnt);
   if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, n), pack8(x));
-  if (ssq) {
+  if (want_ssq) {
     float xr[8];
     if (p.out_f32) {
 #pragma unroll
@@ -341,7 +341,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       if (e < cnt) q += xr[e] * xr[e];
-    *ssq = q;
+    ssq = q;
   }
 }
 
@@ -721,7 +721,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
                             ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps)
                             : 1.f;
         epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e],
-                        (SSO && p.ss_out) ? &ssq : nullptr);
+                        SSO && p.ss_out, ssq);
         }
       next_item:
         if (SSO && p.ss_out && splits == 1) {
@@ -736,26 +736,34 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// gemm_geglu_wide_kernel: the wide GeGLU projection (Gemma-2B's gate/up over
-// the prefix: M ~ 800, N = 16384 per weight, K = 2048).  A 256 x 256 tile
-// (256 rows x 128 columns of each weight) for 4 waves; wave (wm, wn) owns
-// rows 128 wm .. + 127 and columns 64 wn .. + 63 of both weights, i.e. 16
-// 32x32 accumulators held in AGPRs, so 8 fragment reads from LDS feed 16
-// MFMAs (the 8-wave 128 x 64 split of gemm_tile_kernel needs 12 for 16).
+// gemm_wide_kernel: large-M GEMMs (the prefix gate/up projection at every
+// batch; the other prefix and SigLIP GEMMs once a batch gives them >= 128
+// such tiles).  A 256 x 256 tile (GEGLU: 256 rows x 128 columns of each
+// weight) for 4 waves; wave (wm, wn) owns rows 128 wm .. + 127 and columns
+// 128 wn .. + 127 (GEGLU: 64 wn .. + 63 of both weights), i.e. 16 32x32
+// accumulators held in AGPRs, so 8 fragment reads from LDS feed 16 MFMAs
+// (the 8-wave 128 x 64 split of gemm_tile_kernel needs 12 for 16).
 // Each wave loads one 128-row band of every slab by LDS DMA (waves 0, 1 the
-// A rows, 2 the gate rows, 3 the up rows): per load one VGPR offset, the
-// slab advance in the scalar offset, rows past the operand out of the
-// buffer view (zeros).  K moves in 64-wide slabs through a 2-stage ring
-// with one barrier per slab; K % 64 == 0.  LDS rows are 128 bytes with the
-// 16-byte chunk index XOR (row >> 1) & 7, as in gemm_tile_kernel.
+// A rows, 2 and 3 the B rows: GEGLU the gate and the up rows): per load one
+// VGPR offset, the slab advance in the scalar offset, rows past the operand
+// out of the buffer view (zeros).  K moves in 64-wide slabs through a
+// 2-stage ring with one barrier per slab; K % 64 == 0, one pass (no split).
+// LDS rows are 128 bytes with the 16-byte chunk index XOR (row >> 1) & 7,
+// as in gemm_tile_kernel.  The epilogue is gemm_tile_kernel's (epi_load /
+// epi_store per 8-column chunk), including ss_out for PLAIN.
 // ---------------------------------------------------------------------------
-constexpr int kGwBM = 256, kGwBN = 128;  // rows; columns of each weight
+constexpr int kGwBM = 256, kGwBN = 256;  // rows, columns (GEGLU: 2 x 128)
+#ifndef FVX_WIDE_EB
+#define FVX_WIDE_EB 4
+#endif
 constexpr int kGwStage = 512 * 128;
 constexpr int kGwELD = 128 + 4;          // epilogue scratch stride (floats)
 
-template <bool SUM_A>  // fused RMSNorm sums A's squares here (else: ss_in or none)
-__global__ __launch_bounds__(256, 1) void gemm_geglu_wide_kernel(GemmArgs p, int m_tiles,
-                                                                 int n_tiles, int vec_ok) {
+template <int MODE, bool SUM_A>  // SUM_A: the fused RMSNorm sums A's squares here
+__global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_tiles,
+                                                           int n_tiles, int vec_ok) {
+  constexpr bool GG = MODE == FVX_GEMM_GEGLU;
+  constexpr int WNO = GG ? 64 : 128;  // output columns per wave
   __shared__ __align__(16) char smem[2 * kGwStage];
   __shared__ float sRow[kGwBM];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -768,17 +776,17 @@ __global__ __launch_bounds__(256, 1) void gemm_geglu_wide_kernel(GemmArgs p, int
   if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
   const int64_t M = p.m, N = p.n, K = p.k;
-  const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * kGwBN;
+  const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * (GG ? 128 : 256);
   const int nk = (int)(K / 64);
 
-  // this wave's band
+  // this wave's band: 128 rows of A (waves 0, 1) or of B (2, 3)
   const bool isa = wave < 2;
-  const int64_t r0 = isa ? m0 + 128 * wave : n0;
+  const int64_t r0 = isa ? m0 + 128 * wave : (GG ? n0 : n0 + 128 * (wave - 2));
   const int64_t rlim = (isa ? M : N) - r0;
   const int64_t nrows = rlim <= 0 ? 0 : (rlim < 128 ? rlim : 128);
   const uint32_t ld2 = (uint32_t)(isa ? p.lda : p.ldb) * 2;
   const bf16_t* band = isa ? (const bf16_t*)p.a + r0 * p.lda
-                           : (const bf16_t*)(wave == 2 ? p.b : p.b2) + r0 * p.ldb;
+                           : (const bf16_t*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb;
   const i32x4_t rs = make_rsrc4(band, (uint32_t)(nrows * ld2));
   // load i: LDS rows 128 wave + 8 i + (lane >> 3), slot lane & 7 holds global
   // chunk slot ^ (((8 i + (lane >> 3)) >> 1) & 7)
@@ -803,6 +811,10 @@ __global__ __launch_bounds__(256, 1) void gemm_geglu_wide_kernel(GemmArgs p, int
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   float ss[4] = {0.f, 0.f, 0.f, 0.f};
   const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
+  // LDS row of B fragment j of this wave (GEGLU: gate blocks, then up)
+  auto brow = [&](int j) {
+    return GG ? 256 + (j >> 1) * 128 + wn * 64 + 32 * (j & 1) : 256 + wn * 128 + 32 * j;
+  };
   auto compute = [&](int stage) {
     const char* s = smem + stage * kGwStage;
     bf16x8 af[2][4], bfr[2][4];
@@ -812,9 +824,7 @@ __global__ __launch_bounds__(256, 1) void gemm_geglu_wide_kernel(GemmArgs p, int
       for (int i = 0; i < 4; ++i)
         af[b][i] = *(const bf16x8*)(s + (wm * 128 + 32 * i + fr) * 128 + cpos);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)  // gate blocks, then up blocks
-        bfr[b][j] = *(const bf16x8*)(s + (256 + (j >> 1) * 128 + wn * 64 + 32 * (j & 1) + fr) * 128 +
-                                     cpos);
+      for (int j = 0; j < 4; ++j) bfr[b][j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
     };
     rd(0, 0);
 #pragma unroll
@@ -855,34 +865,70 @@ __global__ __launch_bounds__(256, 1) void gemm_geglu_wide_kernel(GemmArgs p, int
   }
   __syncthreads();  // also: every wave is done with the ring
 
-  // each 32-row block through the wave's LDS scratch [32][kGwELD] (gate
-  // columns 0..63, up 64..127); lane item q: row q / 8, columns 8 (q % 8)
+  // each 32-row block through the wave's LDS scratch [32][kGwELD] (GEGLU:
+  // gate columns 0..63, up 64..127); lane item q: row q / CH, 8 columns
+  // 8 (q % CH) with CH = WNO / 8 chunks per row
+  constexpr int CH = WNO / 8, ITEMS = 32 * CH / 64, EB = FVX_WIDE_EB < ITEMS ? FVX_WIDE_EB : ITEMS;
   float* scr = (float*)smem + wave * 32 * kGwELD;
-  const int64_t nw0 = n0 + wn * 64;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  const int64_t nw0 = n0 + wn * WNO;
+  // block i of the accumulators -> scratch (compile-time indices, so the
+  // accumulators stay in registers); the item loops below are real loops,
+  // which keeps the epilogue code small enough for the kernel arguments to
+  // stay in SGPRs
+  auto to_scr = [&](auto ic) {
+    constexpr int i = decltype(ic)::value;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * kGwELD + 32 * j + fr] = acc[i][j][r];
+  };
+#pragma unroll 1
+  for (int i = 0; i < 4; ++i) {
+    switch (i) {
+      case 0: to_scr(IntC<0>{}); break;
+      case 1: to_scr(IntC<1>{}); break;
+      case 2: to_scr(IntC<2>{}); break;
+      default: to_scr(IntC<3>{}); break;
+    }
     const int64_t rb = m0 + wm * 128 + 32 * i;
+#pragma unroll 1
+    for (int e0 = 0; e0 < ITEMS; e0 += EB) {
+      EpiIn in[EB];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int q = lane + 64 * e, row = q >> 3, ch = q & 7;
-      const int64_t m = rb + row, nn = nw0 + 8 * ch;
-      const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-      if (m >= M || cnt <= 0) continue;
-      float v[8], u[8];
-      const float* sv = scr + row * kGwELD + 8 * ch;
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        v[x] = sv[x];
-        u[x] = sv[64 + x];
+      for (int e = 0; e < EB; ++e) {
+        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
+        const int64_t nn = nw0 + 8 * ch;
+        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+        epi_load<MODE>(p, rb + row, nn, vec_ok && cnt == 8, cnt, in[e]);
       }
-      const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
-      EpiIn in;
-      epi_store<FVX_GEMM_GEGLU>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in);
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
+        const int64_t m = rb + row, nn = nw0 + 8 * ch;
+        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+        constexpr bool SSO = MODE == FVX_GEMM_PLAIN;
+        float ssq = 0.f;
+        if (m < M && cnt > 0) {
+          float v[8], u[8];
+          const float* sv = scr + row * kGwELD + 8 * ch;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            v[x] = sv[x];
+            u[x] = GG ? sv[64 + x] : 0.f;
+          }
+          const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
+          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e],
+                          SSO && p.ss_out, ssq);
+        }
+        if (SSO && p.ss_out) {
+          // the 8 lanes of a row's 64-column block add their sums
+          ssq += __shfl_xor(ssq, 1, 64);
+          ssq += __shfl_xor(ssq, 2, 64);
+          ssq += __shfl_xor(ssq, 4, 64);
+          if ((ch & 7) == 0 && m < M && nn < N) p.ss_out[(nn / 64) * p.ss_ld + m] = ssq;
+        }
+      }
     }
   }
 }
@@ -1191,7 +1237,8 @@ __global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
       u[e] *= wsc2[e];
     }
   }
-  epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in);
+  float no_ssq;
+  epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in, false, no_ssq);
 }
 
 // Sum of the split partials of either GEMM kernel + epilogue.  Thread t of
@@ -1407,9 +1454,16 @@ static int validate(const GemmArgs& d) {
 // Small tiles win on these shapes: the extra workgroups hide more latency
 // than they cost in LDS traffic per flop; deeper rings win only when the
 // grid leaves CUs idle.
-static const int kTileBM[] = {64, 256, 64};
-static const int kTileBN[] = {128, 256, 128};
-constexpr int kTileCfgs = 3;
+static const int kTileBM[] = {64, 256, 64, 256};
+static const int kTileBN[] = {128, 256, 128, 256};
+constexpr int kTileCfgs = 4;
+constexpr int kWideCfg = 3;  // gemm_wide_kernel
+#ifndef FVX_WIDE_MIN_TILES
+#define FVX_WIDE_MIN_TILES 128
+#endif
+#ifndef FVX_WIDE_MIN_K
+#define FVX_WIDE_MIN_K 2048
+#endif
 
 static int tile_bm(int cfg, int fp8) { return cfg == 1 && fp8 ? 128 : kTileBM[cfg]; }
 
@@ -1417,18 +1471,34 @@ struct TilePlan {
   int cfg, splits;
 };
 
-// Config 1 for GeGLU projections that still give >= 256 of its tiles; else
-// 64 x 128 tiles, with the 4-stage ring (config 2) when they number <= 256.
-// A long K (>= 4096) with fewer than 128 tiles is split in two (SigLIP fc2);
-// with more tiles the partials cost more than the idle CUs.
+// The wide kernel (bf16, K % 64 == 0, PLAIN / GEGLU / QKV_ROPE) once its
+// 256 x 256 tiles number >= 256 (GEGLU) or, for PLAIN / QKV_ROPE, fill the
+// CUs (below) with K >= FVX_WIDE_MIN_K; config 1
+// for other GeGLU projections with >= 256 such tiles (fp8); else 64 x 128
+// tiles, with the 4-stage ring (config 2) when they number <= 256.  A long
+// K (>= 4096) with fewer than 128 tiles is split in two (SigLIP fc2); with
+// more tiles the partials cost more than the idle CUs.
 static TilePlan plan_tile(const GemmArgs& d) {
   TilePlan t;
   const bool gg = d.mode == FVX_GEMM_GEGLU;
   const int64_t bn = 128 / (gg ? 2 : 1);
   const int64_t tiles = ((d.m + 63) / 64) * ((d.n + bn - 1) / bn);
-  if (gg && ((d.m + 255) / 256) * ((d.n + 127) / 128) >= 256) t.cfg = 1;
-  else t.cfg = tiles <= 256 ? 2 : 0;
+  const int64_t wtiles = ((d.m + 255) / 256) * ((d.n + 2 * bn - 1) / (2 * bn));
+  const bool wide_ok = !d.b_fp8 && d.k % 64 == 0 && d.split_k <= 1 &&
+                       (d.mode == FVX_GEMM_PLAIN || gg || d.mode == FVX_GEMM_QKV_ROPE);
   t.splits = 1;
+  // PLAIN / QKV: one workgroup of 256 x 256 per CU at a time, so the tiles
+  // must fill the last round (>= 3/4 of 256 CUs) and K must amortize the
+  // epilogue's 256 x 256 operand stream (measured: K = 2048 gains a little,
+  // K = 1152 loses; 260 tiles lose to the 64 x 128 kernel)
+  const int64_t rounds = (wtiles + 255) / 256;
+  const bool fill = wtiles >= FVX_WIDE_MIN_TILES && 4 * wtiles >= 3 * 256 * rounds;
+  if (wide_ok && (gg ? wtiles >= 256 : (fill && d.k >= FVX_WIDE_MIN_K))) {
+    t.cfg = kWideCfg;
+    return t;
+  }
+  if (gg && wtiles >= 256) t.cfg = 1;
+  else t.cfg = tiles <= 256 ? 2 : 0;
   if (d.ss_out) return t;  // written by the one-pass epilogue
   if (d.split_k > 0) t.splits = d.split_k;
   else if (t.cfg != 1 && tiles < 128 && d.k >= 4096) t.splits = 2;
@@ -1461,15 +1531,25 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   FVX_REQUIRE(splits == 1 || aligned16(d.workspace), FVX_ERR_ALIGN,
               "gemm: workspace must be 16B aligned");
   const int vec_ok = epi_vec_ok(d) ? 1 : 0;
-  if (gg && cfg == 1 && !d.b_fp8 && splits == 1 && d.k % 64 == 0) {
-    // same 256 x (2 x 128) tiling as config 1, 4 waves of 128 x 128
-    if (d.rownorm && !d.ss_in)
-      hipLaunchKernelGGL(gemm_geglu_wide_kernel<true>, dim3((unsigned)(m_tiles * n_tiles)),
-                         dim3(256), 0, s, d, m_tiles, n_tiles, vec_ok);
-    else
-      hipLaunchKernelGGL(gemm_geglu_wide_kernel<false>, dim3((unsigned)(m_tiles * n_tiles)),
-                         dim3(256), 0, s, d, m_tiles, n_tiles, vec_ok);
-    return launch_status("gemm(geglu wide)");
+  if (cfg == kWideCfg) {
+    FVX_REQUIRE(!d.b_fp8 && d.k % 64 == 0 && d.mode != FVX_GEMM_EULER, FVX_ERR_ARG,
+                "gemm: the wide kernel needs bf16 weights, K %% 64 == 0, no EULER");
+    // 256 x 256 tiles (GEGLU: 256 x 2 x 128), 4 waves of 128 x 128
+    const unsigned nb = (unsigned)(m_tiles * n_tiles);
+#define LW(MODE)                                                                    \
+  if (d.rownorm && !d.ss_in)                                                        \
+    hipLaunchKernelGGL((gemm_wide_kernel<MODE, true>), dim3(nb), dim3(256), 0, s, d,  \
+                       m_tiles, n_tiles, vec_ok);                                   \
+  else                                                                              \
+    hipLaunchKernelGGL((gemm_wide_kernel<MODE, false>), dim3(nb), dim3(256), 0, s, d, \
+                       m_tiles, n_tiles, vec_ok)
+    switch (d.mode) {
+      case FVX_GEMM_GEGLU: LW(FVX_GEMM_GEGLU); break;
+      case FVX_GEMM_QKV_ROPE: LW(FVX_GEMM_QKV_ROPE); break;
+      default: LW(FVX_GEMM_PLAIN); break;
+    }
+#undef LW
+    return launch_status("gemm(wide)");
   }
   dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
 #define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_)                                   \
