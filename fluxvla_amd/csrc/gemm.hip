@@ -958,6 +958,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
 // dirty in a non-coherent L2, which is what a release/acquire pair would
 // have to write back and invalidate (tens of microseconds per GEMM here).
 constexpr int kSkWaves = 8;
+// fp8: 4 waves, each with the full 512-register file (its A quantization
+// does not fit 256 registers with two sets of loads in flight)
+constexpr int sk_waves(bool f8) { return f8 ? 4 : kSkWaves; }
 constexpr int kSkStep = 3;    // MFMA steps (of 32 k) per register set (GEGLU: 2)
 constexpr int kSkMaxSplits = 4;
 
@@ -993,13 +996,13 @@ __device__ __forceinline__ void sc1_load8(__amdgpu_buffer_rsrc_t r, int off,
 }
 
 template <int MODE, bool F8>
-__global__ __launch_bounds__(512) void gemm_skinny_kernel(GemmArgs p,
+__global__ __launch_bounds__(64 * sk_waves(F8)) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
                                                           int64_t kc,
                                                           int vec_ok) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
   // F8: one register set = one 128-k step of the fp8 MFMA (4 A blocks of 32)
-  constexpr int W = kSkWaves, S = F8 ? 4 : (NB == 2 ? 2 : kSkStep);
+  constexpr int W = sk_waves(F8), S = F8 ? 4 : (NB == 2 ? 2 : kSkStep);
   __shared__ float sP[W][NB][64][16 + 1];
   __shared__ float sS[W][64];
   __shared__ int s_last;
@@ -1305,7 +1308,7 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
   SkinnyPlan s;
   const int nb = d.mode == FVX_GEMM_GEGLU ? 2 : 1;
   s.n_tiles = (int)((d.n + 15) / 16);
-  const int64_t unit = (d.b_fp8 ? 128 : 32) * kSkWaves;
+  const int64_t unit = (d.b_fp8 ? 128 : 32) * sk_waves(d.b_fp8);
   const int64_t max_splits = (d.k + unit - 1) / unit;
   int64_t sp = d.split_k;
   if (sp <= 0) {
@@ -1619,7 +1622,7 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
     const int vec_ok = epi_vec_ok(d) ? 1 : 0;
 #define L(MODE)                                                                 \
   if (d.b_fp8)                                                                   \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true>), grid, dim3(64 * kSkWaves), \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true>), grid, dim3(64 * sk_waves(true)), \
                        0, s, d, sp.splits, sp.kc, vec_ok);                       \
   else                                                                           \
     hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false>), grid, dim3(64 * kSkWaves), \
