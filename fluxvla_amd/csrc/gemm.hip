@@ -934,6 +934,219 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
 }
 
 // ---------------------------------------------------------------------------
+// gemm_wide_f8_kernel: gemm_wide_kernel with fp8 (e4m3) weights.  Same tile
+// and wave split; the MFMA is the block-scaled v_mfma_scale_f32_32x32x64
+// (A and B as e4m3, one power-of-two scale per A row and 64-k slab, the
+// weights' per-channel scales applied in the epilogue).  The bf16 A tile is
+// quantized as it feeds the MFMAs, the same way as gemm_tile_kernel's fp8
+// path: one scale per (row, 64-k slab) from the slab's largest magnitude,
+// shared by the two lanes (l, l ^ 32) holding the row's two 32-k halves.
+// Slabs of 64 k: A 256 rows x 128 B (bf16) and B 256 rows x 64 B (e4m3),
+// 48 KiB per stage, a 3-stage ring.  B rows carry the 16-byte chunk index
+// XOR (row >> 2) & 3 (4 chunks per 64-byte row).
+// ---------------------------------------------------------------------------
+constexpr int kGw8AStage = 256 * 128, kGw8Stage = kGw8AStage + 256 * 64;
+constexpr int kGw8Stages = 3;
+
+template <int MODE, bool SUM_A>
+__global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_tiles,
+                                                              int n_tiles, int vec_ok) {
+  constexpr bool GG = MODE == FVX_GEMM_GEGLU;
+  constexpr int WNO = GG ? 64 : 128;  // output columns per wave
+  __shared__ __align__(16) char smem[kGw8Stages * kGw8Stage];
+  __shared__ float sRow[kGwBM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int nblk = m_tiles * n_tiles;
+  int bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
+  const int64_t M = p.m, N = p.n, K = p.k;
+  const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * (GG ? 128 : 256);
+  const int nk = (int)(K / 64);
+
+  // this wave's band: 128 rows of A (waves 0, 1; 16 loads of 8 rows x 128 B
+  // per slab) or of B (2, 3; 8 loads of 16 rows x 64 B)
+  const bool isa = wave < 2;
+  const int64_t r0 = isa ? m0 + 128 * wave : (GG ? n0 : n0 + 128 * (wave - 2));
+  const int64_t rlim = (isa ? M : N) - r0;
+  const int64_t nrows = rlim <= 0 ? 0 : (rlim < 128 ? rlim : 128);
+  const uint32_t ld = isa ? (uint32_t)p.lda * 2 : (uint32_t)p.ldb;  // bytes per row
+  const char* band = isa ? (const char*)p.a + r0 * p.lda * 2
+                         : (const char*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb;
+  const i32x4_t rs = make_rsrc4(band, (uint32_t)(nrows * ld));
+  uint32_t vo0, vo1, lds0;
+  if (isa) {
+    // rows 8 i + (lane >> 3), slot lane & 7 <- chunk slot ^ ((row >> 1) & 7)
+    const int lr = lane >> 3, lc = lane & 7;
+    vo0 = (uint32_t)lr * ld + 16u * (uint32_t)(lc ^ (lr >> 1));
+    vo1 = (uint32_t)lr * ld + 16u * (uint32_t)(lc ^ (lr >> 1) ^ 4);
+    lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * 128 * 128);
+  } else {
+    // rows 16 i + (lane >> 2), slot lane & 3 <- chunk slot ^ ((row >> 2) & 3)
+    const int lr = lane >> 2, lc = lane & 3;
+    vo0 = vo1 = (uint32_t)lr * ld + 16u * (uint32_t)(lc ^ ((lr >> 2) & 3));
+    lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + kGw8AStage + (wave - 2) * 128 * 64);
+  }
+  auto issue = [&](int t, int stage) {
+    if (isa) {
+      const uint32_t so = (uint32_t)t * 128u;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        load_lds16_so(rs, lds0 + stage * kGw8Stage + i * 1024,
+                      ((i & 1) ? vo1 : vo0) + (uint32_t)(8 * i) * ld, so);
+    } else {
+      const uint32_t so = (uint32_t)t * 64u;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        load_lds16_so(rs, lds0 + stage * kGw8Stage + i * 1024, vo0 + (uint32_t)(16 * i) * ld, so);
+    }
+  };
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+  const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
+  const int swb = (fr >> 2) & 3;
+  auto brow = [&](int j) {
+    return GG ? (j >> 1) * 128 + wn * 64 + 32 * (j & 1) : wn * 128 + 32 * j;
+  };
+  // lane (fr, hk): k = 32 hk .. + 31 of the slab for A row / B column fr
+  auto compute = [&](int stage) {
+    const char* sa = smem + stage * kGw8Stage;
+    const char* sb = sa + kGw8AStage;
+    i32x8_t bq[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const char* row = sb + (brow(j) + fr) * 64;
+      const bf16x8 b0 = *(const bf16x8*)(row + (((2 * hk) ^ swb) * 16));
+      const bf16x8 b1 = *(const bf16x8*)(row + (((2 * hk + 1) ^ swb) * 16));
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        bq[j][x] = (int)b0.w[x];
+        bq[j][4 + x] = (int)b1.w[x];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const char* row = sa + (wm * 128 + 32 * i + fr) * 128;
+      bf16x8 av[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) av[c] = *(const bf16x8*)(row + (((4 * hk + c) ^ sw) * 16));
+      if (SUM_A)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
+      int ae;
+      const i32x8_t aq = quant_fp8x32<32, 0>(av, &ae);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x64_f8(aq, ae, bq[j], 127, acc[i][j]);
+    }
+  };
+
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  float ss_pre = 0.f;
+  if (!SUM_A && p.rownorm && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
+  for (int t = 0; t < nk; ++t) {
+    // this wave's loads of slab t landed (slab t + 1's may still fly)
+    if (t + 1 < nk) {
+      if (isa)
+        wait_vmcnt<16>();
+      else
+        wait_vmcnt<8>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();  // everyone's, and slab t - 1 is consumed
+    if (t + 2 < nk) issue(t + 2, (t + 2) % kGw8Stages);
+    compute(t % kGw8Stages);
+  }
+
+  if (!SUM_A) {
+    sRow[tid] = ss_pre;
+  } else if (wn == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float s2 = ss[i] + __shfl_xor(ss[i], 32, 64);
+      if (lane < 32) sRow[wm * 128 + 32 * i + lane] = s2;
+    }
+  }
+  __syncthreads();  // also: every wave is done with the ring
+
+  constexpr int CH = WNO / 8, ITEMS = 32 * CH / 64, EB = 4;
+  float* scr = (float*)smem + wave * 32 * kGwELD;
+  const int64_t nw0 = n0 + wn * WNO;
+  auto to_scr = [&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * kGwELD + 32 * j + fr] = acc[i][j][r];
+  };
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.b_scale, rec_bytes(N * 4));
+  const __amdgpu_buffer_rsrc_t rsc2 = make_rsrc(GG ? p.b2_scale : p.b_scale, rec_bytes(N * 4));
+#pragma unroll 1
+  for (int i = 0; i < 4; ++i) {
+    switch (i) {
+      case 0: to_scr(IntC<0>{}); break;
+      case 1: to_scr(IntC<1>{}); break;
+      case 2: to_scr(IntC<2>{}); break;
+      default: to_scr(IntC<3>{}); break;
+    }
+    const int64_t rb = m0 + wm * 128 + 32 * i;
+#pragma unroll 1
+    for (int e0 = 0; e0 < ITEMS; e0 += EB) {
+      EpiIn in[EB];
+      float w0[EB][8], w1[EB][8];
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
+        const int64_t nn = nw0 + 8 * ch;
+        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+        const bool vec = vec_ok && cnt == 8;
+        epi_load<MODE>(p, rb + row, nn, vec, cnt, in[e]);
+        bl_f8(rsc, (uint32_t)(nn * 4), vec, w0[e]);
+        if (GG) bl_f8(rsc2, (uint32_t)(nn * 4), vec, w1[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
+        const int64_t m = rb + row, nn = nw0 + 8 * ch;
+        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+        constexpr bool SSO = MODE == FVX_GEMM_PLAIN;
+        float ssq = 0.f;
+        if (m < M && cnt > 0) {
+          float v[8], u[8];
+          const float* sv = scr + row * kGwELD + 8 * ch;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            v[x] = sv[x] * w0[e][x];
+            u[x] = GG ? sv[64 + x] * w1[e][x] : 0.f;
+          }
+          const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
+          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e],
+                          SSO && p.ss_out, ssq);
+        }
+        if (SSO && p.ss_out) {
+          ssq += __shfl_xor(ssq, 1, 64);
+          ssq += __shfl_xor(ssq, 2, 64);
+          ssq += __shfl_xor(ssq, 4, 64);
+          if ((ch & 7) == 0 && m < M && nn < N) p.ss_out[(nn / 64) * p.ss_ld + m] = ssq;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny (M <= 64) weight-streaming kernels
 // ---------------------------------------------------------------------------
 // gemm_skinny_kernel: M <= 64 (the bs=1 action expert, M = 50/51).  The op is
@@ -1467,6 +1680,9 @@ constexpr int kWideCfg = 3;  // gemm_wide_kernel
 #ifndef FVX_WIDE_MIN_K
 #define FVX_WIDE_MIN_K 2048
 #endif
+#ifndef FVX_WIDE_F8
+#define FVX_WIDE_F8 1
+#endif
 
 static int tile_bm(int cfg, int fp8) { return cfg == 1 && fp8 ? 128 : kTileBM[cfg]; }
 
@@ -1487,7 +1703,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   const int64_t bn = 128 / (gg ? 2 : 1);
   const int64_t tiles = ((d.m + 63) / 64) * ((d.n + bn - 1) / bn);
   const int64_t wtiles = ((d.m + 255) / 256) * ((d.n + 2 * bn - 1) / (2 * bn));
-  const bool wide_ok = !d.b_fp8 && d.k % 64 == 0 && d.split_k <= 1 &&
+  const bool wide_ok = (!d.b_fp8 || FVX_WIDE_F8) && d.k % 64 == 0 && d.split_k <= 1 &&
                        (d.mode == FVX_GEMM_PLAIN || gg || d.mode == FVX_GEMM_QKV_ROPE);
   t.splits = 1;
   // PLAIN / QKV: one workgroup of 256 x 256 per CU at a time, so the tiles
@@ -1535,8 +1751,8 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
               "gemm: workspace must be 16B aligned");
   const int vec_ok = epi_vec_ok(d) ? 1 : 0;
   if (cfg == kWideCfg) {
-    FVX_REQUIRE(!d.b_fp8 && d.k % 64 == 0 && d.mode != FVX_GEMM_EULER, FVX_ERR_ARG,
-                "gemm: the wide kernel needs bf16 weights, K %% 64 == 0, no EULER");
+    FVX_REQUIRE(d.k % 64 == 0 && d.mode != FVX_GEMM_EULER, FVX_ERR_ARG,
+                "gemm: the wide kernel needs K %% 64 == 0, no EULER");
     // 256 x 256 tiles (GEGLU: 256 x 2 x 128), 4 waves of 128 x 128
     const unsigned nb = (unsigned)(m_tiles * n_tiles);
 #define LW(MODE)                                                                    \
@@ -1546,11 +1762,27 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   else                                                                              \
     hipLaunchKernelGGL((gemm_wide_kernel<MODE, false>), dim3(nb), dim3(256), 0, s, d, \
                        m_tiles, n_tiles, vec_ok)
-    switch (d.mode) {
-      case FVX_GEMM_GEGLU: LW(FVX_GEMM_GEGLU); break;
-      case FVX_GEMM_QKV_ROPE: LW(FVX_GEMM_QKV_ROPE); break;
-      default: LW(FVX_GEMM_PLAIN); break;
+#define LW8(MODE)                                                                      \
+  if (d.rownorm && !d.ss_in)                                                           \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true>), dim3(nb), dim3(256), 0, s, d,  \
+                       m_tiles, n_tiles, vec_ok);                                      \
+  else                                                                                 \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false>), dim3(nb), dim3(256), 0, s, d, \
+                       m_tiles, n_tiles, vec_ok)
+    if (d.b_fp8) {
+      switch (d.mode) {
+        case FVX_GEMM_GEGLU: LW8(FVX_GEMM_GEGLU); break;
+        case FVX_GEMM_QKV_ROPE: LW8(FVX_GEMM_QKV_ROPE); break;
+        default: LW8(FVX_GEMM_PLAIN); break;
+      }
+    } else {
+      switch (d.mode) {
+        case FVX_GEMM_GEGLU: LW(FVX_GEMM_GEGLU); break;
+        case FVX_GEMM_QKV_ROPE: LW(FVX_GEMM_QKV_ROPE); break;
+        default: LW(FVX_GEMM_PLAIN); break;
+      }
     }
+#undef LW8
 #undef LW
     return launch_status("gemm(wide)");
   }

@@ -187,3 +187,43 @@ def test_fp8_weight_quantization_and_layout(K, cuda):
     pos = (((n // 16) * 2 + kk // 128) * 2048 + ((r // 8) % 4 * 16 + n % 16) * 32
            + (r // 32) * 8 + kk % 8)
     assert torch.equal(fb[pos.reshape(-1)].view(64, 256), q)
+
+
+def sample_rows(m):
+    rows = {0, 1, 127, 128, 255, 256, m // 2, m - 257, m - 256, m - 2, m - 1}
+    return torch.tensor(sorted(r for r in rows if 0 <= r < m))
+
+
+def test_fp8_wide_geglu(K, cuda):
+    """The wide fp8 kernel (256 x 2 x 128 tiles; the prefix gate/up shape,
+    512 tiles) on sampled rows, against the restatement with per-(row,
+    64-k) activation scales and against the e4m3 rounding bound."""
+    announce('fp8 wide geglu m=816 n=16384 k=2048')
+    m, n, k = 816, 16384, 2048
+    a = randn((m, k), 150, std=1.5)
+    gw, gq = fp8_weight(K, randn((n, k), 151, std=0.02), cuda)
+    uw, uq = fp8_weight(K, randn((n, k), 152, std=0.02), cuda)
+    out = K.gemm_geglu(a.to(cuda), gw, uw, rownorm_eps=1e-6)
+    rows = sample_rows(m)
+    aq = quant_a_ref(a[rows], skinny=False)
+    r = torch.rsqrt(a[rows].double().pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = F.gelu((aq @ gq.t()) * r, approximate='tanh') * ((aq @ uq.t()) * r)
+    assert rel_err(out.cpu()[rows], ref) <= REL_TOL
+
+
+def test_fp8_wide_plain(K, cuda):
+    """The wide fp8 kernel on a PLAIN GEMM with bias and residual (M=6528,
+    N=2048, K=2048: 208 tiles), sampled rows."""
+    announce('fp8 wide plain m=6528 n=2048 k=2048')
+    m, n, k = 6528, 2048, 2048
+    a = randn((m, k), 160, std=1.5)
+    fw, wq = fp8_weight(K, randn((n, k), 161, std=0.02), cuda)
+    bias = randn((n,), 162, std=0.5)
+    res = randn((m, n), 163)
+    out = K.gemm(a.to(cuda), fw, bias=bias.to(cuda), residual=res.to(cuda))
+    rows = sample_rows(m)
+    extra = bias.double() + res[rows].double()
+    ref = quant_a_ref(a[rows], skinny=False) @ wq.t() + extra
+    got = out.cpu()[rows]
+    assert rel_err(got, ref) <= REL_TOL
+    check_bound(got, a[rows], wq, ref_extra=extra)
