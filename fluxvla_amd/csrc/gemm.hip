@@ -240,14 +240,14 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
 }
 
 // v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
-// want_ssq (PLAIN): ssq receives the sum of squares of the values as
-// stored (bf16-rounded unless out_f32) over the cnt columns.
+// want_xo (PLAIN, GEGLU): xo receives the 8 values as stored (bf16-rounded
+// unless out_f32), for the hand-over outputs (epi_handoff).
 template <int MODE>
 __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
                                           int64_t n, bool vec, int cnt,
                                           const float* v, const float* u,
                                           float r, const EpiIn& in,
-                                          bool want_ssq, float& ssq) {
+                                          bool want_xo, float* xo) {
   float x[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = v[e] * r;
@@ -256,6 +256,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
     for (int e = 0; e < 8; ++e) x[e] = gelu_tanh(x[e]) * (u[e] * r);
     st_b8((bf16_t*)p.c + out_row(p, m) * p.ldc + n, x, vec, cnt);
     if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, n), pack8(x));
+    if (want_xo) unpack8(pack8(x), xo);
     return;
   }
   if (MODE == FVX_GEMM_QKV_ROPE) {
@@ -329,19 +330,75 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
   else
     st_b8((bf16_t*)p.c + orow * p.ldc + n, x, vec, cnt);
   if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, n), pack8(x));
-  if (want_ssq) {
-    float xr[8];
+  if (want_xo) {
     if (p.out_f32) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xr[e] = x[e];
+      for (int e = 0; e < 8; ++e) xo[e] = x[e];
     } else {
-      unpack8(pack8(x), xr);
+      unpack8(pack8(x), xo);
     }
+  }
+}
+
+// Hand-over outputs of one row's 64-column block, held as 8-column chunks
+// by 8 consecutive lanes (every lane runs the shuffles; `valid`: this lane's
+// chunk exists, `lead`: its first lane): the row's sum of squares of the
+// stored values (ss_out) and the e4m3 copy with the block's E8M0 exponent
+// (a8_out), quantized exactly as quant_fp8x32 quantizes an A block.
+__device__ __forceinline__ void epi_handoff(const GemmArgs& p, bool valid, bool lead,
+                                            int64_t m, int64_t n, int cnt,
+                                            const float* xo) {
+  if (p.ss_out) {
     float q = 0.f;
+    if (valid)
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (e < cnt) q += xr[e] * xr[e];
-    ssq = q;
+      for (int e = 0; e < 8; ++e)
+        if (e < cnt) q += xo[e] * xo[e];
+    q += __shfl_xor(q, 1, 64);
+    q += __shfl_xor(q, 2, 64);
+    q += __shfl_xor(q, 4, 64);
+    if (lead && valid) p.ss_out[(n / 64) * p.ss_ld + m] = q;
+  }
+  if (p.a8_out) {
+    const bf16x8 b = pack8(xo);
+    uint32_t mx = 0;
+    if (valid)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w = b.w[j] & 0x7fff7fffu;
+        const uint32_t lo = 2 * j < cnt ? (w & 0xffffu) : 0u;
+        const uint32_t hi = 2 * j + 1 < cnt ? (w >> 16) : 0u;
+        mx = lo > mx ? lo : mx;
+        mx = hi > mx ? hi : mx;
+      }
+#pragma unroll
+    for (int sh = 1; sh <= 4; sh <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)mx, sh, 64);
+      mx = o > mx ? o : mx;
+    }
+    const int e = e8m0_for_amax(mx);
+    if (valid) {
+      const float scale = __uint_as_float((uint32_t)e << 23);
+      uint32_t q[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        i16x2_t r = {0, 0};
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(
+            r, __builtin_bit_cast(bf16x2_t, b.w[2 * j]), scale, false);
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(
+            r, __builtin_bit_cast(bf16x2_t, b.w[2 * j + 1]), scale, true);
+        q[j] = __builtin_bit_cast(uint32_t, r);
+      }
+      unsigned char* dst = (unsigned char*)p.a8_out + m * p.a8_out_ld + n;
+      if (cnt == 8) {
+        *(uint2*)dst = uint2{q[0], q[1]};
+      } else {
+#pragma unroll
+        for (int x = 0; x < 8; ++x)
+          if (x < cnt) dst[x] = (unsigned char)(q[x >> 2] >> (8 * (x & 3)));
+      }
+      if (lead) ((unsigned char*)p.a8_out_scale)[(n / 64) * p.a8_out_sld + m] = (unsigned char)e;
+    }
   }
 }
 
@@ -683,10 +740,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
         const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
         const int64_t m = rb + row, nn = nw0 + 8 * ch;
         const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        // ss_out: the 8 lanes of a row (CH == 8: one 64-column block per
-        // wave) add their sums of squares; the shuffles run in every lane
-        constexpr bool SSO = MODE == FVX_GEMM_PLAIN && WNO == 64;
-        float ssq = 0.f;
+        // hand-over outputs: the 8 lanes of a row (CH == 8: one 64-column
+        // block per wave); the shuffles run in every lane
+        constexpr bool HO = MODE == FVX_GEMM_PLAIN && WNO == 64;
+        const bool ho = HO && (p.ss_out || p.a8_out) && splits == 1;
+        float xo[8];
         if (m < M && cnt > 0) {
         float v[8], u[8];
         const float* sv = scr + row * ELD + 8 * ch;
@@ -720,16 +778,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
         const float r = p.rownorm
                             ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps)
                             : 1.f;
-        epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e],
-                        SSO && p.ss_out, ssq);
+        epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e], ho, xo);
         }
       next_item:
-        if (SSO && p.ss_out && splits == 1) {
-          ssq += __shfl_xor(ssq, 1, 64);
-          ssq += __shfl_xor(ssq, 2, 64);
-          ssq += __shfl_xor(ssq, 4, 64);
-          if (ch == 0 && m < M) p.ss_out[(nw0 / 64) * p.ss_ld + m] = ssq;
-        }
+        if (ho) epi_handoff(p, m < M && cnt > 0, ch == 0, m, nn, cnt, xo);
       }
     }
   }
@@ -907,8 +959,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
         const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
         const int64_t m = rb + row, nn = nw0 + 8 * ch;
         const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        constexpr bool SSO = MODE == FVX_GEMM_PLAIN;
-        float ssq = 0.f;
+        const bool ho = (MODE == FVX_GEMM_PLAIN || GG) && (p.ss_out || p.a8_out);
+        float xo[8];
         if (m < M && cnt > 0) {
           float v[8], u[8];
           const float* sv = scr + row * kGwELD + 8 * ch;
@@ -918,16 +970,10 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
             u[x] = GG ? sv[64 + x] : 0.f;
           }
           const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
-          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e],
-                          SSO && p.ss_out, ssq);
+          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e], ho, xo);
         }
-        if (SSO && p.ss_out) {
-          // the 8 lanes of a row's 64-column block add their sums
-          ssq += __shfl_xor(ssq, 1, 64);
-          ssq += __shfl_xor(ssq, 2, 64);
-          ssq += __shfl_xor(ssq, 4, 64);
-          if ((ch & 7) == 0 && m < M && nn < N) p.ss_out[(nn / 64) * p.ss_ld + m] = ssq;
-        }
+        // the 8 lanes of a row's 64-column block
+        if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
       }
     }
   }
@@ -945,14 +991,26 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
 // 48 KiB per stage, a 3-stage ring.  B rows carry the 16-byte chunk index
 // XOR (row >> 2) & 3 (4 chunks per 64-byte row).
 // ---------------------------------------------------------------------------
-constexpr int kGw8AStage = 256 * 128, kGw8Stage = kGw8AStage + 256 * 64;
+// F8A: A arrives as an e4m3 copy with its exponents (a8 / a8_scale, see
+// fvx_gemm_desc): A rows of 64 bytes per slab like the B rows, 256 exponent
+// bytes per slab, no quantization here.
 constexpr int kGw8Stages = 3;
+template <bool F8A>
+struct Gw8Layout {
+  static constexpr int A = F8A ? 256 * 64 : 256 * 128;  // A tile bytes
+  static constexpr int B = 256 * 64;                    // B tile bytes
+  static constexpr int E = F8A ? 256 : 0;               // A exponents
+  static constexpr int STAGE = A + B + E;
+};
 
-template <int MODE, bool SUM_A>
+template <int MODE, bool SUM_A, bool F8A>
 __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_tiles,
                                                               int n_tiles, int vec_ok) {
+  typedef Gw8Layout<F8A> LY;
   constexpr bool GG = MODE == FVX_GEMM_GEGLU;
   constexpr int WNO = GG ? 64 : 128;  // output columns per wave
+  constexpr int kGw8AStage = LY::A, kGw8Stage = LY::STAGE;
+  static_assert(!(F8A && SUM_A), "an e4m3 A has no bf16 squares to sum");
   __shared__ __align__(16) char smem[kGw8Stages * kGw8Stage];
   __shared__ float sRow[kGwBM];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -973,12 +1031,17 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   const int64_t r0 = isa ? m0 + 128 * wave : (GG ? n0 : n0 + 128 * (wave - 2));
   const int64_t rlim = (isa ? M : N) - r0;
   const int64_t nrows = rlim <= 0 ? 0 : (rlim < 128 ? rlim : 128);
-  const uint32_t ld = isa ? (uint32_t)p.lda * 2 : (uint32_t)p.ldb;  // bytes per row
-  const char* band = isa ? (const char*)p.a + r0 * p.lda * 2
+  const uint32_t ld = isa ? (F8A ? (uint32_t)p.a8_ld : (uint32_t)p.lda * 2)
+                          : (uint32_t)p.ldb;  // bytes per row
+  const char* band = isa ? (F8A ? (const char*)p.a8 + r0 * p.a8_ld
+                                : (const char*)p.a + r0 * p.lda * 2)
                          : (const char*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb;
   const i32x4_t rs = make_rsrc4(band, (uint32_t)(nrows * ld));
+  // F8A: the slab's 256 A exponents, one dword per lane (rows 4 l .. 4 l + 3)
+  const i32x4_t rse = make_rsrc4(F8A ? p.a8_scale : p.a,
+                                 F8A ? (uint32_t)((int64_t)nk * p.a8_sld) : 0u);
   uint32_t vo0, vo1, lds0;
-  if (isa) {
+  if (isa && !F8A) {
     // rows 8 i + (lane >> 3), slot lane & 7 <- chunk slot ^ ((row >> 1) & 7)
     const int lr = lane >> 3, lc = lane & 7;
     vo0 = (uint32_t)lr * ld + 16u * (uint32_t)(lc ^ (lr >> 1));
@@ -988,17 +1051,21 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
     // rows 16 i + (lane >> 2), slot lane & 3 <- chunk slot ^ ((row >> 2) & 3)
     const int lr = lane >> 2, lc = lane & 3;
     vo0 = vo1 = (uint32_t)lr * ld + 16u * (uint32_t)(lc ^ ((lr >> 2) & 3));
-    lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + kGw8AStage + (wave - 2) * 128 * 64);
+    lds0 = __builtin_amdgcn_readfirstlane(
+        lds_addr(smem) + (isa ? wave * 128 * 64 : kGw8AStage + (wave - 2) * 128 * 64));
   }
   auto issue = [&](int t, int stage) {
-    if (isa) {
+    if (F8A && wave == 0)
+      load_lds4(rse, lds_addr(smem) + stage * kGw8Stage + LY::A + LY::B,
+                (uint32_t)(t * p.a8_sld + m0 + 4 * lane));
+    if (isa && !F8A) {
       const uint32_t so = (uint32_t)t * 128u;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         load_lds16_so(rs, lds0 + stage * kGw8Stage + i * 1024,
                       ((i & 1) ? vo1 : vo0) + (uint32_t)(8 * i) * ld, so);
     } else {
-      const uint32_t so = (uint32_t)t * 64u;
+      const uint32_t so = (uint32_t)t * 64u;  // 64 one-byte k per row and slab
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         load_lds16_so(rs, lds0 + stage * kGw8Stage + i * 1024, vo0 + (uint32_t)(16 * i) * ld, so);
@@ -1022,6 +1089,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   auto compute = [&](int stage) {
     const char* sa = smem + stage * kGw8Stage;
     const char* sb = sa + kGw8AStage;
+    const unsigned char* se = (const unsigned char*)(sb + LY::B);
     i32x8_t bq[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1036,15 +1104,29 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const char* row = sa + (wm * 128 + 32 * i + fr) * 128;
-      bf16x8 av[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) av[c] = *(const bf16x8*)(row + (((4 * hk + c) ^ sw) * 16));
-      if (SUM_A)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
       int ae;
-      const i32x8_t aq = quant_fp8x32<32, 0>(av, &ae);
+      i32x8_t aq;
+      if (F8A) {
+        const int ra = wm * 128 + 32 * i + fr;
+        const char* row = sa + ra * 64;
+        const bf16x8 a0 = *(const bf16x8*)(row + (((2 * hk) ^ swb) * 16));
+        const bf16x8 a1 = *(const bf16x8*)(row + (((2 * hk + 1) ^ swb) * 16));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          aq[x] = (int)a0.w[x];
+          aq[4 + x] = (int)a1.w[x];
+        }
+        ae = se[ra];
+      } else {
+        const char* row = sa + (wm * 128 + 32 * i + fr) * 128;
+        bf16x8 av[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) av[c] = *(const bf16x8*)(row + (((4 * hk + c) ^ sw) * 16));
+        if (SUM_A)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
+        aq = quant_fp8x32<32, 0>(av, &ae);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x64_f8(aq, ae, bq[j], 127, acc[i][j]);
     }
@@ -1057,7 +1139,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   for (int t = 0; t < nk; ++t) {
     // this wave's loads of slab t landed (slab t + 1's may still fly)
     if (t + 1 < nk) {
-      if (isa)
+      if (F8A && wave == 0)
+        wait_vmcnt<9>();
+      else if (isa && !F8A)
         wait_vmcnt<16>();
       else
         wait_vmcnt<8>();
@@ -1121,8 +1205,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
         const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
         const int64_t m = rb + row, nn = nw0 + 8 * ch;
         const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        constexpr bool SSO = MODE == FVX_GEMM_PLAIN;
-        float ssq = 0.f;
+        const bool ho = (MODE == FVX_GEMM_PLAIN || GG) && (p.ss_out || p.a8_out);
+        float xo[8];
         if (m < M && cnt > 0) {
           float v[8], u[8];
           const float* sv = scr + row * kGwELD + 8 * ch;
@@ -1132,15 +1216,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
             u[x] = GG ? sv[64 + x] * w1[e][x] : 0.f;
           }
           const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
-          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e],
-                          SSO && p.ss_out, ssq);
+          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e], ho, xo);
         }
-        if (SSO && p.ss_out) {
-          ssq += __shfl_xor(ssq, 1, 64);
-          ssq += __shfl_xor(ssq, 2, 64);
-          ssq += __shfl_xor(ssq, 4, 64);
-          if ((ch & 7) == 0 && m < M && nn < N) p.ss_out[(nn / 64) * p.ss_ld + m] = ssq;
-        }
+        if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
       }
     }
   }
@@ -1453,8 +1531,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8)) void gemm_skinny_kernel(GemmArgs
       u[e] *= wsc2[e];
     }
   }
-  float no_ssq;
-  epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in, false, no_ssq);
+  epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in, false, nullptr);
 }
 
 // Sum of the split partials of either GEMM kernel + epilogue.  Thread t of
@@ -1579,6 +1656,19 @@ static int validate(const GemmArgs& d) {
               FVX_ERR_ARG, "gemm: ss_out needs mode PLAIN, m > 64 and ss_ld >= m");
   FVX_REQUIRE(!d.ss_in || (d.rownorm && d.ss_parts > 0 && d.ss_ld >= d.m), FVX_ERR_ARG,
               "gemm: ss_in needs rownorm, ss_parts > 0 and ss_ld >= m");
+  FVX_REQUIRE(!d.a8_out || ((d.mode == FVX_GEMM_PLAIN || d.mode == FVX_GEMM_GEGLU) &&
+                            !d.out_f32 && d.m > 64 && d.a8_out_scale &&
+                            d.a8_out_ld >= d.n && d.a8_out_ld % 8 == 0 &&
+                            d.a8_out_sld >= d.m && ((uintptr_t)d.a8_out & 7) == 0),
+              FVX_ERR_ARG,
+              "gemm: a8_out needs mode PLAIN or GEGLU, a bf16 output, m > 64, "
+              "a8_out_scale, a8_out_ld >= n (multiple of 8), a8_out_sld >= m");
+  FVX_REQUIRE(!d.a8 || (d.a8_scale && d.a8_ld >= d.k && d.a8_ld % 16 == 0 &&
+                        d.a8_sld >= d.m && d.a8_sld % 4 == 0 && aligned16(d.a8) &&
+                        ((uintptr_t)d.a8_scale & 3) == 0),
+              FVX_ERR_ARG,
+              "gemm: a8 needs a8_scale, a8_ld >= k (multiple of 16, 16B aligned) "
+              "and a8_sld >= m (multiple of 4)");
   FVX_REQUIRE(!d.rownorm || d.rownorm_eps >= 0.f, FVX_ERR_ARG,
               "gemm: rownorm_eps must be >= 0");
   FVX_REQUIRE(d.row_group >= 0, FVX_ERR_ARG, "gemm: row_group must be >= 0");
@@ -1718,7 +1808,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   }
   if (gg && wtiles >= 256) t.cfg = 1;
   else t.cfg = tiles <= 256 ? 2 : 0;
-  if (d.ss_out) return t;  // written by the one-pass epilogue
+  if (d.ss_out || d.a8_out) return t;  // written by the one-pass epilogue
   if (d.split_k > 0) t.splits = d.split_k;
   else if (t.cfg != 1 && tiles < 128 && d.k >= 4096) t.splits = 2;
   return t;
@@ -1730,7 +1820,7 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   const int bm = tile_bm(cfg, d.b_fp8), bn = kTileBN[cfg] / (gg ? 2 : 1);
   const int m_tiles = (int)((d.m + bm - 1) / bm);
   const int n_tiles = (int)((d.n + bn - 1) / bn);
-  if (splits < 1 || d.ss_out) splits = 1;  // ss_out is written by the one-pass epilogue
+  if (splits < 1 || d.ss_out || d.a8_out) splits = 1;  // hand-overs: one-pass epilogue
   const int64_t bk = d.b_fp8 ? 128 : 64;
   int64_t kchunk = (d.k + splits - 1) / splits;
   kchunk = (kchunk + bk - 1) / bk * bk;
@@ -1750,6 +1840,8 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   FVX_REQUIRE(splits == 1 || aligned16(d.workspace), FVX_ERR_ALIGN,
               "gemm: workspace must be 16B aligned");
   const int vec_ok = epi_vec_ok(d) ? 1 : 0;
+  FVX_REQUIRE(!(gg && d.a8_out) || cfg == kWideCfg, FVX_ERR_ARG,
+              "gemm: a8_out on a GeGLU GEMM needs the wide kernel (>= 256 of its tiles)");
   if (cfg == kWideCfg) {
     FVX_REQUIRE(d.k % 64 == 0 && d.mode != FVX_GEMM_EULER, FVX_ERR_ARG,
                 "gemm: the wide kernel needs K %% 64 == 0, no EULER");
@@ -1762,13 +1854,18 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   else                                                                              \
     hipLaunchKernelGGL((gemm_wide_kernel<MODE, false>), dim3(nb), dim3(256), 0, s, d, \
                        m_tiles, n_tiles, vec_ok)
-#define LW8(MODE)                                                                      \
-  if (d.rownorm && !d.ss_in)                                                           \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true>), dim3(nb), dim3(256), 0, s, d,  \
-                       m_tiles, n_tiles, vec_ok);                                      \
-  else                                                                                 \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false>), dim3(nb), dim3(256), 0, s, d, \
-                       m_tiles, n_tiles, vec_ok)
+    // the e4m3 copy of A is used when given (a rownorm then needs ss_in)
+    const bool f8a = d.a8 && d.a8_scale && (!d.rownorm || d.ss_in);
+#define LW8(MODE)                                                                          \
+  if (d.rownorm && !d.ss_in)                                                               \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true, false>), dim3(nb), dim3(256), 0, s, \
+                       d, m_tiles, n_tiles, vec_ok);                                       \
+  else if (f8a)                                                                            \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, true>), dim3(nb), dim3(256), 0, s, \
+                       d, m_tiles, n_tiles, vec_ok);                                       \
+  else                                                                                     \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, false>), dim3(nb), dim3(256), 0, s, \
+                       d, m_tiles, n_tiles, vec_ok)
     if (d.b_fp8) {
       switch (d.mode) {
         case FVX_GEMM_GEGLU: LW8(FVX_GEMM_GEGLU); break;

@@ -217,6 +217,31 @@ class Fp8Weight:
         return Fp8Weight(buf, self.scale, n, k, frag=True)
 
 
+class Fp8Act:
+    """An e4m3 copy of an activation matrix [m, k] written by the GEMM that
+    produced it (``gemm(..., a8_out=)``) and read as A by the fp8-weight
+    wide GEMM (``a8=``): ``data`` uint8 [m, k], ``scale`` uint8 E8M0
+    exponents [k / 64, m] (one per row and 64-column block)."""
+
+    def __init__(self, data, scale):
+        self.data, self.scale = data, scale
+
+    @staticmethod
+    def empty(m, k, device):
+        if k % 64:
+            raise ValueError('Fp8Act needs k % 64 == 0')
+        m4 = (m + 3) // 4 * 4
+        return Fp8Act(torch.zeros(m, k, dtype=torch.uint8, device=device),
+                      torch.zeros(k // 64, m4, dtype=torch.uint8, device=device))
+
+    def values(self):
+        """fp32 values it stands for (dequantized)."""
+        m, k = self.data.shape
+        q = self.data.view(torch.float8_e4m3fn).float()
+        e = self.scale[:, :m].t().float()                     # [m, k / 64]
+        return q * torch.pow(2.0, e - 127.0).repeat_interleave(64, 1)
+
+
 def pack_frag_a_ref(a):
     """Torch restatement of the FragA layout (tests): [m <= 64, k] ->
     64 * k elements; rows >= m are zero."""
@@ -307,6 +332,24 @@ def ss_parts(n):
     return (n + 63) // 64
 
 
+def _set_a8(d, a8=None, a8_out=None):
+    """e4m3 activation hand-over (see Fp8Act)."""
+    if a8_out is not None:
+        _check(a8_out.data, 'a8_out', dtype=torch.uint8)
+        _check(a8_out.scale, 'a8_out scale', dtype=torch.uint8)
+        if a8_out.data.shape[0] < d.m or a8_out.data.shape[1] < d.n:
+            raise ValueError('a8_out is smaller than the output')
+        d.a8_out, d.a8_out_ld = a8_out.data.data_ptr(), a8_out.data.stride(0)
+        d.a8_out_scale, d.a8_out_sld = a8_out.scale.data_ptr(), a8_out.scale.stride(0)
+    if a8 is not None:
+        _check(a8.data, 'a8', dtype=torch.uint8)
+        _check(a8.scale, 'a8 scale', dtype=torch.uint8)
+        if a8.data.shape[0] < d.m or a8.data.shape[1] < d.k:
+            raise ValueError('a8 is smaller than A')
+        d.a8, d.a8_ld = a8.data.data_ptr(), a8.data.stride(0)
+        d.a8_scale, d.a8_sld = a8.scale.data_ptr(), a8.scale.stride(0)
+
+
 def _set_ss(d, rownorm_eps, ss_in=None, ss_out=None):
     """Row sums of squares handed between GEMMs: ``ss_out`` (fp32 [parts,
     ld], parts = ss_parts(n)) receives the producer's per-block sums of its
@@ -332,11 +375,11 @@ def _set_ss(d, rownorm_eps, ss_in=None, ss_out=None):
 def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
          gate=None, gate_group=1, pos=None, pos_period=0, act=_lib.ACT_NONE,
          rownorm_eps=None, out_f32=False, row_group=0, row_group_stride=0,
-         split_k=0, c_frag=None, ss_in=None, ss_out=None):
+         split_k=0, c_frag=None, ss_in=None, ss_out=None, a8=None, a8_out=None):
     """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order.
     ``a`` may be a FragA and ``weight`` a FragB; ``c_frag`` (a FragA with
     k == n) also receives the output in the fragment-major layout;
-    ``ss_in`` / ``ss_out``: see _set_ss."""
+    ``ss_in`` / ``ss_out``: see _set_ss; ``a8`` / ``a8_out``: see Fp8Act."""
     d = _gemm_desc(a, weight)
     if out is None:
         out = torch.empty(*_lead_shape(a), d.n,
@@ -366,6 +409,7 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
         d.pos, d.pos_period = pos.data_ptr(), pos_period or pos.shape[0]
     d.act, d.mode, d.out_f32 = int(act), _lib.GEMM_PLAIN, int(bool(out_f32))
     _set_ss(d, rownorm_eps, ss_in, ss_out)
+    _set_a8(d, a8, a8_out)
     d.row_group, d.row_group_stride = row_group, row_group_stride
     d.split_k = split_k
     _set_c_frag(d, c_frag)
@@ -374,7 +418,7 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
 
 
 def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
-               c_frag=None, ss_in=None):
+               c_frag=None, ss_in=None, a8=None, a8_out=None):
     """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T)."""
     d = _gemm_desc(a, gate_w)
     if isinstance(gate_w, Fp8Weight):
@@ -400,6 +444,7 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
     _, d.ldc = _rows_ld(out, 'out')
     d.c, d.mode = out.data_ptr(), _lib.GEMM_GEGLU
     _set_ss(d, rownorm_eps, ss_in)
+    _set_a8(d, a8, a8_out)
     d.split_k = split_k
     _set_c_frag(d, c_frag)
     _run_gemm(d)
@@ -408,7 +453,7 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
 
 def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
                   head_dim, rownorm_eps=None, row_group=0, row_group_stride=0,
-                  split_k=0, v_ld=None, ss_in=None):
+                  split_k=0, v_ld=None, ss_in=None, a8=None):
     """[q|k|v] = a @ w_qkv^T with pair-interleaved RoPE on q and k.
 
     rope: fp32 [max_pos, head_dim/2, 2] (cos, sin); positions: int32 [M].
@@ -433,6 +478,7 @@ def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
         d.v_out, d.ldv, d.v_transposed = v_out.data_ptr(), int(v_ld), 1
     d.n_q_heads, d.head_dim = n_q_heads, head_dim
     _set_ss(d, rownorm_eps, ss_in)
+    _set_a8(d, a8)
     d.row_group, d.row_group_stride = row_group, row_group_stride
     d.split_k = split_k
     _run_gemm(d)

@@ -400,6 +400,11 @@ class PI0Inference:
             'pre_h': e(B * S, cfg.llm_mlp),
             # row sums of squares of x handed between prefix GEMMs
             'pre_ss': e(2, K.ss_parts(cfg.llm_hidden), B * S, dt=torch.float32),
+            # e4m3 copies of x and of the gate/up output (fp8 weights)
+            'pre_a8x': (K.Fp8Act.empty(B * S, cfg.llm_hidden, dev)
+                        if self.weight_dtype == 'fp8' else None),
+            'pre_a8h': (K.Fp8Act.empty(B * S, cfg.llm_mlp, dev)
+                        if self.weight_dtype == 'fp8' else None),
             # K cache [layer][batch][token][dim] (pair-interleaved dims);
             # V cache transposed [layer][batch][dim][token]
             'kc': e(cfg.exp_layers, B, T, D),
@@ -475,6 +480,12 @@ class PI0Inference:
         # row sums of squares of x handed from the residual GEMMs to the
         # next fused RMSNorm (O proj -> gate/up, down -> next QKV)
         ss = b['pre_ss'] if B * S > 64 else [None, None]
+        # fp8 weights: the residual GEMMs and gate/up also hand their outputs
+        # over as e4m3 copies, which the fp8 wide GEMMs read instead of
+        # quantizing their A (same values)
+        a8x = a8h = None
+        if self.weight_dtype == 'fp8' and B * S > 64:
+            a8x, a8h = b['pre_a8x'], b['pre_a8h']
         for i, L in enumerate(W['layers']):
             kc, vc = b['kc'][i], b['vc'][i]
             last = i == n - 1
@@ -487,17 +498,19 @@ class PI0Inference:
                             kc.view(B * T, D), vc, 0 if last else cfg.heads,
                             D, rownorm_eps=cfg.rms_eps, row_group=S,
                             row_group_stride=T, v_ld=T,
-                            ss_in=ss[1] if i > 0 else None)
+                            ss_in=ss[1] if i > 0 else None,
+                            a8=a8x if i > 0 else None)
             if last:
                 break
             K.mqa_attention(b['pre_q'], kc[:, :S], vc, b['pre_ctx'],
                             kgrp=b['kgrp'][:, :S], qgrp=b['qgrp_pre'],
                             v_transposed=True)
             K.gemm(b['pre_ctx'].view(B * S, -1), L['o_w'], out=x, residual=x,
-                   ss_out=ss[0])
+                   ss_out=ss[0], a8_out=a8x)
             K.gemm_geglu(x, L['gate_w'], L['up_w'], out=b['pre_h'],
-                         rownorm_eps=cfg.rms_eps, ss_in=ss[0])
-            K.gemm(b['pre_h'], L['down_w'], out=x, residual=x, ss_out=ss[1])
+                         rownorm_eps=cfg.rms_eps, ss_in=ss[0], a8=a8x, a8_out=a8h)
+            K.gemm(b['pre_h'], L['down_w'], out=x, residual=x, ss_out=ss[1],
+                   a8=a8h, a8_out=a8x)
 
     def _frag_ok(self, B):
         """bs=1 expert GEMMs (M = suffix_len <= 64) run fragment-major."""

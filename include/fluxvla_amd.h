@@ -145,6 +145,20 @@ typedef struct fvx_gemm_desc {
   const float* ss_in;
   int64_t ss_ld;
   int32_t ss_parts;
+  /* e4m3 activations handed from one GEMM to the next (fp8-weight variant;
+   * no counterpart in the reference):
+   *   a8_out / a8_out_scale (PLAIN or GEGLU, bf16 output, M > 64): an e4m3
+   *     copy of the stored output, a8_out[m * a8_out_ld + n] =
+   *     e4m3(c[m][n] / 2^(e - 127)) with one E8M0 exponent e per row and
+   *     64-column block at a8_out_scale[(n / 64) * a8_out_sld + m]: the
+   *     smallest power of two that keeps the block's largest magnitude
+   *     within 448 (the rule the fp8 GEMMs quantize A with);
+   *   a8 / a8_scale (same layout, strides a8_ld / a8_sld): such a copy of
+   *     A.  The fp8-weight wide kernel then reads it instead of quantizing A
+   *     (same values, same result); every other path ignores it, and so
+   *     does a rownorm GEMM without ss_in.  a8_sld % 4 == 0. */
+  void* a8_out; void* a8_out_scale; int64_t a8_out_ld, a8_out_sld;
+  const void* a8; const void* a8_scale; int64_t a8_ld, a8_sld;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */

@@ -227,3 +227,61 @@ def test_fp8_wide_plain(K, cuda):
     got = out.cpu()[rows]
     assert rel_err(got, ref) <= REL_TOL
     check_bound(got, a[rows], wq, ref_extra=extra)
+
+
+def quant_blocks_ref(x):
+    """CPU restatement of the e4m3 hand-over copy of a bf16 matrix [m, n]:
+    per row and 64-column block, e = E - 8 + (mantissa > 96) of the block's
+    largest |value| (clamped to [1, 254]), q = e4m3(x / 2^(e - 127))."""
+    m, n = x.shape
+    bits = (x.view(torch.int16).int() & 0x7FFF).view(m, n // 64, 64)
+    amax = bits.amax(-1)
+    E, mant = (amax >> 7) & 0xFF, amax & 0x7F
+    e = (E - 8 + (mant > 96).int()).clamp(1, 254)
+    sc = torch.pow(2.0, (e - 127).double()).repeat_interleave(64, 1)
+    q = (x.double() / sc).float().to(torch.float8_e4m3fn)
+    return q.view(torch.uint8), e.to(torch.uint8)
+
+
+@pytest.mark.parametrize('m,n,k,geglu', [(300, 1024, 512, False), (816, 16384, 2048, True)])
+def test_fp8_handover_copy_exact(K, cuda, m, n, k, geglu):
+    """The e4m3 copy a GEMM epilogue writes (a8_out) is byte for byte the
+    quantization of its stored bf16 output, exponents included."""
+    announce(f'fp8 hand-over copy m={m} n={n} geglu={geglu}')
+    a = randn((m, k), 170).to(cuda)
+    w = randn((n, k), 171, std=0.03).to(cuda)
+    a8 = K.Fp8Act.empty(m, n, cuda)
+    if geglu:
+        w2 = randn((n, k), 172, std=0.03).to(cuda)
+        out = K.gemm_geglu(a, w, w2, rownorm_eps=1e-6, a8_out=a8)
+    else:
+        out = K.gemm(a, w, a8_out=a8)
+    rows = sample_rows(m)
+    q, e = quant_blocks_ref(out.cpu()[rows])
+    assert torch.equal(a8.data.cpu()[rows], q)
+    assert torch.equal(a8.scale.cpu()[:, rows].t(), e)
+
+
+def test_fp8_handover_consumer_identical(K, cuda):
+    """The fp8 wide GEMM reading the e4m3 copy of A (a8) gives bitwise the
+    result of the same GEMM quantizing the bf16 A itself: the same values
+    and exponents feed the same MFMAs.  Gate/up shape with handed-over row
+    sums, and a PLAIN shape (M=6528)."""
+    announce('fp8 hand-over consumer == self-quantizing')
+    for m, k, n, geglu in ((816, 2048, 16384, True), (6528, 2048, 2048, False)):
+        a0 = randn((m, 256), 180).to(cuda)
+        w0 = randn((k, 256), 181, std=0.05).to(cuda)
+        x = torch.empty(m, k, dtype=torch.bfloat16, device=cuda)
+        ss = torch.zeros(K.ss_parts(k), m, device=cuda)
+        a8 = K.Fp8Act.empty(m, k, cuda)
+        K.gemm(a0, w0, out=x, ss_out=ss, a8_out=a8)      # producer
+        fw = K.Fp8Weight.quantize(randn((n, k), 182, std=0.02).to(cuda))
+        if geglu:
+            fu = K.Fp8Weight.quantize(randn((n, k), 183, std=0.02).to(cuda))
+            got = K.gemm_geglu(x, fw, fu, rownorm_eps=1e-6, ss_in=ss, a8=a8)
+            own = K.gemm_geglu(x, fw, fu, rownorm_eps=1e-6, ss_in=ss)
+        else:
+            res = randn((m, n), 184).to(cuda)
+            got = K.gemm(x, fw, residual=res, a8=a8)
+            own = K.gemm(x, fw, residual=res)
+        assert torch.equal(got, own)
