@@ -799,7 +799,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 // A rows, 2 and 3 the B rows: GEGLU the gate and the up rows): per load one
 // VGPR offset, the slab advance in the scalar offset, rows past the operand
 // out of the buffer view (zeros).  K moves in 64-wide slabs through a
-// 2-stage ring with one barrier per slab; K % 64 == 0, one pass (no split).
+// 2-stage ring; K % 64 == 0, one pass (no split).  The slab's 16 loads per
+// wave are spread between MFMA groups, two after each group of 4 (issued in
+// one burst they fill the texture-address queue and hold the MFMAs back):
+// loads 0..7 of slab t + 2 during the last k step of slab t, 8..15 during
+// the first k step of slab t + 1.  The one barrier per slab sits before the
+// last k step: it publishes slab t + 1 and frees slab t's stage, and the
+// first fragments of slab t + 1 are read while that step's MFMAs run.
 // LDS rows are 128 bytes with the 16-byte chunk index XOR (row >> 1) & 7,
 // as in gemm_tile_kernel.  The epilogue is gemm_tile_kernel's (epi_load /
 // epi_store per 8-column chunk), including ss_out for PLAIN.
@@ -846,12 +852,14 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   const uint32_t vo0 = (uint32_t)lr * ld2 + 16u * (uint32_t)(lc ^ (lr >> 1));
   const uint32_t vo1 = (uint32_t)lr * ld2 + 16u * (uint32_t)(lc ^ (lr >> 1) ^ 4);
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * 128 * 128);
+  // load i (8 rows of the band) of slab t into ring stage `stage`
+  auto issue1 = [&](int t, int stage, int i) {
+    load_lds16_so(rs, lds0 + stage * kGwStage + i * 1024,
+                  ((i & 1) ? vo1 : vo0) + (uint32_t)(8 * i) * ld2, (uint32_t)t * 128u);
+  };
   auto issue = [&](int t, int stage) {
-    const uint32_t so = (uint32_t)t * 128u;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      load_lds16_so(rs, lds0 + stage * kGwStage + i * 1024,
-                    ((i & 1) ? vo1 : vo0) + (uint32_t)(8 * i) * ld2, so);
+    for (int i = 0; i < 16; ++i) issue1(t, stage, i);
   };
 
   f32x16_t acc[4][4];
@@ -867,42 +875,55 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   auto brow = [&](int j) {
     return GG ? 256 + (j >> 1) * 128 + wn * 64 + 32 * (j & 1) : 256 + wn * 128 + 32 * j;
   };
-  auto compute = [&](int stage) {
+  issue(0, 0);
+  // handed-over row sums: thread t takes row m0 + t (waits with slab 0)
+  float ss_pre = 0.f;
+  if (!SUM_A && p.rownorm && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
+  bf16x8 af[2][4], bfr[2][4];
+  auto rd = [&](int stage, int ks, int b) {
     const char* s = smem + stage * kGwStage;
-    bf16x8 af[2][4], bfr[2][4];
-    auto rd = [&](int ks, int b) {
-      const int cpos = ((2 * ks + hk) ^ sw) * 16;
+    const int cpos = ((2 * ks + hk) ^ sw) * 16;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[b][i] = *(const bf16x8*)(s + (wm * 128 + 32 * i + fr) * 128 + cpos);
+    for (int i = 0; i < 4; ++i)
+      af[b][i] = *(const bf16x8*)(s + (wm * 128 + 32 * i + fr) * 128 + cpos);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bfr[b][j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
-    };
-    rd(0, 0);
+    for (int j = 0; j < 4; ++j) bfr[b][j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
+  };
+  for (int x = 0; x < 8; ++x) issue1(nk > 1 ? 1 : 0, 1, x);
+  wait_vmcnt<8>();
+  __syncthreads();
+  rd(0, 0, 0);
+  for (int t = 0; t < nk; ++t) {
+    const int st = t & 1;
+    const int t1 = t + 1 < nk ? t + 1 : nk - 1, t2 = t + 2 < nk ? t + 2 : nk - 1;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int b = ks & 1;
-      if (ks < 3) rd(ks + 1, b ^ 1);
+      if (ks < 3) {
+        rd(st, ks + 1, b ^ 1);
+      } else {
+        wait_vmcnt<0>();   // slab t + 1 landed (this wave's loads)
+        __syncthreads();   // everyone's, and every read of slab t is done
+        rd(st ^ 1, 0, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if (SUM_A) ss[i] += sumsq8(af[b][i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
+        if (ks == 0) {
+          issue1(t1, st ^ 1, 8 + 2 * i);
+          issue1(t1, st ^ 1, 9 + 2 * i);
+        } else if (ks == 3) {
+          issue1(t2, st, 2 * i);
+          issue1(t2, st, 2 * i + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-  };
-
-  issue(0, 0);
-  // handed-over row sums: thread t takes row m0 + t (waits with slab 0)
-  float ss_pre = 0.f;
-  if (!SUM_A && p.rownorm && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
-  for (int t = 0; t < nk; ++t) {
-    wait_vmcnt<0>();   // this wave's loads of slab t landed
-    __syncthreads();   // everyone's, and slab t - 1 is consumed
-    if (t + 1 < nk) issue(t + 1, (t + 1) & 1);
-    compute(t & 1);
   }
+  wait_vmcnt<0>();
 
   // row sums of squares: lanes l and l ^ 32 hold the two k halves of row
   // l % 32 of block i
