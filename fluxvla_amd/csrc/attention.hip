@@ -697,6 +697,361 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
 }
 
 
+// ---------------------------------------------------------------------------
+// attn_decode_t_kernel: the same problems as attn_decode_kernel (head_dim 256,
+// transposed value cache, 64-row groups x key ranges, the same partials for
+// attn_decode_merge_kernel), computed transposed so that nothing crosses
+// waves but the K / V^T tiles.  A workgroup of 2 waves owns 64 query rows;
+// wave w owns rows 32 w .. + 31 and all 256 dims, and per 64-key tile
+//   S^T (64 keys x 32 rows)  = K . Q^T     v_mfma_f32_32x32x16_bf16, K from
+//                                          LDS (A), Q^T in VGPRs (B);
+//   O^T (256 dims x 32 rows) += V^T . P^T  V^T from LDS (A), P^T (B) straight
+//                                          from the S^T accumulators.
+// Lane (q, h) = (lane % 32, lane / 32) ends S^T holding 32 keys of ONE query
+// row q: the A operand rows of K are read in the key order pi(i) = 16 (j >>
+// 1) + 8 h' + 4 (j & 1) + (i & 3) (j = i >> 3, h' = (i >> 2) & 1), so that
+// the accumulator elements 0..7 / 8..15 are keys 8 h .. + 7 / 16 + 8 h .. + 7
+// of the 32-key block, i.e. exactly the B operand of P^T for the 16-key
+// steps of O^T.  The softmax statistics of a row live in lanes q and q + 32
+// (one shuffle), and O^T's accumulators of lane (q, h) all belong to row q,
+// so nothing needs a cross-lane exchange.  There is no online rescale of
+// the 128 O accumulators (which would pull them out of the AGPRs every
+// tile): a row's exp2 reference is its maximum over the first tile in which
+// it sees a key, so P = 2^(s - ref) <= 2^32 as long as no later score
+// exceeds the reference by more than 32 (in the exp2 domain) -- fp32 and
+// bf16 hold that with room to spare.  Should any row of the workgroup go
+// further, the workgroup runs its key range a second time with each row's
+// exact maximum (tracked on the first pass) as the reference.  The K / V^T
+// tiles (the same LDS images as attn_decode_kernel's) move by LDS DMA in a
+// two-stage ring with one barrier per tile; tile t + 1's loads are spread
+// between tile t's S^T MFMAs.  The softmax of the second 32-key block runs
+// under the first P V steps, and tiles that need no masking (neither the
+// range's last, partial tile nor key groups that hide a key from a row of
+// the wave) skip it.
+// ---------------------------------------------------------------------------
+constexpr int kDtKB = 64 * 512, kDtVB = 256 * 128;
+constexpr int kDtStage = kDtKB + kDtVB + 256;    // + the tile's key groups
+constexpr int kDtOffQG = 2 * kDtStage;           // query groups [64]
+constexpr int kDtLDS = kDtOffQG + 64 * 4;
+static_assert(64 * kDecOP * 4 <= 2 * kDtStage, "O rows fit the stages");
+constexpr float kDtLazy = 32.f;                  // log2 of the largest P
+constexpr int kDecTKps = 4 * kDecKT;             // keys per range that select it
+
+__global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
+                                                            int n_rg, int splits,
+                                                            int kps, int hs) {
+  constexpr int HD = 256, KT = 64;
+  __shared__ __align__(16) unsigned char smem[kDtLDS];
+  __shared__ float sLq[64], sMq[64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane & 31, h = lane >> 5;
+  const int nb = (int)gridDim.x, q8 = nb >> 3, r8 = nb & 7;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
+  const int rg = item % n_rg;
+  const int split = (item / n_rg) % splits;
+  const int z = item / (n_rg * splits);
+  const int heads = (int)p.heads, R = (int)p.sq * heads;
+  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
+  const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
+  const bf16_t* K = (const bf16_t*)p.k + zb * p.k_zs1 + zh * p.k_zs2;
+  const bf16_t* Vt = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
+  const int32_t* kgrp = p.kgrp ? p.kgrp + zb * p.kgrp_zs1 : nullptr;
+  const int32_t* qgrp = p.qgrp ? p.qgrp + zb * p.qgrp_zs1 : nullptr;
+  const int kbeg = split * kps;
+  const int kend = kbeg + kps < (int)p.sk ? kbeg + kps : (int)p.sk;
+  const int ntile = (kend - kbeg + KT - 1) / KT;
+  const int qts = (int)p.q_tok_stride, qhs = (int)p.q_head_stride;
+  const int kts = (int)p.k_tok_stride, vds = (int)p.v_d_stride;
+
+  // buffer views: K keys >= kend and Q rows >= R read zero; V^T keys past
+  // kend are zeroed after they are read
+  const i32x4_t rq =
+      make_rsrc4(Q, (uint32_t)(((int)p.sq - 1) * qts + (heads - 1) * qhs + HD) * 2);
+  const i32x4_t rkc = make_rsrc4(K, (uint32_t)kend * kts * 2);
+  const i32x4_t rvc = make_rsrc4(Vt, (uint32_t)HD * vds * 2);
+  const i32x4_t rgc = make_rsrc4(kgrp ? (const void*)kgrp : (const void*)Q,
+                                 kgrp ? (uint32_t)kend * 4 : 0u);
+  const i32x4_t rqg = make_rsrc4(qgrp ? (const void*)qgrp : (const void*)Q,
+                                 qgrp ? (uint32_t)p.sq * 4 : 0u);
+  const uint32_t lbase = lds_addr(smem);
+
+  // load L (0..31) of a tile: K keys 2 L + (lane >> 5) (LDS slot lane & 31 of
+  // the key's 512-byte row holds global chunk slot ^ (key & 15)); V^T dims
+  // 8 L + (lane >> 3) (slot lane & 7 of the dim's 128-byte row holds key
+  // chunk slot ^ ((dim >> 1) & 7)).  Wave w issues K and V loads 16 w .. + 15.
+  auto load_k = [&](int t0, int st, int L) {
+    const int kl = 2 * L + (lane >> 5);
+    const int ch = (lane & 31) ^ (kl & 15);
+    load_lds16(rkc, lbase + st * kDtStage + 2 * L * 512, (uint32_t)((t0 + kl) * kts + 8 * ch) * 2);
+  };
+  auto load_v = [&](int t0, int st, int L) {
+    const int d = 8 * L + (lane >> 3);
+    const int ch = (lane & 7) ^ ((d >> 1) & 7);
+    load_lds16(rvc, lbase + st * kDtStage + kDtKB + 8 * L * 128,
+               (uint32_t)(d * vds + t0 + 8 * ch) * 2);
+  };
+  auto load_g = [&](int t0, int st) {  // the tile's 64 key groups (wave 0)
+    load_lds4(rgc, lbase + st * kDtStage + kDtKB + kDtVB, (uint32_t)(t0 + lane) * 4);
+  };
+
+  // Q rows 64 rg + 2 L + (lane >> 5) into stage 1's K area (K's swizzle), the
+  // query groups, then tile 0 into stage 0
+  {
+    const uint32_t qb = lbase + kDtStage;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int L = 16 * w + i, rl = 2 * L + (lane >> 5), r = rg * 64 + rl;
+      const int tok = row_tok(r, heads, hs);
+      const int ch = (lane & 31) ^ (rl & 15);
+      load_lds16(rq, qb + 2 * L * 512,
+                 r < R ? (uint32_t)(tok * qts + (r - tok * heads) * qhs + 8 * ch) * 2 : kOOB);
+    }
+    if (w == 0) {
+      const int r = rg * 64 + lane;
+      load_lds4(rqg, lbase + kDtOffQG, r < R ? (uint32_t)row_tok(r, heads, hs) * 4 : kOOB);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    load_k(kbeg, 0, 16 * w + i);
+    load_v(kbeg, 0, 16 * w + i);
+  }
+  if (kgrp && w == 0) load_g(kbeg, 0);
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // Q^T fragments (B operand): lane (q, h) holds dims 16 s + 8 h .. + 7 of
+  // row 32 w + q
+  bf16x8 qT[16];
+  int32_t qg;
+  {
+    const int rl = 32 * w + q;
+    const bf16_t* sQ = (const bf16_t*)(smem + kDtStage);
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) qT[s2] = ld8(&sQ[rl * 256 + 8 * ((2 * s2 + h) ^ (rl & 15))]);
+    qg = qgrp ? ((const int32_t*)(smem + kDtOffQG))[rl] : 0;
+  }
+  // the wave's smallest query group (rows past R: their token's group or 0)
+  int qg_min = qg;
+#pragma unroll
+  for (int x = 1; x < 64; x <<= 1) qg_min = min(qg_min, __shfl_xor(qg_min, x, 64));
+  qg_min = __builtin_amdgcn_readfirstlane(qg_min);
+  __syncthreads();  // stage 1 is free for tile 1
+
+  // K A-operand row of this lane: key pi(q) of each 32-key block
+  const int piq = 16 * ((q >> 3) >> 1) + 8 * ((q >> 2) & 1) + 4 * ((q >> 3) & 1) + (q & 3);
+  const float sc = p.scale * kLog2e;
+  // m_ref: the row's exp2 reference, fixed at its first visible key (O and
+  // l are still zero then) or, on the second pass, the exact row maximum
+  float m_ref = -INFINITY, l_run = 0.f, m_max = -INFINITY;
+  f32x16_t o[8];
+  for (int pass = 0;; ++pass) {
+  bool over = false;
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+
+  for (int t = 0; t < ntile; ++t) {
+    const int t0 = kbeg + t * KT, st = t & 1;
+    const bool edge = t0 + KT > kend;  // the range's last, partial tile
+    const bf16_t* sK = (const bf16_t*)(smem + st * kDtStage);
+    const bf16_t* sV = (const bf16_t*)(smem + st * kDtStage + kDtKB);
+    const int32_t* sG = (const int32_t*)(smem + st * kDtStage + kDtKB + kDtVB);
+    // this wave's loads of tile t landed
+    wait_vmcnt<0>();
+    if (edge) {
+      // keys >= kend of this wave's V^T rows (dims 128 w ..) read as zero
+      // (the cache past the range may hold anything; P is 0 there)
+      bf16_t* sVw = (bf16_t*)sV + 128 * w * 64;
+      const int valid = kend - t0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = lane + 64 * i, row = c >> 3, slot = c & 7;
+        const int kc = slot ^ (((128 * w + row) >> 1) & 7);  // key chunk in this slot
+        bf16x8* ptr = (bf16x8*)&sVw[row * 64 + 8 * slot];
+        if (8 * kc + 8 > valid) {
+          bf16x8 v = *ptr;
+#pragma unroll
+          for (int x = 0; x < 4; ++x)
+            v.w[x] &= 8 * kc + 2 * x + 1 < valid ? 0xffffffffu
+                                                  : (8 * kc + 2 * x < valid ? 0xffffu : 0u);
+          *ptr = v;
+        }
+      }
+    }
+    // the barrier publishes everyone's loads of tile t, and every wave is
+    // done with tile t - 1 (stage st ^ 1)
+    __syncthreads();
+
+    // key groups mask some key of this tile for some row of this wave?
+    // (uniform: the tile's largest group against the wave's smallest)
+    bool gmask = false;
+    if (kgrp) {
+      int gk = sG[lane];
+#pragma unroll
+      for (int x = 1; x < 64; x <<= 1) gk = max(gk, __shfl_xor(gk, x, 64));
+      gmask = __builtin_amdgcn_readfirstlane(gk) > qg_min;
+    }
+    const bool more = t + 1 < ntile;  // tile t + 1 is loaded during this one
+    auto rdk = [&](int j) {
+      const int key = 32 * (j & 1) + piq;
+      return ld8(&sK[key * 256 + 8 * ((2 * (j >> 1) + h) ^ (key & 15))]);
+    };
+    auto rdv = [&](int j) {
+      const int d = 32 * (j & 7) + q;
+      return ld8(&sV[d * 64 + 8 * ((2 * (j >> 3) + h) ^ ((d >> 1) & 7))]);
+    };
+    // the tile (masking only on the edge tile or with key groups in play)
+    auto tile = [&](auto masked) {
+      constexpr bool MASKED = decltype(masked)::value;
+      // S^T: step j = 2 s + kb (key block kb, dims 16 s ..; the two blocks'
+      // accumulations alternate, so that no MFMA waits for the previous
+      // one's result), the K fragments through a ring of 8 register sets
+      // read 6 steps ahead
+      f32x16_t sacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+      bf16x8 ring[8], pT[4];
+      // softmax of key block kb (its S^T complete) -> pT[2 kb], pT[2 kb + 1]:
+      // element r is key 32 kb + 16 (r >> 3) + 8 h + (r & 7).  The maximum
+      // is taken on the raw scores (the scale is positive) and the scale
+      // folded into the exponent's FMA.
+      auto softmax = [&](auto kbc) {
+        constexpr int kb = decltype(kbc)::value;
+        f32x16_t& sv = sacc[kb];
+        if (MASKED && (edge || gmask)) {
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int kl0 = 32 * kb + 16 * hf + 8 * h;
+            int32_t kgv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (kgrp) {
+              const int4 ga = *(const int4*)&sG[kl0];
+              const int4 gb = *(const int4*)&sG[kl0 + 4];
+              kgv[0] = ga.x; kgv[1] = ga.y; kgv[2] = ga.z; kgv[3] = ga.w;
+              kgv[4] = gb.x; kgv[5] = gb.y; kgv[6] = gb.z; kgv[7] = gb.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (kgv[e] > qg || t0 + kl0 + e >= kend) sv[8 * hf + e] = -INFINITY;
+          }
+        }
+        float mb = sv[0];
+#pragma unroll
+        for (int e = 1; e < 16; ++e) mb = fmaxf(mb, sv[e]);
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * sc;
+        m_max = fmaxf(m_max, mb);
+        if (m_ref == -INFINITY)
+          m_ref = mb;
+        else
+          over = over || mb > m_ref + kDtLazy;
+        const float nm = m_ref == -INFINITY ? 0.f : -m_ref;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          float pv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            pv[e] = exp2f(fmaf(sv[8 * hf + e], sc, nm));
+            l_run += pv[e];
+          }
+          pT[2 * kb + hf] = pack8(pv);
+        }
+      };
+#pragma unroll
+      for (int j = 0; j < 6; ++j) ring[j] = rdk(j);
+      // (compile-time steps: the loops hold too much code for the unroller)
+      static_for<0, 32>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if (j + 6 < 32) ring[(j + 6) & 7] = rdk(j + 6);
+        sacc[j & 1] = mfma32x32x16(ring[j & 7], qT[j >> 1], sacc[j & 1]);
+        if (more) {
+          if (j == 0 && kgrp && w == 0) load_g(t0 + KT, st ^ 1);
+          if (j < 16)
+            load_k(t0 + KT, st ^ 1, 16 * w + j);
+          else
+            load_v(t0 + KT, st ^ 1, 16 * w + j - 16);
+        }
+      });
+      softmax(IntC<0>{});
+      // O^T += V^T P^T, step j = 8 u + db: V^T A operand lane (i, h) = dim
+      // 32 db + i, keys 16 u + 8 h .. + 7
+#pragma unroll
+      for (int j = 0; j < 6; ++j) ring[j] = rdv(j);
+      static_for<0, 32>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if (j + 6 < 32) ring[(j + 6) & 7] = rdv(j + 6);
+        o[j & 7] = mfma32x32x16(ring[j & 7], pT[j >> 3], o[j & 7]);
+        if (j == 3) softmax(IntC<1>{});
+      });
+    };
+    tile(BoolC<true>{});
+  }
+  wait_vmcnt<0>();
+  // every wave is done with the ring; a row whose scores rose more than
+  // 2^kDtLazy above its reference sends the workgroup through a second
+  // pass with the exact row maxima as references (P <= 1)
+  if (!__syncthreads_or(over) || pass) break;
+  m_ref = m_max;
+  l_run = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    load_k(kbeg, 0, 16 * w + i);
+    load_v(kbeg, 0, 16 * w + i);
+  }
+  if (kgrp && w == 0) load_g(kbeg, 0);
+  }
+  l_run += __shfl_xor(l_run, 32, 64);
+
+  // O rows -> LDS: lane (q, h) holds dims 32 db + 8 (r >> 2) + 4 h + (r & 3)
+  // of row 32 w + q
+  float* sO = (float*)smem;
+  {
+    const int rl = 32 * w + q;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        sO[rl * kDecOP + 32 * db + 8 * (r >> 2) + 4 * h + (r & 3)] = o[db][r];
+    if (h == 0) {
+      sLq[rl] = l_run;
+      sMq[rl] = m_ref;
+    }
+  }
+  __syncthreads();
+  // thread item c: row c >> 5, dims 8 (c & 31) .. + 7
+  if (splits == 1) {
+#pragma unroll 4
+    for (int u = 0; u < 16; ++u) {
+      const int c = tid + 128 * u, i = c >> 5, d0 = (c & 31) * 8;
+      const int r = rg * 64 + i;
+      if (r >= R) continue;
+      const float l = sLq[i];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const f32x4_t a = *(const f32x4_t*)&sO[i * kDecOP + d0];
+      const f32x4_t b = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
+      float v[8] = {a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv,
+                    b[0] * inv, b[1] * inv, b[2] * inv, b[3] * inv};
+      dec_store<8>(p, z, r, d0, hs, v);
+    }
+    return;
+  }
+  float* part = (float*)p.workspace + (((int64_t)z * n_rg + rg) * splits + split) * kDecPF;
+#pragma unroll 4
+  for (int u = 0; u < 16; ++u) {
+    const int c = tid + 128 * u, i = c >> 5, d0 = (c & 31) * 8;
+    *(f32x4_t*)(part + i * 256 + d0) = *(const f32x4_t*)&sO[i * kDecOP + d0];
+    *(f32x4_t*)(part + i * 256 + d0 + 4) = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
+  }
+  if (tid < 64) {
+    part[64 * 256 + tid] = sMq[tid];
+    part[64 * 256 + 64 + tid] = sLq[tid];
+  }
+}
+
 // Merge of the decode partials: one thread per (problem, query row, 4 dims);
 // the loads of up to 16 splits are issued before the running-max merge,
 // which is applied in split order.
@@ -899,8 +1254,15 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "attention: workspace must be 16B aligned");
     const int hs = (d.heads & (d.heads - 1)) == 0 ? __builtin_ctzll((uint64_t)d.heads) : -1;
-    hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)a.n_items), dim3(256),
-                       0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
+    // key ranges of >= 4 tiles (the prefix): attn_decode_t_kernel, ~8 %
+    // faster there; one or two tiles per workgroup (the action expert): the
+    // 4-wave kernel, whose fixed costs are lower
+    if (a.kps >= kDecTKps)
+      hipLaunchKernelGGL(attn_decode_t_kernel, dim3((unsigned)a.n_items), dim3(128),
+                         0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
+    else
+      hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)a.n_items), dim3(256),
+                         0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
     int st = launch_status("attention(decode)");
     if (st || a.splits == 1) return st;
     const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 64;

@@ -200,6 +200,16 @@ __device__ __forceinline__ i32x4_t make_rsrc4(const void* base, uint32_t bytes) 
   return r;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b of a
+// 1-D grid runs on XCD b % 8), and each XCD has its own L2.  xcd_remap gives
+// XCD x the contiguous logical ids [start(x), start(x) + count(x)), count(x)
+// = nblk / 8 (+1 for x < nblk % 8), so that neighbouring tiles (the M tiles
+// of one weight panel) share an L2.  A bijection of [0, nblk) for any nblk.
+__device__ __forceinline__ int xcd_remap(int bid, int nblk) {
+  const int x = bid & 7, local = bid >> 3, per = nblk >> 3, rem = nblk & 7;
+  return x * per + (x < rem ? x : rem) + local;
+}
+
 typedef __attribute__((address_space(3))) char lds_char_t;
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {

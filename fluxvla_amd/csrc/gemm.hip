@@ -459,9 +459,11 @@ static bool epi_vec_ok(const GemmArgs& d) {
 // (16 consecutive rows of one chunk per 16 lanes) are free of bank
 // conflicts.  One barrier per slab: at slab t each wave waits for its own
 // loads of slab t, the barrier publishes everyone's and frees the stage of
-// slab t - 1, which then receives slab t + STAGES - 1.  Loads of slabs past
-// the K range use out-of-view offsets (zeros), so the loop has no branch
-// around a load.
+// slab t - 1, which then receives slab t + STAGES - 1.  Those loads are
+// spread evenly between slab t's MFMA groups rather than issued in one burst
+// (a burst fills the texture-address queue and holds the MFMAs back).  Loads
+// of slabs past the K range use out-of-view offsets (zeros), so the loop has
+// no branch around a load.
 //
 // Per-row sums of squares for the fused RMSNorm are taken from the A
 // fragments as they feed the MFMAs.  The epilogue moves each wave's 32-row
@@ -511,8 +513,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   // XCD-aware tile order: consecutive tile ids (the M tiles of one weight
   // panel, m fastest) land on one XCD and share its L2.
   const int nblk = m_tiles * n_tiles;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int bid = xcd_remap(blockIdx.x, nblk);
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
   const int split = blockIdx.y;
   const int64_t M = p.m, N = p.n, K = p.k;
@@ -563,11 +564,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     }
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * LPW * 1024);
+  auto issue1 = [&](int t, int stage, int i) {
+    load_lds16(rsel[i], lds0 + stage * C::STAGE_BYTES + i * 1024,
+               BK * t < kmax[i] ? voff[i] + (uint32_t)t * (isa[i] ? 2 * BK : 128) : kOOB);
+  };
   auto issue = [&](int t, int stage) {
 #pragma unroll
+    for (int i = 0; i < LPW; ++i) issue1(t, stage, i);
+  };
+  // slab tn's loads spread over the G MFMA groups of a slab: load i goes
+  // after group i G / LPW
+  auto issue_group = [&](int g, int G, int tn, int tst) {
+#pragma unroll
     for (int i = 0; i < LPW; ++i)
-      load_lds16(rsel[i], lds0 + stage * C::STAGE_BYTES + i * 1024,
-                 BK * t < kmax[i] ? voff[i] + (uint32_t)t * (isa[i] ? 2 * BK : 128) : kOOB);
+      if ((i * G) / LPW == g) issue1(tn, tst, i);
   };
 
   f32x16_t acc[FM][FN];
@@ -593,7 +603,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   };
   // rows of a fragment are (multiple of 32) + lane % 32: swizzle (lane >> 1) & 7
   const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
-  auto compute = [&](int stage, auto with_ss) {
+  auto compute = [&](int stage, auto with_ss, int tn, int tst) {
     constexpr bool SS = decltype(with_ss)::value;
     const char* s = smem + stage * C::STAGE_BYTES;
     if (F8) {
@@ -631,6 +641,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 #pragma unroll
           for (int j = 0; j < FN; ++j)
             acc[i][j] = mfma32x32x64_f8(aq[i], ae[i], bq[j], 127, acc[i][j]);
+        issue_group(ks, 2, tn, tst);
+        __builtin_amdgcn_sched_barrier(0);
       }
       return;
     }
@@ -658,6 +670,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
         if (SS) ss[i] += sumsq8(af[b][i]);
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
+        issue_group(ks * FM + i, 4 * FM, tn, tst);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
@@ -676,8 +690,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
         if (t >= nk) break;
         wait_vmcnt<LPW * (STAGES - 2)>();  // this wave's loads of slab t landed
         __syncthreads();                   // everyone's, and slab t-1 is consumed
-        issue(t + STAGES - 1, (s + STAGES - 1) % STAGES);
-        compute(s, with_ss);
+        compute(s, with_ss, t + STAGES - 1, (s + STAGES - 1) % STAGES);
       }
     }
   };
@@ -830,8 +843,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
 
   // XCD-aware tile order (consecutive ids: the M tiles of one weight panel)
   const int nblk = m_tiles * n_tiles;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int bid = xcd_remap(blockIdx.x, nblk);
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
   const int64_t M = p.m, N = p.n, K = p.k;
   const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * (GG ? 128 : 256);
@@ -1009,8 +1021,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
 // path: one scale per (row, 64-k slab) from the slab's largest magnitude,
 // shared by the two lanes (l, l ^ 32) holding the row's two 32-k halves.
 // Slabs of 64 k: A 256 rows x 128 B (bf16) and B 256 rows x 64 B (e4m3),
-// 48 KiB per stage, a 3-stage ring.  B rows carry the 16-byte chunk index
-// XOR (row >> 2) & 3 (4 chunks per 64-byte row).
+// 48 KiB per stage, a 3-stage ring; slab t + 2's loads go between slab t's
+// four MFMA groups.  B rows carry the 16-byte chunk index XOR (row >> 2) & 3
+// (4 chunks per 64-byte row).
 // ---------------------------------------------------------------------------
 // F8A: A arrives as an e4m3 copy with its exponents (a8 / a8_scale, see
 // fvx_gemm_desc): A rows of 64 bytes per slab like the B rows, 256 exponent
@@ -1039,8 +1052,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   const int wm = wave >> 1, wn = wave & 1;
 
   const int nblk = m_tiles * n_tiles;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int bid = xcd_remap(blockIdx.x, nblk);
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
   const int64_t M = p.m, N = p.n, K = p.k;
   const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * (GG ? 128 : 256);
@@ -1075,22 +1087,28 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
     lds0 = __builtin_amdgcn_readfirstlane(
         lds_addr(smem) + (isa ? wave * 128 * 64 : kGw8AStage + (wave - 2) * 128 * 64));
   }
-  auto issue = [&](int t, int stage) {
-    if (F8A && wave == 0)
+  // quarter q of slab t's loads into ring stage `stage` (the four quarters
+  // go between the four MFMA groups of a slab)
+  auto issue_q = [&](int t, int stage, int q) {
+    if (F8A && wave == 0 && q == 0)
       load_lds4(rse, lds_addr(smem) + stage * kGw8Stage + LY::A + LY::B,
                 (uint32_t)(t * p.a8_sld + m0 + 4 * lane));
     if (isa && !F8A) {
       const uint32_t so = (uint32_t)t * 128u;
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
+      for (int i = 4 * q; i < 4 * q + 4; ++i)
         load_lds16_so(rs, lds0 + stage * kGw8Stage + i * 1024,
                       ((i & 1) ? vo1 : vo0) + (uint32_t)(8 * i) * ld, so);
     } else {
       const uint32_t so = (uint32_t)t * 64u;  // 64 one-byte k per row and slab
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 2 * q; i < 2 * q + 2; ++i)
         load_lds16_so(rs, lds0 + stage * kGw8Stage + i * 1024, vo0 + (uint32_t)(16 * i) * ld, so);
     }
+  };
+  auto issue = [&](int t, int stage) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) issue_q(t, stage, q);
   };
 
   f32x16_t acc[4][4];
@@ -1106,8 +1124,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   auto brow = [&](int j) {
     return GG ? (j >> 1) * 128 + wn * 64 + 32 * (j & 1) : wn * 128 + 32 * j;
   };
-  // lane (fr, hk): k = 32 hk .. + 31 of the slab for A row / B column fr
-  auto compute = [&](int stage) {
+  // lane (fr, hk): k = 32 hk .. + 31 of the slab for A row / B column fr;
+  // slab tn's loads go into stage tst between the MFMA groups
+  auto compute = [&](int stage, int tn, int tst) {
     const char* sa = smem + stage * kGw8Stage;
     const char* sb = sa + kGw8AStage;
     const unsigned char* se = (const unsigned char*)(sb + LY::B);
@@ -1150,29 +1169,29 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x64_f8(aq, ae, bq[j], 127, acc[i][j]);
+      issue_q(tn, tst, i);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
+  // every iteration loads a slab (past the end: slab nk - 1 again, into the
+  // free stage), so one slab's loads are in flight behind slab t's
   issue(0, 0);
-  if (nk > 1) issue(1, 1);
+  issue(nk > 1 ? 1 : 0, 1);
   float ss_pre = 0.f;
   if (!SUM_A && p.rownorm && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
   for (int t = 0; t < nk; ++t) {
     // this wave's loads of slab t landed (slab t + 1's may still fly)
-    if (t + 1 < nk) {
-      if (F8A && wave == 0)
-        wait_vmcnt<9>();
-      else if (isa && !F8A)
-        wait_vmcnt<16>();
-      else
-        wait_vmcnt<8>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    if (F8A && wave == 0)
+      wait_vmcnt<9>();
+    else if (isa && !F8A)
+      wait_vmcnt<16>();
+    else
+      wait_vmcnt<8>();
     __syncthreads();  // everyone's, and slab t - 1 is consumed
-    if (t + 2 < nk) issue(t + 2, (t + 2) % kGw8Stages);
-    compute(t % kGw8Stages);
+    compute(t % kGw8Stages, t + 2 < nk ? t + 2 : nk - 1, (t + 2) % kGw8Stages);
   }
+  wait_vmcnt<0>();
 
   if (!SUM_A) {
     sRow[tid] = ss_pre;
@@ -1795,7 +1814,10 @@ constexpr int kWideCfg = 3;  // gemm_wide_kernel
 #define FVX_WIDE_F8 1
 #endif
 
-static int tile_bm(int cfg, int fp8) { return cfg == 1 && fp8 ? 128 : kTileBM[cfg]; }
+static int tile_bm(int cfg, int fp8) {
+  if (fp8) return cfg == 1 ? 128 : (cfg == 3 ? 256 : 64);
+  return kTileBM[cfg];
+}
 
 struct TilePlan {
   int cfg, splits;
@@ -1805,7 +1827,10 @@ struct TilePlan {
 // 256 x 256 tiles number >= 256 (GEGLU) or, for PLAIN / QKV_ROPE, fill the
 // CUs (below) with K >= FVX_WIDE_MIN_K; config 1
 // for other GeGLU projections with >= 256 such tiles (fp8); else 64 x 128
-// tiles, with the 4-stage ring (config 2) when they number <= 256.  A long
+// tiles: the 4-stage ring (config 2, 96 KiB of LDS, one workgroup per CU)
+// when they number <= 256, else the 3-stage ring (config 0, 72 KiB: two
+// workgroups per CU share the second round; with cold weights 2 stages lose
+// up to 25 % and 4 stages more).  A long
 // K (>= 4096) with fewer than 128 tiles is split in two (SigLIP fc2); with
 // more tiles the partials cost more than the idle CUs.
 static TilePlan plan_tile(const GemmArgs& d) {
@@ -1919,7 +1944,7 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   } else {                                                           \
     if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false);                \
     else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false);            \
-    else LT(64, 128, 2, 2, 2, MODE, false);                          \
+    else LT(64, 128, 2, 2, 3, MODE, false);                          \
   }
   FVX_MODE_DISPATCH(d.mode, LCFG)
 #undef LCFG

@@ -444,6 +444,36 @@ def test_attention_decode_block_causal(K, cuda, splits, vt, batch):
                            K.pack_frag_a_ref(o.view(Ssuf, H * D).cpu())[valid])
 
 
+@pytest.mark.parametrize('splits', [0, 1, 14])
+@pytest.mark.parametrize('spike', ['late', 'early'])
+def test_attention_decode_score_jump(K, cuda, splits, spike):
+    """Scores of one 64-key tile far above the others (~900 in the exp2
+    domain).  'late': the jump comes after the rows fixed their exp2
+    reference on an earlier tile; with one key range (splits=1, the
+    transposed kernel) that sends the workgroup through its second pass
+    (exact row maxima), with 14 ranges (the 4-wave kernel) the online
+    rescale takes it.  'early': the first tile holds the peak and the later
+    keys underflow towards zero."""
+    announce(f'attention decode score jump {spike} splits={splits}')
+    P, Ssuf, H, D = 816, 51, 8, 256
+    T = P + Ssuf
+    q = randn((1, Ssuf, H, D), 96)
+    cache_k = randn((1, T, D), 97)
+    cache_v = randn((1, T, D), 98)
+    lo = 320 if spike == 'late' else 0
+    # keys lo .. lo + 63 aligned with every query of token 0, head 0
+    cache_k[0, lo:lo + 64] = (q[0, 0, 0].float() * 40.0).bfloat16()
+    o = torch.empty(1, Ssuf, H, D, dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros(1, D, 872, dtype=torch.bfloat16)  # value cache, 8-aligned rows
+    vc[:, :, :T] = cache_v.transpose(1, 2)
+    K.mqa_attention(q.to(cuda), cache_k.to(cuda), vc.to(cuda), o,
+                    kv_splits=splits, v_transposed=True)
+    ref = sdpa_ref(q.double().transpose(1, 2), cache_k.double()[:, None],
+                   cache_v.double()[:, None]).transpose(1, 2)
+    assert torch.isfinite(o.float()).all()
+    assert rel_err(o, ref) <= REL_TOL
+
+
 def test_attention_siglip_packed(K, cuda):
     announce('attention siglip packed hd=72')
     nv, S, H, D = 3, 256, 16, 72
