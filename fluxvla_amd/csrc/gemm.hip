@@ -510,12 +510,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
 
-  // XCD-aware tile order: consecutive tile ids (the M tiles of one weight
-  // panel, m fastest) land on one XCD and share its L2.
+  // XCD-aware order over (split, tile): consecutive ids (the M tiles of one
+  // weight panel, m fastest, then the panels of one K range) land on one
+  // XCD and share its L2 -- with splits, an XCD works on one K range and
+  // reads only that slice of A and B.
   const int nblk = m_tiles * n_tiles;
-  const int bid = xcd_remap(blockIdx.x, nblk);
+  const int lid = xcd_remap(blockIdx.x + nblk * blockIdx.y, nblk * splits);
+  const int bid = lid % nblk, split = lid / nblk;
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
-  const int split = blockIdx.y;
   const int64_t M = p.m, N = p.n, K = p.k;
   const int64_t m0 = (int64_t)m_tile * BM, n0 = (int64_t)n_tile * (BN / NB);
   const int64_t kb = (int64_t)split * kchunk;
@@ -1574,51 +1576,78 @@ __global__ __launch_bounds__(64 * sk_waves(F8)) void gemm_skinny_kernel(GemmArgs
   epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in, false, nullptr);
 }
 
-// Sum of the split partials of either GEMM kernel + epilogue.  Thread t of
-// block (x, y): column 64 x + t % 64, row 4 y + t / 64; the loads of 16
-// splits are issued before their adds (one memory latency per 16), added in
+// Sum of the split partials of either GEMM kernel + epilogue.  Thread t
+// owns 8 consecutive columns of one row (chunk c = 256 blockIdx.x + t: row
+// c / CH, columns 8 (c % CH) .., CH = ceil(N / 8) chunks per row) and runs
+// the tile kernel's 8-column epilogue on them; the partials are read 16
+// bytes at a time (N % 4 == 0) through a buffer view (past it: zeros),
+// the loads of up to 8 splits in flight before their adds, which follow
 // split order (deterministic).
 template <int MODE>
 __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
-                                                                  int splits) {
+                                                                  int splits,
+                                                                  int vec_ok) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
-  constexpr int UN = 16;  // loads in flight per pass
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int64_t N = p.n, K = p.k;
-  const int64_t n = (int64_t)blockIdx.x * 64 + lane;
-  const int64_t row = (int64_t)blockIdx.y * 4 + (tid >> 6);
-  const bool ok = n < N && row < p.m;
+  constexpr int UN = 8;  // splits in flight per pass
+  const int64_t N = p.n, K = p.k, M = p.m;
+  const int64_t CH = (N + 7) / 8;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t m = c / CH, nn = (c % CH) * 8;
+  if (m >= M) return;
+  const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+  const bool v4 = (N & 3) == 0;
   const float* ws = (const float*)((const char*)p.workspace + kCounterBytes);
-  const int64_t M = p.m;
   const int64_t plane = (int64_t)splits * M * N;
-  // unconditional loads through a view of the partials (masked: past it)
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(ws, rec_bytes((NB * plane + (int64_t)splits * M) * 4));
-  float v = 0.f, u = 0.f, ss = 0.f;
+  EpiIn in;
+  epi_load<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, in);
+  float v[8], u[8], ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = u[e] = 0.f;
+  auto ld8f = [&](int64_t off, float* d) {  // 8 floats at element offset off
+    if (v4) {
+      const f32x4_t a = bload4f(rw, (uint32_t)(off * 4));
+      const f32x4_t b = bload4f(rw, cnt > 4 ? (uint32_t)((off + 4) * 4) : kOOB);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        d[e] = a[e];
+        d[4 + e] = b[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] = bload1f(rw, e < cnt ? (uint32_t)((off + e) * 4) : kOOB);
+    }
+  };
   for (int s0 = 0; s0 < splits; s0 += UN) {
-    float t[NB][UN], q[UN];
+    float t[UN][NB][8], q[UN];
 #pragma unroll
     for (int i = 0; i < UN; ++i) {
-      const int s = s0 + i;
-      const bool in = ok && s < splits;
+      const int sp = s0 + i;
+      const bool in_ = sp < splits;
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-        t[b][i] = bload1f(rw, in ? (uint32_t)((b * plane + ((int64_t)s * M + row) * N + n) * 4)
-                                 : kOOB);
-      q[i] = bload1f(rw, (in && p.rownorm) ? (uint32_t)((NB * plane + (int64_t)s * M + row) * 4)
-                                           : kOOB);
+      for (int b = 0; b < NB; ++b) {
+        if (in_)
+          ld8f(b * plane + ((int64_t)sp * M + m) * N + nn, t[i][b]);
+        else
+#pragma unroll
+          for (int e = 0; e < 8; ++e) t[i][b][e] = 0.f;
+      }
+      q[i] = bload1f(rw, (in_ && p.rownorm) ? (uint32_t)((NB * plane + (int64_t)sp * M + m) * 4)
+                                            : kOOB);
     }
 #pragma unroll
     for (int i = 0; i < UN; ++i) {
-      v += t[0][i];
-      u += t[NB - 1][i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] += t[i][0][e];
+        u[e] += t[i][NB - 1][e];
+      }
       ss += q[i];
     }
   }
-  float rs[1] = {p.rownorm ? rsqrtf(ss / (float)K + p.rownorm_eps) : 1.f};
-  float vv[1] = {v}, uu[1] = {u};
-  float pv[1] = {(MODE == FVX_GEMM_QKV_ROPE) ? __shfl_xor(v, 1, 64) : 0.f};
-  if (ok) epilogue4<MODE, 1>(p, row, n, vv, uu, pv, rs);
+  const float r = p.rownorm ? rsqrtf(ss / (float)K + p.rownorm_eps) : 1.f;
+  epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in, false, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1951,10 +1980,11 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
 #undef LT
   int st3 = launch_status("gemm(tile)");
   if (st3 || splits == 1) return st3;
-#define L(MODE)                                                            \
-  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                     \
-                     dim3((unsigned)((d.n + 63) / 64), (unsigned)((d.m + 3) / 4)), \
-                     dim3(256), 0, s, d, splits)
+  const int64_t chunks = d.m * ((d.n + 7) / 8);
+#define L(MODE)                                                                  \
+  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                           \
+                     dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s, d, \
+                     splits, vec_ok)
   FVX_MODE_DISPATCH(d.mode, L)
 #undef L
   return launch_status("gemm(reduce)");
