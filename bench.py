@@ -82,7 +82,7 @@ def time_dominant_kernel(model, iters=20):
     flops = 2.0 * M * N * Kd * 2
     achieved = flops / (us * 1e-6) / 1e12
     return {
-        'kernel': 'gemm_geglu_wide_kernel (prefix gate/up, '
+        'kernel': 'gemm_wide_kernel<GEGLU> (prefix gate/up, '
                   f'M={M} N={N}x2 K={Kd})',
         'bound': 'mfma',
         'achieved': round(achieved, 2),
@@ -240,13 +240,13 @@ def kernel_table(model):
         ('gemm_tile_kernel<64,128,PLAIN> o-proj (prefix)', lambda: K.gemm(
             b['pre_ctx'].view(M, -1), L['o_w'], out=b['pre_h'][:, :cfg.llm_hidden],
             residual=px, ss_out=ss_a), 2 * M * cfg.llm_hidden * H * D),
-        ('gemm_geglu_wide_kernel (prefix)', lambda: K.gemm_geglu(
+        ('gemm_wide_kernel<GEGLU> (prefix)', lambda: K.gemm_geglu(
             px, L['gate_w'], L['up_w'], out=b['pre_h'], rownorm_eps=cfg.rms_eps,
             ss_in=ss_a), 4 * M * cfg.llm_mlp * cfg.llm_hidden),
-        ('gemm_tile_kernel<64,128,PLAIN> down (prefix)', lambda: K.gemm(
+        ('gemm_wide_kernel<PLAIN> 8 K ranges + split-K reduce, down (prefix)', lambda: K.gemm(
             b['pre_h'], L['down_w'], out=b['pre_q'].view(M, -1)[:, :cfg.llm_hidden],
             residual=px, ss_out=ss_b), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
-        ('attn_decode_kernel + merge (prefix)', lambda: K.mqa_attention(
+        ('attn_decode_t_kernel + merge (prefix)', lambda: K.mqa_attention(
             b['pre_q'], kc0[:, :S], vc0, b['pre_ctx'], kgrp=b['kgrp'][:, :S],
             qgrp=b['qgrp_pre'], v_transposed=True), 4 * H * S * S * D),
     ]

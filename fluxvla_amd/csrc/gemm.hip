@@ -834,7 +834,8 @@ constexpr int kGwELD = 128 + 4;          // epilogue scratch stride (floats)
 
 template <int MODE, bool SUM_A>  // SUM_A: the fused RMSNorm sums A's squares here
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_tiles,
-                                                           int n_tiles, int vec_ok) {
+                                                           int n_tiles, int vec_ok,
+                                                           int splits, int kchunk) {
   constexpr bool GG = MODE == FVX_GEMM_GEGLU;
   constexpr int WNO = GG ? 64 : 128;  // output columns per wave
   __shared__ __align__(16) char smem[2 * kGwStage];
@@ -843,13 +844,18 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // XCD-aware tile order (consecutive ids: the M tiles of one weight panel)
+  // XCD-aware order over (split, tile): consecutive ids (the M tiles of one
+  // weight panel, then the panels of one K range) share an XCD's L2
   const int nblk = m_tiles * n_tiles;
-  const int bid = xcd_remap(blockIdx.x, nblk);
+  const int lid = xcd_remap(blockIdx.x, nblk * splits);
+  const int bid = lid % nblk, split = lid / nblk;
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
   const int64_t M = p.m, N = p.n, K = p.k;
   const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * (GG ? 128 : 256);
-  const int nk = (int)(K / 64);
+  // K range [kb, kb + 64 nk) (splits > 1: PLAIN without rownorm, fp32
+  // partials for gemm_partial_reduce_kernel)
+  const int64_t kb = (int64_t)split * kchunk;
+  const int nk = (int)(((kb + kchunk < K ? kb + kchunk : K) - kb) / 64);
 
   // this wave's band: 128 rows of A (waves 0, 1) or of B (2, 3)
   const bool isa = wave < 2;
@@ -857,8 +863,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   const int64_t rlim = (isa ? M : N) - r0;
   const int64_t nrows = rlim <= 0 ? 0 : (rlim < 128 ? rlim : 128);
   const uint32_t ld2 = (uint32_t)(isa ? p.lda : p.ldb) * 2;
-  const bf16_t* band = isa ? (const bf16_t*)p.a + r0 * p.lda
-                           : (const bf16_t*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb;
+  const bf16_t* band = isa ? (const bf16_t*)p.a + r0 * p.lda + kb
+                           : (const bf16_t*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb + kb;
   const i32x4_t rs = make_rsrc4(band, (uint32_t)(nrows * ld2));
   // load i: LDS rows 128 wave + 8 i + (lane >> 3), slot lane & 7 holds global
   // chunk slot ^ (((8 i + (lane >> 3)) >> 1) & 7)
@@ -979,6 +985,24 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
       default: to_scr(IntC<3>{}); break;
     }
     const int64_t rb = m0 + wm * 128 + 32 * i;
+    if (splits > 1) {
+      // fp32 partials of this K range: ws[(split M + m) N + n]
+      float* ws = (float*)((char*)p.workspace + kCounterBytes) + (int64_t)split * M * N;
+#pragma unroll 1
+      for (int e = 0; e < ITEMS; ++e) {
+        const int q = lane + 64 * e, row = q / CH, ch = q % CH;
+        const int64_t m = rb + row, nn = nw0 + 8 * ch;
+        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+        if (m < M && cnt > 0) {
+          const float* sv = scr + row * kGwELD + 8 * ch;
+          float v[8];
+#pragma unroll
+          for (int x = 0; x < 8; ++x) v[x] = sv[x];
+          st_f8(ws + m * N + nn, v, (N & 3) == 0 && cnt == 8, cnt);
+        }
+      }
+      continue;
+    }
 #pragma unroll 1
     for (int e0 = 0; e0 < ITEMS; e0 += EB) {
       EpiIn in[EB];
@@ -1576,7 +1600,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8)) void gemm_skinny_kernel(GemmArgs
   epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in, false, nullptr);
 }
 
-// Sum of the split partials of either GEMM kernel + epilogue.  Thread t
+// Sum of the split partials of the tile or wide kernel + epilogue.  Thread t
 // owns 8 consecutive columns of one row (chunk c = 256 blockIdx.x + t: row
 // c / CH, columns 8 (c % CH) .., CH = ceil(N / 8) chunks per row) and runs
 // the tile kernel's 8-column epilogue on them; the partials are read 16
@@ -1647,7 +1671,12 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
     }
   }
   const float r = p.rownorm ? rsqrtf(ss / (float)K + p.rownorm_eps) : 1.f;
-  epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in, false, nullptr);
+  // hand-over outputs (PLAIN, N % 64 == 0): the 8 consecutive lanes of a
+  // row's 64-column block
+  const bool ho = MODE == FVX_GEMM_PLAIN && (p.ss_out || p.a8_out);
+  float xo[8];
+  epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in, ho, xo);
+  if (ho) epi_handoff(p, cnt > 0, ((nn / 8) & 7) == 0, m, nn, cnt, xo);
 }
 
 // ---------------------------------------------------------------------------
@@ -1862,6 +1891,12 @@ struct TilePlan {
 // up to 25 % and 4 stages more).  A long
 // K (>= 4096) with fewer than 128 tiles is split in two (SigLIP fc2); with
 // more tiles the partials cost more than the idle CUs.
+// The wide kernel splits K for PLAIN bf16 GEMMs without a fused RMSNorm;
+// the reduce kernel's hand-over outputs need whole 64-column blocks.
+static bool wide_split_ok(const GemmArgs& d) {
+  return d.mode == FVX_GEMM_PLAIN && !d.b_fp8 && !d.rownorm && d.n % 64 == 0;
+}
+
 static TilePlan plan_tile(const GemmArgs& d) {
   TilePlan t;
   const bool gg = d.mode == FVX_GEMM_GEGLU;
@@ -1881,6 +1916,17 @@ static TilePlan plan_tile(const GemmArgs& d) {
     t.cfg = kWideCfg;
     return t;
   }
+  // A long K with few wide tiles (the prefix down projection at bs=1: 32
+  // tiles, K = 16384): the wide kernel over up to 8 K ranges, one per XCD,
+  // so that every byte of A and B passes one L2 (the 64 x 128 grid makes
+  // each XCD stream all of A); fp32 partials, then
+  // gemm_partial_reduce_kernel runs the epilogue and the hand-overs
+  if (wide_ok && wide_split_ok(d) && d.split_k == 0 && d.m > 256 && wtiles <= 64 &&
+      d.k >= 8192) {
+    t.cfg = kWideCfg;
+    t.splits = (int)(256 / wtiles < 8 ? 256 / wtiles : 8);
+    return t;
+  }
   if (gg && wtiles >= 256) t.cfg = 1;
   else t.cfg = tiles <= 256 ? 2 : 0;
   if (d.ss_out || d.a8_out) return t;  // written by the one-pass epilogue
@@ -1895,7 +1941,10 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   const int bm = tile_bm(cfg, d.b_fp8), bn = kTileBN[cfg] / (gg ? 2 : 1);
   const int m_tiles = (int)((d.m + bm - 1) / bm);
   const int n_tiles = (int)((d.n + bn - 1) / bn);
-  if (splits < 1 || d.ss_out || d.a8_out) splits = 1;  // hand-overs: one-pass epilogue
+  // hand-overs come from a one-pass epilogue, except through the reduce
+  // kernel behind a split wide kernel
+  if (splits < 1 || (cfg == kWideCfg ? !wide_split_ok(d) : (d.ss_out || d.a8_out)))
+    splits = 1;
   const int64_t bk = d.b_fp8 ? 128 : 64;
   int64_t kchunk = (d.k + splits - 1) / splits;
   kchunk = (kchunk + bk - 1) / bk * bk;
@@ -1920,15 +1969,17 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   if (cfg == kWideCfg) {
     FVX_REQUIRE(d.k % 64 == 0 && d.mode != FVX_GEMM_EULER, FVX_ERR_ARG,
                 "gemm: the wide kernel needs K %% 64 == 0, no EULER");
-    // 256 x 256 tiles (GEGLU: 256 x 2 x 128), 4 waves of 128 x 128
+    // 256 x 256 tiles (GEGLU: 256 x 2 x 128), 4 waves of 128 x 128; with
+    // splits, (split, tile) workgroups
     const unsigned nb = (unsigned)(m_tiles * n_tiles);
-#define LW(MODE)                                                                    \
-  if (d.rownorm && !d.ss_in)                                                        \
-    hipLaunchKernelGGL((gemm_wide_kernel<MODE, true>), dim3(nb), dim3(256), 0, s, d,  \
-                       m_tiles, n_tiles, vec_ok);                                   \
-  else                                                                              \
-    hipLaunchKernelGGL((gemm_wide_kernel<MODE, false>), dim3(nb), dim3(256), 0, s, d, \
-                       m_tiles, n_tiles, vec_ok)
+    const unsigned nbs = nb * (unsigned)splits;
+#define LW(MODE)                                                                     \
+  if (d.rownorm && !d.ss_in)                                                         \
+    hipLaunchKernelGGL((gemm_wide_kernel<MODE, true>), dim3(nbs), dim3(256), 0, s, d,  \
+                       m_tiles, n_tiles, vec_ok, splits, (int)kchunk);               \
+  else                                                                               \
+    hipLaunchKernelGGL((gemm_wide_kernel<MODE, false>), dim3(nbs), dim3(256), 0, s, d, \
+                       m_tiles, n_tiles, vec_ok, splits, (int)kchunk)
     // the e4m3 copy of A is used when given (a rownorm then needs ss_in)
     const bool f8a = d.a8 && d.a8_scale && (!d.rownorm || d.ss_in);
 #define LW8(MODE)                                                                          \
@@ -1956,30 +2007,32 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     }
 #undef LW8
 #undef LW
-    return launch_status("gemm(wide)");
-  }
-  dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
-#define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_)                                   \
-  hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_>), grid,  \
-                     dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits,      \
-                     kchunk, vec_ok)
-  // fp8 tiles hold 128-k slabs (bf16 A rows of 256 bytes): config 1 becomes
-  // 128 x 256 to stay within the LDS
-#define LCFG(MODE)                                                   \
-  if (d.b_fp8) {                                                     \
-    if (cfg == 1) LT(128, 256, 2, 4, 2, MODE, true);                 \
-    else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, true);             \
-    else LT(64, 128, 2, 2, 2, MODE, true);                           \
-  } else {                                                           \
-    if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false);                \
-    else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false);            \
-    else LT(64, 128, 2, 2, 3, MODE, false);                          \
-  }
-  FVX_MODE_DISPATCH(d.mode, LCFG)
+    const int stw = launch_status("gemm(wide)");
+    if (stw || splits == 1) return stw;
+  } else {
+    dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
+#define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_)                                      \
+    hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_>), grid,\
+                       dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits,     \
+                       kchunk, vec_ok)
+    // fp8 tiles hold 128-k slabs (bf16 A rows of 256 bytes): config 1 becomes
+    // 128 x 256 to stay within the LDS
+#define LCFG(MODE)                                                                    \
+    if (d.b_fp8) {                                                                    \
+      if (cfg == 1) LT(128, 256, 2, 4, 2, MODE, true);                                \
+      else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, true);                            \
+      else LT(64, 128, 2, 2, 2, MODE, true);                                          \
+    } else {                                                                          \
+      if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false);                               \
+      else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false);                           \
+      else LT(64, 128, 2, 2, 3, MODE, false);                                         \
+    }
+    FVX_MODE_DISPATCH(d.mode, LCFG)
 #undef LCFG
 #undef LT
-  int st3 = launch_status("gemm(tile)");
-  if (st3 || splits == 1) return st3;
+    int st3 = launch_status("gemm(tile)");
+    if (st3 || splits == 1) return st3;
+  }
   const int64_t chunks = d.m * ((d.n + 7) / 8);
 #define L(MODE)                                                                  \
   hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                           \

@@ -109,3 +109,38 @@ def test_wide_qkv_rope(K, cuda):
     assert rel_err(q.cpu()[rows].view(-1, nq, hd)[:, :, inv], rq) <= REL_TOL
     assert rel_err(kk.cpu()[rows][:, inv], rk.view(-1, hd)) <= REL_TOL
     assert rel_err(vv.cpu()[rows], rv) <= REL_TOL
+
+
+def test_wide_split_k_down(K, cuda):
+    """The prefix down projection at bs=1 (M=816, N=2048, K=16384: 32 wide
+    tiles) runs the wide kernel over 8 K ranges, then the split-K reduce
+    runs the epilogue (residual in place) and the hand-overs: row sums of
+    squares of the stored output and its e4m3 copy.  Checked against an
+    fp32 GEMM (bf16 op bar), float64 sums and the quantization
+    restatement of the stored output, and against the one-pass 64 x 128
+    kernel (split_k=1) within one bf16 rounding step."""
+    announce('wide split-K down m=816 k=16384')
+    from tests.test_fp8_gpu import quant_blocks_ref
+    m, n, k = 816, 2048, 16384
+    a = randn((m, k), 31)
+    w = randn((n, k), 32, std=0.01)
+    res = randn((m, n), 33)
+    parts = K.ss_parts(n)
+    outs = []
+    for sk in (0, 1):
+        x = res.to(cuda)
+        ss = torch.zeros(parts, m, device=cuda)
+        a8 = K.Fp8Act.empty(m, n, cuda)
+        K.gemm(a.to(cuda), w.to(cuda), out=x, residual=x, ss_out=ss, a8_out=a8,
+               split_k=sk)
+        outs.append((x.cpu(), ss.cpu(), a8))
+    x, ss, a8 = outs[0]
+    ref = a.float() @ w.float().t() + res.float()
+    assert rel_err(x, ref) <= REL_TOL
+    want = x.double().view(m, parts, 64).pow(2).sum(-1).t()
+    assert ((ss.double() - want).abs() <= 1e-5 * want + 1e-6).all()
+    q, e = quant_blocks_ref(x)
+    assert torch.equal(a8.data.cpu(), q)
+    assert torch.equal(a8.scale.cpu()[:, :m].t(), e)
+    x1 = outs[1][0]
+    assert ((x.double() - x1.double()).abs() <= 2.0**-7 * x1.double().abs() + 1e-3).all()
