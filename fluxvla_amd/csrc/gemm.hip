@@ -909,6 +909,12 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
 #pragma unroll
     for (int j = 0; j < 4; ++j) bfr[b][j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
   };
+  // 32-row blocks of this wave that hold rows < M (the last M tile of the
+  // prefix, 816 = 3 x 256 + 48 rows, has 2 of 8): the others skip their
+  // MFMAs, so that tile finishes early and its CU takes the next one
+  bool blk_ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) blk_ok[i] = m0 + wm * 128 + 32 * i < M;
   for (int x = 0; x < 8; ++x) issue1(nk > 1 ? 1 : 0, 1, x);
   wait_vmcnt<8>();
   __syncthreads();
@@ -930,8 +936,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if (SUM_A) ss[i] += sumsq8(af[b][i]);
+        if (blk_ok[i])
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
         if (ks == 0) {
           issue1(t1, st ^ 1, 8 + 2 * i);
           issue1(t1, st ^ 1, 9 + 2 * i);
