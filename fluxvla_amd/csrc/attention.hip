@@ -375,7 +375,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(fvx_attn_desc p,
 constexpr int kDecKT = 64;                      // keys per tile
 constexpr int kDecPP = kDecKT + 8;              // LDS pitch (elements), P rows
 constexpr int kDecOP = 256 + 4;                 // LDS pitch (floats), O rows
-constexpr int64_t kDecPF = 64 * 256 + 2 * 64;   // partial floats per workgroup
+// partial per workgroup: O rows [64][256] bf16 (un-normalized), then the 64
+// row references and the 64 row sums (fp32); sizes in floats
+constexpr int64_t kDecPO = 64 * 256 / 2;
+constexpr int64_t kDecPF = kDecPO + 2 * 64;
 // LDS map (bytes): two stages of [K tile 64 x 512 B | V^T tile 256 x 128 B]
 // (stage 1 first holds the Q rows), then P [2][64][kDecPP] bf16, the row
 // maxima [2][64][4] f32, the key groups [2][4 waves][64] and the query
@@ -687,12 +690,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int c = tid + 256 * u, i = c >> 5, d0 = (c & 31) * 8;
-    *(f32x4_t*)(part + i * 256 + d0) = *(const f32x4_t*)&sO[i * kDecOP + d0];
-    *(f32x4_t*)(part + i * 256 + d0 + 4) = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
+    st8((bf16_t*)part + i * 256 + d0, pack8(&sO[i * kDecOP + d0]));
   }
   if (tid < 64) {
-    part[64 * 256 + tid] = sM[tid];
-    part[64 * 256 + 64 + tid] = ((sL[0][tid] + sL[1][tid]) + sL[2][tid]) + sL[3][tid];
+    part[kDecPO + tid] = sM[tid];
+    part[kDecPO + 64 + tid] = ((sL[0][tid] + sL[1][tid]) + sL[2][tid]) + sL[3][tid];
   }
 }
 
@@ -1043,16 +1045,16 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
 #pragma unroll 4
   for (int u = 0; u < 16; ++u) {
     const int c = tid + 128 * u, i = c >> 5, d0 = (c & 31) * 8;
-    *(f32x4_t*)(part + i * 256 + d0) = *(const f32x4_t*)&sO[i * kDecOP + d0];
-    *(f32x4_t*)(part + i * 256 + d0 + 4) = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
+    st8((bf16_t*)part + i * 256 + d0, pack8(&sO[i * kDecOP + d0]));
   }
   if (tid < 64) {
-    part[64 * 256 + tid] = sMq[tid];
-    part[64 * 256 + 64 + tid] = sLq[tid];
+    part[kDecPO + tid] = sMq[tid];
+    part[kDecPO + 64 + tid] = sLq[tid];
   }
 }
 
-// Merge of the decode partials: one thread per (problem, query row, 4 dims);
+// Merge of the decode partials (bf16 O rows: half the bytes of fp32, within
+// the output's own bf16 rounding): one thread per (problem, query row, 4 dims);
 // the loads of up to 16 splits are issued before the running-max merge,
 // which is applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
@@ -1068,15 +1070,20 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
   float acc[4] = {0.f, 0.f, 0.f, 0.f}, M = -INFINITY, L = 0.f;
   for (int s0 = 0; s0 < splits; s0 += 16) {
-    f32x4_t a[16];
+    float a[16][4];
     float mv[16], lv[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       // splits past the end read as zero (out of the buffer view)
       const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
-      a[u] = bload4f(rw, off + (uint32_t)(i * 256 + d0) * 4);
-      mv[u] = bload1f(rw, off + (uint32_t)(64 * 256 + i) * 4);
-      lv[u] = bload1f(rw, off + (uint32_t)(64 * 256 + 64 + i) * 4);
+      const uint2 ob = __builtin_bit_cast(
+          uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, off + (uint32_t)(i * 256 + d0) * 2, 0, 0));
+      a[u][0] = __uint_as_float(ob.x << 16);
+      a[u][1] = __uint_as_float(ob.x & 0xffff0000u);
+      a[u][2] = __uint_as_float(ob.y << 16);
+      a[u][3] = __uint_as_float(ob.y & 0xffff0000u);
+      mv[u] = bload1f(rw, off + (uint32_t)(kDecPO + i) * 4);
+      lv[u] = bload1f(rw, off + (uint32_t)(kDecPO + 64 + i) * 4);
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
