@@ -1072,7 +1072,8 @@ struct Gw8Layout {
 
 template <int MODE, bool SUM_A, bool F8A>
 __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_tiles,
-                                                              int n_tiles, int vec_ok) {
+                                                              int n_tiles, int vec_ok,
+                                                              int splits, int kchunk) {
   typedef Gw8Layout<F8A> LY;
   constexpr bool GG = MODE == FVX_GEMM_GEGLU;
   constexpr int WNO = GG ? 64 : 128;  // output columns per wave
@@ -1084,12 +1085,17 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
+  // XCD-aware order over (split, tile), as in gemm_wide_kernel
   const int nblk = m_tiles * n_tiles;
-  const int bid = xcd_remap(blockIdx.x, nblk);
+  const int lid = xcd_remap(blockIdx.x, nblk * splits);
+  const int bid = lid % nblk, split = lid / nblk;
   const int m_tile = bid % m_tiles, n_tile = bid / m_tiles;
   const int64_t M = p.m, N = p.n, K = p.k;
   const int64_t m0 = (int64_t)m_tile * kGwBM, n0 = (int64_t)n_tile * (GG ? 128 : 256);
-  const int nk = (int)(K / 64);
+  // K range [kb, kb + 64 nk) (splits > 1: PLAIN without rownorm, partials
+  // scaled by the weight scales for gemm_partial_reduce_kernel)
+  const int64_t kb = (int64_t)split * kchunk;
+  const int nk = (int)(((kb + kchunk < K ? kb + kchunk : K) - kb) / 64);
 
   // this wave's band: 128 rows of A (waves 0, 1; 16 loads of 8 rows x 128 B
   // per slab) or of B (2, 3; 8 loads of 16 rows x 64 B)
@@ -1099,13 +1105,13 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   const int64_t nrows = rlim <= 0 ? 0 : (rlim < 128 ? rlim : 128);
   const uint32_t ld = isa ? (F8A ? (uint32_t)p.a8_ld : (uint32_t)p.lda * 2)
                           : (uint32_t)p.ldb;  // bytes per row
-  const char* band = isa ? (F8A ? (const char*)p.a8 + r0 * p.a8_ld
-                                : (const char*)p.a + r0 * p.lda * 2)
-                         : (const char*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb;
+  const char* band = isa ? (F8A ? (const char*)p.a8 + r0 * p.a8_ld + kb
+                                : (const char*)p.a + r0 * p.lda * 2 + kb * 2)
+                         : (const char*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb + kb;
   const i32x4_t rs = make_rsrc4(band, (uint32_t)(nrows * ld));
   // F8A: the slab's 256 A exponents, one dword per lane (rows 4 l .. 4 l + 3)
   const i32x4_t rse = make_rsrc4(F8A ? p.a8_scale : p.a,
-                                 F8A ? (uint32_t)((int64_t)nk * p.a8_sld) : 0u);
+                                 F8A ? (uint32_t)((K / 64) * p.a8_sld) : 0u);
   uint32_t vo0, vo1, lds0;
   if (isa && !F8A) {
     // rows 8 i + (lane >> 3), slot lane & 7 <- chunk slot ^ ((row >> 1) & 7)
@@ -1125,7 +1131,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   auto issue_q = [&](int t, int stage, int q) {
     if (F8A && wave == 0 && q == 0)
       load_lds4(rse, lds_addr(smem) + stage * kGw8Stage + LY::A + LY::B,
-                (uint32_t)(t * p.a8_sld + m0 + 4 * lane));
+                (uint32_t)((kb / 64 + t) * p.a8_sld + m0 + 4 * lane));
     if (isa && !F8A) {
       const uint32_t so = (uint32_t)t * 128u;
 #pragma unroll
@@ -1259,6 +1265,27 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
       default: to_scr(IntC<3>{}); break;
     }
     const int64_t rb = m0 + wm * 128 + 32 * i;
+    if (splits > 1) {
+      // partials of this K range, scaled by the weight scales:
+      // ws[(split M + m) N + n]
+      float* ws = (float*)((char*)p.workspace + kCounterBytes) + (int64_t)split * M * N;
+#pragma unroll 1
+      for (int e = 0; e < ITEMS; ++e) {
+        const int q = lane + 64 * e, row = q / CH, ch = q % CH;
+        const int64_t m = rb + row, nn = nw0 + 8 * ch;
+        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+        if (m < M && cnt > 0) {
+          const bool vec = vec_ok && cnt == 8;
+          float w0[8], v[8];
+          bl_f8(rsc, (uint32_t)(nn * 4), vec, w0);
+          const float* sv = scr + row * kGwELD + 8 * ch;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) v[x] = sv[x] * w0[x];
+          st_f8(ws + m * N + nn, v, (N & 3) == 0 && cnt == 8, cnt);
+        }
+      }
+      continue;
+    }
 #pragma unroll 1
     for (int e0 = 0; e0 < ITEMS; e0 += EB) {
       EpiIn in[EB];
@@ -1898,10 +1925,10 @@ struct TilePlan {
 // up to 25 % and 4 stages more).  A long
 // K (>= 4096) with fewer than 128 tiles is split in two (SigLIP fc2); with
 // more tiles the partials cost more than the idle CUs.
-// The wide kernel splits K for PLAIN bf16 GEMMs without a fused RMSNorm;
+// The wide kernels split K for PLAIN GEMMs without a fused RMSNorm;
 // the reduce kernel's hand-over outputs need whole 64-column blocks.
 static bool wide_split_ok(const GemmArgs& d) {
-  return d.mode == FVX_GEMM_PLAIN && !d.b_fp8 && !d.rownorm && d.n % 64 == 0;
+  return d.mode == FVX_GEMM_PLAIN && (!d.b_fp8 || FVX_WIDE_F8) && !d.rownorm && d.n % 64 == 0;
 }
 
 static TilePlan plan_tile(const GemmArgs& d) {
@@ -1989,16 +2016,16 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
                        m_tiles, n_tiles, vec_ok, splits, (int)kchunk)
     // the e4m3 copy of A is used when given (a rownorm then needs ss_in)
     const bool f8a = d.a8 && d.a8_scale && (!d.rownorm || d.ss_in);
-#define LW8(MODE)                                                                          \
-  if (d.rownorm && !d.ss_in)                                                               \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true, false>), dim3(nb), dim3(256), 0, s, \
-                       d, m_tiles, n_tiles, vec_ok);                                       \
-  else if (f8a)                                                                            \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, true>), dim3(nb), dim3(256), 0, s, \
-                       d, m_tiles, n_tiles, vec_ok);                                       \
-  else                                                                                     \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, false>), dim3(nb), dim3(256), 0, s, \
-                       d, m_tiles, n_tiles, vec_ok)
+#define LW8(MODE)                                                                           \
+  if (d.rownorm && !d.ss_in)                                                                \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true, false>), dim3(nbs), dim3(256), 0, s, \
+                       d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);                   \
+  else if (f8a)                                                                             \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, true>), dim3(nbs), dim3(256), 0, s, \
+                       d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);                   \
+  else                                                                                      \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, false>), dim3(nbs), dim3(256), 0,  \
+                       s, d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk)
     if (d.b_fp8) {
       switch (d.mode) {
         case FVX_GEMM_GEGLU: LW8(FVX_GEMM_GEGLU); break;

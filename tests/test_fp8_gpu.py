@@ -285,3 +285,40 @@ def test_fp8_handover_consumer_identical(K, cuda):
             got = K.gemm(x, fw, residual=res, a8=a8)
             own = K.gemm(x, fw, residual=res)
         assert torch.equal(got, own)
+
+
+def test_fp8_wide_split_k_down(K, cuda):
+    """The fp8 prefix down projection at bs=1 (M=816, N=2048, K=16384, fp8
+    weights): the fp8 wide kernel over 8 K ranges, partials scaled by the
+    weight scales, then the split-K reduce (residual in place, row sums and
+    e4m3 copy of the output).  A both ways: the e4m3 copy handed over by a
+    producer (a8) and bf16 quantized in the kernel.  Against the float64
+    quantization restatement (bf16 op bar), and the hand-overs against the
+    stored output."""
+    announce('fp8 wide split-K down m=816 k=16384')
+    m, n, k = 816, 2048, 16384
+    a0 = randn((m, 512), 190)
+    w0 = randn((k, 512), 191, std=0.05).to(cuda)
+    fw, wq = fp8_weight(K, randn((n, k), 192, std=0.01), cuda)
+    res = randn((m, n), 193)
+    # producer: A (bf16) and its e4m3 copy
+    a = torch.empty(m, k, dtype=torch.bfloat16, device=cuda)
+    a8 = K.Fp8Act.empty(m, k, cuda)
+    K.gemm(a0.to(cuda), w0, out=a, a8_out=a8)
+    rows = sample_rows(m)
+    ac = a.cpu()
+    ref = quant_a_ref(ac[rows], skinny=False) @ wq.t() + res[rows].double()
+    parts = K.ss_parts(n)
+    for use_a8 in (True, False):
+        x = res.to(cuda)
+        ss = torch.zeros(parts, m, device=cuda)
+        o8 = K.Fp8Act.empty(m, n, cuda)
+        K.gemm(a, fw, out=x, residual=x, ss_out=ss, a8_out=o8,
+               a8=a8 if use_a8 else None)
+        got = x.cpu()
+        assert rel_err(got[rows], ref) <= REL_TOL
+        want = got.double().view(m, parts, 64).pow(2).sum(-1).t()
+        assert ((ss.cpu().double() - want).abs() <= 1e-5 * want + 1e-6).all()
+        q, e = quant_blocks_ref(got)
+        assert torch.equal(o8.data.cpu(), q)
+        assert torch.equal(o8.scale.cpu()[:, :m].t(), e)
