@@ -718,8 +718,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
 // (one shuffle), and O^T's accumulators of lane (q, h) all belong to row q,
 // so nothing needs a cross-lane exchange.  There is no online rescale of
 // the 128 O accumulators (which would pull them out of the AGPRs every
-// tile): a row's exp2 reference is its maximum over the first tile in which
-// it sees a key, so P = 2^(s - ref) <= 2^32 as long as no later score
+// tile): a row's exp2 reference is its maximum over the first 32-key block
+// in which it sees a key, so P = 2^(s - ref) <= 2^32 as long as no later score
 // exceeds the reference by more than 32 (in the exp2 domain) -- fp32 and
 // bf16 hold that with room to spare.  Should any row of the workgroup go
 // further, the workgroup runs its key range a second time with each row's
@@ -736,7 +736,7 @@ constexpr int kDtStage = kDtKB + kDtVB + 256;    // + the tile's key groups
 constexpr int kDtOffQG = 2 * kDtStage;           // query groups [64]
 constexpr int kDtLDS = kDtOffQG + 64 * 4;
 static_assert(64 * kDecOP * 4 <= 2 * kDtStage, "O rows fit the stages");
-constexpr float kDtLazy = 32.f;                  // log2 of the largest P
+constexpr float kDtRefSlack = 32.f;              // log2 of the largest P
 constexpr int kDecTKps = 4 * kDecKT;             // keys per range that select it
 
 __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
@@ -907,8 +907,7 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
       return ld8(&sV[d * 64 + 8 * ((2 * (j >> 3) + h) ^ ((d >> 1) & 7))]);
     };
     // the tile (masking only on the edge tile or with key groups in play)
-    auto tile = [&](auto masked) {
-      constexpr bool MASKED = decltype(masked)::value;
+    {
       // S^T: step j = 2 s + kb (key block kb, dims 16 s ..; the two blocks'
       // accumulations alternate, so that no MFMA waits for the previous
       // one's result), the K fragments through a ring of 8 register sets
@@ -926,7 +925,7 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
       auto softmax = [&](auto kbc) {
         constexpr int kb = decltype(kbc)::value;
         f32x16_t& sv = sacc[kb];
-        if (MASKED && (edge || gmask)) {
+        if (edge || gmask) {  // uniform
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) {
             const int kl0 = 32 * kb + 16 * hf + 8 * h;
@@ -950,7 +949,7 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
         if (m_ref == -INFINITY)
           m_ref = mb;
         else
-          over = over || mb > m_ref + kDtLazy;
+          over = over || mb > m_ref + kDtRefSlack;
         const float nm = m_ref == -INFINITY ? 0.f : -m_ref;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
@@ -989,12 +988,11 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
         o[j & 7] = mfma32x32x16(ring[j & 7], pT[j >> 3], o[j & 7]);
         if (j == 3) softmax(IntC<1>{});
       });
-    };
-    tile(BoolC<true>{});
+    }
   }
   wait_vmcnt<0>();
   // every wave is done with the ring; a row whose scores rose more than
-  // 2^kDtLazy above its reference sends the workgroup through a second
+  // 2^kDtRefSlack above its reference sends the workgroup through a second
   // pass with the exact row maxima as references (P <= 1)
   if (!__syncthreads_or(over) || pass) break;
   m_ref = m_max;

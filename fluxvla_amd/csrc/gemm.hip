@@ -1905,6 +1905,9 @@ constexpr int kWideCfg = 3;  // gemm_wide_kernel
 #ifndef FVX_WIDE_F8
 #define FVX_WIDE_F8 1
 #endif
+#ifndef FVX_WIDE_SPLIT_MIN_K
+#define FVX_WIDE_SPLIT_MIN_K 8192
+#endif
 
 static int tile_bm(int cfg, int fp8) {
   if (fp8) return cfg == 1 ? 128 : (cfg == 3 ? 256 : 64);
@@ -1956,7 +1959,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   // each XCD stream all of A); fp32 partials, then
   // gemm_partial_reduce_kernel runs the epilogue and the hand-overs
   if (wide_ok && wide_split_ok(d) && d.split_k == 0 && d.m > 256 && wtiles <= 64 &&
-      d.k >= 8192) {
+      d.k >= FVX_WIDE_SPLIT_MIN_K) {
     t.cfg = kWideCfg;
     t.splits = (int)(256 / wtiles < 8 ? 256 / wtiles : 8);
     return t;
