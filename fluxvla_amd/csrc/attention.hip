@@ -1052,34 +1052,29 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
 }
 
 // Merge of the decode partials (bf16 O rows: half the bytes of fp32, within
-// the output's own bf16 rounding): one thread per (problem, query row, 4 dims);
-// the loads of up to 16 splits are issued before the running-max merge,
-// which is applied in split order.
+// the output's own bf16 rounding): one thread per (problem, query row, 8
+// dims); the loads of up to 16 splits are issued before the running-max
+// merge, which is applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
     fvx_attn_desc p, int n_rg, int splits, int hs) {
   const int R = (int)(p.sq * p.heads);
   const int gid = blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int)p.n_problems * R * 64) return;
-  const int d0 = (gid & 63) * 4;
-  const int zr = gid >> 6;
+  if (gid >= (int)p.n_problems * R * 32) return;
+  const int d0 = (gid & 31) * 8;
+  const int zr = gid >> 5;
   const int z = zr / R, r = zr % R;
   const int rg = r >> 6, i = r & 63;
   const float* base = (const float*)p.workspace + (((int64_t)z * n_rg + rg) * splits) * kDecPF;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
-  float acc[4] = {0.f, 0.f, 0.f, 0.f}, M = -INFINITY, L = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, M = -INFINITY, L = 0.f;
   for (int s0 = 0; s0 < splits; s0 += 16) {
-    float a[16][4];
+    bf16x8 a[16];
     float mv[16], lv[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       // splits past the end read as zero (out of the buffer view)
       const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
-      const uint2 ob = __builtin_bit_cast(
-          uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, off + (uint32_t)(i * 256 + d0) * 2, 0, 0));
-      a[u][0] = __uint_as_float(ob.x << 16);
-      a[u][1] = __uint_as_float(ob.x & 0xffff0000u);
-      a[u][2] = __uint_as_float(ob.y << 16);
-      a[u][3] = __uint_as_float(ob.y & 0xffff0000u);
+      a[u] = bload8(rw, off + (uint32_t)(i * 256 + d0) * 2);
       mv[u] = bload1f(rw, off + (uint32_t)(kDecPO + i) * 4);
       lv[u] = bload1f(rw, off + (uint32_t)(kDecPO + 64 + i) * 4);
     }
@@ -1089,8 +1084,10 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
         const float mn = fmaxf(M, mv[u]);
         const float mr = (mn == -INFINITY) ? 0.f : mn;
         const float wa = exp2f(M - mr), wb = exp2f(mv[u] - mr);
+        float av[8];
+        unpack8(a[u], av);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = acc[e] * wa + a[u][e] * wb;
+        for (int e = 0; e < 8; ++e) acc[e] = acc[e] * wa + av[e] * wb;
         L = L * wa + lv[u] * wb;
         M = mn;
       }
@@ -1098,8 +1095,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) acc[e] *= inv;
-  dec_store<4>(p, z, r, d0, hs, acc);
+  for (int e = 0; e < 8; ++e) acc[e] *= inv;
+  dec_store<8>(p, z, r, d0, hs, acc);
 }
 
 struct AttnPlan {
@@ -1270,7 +1267,7 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
                          0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
     int st = launch_status("attention(decode)");
     if (st || a.splits == 1) return st;
-    const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 64;
+    const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 32;
     hipLaunchKernelGGL(attn_decode_merge_kernel,
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                        d, a.n_rb, a.splits, hs);
