@@ -1014,8 +1014,9 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
 #pragma unroll
     for (int db = 0; db < 8; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        sO[rl * kDecOP + 32 * db + 8 * (r >> 2) + 4 * h + (r & 3)] = o[db][r];
+      for (int j = 0; j < 4; ++j)  // elements 4 j .. 4 j + 3: 4 consecutive dims
+        *(f32x4_t*)&sO[rl * kDecOP + 32 * db + 8 * j + 4 * h] =
+            f32x4_t{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
     if (h == 0) {
       sLq[rl] = l_run;
       sMq[rl] = m_ref;
