@@ -18,9 +18,12 @@
 // and never produce NaN (a row that has seen no visible key yet keeps a zero
 // reference).  With kv_splits > 1 each split writes (O, m, l) partials to a
 // workspace and a merge kernel, the next kernel on the stream, combines them
-// in split order (deterministic).  The decode-shaped action-expert attention
-// (408 query rows against the 867-key prefix+suffix cache) runs the
-// barrier-free attn_decode_kernel further below.
+// in split order (deterministic).  This kernel serves SigLIP (head dim 72)
+// and any head dim other than 256 or a non-transposed V.  Head dim 256 with
+// the transposed value cache runs attn_decode_kernel (the action expert: 408
+// query rows against the 867-key prefix+suffix cache, one 64-key tile per
+// workgroup) or attn_decode_t_kernel (the prefix prefill, key ranges of >= 4
+// tiles), both further below.
 #include <math.h>
 
 #include "capi_util.h"

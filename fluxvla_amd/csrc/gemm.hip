@@ -1,34 +1,35 @@
-// bf16 MFMA GEMM family with fused epilogues (gfx950).
+// bf16 / fp8 MFMA GEMM family with fused epilogues (gfx950).
 //
 //   acc[m][n] = sum_k A[m][k] * B[n][k]      A: activations, B: nn.Linear weight
 //
-// Two kernels share one epilogue:
+// Kernels (all share the 8-column epilogue epi_load / epi_store):
 //
-//  * gemm_tile_kernel<BM, BN, MODE>: 256 threads, 2x2 waves, BMxBN output tile,
-//    K staged through LDS 64 at a time (register prefetch of the next K slab
-//    while the current one feeds v_mfma_f32_16x16x32_bf16).  Used when M > 64
-//    (SigLIP M=768, Gemma prefix M=816, batched expert).  Tiles are ordered
-//    m-fastest within an n-panel and block ids are remapped so that one XCD
-//    owns consecutive tiles: the m-tiles of one weight panel run on the same
-//    XCD back to back and reuse that panel from its L2.
+//  * gemm_tile_kernel<BM, BN, WGM, WGN, STAGES, MODE, FP8>: M > 64 (SigLIP
+//    M=768, Gemma prefix M=816, batched expert).  64 x 128 tiles of 2 x 2
+//    waves on v_mfma_f32_32x32x16_bf16 (fp8: the block-scaled 32x32x64), K in
+//    64-wide slabs through a 3- or 4-stage LDS ring filled by LDS DMA
+//    (buffer_load ... lds), the slab loads spread between MFMA groups.
+//  * gemm_wide_kernel<MODE, SUM_A> / gemm_wide_f8_kernel: 256 x 256 tiles of
+//    4 waves (128 x 128 each, accumulators in AGPRs) for the prefix gate/up
+//    at every batch, batched prefixes, and -- over up to 8 K ranges, one
+//    per XCD -- long-K GEMMs with few tiles (the prefix down projection).
+//  * gemm_skinny_kernel<MODE, FP8>: M <= 64 (the bs=1 action expert,
+//    M=50/51).  A weight stream: a workgroup owns 16 output columns and
+//    reads its weight rows straight from memory as MFMA B fragments
+//    (fragment-major weights: 1 KiB per operand); K splits over workgroups
+//    meet through write-through partials and an arrival counter.
+//  * gemm_partial_reduce_kernel: the split-K sum (in split order,
+//    deterministic) and epilogue behind the tile and wide kernels.
 //
-//  * gemm_skinny_kernel<MODE>: M <= 64 (the bs=1 action expert, M=50/51).
-//    The op is a weight stream: each wave owns 16 output columns and pulls
-//    its weight rows straight from HBM as MFMA B fragments (16 contiguous
-//    bytes per lane); the activation slab is staged once per workgroup in
-//    LDS.  K is split over blockIdx.y in ranges of <= 256 so that ~256+
-//    workgroups stream weights; fp32 partials go to a workspace and
-//    gemm_partial_reduce_kernel, the next kernel on the stream, sums them in
-//    split order (deterministic) and runs the epilogue.  (A single-kernel
-//    variant in which the last workgroup to arrive reduced the partials
-//    behind device-scope fences cost 30-40 us per GEMM on MI355X: the
-//    agent-scope release/acquire writes back and invalidates the per-XCD
-//    L2.)
+// Tiles are ordered m-fastest within a weight panel and block ids remapped
+// (xcd_remap) so that one XCD owns consecutive tiles: the m-tiles of a
+// panel run on one XCD and reuse the panel from its L2.
 //
 // Per-row RMSNorm ("rownorm") is fused: the kernel that streams A also
-// accumulates sum(A[m][:]^2) and scales the accumulator by
-// rsqrt(mean + eps) in the epilogue, so (x * r) @ W' == r * (x @ W') needs no
-// separate normalization pass (the (1 + w) Gemma scale is folded into W').
+// accumulates sum(A[m][:]^2) (or takes the sums handed over by the GEMM that
+// produced A, ss_in / ss_out) and scales the accumulator by rsqrt(mean +
+// eps) in the epilogue, so (x * r) @ W' == r * (x @ W') needs no separate
+// normalization pass (the (1 + w) Gemma scale is folded into W').
 #include "capi_util.h"
 #include "common.h"
 
