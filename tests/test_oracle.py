@@ -345,3 +345,213 @@ def test_one_step_equals_single_denoise():
     v = O.denoise_step(sd, cfg, inp['states'], pad, kvs, inp['noise'],
                        torch.tensor([1.0]))
     assert torch.allclose(out, inp['noise'] - v, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# closed forms that pin the modulation order, the gated residual, the suffix
+# embeddings and the prefix language scale (each with a planted mistake that
+# the same check must reject)
+# ---------------------------------------------------------------------------
+def _unit_rows(n, d):
+    """Rows of +-1 entries: mean(x^2) = 1 exactly, so rms-normalised x is
+    x / sqrt(1 + eps)."""
+    g = torch.Generator().manual_seed(40)
+    return torch.where(torch.rand(n, d, generator=g) > 0.5, 1.0, -1.0)
+
+
+def _adarms_closed_form_ok(fn):
+    """dense weight 0, bias [scale = 0.5 | shift = 2 | gate = -3]: for x =
+    +-1 the output must be n * 1.5 + 2 with n = x / sqrt(1 + eps), i.e.
+    ~3.5 for +1 and ~0.5 for -1 (condition_gemma.py:136-145 chunks the
+    modulation as scale, shift, gate), and the gate -3 everywhere."""
+    eps = 1e-6
+    d = 8
+    x = _unit_rows(6, d)[None]
+    cond = torch.randn(1, 5, generator=torch.Generator().manual_seed(41))
+    b = torch.cat([torch.full((d,), 0.5), torch.full((d,), 2.0),
+                   torch.full((d,), -3.0)])
+    y, gate = fn(x, cond, torch.zeros(3 * d, 5), b, eps)
+    n = 1.0 / math.sqrt(1.0 + eps)
+    want = torch.where(x > 0, 1.5 * n + 2.0, -1.5 * n + 2.0)
+    return (torch.allclose(y, want, atol=1e-6) and
+            torch.allclose(gate, torch.full_like(gate, -3.0)))
+
+
+def test_adarms_modulation_order_closed_form():
+    assert _adarms_closed_form_ok(O.ada_rms_norm)
+
+    # planted mistakes: scale/shift swapped, gate taken from the wrong chunk
+    def swapped(x, cond, w, b, eps):
+        d = b.numel() // 3
+        b2 = torch.cat([b[d:2 * d], b[:d], b[2 * d:]])
+        return O.ada_rms_norm(x, cond, w, b2, eps)
+
+    def gate_first(x, cond, w, b, eps):
+        d = b.numel() // 3
+        b2 = torch.cat([b[2 * d:], b[d:2 * d], b[:d]])
+        return O.ada_rms_norm(x, cond, w, b2, eps)
+
+    assert not _adarms_closed_form_ok(swapped)
+    assert not _adarms_closed_form_ok(gate_first)
+
+
+def _pi05_layer_sd(cfg, gate_value):
+    """One adaRMS expert layer whose dense modulations are zero except the
+    gate bias (scale = shift = 0, gate = gate_value)."""
+    sd = {k: v.float() for k, v in make_state_dict(cfg, seed=42).items()
+          if k.startswith('llm_expert.layers.0.')}
+    hid = cfg.exp_hidden
+    for norm in ('input_layernorm', 'post_attention_layernorm'):
+        pre = f'llm_expert.layers.0.{norm}.dense'
+        sd[pre + '.weight'] = torch.zeros_like(sd[pre + '.weight'])
+        sd[pre + '.bias'] = torch.cat([torch.zeros(2 * hid),
+                                       torch.full((hid,), gate_value)])
+    return sd
+
+
+def test_gated_residual_closed_form():
+    """condition_gemma.py:319-337 (`x + y * gate`): gate 0 leaves the stream
+    unchanged; gate 1 with scale = shift = 0 equals the ungated layer with a
+    plain RMSNorm of weight 0 (1 + w = 1)."""
+    cfg = tiny(pi05=True, exp_hidden=32, exp_mlp=48, heads=2, head_dim=8,
+               proj_width=16, exp_layers=1)
+    g = torch.Generator().manual_seed(43)
+    B, S = 1, 5
+    h = torch.randn(B, S, cfg.exp_hidden, generator=g)
+    cond = torch.randn(B, cfg.proj_width, generator=g)
+    pos = torch.arange(S)[None]
+    cos, sin = O.rope_cos_sin(pos, cfg.head_dim, cfg.rope_theta)
+    pre = 'llm_expert.layers.0'
+    out0, _ = O.gemma_layer(_pi05_layer_sd(cfg, 0.0), pre, h, cos, sin, None,
+                            None, cond, cfg)
+    assert torch.equal(out0, h)
+    sd1 = _pi05_layer_sd(cfg, 1.0)
+    out1, _ = O.gemma_layer(sd1, pre, h, cos, sin, None, None, cond, cfg)
+    plain = dict(sd1)
+    for norm in ('input_layernorm', 'post_attention_layernorm'):
+        plain[f'{pre}.{norm}.weight'] = torch.zeros(cfg.exp_hidden)
+    ref, _ = O.gemma_layer(plain, pre, h, cos, sin, None, None, None, cfg)
+    assert torch.allclose(out1, ref, atol=1e-5)
+    assert not torch.allclose(out1, h, atol=1e-3)
+    # gate 2: the attention and MLP deltas of the first half double
+    out2, _ = O.gemma_layer(_pi05_layer_sd(cfg, 2.0), pre, h, cos, sin, None,
+                            None, cond, cfg)
+    assert not torch.allclose(out2, out1, atol=1e-3)
+
+
+def _suffix_cfg(pi05):
+    return tiny(pi05=pi05, proj_width=32, exp_hidden=32, vit_layers=0,
+                llm_layers=0, exp_layers=0)
+
+
+def _eye_sd(cfg):
+    """Projection weights that expose the suffix embedding's structure:
+    action_in / state_proj copy their 32 inputs into the first 32 outputs,
+    action_time_mlp_in is [I | 0] (action half only), mlp_out is 2 I, time
+    MLPs are the identity; every bias is zero."""
+    w, ad = cfg.proj_width, cfg.max_action_dim
+    sd = {}
+    eye_in = torch.zeros(w, ad)
+    eye_in[:ad, :ad] = torch.eye(ad)
+    for nm in ('action_in_proj', 'state_proj'):
+        sd[f'{nm}.projector.weight'] = eye_in.clone()
+        sd[f'{nm}.projector.bias'] = torch.zeros(w)
+    sd['action_time_mlp_in.projector.weight'] = torch.cat(
+        [torch.eye(w), torch.zeros(w, w)], 1)
+    sd['action_time_mlp_in.projector.bias'] = torch.zeros(w)
+    sd['action_time_mlp_out.projector.weight'] = 2 * torch.eye(w)
+    sd['action_time_mlp_out.projector.bias'] = torch.zeros(w)
+    for nm in ('time_mlp_in', 'time_mlp_out'):
+        sd[f'{nm}.projector.weight'] = torch.eye(w)
+        sd[f'{nm}.projector.bias'] = torch.zeros(w)
+    return sd
+
+
+def test_pi0_embed_suffix_closed_form():
+    """pi0_flowmatching.py:252-321: row 0 is state_proj(state); rows 1.. are
+    mlp_out(silu(mlp_in(cat([action_in(x_t), temb])))), so with the weights
+    of _eye_sd the action rows are 2 * silu(x_t) on the first 32 dims and 0
+    elsewhere; with mlp_in = [0 | I] they become 2 * silu(temb)."""
+    cfg = _suffix_cfg(False)
+    sd = _eye_sd(cfg)
+    g = torch.Generator().manual_seed(44)
+    B, n = 2, cfg.n_action_steps
+    x_t = torch.randn(B, n, cfg.max_action_dim, generator=g)
+    states = torch.rand(B, cfg.state_dim, generator=g) * 2 - 1
+    t = torch.tensor([0.7, 0.3])
+    embs, pad, att, cond = O.embed_suffix(sd, cfg, states, x_t, t)
+    assert cond is None and embs.shape == (B, n + 1, cfg.proj_width)
+    assert torch.equal(embs[:, 0], states)            # state row first
+    silu = x_t * torch.sigmoid(x_t)
+    assert torch.allclose(embs[:, 1:], 2 * silu, atol=1e-6)
+    # planted mistakes that the same closed form must reject
+    assert not torch.allclose(embs[:, 1:], torch.nn.functional.silu(2 * x_t),
+                              atol=1e-3)              # SiLU after mlp_out
+    # time half: mlp_in = [0 | I]
+    sd['action_time_mlp_in.projector.weight'] = torch.cat(
+        [torch.zeros(cfg.proj_width, cfg.proj_width),
+         torch.eye(cfg.proj_width)], 1)
+    embs, _, _, _ = O.embed_suffix(sd, cfg, states, x_t, t)
+    temb = O.sinusoidal_pos_embedding(t, cfg.proj_width, 4e-3, 4.0)
+    want = 2 * temb * torch.sigmoid(temb)
+    assert torch.allclose(embs[:, 1:], want[:, None].expand(B, n, -1),
+                          atol=1e-6)
+
+
+def test_pi05_embed_suffix_closed_form():
+    """pi05_flowmatching.py:68-127: the tokens are action_in(x_t) alone and
+    the adaRMS condition is silu(mlp_out(silu(mlp_in(temb)))); with identity
+    time MLPs it is silu(silu(temb)), and with mlp_in = 2 I it is
+    silu(silu(2 temb)) (not 2 silu(...): the scale sits inside)."""
+    cfg = _suffix_cfg(True)
+    sd = _eye_sd(cfg)
+    g = torch.Generator().manual_seed(45)
+    B, n = 2, cfg.n_action_steps
+    x_t = torch.randn(B, n, cfg.max_action_dim, generator=g)
+    t = torch.tensor([1.0, 0.4])
+    embs, pad, att, cond = O.embed_suffix(sd, cfg, torch.zeros(B, 32), x_t, t)
+    assert embs.shape == (B, n, cfg.proj_width)
+    assert torch.equal(embs[..., :cfg.max_action_dim], x_t)
+    assert torch.equal(embs[..., cfg.max_action_dim:],
+                       torch.zeros(B, n, cfg.proj_width - cfg.max_action_dim))
+    temb = O.sinusoidal_pos_embedding(t, cfg.proj_width, 4e-3, 4.0)
+
+    def silu(v):
+        return v * torch.sigmoid(v)
+    assert torch.allclose(cond, silu(silu(temb)), atol=1e-6)
+    sd['time_mlp_in.projector.weight'] = 2 * torch.eye(cfg.proj_width)
+    _, _, _, cond2 = O.embed_suffix(sd, cfg, torch.zeros(B, 32), x_t, t)
+    assert torch.allclose(cond2, silu(silu(2 * temb)), atol=1e-6)
+    assert not torch.allclose(cond2, 2 * silu(silu(temb)), atol=1e-3)
+
+
+def test_embed_prefix_language_scale_and_image_rows():
+    """pi0_flowmatching.py:204-250: language rows are embed_tokens[ids] *
+    sqrt(width) (table row i filled with i / 64 -> ids / 64 * sqrt(width));
+    image rows carry no such scale (projector weight 0, bias c -> exactly
+    c)."""
+    cfg = tiny(vit_hidden=64, vit_heads=4, vit_layers=1, vit_mlp=96,
+               llm_hidden=64, image_size=28, patch=14, vocab=50,
+               max_prompt_len=6, llm_layers=0, exp_layers=0)
+    sd = {k: v.float() for k, v in make_state_dict(cfg, seed=46).items()}
+    sd['llm_backbone.embed_tokens.weight'] = (
+        torch.arange(cfg.vocab, dtype=torch.float32)[:, None] / 64.0
+    ).expand(cfg.vocab, cfg.llm_hidden).contiguous()
+    c = torch.linspace(-1, 1, cfg.llm_hidden)
+    sd['projector.projector.weight'] = torch.zeros(cfg.llm_hidden,
+                                                   cfg.vit_hidden)
+    sd['projector.projector.bias'] = c
+    g = torch.Generator().manual_seed(47)
+    B = 2
+    images = torch.rand(B, 3 * cfg.n_views, 28, 28, generator=g) * 2 - 1
+    ids = torch.randint(0, cfg.vocab, (B, cfg.max_prompt_len), generator=g)
+    img_masks = torch.ones(B, cfg.n_views, dtype=torch.bool)
+    lang_masks = torch.ones(B, cfg.max_prompt_len, dtype=torch.bool)
+    embs, pad, att = O.embed_prefix(sd, cfg, images, ids, img_masks,
+                                    lang_masks)
+    n_img = cfg.n_views * cfg.num_patches
+    assert embs.shape == (B, n_img + cfg.max_prompt_len, cfg.llm_hidden)
+    assert torch.equal(embs[:, :n_img], c.expand(B, n_img, -1))
+    want = (ids.float() / 64.0 * 8.0)[..., None].expand(-1, -1, cfg.llm_hidden)
+    assert torch.allclose(embs[:, n_img:], want, atol=1e-6)   # sqrt(64) = 8
+    assert not att.any() and pad.all()

@@ -163,3 +163,65 @@ def test_fp8_chunk_matches_oracle(cuda, pi05):
         print(f'fp8 chunk max abs err {err:.3e} vs dequantized-weight oracle, '
               f'{(got - ref_bf16).abs().max().item():.3e} vs bf16-weight oracle')
         assert err <= FP8_CHUNK_ATOL
+
+
+# ---------------------------------------------------------------------------
+# batched chunks (BASELINE configs 4 and 5 at bs 8 / 32): real widths, two
+# layers per tower; the samples of a batch are independent, so the chunk is
+# compared per sample against oracle runs of the first and last sample and
+# of one sample with a padded prompt and a missing camera view.  At these
+# batch sizes the prefix GEMMs take the 256 x 256 wide kernel, the expert
+# runs tiled (M = 8 x 51 / 32 x 50) instead of skinny, and attention runs
+# 8 / 32 problems per call.
+# ---------------------------------------------------------------------------
+def _batched_inputs(cfg, batch, seed, masked):
+    inp = make_inputs(cfg, batch=batch, seed=seed)
+    inp['lang_masks'][masked, 17:] = False
+    inp['img_masks'][masked, 1] = False
+    return inp
+
+
+def _check_samples(m, sd_ref, cfg, inp, samples, atol, cuda, label):
+    got = m.predict_action(inp['images'].to(cuda),
+                           inp['lang_tokens'].to(cuda),
+                           inp['states'].to(cuda), inp['img_masks'].to(cuda),
+                           inp['lang_masks'].to(cuda),
+                           noise=inp['noise'].to(cuda)).cpu()
+    assert torch.isfinite(got).all()
+    worst = 0.0
+    for s in samples:
+        sl = {k: v[s:s + 1] for k, v in inp.items()}
+        ref = O.predict_action(sd_ref, cfg, sl['images'], sl['lang_tokens'],
+                               sl['states'], sl['img_masks'],
+                               sl['lang_masks'], sl['noise'])
+        err = (got[s:s + 1] - ref).abs().max().item()
+        print(f'{label} sample {s}: chunk max abs err {err:.3e}', flush=True)
+        worst = max(worst, err)
+    assert worst <= atol, worst
+
+
+def test_pi0_bs8_chunk_matches_oracle(cuda):
+    """C4 at bs = 8 (bf16 weights)."""
+    from fluxvla_amd.pi0_inference import PI0Inference
+    announce('pi0 chunk batch=8 (C4)')
+    cfg = tiny()
+    sd = make_state_dict(cfg, seed=0)
+    m = PI0Inference(cfg, sd, device='cuda', max_batch=8)
+    inp = _batched_inputs(cfg, 8, seed=51, masked=3)
+    _check_samples(m, sd, cfg, inp, (0, 3, 7), CHUNK_ATOL, cuda, 'C4 bs=8')
+
+
+@pytest.mark.parametrize('batch', [8, 32])
+def test_pi05_fp8_batched_chunk_matches_oracle(cuda, batch):
+    """C5 at bs = 8 and 32: fp8 e4m3 weights (default variant), checked
+    against the oracle run on the dequantized weights."""
+    from fluxvla_amd.pi0_inference import PI0Inference
+    announce(f'pi05 fp8 chunk batch={batch} (C5)')
+    cfg = tiny(pi05=True)
+    sd = make_state_dict(cfg, seed=0)
+    m = PI0Inference(cfg, sd, device='cuda', max_batch=batch,
+                     weight_dtype='fp8')
+    sdq = m.dequantized_state_dict(sd)
+    inp = _batched_inputs(cfg, batch, seed=52 + batch, masked=batch // 2)
+    _check_samples(m, sdq, cfg, inp, (0, batch // 2, batch - 1),
+                   FP8_CHUNK_ATOL, cuda, f'C5 fp8 bs={batch}')
