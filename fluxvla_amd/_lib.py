@@ -23,6 +23,9 @@ FVX_ERR_LAUNCH = -4
 FVX_ERR_ARG = -5
 FVX_ERR_WORKSPACE = -6
 
+# fvx_gemm_noalloc's static split-K scratch per GPU
+GEMM_NOALLOC_SCRATCH_BYTES = 32 << 20
+
 GEMM_PLAIN, GEMM_GEGLU, GEMM_QKV_ROPE, GEMM_EULER = 0, 1, 2, 3
 ACT_NONE, ACT_SILU, ACT_GELU_TANH = 0, 1, 2
 
@@ -97,6 +100,7 @@ SIGNATURES = {
     'fvx_last_error': (ctypes.c_char_p, []),
     'fvx_gemm_workspace_bytes': (c_i64, [ctypes.POINTER(GemmDesc)]),
     'fvx_gemm': (c_i32, [ctypes.POINTER(GemmDesc), c_vp]),
+    'fvx_gemm_noalloc': (c_i32, [ctypes.POINTER(GemmDesc), c_vp]),
     'fvx_rms_norm_residual':
     (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
     'fvx_layer_norm': (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32,

@@ -30,6 +30,8 @@
 // produced A, ss_in / ss_out) and scales the accumulator by rsqrt(mean +
 // eps) in the epilogue, so (x * r) @ W' == r * (x @ W') needs no separate
 // normalization pass (the (1 + w) Gemma scale is folded into W').
+#include <mutex>
+
 #include "capi_util.h"
 #include "common.h"
 
@@ -2129,4 +2131,84 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
   }
   TilePlan tp = plan_tile(d);
   return run_tile(d, tp.cfg, tp.splits, s);
+}
+
+// ---------------------------------------------------------------------------
+// fvx_gemm_noalloc: fvx_gemm with its split-K scratch in a file-scope device
+// array instead of a caller-passed workspace, for callers that cannot
+// allocate.  The array's name is only a host-side stand-in: its device
+// address (one copy per GPU) comes from hipGetSymbolAddress, taken once per
+// device with that device current, and only that address is handed to
+// kernels.  The first kCounterBytes hold the split-K arrival counters, which
+// must start at zero: a fill kernel clears them at set-up and every call
+// leaves them zero again.  Calls that overlap on one GPU share the array and
+// race.
+// ---------------------------------------------------------------------------
+namespace fvx {
+
+constexpr int64_t kScratchBytes = FVX_GEMM_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ void scratch_clear_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kScratchMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchMaxDevices];  // device address per GPU
+
+// Device address of `scratch` on the stream's device (set up on first use).
+static int scratch_for_stream(hipStream_t s, void** out) {
+  int dev = -1, cur = -1;
+  hipError_t e = hipStreamGetDevice(s, &dev);
+  if (e == hipSuccess) e = hipGetDevice(&cur);
+  if (e != hipSuccess)
+    return set_error(FVX_ERR_LAUNCH, "gemm_noalloc: device query failed: %s",
+                     hipGetErrorString(e));
+  FVX_REQUIRE(dev >= 0 && dev < kScratchMaxDevices, FVX_ERR_ARG,
+              "gemm_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+      return set_error(FVX_ERR_LAUNCH, "gemm_noalloc: hipSetDevice(%d) failed: %s", dev,
+                       hipGetErrorString(e));
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return set_error(FVX_ERR_LAUNCH, "gemm_noalloc: hipGetSymbolAddress failed: %s",
+                       hipGetErrorString(e));
+    const int words = kCounterBytes / 4;
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3((words + 255) / 256), dim3(256), 0, s,
+                       (uint32_t*)p, words);
+    const int st = launch_status("gemm_noalloc(clear)");
+    if (st) return st;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FVX_OK;
+}
+
+}  // namespace fvx
+
+extern "C" int fvx_gemm_noalloc(const fvx_gemm_desc* dp, void* stream) {
+  clear_error();
+  FVX_REQUIRE(dp, FVX_ERR_NULL, "gemm_noalloc: descriptor is NULL");
+  fvx_gemm_desc d = *dp;
+  d.workspace = nullptr;
+  d.workspace_bytes = 0;
+  const int64_t need = fvx_gemm_workspace_bytes(&d);
+  if (need > kScratchBytes)
+    return set_error(FVX_ERR_WORKSPACE,
+                     "gemm_noalloc: m=%lld n=%lld k=%lld needs %lld bytes of split-K "
+                     "scratch; the static scratch holds %lld",
+                     (long long)d.m, (long long)d.n, (long long)d.k, (long long)need,
+                     (long long)kScratchBytes);
+  void* ws = nullptr;
+  const int st = scratch_for_stream((hipStream_t)stream, &ws);
+  if (st) return st;
+  d.workspace = ws;
+  d.workspace_bytes = kScratchBytes;
+  return fvx_gemm(&d, stream);
 }

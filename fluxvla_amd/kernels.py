@@ -306,6 +306,11 @@ def _gemm_desc(a, w):
     return d
 
 
+def fvx_workspace_bytes(d):
+    """Split-K workspace bytes fvx_gemm would use for descriptor ``d``."""
+    return _lib.load().fvx_gemm_workspace_bytes(ctypes.byref(d))
+
+
 def _lead_shape(a):
     return (a.m,) if isinstance(a, FragA) else tuple(a.shape[:-1])
 
@@ -322,8 +327,13 @@ def _set_c_frag(d, c_frag):
         d.c_frag = c_frag.buf.data_ptr()
 
 
-def _run_gemm(d):
-    _lib.call('fvx_gemm', ctypes.byref(d), _stream())
+def _run_gemm(d, noalloc=False):
+    if noalloc:
+        # library-owned static scratch instead of the caller's workspace
+        d.workspace, d.workspace_bytes = None, 0
+        _lib.call('fvx_gemm_noalloc', ctypes.byref(d), _stream())
+    else:
+        _lib.call('fvx_gemm', ctypes.byref(d), _stream())
 
 
 def ss_parts(n):
@@ -375,11 +385,14 @@ def _set_ss(d, rownorm_eps, ss_in=None, ss_out=None):
 def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
          gate=None, gate_group=1, pos=None, pos_period=0, act=_lib.ACT_NONE,
          rownorm_eps=None, out_f32=False, row_group=0, row_group_stride=0,
-         split_k=0, c_frag=None, ss_in=None, ss_out=None, a8=None, a8_out=None):
+         split_k=0, c_frag=None, ss_in=None, ss_out=None, a8=None, a8_out=None,
+         noalloc=False):
     """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order.
     ``a`` may be a FragA and ``weight`` a FragB; ``c_frag`` (a FragA with
     k == n) also receives the output in the fragment-major layout;
-    ``ss_in`` / ``ss_out``: see _set_ss; ``a8`` / ``a8_out``: see Fp8Act."""
+    ``ss_in`` / ``ss_out``: see _set_ss; ``a8`` / ``a8_out``: see Fp8Act.
+    ``noalloc``: run through fvx_gemm_noalloc (split-K scratch in the
+    library's static device array, no workspace)."""
     d = _gemm_desc(a, weight)
     if out is None:
         out = torch.empty(*_lead_shape(a), d.n,
@@ -413,7 +426,7 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
     d.row_group, d.row_group_stride = row_group, row_group_stride
     d.split_k = split_k
     _set_c_frag(d, c_frag)
-    _run_gemm(d)
+    _run_gemm(d, noalloc)
     return out
 
 

@@ -174,6 +174,24 @@ int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d);
 int fvx_gemm(const fvx_gemm_desc* d, void* stream);
 
 /*
+ * fvx_gemm without a caller-passed workspace: the split-K scratch (arrival
+ * counters + fp32 partials) lives in a library-owned static device array of
+ * FVX_GEMM_NOALLOC_SCRATCH_BYTES per GPU, set up on the first call on a
+ * device (its address fetched once, its counters cleared by a small kernel
+ * on `stream`).  d->workspace and d->workspace_bytes are ignored.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Nothing here allocates or frees.
+ * Limit: a problem whose fvx_gemm_workspace_bytes() exceeds the scratch
+ * returns FVX_ERR_WORKSPACE without launching.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams or
+ * threads) race; calls on one stream do not.  The stream's device must be
+ * reachable with hipSetDevice from the calling thread.
+ */
+#define FVX_GEMM_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int fvx_gemm_noalloc(const fvx_gemm_desc* d, void* stream);
+
+/*
  * Fused residual-add + RMSNorm.  Replaces GemmaRMSNorm.forward followed by
  * the residual add (fluxvla/models/backbones/llms/condition_gemma.py:75-116,
  * :319-337) and the weight-less rms_norm_kernel
