@@ -68,6 +68,7 @@ class GemmDesc(ctypes.Structure):
         ('ss_out', c_vp), ('ss_in', c_vp), ('ss_ld', c_i64), ('ss_parts', c_i32),
         ('a8_out', c_vp), ('a8_out_scale', c_vp), ('a8_out_ld', c_i64), ('a8_out_sld', c_i64),
         ('a8', c_vp), ('a8_scale', c_vp), ('a8_ld', c_i64), ('a8_sld', c_i64),
+        ('fp8_act', c_i32),
     ]
 
 

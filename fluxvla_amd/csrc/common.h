@@ -152,6 +152,19 @@ __device__ __forceinline__ i32x8_t quant_fp8x32(const bf16x8* v, int* e8) {
   return q;
 }
 
+// Eight e4m3 bytes (k order, `lo` holds the first four) -> eight bf16
+// (v_cvt_scalef32_pk_bf16_fp8 with scale 1, two values per instruction).
+// Exact: every e4m3 value, subnormals included, is a bf16 value (3 mantissa
+// bits within bf16's 7, exponents 2^-9 .. 2^8 within its range).
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
+  bf16x8 r;
+  r.w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.f, false));
+  r.w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.f, true));
+  r.w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.f, false));
+  r.w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.f, true));
+  return r;
+}
+
 // D(16x16) += A(16x128) * B(128x16), e4m3 inputs with E8M0 block scales:
 // lane l holds 32 k-values of A row (l % 16) and of B column (l % 16) (the
 // same k positions in A and B), scaled by 2^(sa - 127) and 2^(sb - 127).

@@ -498,10 +498,13 @@ struct TileCfg {
   static_assert(NT >= BM, "row sums");
 };
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8>
+// F8 && A16 (W8A16): the F8 LDS layout (128-k slabs, e4m3 weight rows), but
+// A stays bf16 and each 8 weight bytes become one bf16 MFMA fragment.
+template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8, bool A16>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     GemmArgs p, int m_tiles, int n_tiles, int splits, int64_t kchunk,
     int vec_ok) {
+  static_assert(!A16 || F8, "W8A16 is an fp8-weight variant");
   typedef TileCfg<BM, BN, WGM, WGN, STAGES, MODE, F8> C;
   constexpr int NB = C::NB, WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
   constexpr int LPW = C::LPW, WNO = C::WNO, ELD = C::ELD, BK = C::BK;
@@ -619,33 +622,54 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
       for (int ks = 0; ks < 2; ++ks) {
         i32x8_t aq[FM], bq[FN];
         int ae[FM];
+        bf16x8 av[FM][4], bw[FN][4];
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
           const char* row = s + (ks * BM + wm * WM + 32 * i + fr) * 128;
-          bf16x8 av[4];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) av[c] = *(const bf16x8*)(row + (((4 * hk + c) ^ sw) * 16));
+          for (int c = 0; c < 4; ++c)
+            av[i][c] = *(const bf16x8*)(row + (((4 * hk + c) ^ sw) * 16));
           if (SS)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
-          aq[i] = quant_fp8x32<32, 0>(av, &ae[i]);  // (row, 64-k step) scale
+            for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[i][c]);
+          if (!A16) aq[i] = quant_fp8x32<32, 0>(av[i], &ae[i]);  // (row, 64-k step) scale
         }
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const char* row = s + (brow(j) + fr) * 128;
           const bf16x8 b0 = *(const bf16x8*)(row + (((4 * ks + 2 * hk) ^ sw) * 16));
           const bf16x8 b1 = *(const bf16x8*)(row + (((4 * ks + 2 * hk + 1) ^ sw) * 16));
+          if (A16) {
+            // k = 64 ks + 32 hk + 8 c + j: bytes 8c .. of b0 (c < 2), b1
+            bw[j][0] = e4m3x8_to_bf16(b0.w[0], b0.w[1]);
+            bw[j][1] = e4m3x8_to_bf16(b0.w[2], b0.w[3]);
+            bw[j][2] = e4m3x8_to_bf16(b1.w[0], b1.w[1]);
+            bw[j][3] = e4m3x8_to_bf16(b1.w[2], b1.w[3]);
+          } else {
 #pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            bq[j][x] = (int)b0.w[x];
-            bq[j][4 + x] = (int)b1.w[x];
+            for (int x = 0; x < 4; ++x) {
+              bq[j][x] = (int)b0.w[x];
+              bq[j][4 + x] = (int)b1.w[x];
+            }
           }
         }
+        if (A16) {
+          // lane (fr, hk) holds A row / B column fr at k = 64 ks + 32 hk +
+          // 8 c + j: MFMA c sums those 16 k (hk = 0, 1) of the 64
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+          for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = mfma32x32x64_f8(aq[i], ae[i], bq[j], 127, acc[i][j]);
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+              for (int j = 0; j < FN; ++j)
+                acc[i][j] = mfma32x32x16(av[i][c], bw[j][c], acc[i][j]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = mfma32x32x64_f8(aq[i], ae[i], bq[j], 127, acc[i][j]);
+        }
         issue_group(ks, 2, tn, tst);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1073,10 +1097,14 @@ struct Gw8Layout {
   static constexpr int STAGE = A + B + E;
 };
 
-template <int MODE, bool SUM_A, bool F8A>
+// A16 (W8A16): A stays bf16 (no quantization, F8A off) and each 8 weight
+// bytes become one bf16 fragment of v_mfma_f32_32x32x16_bf16: per slab and
+// wave 64 bf16 MFMAs, as in gemm_wide_kernel, on half its B bytes.
+template <int MODE, bool SUM_A, bool F8A, bool A16>
 __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_tiles,
                                                               int n_tiles, int vec_ok,
                                                               int splits, int kchunk) {
+  static_assert(!(A16 && F8A), "W8A16 reads a bf16 A");
   typedef Gw8Layout<F8A> LY;
   constexpr bool GG = MODE == FVX_GEMM_GEGLU;
   constexpr int WNO = GG ? 64 : 128;  // output columns per wave
@@ -1173,15 +1201,23 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
     const char* sb = sa + kGw8AStage;
     const unsigned char* se = (const unsigned char*)(sb + LY::B);
     i32x8_t bq[4];
+    bf16x8 bw[4][4];  // A16: [j][c], k = 32 hk + 8 c + 0..7
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const char* row = sb + (brow(j) + fr) * 64;
       const bf16x8 b0 = *(const bf16x8*)(row + (((2 * hk) ^ swb) * 16));
       const bf16x8 b1 = *(const bf16x8*)(row + (((2 * hk + 1) ^ swb) * 16));
+      if (A16) {
+        bw[j][0] = e4m3x8_to_bf16(b0.w[0], b0.w[1]);
+        bw[j][1] = e4m3x8_to_bf16(b0.w[2], b0.w[3]);
+        bw[j][2] = e4m3x8_to_bf16(b1.w[0], b1.w[1]);
+        bw[j][3] = e4m3x8_to_bf16(b1.w[2], b1.w[3]);
+      } else {
 #pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        bq[j][x] = (int)b0.w[x];
-        bq[j][4 + x] = (int)b1.w[x];
+        for (int x = 0; x < 4; ++x) {
+          bq[j][x] = (int)b0.w[x];
+          bq[j][4 + x] = (int)b1.w[x];
+        }
       }
     }
 #pragma unroll
@@ -1207,10 +1243,19 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
         if (SUM_A)
 #pragma unroll
           for (int c = 0; c < 4; ++c) ss[i] += sumsq8(av[c]);
-        aq = quant_fp8x32<32, 0>(av, &ae);
-      }
+        if (A16) {
+          // MFMA c sums k = 32 hk + 8 c + 0..7 (hk = 0, 1) of the slab
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x64_f8(aq, ae, bq[j], 127, acc[i][j]);
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(av[c], bw[j][c], acc[i][j]);
+        } else {
+          aq = quant_fp8x32<32, 0>(av, &ae);
+        }
+      }
+      if (!A16)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x64_f8(aq, ae, bq[j], 127, acc[i][j]);
       issue_q(tn, tst, i);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1352,10 +1397,20 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
 // dirty in a non-coherent L2, which is what a release/acquire pair would
 // have to write back and invalidate (tens of microseconds per GEMM here).
 constexpr int kSkWaves = 8;
-// fp8: 4 waves, each with the full 512-register file (its A quantization
-// does not fit 256 registers with two sets of loads in flight)
-constexpr int sk_waves(bool f8) { return f8 ? 4 : kSkWaves; }
+// W8A8 (fp8 weights, A quantized here): 4 waves, each with the full
+// 512-register file (its A quantization does not fit 256 registers with two
+// sets of loads in flight); bf16 and W8A16 (fp8 weights converted to bf16
+// in registers, A bf16): 8
+constexpr int sk_waves(bool f8, bool a16) { return f8 && !a16 ? 4 : kSkWaves; }
 constexpr int kSkStep = 3;    // MFMA steps (of 32 k) per register set (GEGLU: 2)
+// steps per register set: W8A8 one 128-k fp8 block; W8A16 one 16-byte half
+// of a lane's 32 weight bytes (2 steps; 4 spilled in the PLAIN kernel)
+constexpr int sk_steps(int nb, bool f8, bool a16) {
+  return f8 ? (a16 ? 2 : 4) : (nb == 2 ? 2 : kSkStep);
+}
+// K granule of one wave's slice (a multiple of the register-set steps that
+// the weight layout needs: W8A8 a 128-k block, W8A16 a 64-k half)
+constexpr int sk_kgran(bool f8, bool a16) { return f8 ? (a16 ? 64 : 128) : 32; }
 constexpr int kSkMaxSplits = 4;
 
 __host__ __device__ constexpr int skinny_block_floats(int nb) {
@@ -1389,14 +1444,17 @@ __device__ __forceinline__ void sc1_load8(__amdgpu_buffer_rsrc_t r, int off,
   }
 }
 
-template <int MODE, bool F8>
-__global__ __launch_bounds__(64 * sk_waves(F8)) void gemm_skinny_kernel(GemmArgs p,
+template <int MODE, bool F8, bool A16>
+__global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
                                                           int64_t kc,
                                                           int vec_ok) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
-  // F8: one register set = one 128-k step of the fp8 MFMA (4 A blocks of 32)
-  constexpr int W = sk_waves(F8), S = F8 ? 4 : (NB == 2 ? 2 : kSkStep);
+  // W8A8: one register set = one 128-k step of the fp8 MFMA (4 A blocks of
+  // 32); W8A16: S 32-k steps of bf16 MFMAs whose B fragments are converted
+  // from 8 e4m3 bytes each (a 16-byte load holds two steps)
+  static_assert(!A16 || F8, "W8A16 is an fp8-weight variant");
+  constexpr int W = sk_waves(F8, A16), S = sk_steps(NB, F8, A16);
   __shared__ float sP[W][NB][64][16 + 1];
   __shared__ float sS[W][64];
   __shared__ int s_last;
@@ -1460,7 +1518,13 @@ __global__ __launch_bounds__(64 * sk_waves(F8)) void gemm_skinny_kernel(GemmArgs
       for (int b = 0; b < NB; ++b) {
         if (!F8)
           rb[set][t][b] = bld(rb_rs[b], (kin && bval) ? b0 + ks * b_ks : kOOB);
-        else if (t < 2)  // the step's 32 fp8 bytes: two 16-byte halves
+        else if (A16) {
+          // steps ks, ks + 1 (ks even): half (ks / 2) % 2 of the lane's 32
+          // bytes in 128-k block ks / 4
+          if (t % 2 == 0)
+            rb[set][t / 2][b] =
+                bld(rb_rs[b], kin ? b0 + (ks >> 2) * 2048u + ((ks >> 1) & 1u) * 16u : kOOB);
+        } else if (t < 2)  // the step's 32 fp8 bytes: two 16-byte halves
           rb[set][t][b] = bld(rb_rs[b], kin ? b0 + (ks0 + t0) * b_ks + 16 * t : kOOB);
       }
 #pragma unroll
@@ -1477,6 +1541,28 @@ __global__ __launch_bounds__(64 * sk_waves(F8)) void gemm_skinny_kernel(GemmArgs
     for (int f = 0; f < 4; ++f) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float ss[4] = {0.f, 0.f, 0.f, 0.f};
   auto compute = [&](int set) {
+    if (A16) {
+      // lane (fr, g) holds weight bytes k = 32 t + 8 g + j of column n0 + fr
+      // (the k positions of its A fragments): bf16 MFMAs on the converted
+      // weights
+#pragma unroll
+      for (int t = 0; t < S; ++t) {
+        bf16x8 bw[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const bf16x8& raw = rb[set][t / 2][b];
+          bw[b] = (t % 2 == 0) ? e4m3x8_to_bf16(raw.w[0], raw.w[1])
+                               : e4m3x8_to_bf16(raw.w[2], raw.w[3]);
+        }
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          if (p.rownorm) ss[f] += sumsq8(ra[set][t][f]);
+#pragma unroll
+          for (int b = 0; b < NB; ++b) acc[b][f] = mfma16x16x32(ra[set][t][f], bw[b], acc[b][f]);
+        }
+      }
+      return;
+    }
     if (F8) {
       // lane (fr, g) holds k = 32 t + 8 g + j of row 16 f + fr: quantize the
       // row's 128 values of the step with one power-of-two scale, one fp8
@@ -1733,7 +1819,8 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
   SkinnyPlan s;
   const int nb = d.mode == FVX_GEMM_GEGLU ? 2 : 1;
   s.n_tiles = (int)((d.n + 15) / 16);
-  const int64_t unit = (d.b_fp8 ? 128 : 32) * sk_waves(d.b_fp8);
+  const bool f8 = d.b_fp8 != 0, a16 = f8 && !d.fp8_act;
+  const int64_t unit = (int64_t)sk_kgran(f8, a16) * sk_waves(f8, a16);
   const int64_t max_splits = (d.k + unit - 1) / unit;
   int64_t sp = d.split_k;
   if (sp <= 0) {
@@ -1835,6 +1922,8 @@ static int validate(const GemmArgs& d) {
       FVX_REQUIRE(d.xt, FVX_ERR_NULL, "gemm(euler): xt required");
       break;
   }
+  FVX_REQUIRE(d.fp8_act == 0 || (d.fp8_act == 1 && d.b_fp8), FVX_ERR_ARG,
+              "gemm: fp8_act must be 0, or 1 with b_fp8 (got %d)", d.fp8_act);
   if (d.b_fp8) {
     FVX_REQUIRE(d.b_scale && (d.mode != FVX_GEMM_GEGLU || d.b2_scale), FVX_ERR_NULL,
                 "gemm(fp8): b_scale (and b2_scale for GEGLU) required");
@@ -2023,15 +2112,21 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     // the e4m3 copy of A is used when given (a rownorm then needs ss_in)
     const bool f8a = d.a8 && d.a8_scale && (!d.rownorm || d.ss_in);
 #define LW8(MODE)                                                                           \
-  if (d.rownorm && !d.ss_in)                                                                \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true, false>), dim3(nbs), dim3(256), 0, s, \
-                       d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);                   \
+  if (!d.fp8_act && d.rownorm && !d.ss_in)                                                  \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true, false, true>), dim3(nbs), dim3(256), \
+                       0, s, d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);             \
+  else if (!d.fp8_act)                                                                      \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, false, true>), dim3(nbs), dim3(256),\
+                       0, s, d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);             \
+  else if (d.rownorm && !d.ss_in)                                                           \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, true, false, false>), dim3(nbs), dim3(256),\
+                       0, s, d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);             \
   else if (f8a)                                                                             \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, true>), dim3(nbs), dim3(256), 0, s, \
-                       d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);                   \
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, true, false>), dim3(nbs), dim3(256),\
+                       0, s, d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk);             \
   else                                                                                      \
-    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, false>), dim3(nbs), dim3(256), 0,  \
-                       s, d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk)
+    hipLaunchKernelGGL((gemm_wide_f8_kernel<MODE, false, false, false>), dim3(nbs),         \
+                       dim3(256), 0, s, d, m_tiles, n_tiles, vec_ok, splits, (int)kchunk)
     if (d.b_fp8) {
       switch (d.mode) {
         case FVX_GEMM_GEGLU: LW8(FVX_GEMM_GEGLU); break;
@@ -2051,24 +2146,29 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     if (stw || splits == 1) return stw;
   } else {
     dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
-#define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_)                                      \
-    hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_>), grid,\
-                       dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits,     \
+#define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_)                                 \
+    hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_>),  \
+                       grid, dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits, \
                        kchunk, vec_ok)
     // fp8 tiles hold 128-k slabs (bf16 A rows of 256 bytes): config 1 becomes
     // 128 x 256 to stay within the LDS
+#define LCFG8(MODE, A16_)                                                             \
+      if (cfg == 1) LT(128, 256, 2, 4, 2, MODE, true, A16_);                          \
+      else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, true, A16_);                      \
+      else LT(64, 128, 2, 2, 2, MODE, true, A16_);
 #define LCFG(MODE)                                                                    \
-    if (d.b_fp8) {                                                                    \
-      if (cfg == 1) LT(128, 256, 2, 4, 2, MODE, true);                                \
-      else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, true);                            \
-      else LT(64, 128, 2, 2, 2, MODE, true);                                          \
+    if (d.b_fp8 && d.fp8_act) {                                                       \
+      LCFG8(MODE, false)                                                              \
+    } else if (d.b_fp8) {                                                             \
+      LCFG8(MODE, true)                                                               \
     } else {                                                                          \
-      if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false);                               \
-      else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false);                           \
-      else LT(64, 128, 2, 2, 3, MODE, false);                                         \
+      if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false, false);                        \
+      else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false, false);                    \
+      else LT(64, 128, 2, 2, 3, MODE, false, false);                                  \
     }
     FVX_MODE_DISPATCH(d.mode, LCFG)
 #undef LCFG
+#undef LCFG8
 #undef LT
     int st3 = launch_status("gemm(tile)");
     if (st3 || splits == 1) return st3;
@@ -2119,11 +2219,14 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
     dim3 grid((unsigned)sp.n_tiles, (unsigned)sp.splits);
     const int vec_ok = epi_vec_ok(d) ? 1 : 0;
 #define L(MODE)                                                                 \
-  if (d.b_fp8)                                                                   \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true>), grid, dim3(64 * sk_waves(true)), \
-                       0, s, d, sp.splits, sp.kc, vec_ok);                       \
+  if (d.b_fp8 && d.fp8_act)                                                      \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, false>), grid,            \
+                       dim3(64 * sk_waves(true, false)), 0, s, d, sp.splits, sp.kc, vec_ok); \
+  else if (d.b_fp8)                                                              \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true>), grid,             \
+                       dim3(64 * sk_waves(true, true)), 0, s, d, sp.splits, sp.kc, vec_ok); \
   else                                                                           \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false>), grid, dim3(64 * kSkWaves), \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false>), grid, dim3(64 * kSkWaves), \
                        0, s, d, sp.splits, sp.kc, vec_ok)
     FVX_MODE_DISPATCH(d.mode, L)
 #undef L

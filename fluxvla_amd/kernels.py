@@ -171,24 +171,35 @@ class FragB:
         return FragB(buf, n, k)
 
 
+FP8_ACTS = ('bf16', 'e4m3')
+
+
 class Fp8Weight:
     """An nn.Linear weight [n, k] quantized to OCP e4m3fn (max 448) with one
     fp32 scale per output channel: W[j] ~= scale[j] * e4m3(data[j]),
     scale[j] = max_i |W[j, i]| / 448.  ``data`` is uint8, row-major
     ([n, k], ldb = k bytes) or, with ``frag``, in the fp8 fragment-major
     layout of fvx_gemm_desc (one 16 x 128 MFMA operand per 2 KiB; needs
-    n % 16 == 0 and k % 128 == 0) for the M <= 64 skinny GEMM."""
+    n % 16 == 0 and k % 128 == 0) for the M <= 64 skinny GEMM.
 
-    def __init__(self, data, scale, n, k, frag=False):
+    ``act`` selects the GEMM arithmetic (fvx_gemm_desc.fp8_act): 'bf16'
+    (W8A16, the default: the e4m3 bytes become bf16 in registers, bf16
+    MFMA, fp32 accumulation, i.e. exactly a @ dequantize()^T) or 'e4m3'
+    (W8A8: the activations are quantized to e4m3 per row and k step)."""
+
+    def __init__(self, data, scale, n, k, frag=False, act='bf16'):
+        if act not in FP8_ACTS:
+            raise ValueError(f'act must be one of {FP8_ACTS}, got {act!r}')
         self.data, self.scale, self.n, self.k, self.frag = data, scale, n, k, frag
+        self.act = act
 
     @staticmethod
-    def quantize(w):
+    def quantize(w, act='bf16'):
         n, k = w.shape
         wf = w.float()
         s = (wf.abs().amax(1) / 448.0).clamp_min(torch.finfo(torch.float32).tiny)
         q = (wf / s[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
-        return Fp8Weight(q.contiguous(), s.contiguous(), n, k)
+        return Fp8Weight(q.contiguous(), s.contiguous(), n, k, act=act)
 
     def dequantize(self):
         """fp32 [n, k] (row-major weights only)."""
@@ -203,7 +214,7 @@ class Fp8Weight:
             raise ValueError('rows() needs the row-major layout')
         end = self.n if end is None else end
         return Fp8Weight(self.data[start:end], self.scale[start:end],
-                         end - start, self.k)
+                         end - start, self.k, act=self.act)
 
     def pack_frag(self):
         """Fragment-major copy: byte (n, k) of block (n/16, k/128) at lane
@@ -214,7 +225,7 @@ class Fp8Weight:
                              f'and k % 128 == 0, got {(n, k)}')
         buf = (self.data.view(n // 16, 16, k // 128, 4, 4, 8)
                .permute(0, 2, 4, 1, 3, 5).contiguous().view(-1))
-        return Fp8Weight(buf, self.scale, n, k, frag=True)
+        return Fp8Weight(buf, self.scale, n, k, frag=True, act=self.act)
 
 
 class Fp8Act:
@@ -289,6 +300,7 @@ def _gemm_desc(a, w):
         ldb = w.k if w.frag else w.data.stride(0)
         d.b, d.b_frag, d.b_fp8 = w.data.data_ptr(), int(w.frag), 1
         d.b_scale = w.scale.data_ptr()
+        d.fp8_act = int(w.act == 'e4m3')
     else:
         _check(w, 'weight', contiguous=False)
         n, ldb = _rows_ld(w, 'weight')
@@ -436,6 +448,7 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
     d = _gemm_desc(a, gate_w)
     if isinstance(gate_w, Fp8Weight):
         if (not isinstance(up_w, Fp8Weight) or up_w.frag != gate_w.frag or
+                up_w.act != gate_w.act or
                 (up_w.n, up_w.k) != (gate_w.n, gate_w.k) or
                 (not up_w.frag and up_w.data.stride() != gate_w.data.stride())):
             raise ValueError('up_w must be an Fp8Weight laid out like gate_w')

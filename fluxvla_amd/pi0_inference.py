@@ -131,16 +131,21 @@ def prepare_gemma(sd, cfg: PI0Config, role, device):
 LINEARS = ('qkv_w', 'o_w', 'gate_w', 'up_w', 'down_w')
 
 
-def quantize_linears(w):
+WEIGHT_DTYPES = ('bf16', 'fp8', 'fp8_w8a8')
+
+
+def quantize_linears(w, act='bf16'):
     """fp8 variant (PI0.5 config 5): every linear layer of a Gemma tower
     (Q|K|V, O, gate, up, down) as OCP e4m3fn with one fp32 scale per output
     channel, s = max|W[j]| / 448, taken after the (1 + w) fold and the Q/K
     interleave, so the quantized weight is exactly the one the GEMM applies.
-    The reference has no fp8 path; the activations stay bf16 and the GEMM
-    kernels quantize them per row and k step on the fly."""
+    The reference has no fp8 path.  ``act='bf16'`` (W8A16, config 5 as
+    stated: bf16 activations, fp32 accumulate): the kernels convert the
+    e4m3 bytes to bf16 in registers; ``act='e4m3'`` (W8A8, opt-in): they
+    quantize the activations per row and k step on the fly."""
     for L in w['layers']:
         for nm in LINEARS:
-            L[nm] = K.Fp8Weight.quantize(L[nm])
+            L[nm] = K.Fp8Weight.quantize(L[nm], act=act)
     return w
 
 
@@ -244,9 +249,12 @@ class PI0Inference:
 
     def __init__(self, cfg: PI0Config, state_dict, device='cuda',
                  max_batch=1, use_graph=True, weight_dtype='bf16'):
-        if weight_dtype not in ('bf16', 'fp8'):
-            raise ValueError(f"weight_dtype must be 'bf16' or 'fp8', got "
-                             f'{weight_dtype!r}')
+        """``weight_dtype``: 'bf16'; 'fp8' (e4m3 Gemma linears, bf16
+        activations: W8A16); 'fp8_w8a8' (e4m3 linears and e4m3 activations,
+        quantized per row and k step in the GEMMs)."""
+        if weight_dtype not in WEIGHT_DTYPES:
+            raise ValueError(f'weight_dtype must be one of {WEIGHT_DTYPES}, '
+                             f'got {weight_dtype!r}')
         self.cfg = cfg
         self.device = torch.device(device)
         self.use_graph = use_graph
@@ -265,9 +273,10 @@ class PI0Inference:
         self.vis = prepare_siglip(sd, cfg, dev)
         self.llm = prepare_gemma(sd, cfg, 'llm', dev)
         self.exp = prepare_gemma(sd, cfg, 'expert', dev)
-        if self.weight_dtype == 'fp8':
-            quantize_linears(self.llm)
-            quantize_linears(self.exp)
+        if self.fp8:
+            act = 'e4m3' if self.weight_dtype == 'fp8_w8a8' else 'bf16'
+            quantize_linears(self.llm, act)
+            quantize_linears(self.exp, act)
         self.proj = prepare_projector(sd, 'projector', dev)
         self.act_in = prepare_projector(sd, 'action_in_proj', dev)
         out = prepare_projector(sd, 'action_out_proj', dev)
@@ -329,6 +338,10 @@ class PI0Inference:
             self.mlp_in_a_f = F(self.mlp_in_a)
             self.mlp_out_f = F(self.mlp_out['w'])
 
+    @property
+    def fp8(self):
+        return self.weight_dtype in ('fp8', 'fp8_w8a8')
+
     def dequantized_state_dict(self, sd):
         """fp8 models: the state dict whose fp32 forward is the model the
         fp8 pipeline runs -- every quantized linear replaced by its
@@ -336,7 +349,7 @@ class PI0Inference:
         with the preparation's (1 + w) fold and Q/K interleave undone, so a
         reference implementation's own norms and RoPE apply to it unchanged.
         Tensors are fp32 on the CPU; the other entries are those of ``sd``."""
-        if self.weight_dtype != 'fp8':
+        if not self.fp8:
             raise ValueError('dequantized_state_dict needs an fp8 model')
         cfg = self.cfg
         H, D = cfg.heads, cfg.head_dim
@@ -400,11 +413,11 @@ class PI0Inference:
             'pre_h': e(B * S, cfg.llm_mlp),
             # row sums of squares of x handed between prefix GEMMs
             'pre_ss': e(2, K.ss_parts(cfg.llm_hidden), B * S, dt=torch.float32),
-            # e4m3 copies of x and of the gate/up output (fp8 weights)
+            # e4m3 copies of x and of the gate/up output (W8A8 weights)
             'pre_a8x': (K.Fp8Act.empty(B * S, cfg.llm_hidden, dev)
-                        if self.weight_dtype == 'fp8' else None),
+                        if self.weight_dtype == 'fp8_w8a8' else None),
             'pre_a8h': (K.Fp8Act.empty(B * S, cfg.llm_mlp, dev)
-                        if self.weight_dtype == 'fp8' else None),
+                        if self.weight_dtype == 'fp8_w8a8' else None),
             # K cache [layer][batch][token][dim] (pair-interleaved dims);
             # V cache transposed [layer][batch][dim][token]
             'kc': e(cfg.exp_layers, B, T, D),
@@ -480,11 +493,11 @@ class PI0Inference:
         # row sums of squares of x handed from the residual GEMMs to the
         # next fused RMSNorm (O proj -> gate/up, down -> next QKV)
         ss = b['pre_ss'] if B * S > 64 else [None, None]
-        # fp8 weights: the residual GEMMs and gate/up also hand their outputs
-        # over as e4m3 copies, which the fp8 wide GEMMs read instead of
-        # quantizing their A (same values)
+        # W8A8 weights: the residual GEMMs and gate/up also hand their
+        # outputs over as e4m3 copies, which the fp8 wide GEMMs read instead
+        # of quantizing their A (same values)
         a8x = a8h = None
-        if self.weight_dtype == 'fp8' and B * S > 64:
+        if self.weight_dtype == 'fp8_w8a8' and B * S > 64:
             a8x, a8h = b['pre_a8x'], b['pre_a8h']
         for i, L in enumerate(W['layers']):
             kc, vc = b['kc'][i], b['vc'][i]

@@ -120,10 +120,17 @@ typedef struct fvx_gemm_desc {
   void* c_frag;
   /* fp8 weights (PI0.5 quantized variant; no counterpart in the reference,
    * which has no fp8 path): b (and b2) hold OCP e4m3fn bytes with one fp32
-   * scale per output channel, W[n][k] = b_scale[n] * e4m3(b[n][k]).  The
-   * activations stay bf16 in memory; the kernels quantize each 32-wide k
-   * block of an A row to e4m3 with its own power-of-two scale on the fly and
-   * run the block-scaled fp8 MFMA.  ldb counts bytes.  K % 128 == 0.
+   * scale per output channel, W[n][k] = b_scale[n] * e4m3(b[n][k]).
+   * ldb counts bytes.  K % 128 == 0.  The arithmetic follows fp8_act:
+   *   0 (W8A16, the default): A stays bf16; the kernels convert the e4m3
+   *     bytes to bf16 in registers (exact: every e4m3 value is a bf16
+   *     value), run the bf16 MFMA with fp32 accumulation and scale the
+   *     accumulator by b_scale[n] in the epilogue, i.e. exactly
+   *     A @ dequant(W)^T up to fp32 summation order;
+   *   1 (W8A8): each row of A is quantized to e4m3 on the fly with one
+   *     power-of-two (E8M0) scale per row and k step -- 64 wide in the
+   *     tiled and wide kernels, 128 wide in the M <= 64 kernel -- and the
+   *     block-scaled fp8 MFMA runs; a8 (below) can hand the copy over.
    *   b_frag with b_fp8: element (n, k) at byte
    *     ((n/16) * (K/128) + k/128) * 2048 + ((k%128)/8 % 4 * 16 + n%16) * 32
    *     + (k%128)/32 * 8 + k%8
@@ -154,11 +161,14 @@ typedef struct fvx_gemm_desc {
    *     smallest power of two that keeps the block's largest magnitude
    *     within 448 (the rule the fp8 GEMMs quantize A with);
    *   a8 / a8_scale (same layout, strides a8_ld / a8_sld): such a copy of
-   *     A.  The fp8-weight wide kernel then reads it instead of quantizing A
-   *     (same values, same result); every other path ignores it, and so
-   *     does a rownorm GEMM without ss_in.  a8_sld % 4 == 0. */
+   *     A.  The W8A8 fp8-weight wide kernel then reads it instead of
+   *     quantizing A (same values, same result); every other path ignores
+   *     it, and so does a rownorm GEMM without ss_in.  a8_sld % 4 == 0. */
   void* a8_out; void* a8_out_scale; int64_t a8_out_ld, a8_out_sld;
   const void* a8; const void* a8_scale; int64_t a8_ld, a8_sld;
+  /* with b_fp8: 0 = bf16 activations (W8A16), 1 = e4m3 activations (W8A8);
+   * see b_fp8 above.  a8 is read only by W8A8 GEMMs. */
+  int32_t fp8_act;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */

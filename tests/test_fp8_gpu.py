@@ -1,6 +1,13 @@
-"""fp8 (e4m3) weight GEMMs: the PI0.5 quantized-weight variant.
+"""fp8 (e4m3) weight GEMMs: the PI0.5 quantized-weight variant, in its two
+arithmetics: W8A16 (the default: bf16 activations, the e4m3 weights
+converted to bf16 in registers, bf16 MFMA, fp32 accumulation) and W8A8
+(opt-in: activations quantized to e4m3 per row and k step).
 
-The reference has no fp8 path, so the kernels are pinned two ways:
+W8A16 is pinned against float64 a @ dequant(W)^T (exact up to fp32
+summation order), and the conversion itself bit for bit: a one-hot A
+times weights holding every finite e4m3 byte returns each byte's value.
+
+The reference has no fp8 path, so the W8A8 kernels are pinned two ways:
 
 * exactly, against a float64 restatement of what they compute: the weight
   dequantized from its e4m3 bytes and per-channel scale, and the A values of
@@ -72,8 +79,8 @@ def quant_a_ref(a, skinny):
     return q * sc
 
 
-def fp8_weight(K, w, cuda, frag=False):
-    fw = K.Fp8Weight.quantize(w.to(cuda))
+def fp8_weight(K, w, cuda, frag=False, act='e4m3'):
+    fw = K.Fp8Weight.quantize(w.to(cuda), act=act)
     wq = fw.dequantize().double().cpu()
     return (fw.pack_frag() if frag else fw), wq
 
@@ -174,7 +181,7 @@ def test_fp8_weight_quantization_and_layout(K, cuda):
     placing (n, k) where fvx_gemm_desc documents it."""
     announce('fp8 weight quantization and packing')
     w = randn((64, 256), 140, std=0.03)
-    fw = K.Fp8Weight.quantize(w.to(cuda))
+    fw = K.Fp8Weight.quantize(w.to(cuda), act='e4m3')
     assert torch.allclose(fw.scale.cpu(), w.float().abs().amax(1) / 448.0)
     wd = fw.dequantize().cpu()
     assert ((wd - w.float()).abs() <= 2.0**-4 * w.float().abs() +
@@ -275,9 +282,10 @@ def test_fp8_handover_consumer_identical(K, cuda):
         ss = torch.zeros(K.ss_parts(k), m, device=cuda)
         a8 = K.Fp8Act.empty(m, k, cuda)
         K.gemm(a0, w0, out=x, ss_out=ss, a8_out=a8)      # producer
-        fw = K.Fp8Weight.quantize(randn((n, k), 182, std=0.02).to(cuda))
+        fw = K.Fp8Weight.quantize(randn((n, k), 182, std=0.02).to(cuda), act='e4m3')
         if geglu:
-            fu = K.Fp8Weight.quantize(randn((n, k), 183, std=0.02).to(cuda))
+            fu = K.Fp8Weight.quantize(randn((n, k), 183, std=0.02).to(cuda),
+                                      act='e4m3')
             got = K.gemm_geglu(x, fw, fu, rownorm_eps=1e-6, ss_in=ss, a8=a8)
             own = K.gemm_geglu(x, fw, fu, rownorm_eps=1e-6, ss_in=ss)
         else:
@@ -322,3 +330,120 @@ def test_fp8_wide_split_k_down(K, cuda):
         q, e = quant_blocks_ref(got)
         assert torch.equal(o8.data.cpu(), q)
         assert torch.equal(o8.scale.cpu()[:, :m].t(), e)
+
+
+# ---------------------------------------------------------------------------
+# W8A16 (the default fp8 arithmetic)
+# ---------------------------------------------------------------------------
+# fp32 accumulation + the bf16 output rounding (half an ulp of an element
+# up to twice the largest |ref| binade: ~2^-8 of max |ref|); an e4m3 rounding
+# of the activations (2^-4 relative) would exceed it by an order of magnitude
+W16_TOL = 5e-3
+
+
+def test_w8a16_conversion_exact(K, cuda):
+    """Weights holding every finite e4m3 byte (scale 1) times a one-hot A
+    (fp32 output): out[m, n] is exactly the e4m3 value of W[n, m], subnormals
+    and signed zeros included -- through the tiled (M = 128) and the skinny
+    fragment-major (M = 64) kernels."""
+    announce('w8a16 e4m3 -> bf16 conversion exact')
+    codes = torch.tensor([c for c in range(256) if c & 0x7F != 0x7F],
+                         dtype=torch.uint8)                       # 254 finite
+    n, k = 256, 128
+    data = torch.zeros(n, k, dtype=torch.uint8)
+    for r in range(n):
+        data[r] = codes[(torch.arange(k) + 7 * r) % len(codes)]
+    fw = K.Fp8Weight(data.to(cuda), torch.ones(n, device=cuda), n, k)
+    want = data.view(torch.float8_e4m3fn).float().t()              # [k, n]
+    a = torch.eye(k, dtype=torch.bfloat16, device=cuda)
+    out = K.gemm(a, fw, out_f32=True)
+    assert torch.equal(out.cpu(), want)
+    for r0 in (0, 64):
+        af = K.pack_frag(a[r0:r0 + 64], K.FragA.empty(k, cuda).rows(64))
+        o = K.gemm(af, fw.pack_frag(), out_f32=True)
+        assert torch.equal(o.cpu(), want[r0:r0 + 64])
+
+
+@pytest.mark.parametrize('m,n,k', [(300, 384, 512), (816, 2560, 2048),
+                                   (129, 256, 128), (408, 1024, 4096)])
+def test_w8a16_gemm_tile(K, cuda, m, n, k):
+    announce(f'w8a16 gemm tile m={m} n={n} k={k}')
+    a = randn((m, k), 200, std=1.5)
+    fw, wq = fp8_weight(K, randn((n, k), 201, std=0.02), cuda, act='bf16')
+    bias = randn((n,), 202, std=0.5)
+    res = randn((m, n), 203)
+    out = K.gemm(a.to(cuda), fw, bias=bias.to(cuda), residual=res.to(cuda))
+    ref = a.double() @ wq.t() + bias.double() + res.double()
+    assert rel_err(out, ref) <= W16_TOL
+
+
+@pytest.mark.parametrize('m,n,k', [(51, 2560, 1024), (50, 1024, 2048),
+                                   (51, 1024, 4096), (1, 256, 128),
+                                   (33, 4096, 1024)])
+def test_w8a16_gemm_skinny_frag(K, cuda, m, n, k):
+    announce(f'w8a16 gemm skinny m={m} n={n} k={k}')
+    a = randn((m, k), 210, std=1.5)
+    fw, wq = fp8_weight(K, randn((n, k), 211, std=0.02), cuda, frag=True,
+                        act='bf16')
+    af = K.pack_frag(a.to(cuda), K.FragA.empty(k, cuda).rows(m))
+    res = randn((m, n), 212)
+    out = K.gemm(af, fw, residual=res.to(cuda))
+    ref = a.double() @ wq.t() + res.double()
+    assert rel_err(out, ref) <= W16_TOL
+
+
+@pytest.mark.parametrize('m,skinny', [(51, True), (200, False), (816, False)])
+def test_w8a16_gemm_geglu_rownorm(K, cuda, m, skinny):
+    """GeGLU with the fused RMSNorm: skinny, tiled and (M = 816, N = 16384:
+    512 tiles) the wide kernel."""
+    announce(f'w8a16 gemm geglu rownorm m={m} skinny={skinny}')
+    n, k = (16384, 2048) if m == 816 else (512, 1024)
+    a = randn((m, k), 220, std=2.0)
+    gw, gq = fp8_weight(K, randn((n, k), 221, std=0.02), cuda, frag=skinny,
+                        act='bf16')
+    uw, uq = fp8_weight(K, randn((n, k), 222, std=0.02), cuda, frag=skinny,
+                        act='bf16')
+    ad = a.to(cuda)
+    if skinny:
+        ad = K.pack_frag(ad, K.FragA.empty(k, cuda).rows(m))
+    out = K.gemm_geglu(ad, gw, uw, rownorm_eps=1e-6).cpu()
+    rows = sample_rows(m) if m == 816 else torch.arange(m)
+    ar = a[rows].double()
+    r = torch.rsqrt(ar.pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = F.gelu((ar @ gq.t()) * r, approximate='tanh') * ((ar @ uq.t()) * r)
+    assert rel_err(out[rows], ref) <= W16_TOL
+
+
+def test_w8a16_wide_plain_and_qkv(K, cuda):
+    """The wide kernel on PLAIN (M = 6528, 208 tiles) with bias and
+    residual, sampled rows."""
+    announce('w8a16 wide plain m=6528 n=2048 k=2048')
+    m, n, k = 6528, 2048, 2048
+    a = randn((m, k), 230, std=1.5)
+    fw, wq = fp8_weight(K, randn((n, k), 231, std=0.02), cuda, act='bf16')
+    bias = randn((n,), 232, std=0.5)
+    res = randn((m, n), 233)
+    out = K.gemm(a.to(cuda), fw, bias=bias.to(cuda), residual=res.to(cuda))
+    rows = sample_rows(m)
+    ref = a[rows].double() @ wq.t() + bias.double() + res[rows].double()
+    assert rel_err(out.cpu()[rows], ref) <= W16_TOL
+
+
+def test_w8a16_wide_split_k_down(K, cuda):
+    """The bs=1 prefix down projection shape (M = 816, K = 16384): the wide
+    kernel over 8 K ranges with the weight-scaled partials, then the reduce
+    (residual in place, row sums of squares of the output)."""
+    announce('w8a16 wide split-K down m=816 k=16384')
+    m, n, k = 816, 2048, 16384
+    a = randn((m, k), 240)
+    fw, wq = fp8_weight(K, randn((n, k), 241, std=0.01), cuda, act='bf16')
+    res = randn((m, n), 242)
+    x = res.to(cuda)
+    ss = torch.zeros(K.ss_parts(n), m, device=cuda)
+    K.gemm(a.to(cuda), fw, out=x, residual=x, ss_out=ss)
+    rows = sample_rows(m)
+    got = x.cpu()
+    ref = a[rows].double() @ wq.t() + res[rows].double()
+    assert rel_err(got[rows], ref) <= W16_TOL
+    want = got.double().view(m, -1, 64).pow(2).sum(-1).t()
+    assert ((ss.cpu().double() - want).abs() <= 1e-5 * want + 1e-6).all()
