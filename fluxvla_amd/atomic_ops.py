@@ -4,16 +4,21 @@ matmul_bias.py:19-60): same names, argument order and meaning, each running
 the HIP kernels of libfluxvla_amd.so on the current stream and writing into
 the caller's preallocated buffers.
 
-Operand conventions (what the matching prepare hooks in pi0_inference.py
-emit; the reference's own hooks emit the transposed [in, out] layout):
-  * weights are [out_features, in_features] (nn.Linear layout, K contiguous);
-  * Q/K weight rows are pair-interleaved for RoPE (condition_gemma_inference
-    .py:46-63), and the Gemma (1 + w) norm scale is folded in;
+Operand conventions:
+  * weights mean what the reference's hooks hand its ops: a plain tensor is
+    [in_features, out_features] (``W.T``, condition_gemma_inference.py:
+    91-105; ``matmul_bias_cuda`` reads N = weight.size(1)) and is transposed
+    once on first use (weight_layout.as_nk); the ``NKWeight`` values this
+    package's hooks emit (hooks.py) already hold [out, in] and present the
+    reference's [in, out] shape; fragment-major and fp8 weights from the
+    model's own preparation pass through;
+  * Q/K weight columns are pair-interleaved for RoPE (condition_gemma_
+    inference.py:46-63), and the Gemma (1 + w) norm scale is folded in;
   * ``rope_weight`` is either the kernels' fp32 [positions, head_dim/2, 2]
     (cos, sin) table (rows = token positions 0..) or the reference's
-    interleaved bf16 [positions, head_dim] table (converted per call);
-  * patch weights are [hidden, 3*p*p padded to a multiple of 8] in
-    (channel, ky, kx) order.
+    interleaved bf16 [positions, head_dim] table (converted once, cached);
+  * patch weights are the reference's [kH, kW, C, out] (converted once) or
+    the hooks' prepared [out, 3*p*p padded to 8] in (c, ky, kx) order.
 Block-size arguments of the Triton wrappers are accepted and ignored: the
 HIP kernels choose their own tiling.  The unfused attention trio
 (matmul_abT_scale / softmax_kernel_* / matmul_attn_v) is replaced by the
@@ -24,6 +29,7 @@ import torch
 
 from . import kernels as _kern
 from ._lib import ACT_GELU_TANH, ACT_SILU
+from .weight_layout import as_nk, patch_weight_nk
 
 RMS_EPS = 1e-6
 
@@ -41,12 +47,12 @@ def conv2d_embed_res(images, patch_w, patch_b, pos_emb, out, grid_size,
     (atomic_ops.py:34-53).  images: [n_views, H, W, 3] (NHWC, as the
     reference stages them) or [n_views, 3, H, W]."""
     nhwc = images.shape[-1] == 3
-    n = images.shape[0]
-    kp = patch_w.shape[1]
+    kp = (3 * patch_size * patch_size + 7) // 8 * 8
+    w = patch_weight_nk(patch_w, kp)
     patches = _kern.im2col_patches(images, patch_size, kp, channels_last=nhwc)
-    _kern.gemm(patches, patch_w, out=_rows(out), bias=patch_b, pos=pos_emb,
-           pos_period=num_patches)
-    del n, grid_size, vit_hidden
+    _kern.gemm(patches, w, out=_rows(out), bias=patch_b, pos=pos_emb,
+               pos_period=num_patches)
+    del grid_size, vit_hidden
     return out
 
 
@@ -57,7 +63,7 @@ def layer_norm_QKV_matmul_bias(x, norm_w, norm_b, qkv_w, qkv_b, out, x_norm,
     eps follows the SigLIP config (1e-6); the reference Triton kernel's
     default is 1e-5 (norm_triton_ops.py:97)."""
     _kern.layer_norm(_rows(x), norm_w, norm_b, eps, out=_rows(x_norm))
-    _kern.gemm(_rows(x_norm), qkv_w, out=_rows(out), bias=qkv_b)
+    _kern.gemm(_rows(x_norm), as_nk(qkv_w), out=_rows(out), bias=qkv_b)
     return out
 
 
@@ -73,8 +79,9 @@ def AttnMultiKey(QKV, num_patches, vit_num_heads, vit_head_dim, vit_hidden):
 
 
 def matmul_bias_res(x, weight, bias, res, out, buf, num_patches, vit_hidden):
-    """out = x @ W^T + bias + res (atomic_ops.py:79-80)."""
-    _kern.gemm(_rows(x), weight, out=_rows(out), bias=bias, residual=_rows(res))
+    """out = x @ W + bias + res (atomic_ops.py:79-80)."""
+    _kern.gemm(_rows(x), as_nk(weight), out=_rows(out), bias=bias,
+               residual=_rows(res))
     return out
 
 
@@ -83,15 +90,16 @@ def layer_norm_matmul_bias_gelu(x, norm_w, norm_b, weight, bias, out, x_norm,
                                 eps=1e-6):
     """LayerNorm then fc1 + bias + gelu_tanh (atomic_ops.py:83-104)."""
     _kern.layer_norm(_rows(x), norm_w, norm_b, eps, out=_rows(x_norm))
-    _kern.gemm(_rows(x_norm), weight, out=_rows(out), bias=bias,
-           act=ACT_GELU_TANH)
+    _kern.gemm(_rows(x_norm), as_nk(weight), out=_rows(out), bias=bias,
+               act=ACT_GELU_TANH)
     return out
 
 
 def matmul_split_k_bias_res(x, weight, bias, res, out, buf, num_patches,
                             vit_intermediate, vit_hidden):
     """fc2 + bias + residual (atomic_ops.py:107-109)."""
-    _kern.gemm(_rows(x), weight, out=_rows(out), bias=bias, residual=_rows(res))
+    _kern.gemm(_rows(x), as_nk(weight), out=_rows(out), bias=bias,
+               residual=_rows(res))
     return out
 
 
@@ -99,23 +107,48 @@ def layer_norm_matmul_bias(x, norm_w, norm_b, proj_w, proj_b, out, x_norm,
                            num_patches, in_features, out_features, eps=1e-5):
     """LayerNorm then projection + bias (atomic_ops.py:117-149)."""
     _kern.layer_norm(_rows(x), norm_w, norm_b, eps, out=_rows(x_norm))
-    _kern.gemm(_rows(x_norm), proj_w, out=_rows(out), bias=proj_b)
+    _kern.gemm(_rows(x_norm), as_nk(proj_w), out=_rows(out), bias=proj_b)
     return out
 
 
 # ---------------------------------------------------------------------------
 # Gemma ops
 # ---------------------------------------------------------------------------
+_rope_cache = {}
+
+
+def _qrows(Q, rows):
+    """Q as [tokens, heads * head_dim]: the reference's buffers hold it as
+    [tokens * heads, head_dim] (pi05_flowmatching_inference.py:400-401),
+    the same memory."""
+    if not Q.is_contiguous():
+        raise ValueError('Q must be contiguous')
+    return Q.view(rows, -1)
+
+
 def _rope_args(rope_weight, rows, device):
+    """(fp32 [positions, hd/2, 2] table, int32 positions 0..rows-1).  A
+    reference bf16 table is converted once per (tensor, version) and the
+    position vector made once per (rows, device), so repeated calls (and
+    graph capture after a warm-up call) allocate nothing."""
     if rope_weight.dtype == torch.float32 and rope_weight.dim() == 3:
         table = rope_weight
     else:  # reference table: interleaved (cos, sin) bf16 [positions, hd]
-        table = rope_weight.float().view(rope_weight.shape[0], -1,
-                                         2).contiguous()
-    pos = torch.arange(rows, dtype=torch.int32, device=device)
+        key = ('tab', rope_weight.data_ptr(), tuple(rope_weight.shape),
+               rope_weight._version, rope_weight.device)
+        hit = _rope_cache.get(key)
+        if hit is None:  # the source stays referenced: its address is its own
+            hit = _rope_cache[key] = (rope_weight, rope_weight.float().reshape(
+                rope_weight.shape[0], -1, 2).contiguous())
+        table = hit[1]
     if table.shape[0] < rows:
         raise ValueError(f'rope table has {table.shape[0]} positions, need '
                          f'{rows}')
+    key = ('pos', rows, torch.device(device))
+    pos = _rope_cache.get(key)
+    if pos is None:
+        pos = _rope_cache[key] = torch.arange(rows, dtype=torch.int32,
+                                              device=device)
     return table, pos
 
 
@@ -128,8 +161,9 @@ def rms_matmul_qkv_rope(x, weight_qkv, rope_weight, Q, K, V, x_norm,
     normalization never leaves registers."""
     rows = _rows(x).shape[0]
     table, pos = _rope_args(rope_weight, rows, x.device)
-    _kern.gemm_qkv_rope(_rows(x), weight_qkv, table, pos, _rows(Q), _rows(K),
-                    _rows(V), num_kv_heads, head_dim, rownorm_eps=RMS_EPS)
+    _kern.gemm_qkv_rope(_rows(x), as_nk(weight_qkv), table, pos,
+                        _qrows(Q, rows), _rows(K), _rows(V), num_kv_heads,
+                        head_dim, rownorm_eps=RMS_EPS)
 
 
 def matmul_qkv_rope(x_normed, weight_qkv, rope_weight, Q, K, V, hidden_dim,
@@ -137,14 +171,15 @@ def matmul_qkv_rope(x_normed, weight_qkv, rope_weight, Q, K, V, hidden_dim,
     """QKV GEMM + RoPE without a norm (atomic_ops.py:303-311)."""
     rows = _rows(x_normed).shape[0]
     table, pos = _rope_args(rope_weight, rows, x_normed.device)
-    _kern.gemm_qkv_rope(_rows(x_normed), weight_qkv, table, pos, _rows(Q),
-                    _rows(K), _rows(V), num_kv_heads, head_dim)
+    _kern.gemm_qkv_rope(_rows(x_normed), as_nk(weight_qkv), table, pos,
+                        _qrows(Q, rows), _rows(K), _rows(V), num_kv_heads,
+                        head_dim)
 
 
 def matmul_res(x, weight, out, in_features, out_features):
-    """out += x @ W^T in place (atomic_ops.py:172-188)."""
+    """out += x @ W in place (atomic_ops.py:172-188)."""
     o = _rows(out)
-    _kern.gemm(_rows(x), weight, out=o, residual=o)
+    _kern.gemm(_rows(x), as_nk(weight), out=o, residual=o)
     return out
 
 
@@ -152,13 +187,14 @@ def rms_matmul_gate(x, gate_w, up_w, out, x_norm, hidden_dim,
                     intermediate_dim):
     """RMSNorm fused into the GeGLU dual GEMM (atomic_ops.py:196-201):
     out = gelu_tanh(n(x) @ Wg^T) * (n(x) @ Wu^T); x_norm is not written."""
-    _kern.gemm_geglu(_rows(x), gate_w, up_w, out=_rows(out), rownorm_eps=RMS_EPS)
+    _kern.gemm_geglu(_rows(x), as_nk(gate_w), as_nk(up_w), out=_rows(out),
+                     rownorm_eps=RMS_EPS)
     return out
 
 
 def matmul_gate(x, gate_w, up_w, out, in_features, intermediate_dim):
     """GeGLU dual GEMM without a norm (atomic_ops.py:373-378)."""
-    _kern.gemm_geglu(_rows(x), gate_w, up_w, out=_rows(out))
+    _kern.gemm_geglu(_rows(x), as_nk(gate_w), as_nk(up_w), out=_rows(out))
     return out
 
 
@@ -172,15 +208,16 @@ def matmul_attn_v(x, V, out, head_dim):
 
 
 def matmul_bias_silu(x, weight, bias, out, in_features, out_features):
-    """silu(x @ W^T + b) (atomic_ops.py:229-243)."""
-    _kern.gemm(_rows(x), weight, out=_rows(out), bias=bias, act=ACT_SILU)
+    """silu(x @ W + b) (atomic_ops.py:229-243)."""
+    _kern.gemm(_rows(x), as_nk(weight), out=_rows(out), bias=bias,
+               act=ACT_SILU)
     return out
 
 
 def matmul_bias_small(x, weight, bias, out, in_features, out_features,
                       BLOCK_SIZE_N=32, BLOCK_SIZE_M=32, BLOCK_SIZE_K=32):
-    """x @ W^T + b (atomic_ops.py:251-273)."""
-    _kern.gemm(_rows(x), weight, out=_rows(out), bias=bias)
+    """x @ W + b (atomic_ops.py:251-273)."""
+    _kern.gemm(_rows(x), as_nk(weight), out=_rows(out), bias=bias)
     return out
 
 
@@ -189,33 +226,33 @@ def adarms_norm_style_proj(x, time_emb, mod_w, mod_b, x_normed, gate, style,
     """style = dense(time_emb) (row 0 is the one the norm reads), then
     x_normed = rms(x) * (1 + scale) + shift and gate
     (atomic_ops.py:278-299, norm_triton_ops.py:355-395)."""
-    _kern.gemm(_rows(time_emb)[:1], mod_w, out=_rows(style)[:1], bias=mod_b)
+    _kern.gemm(_rows(time_emb)[:1], as_nk(mod_w), out=_rows(style)[:1],
+               bias=mod_b)
     _kern.adarms_norm(_rows(x), _rows(style)[:1], out=_rows(x_normed),
                   gate_out=_rows(gate), eps=RMS_EPS)
 
 
 def matmul_res_gate(x, weight, out, gate, in_features, out_features,
                     BLOCK_SIZE_N=32, BLOCK_SIZE_M=32, BLOCK_SIZE_K=128):
-    """out += (x @ W^T) * gate in place (atomic_ops.py:343-365)."""
+    """out += (x @ W) * gate in place (atomic_ops.py:343-365)."""
     o = _rows(out)
-    _kern.gemm(_rows(x), weight, out=o, residual=o, gate=_rows(gate))
+    _kern.gemm(_rows(x), as_nk(weight), out=o, residual=o, gate=_rows(gate))
     return out
 
 
 # ---------------------------------------------------------------------------
 # matmul_bias_cuda (cuBLASLt GEMM + bias (+ residual) in the reference)
 # ---------------------------------------------------------------------------
-def matmul_bias_cuda(inp, weight, bias, out=None, res=None,
-                     weight_layout='nk'):
+def matmul_bias_cuda(inp, weight, bias, out=None, res=None):
     """out = inp @ W + bias (+ res), inp 2-D or 3-D bf16 (matmul_bias.py:
-    19-60).  ``weight_layout='nk'``: weight is [N, K] (this product's prepare
-    hooks); ``'kn'``: the reference's [K, N], transposed once per call."""
+    19-60).  ``weight`` is the reference's [K, N] (a plain tensor, transposed
+    once and cached) or an ``NKWeight`` from this package's hooks."""
     orig = inp.shape
     a = inp.reshape(-1, orig[-1])
-    w = weight if weight_layout == 'nk' else weight.t().contiguous()
+    w = as_nk(weight)
     if w.shape[1] != a.shape[1]:
-        raise ValueError(f'weight {tuple(weight.shape)} does not match '
-                         f'inp {tuple(orig)} for layout {weight_layout!r}')
+        raise ValueError(f'weight of logical shape {tuple(weight.shape)} '
+                         f'([K, N]) does not match inp {tuple(orig)}')
     N = w.shape[0]
     if out is None:
         out = torch.empty(*orig[:-1], N, dtype=inp.dtype, device=inp.device)

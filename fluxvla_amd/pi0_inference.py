@@ -262,6 +262,7 @@ class PI0Inference:
         self.weight_dtype = weight_dtype
         K.workspace(self.device)
         K.workspace(self.device, 'attn')
+        self._sd = state_dict
         self.prepare_triton_inference(state_dict)
         self._graphs = {}
         self._bufs = {}
@@ -337,6 +338,37 @@ class PI0Inference:
             self.act_in_f = F(self.act_in['w'])
             self.mlp_in_a_f = F(self.mlp_in_a)
             self.mlp_out_f = F(self.mlp_out['w'])
+
+    # -- the reference's module attributes with their prepare_triton hooks
+    #    (pi05_flowmatching_inference.py:596-619): each returns the
+    #    reference-keyed dict of hooks.py for its part of the state dict
+    @property
+    def vision_backbone(self):
+        from .hooks import SigLIPViTBackboneInference
+        return SigLIPViTBackboneInference(self._sd, self.cfg, self.device)
+
+    @property
+    def llm_backbone(self):
+        from .hooks import ConditionGemmaInferenceModel
+        return ConditionGemmaInferenceModel(self._sd, self.cfg, 'llm_backbone',
+                                            self.device)
+
+    @property
+    def llm_expert(self):
+        from .hooks import ConditionGemmaInferenceModel
+        return ConditionGemmaInferenceModel(self._sd, self.cfg, 'llm_expert',
+                                            self.device)
+
+    def projector_hook(self, module):
+        """LinearProjectorInference of ``module`` ('projector',
+        'action_in_proj', 'action_out_proj', 'time_mlp_in', ...)."""
+        from .hooks import LinearProjectorInference
+        return LinearProjectorInference.from_state_dict(self._sd, module,
+                                                        self.device)
+
+    @property
+    def projector(self):
+        return self.projector_hook('projector')
 
     @property
     def fp8(self):
