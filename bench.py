@@ -322,6 +322,44 @@ def kernel_only(iters=10):
         '3 x copy 256 MiB')
 
 
+def calibration_copy(nbytes=256 << 20, reps=3):
+    """A plain device copy of known size: it fetches and writes exactly
+    ``nbytes`` per dispatch, which calibrates rocprofv3's FETCH_SIZE /
+    WRITE_SIZE counters."""
+    import torch
+    src = torch.ones(nbytes, dtype=torch.uint8, device='cuda')
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def table_only():
+    """The per-kernel table alone (bs=1 PI0 model, one chunk first so the
+    buffers hold chunk data), then the calibration copy: the program the
+    rocprofv3 kernel-trace and FETCH_SIZE / WRITE_SIZE passes run."""
+    import torch
+
+    from fluxvla_amd.config import PI0
+    from fluxvla_amd.pi0_inference import PI0Inference
+    from fluxvla_amd.weights import make_inputs, make_state_dict
+    dev = torch.device('cuda', 0)
+    sd = make_state_dict(PI0, seed=0, device=dev)
+    model = PI0Inference(PI0, sd, device=dev, max_batch=1)
+    inp = {k: v.to(dev) for k, v in make_inputs(PI0, batch=1, seed=1).items()}
+    model.predict_action(inp['images'], inp['lang_tokens'], inp['states'],
+                         inp['img_masks'], inp['lang_masks'],
+                         noise=inp['noise'])
+    torch.cuda.synchronize()
+    rows = kernel_table(model)
+    for r in rows:
+        log(f"  {r['kernel']:56s} {r['avg_us']:9.2f} us "
+            f"{r['achieved']:8.1f} {r['unit']} ({100 * r['frac']:.1f} %)")
+    calibration_copy()
+    log('table-only: done (last dispatches: 3 x copy 256 MiB)')
+    print(json.dumps({'kernels': rows}), flush=True)
+
+
 def cpu_model_name():
     """The host CPU's model string (/proc/cpuinfo), else platform's guess."""
     import platform
@@ -544,6 +582,10 @@ def main():
     ap.add_argument('--kernel-only', action='store_true',
                     help='run only the dominant kernel + a calibration copy '
                     '(for rocprofv3 --pmc passes)')
+    ap.add_argument('--table-only', action='store_true',
+                    help='run only the per-kernel table (every main kernel '
+                    'of the chunk at its chunk shape) + a calibration copy '
+                    '(for rocprofv3 --kernel-trace / --pmc passes)')
     args = ap.parse_args()
     if args.gpus != 1:
         print('bench.py: this build runs on one GPU; multi-GPU figures are '
@@ -553,6 +595,9 @@ def main():
 
     if args.kernel_only:
         kernel_only()
+        return
+    if args.table_only:
+        table_only()
         return
 
     import torch

@@ -92,6 +92,9 @@ class AttnDesc(ctypes.Structure):
         ('kv_splits', c_i32),
         ('workspace', c_vp), ('workspace_bytes', c_i64),
         ('o_frag', c_vp),
+        ('prefetch', c_vp * 8), ('prefetch_bytes', c_i64 * 8),
+        ('prefetch_tile_bytes', c_i64 * 8),
+        ('prefetch_wgs', c_i32),
     ]
 
 

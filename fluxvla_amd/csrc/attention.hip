@@ -425,18 +425,75 @@ __device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int z, int r,
   }
 }
 
+// Prefetch role of the workgroups past the attention items (prefetch
+// index pw of npw, on XCD blockIdx % 8).  Each range moves in whole 1 KiB
+// wave blocks by LDS DMA into one 1 KiB slot per wave, overwritten and
+// never read: the point is the cache fill.  A range without tiles is split
+// evenly over all prefetch workgroups; a tiled range's tile j goes to the
+// prefetch workgroups on XCD j % 8 (split evenly among them), so that it
+// lands in the L2 of the XCD whose workgroup will read it.  Every load
+// completes before the wave ends.
+__device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
+                             unsigned char* smem) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(smem) + w * 1024);
+  const int xcd = (int)(blockIdx.x & 7);
+  // prefetch workgroups on this XCD: indices q0, q0 + 8, ... < npw
+  const int q0 = ((xcd - first) % 8 + 8) % 8;
+  const int xrank = (pw - q0) / 8, xcount = (npw - q0 + 7) / 8;
+#pragma unroll 1
+  for (int r = 0; r < 8; ++r) {
+    const int64_t bytes = p.prefetch_bytes[r];
+    if (!p.prefetch[r] || bytes <= 0) continue;
+    // 32-bit offsets: a range of up to 2 GiB per view
+    const i32x4_t rs = make_rsrc4(p.prefetch[r], bytes < 0x7fffffff ? (uint32_t)bytes
+                                                                    : 0x7fffffffu);
+    const int64_t tb = p.prefetch_tile_bytes[r];
+    if (tb > 0) {
+      // this XCD's tiles j = xcd, xcd + 8, ...: their blocks in order, a
+      // contiguous share per prefetch workgroup of the XCD
+      const int64_t bpt = tb / 1024, ntiles = bytes / tb;
+      const int64_t xt = ntiles > xcd ? (ntiles - xcd + 7) / 8 : 0;
+      const int64_t nblk = xt * bpt;
+      const int64_t per = (nblk + xcount - 1) / xcount;
+      const int64_t b0 = (int64_t)xrank * per;
+      const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
+#pragma unroll 1
+      for (int64_t b = b0 + w; b < b1; b += 4) {
+        const int64_t j = xcd + 8 * (b / bpt);
+        load_lds16(rs, lds, (uint32_t)(j * tb + (b % bpt) * 1024) + (uint32_t)lane * 16u);
+      }
+    } else {
+      const int64_t nblk = (bytes + 1023) / 1024;
+      const int64_t per = (nblk + npw - 1) / npw;
+      const int64_t b0 = (int64_t)pw * per;
+      const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
+#pragma unroll 1
+      for (int64_t b = b0 + w; b < b1; b += 4)
+        load_lds16(rs, lds, (uint32_t)(b * 1024) + (uint32_t)lane * 16u);
+    }
+  }
+  wait_vmcnt<0>();
+}
+
 __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
                                                           int n_rg, int splits,
-                                                          int kps, int hs) {
+                                                          int kps, int hs,
+                                                          int n_items) {
   constexpr int HD = 256, KT = kDecKT;
   __shared__ __align__(16) unsigned char smem[kDecLDS];
   __shared__ float sL[4][64], sM[64];
+  if ((int)blockIdx.x >= n_items) {
+    dec_prefetch(p, (int)blockIdx.x - n_items, (int)gridDim.x - n_items, n_items, smem);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, g = lane >> 4;
   // XCD-aware order: consecutive items (the row groups of one key range)
   // land on one XCD and share its L2 copy of the range's K / V tiles.
-  const int nb = (int)gridDim.x, q8 = nb >> 3, r8 = nb & 7;
+  const int nb = n_items, q8 = nb >> 3, r8 = nb & 7;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
   const int rg = item % n_rg;
@@ -1139,6 +1196,27 @@ static AttnPlan plan_attn(const fvx_attn_desc& d) {
 
 using namespace fvx;
 
+static bool has_prefetch(const fvx_attn_desc& d) {
+  for (int r = 0; r < 8; ++r)
+    if (d.prefetch[r] && d.prefetch_bytes[r] > 0) return true;
+  return false;
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 struct DecodePlan {
   int n_rb, splits, n_items;
   int64_t kps, ws_bytes;
@@ -1247,6 +1325,16 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
               FVX_ERR_ARG,
               "attention: o_frag needs the decode path (transposed V, head_dim "
               "256), n_problems * sq <= 64 and 16B-aligned outputs");
+  for (int r = 0; r < 8; ++r)
+    FVX_REQUIRE(!d.prefetch[r] ||
+                    (aligned16(d.prefetch[r]) && d.prefetch_bytes[r] >= 0 &&
+                     d.prefetch_bytes[r] % 1024 == 0 && d.prefetch_tile_bytes[r] >= 0 &&
+                     d.prefetch_tile_bytes[r] % 1024 == 0),
+                FVX_ERR_ARG,
+                "attention: prefetch ranges need 16B-aligned pointers and byte "
+                "and tile-byte counts that are multiples of 1024");
+  FVX_REQUIRE(d.prefetch_wgs >= 0 && d.prefetch_wgs <= 4096, FVX_ERR_ARG,
+              "attention: prefetch_wgs must be in [0, 4096]");
   if (d.sq == 0 || d.n_problems == 0) return FVX_OK;
   FVX_REQUIRE(d.sk > 0, FVX_ERR_SHAPE, "attention: sk must be > 0");
   hipStream_t s = (hipStream_t)stream;
@@ -1260,6 +1348,14 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "attention: workspace must be 16B aligned");
     const int hs = (d.heads & (d.heads - 1)) == 0 ? __builtin_ctzll((uint64_t)d.heads) : -1;
+    int pf_wgs = 0;  // prefetch workgroups (the 4-wave kernel only)
+    if (a.kps < kDecTKps && has_prefetch(d)) {
+      pf_wgs = d.prefetch_wgs;
+      if (pf_wgs <= 0) {
+        const int cus = device_cus();
+        pf_wgs = cus > a.n_items ? cus - a.n_items : 0;
+      }
+    }
     // key ranges of >= 4 tiles (the prefix): attn_decode_t_kernel, ~8 %
     // faster there; one or two tiles per workgroup (the action expert): the
     // 4-wave kernel, whose fixed costs are lower
@@ -1267,8 +1363,9 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
       hipLaunchKernelGGL(attn_decode_t_kernel, dim3((unsigned)a.n_items), dim3(128),
                          0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
     else
-      hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)a.n_items), dim3(256),
-                         0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
+      hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)(a.n_items + pf_wgs)),
+                         dim3(256), 0, s, d, a.n_rb, a.splits, (int)a.kps, hs,
+                         a.n_items);
     int st = launch_status("attention(decode)");
     if (st || a.splits == 1) return st;
     const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 32;

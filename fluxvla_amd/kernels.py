@@ -573,8 +573,43 @@ def run_attention(d):
     _lib.call('fvx_attention', ctypes.byref(d), _stream())
 
 
+def _device_buffer(t):
+    """The device tensor behind a weight object (fragment-major, fp8 or
+    plain)."""
+    if isinstance(t, FragB):
+        return t.buf
+    if isinstance(t, Fp8Weight):
+        return t.data
+    return t
+
+
+def _set_prefetch(d, prefetch, prefetch_wgs, place=True):
+    """Up to 8 ranges the decode attention's idle workgroups pull into the
+    caches (fvx_attn_desc.prefetch).  Fragment-major weights (FragB, frag
+    Fp8Weight) are sequences of 16-column tiles, tile j read by a workgroup
+    on XCD j % 8: with ``place`` each tile is fetched from that XCD."""
+    items = list(prefetch or ())
+    if len(items) > 8:
+        raise ValueError('at most 8 prefetch ranges')
+    for i, t in enumerate(items):
+        buf = _device_buffer(t)
+        _check(buf, f'prefetch[{i}]', dtype=None)
+        nbytes = buf.numel() * buf.element_size()
+        tile = 0
+        if place and (isinstance(t, FragB) or
+                      (isinstance(t, Fp8Weight) and t.frag)):
+            tile = nbytes // (t.n // 16)
+            if tile % 1024:
+                tile = 0
+        d.prefetch[i] = buf.data_ptr()
+        d.prefetch_bytes[i] = nbytes - nbytes % 1024
+        d.prefetch_tile_bytes[i] = tile
+    d.prefetch_wgs = int(prefetch_wgs)
+
+
 def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
-                  v_transposed=False, o_frag=None):
+                  v_transposed=False, o_frag=None, prefetch=None,
+                  prefetch_wgs=0, prefetch_place=True):
     """Batched multi-query attention.
 
     q: [B, Sq, H, D] (or [B, Sq, H*D]); k: [B, Sk, D] (row stride may exceed
@@ -582,7 +617,11 @@ def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
     cache [B, D, T >= Sk] (keys contiguous); o like q.  kgrp: int32 [B, Sk],
     qgrp: int32 [B, Sq] (visible iff kgrp[j] <= qgrp[i]).  ``o_frag`` (a
     FragA with k = H*D, decode path only) also receives the output in the
-    fragment-major layout, ready as the o-projection's A operand."""
+    fragment-major layout, ready as the o-projection's A operand.
+    ``prefetch``: up to 8 tensors / prepared weights that idle workgroups
+    of the decode kernel read into the caches meanwhile (the next GEMMs'
+    weights; ``prefetch_wgs`` of them, 0 = fill the CUs; see
+    _set_prefetch for ``prefetch_place``)."""
     B, Sq = q.shape[0], q.shape[1]
     D = k.shape[-1]
     H = (q.shape[2] if q.dim() == 4 else q.shape[2] // D)
@@ -606,6 +645,8 @@ def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
             raise ValueError('o_frag must have k == heads * head_dim')
         _check(o_frag.buf, 'o_frag')
         d.o_frag = o_frag.buf.data_ptr()
+    if prefetch:
+        _set_prefetch(d, prefetch, prefetch_wgs, prefetch_place)
     run_attention(d)
     return o
 

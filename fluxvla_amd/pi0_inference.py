@@ -259,6 +259,11 @@ class PI0Inference:
         self.device = torch.device(device)
         self.use_graph = use_graph
         self.max_batch = max_batch
+        # bs=1 expert: the attention's idle workgroups prefetch the next
+        # GEMMs' weights, each 16-column tile into the L2 of the XCD that
+        # will read it (prefetch_place) or the memory-side cache
+        self.prefetch = True
+        self.prefetch_place = True
         self.weight_dtype = weight_dtype
         K.workspace(self.device)
         K.workspace(self.device, 'attn')
@@ -579,13 +584,26 @@ class PI0Inference:
                         vc[:, :, S:], cfg.heads, D,
                         rownorm_eps=cfg.rms_eps, row_group=Ss,
                         row_group_stride=T, v_ld=T)
+        # the attention leaves most CUs idle: its extra workgroups pull the
+        # next three GEMMs' weights into the memory-side cache meanwhile
         K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
                         kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True,
-                        o_frag=ctxf)
+                        o_frag=ctxf, prefetch=self._prefetch_list(i),
+                        prefetch_place=self.prefetch_place)
         K.gemm(ctxf, Lf['o_w'], out=x, residual=x, c_frag=xf)
         K.gemm_geglu(xf, Lf['gate_w'], Lf['up_w'], out=b['ex_h'],
                      rownorm_eps=cfg.rms_eps, c_frag=hf)
         K.gemm(hf, Lf['down_w'], out=x, residual=x, c_frag=xf)
+
+    def _prefetch_list(self, i):
+        """The weights expert layer i's attention prefetches: its O, gate,
+        up and down weights and the next layer's Q|K|V (layer 0's after the
+        last: the next Euler step starts there), or None when prefetching
+        is off."""
+        if not self.prefetch:
+            return None
+        Lf, Ln = self.exp_f[i], self.exp_f[(i + 1) % len(self.exp_f)]
+        return [Lf['o_w'], Lf['gate_w'], Lf['up_w'], Lf['down_w'], Ln['qkv_w']]
 
     def _expert_layer_pi0(self, b, B, i, L):
         if self._frag_ok(B):
@@ -609,8 +627,10 @@ class PI0Inference:
 
     def _expert_layer_pi05(self, b, B, i, L, step):
         cfg = self.cfg
+        pf = None
         if self._frag_ok(B):
             L = self.exp_f[i]  # fragment-major weights for the skinny GEMMs
+            pf = self._prefetch_list(i)
         S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
         T = self.kv_len
         x = b['ex_x'].view(B * Ss, hid)
@@ -624,7 +644,8 @@ class PI0Inference:
                         vc[:, :, S:], cfg.heads, D, row_group=Ss,
                         row_group_stride=T, v_ld=T)
         K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
-                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True)
+                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True,
+                        prefetch=pf, prefetch_place=self.prefetch_place)
         K.gemm(b['ex_ctx'].view(B * Ss, -1), L['o_w'], out=x, residual=x,
                gate=gate)
         K.adarms_norm(x, st[2 * i + 1:2 * i + 2], out=xn, gate_out=gate,

@@ -272,6 +272,25 @@ typedef struct fvx_attn_desc {
    * of fvx_gemm_desc.a_frag, row z * sq + token, column head * 256 + d --
    * the A operand of the o-projection. */
   void* o_frag;
+  /* Prefetch (no counterpart in the reference).  Decode path with key
+   * ranges of fewer than 4 tiles (the bs=1 action expert) only: extra
+   * workgroups of the attention launch read the device ranges
+   * [prefetch[i], prefetch[i] + prefetch_bytes[i]) (into LDS, discarded)
+   * while the attention runs on the CUs it leaves idle, so that the next
+   * kernels' operands -- the expert layer's O / gate / up / down weights,
+   * the next layer's Q|K|V weights -- are cached when those kernels start.
+   * prefetch_tile_bytes[i] > 0: the range is a sequence of tiles of that
+   * size, tile j read by a workgroup the hardware places on XCD j % 8 (the
+   * fragment-major weights of the M <= 64 GEMM); each tile is then read
+   * from a CU of that XCD, into that XCD's L2.  0: no placement (the
+   * memory-side cache).  NULL entries are skipped; pointers 16-byte
+   * aligned; bytes (and tile bytes) multiples of 1024.  prefetch_wgs > 0:
+   * that many extra workgroups; 0: as many as leave one workgroup per CU.
+   * Ignored on other paths. */
+  const void* prefetch[8];
+  int64_t prefetch_bytes[8];
+  int64_t prefetch_tile_bytes[8];
+  int32_t prefetch_wgs;
 } fvx_attn_desc;
 
 int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d);

@@ -36,7 +36,7 @@ def test_gemm_desc_layout_matches_c():
     body = text[text.index('typedef struct fvx_gemm_desc'):]
     body = body[:body.index('} fvx_gemm_desc;')]
     body = re.sub(r'/\*.*?\*/', '', body, flags=re.S)
-    c_names = re.findall(r'\*?\s*(\w+)\s*[;,]', body)
+    c_names = re.findall(r'\*?\s*(\w+)\s*(?:\[\d+\])?\s*[;,]', body)
     assert c_names == names
 
 
@@ -46,8 +46,12 @@ def test_attn_desc_layout_matches_c():
     body = text[text.index('typedef struct fvx_attn_desc'):]
     body = body[:body.index('} fvx_attn_desc;')]
     body = re.sub(r'/\*.*?\*/', '', body, flags=re.S)
-    c_names = re.findall(r'\*?\s*(\w+)\s*[;,]', body)
+    c_names = re.findall(r'\*?\s*(\w+)\s*(?:\[\d+\])?\s*[;,]', body)
     assert c_names == names
+    # array fields keep their C lengths
+    fields = dict(_lib.AttnDesc._fields_)
+    assert all(fields[f]._length_ == 8 for f in
+               ('prefetch', 'prefetch_bytes', 'prefetch_tile_bytes'))
 
 
 def _err(lib):

@@ -519,3 +519,34 @@ def test_embed_tokens_and_copy_rows(K, cuda):
                 dst_group_stride=10)
     assert torch.equal(dst[:, 0].cpu(), src)
     assert dst[:, 1:].abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize('place', [False, True])
+def test_decode_attention_prefetch_changes_nothing(cuda, place):
+    """The expert decode attention with prefetch ranges (extra workgroups
+    reading the next GEMMs' fragment-major weights): bitwise the output
+    without them, the prefetched buffers untouched."""
+    from fluxvla_amd import kernels as Kk
+    announce(f'decode attention with prefetch place={place}')
+    g = torch.Generator().manual_seed(70)
+    B, Sq, H, D, S, T = 1, 51, 8, 256, 816, 872
+    q = torch.randn(B, Sq, H, D, generator=g).bfloat16().to(cuda)
+    k = torch.randn(B, T, D, generator=g).bfloat16().to(cuda)
+    vt = torch.randn(B, D, T, generator=g).bfloat16().to(cuda)
+    kgrp = torch.zeros(B, S + Sq, dtype=torch.int32, device=cuda)
+    kgrp[:, S + 1:] = 1
+    qgrp = torch.ones(B, Sq, dtype=torch.int32, device=cuda)
+    qgrp[:, 0] = 0
+    ws = [Kk.FragB.pack((torch.randn(n, kk, generator=g) * 0.02).bfloat16().to(cuda))
+          for n, kk in ((1024, 2048), (4096, 1024), (4096, 1024), (1024, 4096),
+                        (2560, 1024))]
+    before = [w.buf.clone() for w in ws]
+    o1 = torch.empty_like(q)
+    o2 = torch.empty_like(q)
+    Kk.mqa_attention(q, k[:, :S + Sq], vt, o1, kgrp=kgrp, qgrp=qgrp,
+                     v_transposed=True)
+    Kk.mqa_attention(q, k[:, :S + Sq], vt, o2, kgrp=kgrp, qgrp=qgrp,
+                     v_transposed=True, prefetch=ws, prefetch_place=place)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert all(torch.equal(a, w.buf) for a, w in zip(before, ws))
