@@ -248,10 +248,14 @@ class PI0Inference:
     """
 
     def __init__(self, cfg: PI0Config, state_dict, device='cuda',
-                 max_batch=1, use_graph=True, weight_dtype='bf16'):
+                 max_batch=1, use_graph=True, weight_dtype='bf16',
+                 fp8_cache=None):
         """``weight_dtype``: 'bf16'; 'fp8' (e4m3 Gemma linears, bf16
         activations: W8A16); 'fp8_w8a8' (e4m3 linears and e4m3 activations,
-        quantized per row and k step in the GEMMs)."""
+        quantized per row and k step in the GEMMs).  ``fp8_cache``: path of
+        a safetensors file holding the quantized linears; read when it was
+        written for these weights (checkpoint.load_fp8_cache), else the
+        weights are quantized and the file (re)written."""
         if weight_dtype not in WEIGHT_DTYPES:
             raise ValueError(f'weight_dtype must be one of {WEIGHT_DTYPES}, '
                              f'got {weight_dtype!r}')
@@ -265,6 +269,8 @@ class PI0Inference:
         self.prefetch = True
         self.prefetch_place = True
         self.weight_dtype = weight_dtype
+        self.fp8_cache = fp8_cache
+        self.fp8_cache_hit = False
         K.workspace(self.device)
         K.workspace(self.device, 'attn')
         self._sd = state_dict
@@ -280,9 +286,21 @@ class PI0Inference:
         self.llm = prepare_gemma(sd, cfg, 'llm', dev)
         self.exp = prepare_gemma(sd, cfg, 'expert', dev)
         if self.fp8:
+            from .checkpoint import build_fp8_cache, load_fp8_cache
             act = 'e4m3' if self.weight_dtype == 'fp8_w8a8' else 'bf16'
-            quantize_linears(self.llm, act)
-            quantize_linears(self.exp, act)
+            cached = (load_fp8_cache(self.fp8_cache, sd, cfg, act, dev)
+                      if self.fp8_cache else None)
+            if cached is not None:
+                for W, layers in ((self.llm, cached['llm']),
+                                  (self.exp, cached['expert'])):
+                    for L, C in zip(W['layers'], layers):
+                        L.update(C)
+                self.fp8_cache_hit = True
+            else:
+                quantize_linears(self.llm, act)
+                quantize_linears(self.exp, act)
+                if self.fp8_cache:
+                    build_fp8_cache(self, sd, self.fp8_cache)
         self.proj = prepare_projector(sd, 'projector', dev)
         self.act_in = prepare_projector(sd, 'action_in_proj', dev)
         out = prepare_projector(sd, 'action_out_proj', dev)

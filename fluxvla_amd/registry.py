@@ -74,14 +74,26 @@ def config_from_reference(cfg: dict, num_views=None, max_prompt_len=None):
     return PI0Config(**kw)
 
 
-def build_vla_from_cfg(cfg: dict, state_dict, device='cuda', max_batch=1,
-                       num_views=None, max_prompt_len=None, use_graph=True):
+def build_vla_from_cfg(cfg: dict, state_dict=None, device='cuda', max_batch=1,
+                       num_views=None, max_prompt_len=None, use_graph=True,
+                       **kwargs):
     """Build the registered inference model named by ``cfg['type']`` from a
-    state dict with the reference's parameter names."""
+    state dict with the reference's parameter names, or -- without one --
+    from the config's ``pretrained_name_or_path`` through its
+    ``name_mapping`` / ``strict_mapping`` (BaseVLA.from_pretrained,
+    base_vla.py:190-288).  Extra keyword arguments go to the model
+    (``weight_dtype``, ``fp8_cache``)."""
     name = cfg['type']
     if name not in VLAS:
         raise KeyError(f'{name} is not a registered VLA type '
                        f'({sorted(VLAS)})')
     pcfg = config_from_reference(cfg, num_views, max_prompt_len)
+    if state_dict is None:
+        from .checkpoint import from_pretrained
+        path = cfg.get('pretrained_name_or_path')
+        if not path:
+            raise ValueError('no state_dict and no pretrained_name_or_path')
+        state_dict = from_pretrained(pcfg, path, cfg.get('name_mapping'),
+                                     strict=cfg.get('strict_mapping', True))
     return VLAS[name](pcfg, state_dict, device=device, max_batch=max_batch,
-                      use_graph=use_graph)
+                      use_graph=use_graph, **kwargs)
