@@ -113,11 +113,19 @@ def map_state_dict(params, ckpt, name_mapping=None, strict=True,
 
 
 def from_pretrained(cfg: PI0Config, path, name_mapping=PI0_NAME_MAPPING,
-                    strict=True, dtype=torch.bfloat16):
-    """State dict of the PI0 / PI0.5 model ``cfg`` from a checkpoint."""
+                    strict=False, dtype=torch.bfloat16):
+    """State dict of the PI0 / PI0.5 model ``cfg`` from a checkpoint.
+    ``strict`` defaults to the reference's ``strict_mapping=False``
+    (base_vla.py:55): unmatched parameters are collected rather than raised
+    one by one -- but the inference model has no initialized fallback for
+    them, so any left over is an error naming them all."""
     params = [(n, s) for n, s, _, _ in param_specs(cfg)]
     sd, skipped = map_state_dict(params, load_checkpoint(path), name_mapping,
                                  strict, dtype)
+    if skipped:
+        raise ValueError(f'{len(skipped)} parameters not found in {path} '
+                         f'(after name_mapping): {skipped[:8]}'
+                         + (' ...' if len(skipped) > 8 else ''))
     return sd
 
 

@@ -94,6 +94,6 @@ def build_vla_from_cfg(cfg: dict, state_dict=None, device='cuda', max_batch=1,
         if not path:
             raise ValueError('no state_dict and no pretrained_name_or_path')
         state_dict = from_pretrained(pcfg, path, cfg.get('name_mapping'),
-                                     strict=cfg.get('strict_mapping', True))
+                                     strict=cfg.get('strict_mapping', False))
     return VLAS[name](pcfg, state_dict, device=device, max_batch=max_batch,
                       use_graph=use_graph, **kwargs)

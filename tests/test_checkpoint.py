@@ -88,6 +88,16 @@ def test_mapping_errors_and_skips(ckpt):
     assert all(torch.equal(out[k], sd[k]) for k in sd)
 
 
+def test_from_pretrained_names_missing_parameters(ckpt, tmp_path):
+    cfg, sd, path = ckpt
+    raw = load_file(path)
+    gone = 'paligemma_with_expert.gemma_expert.model.layers.0.mlp.up_proj.weight'
+    p = str(tmp_path / 'partial.safetensors')
+    save_file({k: v for k, v in raw.items() if k != gone}, p)
+    with pytest.raises(ValueError, match='llm_expert.layers.0.mlp.up_proj'):
+        C.from_pretrained(cfg, p)
+
+
 def test_unsupported_format(tmp_path):
     p = tmp_path / 'x.bin'
     p.write_bytes(b'0')
