@@ -260,13 +260,13 @@ def kernel_table(model):
         ('gemm_tile_kernel<64,128,PLAIN> qkv+bias (SigLIP)', lambda: K.gemm(
             vxn, V['qkv_w'], out=b['vis_qkv'], bias=V['qkv_b']),
          2 * Mv * 3 * vh * vh),
-        ('gemm_tile_kernel<64,128,PLAIN> o-proj+bias+res (SigLIP)',
+        ('gemm_tile_kernel<64,64,PLAIN> o-proj+bias+res (SigLIP)',
          lambda: K.gemm(b['vis_ctx'], V['o_w'], out=vxn, bias=V['o_b'],
                         residual=vx), 2 * Mv * vh * vh),
         ('gemm_tile_kernel<64,128,PLAIN> fc1+bias+gelu (SigLIP)', lambda: K.gemm(
             vxn, V['fc1_w'], out=b['vis_h'], bias=V['fc1_b'], act=2),
          2 * Mv * cfg.vit_mlp * vh),
-        ('gemm_tile_kernel<64,128,PLAIN> fc2+bias+res, split-K 2 (SigLIP)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,64,PLAIN> fc2+bias+res (SigLIP)', lambda: K.gemm(
             b['vis_h'], V['fc2_w'], out=vxn, bias=V['fc2_b'], residual=vx),
          2 * Mv * vh * cfg.vit_mlp),
         ('attn_kernel<96,80> (SigLIP)', lambda: K.mha_packed_qkv(

@@ -1984,10 +1984,14 @@ static int validate(const GemmArgs& d) {
 // Small tiles win on these shapes: the extra workgroups hide more latency
 // than they cost in LDS traffic per flop; deeper rings win only when the
 // grid leaves CUs idle.
-static const int kTileBM[] = {64, 256, 64, 256};
-static const int kTileBN[] = {128, 256, 128, 256};
-constexpr int kTileCfgs = 4;
+static const int kTileBM[] = {64, 256, 64, 256, 64};
+static const int kTileBN[] = {128, 256, 128, 256, 64};
+constexpr int kTileCfgs = 5;
 constexpr int kWideCfg = 3;  // gemm_wide_kernel
+// 4: 64 x 64, 2 x 2 waves of 32 x 32, 4 stages -- bf16 PLAIN / QKV / EULER
+// GEMMs with fewer than 128 tiles of 64 x 128 (SigLIP o-proj, fc2: M = 768,
+// N = 1152): twice the workgroups instead of idle CUs or a split-K pass
+constexpr int kSmallCfg = 4;
 #ifndef FVX_WIDE_MIN_TILES
 #define FVX_WIDE_MIN_TILES 128
 #endif
@@ -1999,6 +2003,12 @@ constexpr int kWideCfg = 3;  // gemm_wide_kernel
 #endif
 #ifndef FVX_WIDE_SPLIT_MIN_K
 #define FVX_WIDE_SPLIT_MIN_K 8192
+#endif
+#ifndef FVX_SMALL_TILES
+#define FVX_SMALL_TILES 1
+#endif
+#ifndef FVX_SMALL_MAX_TILES
+#define FVX_SMALL_MAX_TILES 128
 #endif
 
 static int tile_bm(int cfg, int fp8) {
@@ -2059,13 +2069,29 @@ static TilePlan plan_tile(const GemmArgs& d) {
   if (gg && wtiles >= 256) t.cfg = 1;
   else t.cfg = tiles <= 256 ? 2 : 0;
   if (d.ss_out || d.a8_out) return t;  // written by the one-pass epilogue
+  if (FVX_SMALL_TILES && !gg && !d.b_fp8 && d.split_k == 0 && tiles < FVX_SMALL_MAX_TILES) {
+    t.cfg = kSmallCfg;
+    return t;
+  }
   if (d.split_k > 0) t.splits = d.split_k;
   else if (t.cfg != 1 && tiles < 128 && d.k >= 4096) t.splits = 2;
   return t;
 }
 
+// 64 x 64 tiles (kSmallCfg): not instantiated for GEGLU, whose tiles hold
+// two weights' columns
+template <int MODE>
+static void launch_small_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int m_tiles,
+                              int n_tiles, int splits, int64_t kchunk, int vec_ok) {
+  if constexpr (MODE != FVX_GEMM_GEGLU)
+    hipLaunchKernelGGL((gemm_tile_kernel<64, 64, 2, 2, 4, MODE, false, false>), grid,
+                       dim3(256), 0, s, d, m_tiles, n_tiles, splits, kchunk, vec_ok);
+}
+
 static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   FVX_REQUIRE(cfg >= 0 && cfg < kTileCfgs, FVX_ERR_ARG, "gemm: bad tile config %d", cfg);
+  FVX_REQUIRE(cfg != kSmallCfg || (d.mode != FVX_GEMM_GEGLU && !d.b_fp8), FVX_ERR_ARG,
+              "gemm: the 64 x 64 tile configuration takes no GEGLU / fp8 weights");
   const bool gg = d.mode == FVX_GEMM_GEGLU;
   const int bm = tile_bm(cfg, d.b_fp8), bn = kTileBN[cfg] / (gg ? 2 : 1);
   const int m_tiles = (int)((d.m + bm - 1) / bm);
@@ -2164,6 +2190,8 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     } else {                                                                          \
       if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false, false);                        \
       else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false, false);                    \
+      else if (cfg == kSmallCfg)                                                      \
+        launch_small_tile<MODE>(grid, s, d, m_tiles, n_tiles, splits, kchunk, vec_ok); \
       else LT(64, 128, 2, 2, 3, MODE, false, false);                                  \
     }
     FVX_MODE_DISPATCH(d.mode, LCFG)

@@ -290,7 +290,8 @@ def interleave_perm(hd):
     return idx
 
 
-@pytest.mark.parametrize('m,k,start', [(51, 1024, 816), (816, 2048, 0)])
+@pytest.mark.parametrize('m,k,start', [(51, 1024, 816), (816, 2048, 0),
+                                         (102, 1024, 816)])
 @pytest.mark.parametrize('vt', [False, True])
 def test_gemm_qkv_rope(K, cuda, m, k, start, vt):
     announce(f'gemm qkv_rope m={m} k={k} v_transposed={vt}')
