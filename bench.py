@@ -41,16 +41,27 @@ def log(msg):
     print(f'[bench] {msg}', file=sys.stderr, flush=True)
 
 
-def measured_traffic():
-    """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 FETCH_SIZE + WRITE_SIZE passes (counter-calibrated)."""
-    import re
-    path = os.path.join(ROOT, 'profiles', 'prefix_geglu_gemm_traffic.md')
+TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'pi0_bs1_kernel_table_traffic.md')
+
+
+def measured_traffic(row=None):
+    """HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)
+    of a kernel-table row from the committed profile, keyed by row name
+    (all rows if ``row`` is None); None where absent."""
     try:
-        m = re.search(r'traffic_bytes_per_launch:\s*(\d+)', open(path).read())
-        return int(m.group(1)) if m else None
+        text = open(TRAFFIC_PROFILE).read()
     except OSError:
-        return None
+        return None if row is not None else {}
+    out = {}
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip('|').split('|')]
+        if len(cells) < 6:
+            continue
+        try:
+            out[cells[0]] = int(round((float(cells[4]) + float(cells[5])) * 1e6))
+        except ValueError:
+            continue
+    return out if row is None else out.get(row)
 
 
 def time_dominant_kernel(model, iters=20):
@@ -91,8 +102,9 @@ def time_dominant_kernel(model, iters=20):
         'peak': PEAK_BF16_TFLOPS,
         'unit': 'TFLOP/s',
         'frac': round(achieved / PEAK_BF16_TFLOPS, 4),
-        'traffic': measured_traffic(),
-        'traffic_unit': 'bytes/launch (rocprofv3 FETCH_SIZE + WRITE_SIZE)',
+        'traffic': measured_traffic('gemm_wide_kernel<GEGLU> (prefix)'),
+        'traffic_unit': 'bytes/launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, '
+                        'profiles/pi0_bs1_kernel_table_traffic.md)',
         'avg_us': round(us, 2),
         'flops_per_launch': flops,
     }
@@ -146,10 +158,11 @@ def _row(name, shape, bound, work, us):
     else:
         achieved = work / (us * 1e-6) / 1e12
         peak, unit = PEAK_BF16_TFLOPS, 'TFLOP/s'
+    # HBM bytes per launch from the committed rocprofv3 counter passes
     return {'kernel': name, 'shape': shape, 'bound': bound,
             'avg_us': round(us, 2), 'achieved': round(achieved, 1),
             'peak': peak, 'unit': unit, 'frac': round(achieved / peak, 4),
-            'work': work}
+            'work': work, 'traffic': measured_traffic(name)}
 
 
 def kernel_table(model):
