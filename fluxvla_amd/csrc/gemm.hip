@@ -51,74 +51,6 @@ __device__ __forceinline__ int64_t out_row(const GemmArgs& p, int64_t m) {
              : m;
 }
 
-// Epilogue for one MFMA output fragment: rows row0 + j (j < 4) of column n.
-// v: main accumulator, u: GEGLU up accumulator, pv: value of column n ^ 1
-// (QKV_ROPE partner), rs: per-row RMS factors (used when p.rownorm).
-template <int MODE, int NR = 4>
-__device__ __forceinline__ void epilogue4(const GemmArgs& p, int64_t row0,
-                                          int64_t n, const float* v,
-                                          const float* u, const float* pv,
-                                          const float* rs) {
-  if (n >= p.n) return;
-#pragma unroll
-  for (int j = 0; j < NR; ++j) {
-    const int64_t m = row0 + j;
-    if (m >= p.m) break;
-    const float r = p.rownorm ? rs[j] : 1.f;
-    float x = v[j] * r;
-    if (MODE == FVX_GEMM_GEGLU) {
-      x = gelu_tanh(x) * (u[j] * r);
-      ((bf16_t*)p.c)[out_row(p, m) * p.ldc + n] = f2bf(x);
-      continue;
-    }
-    if (MODE == FVX_GEMM_QKV_ROPE) {
-      const int hd = p.head_dim;
-      const int64_t qcols = (int64_t)p.n_q_heads * hd;
-      if (n < qcols + hd) {
-        const int i = (int)(n % hd) >> 1;
-        const float2 cs =
-            *(const float2*)(p.rope + ((int64_t)p.positions[m] * (hd >> 1) + i) * 2);
-        const float px = pv[j] * r;
-        x = (n & 1) ? (x * cs.x + px * cs.y) : (x * cs.x - px * cs.y);
-        if (n < qcols)
-          ((bf16_t*)p.q_out)[m * p.ldq + n] = f2bf(x);
-        else
-          ((bf16_t*)p.k_out)[out_row(p, m) * p.ldk + (n - qcols)] = f2bf(x);
-      } else if (p.v_transposed) {
-        // V^T cache: [group][head_dim][ldv], tokens contiguous
-        const int64_t b = p.row_group > 0 ? m / p.row_group : 0;
-        const int64_t t = p.row_group > 0 ? m % p.row_group : m;
-        ((bf16_t*)p.v_out)[(b * hd + (n - qcols - hd)) * p.ldv + t] = f2bf(x);
-      } else {
-        ((bf16_t*)p.v_out)[out_row(p, m) * p.ldv + (n - qcols - hd)] = f2bf(x);
-      }
-      continue;
-    }
-    if (p.bias) x += bf2f(((const bf16_t*)p.bias)[n]);
-    if (p.bias_f32) x += p.bias_f32[n];
-    if (MODE == FVX_GEMM_EULER) {
-      float* xt = p.xt + m * p.ldx + n;
-      const float nx = *xt + p.dt * x;
-      *xt = nx;
-      if (p.xt_bf16) ((bf16_t*)p.xt_bf16)[m * p.ldxb + n] = f2bf(nx);
-      continue;
-    }
-    if (p.act == FVX_ACT_SILU)
-      x = silu(x);
-    else if (p.act == FVX_ACT_GELU_TANH)
-      x = gelu_tanh(x);
-    if (p.gate)
-      x *= bf2f(((const bf16_t*)p.gate)[(m / p.gate_group) * p.ldg + n]);
-    const int64_t orow = out_row(p, m);
-    if (p.residual) x += bf2f(((const bf16_t*)p.residual)[orow * p.ldr + n]);
-    if (p.pos) x += bf2f(((const bf16_t*)p.pos)[(m % p.pos_period) * p.ldp + n]);
-    if (p.out_f32)
-      ((float*)p.c)[orow * p.ldc + n] = x;
-    else
-      ((bf16_t*)p.c)[orow * p.ldc + n] = f2bf(x);
-  }
-}
-
 // sum of squares of 8 bf16 values: four v_dot2c_f32_bf16 (fp32 accumulate)
 __device__ __forceinline__ float sumsq8(const bf16x8& v) {
   typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
