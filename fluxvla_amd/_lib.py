@@ -69,6 +69,11 @@ class GemmDesc(ctypes.Structure):
         ('a8_out', c_vp), ('a8_out_scale', c_vp), ('a8_out_ld', c_i64), ('a8_out_sld', c_i64),
         ('a8', c_vp), ('a8_scale', c_vp), ('a8_ld', c_i64), ('a8_sld', c_i64),
         ('fp8_act', c_i32),
+        ('rtc_lock', c_vp), ('rtc_period', c_i64),
+        ('bias_f32_locked', c_vp),
+        ('rtc_prev', c_vp), ('ld_prev', c_i64),
+        ('rtc_cw', c_vp),
+        ('rtc_omt', c_f32),
     ]
 
 
@@ -111,6 +116,9 @@ SIGNATURES = {
                                c_vp]),
     'fvx_adarms_norm': (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                                 c_i64, c_f32, c_vp]),
+    'fvx_adarms_norm_locked': (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp,
+                                       c_vp, c_i64, c_i64, c_i64, c_i64,
+                                       c_f32, c_vp]),
     'fvx_attention_workspace_bytes': (c_i64, [ctypes.POINTER(AttnDesc)]),
     'fvx_attention': (c_i32, [ctypes.POINTER(AttnDesc), c_vp]),
     'fvx_im2col_patches': (c_i32, [c_vp, c_i32, c_i32, c_vp, c_i64, c_i64,

@@ -7,6 +7,7 @@ Gemma-2B prefix (width 2048, 18 layers, 8 query heads / 1 KV head, head_dim
 50-step action chunk of 32 dims, 10 Euler steps.
 """
 from dataclasses import dataclass, replace
+from typing import Optional
 
 
 @dataclass(frozen=True)
@@ -44,6 +45,10 @@ class PI0Config:
     pi05: bool = False
     # prompt length reserved in the static buffers
     max_prompt_len: int = 48
+    # the robot's real action dims (pi0_flowmatching.py:108,168): shorter
+    # previous chunks given for real-time chunking are zero-padded to
+    # max_action_dim when set (:747-751)
+    ori_action_dim: Optional[int] = None
 
     @property
     def num_patches(self):

@@ -77,8 +77,11 @@ __device__ __forceinline__ float sumsq8(const bf16x8& v) {
 // ---------------------------------------------------------------------------
 struct EpiIn {
   bf16x8 res, gate, pos, bias;
-  float f0[8];  // bias_f32 (PLAIN, EULER) or RoPE (cos, sin) x 4 (QKV_ROPE)
-  float xt[8];  // EULER state
+  float f0[8];    // bias_f32 (PLAIN, EULER) or RoPE (cos, sin) x 4 (QKV_ROPE)
+  float xt[8];    // EULER state
+  float prev[8];  // EULER with RTC: the previous chunk's actions
+  float cw;       // EULER with RTC guidance: the row's correction weight
+  bool locked;    // PLAIN, EULER: the row is in the RTC locked prefix
 };
 
 __device__ __forceinline__ void st_b8(bf16_t* dst, const float* x, bool vec,
@@ -156,11 +159,19 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
   }
   const int64_t N = p.n;
   in.bias = bl_b8(make_rsrc(p.bias, p.bias ? rec_bytes(N * 2) : 0u), (uint32_t)(n * 2), vec);
-  bl_f8(make_rsrc(p.bias_f32, p.bias_f32 ? rec_bytes(N * 4) : 0u), (uint32_t)(n * 4), vec,
-        in.f0);
+  // real-time chunking: row position within the chunk and the locked prefix
+  const int64_t rr = p.rtc_period > 0 ? m % p.rtc_period : 0;
+  in.locked = false;
+  if (p.rtc_lock) in.locked = rr < (int64_t)*p.rtc_lock;
+  const float* bf = in.locked && p.bias_f32_locked ? p.bias_f32_locked : p.bias_f32;
+  bl_f8(make_rsrc(bf, bf ? rec_bytes(N * 4) : 0u), (uint32_t)(n * 4), vec, in.f0);
   if (MODE == FVX_GEMM_EULER) {
     bl_f8(make_rsrc(p.xt, rec_bytes(p.m * p.ldx * 4)), (uint32_t)((m * p.ldx + n) * 4), vec,
           in.xt);
+    bl_f8(make_rsrc(p.rtc_prev, p.rtc_prev ? rec_bytes(p.m * p.ld_prev * 4) : 0u),
+          (uint32_t)((m * p.ld_prev + n) * 4), vec, in.prev);
+    in.cw = bload1f(make_rsrc(p.rtc_cw, p.rtc_cw ? rec_bytes(p.rtc_period * 4) : 0u),
+                    (uint32_t)(rr * 4));
     return;
   }
   const int64_t gg = p.gate_group > 0 ? p.gate_group : 1;
@@ -233,6 +244,17 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
     float nx[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) nx[e] = in.xt[e] + p.dt * x[e];
+    if (p.rtc_cw) {
+      // guidance: x_1 = xt - omt * v is the predicted clean chunk; the
+      // velocity is corrected by gw * w_r * (prev - x_1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        nx[e] += in.cw * (in.prev[e] - in.xt[e] + p.rtc_omt * x[e]);
+    }
+    if (in.locked && p.rtc_prev) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) nx[e] = in.prev[e];
+    }
     st_f8(p.xt + m * p.ldx + n, nx, vec, cnt);
     if (p.xt_bf16) st_b8((bf16_t*)p.xt_bf16 + m * p.ldxb + n, nx, vec, cnt);
     return;
@@ -366,11 +388,13 @@ static bool epi_vec_ok(const GemmArgs& d) {
              d.ldq % 8 == 0 && al(d.k_out) && d.ldk % 8 == 0 &&
              (d.v_transposed || (al(d.v_out) && d.ldv % 8 == 0));
     case FVX_GEMM_EULER:
-      return al(d.bias) && al(d.bias_f32) && al(d.xt) && d.ldx % 4 == 0 &&
-             (!d.xt_bf16 || (al(d.xt_bf16) && d.ldxb % 8 == 0));
+      return al(d.bias) && al(d.bias_f32) && al(d.bias_f32_locked) && al(d.xt) &&
+             d.ldx % 4 == 0 && (!d.xt_bf16 || (al(d.xt_bf16) && d.ldxb % 8 == 0)) &&
+             (!d.rtc_prev || (al(d.rtc_prev) && d.ld_prev % 4 == 0));
     default:
       return al(d.c) && d.ldc % (d.out_f32 ? 4 : 8) == 0 && al(d.bias) &&
-             al(d.bias_f32) && (!d.gate || (al(d.gate) && d.ldg % 8 == 0)) &&
+             al(d.bias_f32) && al(d.bias_f32_locked) &&
+             (!d.gate || (al(d.gate) && d.ldg % 8 == 0)) &&
              (!d.residual || (al(d.residual) && d.ldr % 8 == 0)) &&
              (!d.pos || (al(d.pos) && d.ldp % 8 == 0));
   }
@@ -1854,6 +1878,20 @@ static int validate(const GemmArgs& d) {
       FVX_REQUIRE(d.xt, FVX_ERR_NULL, "gemm(euler): xt required");
       break;
   }
+  const bool rtc = d.rtc_lock || d.bias_f32_locked || d.rtc_prev || d.rtc_cw;
+  FVX_REQUIRE(!rtc || ((d.mode == FVX_GEMM_PLAIN || d.mode == FVX_GEMM_EULER) &&
+                       d.rtc_period > 0),
+              FVX_ERR_ARG, "gemm: RTC fields need mode PLAIN or EULER and rtc_period > 0");
+  FVX_REQUIRE(!d.bias_f32_locked || (d.rtc_lock && d.bias_f32), FVX_ERR_ARG,
+              "gemm: bias_f32_locked needs rtc_lock and bias_f32");
+  FVX_REQUIRE(!(d.rtc_prev || d.rtc_cw) || d.mode == FVX_GEMM_EULER, FVX_ERR_ARG,
+              "gemm: rtc_prev / rtc_cw need mode EULER");
+  FVX_REQUIRE(!d.rtc_cw || d.rtc_prev, FVX_ERR_ARG, "gemm: rtc_cw needs rtc_prev");
+  FVX_REQUIRE(!d.rtc_prev || (d.ld_prev >= d.n && (d.rtc_lock || d.rtc_cw)), FVX_ERR_ARG,
+              "gemm: rtc_prev needs ld_prev >= n and rtc_lock or rtc_cw");
+  FVX_REQUIRE(((uintptr_t)d.rtc_lock & 3) == 0 && ((uintptr_t)d.rtc_prev & 3) == 0 &&
+                  ((uintptr_t)d.rtc_cw & 3) == 0 && ((uintptr_t)d.bias_f32_locked & 3) == 0,
+              FVX_ERR_ALIGN, "gemm: RTC pointers must be 4B aligned");
   FVX_REQUIRE(d.fp8_act == 0 || (d.fp8_act == 1 && d.b_fp8), FVX_ERR_ARG,
               "gemm: fp8_act must be 0, or 1 with b_fp8 (got %d)", d.fp8_act);
   if (d.b_fp8) {

@@ -129,14 +129,18 @@ template <int NV>
 __global__ __launch_bounds__(256) void adarms_norm_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ style,
     bf16_t* __restrict__ out, bf16_t* __restrict__ gate_out, int64_t rows,
-    int cols, int64_t rows_per_style, int64_t style_stride, float eps) {
+    int cols, int64_t rows_per_style, int64_t style_stride, float eps,
+    const bf16_t* __restrict__ style_locked, const int32_t* __restrict__ lock,
+    int64_t lock_period) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nvec = cols >> 3;
-  const int64_t so = (row / rows_per_style) * style_stride;
+  // rows of the locked prefix (real-time chunking) use the time-0 style row
+  const bool locked = lock && (row % lock_period) < (int64_t)*lock;
+  const bf16_t* srow = locked ? style_locked : style + (row / rows_per_style) * style_stride;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * cols, (uint32_t)cols * 2);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(style + so, (uint32_t)cols * 6);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(srow, (uint32_t)cols * 6);
   bf16x8 xv[NV], scv[NV], shv[NV], gv[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -245,11 +249,11 @@ extern "C" int fvx_layer_norm(const void* x, const void* weight,
   return launch_status("layer_norm");
 }
 
-extern "C" int fvx_adarms_norm(const void* x, const void* style, void* out,
-                               void* gate_out, int64_t rows, int64_t cols,
-                               int64_t rows_per_style, int64_t style_stride,
-                               float eps, void* stream) {
-  clear_error();
+static int adarms_launch(const void* x, const void* style,
+                         const void* style_locked, const int32_t* lock,
+                         int64_t lock_period, void* out, void* gate_out,
+                         int64_t rows, int64_t cols, int64_t rows_per_style,
+                         int64_t style_stride, float eps, void* stream) {
   FVX_REQUIRE(x && style && out, FVX_ERR_NULL,
               "adarms_norm: x, style, out required");
   int st = check_rows("adarms_norm", rows, cols);
@@ -270,8 +274,38 @@ extern "C" int fvx_adarms_norm(const void* x, const void* style, void* out,
   hipLaunchKernelGGL(adarms_norm_kernel<NV>, grid, dim3(256), 0, s,         \
                      (const bf16_t*)x, (const bf16_t*)style, (bf16_t*)out,  \
                      (bf16_t*)gate_out, rows, (int)cols, rows_per_style,    \
-                     style_stride, eps)
+                     style_stride, eps, (const bf16_t*)style_locked, lock,  \
+                     lock_period)
   FVX_NV_DISPATCH(nv, L)
 #undef L
   return launch_status("adarms_norm");
+}
+
+extern "C" int fvx_adarms_norm(const void* x, const void* style, void* out,
+                               void* gate_out, int64_t rows, int64_t cols,
+                               int64_t rows_per_style, int64_t style_stride,
+                               float eps, void* stream) {
+  clear_error();
+  return adarms_launch(x, style, nullptr, nullptr, 1, out, gate_out, rows,
+                       cols, rows_per_style, style_stride, eps, stream);
+}
+
+extern "C" int fvx_adarms_norm_locked(const void* x, const void* style,
+                                      const void* style_locked,
+                                      const int32_t* lock, int64_t lock_period,
+                                      void* out, void* gate_out, int64_t rows,
+                                      int64_t cols, int64_t rows_per_style,
+                                      int64_t style_stride, float eps,
+                                      void* stream) {
+  clear_error();
+  FVX_REQUIRE(style_locked && lock, FVX_ERR_NULL,
+              "adarms_norm_locked: style_locked and lock required");
+  FVX_REQUIRE(lock_period > 0, FVX_ERR_SHAPE,
+              "adarms_norm_locked: lock_period must be > 0");
+  FVX_REQUIRE(aligned16(style_locked) && ((uintptr_t)lock & 3) == 0,
+              FVX_ERR_ALIGN,
+              "adarms_norm_locked: style_locked 16B, lock 4B aligned");
+  return adarms_launch(x, style, style_locked, lock, lock_period, out,
+                       gate_out, rows, cols, rows_per_style, style_stride, eps,
+                       stream);
 }

@@ -110,9 +110,12 @@ def layer_norm(x, weight, bias, eps=1e-6, out=None):
 
 
 def adarms_norm(x, style, out=None, gate_out=None, rows_per_style=None,
-                eps=1e-6):
+                eps=1e-6, style_locked=None, lock=None, lock_period=None):
     """style rows [scale | shift | gate] (bf16, 3*cols wide), one per
-    ``rows_per_style`` rows of x (default: one style row for all rows)."""
+    ``rows_per_style`` rows of x (default: one style row for all rows).
+    ``lock`` (device int32 [1]) with ``style_locked`` (one style row) and
+    ``lock_period``: rows with row % lock_period < lock take style_locked
+    (the prefix method of real-time chunking)."""
     _check(x, 'x')
     cols = x.shape[-1]
     rows = x.numel() // cols
@@ -124,6 +127,16 @@ def adarms_norm(x, style, out=None, gate_out=None, rows_per_style=None,
         out = torch.empty_like(x)
     _check(out, 'out')
     _check(gate_out, 'gate_out', allow_none=True)
+    if lock is not None:
+        _check(lock, 'lock', dtype=torch.int32)
+        _check(style_locked, 'style_locked', contiguous=False)
+        if style_locked.shape[-1] < 3 * cols:
+            raise ValueError('style_locked must hold 3 * cols values')
+        _lib.call('fvx_adarms_norm_locked', _ptr(x), _ptr(style),
+                  _ptr(style_locked), _ptr(lock), int(lock_period), _ptr(out),
+                  _ptr(gate_out), rows, cols, int(rows_per_style), sld,
+                  float(eps), _stream())
+        return out, gate_out
     _lib.call('fvx_adarms_norm', _ptr(x), _ptr(style), _ptr(out),
               _ptr(gate_out), rows, cols, int(rows_per_style), sld,
               float(eps), _stream())
@@ -398,13 +411,15 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
          gate=None, gate_group=1, pos=None, pos_period=0, act=_lib.ACT_NONE,
          rownorm_eps=None, out_f32=False, row_group=0, row_group_stride=0,
          split_k=0, c_frag=None, ss_in=None, ss_out=None, a8=None, a8_out=None,
-         noalloc=False):
+         noalloc=False, rtc_lock=None, rtc_period=0, bias_f32_locked=None):
     """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order.
     ``a`` may be a FragA and ``weight`` a FragB; ``c_frag`` (a FragA with
     k == n) also receives the output in the fragment-major layout;
     ``ss_in`` / ``ss_out``: see _set_ss; ``a8`` / ``a8_out``: see Fp8Act.
     ``noalloc``: run through fvx_gemm_noalloc (split-K scratch in the
-    library's static device array, no workspace)."""
+    library's static device array, no workspace).  ``rtc_lock`` (device
+    int32 [1]), ``rtc_period``, ``bias_f32_locked``: rows with
+    m % rtc_period < rtc_lock add bias_f32_locked instead of bias_f32."""
     d = _gemm_desc(a, weight)
     if out is None:
         out = torch.empty(*_lead_shape(a), d.n,
@@ -433,6 +448,7 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
         _, d.ldp = _rows_ld(pos, 'pos')
         d.pos, d.pos_period = pos.data_ptr(), pos_period or pos.shape[0]
     d.act, d.mode, d.out_f32 = int(act), _lib.GEMM_PLAIN, int(bool(out_f32))
+    _set_rtc(d, rtc_lock, rtc_period, bias_f32_locked)
     _set_ss(d, rownorm_eps, ss_in, ss_out)
     _set_a8(d, a8, a8_out)
     d.row_group, d.row_group_stride = row_group, row_group_stride
@@ -510,9 +526,42 @@ def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
     _run_gemm(d)
 
 
+def _set_rtc(d, lock=None, period=0, bias_f32_locked=None, prev=None,
+             cw=None, omt=0.0):
+    """Real-time chunking fields of fvx_gemm_desc (rtc_*)."""
+    if lock is None and bias_f32_locked is None and prev is None and cw is None:
+        return
+    if period <= 0:
+        raise ValueError('real-time chunking needs rtc_period > 0')
+    d.rtc_period = int(period)
+    if lock is not None:
+        _check(lock, 'rtc_lock', dtype=torch.int32)
+        d.rtc_lock = lock.data_ptr()
+    if bias_f32_locked is not None:
+        _check(bias_f32_locked, 'bias_f32_locked', dtype=torch.float32)
+        if bias_f32_locked.numel() < d.n:
+            raise ValueError('bias_f32_locked needs n values')
+        d.bias_f32_locked = bias_f32_locked.data_ptr()
+    if prev is not None:
+        _check(prev, 'rtc_prev', dtype=torch.float32, contiguous=False)
+        rows, d.ld_prev = _rows_ld(prev, 'rtc_prev')
+        if rows < d.m or prev.shape[-1] < d.n:
+            raise ValueError(f'rtc_prev must cover [{d.m}, {d.n}]')
+        d.rtc_prev = prev.data_ptr()
+    if cw is not None:
+        _check(cw, 'rtc_cw', dtype=torch.float32)
+        if cw.numel() < period:
+            raise ValueError('rtc_cw needs rtc_period values')
+        d.rtc_cw, d.rtc_omt = cw.data_ptr(), float(omt)
+
+
 def gemm_euler(a, weight, bias, xt, dt, xt_bf16=None, rownorm_eps=None,
-               split_k=0):
-    """v = a @ weight^T + bias; xt += dt * v (fp32, in place); xt_bf16 mirrors."""
+               split_k=0, bias_f32=None, rtc_lock=None, rtc_period=0,
+               rtc_prev=None, rtc_cw=None, rtc_omt=0.0):
+    """v = a @ weight^T + bias; xt += dt * v (fp32, in place); xt_bf16 mirrors.
+    Real-time chunking (see fvx_gemm_desc): rows with m % rtc_period <
+    rtc_lock store rtc_prev (prefix method); with ``rtc_cw`` every row adds
+    rtc_cw[m % rtc_period] * (rtc_prev - xt + rtc_omt * v) (guidance)."""
     d = _gemm_desc(a, weight)
     _check(xt, 'xt', dtype=torch.float32, contiguous=False)
     d.mode = _lib.GEMM_EULER
@@ -523,9 +572,13 @@ def gemm_euler(a, weight, bias, xt, dt, xt_bf16=None, rownorm_eps=None,
     if bias is not None:
         _check(bias, 'bias')
         d.bias = bias.data_ptr()
+    if bias_f32 is not None:
+        _check(bias_f32, 'bias_f32', dtype=torch.float32)
+        d.bias_f32 = bias_f32.data_ptr()
     d.dt = float(dt)
     if rownorm_eps is not None:
         d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
+    _set_rtc(d, rtc_lock, rtc_period, prev=rtc_prev, cw=rtc_cw, omt=rtc_omt)
     d.split_k = split_k
     _run_gemm(d)
 

@@ -19,6 +19,7 @@ import math
 import torch
 
 from . import kernels as K
+from . import rtc as R
 from ._lib import ACT_GELU_TANH, ACT_SILU
 from .config import PI0Config
 
@@ -310,24 +311,28 @@ class PI0Inference:
                         self.exp.pop('final_scale')[None]).to(BF16)
         self.act_out = out
         self.times, self.dt = euler_times(cfg.num_steps)
-        temb = sinusoid(self.times, cfg.proj_width).to(BF16).to(dev)
+        self._rtc_omt = R.guidance_omt(self.times)
+        # the last row is time 0: the positions real-time chunking locks
+        temb = sinusoid(self.times + [0.0], cfg.proj_width).to(BF16).to(dev)
         w = cfg.proj_width
         if cfg.pi05:
             tin = prepare_projector(sd, 'time_mlp_in', dev)
             tout = prepare_projector(sd, 'time_mlp_out', dev)
             h = K.gemm(temb, tin['w'], bias=tin['b'], act=ACT_SILU)
-            self.cond = K.gemm(h, tout['w'], bias=tout['b'], act=ACT_SILU)
+            cond = K.gemm(h, tout['w'], bias=tout['b'], act=ACT_SILU)
             # adaRMS style rows depend only on (step, layer): precomputed once
             styles = []
             for L in self.exp['layers']:
-                styles.append(K.gemm(self.cond, L['attn_mod_w'],
+                styles.append(K.gemm(cond, L['attn_mod_w'],
                                      bias=L['attn_mod_b']))
-                styles.append(K.gemm(self.cond, L['ffn_mod_w'],
+                styles.append(K.gemm(cond, L['ffn_mod_w'],
                                      bias=L['ffn_mod_b']))
-            styles.append(K.gemm(self.cond, self.exp['final_mod_w'],
+            styles.append(K.gemm(cond, self.exp['final_mod_w'],
                                  bias=self.exp['final_mod_b']))
-            # [steps, 2 * layers + 1, 3 * width]
-            self.styles = torch.stack(styles, 1).contiguous()
+            # [steps, 2 * layers + 1, 3 * width], and the time-0 rows
+            styles = torch.stack(styles, 1)
+            self.styles = styles[:-1].contiguous()
+            self.styles0 = styles[-1].contiguous()
         else:
             self.state = prepare_projector(sd, 'state_proj', dev)
             mi = prepare_projector(sd, 'action_time_mlp_in', dev)
@@ -336,7 +341,9 @@ class PI0Inference:
             # time_emb @ Wt^T: the time half is a per-step fp32 bias.
             self.mlp_in_a = mi['w'][:, :w].contiguous()
             wt = mi['w'][:, w:].contiguous()
-            self.step_bias = K.gemm(temb, wt, bias=mi['b'], out_f32=True)
+            bias = K.gemm(temb, wt, bias=mi['b'], out_f32=True)
+            self.step_bias = bias[:-1].contiguous()
+            self.step_bias0 = bias[-1].contiguous()
             self.mlp_out = mo
         self.rope = K.rope_table(cfg.prefix_len + cfg.suffix_len + 8,
                                  cfg.head_dim, cfg.rope_theta, device=dev)
@@ -500,6 +507,13 @@ class PI0Inference:
             'xt': e(B, cfg.n_action_steps, cfg.max_action_dim,
                     dt=torch.float32),
             'xt_bf16': e(B, cfg.n_action_steps, cfg.max_action_dim),
+            # real-time chunking: locked prefix length, the previous chunk
+            # (zero rows past its length) and the guidance weights per step
+            'rtc_lock': e(1, dt=torch.int32),
+            'rtc_prev': e(B, cfg.n_action_steps, cfg.max_action_dim,
+                          dt=torch.float32),
+            'rtc_cw': e(len(self.times), cfg.n_action_steps,
+                        dt=torch.float32),
         }
         self._bufs[B] = b
         return b
@@ -643,7 +657,7 @@ class PI0Inference:
                      rownorm_eps=cfg.rms_eps)
         K.gemm(b['ex_h'], L['down_w'], out=x, residual=x)
 
-    def _expert_layer_pi05(self, b, B, i, L, step):
+    def _expert_layer_pi05(self, b, B, i, L, step, rtc=None):
         cfg = self.cfg
         pf = None
         if self._frag_ok(B):
@@ -655,8 +669,12 @@ class PI0Inference:
         xn, gate = b['ex_xn'].view(B * Ss, hid), b['ex_gate'].view(B * Ss, hid)
         kc, vc = b['kc'][i], b['vc'][i]
         st = self.styles[step]
+        # prefix RTC: locked positions are conditioned on time 0
+        lk = ({'lock': b['rtc_lock'], 'lock_period': Ss}
+              if rtc == 'prefix' else {})
         K.adarms_norm(x, st[2 * i:2 * i + 1], out=xn, gate_out=gate,
-                      eps=cfg.rms_eps)
+                      eps=cfg.rms_eps,
+                      style_locked=self.styles0[2 * i] if lk else None, **lk)
         K.gemm_qkv_rope(xn, L['qkv_w'], self.rope, b['pos_suf'],
                         b['ex_q'].view(B * Ss, -1), kc.view(B * T, D)[S:],
                         vc[:, :, S:], cfg.heads, D, row_group=Ss,
@@ -667,16 +685,19 @@ class PI0Inference:
         K.gemm(b['ex_ctx'].view(B * Ss, -1), L['o_w'], out=x, residual=x,
                gate=gate)
         K.adarms_norm(x, st[2 * i + 1:2 * i + 2], out=xn, gate_out=gate,
-                      eps=cfg.rms_eps)
+                      eps=cfg.rms_eps,
+                      style_locked=self.styles0[2 * i + 1] if lk else None,
+                      **lk)
         K.gemm_geglu(xn, L['gate_w'], L['up_w'], out=b['ex_h'])
         K.gemm(b['ex_h'], L['down_w'], out=x, residual=x, gate=gate)
 
-    def transformer_decoder(self, b, B):
+    def transformer_decoder(self, b, B, rtc=None):
         """The Euler loop of the action expert
         (pi05_flowmatching_inference.py:155-312 / pi0_flowmatching.py:
         642-649, 787-831): suffix embedding, expert layers against the
         cached prefix K/V, final norm + action_out_proj + Euler update fused
-        in one GEMM epilogue."""
+        in one GEMM epilogue.  ``rtc``: None, 'prefix' or 'guidance' (real-
+        time chunking, pi0_flowmatching.py:651-700; see fluxvla_amd.rtc)."""
         cfg = self.cfg
         Ss, na, hid = cfg.suffix_len, cfg.n_action_steps, cfg.exp_hidden
         x3 = b['ex_x']
@@ -694,8 +715,12 @@ class PI0Inference:
                        bias=self.act_in['b'])
             else:
                 K.gemm(xt_b, w_in, out=b['act_h1'], bias=self.act_in['b'])
+                # prefix RTC: locked positions take the time-0 embedding
+                lk = ({'rtc_lock': b['rtc_lock'], 'rtc_period': na,
+                       'bias_f32_locked': self.step_bias0}
+                      if rtc == 'prefix' else {})
                 K.gemm(b['act_h1'], w_mi, out=b['act_h2'],
-                       bias_f32=self.step_bias[step], act=ACT_SILU)
+                       bias_f32=self.step_bias[step], act=ACT_SILU, **lk)
                 K.gemm(b['act_h2'], w_mo,
                        out=x3.view(B * Ss, hid)[1:], bias=self.mlp_out['b'],
                        row_group=na, row_group_stride=Ss)
@@ -705,7 +730,7 @@ class PI0Inference:
                     K.pack_frag(x3.view(Ss, hid), b['ex_xf'].rows(Ss))
             for i, L in enumerate(self.exp['layers']):
                 if cfg.pi05:
-                    self._expert_layer_pi05(b, B, i, L, step)
+                    self._expert_layer_pi05(b, B, i, L, step, rtc)
                 else:
                     self._expert_layer_pi0(b, B, i, L)
             lead = Ss - na
@@ -714,19 +739,34 @@ class PI0Inference:
                 if cfg.pi05:
                     xn = b['ex_xn'][s, lead:]
                     st = self.styles[step, -1:]
-                    K.adarms_norm(a, st, out=xn, eps=cfg.rms_eps)
+                    lk = ({'style_locked': self.styles0[-1],
+                           'lock': b['rtc_lock'], 'lock_period': na}
+                          if rtc == 'prefix' else {})
+                    K.adarms_norm(a, st, out=xn, eps=cfg.rms_eps, **lk)
                     a, rn = xn, None
                 else:
                     rn = cfg.rms_eps
                 K.gemm_euler(a, self.act_out_f, self.act_out['b'],
                              b['xt'][s], self.dt, xt_bf16=b['xt_bf16'][s],
-                             rownorm_eps=rn)
+                             rownorm_eps=rn, **self._euler_rtc(b, s, step, rtc))
 
-    def _run(self, B):
+    def _euler_rtc(self, b, s, step, rtc):
+        """Real-time chunking arguments of sample s's Euler GEMM."""
+        na = self.cfg.n_action_steps
+        if rtc == 'prefix':
+            return {'rtc_lock': b['rtc_lock'], 'rtc_period': na,
+                    'rtc_prev': b['rtc_prev'][s]}
+        if rtc == 'guidance':
+            return {'rtc_period': na, 'rtc_prev': b['rtc_prev'][s],
+                    'rtc_cw': b['rtc_cw'][step],
+                    'rtc_omt': self._rtc_omt[step]}
+        return {}
+
+    def _run(self, B, rtc=None):
         b = self._buffers(B)
         self.vision_encoder(b, B)
         self.transformer_encoder(b, B)
-        self.transformer_decoder(b, B)
+        self.transformer_decoder(b, B, rtc)
 
     # -- request staging (_triton_forward, :486-512) ---------------------------
     @torch.no_grad()
@@ -762,15 +802,47 @@ class PI0Inference:
         b['xt'].copy_(noise, non_blocking=True)
         b['xt_bf16'].copy_(noise, non_blocking=True)
 
-    def _capture(self, B):
+    def _stage_rtc(self, b, rtc, prev, prefix_len, rtc_config):
+        """Real-time chunking inputs: the previous chunk (zero rows past its
+        length), and either the locked prefix length with the locked rows of
+        x_t replaced (prefix, pi0_flowmatching.py:651-669) or the per-step
+        guidance weights (guidance, :671-700)."""
+        if rtc is None:
+            return
+        cfg, na = self.cfg, self.cfg.n_action_steps
+        prev = R.pad_prev_actions(prev.to(self.device, torch.float32),
+                                  cfg.max_action_dim, cfg.ori_action_dim)
+        B, L = b['xt'].shape[0], prev.shape[1]
+        if prev.shape[0] != B:
+            raise ValueError(f'prev_actions has batch {prev.shape[0]}, '
+                             f'the request {B}')
+        if rtc == 'prefix':
+            lock = min(prefix_len, na)
+            if L < lock:
+                raise ValueError(f'prefix_len {prefix_len} needs {lock} rows '
+                                 f'of prev_actions, got {L}')
+            b['rtc_prev'].zero_()
+            b['rtc_prev'][:, :lock].copy_(prev[:, :lock])
+            b['rtc_lock'].fill_(lock)
+            b['xt'][:, :lock].copy_(prev[:, :lock])
+            b['xt_bf16'][:, :lock].copy_(prev[:, :lock])
+        else:
+            if L > na:
+                raise ValueError(f'prev_actions has {L} rows, the chunk {na}')
+            b['rtc_prev'].zero_()
+            b['rtc_prev'][:, :L].copy_(prev)
+            b['rtc_cw'].copy_(R.guidance_cw(self.times, self.dt, na,
+                                            prefix_len, L, rtc_config))
+
+    def _capture(self, B, rtc=None):
         g = torch.cuda.CUDAGraph()
         stream = torch.cuda.Stream(device=self.device)
         stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(stream):
-            self._run(B)  # warm-up on the capture stream
+            self._run(B, rtc)  # warm-up on the capture stream
             torch.cuda.synchronize(self.device)
             g.capture_begin()
-            self._run(B)
+            self._run(B, rtc)
             g.capture_end()
         torch.cuda.current_stream(self.device).wait_stream(stream)
         torch.cuda.synchronize(self.device)
@@ -779,7 +851,11 @@ class PI0Inference:
     @torch.no_grad()
     def predict_action(self, images, lang_tokens, states, img_masks=None,
                        lang_masks=None, past_key_values=None, noise=None,
-                       *args, **kwargs):
+                       prev_actions=None, prefix_len: int = 0,
+                       rtc_config: dict = None, *args, **kwargs):
+        """The reference signature (pi0_flowmatching.py:702-715), real-time
+        chunking included: with prev_actions, prefix_len > 0 and rtc_config
+        the loop is the 'prefix' (default) or 'guidance' method."""
         cfg = self.cfg
         B = images.shape[0]
         if B > self.max_batch:
@@ -787,16 +863,22 @@ class PI0Inference:
         if noise is None:
             noise = torch.randn(B, cfg.n_action_steps, cfg.max_action_dim,
                                 device=self.device)
+        rtc = R.select_method(prev_actions, prefix_len, rtc_config)
         b = self._buffers(B)
-        self._stage(b, images, lang_tokens, states, img_masks, lang_masks,
-                    noise)
+
+        def stage():
+            self._stage(b, images, lang_tokens, states, img_masks, lang_masks,
+                        noise)
+            self._stage_rtc(b, rtc, prev_actions, prefix_len, rtc_config)
+
+        stage()
         if self.use_graph:
-            g = self._graphs.get(B)
+            key = B if rtc is None else (B, rtc)
+            g = self._graphs.get(key)
             if g is None:
-                g = self._graphs[B] = self._capture(B)
-                self._stage(b, images, lang_tokens, states, img_masks,
-                            lang_masks, noise)
+                g = self._graphs[key] = self._capture(B, rtc)
+                stage()
             g.replay()
         else:
-            self._run(B)
+            self._run(B, rtc)
         return b['xt'].clone()

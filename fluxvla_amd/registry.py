@@ -61,6 +61,7 @@ def config_from_reference(cfg: dict, num_views=None, max_prompt_len=None):
         proj_width=cfg.get('proj_width', 1024),
         n_action_steps=cfg.get('n_action_steps', 50),
         max_action_dim=cfg.get('max_action_dim', 32),
+        ori_action_dim=cfg.get('ori_action_dim'),
         num_steps=cfg.get('num_steps', 10), pi05=pi05)
     if not pi05 and cfg.get('state_proj'):
         kw['state_dim'] = cfg['state_proj']['in_dim']

@@ -60,7 +60,8 @@ enum fvx_act { FVX_ACT_NONE = 0, FVX_ACT_SILU = 1, FVX_ACT_GELU_TANH = 2 };
  * followed by the fused epilogue, applied in this order:
  *   v = acc
  *   v *= rsqrt(mean_k(A[m][k]^2) + rownorm_eps)      if rownorm
- *   v += bias[n] (bf16) ; v += bias_f32[n] (fp32)    if given
+ *   v += bias[n] (bf16) ; v += bias_f32[n] (fp32)    if given (locked RTC
+ *        rows: bias_f32_locked[n], see below)
  *   v = act(v)
  *   v *= gate[(m / gate_group) * ldg + n]            if gate
  *   v += residual[orow(m) * ldr + n]                 if residual (may alias c)
@@ -169,6 +170,31 @@ typedef struct fvx_gemm_desc {
   /* with b_fp8: 0 = bf16 activations (W8A16), 1 = e4m3 activations (W8A8);
    * see b_fp8 above.  a8 is read only by W8A8 GEMMs. */
   int32_t fp8_act;
+  /* Real-time chunking (RTC) of the Euler loop.  Replaces the per-step
+   * tensor updates of PI0FlowMatching._predict_action_prefix_rtc and
+   * _predict_action_guidance_rtc (fluxvla/models/vlas/pi0_flowmatching.py:
+   * 651-700) and apply_rtc_guidance without VJP
+   * (fluxvla/engines/utils/rtc_guidance.py:107-155).
+   * Row m is "locked" when rtc_lock is given and (m % rtc_period) <
+   * *rtc_lock (a device int32, so one captured graph serves every prefix
+   * length):
+   *   PLAIN, EULER: locked rows add bias_f32_locked instead of bias_f32
+   *     (the prefix method gives locked positions time 0);
+   *   EULER with rtc_prev: locked rows store rtc_prev[m * ld_prev + n].
+   * EULER with rtc_cw (guidance method): every row stores
+   *     xt + dt * v + rtc_cw[m % rtc_period]
+   *                   * (rtc_prev[m * ld_prev + n] - xt + rtc_omt * v)
+   *   (rtc_cw[r] = -dt * guidance weight * prefix weight of row r, 0 for rows
+   *   without guidance; rtc_prev then needs all m rows).
+   * rtc_period > 0 is required with any of these.  All zero / NULL: the
+   * plain epilogues above. */
+  const int32_t* rtc_lock;
+  int64_t rtc_period;
+  const float* bias_f32_locked;    /* [n] fp32 */
+  const float* rtc_prev;           /* fp32, row stride ld_prev */
+  int64_t ld_prev;
+  const float* rtc_cw;             /* [rtc_period] fp32 */
+  float rtc_omt;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */
@@ -229,6 +255,20 @@ int fvx_adarms_norm(const void* x, const void* style, void* out,
                     void* gate_out, int64_t rows, int64_t cols,
                     int64_t rows_per_style, int64_t style_stride, float eps,
                     void* stream);
+
+/* fvx_adarms_norm with per-position conditioning for the prefix method of
+ * real-time chunking: rows with (row % lock_period) < *lock (device int32)
+ * take their [scale | shift | gate] from the single row style_locked (the
+ * conditioning at time 0) instead of style.  Replaces the per-position
+ * adarms_cond of PI05FlowMatching.embed_suffix with a [B, T] timestep
+ * (fluxvla/models/vlas/pi05_flowmatching.py:68-127,
+ * condition_gemma.py:126-145) under _predict_action_prefix_rtc
+ * (pi0_flowmatching.py:651-669). */
+int fvx_adarms_norm_locked(const void* x, const void* style,
+                           const void* style_locked, const int32_t* lock,
+                           int64_t lock_period, void* out, void* gate_out,
+                           int64_t rows, int64_t cols, int64_t rows_per_style,
+                           int64_t style_stride, float eps, void* stream);
 
 /*
  * Fused multi-query attention: softmax(Q K^T * scale + mask) V, flash-style

@@ -10,6 +10,8 @@ It restates the reference's eager PyTorch path, which the reference itself
 uses as PI0's only inference path (BaseVLA -> PI0FlowMatching.predict_action):
 
   predict_action   fluxvla/models/vlas/pi0_flowmatching.py:702-785, 642-649
+  RTC loops        pi0_flowmatching.py:651-700,
+                   fluxvla/engines/utils/rtc_guidance.py:28-155 (no VJP)
   embed_prefix     pi0_flowmatching.py:204-250
   embed_suffix     pi0_flowmatching.py:252-321 (PI0),
                    fluxvla/models/vlas/pi05_flowmatching.py:68-127 (PI0.5)
@@ -358,11 +360,141 @@ def denoise_step(P, cfg, states, prefix_pad, kvs, x_t, timestep):
                   P['action_out_proj.projector.bias'])
 
 
+# ---------------------------------------------------------------------------
+# Euler loops: plain and real-time chunking (RTC)
+# ---------------------------------------------------------------------------
+def euler_plain(x_t, denoise, bsize, dt):
+    """_predict_action_plain (pi0_flowmatching.py:642-649)."""
+    time = torch.tensor(1.0, dtype=torch.float32)
+    while time >= -dt / 2:
+        v_t = denoise(x_t, time.expand(bsize))
+        x_t += dt * v_t
+        time += dt
+    return x_t
+
+
+def euler_prefix_rtc(x_t, denoise, bsize, dt, prev_actions, prefix_len,
+                     n_action_steps):
+    """_predict_action_prefix_rtc (pi0_flowmatching.py:651-669): the first
+    prefix_len positions are overwritten with the previous chunk before
+    every denoise call and at the end, and are denoised at time 0 (clean)."""
+    time = torch.tensor(1.0, dtype=torch.float32)
+    prefix_mask = torch.zeros(bsize, n_action_steps, dtype=torch.bool)
+    prefix_mask[:, :prefix_len] = True
+    while time >= -dt / 2:
+        t_batch = time.expand(bsize)
+        x_t[:, :prefix_len] = prev_actions[:, :prefix_len]
+        t_pos = t_batch.unsqueeze(1).expand(-1, n_action_steps).clone()
+        t_pos[prefix_mask] = 0.0
+        v_t = denoise(x_t, t_pos)
+        x_t += dt * v_t
+        time += dt
+    x_t[:, :prefix_len] = prev_actions[:, :prefix_len]
+    return x_t
+
+
+def compute_prefix_weights(n_action_steps, prefix_len, decay_end,
+                           schedule='exp'):
+    """compute_prefix_weights (fluxvla/engines/utils/rtc_guidance.py:28-80):
+    1 on the locked prefix, then a decay to decay_end ('exp': exp(-3 f),
+    'linear': 1 - f, 'ones', 'zeros'; f from 0 to 1 over the decay)."""
+    weights = torch.zeros(n_action_steps)
+    if prefix_len <= 0:
+        return weights
+    weights[:min(prefix_len, n_action_steps)] = 1.0
+    if decay_end > prefix_len:
+        decay_len = decay_end - prefix_len
+        for i in range(decay_len):
+            pos = prefix_len + i
+            if pos >= n_action_steps:
+                break
+            frac = i / max(decay_len - 1, 1)
+            if schedule == 'exp':
+                weights[pos] = math.exp(-3.0 * frac)
+            elif schedule == 'linear':
+                weights[pos] = 1.0 - frac
+            elif schedule == 'ones':
+                weights[pos] = 1.0
+            elif schedule == 'zeros':
+                weights[pos] = 0.0
+            else:
+                raise ValueError(f'Unknown schedule: {schedule}')
+    return weights
+
+
+def compute_guidance_weight(t, max_guidance_weight):
+    """compute_guidance_weight (rtc_guidance.py:83-104), t in [0, 1] with
+    0 = noise: min((1-t)/t * (t^2 + (1-t)^2) / (1-t)^2, max), in double."""
+    eps = 1e-6
+    t_clamped = max(t, eps)
+    one_minus_t = max(1.0 - t, eps)
+    inv_r2 = (t_clamped**2 + one_minus_t**2) / (one_minus_t**2)
+    c = one_minus_t / t_clamped
+    return min(c * inv_r2, max_guidance_weight)
+
+
+def apply_rtc_guidance(x_t, denoise_fn, prev_actions, prefix_weights, t,
+                       max_guidance_weight):
+    """apply_rtc_guidance without VJP (rtc_guidance.py:107-155): v + gw *
+    w * (prev - x_1) on the first L_prev positions, x_1 = x_t + v (1 - t)."""
+    eps = 1e-6
+    one_minus_t = max(1.0 - t, eps)
+    w = prefix_weights[None, :, None]
+    gw = compute_guidance_weight(t, max_guidance_weight)
+    v_t = denoise_fn(x_t)
+    x_1 = x_t + v_t * one_minus_t
+    L_prev = prev_actions.shape[1]
+    error_full = torch.zeros_like(x_1)
+    if L_prev:
+        error_full[:, :L_prev] = (prev_actions - x_1[:, :L_prev]) * w[:, :L_prev]
+    return v_t + gw * error_full
+
+
+def euler_guidance_rtc(x_t, denoise, bsize, dt, prev_actions, prefix_len,
+                       rtc_config, n_action_steps):
+    """_predict_action_guidance_rtc (pi0_flowmatching.py:671-700) with
+    use_vjp False: the guidance works in the 0 = noise time convention, so
+    the model velocity enters negated."""
+    if rtc_config.get('use_vjp', False):
+        raise NotImplementedError('guidance RTC with use_vjp')
+    prefix_weights = compute_prefix_weights(
+        n_action_steps, prefix_len, rtc_config.get('decay_end', prefix_len * 2),
+        rtc_config.get('schedule', 'exp'))
+    max_gw = rtc_config.get('max_guidance_weight', 5.0)
+    time = torch.tensor(1.0, dtype=torch.float32)
+    while time >= -dt / 2:
+        t_batch = time.expand(bsize)
+        v_fm = apply_rtc_guidance(x_t, lambda x: -denoise(x, t_batch),
+                                  prev_actions, prefix_weights,
+                                  1.0 - time.item(), max_gw)
+        x_t += dt * (-v_fm)
+        time += dt
+    return x_t
+
+
+def rtc_inputs(cfg, prev_actions, prefix_len, rtc_config):
+    """predict_action's RTC selection (pi0_flowmatching.py:747-756): prev
+    padded to max_action_dim when ori_action_dim is set; the method is
+    rtc_config['method'] (default 'prefix') when prev_actions, prefix_len > 0
+    and rtc_config are all given, else None (plain loop)."""
+    if (prev_actions is not None and cfg.ori_action_dim is not None
+            and prev_actions.shape[-1] < cfg.max_action_dim):
+        prev_actions = F.pad(prev_actions,
+                             (0, cfg.max_action_dim - prev_actions.shape[-1]),
+                             value=0.0)
+    method = None
+    if prev_actions is not None and prefix_len > 0 and rtc_config:
+        method = rtc_config.get('method', 'prefix')
+    return prev_actions, method
+
+
 @torch.no_grad()
 def predict_action(P, cfg, images, lang_tokens, states, img_masks=None,
-                   lang_masks=None, noise=None, num_steps=None):
-    """PI0FlowMatching.predict_action without RTC (pi0_flowmatching.py:
-    702-785, plain Euler loop :642-649), all on the CPU in fp32."""
+                   lang_masks=None, noise=None, num_steps=None,
+                   prev_actions=None, prefix_len=0, rtc_config=None):
+    """PI0FlowMatching.predict_action (pi0_flowmatching.py:702-785): prefix
+    cache, then the plain, prefix-RTC or guidance-RTC Euler loop, all on the
+    CPU in fp32."""
     B = images.shape[0]
     if img_masks is None:
         img_masks = torch.ones(B, images.shape[1] // 3, dtype=torch.bool)
@@ -372,11 +504,19 @@ def predict_action(P, cfg, images, lang_tokens, states, img_masks=None,
                                      lang_masks)
     steps = cfg.num_steps if num_steps is None else num_steps
     dt = torch.tensor(-1.0 / steps, dtype=torch.float32)
+    if prev_actions is not None:
+        prev_actions = prev_actions.float()
+    prev_actions, method = rtc_inputs(cfg, prev_actions, prefix_len,
+                                      rtc_config)
     x_t = noise.float().clone()
-    time = torch.tensor(1.0, dtype=torch.float32)
-    while time >= -dt / 2:
-        v = denoise_step(P, cfg, states.float(), prefix_pad, kvs, x_t,
-                         time.expand(B))
-        x_t += dt * v
-        time += dt
-    return x_t
+
+    def denoise(x, t):
+        return denoise_step(P, cfg, states.float(), prefix_pad, kvs, x, t)
+
+    if method == 'prefix':
+        return euler_prefix_rtc(x_t, denoise, B, dt, prev_actions, prefix_len,
+                                cfg.n_action_steps)
+    if method == 'guidance':
+        return euler_guidance_rtc(x_t, denoise, B, dt, prev_actions,
+                                  prefix_len, rtc_config, cfg.n_action_steps)
+    return euler_plain(x_t, denoise, B, dt)

@@ -167,3 +167,58 @@ def test_fragment_major_layouts():
         off = (((r // 16) * (k // 32) + c // 32) * 64 + (c % 32) // 8 * 16 +
                r % 16) * 8 + c % 8
         assert pb[off].item() == w[r, c].item()
+
+
+# ---------------------------------------------------------------------------
+# Real-time chunking host tables (fluxvla_amd/rtc.py) against the oracle
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize('schedule', ['exp', 'linear', 'ones', 'zeros'])
+@pytest.mark.parametrize('prefix_len,decay_end', [(5, 10), (0, 10), (48, 60),
+                                                  (7, 7), (3, 4)])
+def test_rtc_prefix_weights_match_oracle(schedule, prefix_len, decay_end):
+    from fluxvla_amd import rtc as R
+    assert torch.equal(
+        R.compute_prefix_weights(50, prefix_len, decay_end, schedule),
+        O.compute_prefix_weights(50, prefix_len, decay_end, schedule))
+
+
+def test_rtc_guidance_cw_matches_oracle_update():
+    """One guidance step through the fused update x + dt v + cw (prev - x +
+    omt v) equals the oracle's apply_rtc_guidance step at every step."""
+    from fluxvla_amd import rtc as R
+    g = torch.Generator().manual_seed(3)
+    times, dt = P.euler_times(10)
+    rc = {'max_guidance_weight': 4.0, 'decay_end': 16, 'schedule': 'exp'}
+    L = 30
+    cw = R.guidance_cw(times, dt, 50, 6, L, rc)
+    omt = R.guidance_omt(times)
+    w = O.compute_prefix_weights(50, 6, 16, 'exp')
+    x = torch.randn(1, 50, 32, generator=g)
+    v = torch.randn(1, 50, 32, generator=g)
+    prev = torch.randn(1, L, 32, generator=g)
+    prev_pad = torch.zeros(1, 50, 32)
+    prev_pad[:, :L] = prev
+    for k, time in enumerate(times):
+        v_fm = O.apply_rtc_guidance(x, lambda z: -v, prev, w, 1.0 - time, 4.0)
+        ref = x + dt * (-v_fm)
+        got = x + dt * v + cw[k][None, :, None] * (prev_pad - x + omt[k] * v)
+        assert torch.allclose(got, ref, atol=1e-5), k
+    assert torch.equal(cw[:, L:], torch.zeros(10, 50 - L))
+
+
+def test_rtc_method_selection_and_padding():
+    from fluxvla_amd import rtc as R
+    prev = torch.ones(1, 5, 14)
+    assert R.select_method(prev, 3, {'enabled': True}) == 'prefix'
+    assert R.select_method(prev, 3, {'method': 'guidance'}) == 'guidance'
+    assert R.select_method(prev, 0, {'method': 'prefix'}) is None
+    assert R.select_method(None, 3, {'method': 'prefix'}) is None
+    assert R.select_method(prev, 3, None) is None
+    assert R.select_method(prev, 3, {'method': 'other'}) is None
+    with pytest.raises(NotImplementedError):
+        R.select_method(prev, 3, {'method': 'guidance', 'use_vjp': True})
+    p = R.pad_prev_actions(prev, 32, 14)
+    assert p.shape == (1, 5, 32) and torch.equal(p[..., 14:],
+                                                 torch.zeros(1, 5, 18))
+    with pytest.raises(ValueError):
+        R.pad_prev_actions(prev, 32, None)

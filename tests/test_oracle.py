@@ -555,3 +555,146 @@ def test_embed_prefix_language_scale_and_image_rows():
     want = (ids.float() / 64.0 * 8.0)[..., None].expand(-1, -1, cfg.llm_hidden)
     assert torch.allclose(embs[:, n_img:], want, atol=1e-6)   # sqrt(64) = 8
     assert not att.any() and pad.all()
+
+
+# ---------------------------------------------------------------------------
+# Real-time chunking (pi0_flowmatching.py:651-700, rtc_guidance.py:28-155)
+# ---------------------------------------------------------------------------
+def test_prefix_weights_closed_form():
+    """Locked prefix 1; the decay runs from 1 at prefix_len to its end value
+    at decay_end - 1 (exp: exp(-3), linear: 0); zero after decay_end."""
+    w = O.compute_prefix_weights(50, 5, 15, 'exp')
+    assert torch.equal(w[:5], torch.ones(5))
+    assert w[5].item() == 1.0
+    assert abs(w[14].item() - math.exp(-3.0)) < 1e-7
+    assert abs(w[10].item() - math.exp(-3.0 * 5 / 9)) < 1e-7
+    assert torch.equal(w[15:], torch.zeros(35))
+    assert torch.all(w[5:15][1:] < w[5:15][:-1])  # strictly decaying
+    lin = O.compute_prefix_weights(50, 5, 15, 'linear')
+    assert abs(lin[14].item()) < 1e-7 and abs(lin[8].item() - 2 / 3) < 1e-7
+    assert torch.equal(O.compute_prefix_weights(50, 5, 15, 'ones')[:15],
+                       torch.ones(15))
+    z = O.compute_prefix_weights(50, 5, 15, 'zeros')
+    assert torch.equal(z, torch.cat([torch.ones(5), torch.zeros(45)]))
+    # no prefix: all zero; decay clipped at the chunk end; prefix clipped
+    assert torch.equal(O.compute_prefix_weights(50, 0, 10), torch.zeros(50))
+    assert O.compute_prefix_weights(10, 8, 20)[9].item() > 0
+    assert torch.equal(O.compute_prefix_weights(10, 12, 24), torch.ones(10))
+    # a one-long decay is weight 1 (f = 0)
+    assert O.compute_prefix_weights(50, 5, 6, 'exp')[5].item() == 1.0
+    with pytest.raises(ValueError):
+        O.compute_prefix_weights(50, 5, 15, 'cosine')
+
+
+def test_guidance_weight_closed_form():
+    """(1-t)/t * (t^2 + (1-t)^2)/(1-t)^2: 2 at t = 1/2, 82/9 at t = 0.9,
+    capped by the maximum, and the maximum at t = 0 (pure noise)."""
+    assert abs(O.compute_guidance_weight(0.5, 100.0) - 2.0) < 1e-12
+    assert abs(O.compute_guidance_weight(0.9, 100.0) - 82.0 / 9.0) < 1e-9
+    assert O.compute_guidance_weight(0.9, 5.0) == 5.0
+    assert O.compute_guidance_weight(0.0, 5.0) == 5.0
+    assert abs(O.compute_guidance_weight(0.25, 100.0) -
+               3.0 * (0.0625 + 0.5625) / 0.5625) < 1e-12
+
+
+def _elementwise_denoiser(calls):
+    """v = -(x + t): rows are independent, time enters per position."""
+    def denoise(x, t):
+        calls.append((x.clone(), t.clone()))
+        tt = t[:, :, None] if t.dim() == 2 else t[:, None, None]
+        return -(x + tt)
+    return denoise
+
+
+def test_prefix_rtc_loop_contract():
+    """Every denoise call sees the previous chunk on the locked rows and time
+    0 there (the current time elsewhere); the result holds the previous
+    chunk on the locked rows and, on the others, what the plain loop gives
+    for a row-independent denoiser fed the same per-position times."""
+    g = torch.Generator().manual_seed(0)
+    B, T, D, p = 2, 50, 32, 7
+    noise = torch.randn(B, T, D, generator=g)
+    prev = torch.randn(B, 30, D, generator=g)
+    dt = torch.tensor(-0.1)
+    calls = []
+    out = O.euler_prefix_rtc(noise.clone(), _elementwise_denoiser(calls), B,
+                             dt, prev, p, T)
+    times = O.euler_times(10)
+    assert len(calls) == 10
+    for (x, t), time in zip(calls, times):
+        assert torch.equal(x[:, :p], prev[:, :p])
+        assert torch.equal(t[:, :p], torch.zeros(B, p))
+        assert torch.all(t[:, p:] == time)
+    assert torch.equal(out[:, :p], prev[:, :p])
+    # unlocked rows: x <- x + dt * -(x + time), a scalar recursion per value
+    x = noise[:, p:].clone()
+    for time in times:
+        x = x + dt * -(x + time)
+    assert torch.allclose(out[:, p:], x, atol=1e-6)
+
+
+def test_guidance_rtc_constant_velocity():
+    """Constant velocity c: the plain loop ends at noise - c, which is also
+    the clean-chunk estimate x_1 = x - time * c at every step.  Guided
+    towards exactly that chunk the correction vanishes; guided towards it
+    plus delta on a row of weight w, the distance to the target shrinks by
+    (1 + dt * gw_k * w) per step, a row of weight 0 keeps the plain result,
+    and rows past the previous chunk are not guided."""
+    g = torch.Generator().manual_seed(1)
+    B, T, D = 1, 50, 32
+    noise = torch.randn(B, T, D, generator=g)
+    c = torch.randn(B, T, D, generator=g)
+    dt = torch.tensor(-0.1)
+
+    def denoise(x, t):
+        return c.clone()
+
+    plain = noise - c
+    rc = {'method': 'guidance', 'max_guidance_weight': 5.0, 'decay_end': 12,
+          'schedule': 'linear'}
+    out = O.euler_guidance_rtc(noise.clone(), denoise, B, dt, plain.clone(), 4,
+                               rc, T)
+    assert torch.allclose(out, plain, atol=1e-5)
+    delta = torch.randn(B, 40, D, generator=g)
+    prev = plain[:, :40] + delta
+    out = O.euler_guidance_rtc(noise.clone(), denoise, B, dt, prev, 4, rc, T)
+    w = O.compute_prefix_weights(T, 4, 12, 'linear')
+    times = O.euler_times(10)
+    gws = [O.compute_guidance_weight(1.0 - tm, 5.0) for tm in times]
+    assert gws[0] == 5.0
+    for r in (0, 3, 6, 10, 20, 45):
+        f = 1.0
+        for gw in gws:
+            f *= 1.0 - 0.1 * gw * (w[r].item() if r < 40 else 0.0)
+        d = delta[:, r] if r < 40 else torch.zeros(B, D)
+        expect = plain[:, r] + d * (1.0 - f)
+        assert torch.allclose(out[:, r], expect, atol=1e-4), r
+    # gw is the maximum at both ends of the schedule and 2 at time 1/2
+    assert gws[-1] == 5.0 and abs(gws[5] - 2.0) < 1e-5
+    # a weight-1 row closes 1 - 0.5^2 * (1 - 0.1 * 4.25)^2 * ... of delta;
+    # with the sign of the correction flipped it would grow instead
+    assert (out[:, 0] - prev[:, 0]).abs().max() < 0.05 * delta[:, 0].abs().max()
+
+
+def test_guidance_without_previous_rows():
+    """A previous chunk with no rows guides nothing (rtc_guidance.py:142-144)."""
+    x = torch.randn(1, 50, 32)
+    v = torch.randn(1, 50, 32)
+    got = O.apply_rtc_guidance(x, lambda z: v.clone(), torch.zeros(1, 0, 32),
+                               torch.ones(50), 0.3, 5.0)
+    assert torch.equal(got, v)
+
+
+def test_rtc_method_selection():
+    """predict_action runs RTC only with prev_actions, prefix_len > 0 and a
+    config; shorter action dims are zero-padded with ori_action_dim."""
+    cfg = PI0Config(ori_action_dim=14)
+    prev = torch.ones(1, 5, 14)
+    p, m = O.rtc_inputs(cfg, prev, 3, {'method': 'guidance'})
+    assert m == 'guidance' and p.shape == (1, 5, 32)
+    assert torch.equal(p[..., 14:], torch.zeros(1, 5, 18))
+    assert O.rtc_inputs(cfg, prev, 3, {})[1] is None
+    assert O.rtc_inputs(cfg, prev, 0, {'method': 'prefix'})[1] is None
+    assert O.rtc_inputs(cfg, None, 3, {'method': 'prefix'})[1] is None
+    assert O.rtc_inputs(cfg, prev, 3, {'enabled': True})[1] == 'prefix'
+    assert O.rtc_inputs(PI0Config(), prev, 3, {})[0].shape[-1] == 14
