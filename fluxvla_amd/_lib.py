@@ -103,6 +103,24 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class ImageDesc(ctypes.Structure):
+    """Mirror of ``fvx_image_desc``."""
+    _fields_ = [
+        ('src', c_vp), ('src_u8', c_i32), ('src_hwc', c_i32),
+        ('n', c_i64), ('src_h', c_i64), ('src_w', c_i64),
+        ('src_img_stride', c_i64),
+        ('dst', c_vp), ('dst_h', c_i64), ('dst_w', c_i64),
+        ('dst_img_stride', c_i64),
+        ('rh', c_i64), ('rw', c_i64), ('off_y', c_i64), ('off_x', c_i64),
+        ('pad_value', c_f32),
+        ('filter', c_i32), ('round_u8', c_i32), ('swap_rb', c_i32),
+        ('pre_div', c_f32),
+        ('mean', c_f32 * 3), ('den', c_f32 * 3),
+    ]
+
+
+RESIZE_LINEAR, RESIZE_PIL_BILINEAR = 0, 1
+
 # name -> (restype, argtypes); the exact set declared by include/fluxvla_amd.h
 SIGNATURES = {
     'fvx_version': (c_i32, []),
@@ -128,6 +146,7 @@ SIGNATURES = {
     'fvx_pack_frag': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     'fvx_copy_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64,
                               c_i64, c_vp]),
+    'fvx_resize_normalize': (c_i32, [ctypes.POINTER(ImageDesc), c_vp]),
 }
 
 _lib = None

@@ -781,3 +781,46 @@ def rope_table(max_pos, head_dim, theta=10000.0, device=None):
     t = torch.stack([torch.cos(ph), torch.sin(ph)], dim=-1).contiguous()
     return t.to(device) if device is not None else t
 
+
+
+# ---------------------------------------------------------------------------
+# Camera-frame preprocessing
+# ---------------------------------------------------------------------------
+def resize_normalize(src, out, *, hwc, region=None, pad_value=0.0,
+                     filter=_lib.RESIZE_LINEAR, round_u8=False, swap_rb=False,
+                     mean=(0.0, 0.0, 0.0), den=(1.0, 1.0, 1.0), pre_div=1.0):
+    """n RGB images -> fp32 CHW planes ``out`` [n, 3, H, W] (a view with unit
+    plane strides; the image stride may be larger, e.g. one view of the
+    model's [B, 3 * views, H, W] buffer).  ``src``: uint8 or fp32 [n, h, w, 3]
+    (``hwc``) or [n, 3, h, w], contiguous per image.  ``region`` = (off_y,
+    off_x, rh, rw): where the resized picture goes, pad_value elsewhere
+    (default: the whole output).  out = (v / pre_div - mean[c]) / den[c]."""
+    if src.dtype not in (torch.uint8, torch.float32):
+        raise ValueError(f'src must be uint8 or fp32, got {src.dtype}')
+    if src.dim() != 4 or (src.shape[3] if hwc else src.shape[1]) != 3:
+        raise ValueError(f'src must be [n, h, w, 3] (hwc) or [n, 3, h, w], '
+                         f'got {tuple(src.shape)}')
+    _check(out, 'out', dtype=torch.float32, contiguous=False)
+    n = src.shape[0]
+    h, w = (src.shape[1], src.shape[2]) if hwc else (src.shape[2], src.shape[3])
+    if src.stride()[1:] != torch.empty(src.shape[1:]).stride():
+        raise ValueError('src images must be contiguous')
+    if (out.dim() != 4 or out.shape[0] != n or out.shape[1] != 3 or
+            out.stride(3) != 1 or out.stride(2) != out.shape[3] or
+            out.stride(1) != out.shape[2] * out.shape[3]):
+        raise ValueError('out must be [n, 3, H, W] with contiguous planes')
+    H, W = out.shape[2], out.shape[3]
+    off_y, off_x, rh, rw = region if region is not None else (0, 0, H, W)
+    d = _lib.ImageDesc()
+    d.src, d.src_u8, d.src_hwc = src.data_ptr(), int(src.dtype == torch.uint8), int(hwc)
+    d.n, d.src_h, d.src_w = n, h, w
+    d.src_img_stride = src.stride(0) if n > 1 else 3 * h * w
+    d.dst, d.dst_h, d.dst_w = out.data_ptr(), H, W
+    d.dst_img_stride = out.stride(0) if n > 1 else 3 * H * W
+    d.rh, d.rw, d.off_y, d.off_x = rh, rw, off_y, off_x
+    d.pad_value, d.filter = float(pad_value), int(filter)
+    d.round_u8, d.swap_rb, d.pre_div = int(round_u8), int(swap_rb), float(pre_div)
+    for c in range(3):
+        d.mean[c], d.den[c] = float(mean[c]), float(den[c])
+    _lib.call('fvx_resize_normalize', ctypes.byref(d), _stream())
+    return out

@@ -778,8 +778,14 @@ class PI0Inference:
         b['images'].copy_(images, non_blocking=True)
         L = lang_tokens.shape[1]
         if L > cfg.max_prompt_len:
-            raise ValueError(f'prompt of {L} tokens exceeds max_prompt_len='
-                             f'{cfg.max_prompt_len}')
+            # ProcessPrompts pads to its max_len (180 by default): padding
+            # past the buffer's prompt length carries no keys and is dropped
+            P = cfg.max_prompt_len
+            if lang_masks is None or bool(lang_masks[:, P:].any()):
+                raise ValueError(f'prompt of {L} tokens exceeds '
+                                 f'max_prompt_len={P}')
+            lang_tokens, lang_masks, L = (lang_tokens[:, :P],
+                                          lang_masks[:, :P], P)
         b['ids'].zero_()
         b['ids'][:, :L].copy_(lang_tokens, non_blocking=True)
         if img_masks is None:

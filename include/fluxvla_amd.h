@@ -374,6 +374,48 @@ int fvx_copy_rows(const void* src, int64_t src_ld, void* dst, int64_t dst_ld,
 int fvx_pack_frag(const void* src, int64_t src_ld, void* dst, int64_t rows,
                   int64_t cols, void* stream);
 
+/*
+ * Camera-frame preprocessing: resize + pad + normalize + channel reorder of n
+ * RGB images into fp32 CHW planes (the patch embedding's input).  Replaces the
+ * host transforms ResizeImages (cv2 INTER_LINEAR), ResizeImagesWithPad,
+ * NormalizeImages and TransformImage (PIL BILINEAR)
+ * (fluxvla/transforms/transform_images.py:80-200, 313-390, 414-560) and
+ * resize_with_pad (fluxvla/engines/utils/model_utils.py:98-120).
+ *
+ * dst pixel (y, x) of image i, channel c:
+ *   inside [off_y, off_y + rh) x [off_x, off_x + rw): the source resized to
+ *     rh x rw, sampled at (y - off_y, x - off_x), source channel c (2 - c
+ *     with swap_rb);
+ *   elsewhere: pad_value;
+ *   out = (v / pre_div - mean[c]) / den[c]   (fp32 division, as numpy does)
+ * Filters: LINEAR -- two-tap bilinear, half-pixel centres, edge clamp, fp32
+ *   (torch's bilinear interpolate with align_corners=False; OpenCV's
+ *   INTER_LINEAR up to its 11-bit weight rounding); round_u8 rounds the
+ *   resized value to uint8 as a uint8 resize returns it.
+ *   PIL_BILINEAR -- Pillow's antialiased BILINEAR resample (uint8 sources):
+ *   triangle filter widened by the downscale factor, 22-bit fixed-point
+ *   weights, horizontal then vertical pass, each rounded to uint8.
+ * Sources: uint8 or fp32 (LINEAR without rounding), interleaved [h][w][3]
+ * (src_hwc) or planar [3][h][w]; image i at src + i * src_img_stride
+ * elements, dst planes at dst + i * dst_img_stride elements.
+ */
+enum fvx_resize_filter { FVX_RESIZE_LINEAR = 0, FVX_RESIZE_PIL_BILINEAR = 1 };
+
+typedef struct fvx_image_desc {
+  const void* src;
+  int32_t src_u8, src_hwc;
+  int64_t n, src_h, src_w, src_img_stride;
+  float* dst;
+  int64_t dst_h, dst_w, dst_img_stride;
+  int64_t rh, rw, off_y, off_x;
+  float pad_value;
+  int32_t filter, round_u8, swap_rb;
+  float pre_div;
+  float mean[3], den[3];
+} fvx_image_desc;
+
+int fvx_resize_normalize(const fvx_image_desc* desc, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
