@@ -1358,11 +1358,13 @@ constexpr int kSkWaves = 8;
 // sets of loads in flight); bf16 and W8A16 (fp8 weights converted to bf16
 // in registers, A bf16): 8
 constexpr int sk_waves(bool f8, bool a16) { return f8 && !a16 ? 4 : kSkWaves; }
-constexpr int kSkStep = 3;    // MFMA steps (of 32 k) per register set (GEGLU: 2)
 // steps per register set: W8A8 one 128-k fp8 block; W8A16 one 16-byte half
-// of a lane's 32 weight bytes (2 steps; 4 spilled in the PLAIN kernel)
-constexpr int sk_steps(int nb, bool f8, bool a16) {
-  return f8 ? (a16 ? 2 : 4) : (nb == 2 ? 2 : kSkStep);
+// of a lane's 32 weight bytes (2 steps; 4 spilled in the PLAIN kernel);
+// bf16: as many 32-k steps as the registers hold with two sets in flight --
+// fewer activation row blocks per workgroup (rb) leave room for more
+constexpr int sk_steps(int nb, bool f8, bool a16, int rb) {
+  return f8 ? (a16 ? 2 : 4)
+            : (rb == 4 ? (nb == 2 ? 2 : 3) : rb == 2 ? (nb == 2 ? 3 : 4) : (nb == 2 ? 6 : 8));
 }
 // K granule of one wave's slice (a multiple of the register-set steps that
 // the weight layout needs: W8A8 a 128-k block, W8A16 a 64-k half)
@@ -1400,24 +1402,29 @@ __device__ __forceinline__ void sc1_load8(__amdgpu_buffer_rsrc_t r, int off,
   }
 }
 
-template <int MODE, bool F8, bool A16>
+template <int MODE, bool F8, bool A16, int RB>
 __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
                                                           int64_t kc,
                                                           int vec_ok) {
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
+  // RB activation row blocks of 16 per workgroup: row group blockIdx.z
+  // covers rows 16 RB z .. + 16 RB - 1 (fewer row blocks, more workgroups)
+  static_assert(RB == 4 || !F8 || A16, "W8A8 skinny GEMMs take all 4 row blocks");
+  constexpr int RR = 16 * RB;
   // W8A8: one register set = one 128-k step of the fp8 MFMA (4 A blocks of
   // 32); W8A16: S 32-k steps of bf16 MFMAs whose B fragments are converted
   // from 8 e4m3 bytes each (a 16-byte load holds two steps)
   static_assert(!A16 || F8, "W8A16 is an fp8-weight variant");
-  constexpr int W = sk_waves(F8, A16), S = sk_steps(NB, F8, A16);
-  __shared__ float sP[W][NB][64][16 + 1];
-  __shared__ float sS[W][64];
+  constexpr int W = sk_waves(F8, A16), S = sk_steps(NB, F8, A16, RB);
+  __shared__ float sP[W][NB][RR][16 + 1];
+  __shared__ float sS[W][RR];
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
-  const int tile = blockIdx.x, split = blockIdx.y;
+  const int tile = blockIdx.x, split = blockIdx.y, rg = blockIdx.z;
+  const int fb0 = rg * RB;  // first row block of the workgroup
   const int64_t M = p.m, N = p.n, K = p.k;
   const int64_t n0 = (int64_t)tile * 16;
   const int64_t n = n0 + fr;
@@ -1463,7 +1470,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   };
 
-  bf16x8 ra[2][S][4], rb[2][S][NB];
+  bf16x8 ra[2][S][RB], rb[2][S][NB];
   // unconditional loads: a masked-out fragment gets an offset past the view
   auto load = [&](int t0, int set) {
 #pragma unroll
@@ -1484,18 +1491,20 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
           rb[set][t][b] = bld(rb_rs[b], kin ? b0 + (ks0 + t0) * b_ks + 16 * t : kOOB);
       }
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        const bool rin = p.a_frag || f * 16 + fr < M;
-        ra[set][t][f] = bld(ra_rs, (kin && rin) ? a0 + ks * a_ks + f * a_f : kOOB);
+      for (int f = 0; f < RB; ++f) {
+        const bool rin = p.a_frag || (fb0 + f) * 16 + fr < M;
+        ra[set][t][f] = bld(ra_rs, (kin && rin) ? a0 + ks * a_ks + (fb0 + f) * a_f : kOOB);
       }
     }
   };
-  f32x4_t acc[NB][4];
+  f32x4_t acc[NB][RB];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int f = 0; f < 4; ++f) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < RB; ++f) acc[b][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[RB];
+#pragma unroll
+  for (int f = 0; f < RB; ++f) ss[f] = 0.f;
   auto compute = [&](int set) {
     if (A16) {
       // lane (fr, g) holds weight bytes k = 32 t + 8 g + j of column n0 + fr
@@ -1511,7 +1520,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
                                : e4m3x8_to_bf16(raw.w[2], raw.w[3]);
         }
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
+        for (int f = 0; f < RB; ++f) {
           if (p.rownorm) ss[f] += sumsq8(ra[set][t][f]);
 #pragma unroll
           for (int b = 0; b < NB; ++b) acc[b][f] = mfma16x16x32(ra[set][t][f], bw[b], acc[b][f]);
@@ -1524,7 +1533,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
       // row's 128 values of the step with one power-of-two scale, one fp8
       // MFMA per row block
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
+      for (int f = 0; f < RB; ++f) {
         const bf16x8 av[4] = {ra[set][0][f], ra[set][1][f], ra[set][2][f], ra[set][3][f]};
         if (p.rownorm)
 #pragma unroll
@@ -1547,7 +1556,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
 #pragma unroll
     for (int t = 0; t < S; ++t)
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
+      for (int f = 0; f < RB; ++f) {
         if (p.rownorm) ss[f] += sumsq8(ra[set][t][f]);
 #pragma unroll
         for (int b = 0; b < NB; ++b)
@@ -1557,11 +1566,13 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   if (nst > 0) load(0, 0);
   // The epilogue's reads (residual, gate, bias, RoPE table, Euler state) do
   // not depend on the product: issue them now so that their latency hides
-  // under the K loop.  Thread t < 128 owns row t / 2, columns n0 + 8 (t % 2).
-  const int row = (tid >> 1) & 63, half = tid & 1;
+  // under the K loop.  Thread t < 2 RR owns local row t / 2 (global row
+  // 16 fb0 + t / 2), columns n0 + 8 (t % 2).
+  const int lrow = (tid >> 1) & (RR - 1), half = tid & 1;
+  const int row = fb0 * 16 + lrow;
   const int64_t ncol = n0 + 8 * half;
   const int cnt = (int)(N - ncol < 8 ? N - ncol : 8);
-  const bool mine = tid < 128 && row < M && cnt > 0;
+  const bool mine = tid < 2 * RR && row < M && cnt > 0;
   const bool vec = vec_ok && cnt == 8;
   EpiIn in;
   if (mine) epi_load<MODE>(p, row, ncol, vec, cnt, in);
@@ -1579,16 +1590,16 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
     compute(1);
   }
 
-  // wave partials -> LDS; lane holds column fr, rows 16 f + 4 g + j
+  // wave partials -> LDS; lane holds column fr, local rows 16 f + 4 g + j
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+    for (int f = 0; f < RB; ++f)
 #pragma unroll
       for (int j = 0; j < 4; ++j) sP[wave][b][f * 16 + 4 * g + j][fr] = acc[b][f][j];
   if (p.rownorm) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < RB; ++f) {
       float v = ss[f];
       v += __shfl_xor(v, 16, 64);
       v += __shfl_xor(v, 32, 64);
@@ -1597,7 +1608,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   }
   __syncthreads();
 
-  // thread t < 128: row t / 2, columns n0 + 8 (t % 2) .. + 7
+  // thread t < 2 RR: local row t / 2, columns n0 + 8 (t % 2) .. + 7
   float v[8], u[8], rsum = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = u[e] = 0.f;
@@ -1606,10 +1617,10 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
     for (int w = 0; w < W; ++w) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        v[e] += sP[w][0][row][8 * half + e];
-        if (NB == 2) u[e] += sP[w][NB - 1][row][8 * half + e];
+        v[e] += sP[w][0][lrow][8 * half + e];
+        if (NB == 2) u[e] += sP[w][NB - 1][lrow][8 * half + e];
       }
-      if (p.rownorm) rsum += sS[w][row];
+      if (p.rownorm) rsum += sS[w][lrow];
     }
   }
 
@@ -1618,7 +1629,8 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
     constexpr int BLK = skinny_block_floats(NB);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (char*)p.workspace + kCounterBytes, 0, 0x7fffffff, 0x00020000);
-    const int base = (tile * splits + split) * BLK * 4;
+    const int cell = tile * (int)gridDim.z + rg;  // (column tile, row group)
+    const int base = (cell * splits + split) * BLK * 4;
     if (mine) {
       sc1_store8(rs, base + (row * 16 + 8 * half) * 4, v);
       if (NB == 2) sc1_store8(rs, base + ((64 + row) * 16 + 8 * half) * 4, u);
@@ -1630,7 +1642,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-      uint32_t* ctr = (uint32_t*)p.workspace + tile;
+      uint32_t* ctr = (uint32_t*)p.workspace + cell;
       const uint32_t old =
           __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int last = old == (uint32_t)(splits - 1);
@@ -1644,7 +1656,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
 #pragma unroll
     for (int s = 0; s < kSkMaxSplits; ++s) {
       if (s < splits) {
-        const int bs = (tile * splits + s) * BLK * 4;
+        const int bs = (cell * splits + s) * BLK * 4;
         sc1_load8(rs, bs + (row * 16 + 8 * half) * 4, tv[s]);
         if (NB == 2) sc1_load8(rs, bs + ((64 + row) * 16 + 8 * half) * 4, tu[s]);
         tr[s] = p.rownorm ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
@@ -1763,6 +1775,7 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
 // ---------------------------------------------------------------------------
 struct SkinnyPlan {
   int n_tiles, splits;
+  int rb, row_groups;  // activation row blocks per workgroup, row groups
   int64_t kc, ws_bytes;
 };
 
@@ -1776,9 +1789,28 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
   const int nb = d.mode == FVX_GEMM_GEGLU ? 2 : 1;
   s.n_tiles = (int)((d.n + 15) / 16);
   const bool f8 = d.b_fp8 != 0, a16 = f8 && !d.fp8_act;
+  // Fewer activation row blocks per workgroup spread a GEMM with few column
+  // tiles over more CUs with no K split: per-CU operand bytes, not HBM,
+  // bound these kernels (~115 GB/s per CU from L2).  The smallest row block
+  // count whose grid still fits one workgroup per CU wins; past 256
+  // workgroups the second round costs more than the narrower tiles save.
+  s.rb = 4;
+  if (!(f8 && !a16) && d.split_k <= 0) {
+    for (int rb = 1; rb < 4; rb *= 2) {
+      const int64_t groups = (d.m + 16 * rb - 1) / (16 * rb);
+      const int64_t bytes = (16 * rb * 2 + 16 * nb * (f8 ? 1 : 2)) * d.k;
+      if (s.n_tiles * groups <= 256 && bytes <= 400 * 1024) {
+        s.rb = rb;
+        break;
+      }
+    }
+  }
+  s.row_groups = (int)((d.m + 16 * s.rb - 1) / (16 * s.rb));
+  if (s.row_groups < 1) s.row_groups = 1;
   const int64_t unit = (int64_t)sk_kgran(f8, a16) * sk_waves(f8, a16);
   const int64_t max_splits = (d.k + unit - 1) / unit;
   int64_t sp = d.split_k;
+  if (sp <= 0 && s.rb < 4) sp = 1;
   if (sp <= 0) {
     const int64_t bytes = (64 * 2 + 16 * nb * (d.b_fp8 ? 1 : 2)) * d.k;
     sp = (bytes + 400 * 1024 - 1) / (400 * 1024);
@@ -1792,7 +1824,7 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
   kc = (kc + unit - 1) / unit * unit;
   s.splits = (int)((d.k + kc - 1) / kc);
   s.kc = kc;
-  s.ws_bytes = s.splits > 1 ? kCounterBytes + (int64_t)s.n_tiles * s.splits *
+  s.ws_bytes = s.splits > 1 ? kCounterBytes + (int64_t)s.n_tiles * s.row_groups * s.splits *
                                                    skinny_block_floats(nb) * 4
                              : 0;
   return s;
@@ -1808,7 +1840,7 @@ static bool use_skinny(const GemmArgs& d) {
   const int64_t a_bytes = d.a_frag ? (d.k / 32) * 4 * 1024 : 64 * d.lda * 2;
   const int64_t b_bytes = d.b_frag ? (int64_t)s.n_tiles * 16 * d.k * (d.b_fp8 ? 1 : 2)
                                    : (int64_t)s.n_tiles * 16 * d.ldb * 2;
-  return s.n_tiles <= kMaxSkinnyTiles && s.ws_bytes < ((int64_t)1 << 31) &&
+  return s.n_tiles * s.row_groups <= kMaxSkinnyTiles && s.ws_bytes < ((int64_t)1 << 31) &&
          a_bytes < ((int64_t)1 << 31) && b_bytes < ((int64_t)1 << 31);
 }
 
@@ -2214,18 +2246,30 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
                        (long long)d.workspace_bytes);
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "gemm: workspace must be 16B aligned");
-    dim3 grid((unsigned)sp.n_tiles, (unsigned)sp.splits);
+    dim3 grid((unsigned)sp.n_tiles, (unsigned)sp.splits, (unsigned)sp.row_groups);
     const int vec_ok = epi_vec_ok(d) ? 1 : 0;
 #define L(MODE)                                                                 \
   if (d.b_fp8 && d.fp8_act)                                                      \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, false>), grid,            \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, false, 4>), grid,         \
                        dim3(64 * sk_waves(true, false)), 0, s, d, sp.splits, sp.kc, vec_ok); \
-  else if (d.b_fp8)                                                              \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true>), grid,             \
+  else if (d.b_fp8 && sp.rb == 1)                                                \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 1>), grid,          \
                        dim3(64 * sk_waves(true, true)), 0, s, d, sp.splits, sp.kc, vec_ok); \
+  else if (d.b_fp8 && sp.rb == 2)                                                \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 2>), grid,          \
+                       dim3(64 * sk_waves(true, true)), 0, s, d, sp.splits, sp.kc, vec_ok); \
+  else if (d.b_fp8)                                                              \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 4>), grid,          \
+                       dim3(64 * sk_waves(true, true)), 0, s, d, sp.splits, sp.kc, vec_ok); \
+  else if (sp.rb == 1)                                                           \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 1>), grid,        \
+                       dim3(64 * kSkWaves), 0, s, d, sp.splits, sp.kc, vec_ok);  \
+  else if (sp.rb == 2)                                                           \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 2>), grid,        \
+                       dim3(64 * kSkWaves), 0, s, d, sp.splits, sp.kc, vec_ok);  \
   else                                                                           \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false>), grid, dim3(64 * kSkWaves), \
-                       0, s, d, sp.splits, sp.kc, vec_ok)
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 4>), grid,        \
+                       dim3(64 * kSkWaves), 0, s, d, sp.splits, sp.kc, vec_ok)
     FVX_MODE_DISPATCH(d.mode, L)
 #undef L
     return launch_status("gemm(skinny)");

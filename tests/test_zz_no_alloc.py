@@ -28,7 +28,7 @@ def _operands(m, n, k, seed, dev):
 
 @pytest.mark.parametrize('shape', [
     # (m, n, k), then the smaller second call
-    ((51, 1024, 4096), (20, 1024, 4096)),     # skinny, 2 K ranges
+    ((51, 1024, 8192), (20, 1024, 8192)),     # skinny, 4 K ranges
     ((300, 512, 8192), (272, 512, 8192)),     # wide kernel, 8 K ranges + reduce
 ])
 def test_noalloc_matches_workspace_gemm(cuda, shape):
