@@ -20,6 +20,11 @@ Also reported on the same JSON line:
                 PyTorch path) timed on this host: 1 warm-up + median of 3
                 chunks, and config 1 alone (median of 20);
   configs       BASELINE configs 4 and 5 (ms/chunk, actions/s, accuracy);
+  rtc           the same chunk with real-time chunking (prefix and guidance
+                methods, previous chunk of 30 rows, prefix 5);
+  serving       one predict_action request through the serving boundary
+                (three 480x640 JPEG frames, msgpack): host decode, device
+                preprocessing + chunk + device-to-host, reply encoding;
   parity        max abs error of the GPU chunk vs that CPU chunk.
 """
 import argparse
@@ -578,6 +583,96 @@ def other_configs(pi0_model, sd0, dev, parity=True):
     return rows, parity_res
 
 
+def rtc_times(model, dinp, steps=10):
+    """ms/chunk of the prefix and guidance RTC loops at bs=1 (each its own
+    captured graph), and the locked rows' exactness."""
+    import torch
+    g = torch.Generator().manual_seed(5)
+    prev = (torch.randn(1, 30, 32, generator=g) * 0.5).to(dinp['images'].device)
+    out = {}
+    for method in ('prefix', 'guidance'):
+        rc = {'enabled': True, 'method': method, 'max_guidance_weight': 5.0}
+
+        def step():
+            return model.predict_action(dinp['images'], dinp['lang_tokens'],
+                                        dinp['states'], dinp['img_masks'],
+                                        dinp['lang_masks'], noise=dinp['noise'],
+                                        prev_actions=prev, prefix_len=5,
+                                        rtc_config=rc)
+        for _ in range(2):
+            a = step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            a = step()
+        torch.cuda.synchronize()
+        out[method] = {'ms_per_chunk': round((time.perf_counter() - t0) * 1e3 / steps, 3)}
+        if method == 'prefix':
+            out[method]['locked_rows_exact'] = bool(torch.equal(a[:, :5], prev[:, :5]))
+    return out
+
+
+def serving_latency(model, cfg, dinp, reps=10):
+    """One predict_action request end to end through the serving boundary:
+    three 480x640 uint8 frames JPEG-encoded in a msgpack request; the
+    server decodes them (host), uploads the uint8 frames, preprocesses them
+    on the GPU (ResizeImages + NormalizeImages of the PI0 aloha config),
+    runs the chunk graph, copies the actions to the host and encodes the
+    reply.  Medians over ``reps`` requests."""
+    import numpy as np
+    import torch
+
+    from fluxvla_amd.preprocess import ImagePreprocessor
+    from fluxvla_amd.serving import serializers as S
+    from fluxvla_amd.serving.server import ObsToInputs, create_server
+    cams = ['cam_high', 'cam_left_wrist', 'cam_right_wrist']
+    g = torch.Generator().manual_seed(3)
+    obs = {c: torch.randint(0, 256, (480, 640, 3), generator=g,
+                            dtype=torch.uint8).numpy() for c in cams}
+    obs['state'] = dinp['states'][0].cpu().numpy()
+    obs['lang_tokens'] = dinp['lang_tokens'][0].cpu().numpy()
+    obs['lang_masks'] = dinp['lang_masks'][0].cpu().numpy()
+    means = [[123.515625, 116.04492188, 103.59375]] * 3
+    stds = [[58.27148438, 57.02636719, 57.27539062]] * 3
+    pre = ImagePreprocessor.from_transforms([
+        dict(type='ResizeImages', height=224, width=224),
+        dict(type='NormalizeImages', means=means, stds=stds)])
+    ds = ObsToInputs(cams, pre, device=dinp['images'].device,
+                     state_dim=cfg.state_dim)
+    srv = create_server(model, dataset=ds, device=str(dinp['images'].device),
+                        bind=False)
+    req = S.encode_predict_request(obs, '')
+    dec, handle, infer = [], [], []
+    for i in range(reps + 2):
+        t0 = time.perf_counter()
+        S.decode_predict_request(req)
+        t1 = time.perf_counter()
+        resp = S.decode_predict_response(srv.handle(req))
+        t2 = time.perf_counter()
+        if i >= 2:
+            dec.append((t1 - t0) * 1e3)
+            handle.append((t2 - t1) * 1e3)
+            infer.append(resp['infer_time'] * 1e3)
+    # the preprocessing kernels alone (3 views), HIP events
+    views = [torch.from_numpy(obs[c])[None].to(dinp['images'].device) for c in cams]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    pre(views)
+    e0.record()
+    for _ in range(20):
+        pre(views)
+    e1.record()
+    torch.cuda.synchronize()
+    med = lambda v: round(float(np.median(v)), 3)  # noqa: E731
+    return {'request_ms': med(handle), 'host_decode_ms': med(dec),
+            'predict_action_ms': med(infer),
+            'gpu_preprocess_us': round(e0.elapsed_time(e1) * 1e3 / 20, 2),
+            'request_bytes': len(req),
+            'note': 'request_ms = host JPEG/msgpack decode + uint8 upload + GPU '
+                    'preprocessing + chunk graph + actions to host + reply '
+                    'encoding; predict_action_ms = from the first device copy '
+                    'to the actions on the host'}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -592,6 +687,8 @@ def main():
     ap.add_argument('--no-configs', action='store_true',
                     help='skip the other BASELINE configs (PI0 bs 8, PI0.5 '
                     'fp8 bs 1/8/32)')
+    ap.add_argument('--no-serving', action='store_true',
+                    help='skip the RTC and serving-request timings')
     ap.add_argument('--kernel-only', action='store_true',
                     help='run only the dominant kernel + a calibration copy '
                     '(for rocprofv3 --pmc passes)')
@@ -675,6 +772,14 @@ def main():
         log(f"cpu {cpu['value']} ms on {cpu['cores']} threads; gpu vs cpu "
             f'max abs err {err:.3e}')
 
+    rtc, serving = None, None
+    if B == 1 and not args.no_serving:
+        log('real-time chunking and a served request')
+        rtc = rtc_times(model, dinp)
+        serving = serving_latency(model, cfg, dinp)
+        log(f'  rtc {rtc}')
+        log(f'  serving {serving}')
+
     configs, fp8_parity = None, None
     if B == 1 and not args.no_configs:
         log('other BASELINE configs')
@@ -714,6 +819,8 @@ def main():
             'chunk_max_abs_err_vs_cpu_oracle': err, 'tolerance': 2e-2},
         'configs': configs,
         'fp8_parity': fp8_parity,
+        'rtc': rtc,
+        'serving': serving,
     }
     print(json.dumps(res), flush=True)
 

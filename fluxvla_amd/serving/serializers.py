@@ -21,6 +21,7 @@ OpenCV client's stream means.
 """
 from __future__ import annotations
 import io
+from concurrent.futures import ThreadPoolExecutor
 from typing import Any
 
 import msgpack
@@ -58,6 +59,22 @@ def decode_image(data: bytes) -> np.ndarray:
     from PIL import Image
     img = Image.open(io.BytesIO(data)).convert('RGB')
     return np.ascontiguousarray(np.asarray(img)[:, :, ::-1])
+
+
+_POOL = None
+
+
+def decode_images(blobs: dict) -> dict:
+    """Decode several JPEG frames at once: the codec releases the GIL, so
+    the camera views decode on parallel host threads (the reference decodes
+    them one after another)."""
+    global _POOL
+    if len(blobs) < 2:
+        return {k: decode_image(v) for k, v in blobs.items()}
+    if _POOL is None:
+        _POOL = ThreadPoolExecutor(max_workers=4, thread_name_prefix='jpeg')
+    keys = list(blobs)
+    return dict(zip(keys, _POOL.map(decode_image, [blobs[k] for k in keys])))
 
 
 def encode_array(arr: np.ndarray) -> bytes:
@@ -122,16 +139,18 @@ class ObsSerializer:
 
     @staticmethod
     def from_bytes(data: bytes) -> dict:
-        obs = {}
+        obs, jpegs = {}, {}
         for k, v in msgpack.unpackb(data, raw=False).items():
             if isinstance(v, dict) and '__jpeg__' in v:
-                obs[k] = decode_image(v['data'])
+                jpegs[k] = v['data']
+                obs[k] = None  # keeps the key order
             elif isinstance(v, dict) and '__ndarray__' in v:
                 obs[k] = decode_array(v['data'])
             elif isinstance(v, bytes):
                 obs[k] = v.decode()
             else:
                 obs[k] = v
+        obs.update(decode_images(jpegs))
         return obs
 
 
@@ -205,7 +224,7 @@ class ObsSerializerProto:
 
     @staticmethod
     def obs_from_proto(msg) -> dict:
-        obs = {k: decode_image(v) for k, v in msg.images.items()}
+        obs = decode_images(dict(msg.images.items()))
         obs.update({k: decode_array(v) for k, v in msg.arrays.items()})
         obs.update(dict(msg.strings.items()))
         return obs
