@@ -74,6 +74,7 @@ class GemmDesc(ctypes.Structure):
         ('rtc_prev', c_vp), ('ld_prev', c_i64),
         ('rtc_cw', c_vp),
         ('rtc_omt', c_f32),
+        ('a_scale', c_vp), ('bias2_f32', c_vp),
     ]
 
 

@@ -1402,7 +1402,7 @@ __device__ __forceinline__ void sc1_load8(__amdgpu_buffer_rsrc_t r, int off,
   }
 }
 
-template <int MODE, bool F8, bool A16, int RB>
+template <int MODE, bool F8, bool A16, int RB, bool ASC>
 __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
                                                           int64_t kc,
@@ -1411,6 +1411,9 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   // RB activation row blocks of 16 per workgroup: row group blockIdx.z
   // covers rows 16 RB z .. + 16 RB - 1 (fewer row blocks, more workgroups)
   static_assert(RB == 4 || !F8 || A16, "W8A8 skinny GEMMs take all 4 row blocks");
+  // ASC: adaptive RMSNorm folded in -- A's column k scaled by (1 +
+  // a_scale[k]) as it is loaded (bf16 A, i.e. bf16 or W8A16 weights)
+  static_assert(!ASC || !F8 || A16, "a_scale needs bf16 activations");
   constexpr int RR = 16 * RB;
   // W8A8: one register set = one 128-k step of the fp8 MFMA (4 A blocks of
   // 32); W8A16: S 32-k steps of bf16 MFMAs whose B fragments are converted
@@ -1471,6 +1474,8 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   };
 
   bf16x8 ra[2][S][RB], rb[2][S][NB];
+  bf16x8 rsc[2][S];  // ASC: a_scale of the lane's 8 k positions per step
+  const __amdgpu_buffer_rsrc_t rsc_rs = make_rsrc(p.a_scale, ASC ? rec_bytes(K * 2) : 0u);
   // unconditional loads: a masked-out fragment gets an offset past the view
   auto load = [&](int t0, int set) {
 #pragma unroll
@@ -1495,6 +1500,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
         const bool rin = p.a_frag || (fb0 + f) * 16 + fr < M;
         ra[set][t][f] = bld(ra_rs, (kin && rin) ? a0 + ks * a_ks + (fb0 + f) * a_f : kOOB);
       }
+      if (ASC) rsc[set][t] = bld(rsc_rs, kin ? ks * 64u + 16u * (uint32_t)g : kOOB);
     }
   };
   f32x4_t acc[NB][RB];
@@ -1505,6 +1511,17 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   float ss[RB];
 #pragma unroll
   for (int f = 0; f < RB; ++f) ss[f] = 0.f;
+  // ASC: the A fragment as the MFMA sees it, bf16(x[k] * (1 + a_scale[k]))
+  // with the factor in fp32 (as GemmaRMSNorm forms it)
+  auto scaled = [&](const bf16x8& a, const bf16x8& sc) {
+    if (!ASC) return a;
+    float x[8], y[8];
+    unpack8(a, x);
+    unpack8(sc, y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= 1.f + y[e];
+    return pack8(x);
+  };
   auto compute = [&](int set) {
     if (A16) {
       // lane (fr, g) holds weight bytes k = 32 t + 8 g + j of column n0 + fr
@@ -1522,8 +1539,9 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
 #pragma unroll
         for (int f = 0; f < RB; ++f) {
           if (p.rownorm) ss[f] += sumsq8(ra[set][t][f]);
+          const bf16x8 av = scaled(ra[set][t][f], rsc[set][t]);
 #pragma unroll
-          for (int b = 0; b < NB; ++b) acc[b][f] = mfma16x16x32(ra[set][t][f], bw[b], acc[b][f]);
+          for (int b = 0; b < NB; ++b) acc[b][f] = mfma16x16x32(av, bw[b], acc[b][f]);
         }
       }
       return;
@@ -1558,9 +1576,10 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
 #pragma unroll
       for (int f = 0; f < RB; ++f) {
         if (p.rownorm) ss[f] += sumsq8(ra[set][t][f]);
+        const bf16x8 av = scaled(ra[set][t][f], rsc[set][t]);
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-          acc[b][f] = mfma16x16x32(ra[set][t][f], rb[set][t][b], acc[b][f]);
+          acc[b][f] = mfma16x16x32(av, rb[set][t][b], acc[b][f]);
       }
   };
   if (nst > 0) load(0, 0);
@@ -1576,6 +1595,15 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   const bool vec = vec_ok && cnt == 8;
   EpiIn in;
   if (mine) epi_load<MODE>(p, row, ncol, vec, cnt, in);
+  // ASC with QKV_ROPE / GEGLU: the folded shift's fp32 biases (gate, up)
+  constexpr bool FB = ASC && (MODE == FVX_GEMM_QKV_ROPE || MODE == FVX_GEMM_GEGLU);
+  float fb[8], fb2[8];
+  if (FB) {
+    bl_f8(make_rsrc(p.bias_f32, p.bias_f32 ? rec_bytes(N * 4) : 0u), (uint32_t)(ncol * 4), vec,
+          fb);
+    bl_f8(make_rsrc(p.bias2_f32, p.bias2_f32 ? rec_bytes(N * 4) : 0u), (uint32_t)(ncol * 4),
+          vec, fb2);
+  }
   float wsc[8], wsc2[8];  // fp8 per-channel weight scales of the 8 columns
   if (F8) {
     bl_f8(make_rsrc(p.b_scale, rec_bytes(N * 4)), (uint32_t)(ncol * 4), vec, wsc);
@@ -1680,13 +1708,23 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
     }
   }
   if (!mine) return;
-  const float r = p.rownorm ? rsqrtf(rsum / (float)K + p.rownorm_eps) : 1.f;
+  float r = p.rownorm ? rsqrtf(rsum / (float)K + p.rownorm_eps) : 1.f;
   if (F8) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       v[e] *= wsc[e];
       u[e] *= wsc2[e];
     }
+  }
+  if (FB) {
+    // RMS factor, then the shift's biases (the QKV / GeGLU epilogues have
+    // no bias of their own)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] = v[e] * r + fb[e];
+      u[e] = u[e] * r + fb2[e];
+    }
+    r = 1.f;
   }
   epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in, false, nullptr);
 }
@@ -1919,6 +1957,20 @@ static int validate(const GemmArgs& d) {
   FVX_REQUIRE(!(d.rtc_prev || d.rtc_cw) || d.mode == FVX_GEMM_EULER, FVX_ERR_ARG,
               "gemm: rtc_prev / rtc_cw need mode EULER");
   FVX_REQUIRE(!d.rtc_cw || d.rtc_prev, FVX_ERR_ARG, "gemm: rtc_cw needs rtc_prev");
+  FVX_REQUIRE(!d.a_scale || ((d.mode == FVX_GEMM_QKV_ROPE || d.mode == FVX_GEMM_GEGLU ||
+                              d.mode == FVX_GEMM_EULER) &&
+                             !(d.b_fp8 && d.fp8_act) && aligned16(d.a_scale) && use_skinny(d)),
+              FVX_ERR_ARG,
+              "gemm: a_scale needs mode QKV_ROPE, GEGLU or EULER, bf16 activations, "
+              "M <= 64 (skinny) and a 16B-aligned bf16 [K] vector");
+  FVX_REQUIRE(!((d.mode == FVX_GEMM_QKV_ROPE || d.mode == FVX_GEMM_GEGLU) &&
+                (d.bias || ((d.bias_f32 || d.bias2_f32) && !d.a_scale))),
+              FVX_ERR_ARG,
+              "gemm: QKV_ROPE / GEGLU take fp32 biases only with a_scale, no bf16 bias");
+  FVX_REQUIRE(!d.bias2_f32 || d.mode == FVX_GEMM_GEGLU, FVX_ERR_ARG,
+              "gemm: bias2_f32 is the GEGLU up half's bias");
+  FVX_REQUIRE(((uintptr_t)d.bias2_f32 & 15) == 0, FVX_ERR_ALIGN,
+              "gemm: bias2_f32 must be 16B aligned");
   FVX_REQUIRE(!d.rtc_prev || (d.ld_prev >= d.n && (d.rtc_lock || d.rtc_cw)), FVX_ERR_ARG,
               "gemm: rtc_prev needs ld_prev >= n and rtc_lock or rtc_cw");
   FVX_REQUIRE(((uintptr_t)d.rtc_lock & 3) == 0 && ((uintptr_t)d.rtc_prev & 3) == 0 &&
@@ -2227,6 +2279,26 @@ extern "C" int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d) {
   return kCounterBytes + ((int64_t)nb * sp * d->m * d->n + sp * d->m) * 4;
 }
 
+// Skinny GEMMs with the adaptive RMSNorm folded in (a_scale): QKV_ROPE,
+// GEGLU and EULER, bf16 or W8A16 weights.
+template <int MODE>
+static void launch_skinny_asc(const GemmArgs& d, const SkinnyPlan& sp, dim3 grid,
+                              hipStream_t s, int vec_ok) {
+  if constexpr (MODE == FVX_GEMM_PLAIN) {
+    return;  // refused by validate()
+  } else {
+#define LA(F8, RBV)                                                                   \
+  hipLaunchKernelGGL((gemm_skinny_kernel<MODE, F8, F8, RBV, true>), grid,             \
+                     dim3(64 * sk_waves(F8, F8)), 0, s, d, sp.splits, sp.kc, vec_ok)
+    if (d.b_fp8) {
+      if (sp.rb == 1) LA(true, 1); else if (sp.rb == 2) LA(true, 2); else LA(true, 4);
+    } else {
+      if (sp.rb == 1) LA(false, 1); else if (sp.rb == 2) LA(false, 2); else LA(false, 4);
+    }
+#undef LA
+  }
+}
+
 extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
   clear_error();
   FVX_REQUIRE(dp, FVX_ERR_NULL, "gemm: descriptor is NULL");
@@ -2250,25 +2322,27 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
     const int vec_ok = epi_vec_ok(d) ? 1 : 0;
 #define L(MODE)                                                                 \
   if (d.b_fp8 && d.fp8_act)                                                      \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, false, 4>), grid,         \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, false, 4, false>), grid,  \
                        dim3(64 * sk_waves(true, false)), 0, s, d, sp.splits, sp.kc, vec_ok); \
+  else if (d.a_scale)                                                           \
+    launch_skinny_asc<MODE>(d, sp, grid, s, vec_ok);                             \
   else if (d.b_fp8 && sp.rb == 1)                                                \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 1>), grid,          \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 1, false>), grid,   \
                        dim3(64 * sk_waves(true, true)), 0, s, d, sp.splits, sp.kc, vec_ok); \
   else if (d.b_fp8 && sp.rb == 2)                                                \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 2>), grid,          \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 2, false>), grid,   \
                        dim3(64 * sk_waves(true, true)), 0, s, d, sp.splits, sp.kc, vec_ok); \
   else if (d.b_fp8)                                                              \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 4>), grid,          \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, true, 4, false>), grid,   \
                        dim3(64 * sk_waves(true, true)), 0, s, d, sp.splits, sp.kc, vec_ok); \
   else if (sp.rb == 1)                                                           \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 1>), grid,        \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 1, false>), grid, \
                        dim3(64 * kSkWaves), 0, s, d, sp.splits, sp.kc, vec_ok);  \
   else if (sp.rb == 2)                                                           \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 2>), grid,        \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 2, false>), grid, \
                        dim3(64 * kSkWaves), 0, s, d, sp.splits, sp.kc, vec_ok);  \
   else                                                                           \
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 4>), grid,        \
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, false, false, 4, false>), grid, \
                        dim3(64 * kSkWaves), 0, s, d, sp.splits, sp.kc, vec_ok)
     FVX_MODE_DISPATCH(d.mode, L)
 #undef L

@@ -458,9 +458,31 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
     return out
 
 
+def _set_a_scale(d, a_scale=None, bias_f32=None, bias2_f32=None):
+    """Adaptive RMSNorm folded into an M <= 64 GEMM (fvx_gemm_desc.a_scale):
+    A's column k times (1 + a_scale[k]) (bf16 [K]: the style's scale); fp32
+    biases after the RMS factor (QKV_ROPE: bias_f32; GEGLU: bias_f32 gate
+    half, bias2_f32 up)."""
+    if a_scale is not None:
+        _check(a_scale, 'a_scale')
+        if a_scale.numel() < d.k:
+            raise ValueError('a_scale needs K values')
+        d.a_scale = a_scale.data_ptr()
+    for t, nm in ((bias_f32, 'bias_f32'), (bias2_f32, 'bias2_f32')):
+        if t is not None:
+            _check(t, nm, dtype=torch.float32)
+            if t.numel() < d.n:
+                raise ValueError(f'{nm} needs N values')
+            setattr(d, nm, t.data_ptr())
+
+
 def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
-               c_frag=None, ss_in=None, a8=None, a8_out=None):
-    """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T)."""
+               c_frag=None, ss_in=None, a8=None, a8_out=None, a_scale=None,
+               bias_f32=None, bias2_f32=None):
+    """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T); with ``a_scale`` (the
+    folded adaptive RMSNorm, M <= 64): gelu_tanh(r a' @ gate_w^T + bias_f32)
+    * (r a' @ up_w^T + bias2_f32), a' = a * (1 + a_scale), r the RMS factor
+    of a."""
     d = _gemm_desc(a, gate_w)
     if isinstance(gate_w, Fp8Weight):
         if (not isinstance(up_w, Fp8Weight) or up_w.frag != gate_w.frag or
@@ -485,6 +507,7 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
     _check(out, 'out', contiguous=False)
     _, d.ldc = _rows_ld(out, 'out')
     d.c, d.mode = out.data_ptr(), _lib.GEMM_GEGLU
+    _set_a_scale(d, a_scale, bias_f32, bias2_f32)
     _set_ss(d, rownorm_eps, ss_in)
     _set_a8(d, a8, a8_out)
     d.split_k = split_k
@@ -495,7 +518,8 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
 
 def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
                   head_dim, rownorm_eps=None, row_group=0, row_group_stride=0,
-                  split_k=0, v_ld=None, ss_in=None, a8=None):
+                  split_k=0, v_ld=None, ss_in=None, a8=None, a_scale=None,
+                  bias_f32=None):
     """[q|k|v] = a @ w_qkv^T with pair-interleaved RoPE on q and k.
 
     rope: fp32 [max_pos, head_dim/2, 2] (cos, sin); positions: int32 [M].
@@ -519,6 +543,7 @@ def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
     else:
         d.v_out, d.ldv, d.v_transposed = v_out.data_ptr(), int(v_ld), 1
     d.n_q_heads, d.head_dim = n_q_heads, head_dim
+    _set_a_scale(d, a_scale, bias_f32)
     _set_ss(d, rownorm_eps, ss_in)
     _set_a8(d, a8)
     d.row_group, d.row_group_stride = row_group, row_group_stride
@@ -557,7 +582,7 @@ def _set_rtc(d, lock=None, period=0, bias_f32_locked=None, prev=None,
 
 def gemm_euler(a, weight, bias, xt, dt, xt_bf16=None, rownorm_eps=None,
                split_k=0, bias_f32=None, rtc_lock=None, rtc_period=0,
-               rtc_prev=None, rtc_cw=None, rtc_omt=0.0):
+               rtc_prev=None, rtc_cw=None, rtc_omt=0.0, a_scale=None):
     """v = a @ weight^T + bias; xt += dt * v (fp32, in place); xt_bf16 mirrors.
     Real-time chunking (see fvx_gemm_desc): rows with m % rtc_period <
     rtc_lock store rtc_prev (prefix method); with ``rtc_cw`` every row adds
@@ -579,6 +604,7 @@ def gemm_euler(a, weight, bias, xt, dt, xt_bf16=None, rownorm_eps=None,
     if rownorm_eps is not None:
         d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
     _set_rtc(d, rtc_lock, rtc_period, prev=rtc_prev, cw=rtc_cw, omt=rtc_omt)
+    _set_a_scale(d, a_scale)
     d.split_k = split_k
     _run_gemm(d)
 

@@ -269,6 +269,10 @@ class PI0Inference:
         # will read it (prefetch_place) or the memory-side cache
         self.prefetch = True
         self.prefetch_place = True
+        # PI0.5 at bs=1: the adaptive RMSNorms run inside the next GEMM
+        # (A scaled by 1 + scale as it is loaded, the shift as a bias, the
+        # gate read from the style row by the residual epilogues)
+        self.fold_adarms = True
         self.weight_dtype = weight_dtype
         self.fp8_cache = fp8_cache
         self.fp8_cache_hit = False
@@ -348,7 +352,29 @@ class PI0Inference:
         self.rope = K.rope_table(cfg.prefix_len + cfg.suffix_len + 8,
                                  cfg.head_dim, cfg.rope_theta, device=dev)
         self._prepare_frag_weights()
+        self._prepare_adarms_fold()
         torch.cuda.synchronize(dev)
+
+    def _prepare_adarms_fold(self):
+        """Per (step, layer) fp32 biases shift @ W^T of the folded adaptive
+        RMSNorms (PI0.5): the input norm's shift through Q|K|V, the
+        post-attention norm's through gate and up, the final norm's through
+        action_out_proj.  The (1 + scale) factor and the gate are read from
+        the style rows themselves."""
+        if not self.cfg.pi05 or self.weight_dtype == 'fp8_w8a8':
+            self.fold = None
+            return
+        w = self.cfg.exp_hidden
+        st = self.styles  # [steps, 2 * layers + 1, 3 * w]
+        self.fold = []
+        for i, L in enumerate(self.exp['layers']):
+            ha, hf = st[:, 2 * i, w:2 * w], st[:, 2 * i + 1, w:2 * w]
+            self.fold.append({
+                'qkv': K.gemm(ha, L['qkv_w'], out_f32=True),
+                'gate': K.gemm(hf, L['gate_w'], out_f32=True),
+                'up': K.gemm(hf, L['up_w'], out_f32=True)})
+        self.fold_out = K.gemm(st[:, -1, w:2 * w], self.act_out['w'],
+                               out_f32=True)
 
     def _prepare_frag_weights(self):
         """Fragment-major copies of the action-expert weights for the M <= 64
@@ -657,6 +683,45 @@ class PI0Inference:
                      rownorm_eps=cfg.rms_eps)
         K.gemm(b['ex_h'], L['down_w'], out=x, residual=x)
 
+    def _fold_ok(self, B, rtc):
+        """PI0.5 runs its adaptive RMSNorms folded into the GEMMs at bs=1
+        (per-position styles of the prefix RTC method keep the norm
+        kernels)."""
+        return (self.cfg.pi05 and self.fold_adarms and self.fold is not None
+                and self._frag_ok(B) and rtc != 'prefix')
+
+    def _expert_layer_pi05_fused(self, b, i, step):
+        """_expert_layer_pi05 at bs=1 with the adaptive RMSNorms folded in:
+        the Q|K|V and gate/up GEMMs read the raw stream x (fragment-major),
+        scale its columns by 1 + scale and its rows by the RMS factor and
+        add shift @ W^T; the O and down epilogues multiply by the style's
+        gate before the residual add (condition_gemma.py:126-145, 319-337)."""
+        cfg = self.cfg
+        S, Ss, D, hid = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.exp_hidden
+        T = self.kv_len
+        Lf, fz = self.exp_f[i], self.fold[i]
+        x = b['ex_x'].view(Ss, hid)
+        xf = b['ex_xf'].rows(Ss)
+        ctxf, hf = b['ex_ctxf'].rows(Ss), b['ex_hf'].rows(Ss)
+        kc, vc = b['kc'][i], b['vc'][i]
+        sa, sp = self.styles[step, 2 * i], self.styles[step, 2 * i + 1]
+        K.gemm_qkv_rope(xf, Lf['qkv_w'], self.rope, b['pos_suf'],
+                        b['ex_q'].view(Ss, -1), kc.view(T, D)[S:],
+                        vc[:, :, S:], cfg.heads, D, rownorm_eps=cfg.rms_eps,
+                        row_group=Ss, row_group_stride=T, v_ld=T,
+                        a_scale=sa[:hid], bias_f32=fz['qkv'][step])
+        K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
+                        kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True,
+                        o_frag=ctxf, prefetch=self._prefetch_list(i),
+                        prefetch_place=self.prefetch_place)
+        K.gemm(ctxf, Lf['o_w'], out=x, residual=x,
+               gate=sa[2 * hid:].view(1, hid), gate_group=Ss, c_frag=xf)
+        K.gemm_geglu(xf, Lf['gate_w'], Lf['up_w'], out=b['ex_h'],
+                     rownorm_eps=cfg.rms_eps, c_frag=hf, a_scale=sp[:hid],
+                     bias_f32=fz['gate'][step], bias2_f32=fz['up'][step])
+        K.gemm(hf, Lf['down_w'], out=x, residual=x,
+               gate=sp[2 * hid:].view(1, hid), gate_group=Ss, c_frag=xf)
+
     def _expert_layer_pi05(self, b, B, i, L, step, rtc=None):
         cfg = self.cfg
         pf = None
@@ -709,10 +774,12 @@ class PI0Inference:
                    bias=self.state['b'])
             w_mi = self.mlp_in_a_f if fr else self.mlp_in_a
             w_mo = self.mlp_out_f if fr else self.mlp_out['w']
+        fused = self._fold_ok(B, rtc)
         for step in range(len(self.times)):
             if cfg.pi05:
                 K.gemm(xt_b, w_in, out=x3.view(B * Ss, hid),
-                       bias=self.act_in['b'])
+                       bias=self.act_in['b'],
+                       c_frag=b['ex_xf'].rows(Ss) if fused else None)
             else:
                 K.gemm(xt_b, w_in, out=b['act_h1'], bias=self.act_in['b'])
                 # prefix RTC: locked positions take the time-0 embedding
@@ -729,13 +796,23 @@ class PI0Inference:
                 if fr:
                     K.pack_frag(x3.view(Ss, hid), b['ex_xf'].rows(Ss))
             for i, L in enumerate(self.exp['layers']):
-                if cfg.pi05:
+                if fused:
+                    self._expert_layer_pi05_fused(b, i, step)
+                elif cfg.pi05:
                     self._expert_layer_pi05(b, B, i, L, step, rtc)
                 else:
                     self._expert_layer_pi0(b, B, i, L)
             lead = Ss - na
             for s in range(B):
                 a = x3[s, lead:]
+                if fused:
+                    K.gemm_euler(a, self.act_out_f, self.act_out['b'],
+                                 b['xt'][s], self.dt, xt_bf16=b['xt_bf16'][s],
+                                 rownorm_eps=cfg.rms_eps,
+                                 bias_f32=self.fold_out[step],
+                                 a_scale=self.styles[step, -1, :hid],
+                                 **self._euler_rtc(b, s, step, rtc))
+                    continue
                 if cfg.pi05:
                     xn = b['ex_xn'][s, lead:]
                     st = self.styles[step, -1:]

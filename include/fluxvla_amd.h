@@ -195,6 +195,20 @@ typedef struct fvx_gemm_desc {
   int64_t ld_prev;
   const float* rtc_cw;             /* [rtc_period] fp32 */
   float rtc_omt;
+  /* Adaptive RMSNorm folded into the GEMM (PI0.5 action expert at M <= 64).
+   * a_scale (bf16 [K]): A's column k is multiplied by (1 + a_scale[k]) in
+   * fp32 as it is loaded, then rounded to bf16 for the MFMA (the rownorm sums
+   * use A as given): the adaptive scale of GemmaRMSNorm
+   * (condition_gemma.py:126-145) applied to the raw residual stream, whose
+   * RMS factor the rownorm applies to the product; the shift becomes a bias
+   * (shift @ B^T, precomputed by the caller).
+   * With it, QKV_ROPE and GEGLU take fp32 biases too, after the rownorm
+   * scaling: QKV_ROPE adds bias_f32[n] before the rotation; GEGLU adds
+   * bias_f32[n] to the gate half and bias2_f32[n] to the up half before
+   * gelu_tanh(gate) * up.  M <= 64 (skinny) GEMMs with bf16 or W8A16
+   * weights only; NULL: unused. */
+  const void* a_scale;
+  const float* bias2_f32;          /* [N] fp32, GEGLU up half */
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */
