@@ -763,8 +763,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
 // attn_decode_t_kernel: the same problems as attn_decode_kernel (head_dim 256,
 // transposed value cache, 64-row groups x key ranges, the same partials for
 // attn_decode_merge_kernel), computed transposed so that nothing crosses
-// waves but the K / V^T tiles.  A workgroup of 2 waves owns 64 query rows;
-// wave w owns rows 32 w .. + 31 and all 256 dims, and per 64-key tile
+// waves but the K / V^T tiles.  A workgroup of NW waves owns 32 NW query
+// rows; wave w owns rows 32 w .. + 31 and all 256 dims, and per 64-key tile
 //   S^T (64 keys x 32 rows)  = K . Q^T     v_mfma_f32_32x32x16_bf16, K from
 //                                          LDS (A), Q^T in VGPRs (B);
 //   O^T (256 dims x 32 rows) += V^T . P^T  V^T from LDS (A), P^T (B) straight
@@ -793,27 +793,69 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
 // ---------------------------------------------------------------------------
 constexpr int kDtKB = 64 * 512, kDtVB = 256 * 128;
 constexpr int kDtStage = kDtKB + kDtVB + 256;    // + the tile's key groups
-constexpr int kDtOffQG = 2 * kDtStage;           // query groups [64]
-constexpr int kDtLDS = kDtOffQG + 64 * 4;
-static_assert(64 * kDecOP * 4 <= 2 * kDtStage, "O rows fit the stages");
+constexpr int kDtOffQG = 2 * kDtStage;           // query groups [32 NW]
+// NW waves own 32 NW query rows; the epilogue's O rows ([32 NW][kDecOP] fp32)
+// reuse the LDS from its start
+template <int NW>
+constexpr int dt_lds() {
+  return kDtOffQG + 128 * NW > 128 * NW * kDecOP ? kDtOffQG + 128 * NW
+                                                 : 128 * NW * kDecOP;
+}
+static_assert(dt_lds<4>() <= 160 * 1024, "4-wave LDS fits the CU");
 constexpr float kDtRefSlack = 32.f;              // log2 of the largest P
 constexpr int kDecTKps = 4 * kDecKT;             // keys per range that select it
+// waves per workgroup of attn_decode_t_kernel (2: 64 query rows, 4: 128;
+// 4 measured 15-20 % faster on the prefix)
+constexpr int kDtNW = 4;
+// workgroups the default key-range count aims at (the CUs of an MI355X)
+constexpr int64_t kDtTargetWgs = 256;
+// LDS fragment ring of the tile loop: kDtRing register sets, read kDtAhead
+// MFMA steps ahead of their use (deeper rings measured no faster)
+constexpr int kDtAhead = 6, kDtRing = kDtAhead + 2;
 
-__global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
-                                                            int n_rg, int splits,
-                                                            int kps, int hs) {
-  constexpr int HD = 256, KT = 64;
-  __shared__ __align__(16) unsigned char smem[kDtLDS];
-  __shared__ float sLq[64], sMq[64];
+// The values of lanes l and l ^ 32 combined in both (v_permlane32_swap: a
+// VALU exchange of the wave's halves, where a shuffle is an LDS round trip).
+// Both lanes compute the same expression of the same two values, so they
+// agree bit for bit.
+__device__ __forceinline__ void half_pair(float v, float& a, float& b) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  a = __uint_as_float(s[0]);  // lane l & 31's value
+  b = __uint_as_float(s[1]);  // lane (l & 31) + 32's value
+}
+__device__ __forceinline__ float half_pair_max(float v) {
+  float a, b;
+  half_pair(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float half_pair_sum(float v) {
+  float a, b;
+  half_pair(v, a, b);
+  return a + b;
+}
+
+// NW = 2 or 4 waves: with 4, every K / V^T tile brought into the LDS serves
+// 128 query rows and all four SIMDs of the CU.  n_rg counts 64-row groups
+// (the unit of the partials and of the merge); a 4-wave workgroup covers two
+// of them.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
+                                                                int n_rg, int splits,
+                                                                int kps, int hs) {
+  constexpr int HD = 256, KT = 64, RPW = 32 * NW, LPW = 32 / NW;
+  static_assert(NW == 2 || NW == 4, "2 or 4 waves");
+  __shared__ __align__(16) unsigned char smem[dt_lds<NW>()];
+  __shared__ float sLq[RPW], sMq[RPW];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane & 31, h = lane >> 5;
   const int nb = (int)gridDim.x, q8 = nb >> 3, r8 = nb & 7;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
-  const int rg = item % n_rg;
-  const int split = (item / n_rg) % splits;
-  const int z = item / (n_rg * splits);
+  const int n_rgw = (n_rg * 64 + RPW - 1) / RPW;  // RPW-row groups
+  const int rg = item % n_rgw;
+  const int split = (item / n_rgw) % splits;
+  const int z = item / (n_rgw * splits);
   const int heads = (int)p.heads, R = (int)p.sq * heads;
   const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
@@ -842,7 +884,8 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
   // load L (0..31) of a tile: K keys 2 L + (lane >> 5) (LDS slot lane & 31 of
   // the key's 512-byte row holds global chunk slot ^ (key & 15)); V^T dims
   // 8 L + (lane >> 3) (slot lane & 7 of the dim's 128-byte row holds key
-  // chunk slot ^ ((dim >> 1) & 7)).  Wave w issues K and V loads 16 w .. + 15.
+  // chunk slot ^ ((dim >> 1) & 7)).  Wave w issues K and V loads LPW w ..
+  // LPW w + LPW - 1.
   auto load_k = [&](int t0, int st, int L) {
     const int kl = 2 * L + (lane >> 5);
     const int ch = (lane & 31) ^ (kl & 15);
@@ -858,27 +901,30 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
     load_lds4(rgc, lbase + st * kDtStage + kDtKB + kDtVB, (uint32_t)(t0 + lane) * 4);
   };
 
-  // Q rows 64 rg + 2 L + (lane >> 5) into stage 1's K area (K's swizzle), the
-  // query groups, then tile 0 into stage 0
+  // Q rows RPW rg + 2 L + (lane >> 5) into stage 1 from its start (K's
+  // swizzle; 128 rows fill its K and V^T areas, 64 KB), the query groups,
+  // then tile 0 into stage 0
+  static_assert(RPW * 512 <= kDtKB + kDtVB, "Q rows fit stage 1");
   {
     const uint32_t qb = lbase + kDtStage;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int L = 16 * w + i, rl = 2 * L + (lane >> 5), r = rg * 64 + rl;
+      const int L = 16 * w + i, rl = 2 * L + (lane >> 5), r = rg * RPW + rl;
       const int tok = row_tok(r, heads, hs);
       const int ch = (lane & 31) ^ (rl & 15);
       load_lds16(rq, qb + 2 * L * 512,
                  r < R ? (uint32_t)(tok * qts + (r - tok * heads) * qhs + 8 * ch) * 2 : kOOB);
     }
-    if (w == 0) {
-      const int r = rg * 64 + lane;
-      load_lds4(rqg, lbase + kDtOffQG, r < R ? (uint32_t)row_tok(r, heads, hs) * 4 : kOOB);
+    if (w < NW / 2) {  // 64 rows' groups per wave
+      const int r = rg * RPW + 64 * w + lane;
+      load_lds4(rqg, lbase + kDtOffQG + 256 * w,
+                r < R ? (uint32_t)row_tok(r, heads, hs) * 4 : kOOB);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    load_k(kbeg, 0, 16 * w + i);
-    load_v(kbeg, 0, 16 * w + i);
+  for (int i = 0; i < LPW; ++i) {
+    load_k(kbeg, 0, LPW * w + i);
+    load_v(kbeg, 0, LPW * w + i);
   }
   if (kgrp && w == 0) load_g(kbeg, 0);
   wait_vmcnt<0>();
@@ -925,14 +971,14 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
     // this wave's loads of tile t landed
     wait_vmcnt<0>();
     if (edge) {
-      // keys >= kend of this wave's V^T rows (dims 128 w ..) read as zero
+      // keys >= kend of this wave's V^T rows (dims 8 LPW w ..) read as zero
       // (the cache past the range may hold anything; P is 0 there)
-      bf16_t* sVw = (bf16_t*)sV + 128 * w * 64;
+      bf16_t* sVw = (bf16_t*)sV + 8 * LPW * w * 64;
       const int valid = kend - t0;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < LPW; ++i) {
         const int c = lane + 64 * i, row = c >> 3, slot = c & 7;
-        const int kc = slot ^ (((128 * w + row) >> 1) & 7);  // key chunk in this slot
+        const int kc = slot ^ (((8 * LPW * w + row) >> 1) & 7);  // key chunk in this slot
         bf16x8* ptr = (bf16x8*)&sVw[row * 64 + 8 * slot];
         if (8 * kc + 8 > valid) {
           bf16x8 v = *ptr;
@@ -949,16 +995,11 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
     __syncthreads();
 
     // key groups mask some key of this tile for some row of this wave?
-    // (uniform: the tile's largest group against the wave's smallest)
-    bool gmask = false;
-    if (kgrp) {
-      int gk = sG[lane];
-#pragma unroll
-      for (int x = 1; x < 64; x <<= 1) gk = max(gk, __shfl_xor(gk, x, 64));
-      gmask = __builtin_amdgcn_readfirstlane(gk) > qg_min;
-    }
+    // (uniform: any key group of the tile above the wave's smallest; one
+    // ballot, no cross-lane chain)
+    const bool gmask = kgrp && __ballot(sG[lane] > qg_min) != 0;
     const bool more = t + 1 < ntile;  // tile t + 1 is loaded during this one
-    auto rdk = [&](int j) {
+    auto rdk = [&](int j) {  // S^T step j: key block j & 1, dims 16 (j >> 1) ..
       const int key = 32 * (j & 1) + piq;
       return ld8(&sK[key * 256 + 8 * ((2 * (j >> 1) + h) ^ (key & 15))]);
     };
@@ -970,14 +1011,14 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
     {
       // S^T: step j = 2 s + kb (key block kb, dims 16 s ..; the two blocks'
       // accumulations alternate, so that no MFMA waits for the previous
-      // one's result), the K fragments through a ring of 8 register sets
-      // read 6 steps ahead
+      // one's result), the K fragments through a ring of kDtRing register
+      // sets read kDtAhead steps ahead
       f32x16_t sacc[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-      bf16x8 ring[8], pT[4];
+      bf16x8 ring[kDtRing], pT[4];
       // softmax of key block kb (its S^T complete) -> pT[2 kb], pT[2 kb + 1]:
       // element r is key 32 kb + 16 (r >> 3) + 8 h + (r & 7).  The maximum
       // is taken on the raw scores (the scale is positive) and the scale
@@ -1004,7 +1045,7 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
         float mb = sv[0];
 #pragma unroll
         for (int e = 1; e < 16; ++e) mb = fmaxf(mb, sv[e]);
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * sc;
+        mb = half_pair_max(mb) * sc;
         m_max = fmaxf(m_max, mb);
         if (m_ref == -INFINITY)
           m_ref = mb;
@@ -1023,29 +1064,31 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
         }
       };
 #pragma unroll
-      for (int j = 0; j < 6; ++j) ring[j] = rdk(j);
+      for (int j = 0; j < kDtAhead; ++j) ring[j] = rdk(j);
       // (compile-time steps: the loops hold too much code for the unroller)
       static_for<0, 32>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        if (j + 6 < 32) ring[(j + 6) & 7] = rdk(j + 6);
-        sacc[j & 1] = mfma32x32x16(ring[j & 7], qT[j >> 1], sacc[j & 1]);
-        if (more) {
+        if (j + kDtAhead < 32) ring[(j + kDtAhead) % kDtRing] = rdk(j + kDtAhead);
+        sacc[j & 1] = mfma32x32x16(ring[j % kDtRing], qT[j >> 1], sacc[j & 1]);
+        // the wave's 2 LPW loads of tile t + 1, one every 16 / LPW steps
+        constexpr int EV = 16 / LPW, LL = j / EV;
+        if (more && j % EV == 0) {
           if (j == 0 && kgrp && w == 0) load_g(t0 + KT, st ^ 1);
-          if (j < 16)
-            load_k(t0 + KT, st ^ 1, 16 * w + j);
+          if (LL < LPW)
+            load_k(t0 + KT, st ^ 1, LPW * w + LL);
           else
-            load_v(t0 + KT, st ^ 1, 16 * w + j - 16);
+            load_v(t0 + KT, st ^ 1, LPW * w + LL - LPW);
         }
       });
       softmax(IntC<0>{});
       // O^T += V^T P^T, step j = 8 u + db: V^T A operand lane (i, h) = dim
       // 32 db + i, keys 16 u + 8 h .. + 7
 #pragma unroll
-      for (int j = 0; j < 6; ++j) ring[j] = rdv(j);
+      for (int j = 0; j < kDtAhead; ++j) ring[j] = rdv(j);
       static_for<0, 32>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        if (j + 6 < 32) ring[(j + 6) & 7] = rdv(j + 6);
-        o[j & 7] = mfma32x32x16(ring[j & 7], pT[j >> 3], o[j & 7]);
+        if (j + kDtAhead < 32) ring[(j + kDtAhead) % kDtRing] = rdv(j + kDtAhead);
+        o[j & 7] = mfma32x32x16(ring[j % kDtRing], pT[j >> 3], o[j & 7]);
         if (j == 3) softmax(IntC<1>{});
       });
     }
@@ -1058,13 +1101,13 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
   m_ref = m_max;
   l_run = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    load_k(kbeg, 0, 16 * w + i);
-    load_v(kbeg, 0, 16 * w + i);
+  for (int i = 0; i < LPW; ++i) {
+    load_k(kbeg, 0, LPW * w + i);
+    load_v(kbeg, 0, LPW * w + i);
   }
   if (kgrp && w == 0) load_g(kbeg, 0);
   }
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = half_pair_sum(l_run);
 
   // O rows -> LDS: lane (q, h) holds dims 32 db + 8 (r >> 2) + 4 h + (r & 3)
   // of row 32 w + q
@@ -1087,8 +1130,8 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
   if (splits == 1) {
 #pragma unroll 4
     for (int u = 0; u < 16; ++u) {
-      const int c = tid + 128 * u, i = c >> 5, d0 = (c & 31) * 8;
-      const int r = rg * 64 + i;
+      const int c = tid + 64 * NW * u, i = c >> 5, d0 = (c & 31) * 8;
+      const int r = rg * RPW + i;
       if (r >= R) continue;
       const float l = sLq[i];
       const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -1100,15 +1143,21 @@ __global__ __launch_bounds__(128) void attn_decode_t_kernel(fvx_attn_desc p,
     }
     return;
   }
-  float* part = (float*)p.workspace + (((int64_t)z * n_rg + rg) * splits + split) * kDecPF;
+  // one partial per 64-row group (the merge's unit); a 4-wave workgroup's
+  // second group does not exist when n_rg is odd and this is the last one
+  for (int g = 0; g < NW / 2; ++g) {
+    const int rg64 = rg * (NW / 2) + g;
+    if (rg64 >= n_rg) break;
+    float* part = (float*)p.workspace + (((int64_t)z * n_rg + rg64) * splits + split) * kDecPF;
 #pragma unroll 4
-  for (int u = 0; u < 16; ++u) {
-    const int c = tid + 128 * u, i = c >> 5, d0 = (c & 31) * 8;
-    st8((bf16_t*)part + i * 256 + d0, pack8(&sO[i * kDecOP + d0]));
-  }
-  if (tid < 64) {
-    part[kDecPO + tid] = sMq[tid];
-    part[kDecPO + 64 + tid] = sLq[tid];
+    for (int u = 0; u < 16 / (NW / 2); ++u) {
+      const int c = tid + 64 * NW * u, i = c >> 5, d0 = (c & 31) * 8;
+      st8((bf16_t*)part + i * 256 + d0, pack8(&sO[(64 * g + i) * kDecOP + d0]));
+    }
+    if (tid < 64) {
+      part[kDecPO + tid] = sMq[64 * g + tid];
+      part[kDecPO + 64 + tid] = sLq[64 * g + tid];
+    }
   }
 }
 
@@ -1242,6 +1291,15 @@ static DecodePlan plan_decode(const fvx_attn_desc& d) {
   if (splits <= 0) splits = (128 + groups - 1) / groups;
   if (splits > tiles) splits = tiles;
   if (splits < 1) splits = 1;
+  if (d.kv_splits <= 0 && (tiles + splits - 1) / splits * kDecKT >= kDecTKps) {
+    // the prefix kernel (ranges of >= 4 tiles): as many ranges as keep its
+    // 32 kDtNW-row workgroups within one per CU, each range >= 4 tiles
+    const int64_t wg_groups =
+        ((int64_t)a.n_rb * 64 + 32 * kDtNW - 1) / (32 * kDtNW) * d.n_problems;
+    splits = kDtTargetWgs / wg_groups;
+    while (splits > 1 && (tiles + splits - 1) / splits * kDecKT < kDecTKps) --splits;
+    if (splits < 1) splits = 1;
+  }
   const int64_t kps = (tiles + splits - 1) / splits * kDecKT;
   a.splits = (int)((d.sk + kps - 1) / kps);
   a.kps = kps;
@@ -1359,10 +1417,12 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
     // key ranges of >= 4 tiles (the prefix): attn_decode_t_kernel, ~8 %
     // faster there; one or two tiles per workgroup (the action expert): the
     // 4-wave kernel, whose fixed costs are lower
-    if (a.kps >= kDecTKps)
-      hipLaunchKernelGGL(attn_decode_t_kernel, dim3((unsigned)a.n_items), dim3(128),
-                         0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
-    else
+    if (a.kps >= kDecTKps) {
+      const int64_t groups = (a.n_rb * 64 + 32 * kDtNW - 1) / (32 * kDtNW);
+      const int64_t wgs = d.n_problems * a.splits * groups;
+      hipLaunchKernelGGL(attn_decode_t_kernel<kDtNW>, dim3((unsigned)wgs),
+                         dim3(64 * kDtNW), 0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
+    } else
       hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)(a.n_items + pf_wgs)),
                          dim3(256), 0, s, d, a.n_rb, a.splits, (int)a.kps, hs,
                          a.n_items);

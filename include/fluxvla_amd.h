@@ -304,10 +304,11 @@ int fvx_adarms_norm_locked(const void* x, const void* style,
  * the split partials are merged by a second kernel on the same stream.
  * Problems with a transposed value cache (v_d_stride > 0), head_dim 256 and
  * operand offsets below 2^30 elements run the decode kernels: a workgroup
- * owns 64 query rows and a key range of whole 64-key tiles staged through
- * LDS (about 128 workgroups by default, or kv_splits ranges).  Key ranges
- * of 4 tiles or more (the prefix) run a transposed-score kernel; shorter
- * ranges (the bs=1 action expert) a 4-wave kernel with lower fixed cost.
+ * owns 64 or 128 query rows and a key range of whole 64-key tiles staged
+ * through LDS (about 128 64-row groups x ranges by default, or kv_splits
+ * ranges).  Key ranges of 4 tiles or more (the prefix) run a transposed-
+ * score kernel (128 rows per workgroup); shorter ranges (the bs=1 action
+ * expert) a 4-wave kernel with lower fixed cost.
  */
 typedef struct fvx_attn_desc {
   const void* q; int64_t q_tok_stride, q_head_stride, q_zs1, q_zs2;

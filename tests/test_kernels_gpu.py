@@ -403,6 +403,32 @@ def test_attention_prefix_padded(K, cuda):
     assert rel_err(o[:, pad], ref[:, pad]) <= REL_TOL
 
 
+@pytest.mark.parametrize('splits', [1, 2, 3])
+@pytest.mark.parametrize('batch', [1, 2])
+def test_attention_prefix_key_ranges(K, cuda, splits, batch):
+    """Transposed value cache with ranges of >= 4 key tiles (the prefix
+    kernel): 600 tokens x 8 heads are 75 row groups of 64, an odd count,
+    so the last workgroup of a 128-row kernel has one group past the end;
+    the last range is partial, and padded keys sit inside a range."""
+    announce(f'attention prefix key ranges splits={splits} batch={batch}')
+    S, H, D, T = 600, 8, 256, 640
+    q = randn((batch, S, H, D), 86)
+    k = randn((batch, T, D), 87)
+    v = randn((batch, T, D), 88)
+    kgrp = torch.zeros(batch, S, dtype=torch.int32)
+    kgrp[-1, 130:170] = 2**31 - 1
+    kgrp[:, 580:] = 2**31 - 1
+    qgrp = torch.zeros(batch, S, dtype=torch.int32)
+    o = torch.empty(batch, S, H, D, dtype=torch.bfloat16, device=cuda)
+    vt = v.transpose(1, 2).contiguous().to(cuda)
+    K.mqa_attention(q.to(cuda), k.to(cuda)[:, :S], vt, o, kgrp.to(cuda),
+                    qgrp.to(cuda), kv_splits=splits, v_transposed=True)
+    mask = (kgrp[:, None, :] <= qgrp[:, :, None])
+    ref = sdpa_ref(q.float().transpose(1, 2), k[:, :S].float()[:, None],
+                   v[:, :S].float()[:, None], mask).transpose(1, 2)
+    assert rel_err(o, ref) <= REL_TOL
+
+
 @pytest.mark.parametrize('splits', [0, 1, 5, 14])
 @pytest.mark.parametrize('vt', [False, True])
 @pytest.mark.parametrize('batch', [1, 3])
