@@ -9,8 +9,9 @@
 //    waves on v_mfma_f32_32x32x16_bf16 (fp8: the block-scaled 32x32x64), K in
 //    64-wide slabs through a 3- or 4-stage LDS ring filled by LDS DMA
 //    (buffer_load ... lds), the slab loads spread between MFMA groups.
-//  * gemm_wide_kernel<MODE, SUM_A> / gemm_wide_f8_kernel: 256 x 256 tiles of
-//    4 waves (128 x 128 each, accumulators in AGPRs) for the prefix gate/up
+//  * gemm_wide_kernel<MODE, SUM_A, NWV> / gemm_wide_f8_kernel: 256 x 256
+//    tiles of 8 waves (64 x 128 each; fp8: 4 waves of 128 x 128, the
+//    accumulators in AGPRs) for the prefix gate/up
 //    at every batch, batched prefixes, and -- over up to 8 K ranges, one
 //    per XCD -- long-K GEMMs with few tiles (the prefix down projection).
 //  * gemm_skinny_kernel<MODE, FP8>: M <= 64 (the bs=1 action expert,
@@ -789,19 +790,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 // gemm_wide_kernel: large-M GEMMs (the prefix gate/up projection at every
 // batch; the other prefix and SigLIP GEMMs once a batch gives them >= 128
 // such tiles).  A 256 x 256 tile (GEGLU: 256 rows x 128 columns of each
-// weight) for 4 waves; wave (wm, wn) owns rows 128 wm .. + 127 and columns
-// 128 wn .. + 127 (GEGLU: 64 wn .. + 63 of both weights), i.e. 16 32x32
-// accumulators held in AGPRs, so 8 fragment reads from LDS feed 16 MFMAs
-// (the 8-wave 128 x 64 split of gemm_tile_kernel needs 12 for 16).
-// Each wave loads one 128-row band of every slab by LDS DMA (waves 0, 1 the
-// A rows, 2 and 3 the B rows: GEGLU the gate and the up rows): per load one
+// weight) for NWV waves.  With 4, wave (wm, wn) owns rows 128 wm .. + 127
+// and columns 128 wn .. + 127 (GEGLU: 64 wn .. + 63 of both weights), 16
+// 32x32 accumulators, so 8 fragment reads from LDS feed 16 MFMAs; with 8
+// (two waves per SIMD, the build's choice) rows 64 wm .. + 63 of the same
+// columns, 8 accumulators, 6 reads for 8 MFMAs -- more LDS bytes per MFMA,
+// but the second wave on a SIMD issues its LDS reads while the first waits.
+// Each wave loads one 512 / NWV-row band of every slab by LDS DMA (the first
+// half of the waves the A rows, the others the B rows: GEGLU the gate, then
+// the up rows): per load one
 // VGPR offset, the slab advance in the scalar offset, rows past the operand
 // out of the buffer view (zeros).  K moves in 64-wide slabs through a
-// 2-stage ring; K % 64 == 0, one pass (no split).  The slab's 16 loads per
-// wave are spread between MFMA groups, two after each group of 4 (issued in
-// one burst they fill the texture-address queue and hold the MFMAs back):
-// loads 0..7 of slab t + 2 during the last k step of slab t, 8..15 during
-// the first k step of slab t + 1.  The one barrier per slab sits before the
+// 2-stage ring; K % 64 == 0, one pass (no split).  The slab's 16 (8 waves:
+// 8) loads per wave are spread between MFMA groups, two after each group
+// (issued in one burst they fill the texture-address queue and hold the
+// MFMAs back): the first half of slab t + 2's during the last k step of
+// slab t, the second half during the first k step of slab t + 1.  The one barrier per slab sits before the
 // last k step: it publishes slab t + 1 and frees slab t's stage, and the
 // first fragments of slab t + 1 are read while that step's MFMAs run.
 // LDS rows are 128 bytes with the 16-byte chunk index XOR (row >> 1) & 7,
@@ -814,14 +818,31 @@ constexpr int kGwBM = 256, kGwBN = 256;  // rows, columns (GEGLU: 2 x 128)
 #endif
 constexpr int kGwStage = 512 * 128;
 constexpr int kGwELD = 128 + 4;          // epilogue scratch stride (floats)
+// waves of the bf16 wide kernel: 8 (prefix GeGLU 119 -> 110 us, chunk
+// 16.8 -> 16.4 ms against 4)
+template <int MODE>
+constexpr int wide_waves() { return 8; }
 
-template <int MODE, bool SUM_A>  // SUM_A: the fused RMSNorm sums A's squares here
-__global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_tiles,
-                                                           int n_tiles, int vec_ok,
-                                                           int splits, int kchunk) {
+// NWV waves: 4 (one per SIMD; wave (wm, wn) of 2 x 2 owns 128 rows) or 8
+// (two per SIMD, 4 x 2 waves of 64 rows: half the accumulators per wave, so
+// that a second wave on each SIMD hides the LDS reads of the first -- one
+// wave per SIMD gets ~1 KB per 40-50 cycles out of the LDS, two ~1 KB per
+// 25).
+template <int NWV>
+constexpr int wide_lds_bytes() {
+  return 2 * kGwStage > NWV * 32 * kGwELD * 4 ? 2 * kGwStage : NWV * 32 * kGwELD * 4;
+}
+
+template <int MODE, bool SUM_A, int NWV>  // SUM_A: the fused RMSNorm sums A's squares here
+__global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int m_tiles,
+                                                                int n_tiles, int vec_ok,
+                                                                int splits, int kchunk) {
   constexpr bool GG = MODE == FVX_GEMM_GEGLU;
   constexpr int WNO = GG ? 64 : 128;  // output columns per wave
-  __shared__ __align__(16) char smem[2 * kGwStage];
+  constexpr int WM = NWV == 8 ? 64 : 128, RB = WM / 32;  // rows, row blocks per wave
+  constexpr int BAND = 512 / NWV, LW = BAND / 8;          // DMA band rows, loads per slab
+  static_assert(NWV == 4 || NWV == 8, "4 or 8 waves");
+  __shared__ __align__(16) char smem[wide_lds_bytes<NWV>()];
   __shared__ float sRow[kGwBM];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -840,21 +861,24 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   const int64_t kb = (int64_t)split * kchunk;
   const int nk = (int)(((kb + kchunk < K ? kb + kchunk : K) - kb) / 64);
 
-  // this wave's band: 128 rows of A (waves 0, 1) or of B (2, 3)
-  const bool isa = wave < 2;
-  const int64_t r0 = isa ? m0 + 128 * wave : (GG ? n0 : n0 + 128 * (wave - 2));
+  // this wave's band: BAND rows of A (the first NWV / 2 waves) or of B (the
+  // others; GEGLU: the gate rows, then the up rows)
+  const int bw = wave - NWV / 2;
+  const bool isa = bw < 0;
+  const int64_t r0 = isa ? m0 + BAND * wave
+                         : n0 + BAND * (GG ? bw % (NWV / 4) : bw);
   const int64_t rlim = (isa ? M : N) - r0;
-  const int64_t nrows = rlim <= 0 ? 0 : (rlim < 128 ? rlim : 128);
+  const int64_t nrows = rlim <= 0 ? 0 : (rlim < BAND ? rlim : BAND);
   const uint32_t ld2 = (uint32_t)(isa ? p.lda : p.ldb) * 2;
   const bf16_t* band = isa ? (const bf16_t*)p.a + r0 * p.lda + kb
-                           : (const bf16_t*)((GG && wave == 3) ? p.b2 : p.b) + r0 * p.ldb + kb;
+                           : (const bf16_t*)((GG && bw >= NWV / 4) ? p.b2 : p.b) + r0 * p.ldb + kb;
   const i32x4_t rs = make_rsrc4(band, (uint32_t)(nrows * ld2));
-  // load i: LDS rows 128 wave + 8 i + (lane >> 3), slot lane & 7 holds global
-  // chunk slot ^ (((8 i + (lane >> 3)) >> 1) & 7)
+  // load i: LDS rows BAND wave + 8 i + (lane >> 3), slot lane & 7 holds
+  // global chunk slot ^ (((8 i + (lane >> 3)) >> 1) & 7)
   const int lr = lane >> 3, lc = lane & 7;
   const uint32_t vo0 = (uint32_t)lr * ld2 + 16u * (uint32_t)(lc ^ (lr >> 1));
   const uint32_t vo1 = (uint32_t)lr * ld2 + 16u * (uint32_t)(lc ^ (lr >> 1) ^ 4);
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * 128 * 128);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem) + wave * BAND * 128);
   // load i (8 rows of the band) of slab t into ring stage `stage`
   auto issue1 = [&](int t, int stage, int i) {
     load_lds16_so(rs, lds0 + stage * kGwStage + i * 1024,
@@ -862,44 +886,46 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   };
   auto issue = [&](int t, int stage) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) issue1(t, stage, i);
+    for (int i = 0; i < LW; ++i) issue1(t, stage, i);
   };
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[RB][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+  float ss[RB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) ss[i] = 0.f;
   const int sw = (lane >> 1) & 7, fr = lane & 31, hk = lane >> 5;
   // LDS row of B fragment j of this wave (GEGLU: gate blocks, then up)
   auto brow = [&](int j) {
     return GG ? 256 + (j >> 1) * 128 + wn * 64 + 32 * (j & 1) : 256 + wn * 128 + 32 * j;
   };
   issue(0, 0);
-  // handed-over row sums: thread t takes row m0 + t (waits with slab 0)
+  // handed-over row sums: thread t < 256 takes row m0 + t (waits with slab 0)
   float ss_pre = 0.f;
-  if (!SUM_A && p.rownorm && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
-  bf16x8 af[2][4], bfr[2][4];
+  if (!SUM_A && p.rownorm && tid < kGwBM && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
+  bf16x8 af[2][RB], bfr[2][4];
   auto rd = [&](int stage, int ks, int b) {
     const char* s = smem + stage * kGwStage;
     const int cpos = ((2 * ks + hk) ^ sw) * 16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      af[b][i] = *(const bf16x8*)(s + (wm * 128 + 32 * i + fr) * 128 + cpos);
+    for (int i = 0; i < RB; ++i)
+      af[b][i] = *(const bf16x8*)(s + (wm * WM + 32 * i + fr) * 128 + cpos);
 #pragma unroll
     for (int j = 0; j < 4; ++j) bfr[b][j] = *(const bf16x8*)(s + (brow(j) + fr) * 128 + cpos);
   };
   // 32-row blocks of this wave that hold rows < M (the last M tile of the
   // prefix, 816 = 3 x 256 + 48 rows, has 2 of 8): the others skip their
   // MFMAs, so that tile finishes early and its CU takes the next one
-  bool blk_ok[4];
+  bool blk_ok[RB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) blk_ok[i] = m0 + wm * 128 + 32 * i < M;
-  for (int x = 0; x < 8; ++x) issue1(nk > 1 ? 1 : 0, 1, x);
-  wait_vmcnt<8>();
+  for (int i = 0; i < RB; ++i) blk_ok[i] = m0 + wm * WM + 32 * i < M;
+  for (int x = 0; x < LW / 2; ++x) issue1(nk > 1 ? 1 : 0, 1, x);
+  wait_vmcnt<LW / 2>();
   __syncthreads();
   rd(0, 0, 0);
   for (int t = 0; t < nk; ++t) {
@@ -916,18 +942,22 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
         rd(st ^ 1, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
+      // the wave's LW loads of a slab: the second half of slab t + 1's in
+      // k step 0, the first half of slab t + 2's in k step 3 (after the
+      // barrier that frees its stage), LW / (2 RB) after each MFMA group
+      constexpr int PG = LW / (2 * RB);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < RB; ++i) {
         if (SUM_A) ss[i] += sumsq8(af[b][i]);
         if (blk_ok[i])
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
-        if (ks == 0) {
-          issue1(t1, st ^ 1, 8 + 2 * i);
-          issue1(t1, st ^ 1, 9 + 2 * i);
-        } else if (ks == 3) {
-          issue1(t2, st, 2 * i);
-          issue1(t2, st, 2 * i + 1);
+#pragma unroll
+        for (int g = 0; g < PG; ++g) {
+          if (ks == 0)
+            issue1(t1, st ^ 1, LW / 2 + PG * i + g);
+          else if (ks == 3)
+            issue1(t2, st, PG * i + g);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -938,12 +968,12 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   // row sums of squares: lanes l and l ^ 32 hold the two k halves of row
   // l % 32 of block i
   if (!SUM_A) {
-    sRow[tid] = ss_pre;
+    if (tid < kGwBM) sRow[tid] = ss_pre;
   } else if (wn == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RB; ++i) {
       const float s2 = ss[i] + __shfl_xor(ss[i], 32, 64);
-      if (lane < 32) sRow[wm * 128 + 32 * i + lane] = s2;
+      if (lane < 32) sRow[wm * WM + 32 * i + lane] = s2;
     }
   }
   __syncthreads();  // also: every wave is done with the ring
@@ -951,7 +981,10 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
   // each 32-row block through the wave's LDS scratch [32][kGwELD] (GEGLU:
   // gate columns 0..63, up 64..127); lane item q: row q / CH, 8 columns
   // 8 (q % CH) with CH = WNO / 8 chunks per row
-  constexpr int CH = WNO / 8, ITEMS = 32 * CH / 64, EB = FVX_WIDE_EB < ITEMS ? FVX_WIDE_EB : ITEMS;
+  // (EB items' epilogue inputs in flight; PLAIN's, with 8 waves, one at a
+  // time: more do not fit the 256 registers of two waves per SIMD)
+  constexpr int EB0 = NWV == 8 && MODE == FVX_GEMM_PLAIN ? 1 : FVX_WIDE_EB;
+  constexpr int CH = WNO / 8, ITEMS = 32 * CH / 64, EB = EB0 < ITEMS ? EB0 : ITEMS;
   float* scr = (float*)smem + wave * 32 * kGwELD;
   const int64_t nw0 = n0 + wn * WNO;
   // block i of the accumulators -> scratch (compile-time indices, so the
@@ -967,14 +1000,14 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p, int m_til
         scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * kGwELD + 32 * j + fr] = acc[i][j][r];
   };
 #pragma unroll 1
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < RB; ++i) {
     switch (i) {
       case 0: to_scr(IntC<0>{}); break;
       case 1: to_scr(IntC<1>{}); break;
-      case 2: to_scr(IntC<2>{}); break;
-      default: to_scr(IntC<3>{}); break;
+      case 2: to_scr(IntC<2 % RB>{}); break;
+      default: to_scr(IntC<3 % RB>{}); break;
     }
-    const int64_t rb = m0 + wm * 128 + 32 * i;
+    const int64_t rb = m0 + wm * WM + 32 * i;
     if (splits > 1) {
       // fp32 partials of this K range: ws[(split M + m) N + n]
       float* ws = (float*)((char*)p.workspace + kCounterBytes) + (int64_t)split * M * N;
@@ -2182,13 +2215,17 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     // splits, (split, tile) workgroups
     const unsigned nb = (unsigned)(m_tiles * n_tiles);
     const unsigned nbs = nb * (unsigned)splits;
-#define LW(MODE)                                                                     \
-  if (d.rownorm && !d.ss_in)                                                         \
-    hipLaunchKernelGGL((gemm_wide_kernel<MODE, true>), dim3(nbs), dim3(256), 0, s, d,  \
-                       m_tiles, n_tiles, vec_ok, splits, (int)kchunk);               \
-  else                                                                               \
-    hipLaunchKernelGGL((gemm_wide_kernel<MODE, false>), dim3(nbs), dim3(256), 0, s, d, \
-                       m_tiles, n_tiles, vec_ok, splits, (int)kchunk)
+#define LW(MODE)                                                                       \
+  if (d.rownorm && !d.ss_in)                                                           \
+    hipLaunchKernelGGL((gemm_wide_kernel<MODE, true, wide_waves<MODE>()>), dim3(nbs),    \
+                       dim3(64 * wide_waves<MODE>()), 0, s, d, m_tiles, n_tiles, vec_ok, \
+                       splits,                                                         \
+                       (int)kchunk);                                                   \
+  else                                                                                 \
+    hipLaunchKernelGGL((gemm_wide_kernel<MODE, false, wide_waves<MODE>()>), dim3(nbs),   \
+                       dim3(64 * wide_waves<MODE>()), 0, s, d, m_tiles, n_tiles, vec_ok, \
+                       splits,                                                         \
+                       (int)kchunk)
     // the e4m3 copy of A is used when given (a rownorm then needs ss_in)
     const bool f8a = d.a8 && d.a8_scale && (!d.rownorm || d.ss_in);
 #define LW8(MODE)                                                                           \
