@@ -327,15 +327,19 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), written through the
-  // identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)).
-  const float k2 = 1.5957691216057308f;  // 2 * sqrt(2 / pi)
-  float u = k2 * (x + 0.044715f * x * x * x);
-  // hardware reciprocal (1 ulp) instead of the IEEE division sequence
-  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-u));
+  // identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)) with the exponent in
+  // base 2 and its constants folded: exp(-2u) = 2^(x (a + b x^2)).  The
+  // hardware exp2 and reciprocal (1 ulp) replace the library exp and the
+  // IEEE division; at the ends of the range the reciprocal of 1 + inf is 0
+  // and of 1 + 0 is 1, the limits of the sigmoid.
+  constexpr float a = -1.5957691216057308f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+  constexpr float b = a * 0.044715f;
+  const float t = x * fmaf(b, x * x, a);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 __device__ __forceinline__ float silu(float x) {
-  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
 }  // namespace fvx
