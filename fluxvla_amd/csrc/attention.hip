@@ -382,6 +382,23 @@ constexpr int kDecOP = 256 + 4;                 // LDS pitch (floats), O rows
 // row references and the 64 row sums (fp32); sizes in floats
 constexpr int64_t kDecPO = 64 * 256 / 2;
 constexpr int64_t kDecPF = kDecPO + 2 * 64;
+// An attention workspace opens with the 64-row groups' arrival counters of
+// the in-launch merge (one 256-byte line each); the split partials follow.
+constexpr int64_t kAttnCounterBytes = 64 * 1024;
+constexpr int kAttnMaxGroups = (int)(kAttnCounterBytes / 256);  // a 256-byte line each
+constexpr int kDecMergeSpin = 1 << 16;  // polls before a merge stops waiting
+
+// The value of a 32-bit word as the L2 holds it: a returning atomic add of 0
+// (written out here: the compiler turns an idempotent atomic into a load,
+// which may be served by the CU's L1 and never see another CU's update).
+__device__ __forceinline__ uint32_t l2_atomic_read(uint32_t* p) {
+  uint32_t v;
+  asm volatile("global_atomic_add %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)"
+               : "=v"(v)
+               : "v"(p), "v"(0u)
+               : "memory");
+  return v;
+}
 // LDS map (bytes): two stages of [K tile 64 x 512 B | V^T tile 256 x 128 B]
 // (stage 1 first holds the Q rows), then P [2][64][kDecPP] bf16, the row
 // maxima [2][64][4] f32, the key groups [2][4 waves][64] and the query
@@ -477,25 +494,132 @@ __device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
   wait_vmcnt<0>();
 }
 
+// Row r (problem z), dims d0 .. d0 + 7 of the merged output from the split
+// partials of its 64-row group: the loads of up to 16 splits in flight, then
+// the running-max merge in split order.  AUX: the loads' cache policy (0 for
+// partials of an earlier launch; 1, missing in the vector L1, for partials
+// other CUs of the XCD wrote in this launch).
+template <int AUX>
+__device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int splits,
+                                           int hs, int z, int r, int d0) {
+  const int rg = r >> 6, i = r & 63;
+  const float* base = (const float*)p.workspace + (((int64_t)z * n_rg + rg) * splits) * kDecPF;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, M = -INFINITY, L = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += 16) {
+    bf16x8 a[16];
+    float mv[16], lv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      // splits past the end read as zero (out of the buffer view)
+      const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
+      a[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rw, off + (uint32_t)(i * 256 + d0) * 2, 0, AUX));
+      mv[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          rw, off + (uint32_t)(kDecPO + i) * 4, 0, AUX));
+      lv[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          rw, off + (uint32_t)(kDecPO + 64 + i) * 4, 0, AUX));
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (s0 + u < splits) {
+        const float mn = fmaxf(M, mv[u]);
+        const float mr = (mn == -INFINITY) ? 0.f : mn;
+        const float wa = exp2f(M - mr), wb = exp2f(mv[u] - mr);
+        float av[8];
+        unpack8(a[u], av);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = acc[e] * wa + av[e] * wb;
+        L = L * wa + lv[u] * wb;
+        M = mn;
+      }
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] *= inv;
+  dec_store<8>(p, z, r, d0, hs, acc);
+}
+
+// One merging workgroup of the in-launch merge: 8 rows (chunk) of 64-row
+// group G = z n_rg + rg, 256 threads of (row, 8 dims), on the group's XCD.
+// Thread 0 polls the group's arrival counter (an L2 atomic) until it reaches
+// `splits` -- every range's workgroup has a lower block index on the same
+// XCD, so it was dispatched first, and it waits on nothing; the wait is
+// bounded regardless -- then the partials are read from that XCD's L2.  The
+// group's last merging workgroup resets both of its counters.
+__device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, int hs,
+                             uint32_t* counters, int grp, int chunk) {
+  const int tid = threadIdx.x;
+  const int R = (int)(p.sq * p.heads);
+  const int z = grp / n_rg, rg = grp % n_rg;
+  const int r = rg * 64 + 8 * chunk + (tid >> 5), d0 = (tid & 31) * 8;
+  uint32_t* ctr = counters + (int64_t)grp * 64;
+  if (tid == 0) {
+#pragma unroll 1
+    for (int it = 0; it < kDecMergeSpin; ++it) {
+      if (l2_atomic_read(ctr) >= (uint32_t)splits) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+  dec_merge8<1>(p, n_rg, splits, hs, z, r, d0);
+  if (tid == 0) {
+    const int rows = R - rg * 64 < 64 ? R - rg * 64 : 64;
+    const uint32_t old =
+        __hip_atomic_fetch_add(ctr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (old == (uint32_t)(rows / 8 - 1)) {
+      __hip_atomic_exchange(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_exchange(ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+}
+
+// counters != NULL: the key ranges of each 64-row group G = z n_rg + rg
+// merge inside the launch, all on XCD G % 8 (block b runs on XCD b & 7).
+// Blocks [0, n_items) compute: slot b >> 3 of XCD b & 7 is range slot %
+// splits of the XCD's group slot / splits.  Blocks [n_items, merge_first)
+// merge: slot j of XCD x takes rows 8 (j % 8) .. + 7 of the XCD's group
+// j / 8.  The rest prefetch.  A range's partial goes to the XCD's L2 and is
+// then counted in counters[64 G] (a 256-byte line per group; [64 G + 1]
+// counts the group's merging workgroups).  Slots past the groups (or past
+// R) do nothing.  n_items and merge_first are multiples of 8.
 __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
                                                           int n_rg, int splits,
                                                           int kps, int hs,
-                                                          int n_items) {
+                                                          int n_items,
+                                                          uint32_t* counters,
+                                                          int merge_first) {
   constexpr int HD = 256, KT = kDecKT;
   __shared__ __align__(16) unsigned char smem[kDecLDS];
   __shared__ float sL[4][64], sM[64];
-  if ((int)blockIdx.x >= n_items) {
-    dec_prefetch(p, (int)blockIdx.x - n_items, (int)gridDim.x - n_items, n_items, smem);
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int n_groups = (int)p.n_problems * n_rg;
+  if (counters && (int)blockIdx.x >= n_items && (int)blockIdx.x < merge_first) {
+    const int j = slot - n_items / 8, grp = xcd + 8 * (j / 8);
+    if (grp < n_groups && (grp % n_rg) * 64 + 8 * (j % 8) < (int)(p.sq * p.heads))
+      dec_merge_wg(p, n_rg, splits, hs, counters, grp, j % 8);
+    return;
+  }
+  const int pf0 = counters ? merge_first : n_items;
+  if ((int)blockIdx.x >= pf0) {
+    dec_prefetch(p, (int)blockIdx.x - pf0, (int)gridDim.x - pf0, pf0, smem);
     return;
   }
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, g = lane >> 4;
-  // XCD-aware order: consecutive items (the row groups of one key range)
-  // land on one XCD and share its L2 copy of the range's K / V tiles.
-  const int nb = n_items, q8 = nb >> 3, r8 = nb & 7;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
+  int item;
+  if (counters) {
+    const int grp = xcd + 8 * (slot / splits);
+    if (grp >= n_groups) return;  // an empty slot
+    item = ((grp / n_rg) * splits + slot % splits) * n_rg + grp % n_rg;
+  } else {
+    // XCD-aware order: consecutive items (the row groups of one key range)
+    // land on one XCD and share its L2 copy of the range's K / V tiles.
+    const int nb = n_items, q8 = nb >> 3, r8 = nb & 7;
+    item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
+  }
   const int rg = item % n_rg;
   const int split = (item / n_rg) % splits;
   const int z = item / (n_rg * splits);
@@ -756,6 +880,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     part[kDecPO + tid] = sM[tid];
     part[kDecPO + 64 + tid] = ((sL[0][tid] + sL[1][tid]) + sL[2][tid]) + sL[3][tid];
   }
+  if (!counters) return;
+  // the partial is in this XCD's L2 before it is counted
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0)
+    __hip_atomic_fetch_add(counters + ((int64_t)z * n_rg + rg) * 64, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 
@@ -1173,40 +1304,7 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
   const int d0 = (gid & 31) * 8;
   const int zr = gid >> 5;
   const int z = zr / R, r = zr % R;
-  const int rg = r >> 6, i = r & 63;
-  const float* base = (const float*)p.workspace + (((int64_t)z * n_rg + rg) * splits) * kDecPF;
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, M = -INFINITY, L = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += 16) {
-    bf16x8 a[16];
-    float mv[16], lv[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      // splits past the end read as zero (out of the buffer view)
-      const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
-      a[u] = bload8(rw, off + (uint32_t)(i * 256 + d0) * 2);
-      mv[u] = bload1f(rw, off + (uint32_t)(kDecPO + i) * 4);
-      lv[u] = bload1f(rw, off + (uint32_t)(kDecPO + 64 + i) * 4);
-    }
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      if (s0 + u < splits) {
-        const float mn = fmaxf(M, mv[u]);
-        const float mr = (mn == -INFINITY) ? 0.f : mn;
-        const float wa = exp2f(M - mr), wb = exp2f(mv[u] - mr);
-        float av[8];
-        unpack8(a[u], av);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = acc[e] * wa + av[e] * wb;
-        L = L * wa + lv[u] * wb;
-        M = mn;
-      }
-    }
-  }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] *= inv;
-  dec_store<8>(p, z, r, d0, hs, acc);
+  dec_merge8<0>(p, n_rg, splits, hs, z, r, d0);
 }
 
 struct AttnPlan {
@@ -1237,7 +1335,7 @@ static AttnPlan plan_attn(const fvx_attn_desc& d) {
   a.kps = splits == 1 ? ((d.sk + kKeyTile - 1) / kKeyTile) * kKeyTile : kps;
   const int64_t pf = a.hdp == 256 ? attn_part_floats<256, 256>()
                                   : attn_part_floats<96, 80>();
-  a.ws_bytes = splits > 1 ? blocks * splits * pf * 4 : 0;
+  a.ws_bytes = splits > 1 ? kAttnCounterBytes + blocks * splits * pf * 4 : 0;
   return a;
 }
 
@@ -1304,7 +1402,7 @@ static DecodePlan plan_decode(const fvx_attn_desc& d) {
   a.splits = (int)((d.sk + kps - 1) / kps);
   a.kps = kps;
   a.n_items = (int)(groups * a.splits);
-  a.ws_bytes = a.splits > 1 ? (int64_t)a.n_items * kDecPF * 4 : 0;
+  a.ws_bytes = a.splits > 1 ? kAttnCounterBytes + (int64_t)a.n_items * kDecPF * 4 : 0;
   return a;
 }
 
@@ -1313,6 +1411,20 @@ extern "C" int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d) {
     return 0;
   if (use_decode(*d)) return plan_decode(*d).ws_bytes;
   return plan_attn(*d).ws_bytes;
+}
+
+// The descriptor the kernels see: the split partials start past the arrival
+// counters that open every attention workspace.
+static fvx_attn_desc past_counters(const fvx_attn_desc& d) {
+  fvx_attn_desc k = d;
+  if (d.workspace && d.workspace_bytes >= kAttnCounterBytes) {
+    k.workspace = (char*)d.workspace + kAttnCounterBytes;
+    k.workspace_bytes = d.workspace_bytes - kAttnCounterBytes;
+  } else {
+    k.workspace = nullptr;
+    k.workspace_bytes = 0;
+  }
+  return k;
 }
 
 static int run_generic(const fvx_attn_desc& d, hipStream_t s) {
@@ -1327,22 +1439,23 @@ static int run_generic(const fvx_attn_desc& d, hipStream_t s) {
   }
   FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
               "attention: workspace must be 16B aligned");
+  const fvx_attn_desc dk = past_counters(d);
   dim3 grid((unsigned)a.n_row_blocks, (unsigned)a.splits,
             (unsigned)d.n_problems);
   if (a.hdp == 256)
-    hipLaunchKernelGGL((attn_kernel<256, 256>), grid, dim3(256), 0, s, d,
+    hipLaunchKernelGGL((attn_kernel<256, 256>), grid, dim3(256), 0, s, dk,
                        a.n_row_blocks, a.splits, a.kps);
   else
-    hipLaunchKernelGGL((attn_kernel<96, 80>), grid, dim3(256), 0, s, d,
+    hipLaunchKernelGGL((attn_kernel<96, 80>), grid, dim3(256), 0, s, dk,
                        a.n_row_blocks, a.splits, a.kps);
   int st = launch_status("attention");
   if (st || a.splits == 1) return st;
   dim3 mgrid((unsigned)a.n_row_blocks, 1u, (unsigned)d.n_problems);
   if (a.hdp == 256)
     hipLaunchKernelGGL((attn_merge_kernel<256, 256>), mgrid, dim3(256), 0, s,
-                       d, a.n_row_blocks, a.splits);
+                       dk, a.n_row_blocks, a.splits);
   else
-    hipLaunchKernelGGL((attn_merge_kernel<96, 80>), mgrid, dim3(256), 0, s, d,
+    hipLaunchKernelGGL((attn_merge_kernel<96, 80>), mgrid, dim3(256), 0, s, dk,
                        a.n_row_blocks, a.splits);
   return launch_status("attention");
 }
@@ -1406,12 +1519,23 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "attention: workspace must be 16B aligned");
     const int hs = (d.heads & (d.heads - 1)) == 0 ? __builtin_ctzll((uint64_t)d.heads) : -1;
+    const fvx_attn_desc dk = past_counters(d);
+    // the 4-wave kernel's in-launch merge: each 64-row group's ranges and
+    // its 8 merging workgroups on one XCD, all of them resident at once
+    // (R % 8 == 0: a merging workgroup's 8 rows lie in one group)
+    const int64_t R = d.sq * d.heads;
+    const int groups = (int)(d.n_problems * a.n_rb);
+    const int gpx = (groups + 7) / 8;  // groups per XCD
+    const bool fused = a.kps < kDecTKps && a.splits > 1 && R % 8 == 0 &&
+                       groups <= kAttnMaxGroups && gpx * (a.splits + 8) <= device_cus() / 8;
+    const int item_blocks = fused ? 8 * gpx * a.splits : a.n_items;
+    const int merge_blocks = fused ? 64 * gpx : 0;
     int pf_wgs = 0;  // prefetch workgroups (the 4-wave kernel only)
     if (a.kps < kDecTKps && has_prefetch(d)) {
       pf_wgs = d.prefetch_wgs;
       if (pf_wgs <= 0) {
-        const int cus = device_cus();
-        pf_wgs = cus > a.n_items ? cus - a.n_items : 0;
+        const int cus = device_cus(), used = item_blocks + merge_blocks;
+        pf_wgs = cus > used ? cus - used : 0;
       }
     }
     // key ranges of >= 4 tiles (the prefix): attn_decode_t_kernel, ~8 %
@@ -1421,17 +1545,19 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
       const int64_t groups = (a.n_rb * 64 + 32 * kDtNW - 1) / (32 * kDtNW);
       const int64_t wgs = d.n_problems * a.splits * groups;
       hipLaunchKernelGGL(attn_decode_t_kernel<kDtNW>, dim3((unsigned)wgs),
-                         dim3(64 * kDtNW), 0, s, d, a.n_rb, a.splits, (int)a.kps, hs);
+                         dim3(64 * kDtNW), 0, s, dk, a.n_rb, a.splits, (int)a.kps, hs);
     } else
-      hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)(a.n_items + pf_wgs)),
-                         dim3(256), 0, s, d, a.n_rb, a.splits, (int)a.kps, hs,
-                         a.n_items);
+      hipLaunchKernelGGL(attn_decode_kernel,
+                         dim3((unsigned)(item_blocks + merge_blocks + pf_wgs)), dim3(256), 0,
+                         s, dk, a.n_rb, a.splits, (int)a.kps, hs, item_blocks,
+                         fused ? (uint32_t*)d.workspace : nullptr,
+                         item_blocks + merge_blocks);
     int st = launch_status("attention(decode)");
-    if (st || a.splits == 1) return st;
+    if (st || a.splits == 1 || fused) return st;
     const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 32;
     hipLaunchKernelGGL(attn_decode_merge_kernel,
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                       d, a.n_rb, a.splits, hs);
+                       dk, a.n_rb, a.splits, hs);
     return launch_status("attention(decode merge)");
   }
   return run_generic(d, s);

@@ -17,11 +17,11 @@
  *     problem (thread-local).  Nothing aborts the process.
  *   - Split-K GEMMs and split-KV attention need a device workspace for
  *     their fp32 partials (size from fvx_gemm_workspace_bytes /
- *     fvx_attention_workspace_bytes).  Attention needs no initial contents.
- *     A GEMM workspace holds per-tile arrival counters in its first 4 KiB:
- *     zero them once before the first fvx_gemm call that uses the buffer;
- *     every call leaves them zero again.  Keep attention partials out of a
- *     GEMM workspace.  Calls on one stream may share a workspace; calls
+ *     fvx_attention_workspace_bytes).  A GEMM workspace holds per-tile
+ *     arrival counters in its first 4 KiB, an attention workspace per-row-
+ *     group arrival counters in its first 64 KiB: zero them once before the
+ *     first call that uses the buffer; every call leaves them zero again.
+ *     Keep GEMM and attention workspaces apart.  Calls on one stream may share a workspace; calls
  *     overlapping on different streams must not.  A NULL or too small
  *     workspace is an error (FVX_ERR_WORKSPACE) whenever the problem needs a
  *     split.
@@ -301,7 +301,12 @@ int fvx_adarms_norm_locked(const void* x, const void* style,
  * (fluxvla/engines/utils/model_utils.py:77-95): kgrp = pad ? cumsum(att) :
  * INT32_MAX, qgrp = cumsum(att).  Rows that see no key produce zeros.
  * kv_splits > 1 splits the key range across workgroups (needs workspace);
- * the split partials are merged by a second kernel on the same stream.
+ * the split partials are merged by a second kernel on the same stream, or,
+ * for key ranges of fewer than 4 tiles (the bs=1 action expert) with
+ * sq * heads % 8 == 0, by merging workgroups of the same launch: each
+ * 64-row group's ranges and mergers run on one XCD and meet through its L2;
+ * a merger waits (bounded) only for ranges that precede it in dispatch
+ * order and wait on nothing.
  * Problems with a transposed value cache (v_d_stride > 0), head_dim 256 and
  * operand offsets below 2^30 elements run the decode kernels: a workgroup
  * owns 64 or 128 query rows and a key range of whole 64-key tiles staged
