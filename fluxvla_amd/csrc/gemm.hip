@@ -46,10 +46,21 @@ constexpr int kCounterBytes = 4096;
 constexpr int kMaxSkinnyTiles = kCounterBytes / 4;
 
 
+// Row indices and the epilogue's periods (row_group, gate_group,
+// pos_period, rtc_period) are below 2^31 (the host checks), so quotients and
+// remainders take the 32-bit unsigned divide: the 64-bit one is a long
+// software sequence per lane.
+__device__ __forceinline__ uint32_t udiv32(int64_t a, int64_t b) {
+  return (uint32_t)a / (uint32_t)b;
+}
+__device__ __forceinline__ uint32_t umod32(int64_t a, int64_t b) {
+  return (uint32_t)a % (uint32_t)b;
+}
+
 __device__ __forceinline__ int64_t out_row(const GemmArgs& p, int64_t m) {
-  return p.row_group > 0
-             ? (m / p.row_group) * p.row_group_stride + (m % p.row_group)
-             : m;
+  if (p.row_group <= 0) return m;
+  const uint32_t q = udiv32(m, p.row_group);
+  return (int64_t)q * p.row_group_stride + ((uint32_t)m - q * (uint32_t)p.row_group);
 }
 
 // sum of squares of 8 bf16 values: four v_dot2c_f32_bf16 (fp32 accumulate)
@@ -154,14 +165,14 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.positions, rec_bytes(p.m * 4));
     const int64_t pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (uint32_t)(m * 4), 0, 0);
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.rope, 0x7fffffffu);
-    bl_f8(rr, rot ? (uint32_t)((pos * (hd >> 1) + ((n % hd) >> 1)) * 8) : kOOB, vec,
+    bl_f8(rr, rot ? (uint32_t)((pos * (hd >> 1) + (umod32(n, hd) >> 1)) * 8) : kOOB, vec,
           in.f0);
     return;
   }
   const int64_t N = p.n;
   in.bias = bl_b8(make_rsrc(p.bias, p.bias ? rec_bytes(N * 2) : 0u), (uint32_t)(n * 2), vec);
   // real-time chunking: row position within the chunk and the locked prefix
-  const int64_t rr = p.rtc_period > 0 ? m % p.rtc_period : 0;
+  const int64_t rr = p.rtc_period > 0 ? umod32(m, p.rtc_period) : 0;
   in.locked = false;
   if (p.rtc_lock) in.locked = rr < (int64_t)*p.rtc_lock;
   const float* bf = in.locked && p.bias_f32_locked ? p.bias_f32_locked : p.bias_f32;
@@ -175,15 +186,16 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
                     (uint32_t)(rr * 4));
     return;
   }
-  const int64_t gg = p.gate_group > 0 ? p.gate_group : 1;
-  in.gate = bl_b8(make_rsrc(p.gate, p.gate ? rec_bytes((p.m + gg - 1) / gg * p.ldg * 2) : 0u),
-                  (uint32_t)(((m / gg) * p.ldg + n) * 2), vec);
+  const bool gdiv = p.gate_group > 1;
+  const int64_t grows = gdiv ? udiv32(p.m + p.gate_group - 1, p.gate_group) : p.m;
+  in.gate = bl_b8(make_rsrc(p.gate, p.gate ? rec_bytes(grows * p.ldg * 2) : 0u),
+                  (uint32_t)(((gdiv ? udiv32(m, p.gate_group) : m) * p.ldg + n) * 2), vec);
   in.res = bl_b8(make_rsrc(p.residual,
                            p.residual ? rec_bytes((out_row(p, p.m - 1) + 1) * p.ldr * 2) : 0u),
                  (uint32_t)((out_row(p, m) * p.ldr + n) * 2), vec);
   const int64_t pp = p.pos_period > 0 ? p.pos_period : 1;
   in.pos = bl_b8(make_rsrc(p.pos, p.pos ? rec_bytes(pp * p.ldp * 2) : 0u),
-                 (uint32_t)(((m % pp) * p.ldp + n) * 2), vec);
+                 (uint32_t)(((pp > 1 ? umod32(m, pp) : 0) * p.ldp + n) * 2), vec);
 }
 
 // v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
@@ -225,8 +237,8 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
               cnt);
     } else if (p.v_transposed) {
       // V^T cache: [group][head_dim][ldv], tokens contiguous
-      const int64_t b = p.row_group > 0 ? m / p.row_group : 0;
-      const int64_t t = p.row_group > 0 ? m % p.row_group : m;
+      const int64_t b = p.row_group > 0 ? udiv32(m, p.row_group) : 0;
+      const int64_t t = p.row_group > 0 ? umod32(m, p.row_group) : m;
       bf16_t* dst = (bf16_t*)p.v_out + (b * hd + (n - qcols - hd)) * p.ldv + t;
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -1777,8 +1789,9 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
   constexpr int UN = 8;  // splits in flight per pass
   const int64_t N = p.n, K = p.k, M = p.m;
   const int64_t CH = (N + 7) / 8;
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t m = c / CH, nn = (c % CH) * 8;
+  // M * CH < 2^31 (the split partials fit a 2 GiB buffer view): 32-bit divide
+  const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+  const int64_t m = udiv32(c, CH), nn = (int64_t)(c - (uint32_t)m * (uint32_t)CH) * 8;
   if (m >= M) return;
   const int cnt = (int)(N - nn < 8 ? N - nn : 8);
   const bool v4 = (N & 3) == 0;
@@ -1953,6 +1966,11 @@ static int validate(const GemmArgs& d) {
   FVX_REQUIRE(!d.rownorm || d.rownorm_eps >= 0.f, FVX_ERR_ARG,
               "gemm: rownorm_eps must be >= 0");
   FVX_REQUIRE(d.row_group >= 0, FVX_ERR_ARG, "gemm: row_group must be >= 0");
+  FVX_REQUIRE(d.m < ((int64_t)1 << 31) && d.row_group < ((int64_t)1 << 31) &&
+                  d.gate_group < ((int64_t)1 << 31) && d.pos_period < ((int64_t)1 << 31) &&
+                  d.rtc_period < ((int64_t)1 << 31),
+              FVX_ERR_SHAPE,
+              "gemm: m, row_group, gate_group, pos_period and rtc_period must be < 2^31");
   switch (d.mode) {
     case FVX_GEMM_PLAIN:
       FVX_REQUIRE(d.c, FVX_ERR_NULL, "gemm: c is required");
@@ -2195,10 +2213,11 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   const int64_t need = splits > 1 ? kCounterBytes + ((int64_t)nbm * splits * d.m * d.n +
                                                      (int64_t)splits * d.m) * 4
                                    : 0;
-  if (splits > 1 && (!d.workspace || d.workspace_bytes < need)) {
+  // the partials are read through one buffer view (< 2 GiB)
+  if (splits > 1 && (!d.workspace || d.workspace_bytes < need || need >= ((int64_t)1 << 31))) {
     if (d.split_k > 1)
       return set_error(FVX_ERR_WORKSPACE,
-                       "gemm: split_k=%d needs %lld workspace bytes, got %lld",
+                       "gemm: split_k=%d needs %lld workspace bytes (below 2 GiB), got %lld",
                        d.split_k, (long long)need, (long long)d.workspace_bytes);
     splits = 1;
     kchunk = d.k;
@@ -2313,7 +2332,8 @@ extern "C" int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d) {
   const int64_t sp = plan_tile(*d).splits;
   if (sp <= 1) return 0;
   const int nb = d->mode == FVX_GEMM_GEGLU ? 2 : 1;
-  return kCounterBytes + ((int64_t)nb * sp * d->m * d->n + sp * d->m) * 4;
+  const int64_t need = kCounterBytes + ((int64_t)nb * sp * d->m * d->n + sp * d->m) * 4;
+  return need < ((int64_t)1 << 31) ? need : 0;  // larger: the launch runs unsplit
 }
 
 // Skinny GEMMs with the adaptive RMSNorm folded in (a_scale): QKV_ROPE,
