@@ -78,14 +78,17 @@ __device__ __forceinline__ float sumsq8(const bf16x8& v) {
 // ---------------------------------------------------------------------------
 // Row-chunk epilogue: output columns n .. n + 7 of one row m.
 //
-// epi_load issues every global read the epilogue needs (bias, residual, gate,
-// position table, Euler state, RoPE table) and epi_store computes and writes.
-// Callers run epi_load for all of their chunks before the first epi_store:
-// an in-place operand (residual == c, xt) may alias the output, so a read
-// issued after a store would wait for a full memory round trip per element.
-// `vec`: the chunk holds 8 columns and every operand is 16-byte aligned, so
-// each operand moves as one 16-byte (fp32: two) access; otherwise `cnt`
-// columns are handled one by one.
+// epi_load_col and epi_load_row issue every global read the epilogue needs
+// (the column operands: bias, fp32 biases, the RTC lock; the row operands:
+// residual, gate, position table, Euler state, RoPE table) and epi_store
+// computes and writes.  Callers issue the reads for all of their chunks
+// before the first epi_store: an in-place operand (residual == c, xt) may
+// alias the output, so a read issued after a store would wait for a full
+// memory round trip per element.  A lane of the tile and wide kernels keeps
+// one column chunk in every item, so those kernels read the column operands
+// once per lane.  `vec`: the chunk holds 8 columns and every operand is
+// 16-byte aligned, so each operand moves as one 16-byte (fp32: two) access;
+// otherwise `cnt` columns are handled one by one.
 // ---------------------------------------------------------------------------
 struct EpiIn {
   bf16x8 res, gate, pos, bias;
@@ -153,49 +156,111 @@ __device__ __forceinline__ void bl_f8(__amdgpu_buffer_rsrc_t r, uint32_t off,
   }
 }
 
+// Buffer views of the epilogue's operands: uniform, built once per wave
+// outside the item loops (an absent operand gets an empty view, whose reads
+// return zeros).
+struct EpiViews {
+  __amdgpu_buffer_rsrc_t bias, bf32, gate, res, pos, xt, prev, cw, rope, positions;
+};
+
 template <int MODE>
-__device__ __forceinline__ void epi_load(const GemmArgs& p, int64_t m,
-                                         int64_t n, bool vec, int cnt,
-                                         EpiIn& in) {
-  (void)cnt;
+__device__ __forceinline__ EpiViews epi_views(const GemmArgs& p) {
+  EpiViews V;
+  const int64_t N = p.n;
+  V.bias = V.bf32 = V.gate = V.res = V.pos = V.xt = V.prev = V.cw = V.rope = V.positions =
+      make_rsrc(nullptr, 0u);
+  if (MODE == FVX_GEMM_QKV_ROPE) {
+    V.positions = make_rsrc(p.positions, rec_bytes(p.m * 4));
+    V.rope = make_rsrc(p.rope, 0x7fffffffu);
+  }
+  if (MODE == FVX_GEMM_PLAIN || MODE == FVX_GEMM_EULER) {
+    V.bias = make_rsrc(p.bias, p.bias ? rec_bytes(N * 2) : 0u);
+    V.bf32 = make_rsrc(p.bias_f32, p.bias_f32 ? rec_bytes(N * 4) : 0u);
+  }
+  if (MODE == FVX_GEMM_EULER) {
+    V.xt = make_rsrc(p.xt, rec_bytes(p.m * p.ldx * 4));
+    V.prev = make_rsrc(p.rtc_prev, p.rtc_prev ? rec_bytes(p.m * p.ld_prev * 4) : 0u);
+    V.cw = make_rsrc(p.rtc_cw, p.rtc_cw ? rec_bytes(p.rtc_period * 4) : 0u);
+  }
+  if (MODE == FVX_GEMM_PLAIN) {
+    const bool gdiv = p.gate_group > 1;
+    const int64_t grows = gdiv ? udiv32(p.m + p.gate_group - 1, p.gate_group) : p.m;
+    V.gate = make_rsrc(p.gate, p.gate ? rec_bytes(grows * p.ldg * 2) : 0u);
+    V.res = make_rsrc(p.residual,
+                      p.residual ? rec_bytes((out_row(p, p.m - 1) + 1) * p.ldr * 2) : 0u);
+    const int64_t pp = p.pos_period > 0 ? p.pos_period : 1;
+    V.pos = make_rsrc(p.pos, p.pos ? rec_bytes(pp * p.ldp * 2) : 0u);
+  }
+  return V;
+}
+
+__device__ __align__(16) const float kZeros8[8] = {};
+
+// the column operands of columns n .. n + 7 (bias_f32: the unlocked rows')
+template <int MODE>
+__device__ __forceinline__ void epi_load_col(const EpiViews& V, int64_t n, bool vec,
+                                             EpiIn& in) {
+  if (MODE != FVX_GEMM_PLAIN && MODE != FVX_GEMM_EULER) return;
+  in.bias = bl_b8(V.bias, (uint32_t)(n * 2), vec);
+  bl_f8(V.bf32, (uint32_t)(n * 4), vec, in.f0);
+}
+
+// the row operands of row m, columns n .. n + 7
+template <int MODE>
+__device__ __forceinline__ void epi_load_row(const GemmArgs& p, const EpiViews& V, int64_t m,
+                                             int64_t n, bool vec, int cnt, EpiIn& in) {
   if (MODE == FVX_GEMM_GEGLU) return;
   if (MODE == FVX_GEMM_QKV_ROPE) {
     const int hd = p.head_dim;
     const bool rot = n < (int64_t)(p.n_q_heads + 1) * hd;
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.positions, rec_bytes(p.m * 4));
-    const int64_t pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, (uint32_t)(m * 4), 0, 0);
-    const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.rope, 0x7fffffffu);
-    bl_f8(rr, rot ? (uint32_t)((pos * (hd >> 1) + (umod32(n, hd) >> 1)) * 8) : kOOB, vec,
+    const int64_t pos =
+        (int32_t)__builtin_amdgcn_raw_buffer_load_b32(V.positions, (uint32_t)(m * 4), 0, 0);
+    bl_f8(V.rope, rot ? (uint32_t)((pos * (hd >> 1) + (umod32(n, hd) >> 1)) * 8) : kOOB, vec,
           in.f0);
     return;
   }
-  const int64_t N = p.n;
-  in.bias = bl_b8(make_rsrc(p.bias, p.bias ? rec_bytes(N * 2) : 0u), (uint32_t)(n * 2), vec);
-  // real-time chunking: row position within the chunk and the locked prefix
-  const int64_t rr = p.rtc_period > 0 ? umod32(m, p.rtc_period) : 0;
+  // real-time chunking: the row's position within its chunk and the locked
+  // prefix (*rtc_lock: one scalar load, which waits for no vector load)
+  const int rr = p.rtc_period > 0 ? (int)umod32(m, p.rtc_period) : 0;
   in.locked = false;
-  if (p.rtc_lock) in.locked = rr < (int64_t)*p.rtc_lock;
-  const float* bf = in.locked && p.bias_f32_locked ? p.bias_f32_locked : p.bias_f32;
-  bl_f8(make_rsrc(bf, bf ? rec_bytes(N * 4) : 0u), (uint32_t)(n * 4), vec, in.f0);
+  if (p.rtc_lock) in.locked = rr < *(const __attribute__((address_space(4))) int32_t*)p.rtc_lock;
+  if (p.bias_f32_locked) {
+    // the row picks its fp32 bias array: a per-lane address, so global loads
+    // (a per-lane buffer view would loop over the lanes' views); an absent
+    // array or a column past cnt reads kZeros8
+    const float* b = in.locked ? p.bias_f32_locked : p.bias_f32;
+    if (vec) {
+      const f32x4_t* q = (const f32x4_t*)(b ? b + n : kZeros8);
+      const f32x4_t x0 = q[0], x1 = q[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        in.f0[e] = x0[e];
+        in.f0[4 + e] = x1[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) in.f0[e] = *(b && e < cnt ? b + n + e : kZeros8 + e);
+    }
+  }
   if (MODE == FVX_GEMM_EULER) {
-    bl_f8(make_rsrc(p.xt, rec_bytes(p.m * p.ldx * 4)), (uint32_t)((m * p.ldx + n) * 4), vec,
-          in.xt);
-    bl_f8(make_rsrc(p.rtc_prev, p.rtc_prev ? rec_bytes(p.m * p.ld_prev * 4) : 0u),
-          (uint32_t)((m * p.ld_prev + n) * 4), vec, in.prev);
-    in.cw = bload1f(make_rsrc(p.rtc_cw, p.rtc_cw ? rec_bytes(p.rtc_period * 4) : 0u),
-                    (uint32_t)(rr * 4));
+    bl_f8(V.xt, (uint32_t)((m * p.ldx + n) * 4), vec, in.xt);
+    bl_f8(V.prev, (uint32_t)((m * p.ld_prev + n) * 4), vec, in.prev);
+    in.cw = bload1f(V.cw, (uint32_t)(rr * 4));
     return;
   }
-  const bool gdiv = p.gate_group > 1;
-  const int64_t grows = gdiv ? udiv32(p.m + p.gate_group - 1, p.gate_group) : p.m;
-  in.gate = bl_b8(make_rsrc(p.gate, p.gate ? rec_bytes(grows * p.ldg * 2) : 0u),
-                  (uint32_t)(((gdiv ? udiv32(m, p.gate_group) : m) * p.ldg + n) * 2), vec);
-  in.res = bl_b8(make_rsrc(p.residual,
-                           p.residual ? rec_bytes((out_row(p, p.m - 1) + 1) * p.ldr * 2) : 0u),
-                 (uint32_t)((out_row(p, m) * p.ldr + n) * 2), vec);
-  const int64_t pp = p.pos_period > 0 ? p.pos_period : 1;
-  in.pos = bl_b8(make_rsrc(p.pos, p.pos ? rec_bytes(pp * p.ldp * 2) : 0u),
-                 (uint32_t)(((pp > 1 ? umod32(m, pp) : 0) * p.ldp + n) * 2), vec);
+  in.gate = bl_b8(V.gate, (uint32_t)(((p.gate_group > 1 ? udiv32(m, p.gate_group) : m) * p.ldg + n) * 2),
+                  vec);
+  in.res = bl_b8(V.res, (uint32_t)((out_row(p, m) * p.ldr + n) * 2), vec);
+  in.pos = bl_b8(V.pos,
+                 (uint32_t)(((p.pos_period > 1 ? umod32(m, p.pos_period) : 0) * p.ldp + n) * 2),
+                 vec);
+}
+
+template <int MODE>
+__device__ __forceinline__ void epi_load(const GemmArgs& p, const EpiViews& V, int64_t m,
+                                         int64_t n, bool vec, int cnt, EpiIn& in) {
+  epi_load_col<MODE>(V, n, vec, in);
+  epi_load_row<MODE>(p, V, m, n, vec, cnt, in);
 }
 
 // v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
@@ -721,81 +786,95 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 
   // Epilogue: each 32-row block of the wave's sub-tile goes through the
   // wave's own LDS scratch [32][ELD] fp32 (GEGLU: gate columns, then up).
+  // Lane item q = lane + 64 e covers row q / CH, columns 8 (q % CH) ..: the
+  // same column chunk in every item (64 % CH == 0), so the column operands
+  // and the fp8 weight scales are read once per lane.
   float* scr = (float*)smem + wave * 32 * ELD;
   constexpr int CH = WNO / 8;               // 8-column chunks per row
   constexpr int ITEMS = 32 * CH / 64;       // chunks per lane per block
   constexpr int EB = ITEMS < 4 ? ITEMS : 4; // chunks whose loads fly together
-  const int64_t nw0 = n0 + wn * WNO;
+  constexpr int RS = 64 / CH;               // row step between a lane's items
+  static_assert(64 % CH == 0, "one column chunk per lane");
+  const int ch = lane % CH, row0 = lane / CH;
+  const int64_t nn = n0 + wn * WNO + 8 * ch;
+  const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+  // hand-over outputs: the 8 lanes of a row (CH == 8: one 64-column block
+  // per wave); the shuffles run in every lane
+  constexpr bool HO = MODE == FVX_GEMM_PLAIN && WNO == 64;
+  const bool ho = HO && (p.ss_out || p.a8_out) && splits == 1;
+  const EpiViews V = epi_views<MODE>(p);
+  // VA: every operand is 16B-aligned and N % 8 == 0 (uniform), so every
+  // chunk with columns left holds 8 and moves as whole vectors
+  auto epilogue = [&](auto va) {
+    const bool vec = decltype(va)::value || (vec_ok && cnt == 8);
+    EpiIn col;
+    if (splits == 1) epi_load_col<MODE>(V, nn, vec, col);
+    float w0[8], w1[8];  // fp8: per-output-channel weight scales
+    if (F8) {
+      bl_f8(make_rsrc(p.b_scale, rec_bytes(N * 4)), (uint32_t)(nn * 4), vec, w0);
+      bl_f8(make_rsrc(NB == 2 ? p.b2_scale : p.b_scale, rec_bytes(N * 4)), (uint32_t)(nn * 4),
+            vec, w1);
+    }
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+    for (int i = 0; i < FM; ++i) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * ELD + 32 * j + fr] = acc[i][j][r];
-    const int64_t rb = m0 + wm * WM + 32 * i;
+        for (int r = 0; r < 16; ++r)
+          scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * ELD + 32 * j + fr] = acc[i][j][r];
+      const int64_t rb = m0 + wm * WM + 32 * i + row0;
 #pragma unroll
-    for (int e0 = 0; e0 < ITEMS; e0 += EB) {
-      EpiIn in[EB];
-      if (splits == 1) {
+      for (int e0 = 0; e0 < ITEMS; e0 += EB) {
+        EpiIn in[EB];
+        if (splits == 1) {
+#pragma unroll
+          for (int e = 0; e < EB; ++e) {
+            in[e] = col;
+            epi_load_row<MODE>(p, V, rb + RS * (e0 + e), nn, vec, cnt, in[e]);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < EB; ++e) {
-          const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
-          const int64_t nn = nw0 + 8 * ch;
-          const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-          epi_load<MODE>(p, rb + row, nn, vec_ok && cnt == 8, cnt, in[e]);
-        }
-      }
+          const int row = row0 + RS * (e0 + e);
+          const int64_t m = rb + RS * (e0 + e);
+          float xo[8];
+          if (m < M && cnt > 0) {
+            float v[8], u[8];
+            const float* sv = scr + row * ELD + 8 * ch;
 #pragma unroll
-      for (int e = 0; e < EB; ++e) {
-        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
-        const int64_t m = rb + row, nn = nw0 + 8 * ch;
-        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        // hand-over outputs: the 8 lanes of a row (CH == 8: one 64-column
-        // block per wave); the shuffles run in every lane
-        constexpr bool HO = MODE == FVX_GEMM_PLAIN && WNO == 64;
-        const bool ho = HO && (p.ss_out || p.a8_out) && splits == 1;
-        float xo[8];
-        if (m < M && cnt > 0) {
-        float v[8], u[8];
-        const float* sv = scr + row * ELD + 8 * ch;
+            for (int x = 0; x < 8; ++x) {
+              v[x] = sv[x];
+              u[x] = NB == 2 ? sv[WNO + x] : 0.f;
+            }
+            if (F8) {
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
-          v[x] = sv[x];
-          u[x] = NB == 2 ? sv[WNO + x] : 0.f;
-        }
-        if (F8) {  // per-output-channel weight scales
-          float w0[8], w1[8];
-          const bool sv8 = vec_ok && cnt == 8;
-          bl_f8(make_rsrc(p.b_scale, rec_bytes(N * 4)), (uint32_t)(nn * 4), sv8, w0);
-          bl_f8(make_rsrc(NB == 2 ? p.b2_scale : p.b_scale, rec_bytes(N * 4)),
-                (uint32_t)(nn * 4), sv8, w1);
+              for (int x = 0; x < 8; ++x) {
+                v[x] *= w0[x];
+                u[x] *= w1[x];
+              }
+            }
+            if (splits > 1) {
 #pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            v[x] *= w0[x];
-            u[x] *= w1[x];
+              for (int b = 0; b < NB; ++b) {
+                float* dst = ws + b * plane + ((int64_t)split * M + m) * N + nn;
+#pragma unroll
+                for (int x = 0; x < 8; ++x)
+                  if (x < cnt) dst[x] = b ? u[x] : v[x];
+              }
+            } else {
+              const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
+              epi_store<MODE>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo);
+            }
           }
+          if (ho) epi_handoff(p, m < M && cnt > 0, ch == 0, m, nn, cnt, xo);
         }
-        if (splits > 1) {
-#pragma unroll
-          for (int b = 0; b < NB; ++b) {
-            float* dst = ws + b * plane + ((int64_t)split * M + m) * N + nn;
-#pragma unroll
-            for (int x = 0; x < 8; ++x)
-              if (x < cnt) dst[x] = b ? u[x] : v[x];
-          }
-          goto next_item;
-        }
-        const float r = p.rownorm
-                            ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps)
-                            : 1.f;
-        epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e], ho, xo);
-        }
-      next_item:
-        if (ho) epi_handoff(p, m < M && cnt > 0, ch == 0, m, nn, cnt, xo);
       }
     }
-  }
+  };
+  if (vec_ok && (N & 7) == 0)
+    epilogue(BoolC<true>{});
+  else
+    epilogue(BoolC<false>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -991,14 +1070,21 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
   __syncthreads();  // also: every wave is done with the ring
 
   // each 32-row block through the wave's LDS scratch [32][kGwELD] (GEGLU:
-  // gate columns 0..63, up 64..127); lane item q: row q / CH, 8 columns
-  // 8 (q % CH) with CH = WNO / 8 chunks per row
-  // (EB items' epilogue inputs in flight; PLAIN's, with 8 waves, one at a
-  // time: more do not fit the 256 registers of two waves per SIMD)
+  // gate columns 0..63, up 64..127); lane item q = lane + 64 e: row q / CH,
+  // 8 columns 8 (q % CH) with CH = WNO / 8 chunks per row, the lane's own
+  // column chunk in every item (EB items' epilogue inputs in flight;
+  // PLAIN's, with 8 waves, one at a time and column operands included:
+  // more do not fit the 256 registers of two waves per SIMD)
   constexpr int EB0 = NWV == 8 && MODE == FVX_GEMM_PLAIN ? 1 : FVX_WIDE_EB;
   constexpr int CH = WNO / 8, ITEMS = 32 * CH / 64, EB = EB0 < ITEMS ? EB0 : ITEMS;
+  constexpr int RS = 64 / CH;  // row step between a lane's items
+  static_assert(64 % CH == 0, "one column chunk per lane");
   float* scr = (float*)smem + wave * 32 * kGwELD;
-  const int64_t nw0 = n0 + wn * WNO;
+  const int ch = lane % CH, row0 = lane / CH;
+  const int64_t nn = n0 + wn * WNO + 8 * ch;
+  const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+  const bool ho = (MODE == FVX_GEMM_PLAIN || GG) && (p.ss_out || p.a8_out);
+  const EpiViews V = epi_views<MODE>(p);
   // block i of the accumulators -> scratch (compile-time indices, so the
   // accumulators stay in registers); the item loops below are real loops,
   // which keeps the epilogue code small enough for the kernel arguments to
@@ -1011,63 +1097,59 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
       for (int r = 0; r < 16; ++r)
         scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * kGwELD + 32 * j + fr] = acc[i][j][r];
   };
+  // with N % 8 == 0 every chunk with columns left holds 8: vec is uniform
+  const bool vec = vec_ok && (cnt == 8 || (N & 7) == 0);
+  {
 #pragma unroll 1
-  for (int i = 0; i < RB; ++i) {
-    switch (i) {
-      case 0: to_scr(IntC<0>{}); break;
-      case 1: to_scr(IntC<1>{}); break;
-      case 2: to_scr(IntC<2 % RB>{}); break;
-      default: to_scr(IntC<3 % RB>{}); break;
-    }
-    const int64_t rb = m0 + wm * WM + 32 * i;
-    if (splits > 1) {
-      // fp32 partials of this K range: ws[(split M + m) N + n]
-      float* ws = (float*)((char*)p.workspace + kCounterBytes) + (int64_t)split * M * N;
-#pragma unroll 1
-      for (int e = 0; e < ITEMS; ++e) {
-        const int q = lane + 64 * e, row = q / CH, ch = q % CH;
-        const int64_t m = rb + row, nn = nw0 + 8 * ch;
-        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        if (m < M && cnt > 0) {
-          const float* sv = scr + row * kGwELD + 8 * ch;
-          float v[8];
-#pragma unroll
-          for (int x = 0; x < 8; ++x) v[x] = sv[x];
-          st_f8(ws + m * N + nn, v, (N & 3) == 0 && cnt == 8, cnt);
-        }
+    for (int i = 0; i < RB; ++i) {
+      switch (i) {
+        case 0: to_scr(IntC<0>{}); break;
+        case 1: to_scr(IntC<1>{}); break;
+        case 2: to_scr(IntC<2 % RB>{}); break;
+        default: to_scr(IntC<3 % RB>{}); break;
       }
-      continue;
-    }
+      const int64_t rb = m0 + wm * WM + 32 * i + row0;
+      if (splits > 1) {
+        // fp32 partials of this K range: ws[(split M + m) N + n]
+        float* ws = (float*)((char*)p.workspace + kCounterBytes) + (int64_t)split * M * N;
 #pragma unroll 1
-    for (int e0 = 0; e0 < ITEMS; e0 += EB) {
-      EpiIn in[EB];
+        for (int e = 0; e < ITEMS; ++e) {
+          const int row = row0 + RS * e;
+          const int64_t m = rb + RS * e;
+          if (m < M && cnt > 0) {
+            const float* sv = scr + row * kGwELD + 8 * ch;
+            float v[8];
 #pragma unroll
-      for (int e = 0; e < EB; ++e) {
-        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
-        const int64_t nn = nw0 + 8 * ch;
-        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        epi_load<MODE>(p, rb + row, nn, vec_ok && cnt == 8, cnt, in[e]);
-      }
-#pragma unroll
-      for (int e = 0; e < EB; ++e) {
-        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
-        const int64_t m = rb + row, nn = nw0 + 8 * ch;
-        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        const bool ho = (MODE == FVX_GEMM_PLAIN || GG) && (p.ss_out || p.a8_out);
-        float xo[8];
-        if (m < M && cnt > 0) {
-          float v[8], u[8];
-          const float* sv = scr + row * kGwELD + 8 * ch;
-#pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            v[x] = sv[x];
-            u[x] = GG ? sv[64 + x] : 0.f;
+            for (int x = 0; x < 8; ++x) v[x] = sv[x];
+            st_f8(ws + m * N + nn, v, (N & 3) == 0 && cnt == 8, cnt);
           }
-          const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
-          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e], ho, xo);
         }
-        // the 8 lanes of a row's 64-column block
-        if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
+        continue;
+      }
+#pragma unroll 1
+      for (int e0 = 0; e0 < ITEMS; e0 += EB) {
+        EpiIn in[EB];
+#pragma unroll
+        for (int e = 0; e < EB; ++e) epi_load<MODE>(p, V, rb + RS * (e0 + e), nn, vec, cnt, in[e]);
+#pragma unroll
+        for (int e = 0; e < EB; ++e) {
+          const int row = row0 + RS * (e0 + e);
+          const int64_t m = rb + RS * (e0 + e);
+          float xo[8];
+          if (m < M && cnt > 0) {
+            float v[8], u[8];
+            const float* sv = scr + row * kGwELD + 8 * ch;
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+              v[x] = sv[x];
+              u[x] = GG ? sv[64 + x] : 0.f;
+            }
+            const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
+            epi_store<MODE>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo);
+          }
+          // the 8 lanes of a row's 64-column block
+          if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
+        }
       }
     }
   }
@@ -1292,9 +1374,17 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   }
   __syncthreads();  // also: every wave is done with the ring
 
-  constexpr int CH = WNO / 8, ITEMS = 32 * CH / 64, EB = 4;
+  // lane item q = lane + 64 e: row q / CH, columns 8 (q % CH) .. -- the
+  // lane's own column chunk in every item, so its column operands and
+  // weight scales are read once
+  constexpr int CH = WNO / 8, ITEMS = 32 * CH / 64, EB = 4, RS = 64 / CH;
+  static_assert(64 % CH == 0, "one column chunk per lane");
   float* scr = (float*)smem + wave * 32 * kGwELD;
-  const int64_t nw0 = n0 + wn * WNO;
+  const int ch = lane % CH, row0 = lane / CH;
+  const int64_t nn = n0 + wn * WNO + 8 * ch;
+  const int cnt = (int)(N - nn < 8 ? N - nn : 8);
+  const bool ho = (MODE == FVX_GEMM_PLAIN || GG) && (p.ss_out || p.a8_out);
+  const EpiViews V = epi_views<MODE>(p);
   auto to_scr = [&](auto ic) {
     constexpr int i = decltype(ic)::value;
 #pragma unroll
@@ -1303,71 +1393,67 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
       for (int r = 0; r < 16; ++r)
         scr[(8 * (r >> 2) + 4 * hk + (r & 3)) * kGwELD + 32 * j + fr] = acc[i][j][r];
   };
-  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(p.b_scale, rec_bytes(N * 4));
-  const __amdgpu_buffer_rsrc_t rsc2 = make_rsrc(GG ? p.b2_scale : p.b_scale, rec_bytes(N * 4));
+  // with N % 8 == 0 every chunk with columns left holds 8: vec is uniform
+  const bool vec = vec_ok && (cnt == 8 || (N & 7) == 0);
+  {
+    EpiIn col;
+    if (splits == 1) epi_load_col<MODE>(V, nn, vec, col);
+    float w0[8], w1[8];
+    bl_f8(make_rsrc(p.b_scale, rec_bytes(N * 4)), (uint32_t)(nn * 4), vec, w0);
+    if (GG) bl_f8(make_rsrc(p.b2_scale, rec_bytes(N * 4)), (uint32_t)(nn * 4), vec, w1);
 #pragma unroll 1
-  for (int i = 0; i < 4; ++i) {
-    switch (i) {
-      case 0: to_scr(IntC<0>{}); break;
-      case 1: to_scr(IntC<1>{}); break;
-      case 2: to_scr(IntC<2>{}); break;
-      default: to_scr(IntC<3>{}); break;
-    }
-    const int64_t rb = m0 + wm * 128 + 32 * i;
-    if (splits > 1) {
-      // partials of this K range, scaled by the weight scales:
-      // ws[(split M + m) N + n]
-      float* ws = (float*)((char*)p.workspace + kCounterBytes) + (int64_t)split * M * N;
-#pragma unroll 1
-      for (int e = 0; e < ITEMS; ++e) {
-        const int q = lane + 64 * e, row = q / CH, ch = q % CH;
-        const int64_t m = rb + row, nn = nw0 + 8 * ch;
-        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        if (m < M && cnt > 0) {
-          const bool vec = vec_ok && cnt == 8;
-          float w0[8], v[8];
-          bl_f8(rsc, (uint32_t)(nn * 4), vec, w0);
-          const float* sv = scr + row * kGwELD + 8 * ch;
-#pragma unroll
-          for (int x = 0; x < 8; ++x) v[x] = sv[x] * w0[x];
-          st_f8(ws + m * N + nn, v, (N & 3) == 0 && cnt == 8, cnt);
-        }
+    for (int i = 0; i < 4; ++i) {
+      switch (i) {
+        case 0: to_scr(IntC<0>{}); break;
+        case 1: to_scr(IntC<1>{}); break;
+        case 2: to_scr(IntC<2>{}); break;
+        default: to_scr(IntC<3>{}); break;
       }
-      continue;
-    }
+      const int64_t rb = m0 + wm * 128 + 32 * i + row0;
+      if (splits > 1) {
+        // partials of this K range, scaled by the weight scales:
+        // ws[(split M + m) N + n]
+        float* ws = (float*)((char*)p.workspace + kCounterBytes) + (int64_t)split * M * N;
 #pragma unroll 1
-    for (int e0 = 0; e0 < ITEMS; e0 += EB) {
-      EpiIn in[EB];
-      float w0[EB][8], w1[EB][8];
+        for (int e = 0; e < ITEMS; ++e) {
+          const int row = row0 + RS * e;
+          const int64_t m = rb + RS * e;
+          if (m < M && cnt > 0) {
+            float v[8];
+            const float* sv = scr + row * kGwELD + 8 * ch;
 #pragma unroll
-      for (int e = 0; e < EB; ++e) {
-        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
-        const int64_t nn = nw0 + 8 * ch;
-        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        const bool vec = vec_ok && cnt == 8;
-        epi_load<MODE>(p, rb + row, nn, vec, cnt, in[e]);
-        bl_f8(rsc, (uint32_t)(nn * 4), vec, w0[e]);
-        if (GG) bl_f8(rsc2, (uint32_t)(nn * 4), vec, w1[e]);
-      }
-#pragma unroll
-      for (int e = 0; e < EB; ++e) {
-        const int q = lane + 64 * (e0 + e), row = q / CH, ch = q % CH;
-        const int64_t m = rb + row, nn = nw0 + 8 * ch;
-        const int cnt = (int)(N - nn < 8 ? N - nn : 8);
-        const bool ho = (MODE == FVX_GEMM_PLAIN || GG) && (p.ss_out || p.a8_out);
-        float xo[8];
-        if (m < M && cnt > 0) {
-          float v[8], u[8];
-          const float* sv = scr + row * kGwELD + 8 * ch;
-#pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            v[x] = sv[x] * w0[e][x];
-            u[x] = GG ? sv[64 + x] * w1[e][x] : 0.f;
+            for (int x = 0; x < 8; ++x) v[x] = sv[x] * w0[x];
+            st_f8(ws + m * N + nn, v, (N & 3) == 0 && cnt == 8, cnt);
           }
-          const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
-          epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in[e], ho, xo);
         }
-        if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
+        continue;
+      }
+#pragma unroll 1
+      for (int e0 = 0; e0 < ITEMS; e0 += EB) {
+        EpiIn in[EB];
+#pragma unroll
+        for (int e = 0; e < EB; ++e) {
+          in[e] = col;
+          epi_load_row<MODE>(p, V, rb + RS * (e0 + e), nn, vec, cnt, in[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < EB; ++e) {
+          const int row = row0 + RS * (e0 + e);
+          const int64_t m = rb + RS * (e0 + e);
+          float xo[8];
+          if (m < M && cnt > 0) {
+            float v[8], u[8];
+            const float* sv = scr + row * kGwELD + 8 * ch;
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+              v[x] = sv[x] * w0[x];
+              u[x] = GG ? sv[64 + x] * w1[x] : 0.f;
+            }
+            const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
+            epi_store<MODE>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo);
+          }
+          if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
+        }
       }
     }
   }
@@ -1639,7 +1725,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   const bool mine = tid < 2 * RR && row < M && cnt > 0;
   const bool vec = vec_ok && cnt == 8;
   EpiIn in;
-  if (mine) epi_load<MODE>(p, row, ncol, vec, cnt, in);
+  if (mine) epi_load<MODE>(p, epi_views<MODE>(p), row, ncol, vec, cnt, in);
   // ASC with QKV_ROPE / GEGLU: the folded shift's fp32 biases (gate, up)
   constexpr bool FB = ASC && (MODE == FVX_GEMM_QKV_ROPE || MODE == FVX_GEMM_GEGLU);
   float fb[8], fb2[8];
@@ -1800,7 +1886,7 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(ws, rec_bytes((NB * plane + (int64_t)splits * M) * 4));
   EpiIn in;
-  epi_load<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, in);
+  epi_load<MODE>(p, epi_views<MODE>(p), m, nn, vec_ok && cnt == 8, cnt, in);
   float v[8], u[8], ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = u[e] = 0.f;
