@@ -496,9 +496,11 @@ __device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
 
 // Row r (problem z), dims d0 .. d0 + 7 of the merged output from the split
 // partials of its 64-row group: the loads of up to 16 splits in flight, then
-// the running-max merge in split order.  AUX: the loads' cache policy (0 for
-// partials of an earlier launch; 1, missing in the vector L1, for partials
-// other CUs of the XCD wrote in this launch).
+// per pass of 16 the pass maximum first and the weighted sums after it, in
+// split order (the weights exp2(m_s - max) are independent of each other, so
+// no rescaling chain runs through the splits).  AUX: the loads' cache policy
+// (0 for partials of an earlier launch; 1, missing in the vector L1, for
+// partials other CUs of the XCD wrote in this launch).
 template <int AUX>
 __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int splits,
                                            int hs, int z, int r, int d0) {
@@ -520,20 +522,28 @@ __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int
       lv[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
           rw, off + (uint32_t)(kDecPO + 64 + i) * 4, 0, AUX));
     }
+    float mn = M;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      if (s0 + u < splits) {
-        const float mn = fmaxf(M, mv[u]);
-        const float mr = (mn == -INFINITY) ? 0.f : mn;
-        const float wa = exp2f(M - mr), wb = exp2f(mv[u] - mr);
-        float av[8];
-        unpack8(a[u], av);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = acc[e] * wa + av[e] * wb;
-        L = L * wa + lv[u] * wb;
-        M = mn;
-      }
+      mv[u] = s0 + u < splits ? mv[u] : -INFINITY;
+      mn = fmaxf(mn, mv[u]);
     }
+    // a row no split has seen keys of keeps a zero reference
+    const float mr = (mn == -INFINITY) ? 0.f : mn;
+    const float wa = __builtin_amdgcn_exp2f(M - mr);  // earlier passes (0 on the first)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= wa;
+    L *= wa;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const float wb = __builtin_amdgcn_exp2f(mv[u] - mr);
+      float av[8];
+      unpack8(a[u], av);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(av[e], wb, acc[e]);
+      L = fmaf(lv[u], wb, L);
+    }
+    M = mn;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
@@ -780,12 +790,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
       const f32x4_t t = *(const f32x4_t*)&mxb[(16 * rb + fr) * 4];
       const float m_new = fmaxf(m_run[rb], fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])));
       const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
-      alpha[rb] = exp2f(m_run[rb] - m_ref);
+      // the hardware exp2 (v_exp_f32; results below 2^-126 may flush to
+      // zero, far under a probability's bf16 resolution)
+      alpha[rb] = __builtin_amdgcn_exp2f(m_run[rb] - m_ref);
       m_run[rb] = m_new;
       float pv[4], ps = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        pv[j] = exp2f(sv[rb][j] - m_ref);
+        pv[j] = __builtin_amdgcn_exp2f(sv[rb][j] - m_ref);
         ps += pv[j];
       }
       ps += __shfl_xor(ps, 16, 64);
@@ -1188,7 +1200,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
           float pv[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            pv[e] = exp2f(fmaf(sv[8 * hf + e], sc, nm));
+            pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[8 * hf + e], sc, nm));
             l_run += pv[e];
           }
           pT[2 * kb + hf] = pack8(pv);
