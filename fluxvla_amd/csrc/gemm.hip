@@ -909,6 +909,7 @@ constexpr int kGwBM = 256, kGwBN = 256;  // rows, columns (GEGLU: 2 x 128)
 #endif
 constexpr int kGwStage = 512 * 128;
 constexpr int kGwELD = 128 + 4;          // epilogue scratch stride (floats)
+constexpr int kGhP = 64 + 8;             // GeGLU product scratch stride (bf16)
 // waves of the bf16 wide kernel: 8 (prefix GeGLU 119 -> 110 us, chunk
 // 16.8 -> 16.4 ms against 4)
 template <int MODE>
@@ -1068,6 +1069,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
     }
   }
   __syncthreads();  // also: every wave is done with the ring
+  // each row's RMS factor, once (the epilogue reads it per row)
+  if (p.rownorm) {
+    if (tid < kGwBM) sRow[tid] = rsqrtf(sRow[tid] / (float)K + p.rownorm_eps);
+    __syncthreads();
+  }
 
   // each 32-row block through the wave's LDS scratch [32][kGwELD] (GEGLU:
   // gate columns 0..63, up 64..127); lane item q = lane + 64 e: row q / CH,
@@ -1099,6 +1105,48 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
   };
   // with N % 8 == 0 every chunk with columns left holds 8: vec is uniform
   const bool vec = vec_ok && (cnt == 8 || (N & 7) == 0);
+  // GeGLU without hand-overs, whole vectors: gelu(gate) * up straight from
+  // the accumulators (gate block j and up block j + 2 share the lane layout:
+  // lane (fr, hk), register q holds row 8 (q >> 2) + 4 hk + (q & 3), column
+  // 32 j + fr), so only the bf16 products pass through the scratch, a
+  // quarter of the fp32 gate | up rows' bytes
+  if (GG && !ho && vec_ok && (N & 7) == 0 && splits == 1) {
+    bf16_t* sh = (bf16_t*)scr;  // [32][kGhP] bf16
+    auto gg_to_scr = [&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      float r[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        r[q] = p.rownorm ? sRow[wm * WM + 32 * i + 8 * (q >> 2) + 4 * hk + (q & 3)] : 1.f;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const float g = acc[i][jj][q] * r[q], u = acc[i][jj + 2][q] * r[q];
+          sh[(8 * (q >> 2) + 4 * hk + (q & 3)) * kGhP + 32 * jj + fr] = f2bf(gelu_tanh(g) * u);
+        }
+    };
+#pragma unroll 1
+    for (int i = 0; i < RB; ++i) {
+      switch (i) {
+        case 0: gg_to_scr(IntC<0>{}); break;
+        case 1: gg_to_scr(IntC<1>{}); break;
+        case 2: gg_to_scr(IntC<2 % RB>{}); break;
+        default: gg_to_scr(IntC<3 % RB>{}); break;
+      }
+      const int64_t rb = m0 + wm * WM + 32 * i + row0;
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e) {
+        const int64_t m = rb + RS * e;
+        const bf16x8 h = ld8(sh + (row0 + RS * e) * kGhP + 8 * ch);
+        if (m < M && cnt > 0) {
+          st8((bf16_t*)p.c + out_row(p, m) * p.ldc + nn, h);
+          if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, nn), h);
+        }
+      }
+    }
+    return;
+  }
   {
 #pragma unroll 1
     for (int i = 0; i < RB; ++i) {
@@ -1144,7 +1192,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
               v[x] = sv[x];
               u[x] = GG ? sv[64 + x] : 0.f;
             }
-            const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
+            const float r = p.rownorm ? sRow[m - m0] : 1.f;
             epi_store<MODE>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo);
           }
           // the 8 lanes of a row's 64-column block
