@@ -495,24 +495,26 @@ __device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
 }
 
 // Row r (problem z), dims d0 .. d0 + 7 of the merged output from the split
-// partials of its 64-row group: the loads of up to 16 splits in flight, then
+// partials of its 64-row group: the loads of up to NS splits in flight, then
 // per pass of 16 the pass maximum first and the weighted sums after it, in
 // split order (the weights exp2(m_s - max) are independent of each other, so
 // no rescaling chain runs through the splits).  AUX: the loads' cache policy
 // (0 for partials of an earlier launch; 1, missing in the vector L1, for
 // partials other CUs of the XCD wrote in this launch).
-template <int AUX>
-__device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int splits,
-                                           int hs, int z, int r, int d0) {
+// NS: splits per pass (4, 8 or 16; the smallest that holds `splits`, so
+// no load is spent on splits that do not exist).
+template <int AUX, int NS>
+__device__ __forceinline__ void dec_merge8_ns(const fvx_attn_desc& p, int n_rg, int splits,
+                                              int hs, int z, int r, int d0) {
   const int rg = r >> 6, i = r & 63;
   const float* base = (const float*)p.workspace + (((int64_t)z * n_rg + rg) * splits) * kDecPF;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, M = -INFINITY, L = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += 16) {
-    bf16x8 a[16];
-    float mv[16], lv[16];
+  for (int s0 = 0; s0 < splits; s0 += NS) {
+    bf16x8 a[NS];
+    float mv[NS], lv[NS];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
+    for (int u = 0; u < NS; ++u) {
       // splits past the end read as zero (out of the buffer view)
       const uint32_t off = (uint32_t)((s0 + u) * kDecPF * 4);
       a[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
@@ -524,7 +526,7 @@ __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int
     }
     float mn = M;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
+    for (int u = 0; u < NS; ++u) {
       mv[u] = s0 + u < splits ? mv[u] : -INFINITY;
       mn = fmaxf(mn, mv[u]);
     }
@@ -535,7 +537,7 @@ __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int
     for (int e = 0; e < 8; ++e) acc[e] *= wa;
     L *= wa;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
+    for (int u = 0; u < NS; ++u) {
       const float wb = __builtin_amdgcn_exp2f(mv[u] - mr);
       float av[8];
       unpack8(a[u], av);
@@ -549,6 +551,17 @@ __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] *= inv;
   dec_store<8>(p, z, r, d0, hs, acc);
+}
+
+template <int AUX>
+__device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int splits,
+                                           int hs, int z, int r, int d0) {
+  if (splits <= 4)
+    dec_merge8_ns<AUX, 4>(p, n_rg, splits, hs, z, r, d0);
+  else if (splits <= 8)
+    dec_merge8_ns<AUX, 8>(p, n_rg, splits, hs, z, r, d0);
+  else
+    dec_merge8_ns<AUX, 16>(p, n_rg, splits, hs, z, r, d0);
 }
 
 // One merging workgroup of the in-launch merge: 8 rows (chunk) of 64-row
@@ -1306,8 +1319,8 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
 
 // Merge of the decode partials (bf16 O rows: half the bytes of fp32, within
 // the output's own bf16 rounding): one thread per (problem, query row, 8
-// dims); the loads of up to 16 splits are issued before the running-max
-// merge, which is applied in split order.
+// dims); the loads of up to 4, 8 or 16 splits (as many as there are) are
+// issued before the merge, which is applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
     fvx_attn_desc p, int n_rg, int splits, int hs) {
   const int R = (int)(p.sq * p.heads);
