@@ -134,22 +134,40 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
       make_rsrc(kgrp ? (const void*)kgrp : (const void*)K, kgrp ? (uint32_t)(kend * 4) : 0u);
   bf16x8 rk[CH], rv[CH];
   int32_t rgp = 0;
+  // Each thread's chunks, fixed over the tiles (computed once, 32-bit: the
+  // views are below 2 GiB): global byte offsets relative to the tile's first
+  // key and LDS element offsets.  K chunks are key-major (key i / kchunks,
+  // dims 8 (i % kchunks)); V^T chunks 8 consecutive keys of dim i / 4;
+  // row-major V chunks key i % 32, dims 8 (i / 32).
+  const bool vt = p.v_d_stride > 0;
+  const uint32_t kts2 = (uint32_t)p.k_tok_stride * 2u;
+  const uint32_t vstep2 = vt ? 2u : (uint32_t)p.v_tok_stride * 2u;  // per key
+  uint32_t koff[CH], voff[CH];
+  int kl[CH], vl[CH], vkey[CH];
+  bool cin[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int i = tid + 256 * c;
+    cin[c] = i < tile_chunks;
+    const int kr = i / kchunks, kc = i - kr * kchunks;
+    koff[c] = (uint32_t)kr * kts2 + (uint32_t)kc * 16u;
+    kl[c] = kr * LDK + kc * 8;
+    if (vt) {
+      vkey[c] = (i & 3) * 8;
+      voff[c] = ((uint32_t)(i >> 2) * (uint32_t)p.v_d_stride + (uint32_t)vkey[c]) * 2u;
+      vl[c] = (i >> 2) * LDV + vkey[c];
+    } else {
+      vkey[c] = i % kKeyTile;
+      voff[c] = (uint32_t)vkey[c] * vstep2 + (uint32_t)(i / kKeyTile) * 16u;
+      vl[c] = (i / kKeyTile) * 8 * LDV + vkey[c];
+    }
+  }
   auto prefetch = [&](int64_t t0) {
+    const uint32_t kb = (uint32_t)t0 * kts2, vb = (uint32_t)t0 * vstep2;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int i = tid + 256 * c;
-      const bool in = i < tile_chunks;
-      const int64_t jk = t0 + i / kchunks;  // K: key-major chunks
-      rk[c] = bload8(rkc, in ? (uint32_t)((jk * p.k_tok_stride + (i % kchunks) * 8) * 2) : kOOB);
-      if (p.v_d_stride > 0) {
-        // V^T: chunk = 8 consecutive keys of one dim
-        const int64_t j8 = t0 + (i % 4) * 8;
-        rv[c] = bload8(rvc, in ? (uint32_t)(((i / 4) * p.v_d_stride + j8) * 2) : kOOB);
-      } else {
-        const int64_t jv = t0 + i % kKeyTile;  // V: key-minor chunks
-        rv[c] = bload8(rvc, in ? (uint32_t)((jv * p.v_tok_stride + (i / kKeyTile) * 8) * 2)
-                               : kOOB);
-      }
+      rk[c] = bload8(rkc, cin[c] ? kb + koff[c] : kOOB);
+      rv[c] = bload8(rvc, cin[c] ? vb + voff[c] : kOOB);
     }
     if (kgrp && tid < kKeyTile)
       rgp = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rgc, (uint32_t)((t0 + tid) * 4), 0, 0);
@@ -160,17 +178,14 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     __syncthreads();  // previous tile fully consumed
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int i = tid + 256 * c;
-      if (i < tile_chunks) {
-        st8(&sK[(i / kchunks) * LDK + (i % kchunks) * 8], rk[c]);
-        if (p.v_d_stride > 0) {
-          st8(&sVt[(i / 4) * LDV + (i % 4) * 8],
-              mask_keys(rv[c], kend - (t0 + (i % 4) * 8)));
+      if (cin[c]) {
+        st8(&sK[kl[c]], rk[c]);
+        if (vt) {
+          st8(&sVt[vl[c]], mask_keys(rv[c], (int)(kend - t0) - vkey[c]));
         } else {
           const bf16_t* ve = (const bf16_t*)&rv[c];
-          const int key = i % kKeyTile, c8 = i / kKeyTile;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sVt[(c8 * 8 + e) * LDV + key] = ve[e];
+          for (int e = 0; e < 8; ++e) sVt[vl[c] + e * LDV] = ve[e];
         }
       }
     }
@@ -204,14 +219,14 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
     const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_ref);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
     float psum = 0.f;
     float pr[2][4];
 #pragma unroll
     for (int kf = 0; kf < 2; ++kf)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pr[kf][e] = exp2f(s[kf][e] - m_ref);
+        pr[kf][e] = __builtin_amdgcn_exp2f(s[kf][e] - m_ref);
         psum += pr[kf][e];
       }
     psum += __shfl_xor(psum, 16, 64);
@@ -327,7 +342,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(fvx_attn_desc p,
       t[df] = *(const f32x4_t*)(q + ((wave * ND + df) * 64 + lane) * 4);
     const float ms = q[4 * ND * 64 * 4 + wave * 16 + fr];
     const float ls = q[4 * ND * 64 * 4 + 64 + wave * 16 + fr];
-    const float w = exp2f(ms - mref);
+    const float w = __builtin_amdgcn_exp2f(ms - mref);
     l_run += ls * w;
     float wj[4];
 #pragma unroll
