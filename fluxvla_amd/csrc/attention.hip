@@ -3,15 +3,16 @@
 // One workgroup = 4 waves x 16 query rows.  For MQA every query head of a
 // token shares the single K/V head, so query rows are (token, head) pairs
 // and one K/V tile in LDS feeds all of them (8 heads x 8 tokens per block for
-// Gemma).  Keys stream in tiles of 32:
+// Gemma).  Keys stream in tiles of 64 (two barriers per tile, so the
+// tile is as wide as the registers allow):
 //
 //   S^T(16 keys x 16 rows) = K_tile(16 x d) . Q^T(d x 16)     (MFMA, Q in VGPRs)
 //
-// computing S transposed leaves each lane with 8 scores of ONE query row, so
+// computing S transposed leaves each lane with 16 scores of ONE query row, so
 // the online-softmax statistics need only in-lane math plus two cross-lane
 // shuffles, and the probabilities are already in the A-operand layout of
 //
-//   O(16 rows x 16 d) += P(16 x 32 keys) . V(32 keys x 16 d)
+//   O(16 rows x 16 d) += P(16 x 32 keys) . V(32 keys x 16 d)   (per 32 keys)
 //
 // for which V is stored transposed in LDS (keys contiguous) as it is copied
 // in.  K/V rows past the key range are zero-filled; masked scores are -inf
@@ -31,7 +32,7 @@
 
 namespace fvx {
 
-constexpr int kKeyTile = 32;
+constexpr int kKeyTile = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int HDP, int HDV>
@@ -137,8 +138,8 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
   // Each thread's chunks, fixed over the tiles (computed once, 32-bit: the
   // views are below 2 GiB): global byte offsets relative to the tile's first
   // key and LDS element offsets.  K chunks are key-major (key i / kchunks,
-  // dims 8 (i % kchunks)); V^T chunks 8 consecutive keys of dim i / 4;
-  // row-major V chunks key i % 32, dims 8 (i / 32).
+  // dims 8 (i % kchunks)); V^T chunks 8 consecutive keys of dim i / (tile
+  // / 8); row-major V chunks key i % tile, dims 8 (i / tile).
   const bool vt = p.v_d_stride > 0;
   const uint32_t kts2 = (uint32_t)p.k_tok_stride * 2u;
   const uint32_t vstep2 = vt ? 2u : (uint32_t)p.v_tok_stride * 2u;  // per key
@@ -153,9 +154,10 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     koff[c] = (uint32_t)kr * kts2 + (uint32_t)kc * 16u;
     kl[c] = kr * LDK + kc * 8;
     if (vt) {
-      vkey[c] = (i & 3) * 8;
-      voff[c] = ((uint32_t)(i >> 2) * (uint32_t)p.v_d_stride + (uint32_t)vkey[c]) * 2u;
-      vl[c] = (i >> 2) * LDV + vkey[c];
+      constexpr int KG = kKeyTile / 8;  // 8-key chunks per dim
+      vkey[c] = (i % KG) * 8;
+      voff[c] = ((uint32_t)(i / KG) * (uint32_t)p.v_d_stride + (uint32_t)vkey[c]) * 2u;
+      vl[c] = (i / KG) * LDV + vkey[c];
     } else {
       vkey[c] = i % kKeyTile;
       voff[c] = (uint32_t)vkey[c] * vstep2 + (uint32_t)(i / kKeyTile) * 16u;
@@ -194,9 +196,10 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     if (t0 + kKeyTile < kend) prefetch(t0 + kKeyTile);
 
     // Scores: lane holds keys t0 + kf*16 + 4g + e for its query row.
-    float s[2][4];
+    constexpr int KB = kKeyTile / 16, PC = kKeyTile / 32;
+    float s[KB][4];
 #pragma unroll
-    for (int kf = 0; kf < 2; ++kf) {
+    for (int kf = 0; kf < KB; ++kf) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss)
@@ -212,7 +215,7 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     }
     float tmax = -INFINITY;
 #pragma unroll
-    for (int kf = 0; kf < 2; ++kf)
+    for (int kf = 0; kf < KB; ++kf)
 #pragma unroll
       for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[kf][e]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -221,9 +224,9 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
     float psum = 0.f;
-    float pr[2][4];
+    float pr[KB][4];
 #pragma unroll
-    for (int kf = 0; kf < 2; ++kf)
+    for (int kf = 0; kf < KB; ++kf)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         pr[kf][e] = __builtin_amdgcn_exp2f(s[kf][e] - m_ref);
@@ -234,14 +237,19 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     l_run = l_run * alpha + psum;
     m_run = m_new;
 
-    // P as A operand: keys {4g+e} (e<4) and {16+4g+e} (e>=4).
-    float pf[8];
+    // P as A operand of key block c (32 keys): keys 32c + {4g+e} (e<4) and
+    // 32c + {16+4g+e} (e>=4).
+    bf16x8 pa[PC];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      pf[e] = pr[0][e];
-      pf[4 + e] = pr[1][e];
+    for (int c = 0; c < PC; ++c) {
+      float pf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pf[e] = pr[2 * c][e];
+        pf[4 + e] = pr[2 * c + 1][e];
+      }
+      pa[c] = pack8(pf);
     }
-    const bf16x8 pa = pack8(pf);
     // Rescale O rows 4g+j by alpha of that row (held by lane 4g+j).
     float al[4];
 #pragma unroll
@@ -250,15 +258,18 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
     for (int df = 0; df < ND; ++df) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) o[df][j] *= al[j];
-      const bf16_t* vt = &sVt[(df * 16 + fr) * LDV];
-      bf16x8 vb;
-      const uint2 lo = *(const uint2*)(vt + 4 * g);
-      const uint2 hi = *(const uint2*)(vt + 16 + 4 * g);
-      vb.w[0] = lo.x;
-      vb.w[1] = lo.y;
-      vb.w[2] = hi.x;
-      vb.w[3] = hi.y;
-      o[df] = mfma16x16x32(pa, vb, o[df]);
+#pragma unroll
+      for (int c = 0; c < PC; ++c) {
+        const bf16_t* vt = &sVt[(df * 16 + fr) * LDV + 32 * c];
+        bf16x8 vb;
+        const uint2 lo = *(const uint2*)(vt + 4 * g);
+        const uint2 hi = *(const uint2*)(vt + 16 + 4 * g);
+        vb.w[0] = lo.x;
+        vb.w[1] = lo.y;
+        vb.w[2] = hi.x;
+        vb.w[3] = hi.y;
+        o[df] = mfma16x16x32(pa[c], vb, o[df]);
+      }
     }
   }
 
