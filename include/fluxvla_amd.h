@@ -68,7 +68,9 @@ enum fvx_act { FVX_ACT_NONE = 0, FVX_ACT_SILU = 1, FVX_ACT_GELU_TANH = 2 };
  *   v += pos[(m % pos_period) * ldp + n]             if pos
  *   c[orow(m) * ldc + n] = bf16(v)  (fp32 if out_f32)
  * where orow(m) = (m / row_group) * row_group_stride + m % row_group
- * (identity when row_group == 0).
+ * (identity when row_group == 0).  m, row_group, gate_group, pos_period and
+ * rtc_period must be below 2^31 (FVX_ERR_SHAPE otherwise): the epilogue
+ * divides by them in 32 bits.
  */
 typedef struct fvx_gemm_desc {
   const void* a; int64_t lda;      /* [M, K] bf16 */

@@ -82,6 +82,19 @@ def test_gemm_rejects_bad_arguments():
     assert 'n_q_heads + 2' in _err(lib)
 
 
+def test_gemm_rejects_periods_past_32_bits():
+    # the epilogue divides rows by row_group / gate_group / pos_period /
+    # rtc_period in 32 bits, so the host refuses values from 2^31 on
+    lib = _lib.load()
+    for field in ('row_group', 'gate_group', 'pos_period', 'rtc_period'):
+        d = _lib.GemmDesc()
+        d.a, d.b, d.c = 4096, 8192, 16384
+        d.m, d.n, d.k, d.lda, d.ldb, d.ldc = 4, 8, 16, 16, 16, 8
+        setattr(d, field, 1 << 31)
+        assert lib.fvx_gemm(ctypes.byref(d), None) == _lib.FVX_ERR_SHAPE, field
+        assert '2^31' in _err(lib)
+
+
 def test_gemm_explicit_split_without_workspace_is_an_error():
     lib = _lib.load()
     d = _lib.GemmDesc()
