@@ -502,10 +502,26 @@ __device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
       const int64_t per = (nblk + xcount - 1) / xcount;
       const int64_t b0 = (int64_t)xrank * per;
       const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
+      // block b of the XCD's list: tile xcd + 8 (b / bpt), block b % bpt of
+      // it -- one division for the wave's first block, then steps of 4
+      // blocks carried into the next tile (the loop issues loads, not
+      // divisions)
+      const int nb = b1 > b0 + w ? (int)((b1 - b0 - w + 3) / 4) : 0;
+      if (nb > 0) {
+        const uint32_t ubpt = (uint32_t)bpt, first = (uint32_t)(b0 + w);
+        uint32_t bb = first % ubpt;
+        uint32_t off = (uint32_t)(xcd + 8 * (first / ubpt)) * (uint32_t)tb + bb * 1024u;
+        const uint32_t wrap = 8u * (uint32_t)tb - ubpt * 1024u;
 #pragma unroll 1
-      for (int64_t b = b0 + w; b < b1; b += 4) {
-        const int64_t j = xcd + 8 * (b / bpt);
-        load_lds16(rs, lds, (uint32_t)(j * tb + (b % bpt) * 1024) + (uint32_t)lane * 16u);
+        for (int q = 0; q < nb; ++q) {
+          load_lds16(rs, lds, off + (uint32_t)lane * 16u);
+          bb += 4;
+          off += 4096u;
+          while (bb >= ubpt) {
+            bb -= ubpt;
+            off += wrap;
+          }
+        }
       }
     } else {
       const int64_t nblk = (bytes + 1023) / 1024;
@@ -513,8 +529,8 @@ __device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
       const int64_t b0 = (int64_t)pw * per;
       const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
 #pragma unroll 1
-      for (int64_t b = b0 + w; b < b1; b += 4)
-        load_lds16(rs, lds, (uint32_t)(b * 1024) + (uint32_t)lane * 16u);
+      for (uint32_t off = (uint32_t)(b0 + w) * 1024u; off < (uint32_t)b1 * 1024u; off += 4096u)
+        load_lds16(rs, lds, off + (uint32_t)lane * 16u);
     }
   }
   wait_vmcnt<0>();
