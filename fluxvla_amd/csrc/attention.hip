@@ -79,7 +79,7 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
   const int64_t heads = p.heads;
   const int64_t R = p.sq * heads;
 
-  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
+  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
   const bf16_t* K = (const bf16_t*)p.k + zb * p.k_zs1 + zh * p.k_zs2;
   const bf16_t* V = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
@@ -98,8 +98,8 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
   // This lane's query row (B operand / softmax row).
   const int64_t qrow = (int64_t)rb * 64 + wave * 16 + fr;
   const bool qval = qrow < R;
-  const int64_t qtok = qval ? qrow / heads : 0;
-  const int64_t qhead = qval ? qrow % heads : 0;
+  const int64_t qtok = qval ? (uint32_t)qrow / (uint32_t)heads : 0;
+  const int64_t qhead = qval ? (uint32_t)qrow % (uint32_t)heads : 0;
   const int32_t qg = (qgrp && qval) ? qgrp[qtok] : 0;
   // Branch-free loads through buffer views (an out-of-range offset reads
   // zero), so that every load of a batch is in flight at once.
@@ -310,7 +310,7 @@ __device__ __forceinline__ void store_rows(const fvx_attn_desc& p, bf16_t* O,
   for (int j = 0; j < 4; ++j) {
     const int64_t r = row0 + j;
     if (r >= R) break;
-    const int64_t tok = r / heads, h = r % heads;
+    const int64_t tok = (uint32_t)r / (uint32_t)heads, h = (uint32_t)r % (uint32_t)heads;
     bf16_t* orow = O + tok * p.o_tok_stride + h * p.o_head_stride;
 #pragma unroll
     for (int df = 0; df < ND; ++df) {
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(fvx_attn_desc p,
   const int fr = lane & 15, g = lane >> 4;
   const int rb = blockIdx.x, z = blockIdx.z;
   const int64_t R = p.sq * p.heads;
-  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
+  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
   bf16_t* O = (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2;
   const int64_t blk = (int64_t)z * n_row_blocks + rb;
   const float* ws = (const float*)p.workspace + blk * splits * PF;
@@ -451,7 +451,7 @@ __device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int z, int r,
                                           int d0, int hs, const float* v) {
   const int heads = (int)p.heads;
   const int tok = row_tok(r, heads, hs), h = r - tok * heads;
-  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
+  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
   bf16_t* O = (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2;
   bf16_t* dst = O + (int64_t)tok * p.o_tok_stride + (int64_t)h * p.o_head_stride + d0;
   bf16_t* fdst = p.o_frag ? (bf16_t*)p.o_frag + frag_offset((int64_t)z * p.sq + tok,
@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   const int split = (item / n_rg) % splits;
   const int z = item / (n_rg * splits);
   const int heads = (int)p.heads, R = (int)p.sq * heads;
-  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
+  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
   const bf16_t* K = (const bf16_t*)p.k + zb * p.k_zs1 + zh * p.k_zs2;
   const bf16_t* Vt = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
@@ -1055,7 +1055,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
   const int split = (item / n_rgw) % splits;
   const int z = item / (n_rgw * splits);
   const int heads = (int)p.heads, R = (int)p.sq * heads;
-  const int64_t zb = z / p.zdiv, zh = z % p.zdiv;
+  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
   const bf16_t* K = (const bf16_t*)p.k + zb * p.k_zs1 + zh * p.k_zs2;
   const bf16_t* Vt = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
@@ -1536,6 +1536,10 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
   FVX_REQUIRE(d.sq >= 0 && d.sk >= 0 && d.heads > 0 && d.n_problems >= 0 &&
                   d.zdiv > 0,
               FVX_ERR_SHAPE, "attention: bad sizes");
+  // problem and query-row indices divide in 32 bits
+  FVX_REQUIRE(d.zdiv < ((int64_t)1 << 31) && d.sq * d.heads < ((int64_t)1 << 31) &&
+                  d.n_problems < ((int64_t)1 << 31),
+              FVX_ERR_SHAPE, "attention: sq * heads, n_problems and zdiv must be < 2^31");
   FVX_REQUIRE(d.head_dim > 0 && d.head_dim % 8 == 0 &&
                   (d.head_dim <= 80 || d.head_dim == 256),
               FVX_ERR_SHAPE,

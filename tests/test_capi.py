@@ -126,6 +126,10 @@ def test_norm_and_attention_reject_bad_arguments():
     a.head_dim = 256
     a.kgrp = 4096
     assert lib.fvx_attention(ctypes.byref(a), None) == _lib.FVX_ERR_ARG
+    a.kgrp = 0
+    a.sq, a.heads = 1 << 28, 8  # query rows past 32-bit indices
+    assert lib.fvx_attention(ctypes.byref(a), None) == _lib.FVX_ERR_SHAPE
+    assert '2^31' in _err(lib)
 
 
 def test_data_movement_rejects_bad_arguments():
