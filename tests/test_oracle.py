@@ -698,3 +698,159 @@ def test_rtc_method_selection():
     assert O.rtc_inputs(cfg, None, 3, {'method': 'prefix'})[1] is None
     assert O.rtc_inputs(cfg, prev, 3, {'enabled': True})[1] == 'prefix'
     assert O.rtc_inputs(PI0Config(), prev, 3, {})[0].shape[-1] == 14
+
+
+# ---------------------------------------------------------------------------
+# denoise_step: suffix positions and the output rows
+# ---------------------------------------------------------------------------
+def _joint_cfg():
+    """PI0 with the expert shaped like the prefix LLM, so one Gemma stack
+    can run the joint [prefix | suffix] sequence."""
+    return tiny(llm_hidden=64, exp_hidden=64, llm_mlp=96, exp_mlp=96,
+                heads=4, head_dim=16, proj_width=64, llm_layers=2,
+                exp_layers=2, vit_layers=0)
+
+
+def _joint_setup():
+    cfg = _joint_cfg()
+    sd = {k: v.float() for k, v in make_state_dict(cfg, seed=50).items()}
+    # sharp attention (scores of order 10), so relative positions matter
+    for k in list(sd):
+        if '.q_proj.' in k or '.k_proj.' in k:
+            sd[k] = sd[k] * 25
+    # the expert becomes a copy of the prefix LLM (layers and final norm)
+    for k in list(sd):
+        if k.startswith('llm_backbone.layers.') or k == 'llm_backbone.norm.weight':
+            sd['llm_expert.' + k[len('llm_backbone.'):]] = sd[k].clone()
+    g = torch.Generator().manual_seed(51)
+    B, Sp = 2, 13
+    prefix = torch.randn(B, Sp, cfg.llm_hidden, generator=g)
+    ppad = torch.ones(B, Sp, dtype=torch.bool)
+    ppad[0, 4:7] = False        # a masked camera in the middle
+    ppad[1, 10:] = False        # a padded prompt tail
+    patt = torch.zeros(B, Sp, dtype=torch.bool)
+    states = torch.rand(B, cfg.state_dim, generator=g) * 2 - 1
+    x_t = torch.randn(B, cfg.n_action_steps, cfg.max_action_dim, generator=g)
+    t = torch.tensor([0.8, 0.3])
+    return cfg, sd, prefix, ppad, patt, states, x_t, t
+
+
+def _joint_reference(cfg, sd, prefix, ppad, patt, states, x_t, t):
+    """The training forward's joint pass (pi0_flowmatching.py:590-628): one
+    sequence [prefix | suffix], positions cumsum(joint pad) - 1 and the
+    joint make_att_2d_masks; with the expert equal to the LLM the per-tower
+    layers (:323-434) are one Gemma stack.  The velocity is
+    action_out_proj(suffix_out[:, -n_action_steps:])."""
+    s_emb, spad, satt, _ = O.embed_suffix(sd, cfg, states, x_t, t)
+    embs = torch.cat([prefix, s_emb], 1)
+    pad = torch.cat([ppad, spad], 1)
+    att = torch.cat([patt, satt], 1)
+    pos = torch.cumsum(pad.long(), 1) - 1
+    h, _ = O.gemma_model(sd, 'llm_backbone', cfg.llm_layers, embs, pos,
+                         O.make_att_2d_masks(pad, att), cfg)
+    out = h[:, -cfg.n_action_steps:]
+    return O.linear(out, sd['action_out_proj.projector.weight'],
+                    sd['action_out_proj.projector.bias'])
+
+
+def _cached_velocity(denoise, cfg, sd, prefix, ppad, patt, states, x_t, t):
+    """predict_action's cache (pi0_flowmatching.py:722-742) then one
+    denoise step."""
+    pos = torch.cumsum(ppad.long(), 1) - 1
+    _, kvs = O.gemma_model(sd, 'llm_backbone', cfg.llm_layers, prefix, pos,
+                           O.make_att_2d_masks(ppad, patt), cfg,
+                           kv_only_last=True)
+    return denoise(sd, cfg, states, ppad, kvs, x_t, t)
+
+
+def _planted_denoise(pos_shift=0, first_rows=False):
+    """denoise_step with one planted mistake: suffix positions shifted by
+    pos_shift, or the first n_action_steps rows taken instead of the last."""
+    def fn(P, cfg, states, prefix_pad, kvs, x_t, timestep):
+        embs, spad, satt, cond = O.embed_suffix(P, cfg, states, x_t, timestep)
+        B, Ss = spad.shape
+        full = torch.cat([prefix_pad[:, None, :].expand(B, Ss, -1),
+                          O.make_att_2d_masks(spad, satt)], dim=2)
+        pos = (prefix_pad.sum(-1)[:, None] + torch.cumsum(spad, 1) - 1
+               + pos_shift)
+        h, _ = O.gemma_model(P, 'llm_expert', cfg.exp_layers, embs, pos, full,
+                             cfg, past_kvs=kvs, cond=cond)
+        n = cfg.n_action_steps
+        out = h[:, :n] if first_rows else h[:, -n:]
+        return O.linear(out, P['action_out_proj.projector.weight'],
+                        P['action_out_proj.projector.bias'])
+    return fn
+
+
+def test_denoise_step_cached_equals_joint_pass():
+    """KV caching must not change the velocity: denoise_step's suffix rows
+    over the cached prefix K/V equal the suffix rows of the joint pass,
+    whose positions come from the training forward's cumsum over the whole
+    pad mask (a different code path of the reference).  A suffix position
+    off by one, or the state row kept in the output, breaks it."""
+    args = _joint_setup()
+    want = _joint_reference(*args)
+    got = _cached_velocity(O.denoise_step, *args)
+    assert got.shape == want.shape == (2, args[0].n_action_steps, 32)
+    assert torch.allclose(got, want, atol=2e-5, rtol=1e-4)
+    for bad in (_planted_denoise(pos_shift=-1), _planted_denoise(pos_shift=1),
+                _planted_denoise(first_rows=True)):
+        assert not torch.allclose(_cached_velocity(bad, *args), want,
+                                  atol=1e-3)
+
+
+def test_product_suffix_positions_follow_joint_cumsum(golden):
+    """The kernels' suffix positions (attention_groups) are the suffix part
+    of cumsum(joint pad) - 1, the training forward's rule, on the
+    reference's own pad fixtures and on a padded prefix."""
+    from fluxvla_amd.pi0_inference import attention_groups
+    cases = []
+    for which in ('pi0', 'pi05'):
+        cases.append((torch.from_numpy(golden[f'{which}_prefix_pad_masks']).bool(),
+                      torch.from_numpy(golden[f'{which}_suffix_pad_masks']).bool(),
+                      torch.from_numpy(golden[f'{which}_suffix_att_masks'])))
+    ppad = _joint_setup()[3]
+    cases.append((ppad, torch.ones(2, 51, dtype=torch.bool),
+                  torch.tensor([[1, 1] + [0] * 49] * 2)))
+    for ppad, spad, satt in cases:
+        _, _, _, pos_pre, pos_suf = attention_groups(ppad, satt[0].int().tolist())
+        joint = torch.cumsum(torch.cat([ppad, spad], 1).long(), 1) - 1
+        S = ppad.shape[1]
+        assert torch.equal(pos_suf.long(), joint[:, S:])
+        valid = ppad
+        assert torch.equal(pos_pre.long()[valid], joint[:, :S][valid])
+
+
+def test_denoise_step_output_rows_closed_form():
+    """pi0_flowmatching.py:826-828: v = action_out_proj(final_norm(h))
+    over the last n_action_steps rows, i.e. without the state row.  With a
+    zero expert the stream is the suffix embedding itself; with the _eye_sd
+    projections the action rows are 2 silu(x_t) (zero past dim 32), so
+    v = action_out(y * rsqrt(mean(y^2) + eps) * (1 + w)), y = 2 silu(x_t)."""
+    cfg = tiny(proj_width=64, exp_hidden=64, exp_mlp=96, heads=2,
+               head_dim=16, vit_layers=0, llm_layers=0, exp_layers=1)
+    sd = {k: torch.zeros(v.shape) for k, v in
+          make_state_dict(cfg, seed=52).items() if k.startswith('llm_expert.')}
+    sd.update(_eye_sd(cfg))
+    g = torch.Generator().manual_seed(53)
+    w_norm = torch.randn(cfg.exp_hidden, generator=g) * 0.1
+    sd['llm_expert.norm.weight'] = w_norm
+    W = torch.randn(cfg.max_action_dim, cfg.exp_hidden, generator=g) * 0.1
+    b = torch.randn(cfg.max_action_dim, generator=g) * 0.1
+    sd['action_out_proj.projector.weight'] = W
+    sd['action_out_proj.projector.bias'] = b
+    B, Sp = 2, 7
+    ppad = torch.ones(B, Sp, dtype=torch.bool)
+    kvs = [(torch.randn(B, 1, Sp, cfg.head_dim, generator=g),
+            torch.randn(B, 1, Sp, cfg.head_dim, generator=g))]
+    states = torch.rand(B, cfg.state_dim, generator=g) * 2 - 1
+    x_t = torch.randn(B, cfg.n_action_steps, cfg.max_action_dim, generator=g)
+    t = torch.tensor([0.6, 0.2])
+    y = torch.zeros(B, cfg.n_action_steps, cfg.exp_hidden)
+    y[..., :cfg.max_action_dim] = 2 * x_t * torch.sigmoid(x_t)
+    n = y / torch.sqrt((y * y).mean(-1, keepdim=True) + cfg.rms_eps)
+    want = (n * (1 + w_norm)) @ W.t() + b
+    got = O.denoise_step(sd, cfg, states, ppad, kvs, x_t, t)
+    assert torch.allclose(got, want, atol=1e-5)
+    bad = _planted_denoise(first_rows=True)(sd, cfg, states, ppad, kvs, x_t, t)
+    assert not torch.allclose(bad, want, atol=1e-3)
