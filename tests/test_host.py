@@ -136,7 +136,7 @@ def _reference_style_cfg(type_name, pi05):
 def test_registry_reads_reference_configs(name, pi05):
     from fluxvla_amd.config import PI0Config
     from fluxvla_amd.registry import VLAS, config_from_reference
-    cfg = config_from_reference(_reference_style_cfg(name, pi05))
+    cfg = config_from_reference(_reference_style_cfg(name, pi05), num_views=3)
     assert name in VLAS
     assert cfg == PI0Config(pi05=pi05)
 
@@ -144,7 +144,7 @@ def test_registry_reads_reference_configs(name, pi05):
 def test_registry_rejects_unknown_type():
     from fluxvla_amd.registry import build_vla_from_cfg
     with pytest.raises(KeyError, match='not a registered'):
-        build_vla_from_cfg(dict(type='OpenVLA'), {}, device='cpu')
+        build_vla_from_cfg(dict(type='OpenVLA'))
 
 
 def test_fragment_major_layouts():
