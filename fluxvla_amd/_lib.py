@@ -22,6 +22,7 @@ FVX_ERR_ALIGN = -3
 FVX_ERR_LAUNCH = -4
 FVX_ERR_ARG = -5
 FVX_ERR_WORKSPACE = -6
+FVX_ERR_MERGE = -7
 
 # fvx_gemm_noalloc's static split-K scratch per GPU
 GEMM_NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -101,6 +102,7 @@ class AttnDesc(ctypes.Structure):
         ('prefetch', c_vp * 8), ('prefetch_bytes', c_i64 * 8),
         ('prefetch_tile_bytes', c_i64 * 8),
         ('prefetch_wgs', c_i32),
+        ('merge_no_wait', c_i32),
     ]
 
 
@@ -140,6 +142,7 @@ SIGNATURES = {
                                        c_f32, c_vp]),
     'fvx_attention_workspace_bytes': (c_i64, [ctypes.POINTER(AttnDesc)]),
     'fvx_attention': (c_i32, [ctypes.POINTER(AttnDesc), c_vp]),
+    'fvx_attention_check': (c_i32, [c_vp, c_i64, c_vp]),
     'fvx_im2col_patches': (c_i32, [c_vp, c_i32, c_i32, c_vp, c_i64, c_i64,
                                    c_i64, c_i64, c_i64, c_f32, c_f32, c_vp]),
     'fvx_embed_tokens': (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_f32,

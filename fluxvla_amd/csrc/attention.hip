@@ -409,9 +409,13 @@ constexpr int kDecOP = 256 + 4;                 // LDS pitch (floats), O rows
 constexpr int64_t kDecPO = 64 * 256 / 2;
 constexpr int64_t kDecPF = kDecPO + 2 * 64;
 // An attention workspace opens with the 64-row groups' arrival counters of
-// the in-launch merge (one 256-byte line each); the split partials follow.
+// the in-launch merge (one 256-byte line each); the last line holds the
+// merge status word (the number of merging workgroups that stopped waiting
+// for their key ranges; fvx_attention_check reads and clears it); the split
+// partials follow.
 constexpr int64_t kAttnCounterBytes = 64 * 1024;
-constexpr int kAttnMaxGroups = (int)(kAttnCounterBytes / 256);  // a 256-byte line each
+constexpr int kAttnMaxGroups = (int)(kAttnCounterBytes / 256) - 1;
+constexpr int64_t kAttnStatusWord = (kAttnCounterBytes - 256) / 4;
 constexpr int kDecMergeSpin = 1 << 16;  // polls before a merge stops waiting
 
 // The value of a 32-bit word as the L2 holds it: a returning atomic add of 0
@@ -611,21 +615,33 @@ __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int
 // Thread 0 polls the group's arrival counter (an L2 atomic) until it reaches
 // `splits` -- every range's workgroup has a lower block index on the same
 // XCD, so it was dispatched first, and it waits on nothing; the wait is
-// bounded regardless -- then the partials are read from that XCD's L2.  The
+// bounded regardless (`polls`; 0 only from the descriptor's test hook) --
+// then the partials are read from that XCD's L2.  A workgroup whose polls
+// run out counts itself in the status word and merges what has arrived:
+// that call's output is wrong, and a range arriving after the counters'
+// reset leaves a count behind, so fvx_attention_check reports the status
+// and clears every counter before the next call relies on them.  The
 // group's last merging workgroup resets both of its counters.
 __device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, int hs,
-                             uint32_t* counters, int grp, int chunk) {
+                             uint32_t* counters, int grp, int chunk, int polls) {
   const int tid = threadIdx.x;
   const int R = (int)(p.sq * p.heads);
   const int z = grp / n_rg, rg = grp % n_rg;
   const int r = rg * 64 + 8 * chunk + (tid >> 5), d0 = (tid & 31) * 8;
   uint32_t* ctr = counters + (int64_t)grp * 64;
   if (tid == 0) {
+    bool arrived = false;
 #pragma unroll 1
-    for (int it = 0; it < kDecMergeSpin; ++it) {
-      if (l2_atomic_read(ctr) >= (uint32_t)splits) break;
+    for (int it = 0; it < polls; ++it) {
+      if (l2_atomic_read(ctr) >= (uint32_t)splits) {
+        arrived = true;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
+    if (!arrived)
+      __hip_atomic_fetch_add(counters + kAttnStatusWord, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   dec_merge8<1>(p, n_rg, splits, hs, z, r, d0);
@@ -663,7 +679,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   if (counters && (int)blockIdx.x >= n_items && (int)blockIdx.x < merge_first) {
     const int j = slot - n_items / 8, grp = xcd + 8 * (j / 8);
     if (grp < n_groups && (grp % n_rg) * 64 + 8 * (j % 8) < (int)(p.sq * p.heads))
-      dec_merge_wg(p, n_rg, splits, hs, counters, grp, j % 8);
+      dec_merge_wg(p, n_rg, splits, hs, counters, grp, j % 8,
+                   p.merge_no_wait ? 0 : kDecMergeSpin);
     return;
   }
   const int pf0 = counters ? merge_first : n_items;
@@ -1632,4 +1649,44 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
     return launch_status("attention(decode merge)");
   }
   return run_generic(d, s);
+}
+// Zeroes the attention workspace's counter region (a fill kernel, not a
+// memset node: callers may run it next to captured work).
+__global__ void attn_counters_clear_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+extern "C" int fvx_attention_check(void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  clear_error();
+  FVX_REQUIRE(workspace, FVX_ERR_NULL, "attention_check: workspace is NULL");
+  FVX_REQUIRE(workspace_bytes >= kAttnCounterBytes, FVX_ERR_WORKSPACE,
+              "attention_check: the workspace must hold the %lld-byte counter "
+              "region, got %lld bytes", (long long)kAttnCounterBytes,
+              (long long)workspace_bytes);
+  FVX_REQUIRE(aligned16(workspace), FVX_ERR_ALIGN,
+              "attention_check: workspace must be 16B aligned");
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* counters = (uint32_t*)workspace;
+  uint32_t status = 0;
+  hipError_t e = hipMemcpyAsync(&status, counters + kAttnStatusWord, 4,
+                                hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess)
+    return set_error(FVX_ERR_LAUNCH, "attention_check: reading the status "
+                     "failed: %s", hipGetErrorString(e));
+  if (status == 0) return FVX_OK;
+  const int n = (int)(kAttnCounterBytes / 4);
+  hipLaunchKernelGGL(attn_counters_clear_kernel, dim3((n + 255) / 256), dim3(256), 0, s,
+                     counters, n);
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess)
+    return set_error(FVX_ERR_LAUNCH, "attention_check: clearing the counters "
+                     "failed: %s", hipGetErrorString(e));
+  return set_error(FVX_ERR_MERGE,
+                   "attention: %u merging workgroup(s) stopped waiting for "
+                   "their key ranges, so an earlier call's output is wrong; "
+                   "the merge counters are cleared", status);
 }

@@ -652,6 +652,17 @@ def run_attention(d):
     _lib.call('fvx_attention', ctypes.byref(d), _stream())
 
 
+def attention_check(device=None):
+    """Raise FvxError (status FVX_ERR_MERGE) when an in-launch merge of the
+    decode attention on ``device`` stopped waiting for its key ranges since
+    the last check; the merge counters are then cleared, so the next call is
+    correct.  Waits for the current stream: call it after a call or a chunk,
+    never under graph capture."""
+    ws = workspace(device, 'attn')
+    _lib.call('fvx_attention_check', ctypes.c_void_p(ws.data_ptr()),
+              ctypes.c_int64(ws.numel()), _stream())
+
+
 def _device_buffer(t):
     """The device tensor behind a weight object (fragment-major, fp8 or
     plain)."""
@@ -688,7 +699,7 @@ def _set_prefetch(d, prefetch, prefetch_wgs, place=True):
 
 def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
                   v_transposed=False, o_frag=None, prefetch=None,
-                  prefetch_wgs=0, prefetch_place=True):
+                  prefetch_wgs=0, prefetch_place=True, merge_no_wait=False):
     """Batched multi-query attention.
 
     q: [B, Sq, H, D] (or [B, Sq, H*D]); k: [B, Sk, D] (row stride may exceed
@@ -700,7 +711,9 @@ def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
     ``prefetch``: up to 8 tensors / prepared weights that idle workgroups
     of the decode kernel read into the caches meanwhile (the next GEMMs'
     weights; ``prefetch_wgs`` of them, 0 = fill the CUs; see
-    _set_prefetch for ``prefetch_place``)."""
+    _set_prefetch for ``prefetch_place``).  ``merge_no_wait`` is a test
+    hook: the in-launch merge gives up its wait at once (attention_check
+    then reports it)."""
     B, Sq = q.shape[0], q.shape[1]
     D = k.shape[-1]
     H = (q.shape[2] if q.dim() == 4 else q.shape[2] // D)
@@ -726,6 +739,7 @@ def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
         d.o_frag = o_frag.buf.data_ptr()
     if prefetch:
         _set_prefetch(d, prefetch, prefetch_wgs, prefetch_place)
+    d.merge_no_wait = int(bool(merge_no_wait))
     run_attention(d)
     return o
 

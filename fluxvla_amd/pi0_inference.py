@@ -273,6 +273,9 @@ class PI0Inference:
         # (A scaled by 1 + scale as it is loaded, the shift as a bias, the
         # gate read from the style row by the residual epilogues)
         self.fold_adarms = True
+        # predict_action ends with the attention merge status check (it
+        # waits for the chunk); off, callers run kernels.attention_check
+        self.check_merge = True
         self.weight_dtype = weight_dtype
         self.fp8_cache = fp8_cache
         self.fp8_cache_hit = False
@@ -964,4 +967,10 @@ class PI0Inference:
             g.replay()
         else:
             self._run(B, rtc)
-        return b['xt'].clone()
+        out = b['xt'].clone()
+        if self.check_merge:
+            # waits for the chunk; raises if an in-launch attention merge
+            # stopped waiting (the chunk is then wrong) and clears its
+            # counters for the next call
+            K.attention_check(self.device)
+        return out

@@ -43,6 +43,7 @@ enum fvx_status {
   FVX_ERR_LAUNCH = -4,    /* the HIP launch itself failed */
   FVX_ERR_ARG = -5,       /* an enum / flag argument is invalid */
   FVX_ERR_WORKSPACE = -6, /* workspace too small for the requested split */
+  FVX_ERR_MERGE = -7,     /* an in-launch merge stopped waiting (fvx_attention_check) */
 };
 
 /* GEMM epilogue modes. */
@@ -356,10 +357,28 @@ typedef struct fvx_attn_desc {
   int64_t prefetch_bytes[8];
   int64_t prefetch_tile_bytes[8];
   int32_t prefetch_wgs;
+  /* Test hook, 0 in every real call: nonzero makes the in-launch merge of
+   * the decode path stop waiting for its key ranges at once, as if its
+   * bounded wait had run out (see fvx_attention_check). */
+  int32_t merge_no_wait;
 } fvx_attn_desc;
 
 int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d);
 int fvx_attention(const fvx_attn_desc* d, void* stream);
+
+/*
+ * Status of the decode path's in-launch merge (no counterpart in the
+ * reference, whose attention has no in-launch merge).  The merging
+ * workgroups wait for the key ranges of their row group with a bounded
+ * poll; a workgroup whose poll runs out merges what has arrived, so the
+ * output of that call is wrong, and it counts itself in a status word of
+ * the workspace's counter region.  This call waits for `stream`, reads the
+ * word and, when it is non-zero, clears the whole counter region (so the
+ * next call starts from zero counts) and returns FVX_ERR_MERGE.  It
+ * synchronizes: call it after a call or a chunk, outside graph capture.
+ */
+int fvx_attention_check(void* workspace, int64_t workspace_bytes,
+                        void* stream);
 
 /*
  * SigLIP patch im2col: images [n_img, 3, H, W] (or [n_img, H, W, 3] with
