@@ -6,4 +6,5 @@ from .serializers import (FORMAT_MSGPACK, FORMAT_PROTOBUF, MsgSerializer,  # noq
                           decode_predict_request, decode_predict_response,
                           detect_format, encode_predict_request,
                           encode_predict_response)
-from .server import ObsToInputs, PolicyServer, create_server  # noqa: F401
+from .server import (ChunkEndpoint, ObsToInputs, PolicyServer,  # noqa: F401
+                     create_server)
