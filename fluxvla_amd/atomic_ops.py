@@ -29,7 +29,7 @@ import torch
 
 from . import kernels as _kern
 from ._lib import ACT_GELU_TANH, ACT_SILU
-from .weight_layout import as_nk, patch_weight_nk
+from .weight_layout import _cached, as_nk, patch_weight_nk
 
 RMS_EPS = 1e-6
 
@@ -134,13 +134,10 @@ def _rope_args(rope_weight, rows, device):
     if rope_weight.dtype == torch.float32 and rope_weight.dim() == 3:
         table = rope_weight
     else:  # reference table: interleaved (cos, sin) bf16 [positions, hd]
-        key = ('tab', rope_weight.data_ptr(), tuple(rope_weight.shape),
-               rope_weight._version, rope_weight.device)
-        hit = _rope_cache.get(key)
-        if hit is None:  # the source stays referenced: its address is its own
-            hit = _rope_cache[key] = (rope_weight, rope_weight.float().reshape(
-                rope_weight.shape[0], -1, 2).contiguous())
-        table = hit[1]
+        # converted once into a cached fp32 copy (refreshed in place when
+        # the table changes), like the weights' [out, in] copies
+        table = _cached(rope_weight, 'rope', lambda t: t.float().reshape(
+            t.shape[0], -1, 2).contiguous())
     if table.shape[0] < rows:
         raise ValueError(f'rope table has {table.shape[0]} positions, need '
                          f'{rows}')

@@ -92,20 +92,51 @@ class NKWeight:
                 f'{tuple(self.nk.shape)} [out, in], {self.dtype})')
 
 
-# [out, in] copies of reference-layout weights, made once per weight:
-# key -> (source tensor, kept alive so its address stays its own; copy)
+# [out, in] copies of reference-layout weights, made once per weight and
+# kept at one address: key (tag, address, shape, strides, dtype, device) ->
+# [source tensor (kept alive so its address stays its own), the source's
+# version when the copy was made, the copy, the function that makes it].
+# An in-place update of the source (a new version) is copied into the same
+# copy tensor, so the cache holds one entry per weight and a HIP graph
+# captured over the copy reads the update once the copy is refreshed.
 _nk_cache = {}
 
 
 def clear_layout_cache():
     """Drop the cached [out, in] copies (and the references that keep their
-    source weights alive), e.g. after replacing a model's weights."""
+    source weights alive), e.g. after replacing a model's weights.  Graphs
+    captured over the dropped copies must be captured again."""
     _nk_cache.clear()
 
 
-def _key(t, tag):
-    return (tag, t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype,
-            t.device, t._version)
+def refresh_layout_cache():
+    """Bring every cached copy up to date with an in-place update of its
+    source (eager calls do this for the weights they use; call it before
+    replaying a graph captured before such an update).  Returns the number
+    of copies rewritten."""
+    n = 0
+    for e in _nk_cache.values():
+        if e[0]._version != e[1]:
+            e[2].copy_(e[3](e[0]))
+            e[1] = e[0]._version
+            n += 1
+    return n
+
+
+def _cached(w, tag, make):
+    k = (tag, w.data_ptr(), tuple(w.shape), tuple(w.stride()), w.dtype,
+         w.device)
+    e = _nk_cache.get(k)
+    if e is None:
+        e = _nk_cache[k] = [w, w._version, make(w), make]
+    elif e[1] != w._version:
+        e[2].copy_(make(w))
+        e[1] = w._version
+    return e[2]
+
+
+def _transpose(w):
+    return w.t().contiguous()
 
 
 def as_nk(w):
@@ -120,11 +151,7 @@ def as_nk(w):
     if w.dim() != 2:
         raise ValueError(f'a reference-layout weight must be [in, out], got '
                          f'shape {tuple(w.shape)}')
-    k = _key(w, 'kn')
-    hit = _nk_cache.get(k)
-    if hit is None:
-        hit = _nk_cache[k] = (w, w.t().contiguous())
-    return hit[1]
+    return _cached(w, 'kn', _transpose)
 
 
 def patch_weight_nk(w, k_pad):
@@ -140,15 +167,13 @@ def patch_weight_nk(w, k_pad):
     if w.dim() != 4:
         raise ValueError('a reference patch weight is [kH, kW, C, out], got '
                          f'shape {tuple(w.shape)}')
-    k = _key(w, f'patch{k_pad}')
-    hit = _nk_cache.get(k)
-    if hit is None:
-        kh, kw, c, n = w.shape
-        flat = w.permute(3, 2, 0, 1).reshape(n, c * kh * kw)
-        t = torch.zeros(n, k_pad, dtype=w.dtype, device=w.device)
-        t[:, :c * kh * kw] = flat
-        hit = _nk_cache[k] = (w, t)
-    return hit[1]
+
+    def make(src):
+        kh, kw, c, n = src.shape
+        t = torch.zeros(n, k_pad, dtype=src.dtype, device=src.device)
+        t[:, :c * kh * kw] = src.permute(3, 2, 0, 1).reshape(n, c * kh * kw)
+        return t
+    return _cached(w, f'patch{k_pad}', make)
 
 
 class PatchWeight(NKWeight):

@@ -51,12 +51,26 @@ def test_plain_tensor_means_in_out_and_nkweight_means_out_in():
 
 
 def test_transposed_copy_is_cached_and_sees_in_place_updates():
+    """One cache entry per weight: an in-place update is copied into the
+    same [out, in] tensor (at the same address, so a graph captured over it
+    reads the update after a refresh), never a second copy."""
+    from fluxvla_amd import weight_layout as WL
+    WL.clear_layout_cache()
     w = torch.randn(8, 4)
     a = as_nk(w)
     assert as_nk(w) is a                            # made once
-    w.mul_(2.0)                                     # version bump
-    b = as_nk(w)
-    assert b is not a and torch.equal(b, w.t())
+    ptr = a.data_ptr()
+    for scale in (2.0, 3.0):                        # two updates
+        w.mul_(scale)                               # version bump
+        b = as_nk(w)
+        assert b is a and b.data_ptr() == ptr and torch.equal(b, w.t())
+    assert len(WL._nk_cache) == 1
+    # a graph replay does not call as_nk: refresh_layout_cache updates the
+    # copy for it
+    w.add_(1.0)
+    assert WL.refresh_layout_cache() == 1 and torch.equal(a, w.t())
+    assert WL.refresh_layout_cache() == 0
+    WL.clear_layout_cache()
 
 
 def test_patch_weight_layouts():
