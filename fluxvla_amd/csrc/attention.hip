@@ -482,62 +482,8 @@ __device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int z, int r,
 // completes before the wave ends.
 __device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
                              unsigned char* smem) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(smem) + w * 1024);
-  const int xcd = (int)(blockIdx.x & 7);
-  // prefetch workgroups on this XCD: indices q0, q0 + 8, ... < npw
-  const int q0 = ((xcd - first) % 8 + 8) % 8;
-  const int xrank = (pw - q0) / 8, xcount = (npw - q0 + 7) / 8;
-#pragma unroll 1
-  for (int r = 0; r < 8; ++r) {
-    const int64_t bytes = p.prefetch_bytes[r];
-    if (!p.prefetch[r] || bytes <= 0) continue;
-    // 32-bit offsets: a range of up to 2 GiB per view
-    const i32x4_t rs = make_rsrc4(p.prefetch[r], bytes < 0x7fffffff ? (uint32_t)bytes
-                                                                    : 0x7fffffffu);
-    const int64_t tb = p.prefetch_tile_bytes[r];
-    if (tb > 0) {
-      // this XCD's tiles j = xcd, xcd + 8, ...: their blocks in order, a
-      // contiguous share per prefetch workgroup of the XCD
-      const int64_t bpt = tb / 1024, ntiles = bytes / tb;
-      const int64_t xt = ntiles > xcd ? (ntiles - xcd + 7) / 8 : 0;
-      const int64_t nblk = xt * bpt;
-      const int64_t per = (nblk + xcount - 1) / xcount;
-      const int64_t b0 = (int64_t)xrank * per;
-      const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
-      // block b of the XCD's list: tile xcd + 8 (b / bpt), block b % bpt of
-      // it -- one division for the wave's first block, then steps of 4
-      // blocks carried into the next tile (the loop issues loads, not
-      // divisions)
-      const int nb = b1 > b0 + w ? (int)((b1 - b0 - w + 3) / 4) : 0;
-      if (nb > 0) {
-        const uint32_t ubpt = (uint32_t)bpt, first = (uint32_t)(b0 + w);
-        uint32_t bb = first % ubpt;
-        uint32_t off = (uint32_t)(xcd + 8 * (first / ubpt)) * (uint32_t)tb + bb * 1024u;
-        const uint32_t wrap = 8u * (uint32_t)tb - ubpt * 1024u;
-#pragma unroll 1
-        for (int q = 0; q < nb; ++q) {
-          load_lds16(rs, lds, off + (uint32_t)lane * 16u);
-          bb += 4;
-          off += 4096u;
-          while (bb >= ubpt) {
-            bb -= ubpt;
-            off += wrap;
-          }
-        }
-      }
-    } else {
-      const int64_t nblk = (bytes + 1023) / 1024;
-      const int64_t per = (nblk + npw - 1) / npw;
-      const int64_t b0 = (int64_t)pw * per;
-      const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
-#pragma unroll 1
-      for (uint32_t off = (uint32_t)(b0 + w) * 1024u; off < (uint32_t)b1 * 1024u; off += 4096u)
-        load_lds16(rs, lds, off + (uint32_t)lane * 16u);
-    }
-  }
-  wait_vmcnt<0>();
+  prefetch_ranges<4>(p.prefetch, p.prefetch_bytes, p.prefetch_tile_bytes, pw, npw,
+                     first, lds_addr(smem));
 }
 
 // Row r (problem z), dims d0 .. d0 + 7 of the merged output from the split
@@ -1433,20 +1379,6 @@ static bool has_prefetch(const fvx_attn_desc& d) {
   return false;
 }
 
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-            hipSuccess || n <= 0)
-      n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
 
 struct DecodePlan {
   int n_rb, splits, n_items;

@@ -27,6 +27,21 @@ inline int launch_status(const char* what) {
   return FVX_OK;
 }
 
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 }  // namespace fvx
 
 #define FVX_REQUIRE(cond, code, ...)                    \

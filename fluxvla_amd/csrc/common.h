@@ -342,4 +342,76 @@ __device__ __forceinline__ float silu(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
+// Cache prefetch by the idle workgroups of a launch (no counterpart in the
+// reference).  Workgroup pw of npw prefetching ones (linear block ids first,
+// first + 1, ...; block b runs on XCD b % 8), NW waves, reads up to 8 device
+// ranges [ptr[r], ptr[r] + bytes[r]) by LDS DMA into a discarded 1 KiB slot
+// per wave (lds_base + 1024 w), so that the next kernels find them in the
+// caches.  tile_bytes[r] > 0: the range is a sequence of tiles of that size
+// (the 16-column tiles of a fragment-major weight) and tile j is read only by
+// the prefetching workgroups of XCD j % 8 -- the XCD whose GEMM workgroup
+// will read it -- so it lands in that XCD's L2; 0: an even split over all
+// prefetching workgroups (the memory-side cache).  Bytes and tile bytes are
+// multiples of 1024.
+template <int NW>
+__device__ void prefetch_ranges(const void* const* ptr, const int64_t* bytes_of,
+                                const int64_t* tile_bytes, int pw, int npw, int first,
+                                uint32_t lds_base) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base + w * 1024);
+  const int xcd = (pw + first) & 7;
+  // prefetching workgroups on this XCD: indices q0, q0 + 8, ... < npw
+  const int q0 = ((xcd - first) % 8 + 8) % 8;
+  const int xrank = (pw - q0) / 8, xcount = (npw - q0 + 7) / 8;
+#pragma unroll 1
+  for (int r = 0; r < 8; ++r) {
+    const int64_t bytes = bytes_of[r];
+    if (!ptr[r] || bytes <= 0) continue;
+    // 32-bit offsets: a range of up to 2 GiB per view
+    const i32x4_t rs = make_rsrc4(ptr[r], bytes < 0x7fffffff ? (uint32_t)bytes : 0x7fffffffu);
+    const int64_t tb = tile_bytes[r];
+    if (tb > 0) {
+      // this XCD's tiles j = xcd, xcd + 8, ...: their 1 KiB blocks in order,
+      // a contiguous share per prefetching workgroup of the XCD
+      const int64_t bpt = tb / 1024, ntiles = bytes / tb;
+      const int64_t xt = ntiles > xcd ? (ntiles - xcd + 7) / 8 : 0;
+      const int64_t nblk = xt * bpt;
+      const int64_t per = (nblk + xcount - 1) / xcount;
+      const int64_t b0 = (int64_t)xrank * per;
+      const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
+      // block b of the XCD's list is block b % bpt of tile xcd + 8 (b /
+      // bpt): one division for the wave's first block, then steps of NW
+      // blocks carried into the next tile
+      const int nb = b1 > b0 + w ? (int)((b1 - b0 - w + NW - 1) / NW) : 0;
+      if (nb > 0) {
+        const uint32_t ubpt = (uint32_t)bpt, b = (uint32_t)(b0 + w);
+        uint32_t bb = b % ubpt;
+        uint32_t off = (uint32_t)(xcd + 8 * (b / ubpt)) * (uint32_t)tb + bb * 1024u;
+        const uint32_t wrap = 8u * (uint32_t)tb - ubpt * 1024u;
+#pragma unroll 1
+        for (int q = 0; q < nb; ++q) {
+          load_lds16(rs, lds, off + (uint32_t)lane * 16u);
+          bb += NW;
+          off += NW * 1024u;
+          while (bb >= ubpt) {
+            bb -= ubpt;
+            off += wrap;
+          }
+        }
+      }
+    } else {
+      const int64_t nblk = (bytes + 1023) / 1024;
+      const int64_t per = (nblk + npw - 1) / npw;
+      const int64_t b0 = (int64_t)pw * per;
+      const int64_t b1 = b0 + per < nblk ? b0 + per : nblk;
+#pragma unroll 1
+      for (uint32_t off = (uint32_t)(b0 + w) * 1024u; off < (uint32_t)b1 * 1024u;
+           off += NW * 1024u)
+        load_lds16(rs, lds, off + (uint32_t)lane * 16u);
+    }
+  }
+  wait_vmcnt<0>();
+}
+
 }  // namespace fvx
