@@ -119,6 +119,7 @@ class ImageDesc(ctypes.Structure):
         ('filter', c_i32), ('round_u8', c_i32), ('swap_rb', c_i32),
         ('pre_div', c_f32),
         ('mean', c_f32 * 3), ('den', c_f32 * 3),
+        ('pad_per_channel', c_i32), ('pad_rgb', c_f32 * 3),
     ]
 
 

@@ -88,7 +88,8 @@ __global__ void resize_normalize_kernel(fvx_image_desc d) {
   float v[3];
   const int64_t ry = y - d.off_y, rx = x - d.off_x;
   if (ry < 0 || ry >= d.rh || rx < 0 || rx >= d.rw) {
-    v[0] = v[1] = v[2] = d.pad_value;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) v[c] = d.pad_per_channel ? d.pad_rgb[c] : d.pad_value;
   } else if (d.filter == FVX_RESIZE_PIL_BILINEAR) {
     PilTaps tx, ty;
     pil_taps((int)rx, (int)d.src_w, (int)d.rw, tx);

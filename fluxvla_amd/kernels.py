@@ -834,7 +834,8 @@ def resize_normalize(src, out, *, hwc, region=None, pad_value=0.0,
     model's [B, 3 * views, H, W] buffer).  ``src``: uint8 or fp32 [n, h, w, 3]
     (``hwc``) or [n, 3, h, w], contiguous per image.  ``region`` = (off_y,
     off_x, rh, rw): where the resized picture goes, pad_value elsewhere
-    (default: the whole output).  out = (v / pre_div - mean[c]) / den[c]."""
+    (default: the whole output; a 3-sequence pads each channel with its own
+    value).  out = (v / pre_div - mean[c]) / den[c]."""
     if src.dtype not in (torch.uint8, torch.float32):
         raise ValueError(f'src must be uint8 or fp32, got {src.dtype}')
     if src.dim() != 4 or (src.shape[3] if hwc else src.shape[1]) != 3:
@@ -858,7 +859,15 @@ def resize_normalize(src, out, *, hwc, region=None, pad_value=0.0,
     d.dst, d.dst_h, d.dst_w = out.data_ptr(), H, W
     d.dst_img_stride = out.stride(0) if n > 1 else 3 * H * W
     d.rh, d.rw, d.off_y, d.off_x = rh, rw, off_y, off_x
-    d.pad_value, d.filter = float(pad_value), int(filter)
+    if isinstance(pad_value, (tuple, list)):
+        if len(pad_value) != 3:
+            raise ValueError('a per-channel pad_value needs 3 values')
+        d.pad_per_channel = 1
+        for c in range(3):
+            d.pad_rgb[c] = float(pad_value[c])
+    else:
+        d.pad_value = float(pad_value)
+    d.filter = int(filter)
     d.round_u8, d.swap_rb, d.pre_div = int(round_u8), int(swap_rb), float(pre_div)
     for c in range(3):
         d.mean[c], d.den[c] = float(mean[c]), float(den[c])

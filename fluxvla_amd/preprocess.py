@@ -45,6 +45,10 @@ class ImagePreprocessor:
                  pad_value at pad_direction;
       'pil'      TransformImage 'resize-naive' / 'resize-crop': Pillow
                  BILINEAR (antialiased) to height x width;
+      'letterbox' TransformImage 'letterbox': Pillow BILINEAR keeping the
+                 aspect ratio (sides round(side / ratio), at least 1),
+                 pasted at pad_direction onto a canvas of the fill colour
+                 pad_value (one raw value per channel, or one for all);
       'none'     the frames already have the target size.
     Normalization per view v and channel c: (x / pre_div - mean[v][c]) /
     den[v][c] -- NormalizeImages: den = std + 1e-8 in fp32, pre_div 255
@@ -54,7 +58,7 @@ class ImagePreprocessor:
     def __init__(self, height=224, width=224, resize='linear', means=None,
                  stds=None, eps=1e-8, scale_to_unit_interval=False,
                  pad_value=0, pad_direction='center', swap_rb=False):
-        if resize not in ('linear', 'pad', 'pil', 'none'):
+        if resize not in ('linear', 'pad', 'pil', 'letterbox', 'none'):
             raise ValueError(f'unknown resize {resize!r}')
         if pad_direction not in PAD_POSITIONS:
             raise ValueError(f"Invalid pad_direction '{pad_direction}'")
@@ -87,14 +91,29 @@ class ImagePreprocessor:
                             scale_to_unit_interval=t.get(
                                 'scale_to_unit_interval', False))
             elif ty == 'TransformImage':
+                # transform_images.py:414-623
                 strategy = t.get('image_resize_strategy', 'letterbox')
-                if strategy not in ('resize-naive', 'resize-crop'):
-                    raise NotImplementedError(
-                        f'TransformImage strategy {strategy!r}')
+                if strategy not in ('resize-naive', 'resize-crop',
+                                    'letterbox'):
+                    raise ValueError(f"Image resize strategy '{strategy}' is "
+                                     'not supported!')
                 size = (t.get('input_sizes') or [(3, 224, 224)])[0]
+                if size[-1] != size[-2]:
+                    # the reference hands (H, W) to PIL as (width, height)
+                    raise NotImplementedError(
+                        'TransformImage with non-square input_sizes')
+                means = t.get('means') or [(0.5, 0.5, 0.5)]
                 args.update(height=size[-2], width=size[-1], resize='pil',
-                            means=t.get('means') or [(0.5, 0.5, 0.5)],
+                            means=means,
                             stds=t.get('stds') or [(0.5, 0.5, 0.5)], eps=0.0)
+                if strategy == 'letterbox':
+                    # one fill for all views, from the last view's means
+                    # when none is given (transform_images.py:495-498)
+                    fill = t.get('letterbox_fill') or [
+                        int(x * 255) for x in means[-1]]
+                    args.update(resize='letterbox', pad_value=tuple(fill),
+                                pad_direction=t.get('letterbox_pad_position')
+                                or 'center')
         return cls(**args)
 
     def _norm(self, v):
@@ -110,10 +129,13 @@ class ImagePreprocessor:
 
     def _region(self, h, w):
         H, W = self.height, self.width
-        if self.resize != 'pad':
+        if self.resize not in ('pad', 'letterbox'):
             return 0, 0, H, W
         ratio = max(w / W, h / H)
-        rh, rw = max(1, int(h / ratio)), max(1, int(w / ratio))
+        if self.resize == 'pad':      # transform_images.py:44-46
+            rh, rw = max(1, int(h / ratio)), max(1, int(w / ratio))
+        else:                         # :607-609, Python's round
+            rh, rw = max(1, round(h / ratio)), max(1, round(w / ratio))
         ph, pw = max(0, H - rh), max(0, W - rw)
         return (_pad_split(ph, self.pad_direction, 'top', 'bottom'),
                 _pad_split(pw, self.pad_direction, 'left', 'right'), rh, rw)
@@ -125,6 +147,7 @@ class ImagePreprocessor:
         if out is None:
             out = torch.empty(B, 3 * len(views), self.height, self.width,
                               dtype=torch.float32, device=views[0].device)
+        pil = self.resize in ('pil', 'letterbox')
         for v, img in enumerate(views):
             h, w = (img.shape[1], img.shape[2]) if hwc else img.shape[2:]
             if self.resize == 'none' and (h, w) != (self.height, self.width):
@@ -134,9 +157,8 @@ class ImagePreprocessor:
             K.resize_normalize(
                 img.contiguous(), out[:, 3 * v:3 * v + 3], hwc=hwc,
                 region=self._region(h, w), pad_value=self.pad_value,
-                filter=(RESIZE_PIL_BILINEAR if self.resize == 'pil'
-                        else RESIZE_LINEAR),
-                round_u8=img.dtype == torch.uint8 and self.resize != 'pil',
+                filter=(RESIZE_PIL_BILINEAR if pil else RESIZE_LINEAR),
+                round_u8=img.dtype == torch.uint8 and not pil,
                 swap_rb=self.swap_rb, mean=mean, den=den, pre_div=self.pre_div)
         return out
 

@@ -453,6 +453,11 @@ typedef struct fvx_image_desc {
   int32_t filter, round_u8, swap_rb;
   float pre_div;
   float mean[3], den[3];
+  /* pad_per_channel != 0: the pad is pad_rgb[c] for output channel c (a
+   * raw pixel value, normalized like the picture) instead of pad_value --
+   * TransformImage's letterbox fill colour. */
+  int32_t pad_per_channel;
+  float pad_rgb[3];
 } fvx_image_desc;
 
 int fvx_resize_normalize(const fvx_image_desc* desc, void* stream);

@@ -11,8 +11,9 @@ reduce to:
                        (cv2.resize INTER_LINEAR on uint8 HWC frames)
   ResizeImagesWithPad  transform_images.py:40-77, 147-189
   NormalizeImages      transform_images.py:313-390
-  TransformImage       transform_images.py:414-560, 'resize-naive'
-                       (PIL Image.resize BILINEAR, (x - mean) / std)
+  TransformImage       transform_images.py:414-623, 'resize-naive' and
+                       'letterbox' (PIL Image.resize BILINEAR, paste on a
+                       fill-colour canvas, (x - mean) / std)
   resize_with_pad      fluxvla/engines/utils/model_utils.py:98-120
                        (F.interpolate bilinear, F.pad left/top)
 
@@ -63,6 +64,30 @@ def transform_image_naive(img_hwc, size, mean, std):
     size x size, (x - mean) / std (float64 mean/std), CHW."""
     r = resize_pil_u8(img_hwc, size, size).astype(np.float32)
     out = (r - np.asarray(mean)) / np.asarray(std)
+    return out.transpose(2, 0, 1)
+
+
+def transform_image_letterbox(img_hwc, size, mean, std, fill,
+                              position='center'):
+    """TransformImage.apply_transform with 'letterbox' at a square size
+    (letterbox_pad_transform, transform_images.py:593-623): PIL BILINEAR to
+    round(side / ratio) (at least 1), pasted on an RGB canvas of ``fill``
+    (centred, or against the corner opposite ``position``'s padding), then
+    the resize to size x size (a copy) and (x - mean) / std, CHW."""
+    img = Image.fromarray(np.ascontiguousarray(img_hwc))
+    ratio = max(img.width / size, img.height / size)
+    new_w = max(1, round(img.width / ratio))
+    new_h = max(1, round(img.height / ratio))
+    img = img.resize((new_w, new_h), Image.Resampling.BILINEAR)
+    canvas = Image.new('RGB', (size, size), tuple(fill))
+    if position == 'center':
+        x0, y0 = (size - img.width) // 2, (size - img.height) // 2
+    else:
+        x0 = size - img.width if 'left' in position else 0
+        y0 = size - img.height if 'top' in position else 0
+    canvas.paste(img, (x0, y0))
+    r = np.array(canvas.resize((size, size), Image.Resampling.BILINEAR))
+    out = (r.astype(np.float32) - np.asarray(mean)) / np.asarray(std)
     return out.transpose(2, 0, 1)
 
 

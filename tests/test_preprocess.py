@@ -77,8 +77,21 @@ def test_from_transforms_reference_configs():
         input_sizes=[[3, 224, 224]] * 2, means=means[:2], stds=stds[:2])])
     assert ti.resize == 'pil' and ti._norm(0)[1] == tuple(
         np.float32(stds[0]).tolist())
+    # 'letterbox' (the reference's default strategy): fill from the means
+    # (int(x * 255)), centred unless letterbox_pad_position says otherwise
+    lb = P.ImagePreprocessor.from_transforms([dict(type='TransformImage')])
+    assert lb.resize == 'letterbox' and lb.pad_value == (127, 127, 127)
+    assert lb.pad_direction == 'center'
+    lb2 = P.ImagePreprocessor.from_transforms([dict(
+        type='TransformImage', letterbox_fill=[10, 20, 30],
+        letterbox_pad_position='top-left')])
+    assert lb2.pad_value == (10, 20, 30) and lb2.pad_direction == 'top-left'
+    with pytest.raises(ValueError, match='not supported'):
+        P.ImagePreprocessor.from_transforms([dict(
+            type='TransformImage', image_resize_strategy='squash')])
     with pytest.raises(NotImplementedError):
-        P.ImagePreprocessor.from_transforms([dict(type='TransformImage')])
+        P.ImagePreprocessor.from_transforms([dict(
+            type='TransformImage', input_sizes=[(3, 224, 256)])])
     pad = P.ImagePreprocessor.from_transforms([dict(
         type='ResizeImagesWithPad', height=224, width=224, pad_value=0,
         pad_direction='top-left')])
@@ -129,3 +142,34 @@ def test_normalize_and_pad_closed_forms():
     r = PO.resize_with_pad(t, 224, 224)
     assert r.shape == (1, 3, 224, 224)
     assert torch.all(r[:, :, :112] == -1) and torch.all(r[:, :, 112:] == 1)
+
+
+def test_letterbox_region_rounds_like_python():
+    """letterbox sides are round(side / ratio) (transform_images.py:607-609,
+    Python's round: half to even), where ResizeImagesWithPad truncates."""
+    lb = P.ImagePreprocessor(224, 224, resize='letterbox')
+    assert lb._region(480, 640) == (28, 0, 168, 224)
+    # 45 / (448 / 224) = 22.5 -> 22 (half to even); int() also gives 22,
+    # 47 / 2 = 23.5 -> 24 where int() gives 23
+    assert lb._region(45, 448)[2] == 22
+    assert lb._region(47, 448)[2] == 24
+    assert P.ImagePreprocessor(224, 224, resize='pad')._region(47, 448)[2] == 23
+    corner = P.ImagePreprocessor(224, 224, resize='letterbox',
+                                 pad_direction='top-left')
+    assert corner._region(47, 448) == (200, 0, 24, 224)
+
+
+def test_letterbox_oracle_closed_form():
+    """A constant frame letterboxed: the picture keeps its value, the rest is
+    the fill colour, placed per position; normalization (x - mean) / std in
+    0..255 units as the reference does."""
+    img = np.full((100, 200, 3), 90, np.uint8)
+    out = PO.transform_image_letterbox(img, 64, (0.5, 0.5, 0.5),
+                                       (0.5, 0.5, 0.5), (10, 20, 30))
+    raw = out * 0.5 + 0.5
+    assert np.allclose(raw[:, 16:48, :], 90)
+    assert np.allclose(raw[:, :16, :].reshape(3, -1).T, [10, 20, 30])
+    assert np.allclose(raw[:, 48:, :].reshape(3, -1).T, [10, 20, 30])
+    tl = PO.transform_image_letterbox(img, 64, (0, 0, 0), (1, 1, 1),
+                                      (1, 2, 3), 'top-left')
+    assert np.allclose(tl[:, 32:, :], 90) and np.allclose(tl[0, :32], 1)

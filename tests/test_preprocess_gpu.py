@@ -190,3 +190,34 @@ def test_prompt_padded_past_buffer_is_trimmed(P, cuda):
     with pytest.raises(ValueError):
         m.predict_action(*args, long_t.to(cuda), inp['states'].to(cuda),
                          lang_masks=long_m.to(cuda), noise=inp['noise'].to(cuda))
+
+
+@pytest.mark.parametrize('h,w,position', [(480, 640, 'center'),
+                                          (640, 480, 'top-left'),
+                                          (47, 448, 'bottom-right'),
+                                          (300, 250, 'top-right'),
+                                          (224, 224, 'center')])
+def test_letterbox_bit_exact(P, cuda, h, w, position):
+    """TransformImage 'letterbox' (the reference's default strategy): Pillow
+    resize keeping the aspect ratio, pasted on a per-channel fill colour,
+    then (x - mean) / std; every pixel equal to the Pillow restatement in
+    uint8, the normalized planes within 1e-5."""
+    announce(f'letterbox {h}x{w} {position}')
+    src = frames(7, 2, h, w)
+    means, stds = (0.5, 0.4, 0.3), (0.5, 0.6, 0.7)
+    pre = P.ImagePreprocessor.from_transforms([dict(
+        type='TransformImage', image_resize_strategy='letterbox',
+        input_sizes=[(3, 224, 224)], means=[means], stds=[stds],
+        letterbox_fill=[12, 200, 77], letterbox_pad_position=position)])
+    got = pre([src.to(cuda)]).cpu().numpy()
+    raw = P.ImagePreprocessor(224, 224, resize='letterbox',
+                              pad_value=(12, 200, 77),
+                              pad_direction=position)([src.to(cuda)]).cpu()
+    for i in range(2):
+        ref = PO.transform_image_letterbox(src[i].numpy(), 224, means, stds,
+                                           (12, 200, 77), position)
+        assert np.abs(got[i] - ref).max() <= 1e-5 * np.abs(ref).max(), i
+        ref_u8 = PO.transform_image_letterbox(src[i].numpy(), 224, (0, 0, 0),
+                                              (1, 1, 1), (12, 200, 77),
+                                              position)
+        assert np.array_equal(raw[i].numpy(), ref_u8), i
