@@ -456,18 +456,21 @@ __device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int z, int r,
   const int heads = (int)p.heads;
   const int tok = row_tok(r, heads, hs), h = r - tok * heads;
   const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
-  bf16_t* O = (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2;
-  bf16_t* dst = O + (int64_t)tok * p.o_tok_stride + (int64_t)h * p.o_head_stride + d0;
+  // o may be NULL on this path when o_frag is given (the row-major copy
+  // has no reader then)
+  bf16_t* dst = p.o ? (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2 + (int64_t)tok * p.o_tok_stride +
+                          (int64_t)h * p.o_head_stride + d0
+                    : nullptr;
   bf16_t* fdst = p.o_frag ? (bf16_t*)p.o_frag + frag_offset((int64_t)z * p.sq + tok,
                                                             h * 256 + d0)
                           : nullptr;
   if (NE == 8) {
     const bf16x8 b = pack8(v);
-    st8(dst, b);
+    if (dst) st8(dst, b);
     if (fdst) st8(fdst, b);
   } else {
     const uint2 b = {f2bf2(v[0], v[1]), f2bf2(v[2], v[3])};
-    *(uint2*)dst = b;
+    if (dst) *(uint2*)dst = b;
     if (fdst) *(uint2*)fdst = b;
   }
 }
@@ -545,6 +548,48 @@ __device__ __forceinline__ void dec_merge8_ns(const fvx_attn_desc& p, int n_rg, 
   dec_store<8>(p, z, r, d0, hs, acc);
 }
 
+// dec_merge8_ns for the in-launch merge (splits <= 16, partials of this
+// launch in this XCD's L2): the O rows' loads as above, the splits' row
+// references and sums from sML[split][8 rows] (staged in LDS by the merging
+// workgroup, one load per thread instead of two per split and thread).
+__device__ __forceinline__ void dec_merge8_staged(const fvx_attn_desc& p, int n_rg, int splits,
+                                                  int hs, int z, int r, int d0,
+                                                  const float2* sML) {
+  constexpr int NS = 16;
+  const int rg = r >> 6, i = r & 63, rl = r & 7;
+  const float* base = (const float*)p.workspace + (((int64_t)z * n_rg + rg) * splits) * kDecPF;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
+  bf16x8 a[NS];
+#pragma unroll
+  for (int u = 0; u < NS; ++u)
+    a[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                          rw, (uint32_t)(u * kDecPF * 4 + (i * 256 + d0) * 2), 0,
+                                          1));
+  float mv[NS], lv[NS], mn = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    const float2 ml = sML[u * 8 + rl];
+    mv[u] = u < splits ? ml.x : -INFINITY;
+    lv[u] = u < splits ? ml.y : 0.f;
+    mn = fmaxf(mn, mv[u]);
+  }
+  const float mr = (mn == -INFINITY) ? 0.f : mn;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, L = 0.f;
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    const float wb = __builtin_amdgcn_exp2f(mv[u] - mr);
+    float av[8];
+    unpack8(a[u], av);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(av[e], wb, acc[e]);
+    L = fmaf(lv[u], wb, L);
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] *= inv;
+  dec_store<8>(p, z, r, d0, hs, acc);
+}
+
 template <int AUX>
 __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int splits,
                                            int hs, int z, int r, int d0) {
@@ -569,7 +614,8 @@ __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int
 // and clears every counter before the next call relies on them.  The
 // group's last merging workgroup resets both of its counters.
 __device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, int hs,
-                             uint32_t* counters, int grp, int chunk, int polls) {
+                             uint32_t* counters, int grp, int chunk, int polls,
+                             unsigned char* smem) {
   const int tid = threadIdx.x;
   const int R = (int)(p.sq * p.heads);
   const int z = grp / n_rg, rg = grp % n_rg;
@@ -590,7 +636,21 @@ __device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, int h
                              __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  dec_merge8<1>(p, n_rg, splits, hs, z, r, d0);
+  // the splits' row references and sums of this workgroup's 8 rows: thread
+  // t < 16 splits loads value t & 1 (reference, sum) of row (t >> 1) & 7 of
+  // split t >> 4 into sML
+  float2* sML = (float2*)smem;
+  if (tid < 16 * splits) {
+    const int s = tid >> 4, rl = (tid >> 1) & 7, which = tid & 1;
+    const float* part = (const float*)p.workspace +
+                        (((int64_t)z * n_rg + rg) * splits + s) * kDecPF;
+    const float v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        make_rsrc(part, (uint32_t)(kDecPF * 4)),
+        (uint32_t)(kDecPO + 64 * which + 8 * chunk + rl) * 4, 0, 1));
+    ((float*)sML)[2 * (s * 8 + rl) + which] = v;
+  }
+  __syncthreads();
+  dec_merge8_staged(p, n_rg, splits, hs, z, r, d0, sML);
   if (tid == 0) {
     const int rows = R - rg * 64 < 64 ? R - rg * 64 : 64;
     const uint32_t old =
@@ -626,7 +686,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     const int j = slot - n_items / 8, grp = xcd + 8 * (j / 8);
     if (grp < n_groups && (grp % n_rg) * 64 + 8 * (j % 8) < (int)(p.sq * p.heads))
       dec_merge_wg(p, n_rg, splits, hs, counters, grp, j % 8,
-                   p.merge_no_wait ? 0 : kDecMergeSpin);
+                   p.merge_no_wait ? 0 : kDecMergeSpin, smem);
     return;
   }
   const int pf0 = counters ? merge_first : n_items;
@@ -1480,8 +1540,8 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
   clear_error();
   FVX_REQUIRE(dp, FVX_ERR_NULL, "attention: descriptor is NULL");
   const fvx_attn_desc& d = *dp;
-  FVX_REQUIRE(d.q && d.k && d.v && d.o, FVX_ERR_NULL,
-              "attention: q, k, v, o required");
+  FVX_REQUIRE(d.q && d.k && d.v && (d.o || d.o_frag), FVX_ERR_NULL,
+              "attention: q, k, v and o (or o_frag) required");
   FVX_REQUIRE(d.sq >= 0 && d.sk >= 0 && d.heads > 0 && d.n_problems >= 0 &&
                   d.zdiv > 0,
               FVX_ERR_SHAPE, "attention: bad sizes");
@@ -1546,7 +1606,7 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
     const int64_t R = d.sq * d.heads;
     const int groups = (int)(d.n_problems * a.n_rb);
     const int gpx = (groups + 7) / 8;  // groups per XCD
-    const bool fused = a.kps < kDecTKps && a.splits > 1 && R % 8 == 0 &&
+    const bool fused = a.kps < kDecTKps && a.splits > 1 && a.splits <= 16 && R % 8 == 0 &&
                        groups <= kAttnMaxGroups && gpx * (a.splits + 8) <= device_cus() / 8;
     const int item_blocks = fused ? 8 * gpx * a.splits : a.n_items;
     const int merge_blocks = fused ? 64 * gpx : 0;

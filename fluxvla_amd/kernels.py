@@ -699,7 +699,8 @@ def _set_prefetch(d, prefetch, prefetch_wgs, place=True):
 
 def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
                   v_transposed=False, o_frag=None, prefetch=None,
-                  prefetch_wgs=0, prefetch_place=True, merge_no_wait=False):
+                  prefetch_wgs=0, prefetch_place=True, merge_no_wait=False,
+                  o_row_major=True):
     """Batched multi-query attention.
 
     q: [B, Sq, H, D] (or [B, Sq, H*D]); k: [B, Sk, D] (row stride may exceed
@@ -707,7 +708,9 @@ def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
     cache [B, D, T >= Sk] (keys contiguous); o like q.  kgrp: int32 [B, Sk],
     qgrp: int32 [B, Sq] (visible iff kgrp[j] <= qgrp[i]).  ``o_frag`` (a
     FragA with k = H*D, decode path only) also receives the output in the
-    fragment-major layout, ready as the o-projection's A operand.
+    fragment-major layout, ready as the o-projection's A operand; with
+    ``o_row_major=False`` only that copy is written (``o`` then only gives
+    the shape).
     ``prefetch``: up to 8 tensors / prepared weights that idle workgroups
     of the decode kernel read into the caches meanwhile (the next GEMMs'
     weights; ``prefetch_wgs`` of them, 0 = fill the CUs; see
@@ -740,6 +743,10 @@ def mqa_attention(q, k, v, o, kgrp=None, qgrp=None, scale=None, kv_splits=0,
     if prefetch:
         _set_prefetch(d, prefetch, prefetch_wgs, prefetch_place)
     d.merge_no_wait = int(bool(merge_no_wait))
+    if not o_row_major:
+        if o_frag is None:
+            raise ValueError('o_row_major=False needs o_frag')
+        d.o = None
     run_attention(d)
     return o
 

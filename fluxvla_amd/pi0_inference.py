@@ -649,7 +649,8 @@ class PI0Inference:
         # next three GEMMs' weights into the memory-side cache meanwhile
         K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
                         kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True,
-                        o_frag=ctxf, prefetch=self._prefetch_list(i),
+                        o_frag=ctxf, o_row_major=False,
+                        prefetch=self._prefetch_list(i),
                         prefetch_place=self.prefetch_place)
         K.gemm(ctxf, Lf['o_w'], out=x, residual=x, c_frag=xf)
         K.gemm_geglu(xf, Lf['gate_w'], Lf['up_w'], out=b['ex_h'],
@@ -715,7 +716,8 @@ class PI0Inference:
                         a_scale=sa[:hid], bias_f32=fz['qkv'][step])
         K.mqa_attention(b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'],
                         kgrp=b['kgrp'], qgrp=b['qgrp_suf'], v_transposed=True,
-                        o_frag=ctxf, prefetch=self._prefetch_list(i),
+                        o_frag=ctxf, o_row_major=False,
+                        prefetch=self._prefetch_list(i),
                         prefetch_place=self.prefetch_place)
         K.gemm(ctxf, Lf['o_w'], out=x, residual=x,
                gate=sa[2 * hid:].view(1, hid), gate_group=Ss, c_frag=xf)

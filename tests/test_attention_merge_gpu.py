@@ -74,3 +74,24 @@ def test_wait_expiry_is_reported_and_cleared(K, cuda):
     again = _run(K, cuda, case)
     K.attention_check(cuda)
     assert torch.equal(again, clean)
+
+
+def test_fragment_only_output(K, cuda):
+    """o_row_major=False (the bs=1 expert, whose o-projection reads the
+    fragment-major copy): the fragment-major output equals the one written
+    next to the row-major output, and the row-major buffer is untouched."""
+    announce('attention fragment-only output')
+    q, k, vt, kgrp, qgrp = _expert_case(cuda, 4)
+    Ss, H, D = q.shape[1], q.shape[2], q.shape[3]
+    both_o = torch.empty_like(q)
+    f1 = K.FragA.empty(H * D, cuda).rows(Ss)
+    f1.buf.zero_()
+    K.mqa_attention(q, k, vt, both_o, kgrp, qgrp, v_transposed=True, o_frag=f1)
+    only_o = torch.full_like(q, 7.0)
+    f2 = K.FragA.empty(H * D, cuda).rows(Ss)
+    f2.buf.zero_()
+    K.mqa_attention(q, k, vt, only_o, kgrp, qgrp, v_transposed=True, o_frag=f2,
+                    o_row_major=False)
+    K.attention_check(cuda)
+    assert torch.equal(f1.buf, f2.buf)
+    assert bool((only_o == 7.0).all())
