@@ -269,6 +269,7 @@ class PI0Inference:
         # will read it (prefetch_place) or the memory-side cache
         self.prefetch = True
         self.prefetch_place = True
+        self.prefetch_kv = True
         # PI0.5 at bs=1: the adaptive RMSNorms run inside the next GEMM
         # (A scaled by 1 + scale as it is loaded, the shift as a bias, the
         # gate read from the style row by the residual epilogues)
@@ -664,8 +665,15 @@ class PI0Inference:
         is off."""
         if not self.prefetch:
             return None
-        Lf, Ln = self.exp_f[i], self.exp_f[(i + 1) % len(self.exp_f)]
-        return [Lf['o_w'], Lf['gate_w'], Lf['up_w'], Lf['down_w'], Ln['qkv_w']]
+        n = (i + 1) % len(self.exp_f)
+        Lf, Ln = self.exp_f[i], self.exp_f[n]
+        out = [Lf['o_w'], Lf['gate_w'], Lf['up_w'], Lf['down_w'], Ln['qkv_w']]
+        if self.prefetch_kv:
+            # the next layer's key / value cache (one sample at bs=1) into
+            # the memory-side cache
+            b = self._bufs[1]
+            out += [b['kc'][n], b['vc'][n]]
+        return out
 
     def _expert_layer_pi0(self, b, B, i, L):
         if self._frag_ok(B):
