@@ -9,8 +9,12 @@ One step = one whole chunk: input staging (copy_ into the static buffers)
 plus one HIP graph replay.
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel (prefix GeGLU GEMM, MFMA-bound) timed live
-                with HIP events on the stream it runs on;
+  roofline      the chunk's largest kernel by time (the bs=1 expert's decode
+                attention, latency-bound, judged against HBM) timed live with
+                HIP events on the stream it runs on, as in the chunk;
+  roofline_mfma the largest MFMA-bound kernel (prefix GeGLU GEMM) the same
+                way, weights cycled over the 17 layers, next to hipBLASLt
+                on a plain GEMM of the same flops;
   kernels       the same for every main kernel of the chunk (and the C1
                 RMSNorm+residual op), HBM-bound ones over distinct operand
                 sets so that they do not run from the memory-side cache;
@@ -69,39 +73,104 @@ def measured_traffic(row=None):
     return out if row is None else out.get(row)
 
 
-def time_dominant_kernel(model, iters=20):
-    """Prefix GeGLU GEMM (M=816, K=2048, N=16384 x 2 weights, rownorm with
-    the row sums handed over by the O projection, as in the chunk): the
-    largest single kernel of the chunk.  Times `iters` back-to-back launches
-    on the current stream with HIP events."""
+def _expert_attention_calls(model):
+    """The chunk's expert decode attention launches at bs=1, one per layer:
+    that layer's key / value cache, the chunk's prefetch list (the layer's
+    weights and the next layer's cache) and the fragment-major output only,
+    as _expert_layer_pi0_frag issues them."""
+    from fluxvla_amd import kernels as K
+    cfg = model.cfg
+    b = model._bufs[1]
+    S, Ss = cfg.prefix_len, cfg.suffix_len
+    ctxf = b['ex_ctxf'].rows(Ss)
+    calls = []
+    for i in range(len(model.exp_f)):
+        kc, vc = b['kc'][i], b['vc'][i]
+        calls.append(lambda i=i, kc=kc, vc=vc: K.mqa_attention(
+            b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'], kgrp=b['kgrp'],
+            qgrp=b['qgrp_suf'], v_transposed=True, o_frag=ctxf,
+            o_row_major=False, prefetch=model._prefetch_list(i),
+            prefetch_place=model.prefetch_place))
+    return calls
+
+
+def time_dominant_kernel(model, reps=20):
+    """The chunk's largest kernel by time (rocprofv3 kernel trace of the
+    chunk, profiles/pi0_bs1_chunk_kernel_stats.md): attn_decode_kernel, the
+    bs=1 expert's decode attention (408 query rows = 51 tokens x 8 heads
+    against 867 cached keys, 14 key ranges merged inside the launch, its
+    idle workgroups prefetching the next GEMMs' weights), 180 launches per
+    chunk.  Timed as in the chunk: the 18 layers' launches (each with its
+    layer's cache and prefetch list) in one HIP graph, replayed between HIP
+    events on the stream it runs on; the average per launch keeps the
+    graph's kernel boundary, as the trace's durations do.  It is latency
+    bound (timestamps inside the kernel: the query rows land ~3 us after the
+    start, one tile's softmax and P V take ~2.5 us, the merge ~3.5 us);
+    its roofline is HBM against its algorithmic bytes: the K and V rows of
+    the 867 visible keys and Q and O (408 x 256 bf16 each), 1.31 MB."""
+    cfg = model.cfg
+    calls = _expert_attention_calls(model)
+    us = _launch_time_us(calls, reps, min_calls=len(calls))
+    T = cfg.prefix_len + cfg.suffix_len
+    R = cfg.suffix_len * cfg.heads
+    nbytes = 2 * T * cfg.head_dim * 2 + 2 * R * cfg.head_dim * 2
+    achieved = nbytes / (us * 1e-6) / 1e9
+    return {
+        'kernel': 'attn_decode_kernel (expert decode attention + in-launch '
+                  f'merge + weight prefetch, {R} query rows x {T} keys, '
+                  'hd 256, 14 key ranges)',
+        'bound': 'hbm',
+        'achieved': round(achieved, 1),
+        'peak': PEAK_HBM_GBS,
+        'unit': 'GB/s',
+        'frac': round(achieved / PEAK_HBM_GBS, 4),
+        'traffic': measured_traffic('attn_decode_kernel + merge (expert)'),
+        'traffic_unit': 'bytes/launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, '
+                        'profiles/pi0_bs1_kernel_table_traffic.md; the '
+                        'table row runs without the weight prefetch)',
+        'avg_us': round(us, 2),
+        'bytes_per_launch': nbytes,
+        'launches_per_chunk': cfg.exp_layers * cfg.num_steps,
+    }
+
+
+def time_mfma_kernel(model, reps=10):
+    """The chunk's largest MFMA-bound kernel: the prefix GeGLU GEMM
+    (gemm_wide_kernel<GEGLU>, M=816, K=2048, N=16384 x 2 weights, rownorm
+    with the row sums handed over by the O projection), 17 launches per
+    chunk.  Timed as in the chunk: one launch per prefix layer with that
+    layer's weights (17 x 134 MB, so each launch reads its weights from
+    HBM), in a HIP graph replayed between HIP events.  ``library_us``: the
+    vendor library (hipBLASLt through torch.matmul) on a plain GEMM of the
+    same flops (x @ [Wg; Wu]^T, no epilogue), timed the same way."""
     import torch
 
     from fluxvla_amd import kernels as K
     cfg = model.cfg
     b = model._bufs[1]
-    L = model.llm['layers'][0]
     x = b['pre_x'].view(-1, cfg.llm_hidden)
     h = b['pre_h']
     ss = b['pre_ss'][0]
-    for _ in range(3):
-        K.gemm_geglu(x, L['gate_w'], L['up_w'], out=h, rownorm_eps=cfg.rms_eps,
-                     ss_in=ss)
-    s = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
-        enable_timing=True)
-    e0.record(s)
-    for _ in range(iters):
-        K.gemm_geglu(x, L['gate_w'], L['up_w'], out=h, rownorm_eps=cfg.rms_eps,
-                     ss_in=ss)
-    e1.record(s)
-    e1.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / iters
-    M, N, Kd = x.shape[0], L['gate_w'].shape[0], x.shape[1]
+    layers = model.llm['layers'][:cfg.llm_layers - 1]
+    calls = [lambda L=L: K.gemm_geglu(x, L['gate_w'], L['up_w'], out=h,
+                                      rownorm_eps=cfg.rms_eps, ss_in=ss)
+             for L in layers]
+    us = _launch_time_us(calls, reps, min_calls=len(calls))
+    M, N, Kd = x.shape[0], layers[0]['gate_w'].shape[0], x.shape[1]
     flops = 2.0 * M * N * Kd * 2
     achieved = flops / (us * 1e-6) / 1e12
+    # the library on the same flops: [816, 2048] x [2048, 32768], 4 weight
+    # sets (537 MB) cycled so that it also reads its weights from HBM
+    g = torch.Generator(device=x.device).manual_seed(5)
+    ws = [(torch.randn(2 * N, Kd, device=x.device, generator=g) * 0.02).bfloat16()
+          for _ in range(4)]
+    out = torch.empty(M, 2 * N, device=x.device, dtype=torch.bfloat16)
+    lib_us = _launch_time_us([lambda w=w: torch.matmul(x, w.t(), out=out)
+                              for w in ws], reps, min_calls=8)
+    del ws
     return {
         'kernel': 'gemm_wide_kernel<GEGLU> (prefix gate/up, '
-                  f'M={M} N={N}x2 K={Kd})',
+                  f'M={M} N={N}x2 K={Kd}, 17 layers\' weights cycled)',
         'bound': 'mfma',
         'achieved': round(achieved, 2),
         'peak': PEAK_BF16_TFLOPS,
@@ -112,6 +181,9 @@ def time_dominant_kernel(model, iters=20):
                         'profiles/pi0_bs1_kernel_table_traffic.md)',
         'avg_us': round(us, 2),
         'flops_per_launch': flops,
+        'library_us': round(lib_us, 2),
+        'library': 'hipBLASLt (torch.matmul), plain GEMM of the same flops, '
+                   'no epilogue',
     }
 
 
@@ -199,7 +271,16 @@ def kernel_table(model):
     rows.append(_row('rms_norm_residual_kernel (C1, cache-resident)',
                      '[1024, 2048]', 'hbm', nbytes,
                      _launch_time_us(calls[:1], 20, min_calls=32)))
-    del sets, calls
+    # the floor for these bytes: a plain row copy kernel (fvx_copy_rows)
+    # reading and writing the same 16.8 MB, over 32 operand sets
+    big = [(torch.empty(2048, 2048, dtype=torch.bfloat16, device=dev),
+            torch.empty(2048, 2048, dtype=torch.bfloat16, device=dev))
+           for _ in range(32)]
+    one = _launch_time_us([lambda t=t: K.copy_rows(t[0], t[1]) for t in big],
+                          10)
+    rows.append(_row('copy_rows_kernel, same bytes (C1 floor: an 8.4 MB -> '
+                     '8.4 MB copy)', '[2048, 2048] bf16', 'hbm', nbytes, one))
+    del sets, calls, big
 
     # action expert at bs=1, fragment-major operands as in the chunk
     b = model._bufs[1]
@@ -218,7 +299,8 @@ def kernel_table(model):
             row_group=Ss, row_group_stride=T, v_ld=T))
         att.append(lambda kc=kc, vc=vc: K.mqa_attention(
             b['ex_q'], kc[:, :S + Ss], vc, b['ex_ctx'], kgrp=b['kgrp'],
-            qgrp=b['qgrp_suf'], v_transposed=True, o_frag=ctxf))
+            qgrp=b['qgrp_suf'], v_transposed=True, o_frag=ctxf,
+            o_row_major=False))
         oc.append(lambda Lf=Lf: K.gemm(ctxf, Lf['o_w'], out=x, residual=x,
                                        c_frag=xf))
         ggl.append(lambda Lf=Lf: K.gemm_geglu(xf, Lf['gate_w'], Lf['up_w'],
@@ -244,8 +326,9 @@ def kernel_table(model):
                      f'{Ss * H} query rows x {T_keys} keys', 'hbm', work,
                      _launch_time_us(att, 5)))
 
-    # prefix (M = 816) and SigLIP (M = 768) GEMMs, prefill attention: MFMA
-    L = model.llm['layers'][0]
+    # prefix (M = 816) and SigLIP (M = 768) GEMMs, prefill attention: MFMA;
+    # each row cycles the layers' weights (17 prefix layers, 27 SigLIP
+    # layers), as the chunk reads them: one launch per layer, from HBM
     px = b['pre_x'].view(-1, cfg.llm_hidden)
     M = px.shape[0]
     kc0, vc0 = b['kc'][0], b['vc'][0]
@@ -253,47 +336,51 @@ def kernel_table(model):
     # to the next fused RMSNorm
     ss_a, ss_b = b['pre_ss'][0], b['pre_ss'][1]
     pre = [
-        ('gemm_tile_kernel<64,128,QKV_ROPE> (prefix)', lambda: K.gemm_qkv_rope(
+        ('gemm_tile_kernel<64,128,QKV_ROPE> (prefix)', lambda L: K.gemm_qkv_rope(
             px, L['qkv_w'], model.rope, b['pos_pre'], b['pre_q'].view(M, -1),
             kc0.view(T, D), vc0, H, D, rownorm_eps=cfg.rms_eps, row_group=S,
             row_group_stride=T, v_ld=T, ss_in=ss_b), 2 * M * nq * cfg.llm_hidden),
-        ('gemm_tile_kernel<64,128,PLAIN> o-proj (prefix)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> o-proj (prefix)', lambda L: K.gemm(
             b['pre_ctx'].view(M, -1), L['o_w'], out=b['pre_h'][:, :cfg.llm_hidden],
             residual=px, ss_out=ss_a), 2 * M * cfg.llm_hidden * H * D),
-        ('gemm_wide_kernel<GEGLU> (prefix)', lambda: K.gemm_geglu(
+        ('gemm_wide_kernel<GEGLU> (prefix)', lambda L: K.gemm_geglu(
             px, L['gate_w'], L['up_w'], out=b['pre_h'], rownorm_eps=cfg.rms_eps,
             ss_in=ss_a), 4 * M * cfg.llm_mlp * cfg.llm_hidden),
-        ('gemm_wide_kernel<PLAIN> 8 K ranges + split-K reduce, down (prefix)', lambda: K.gemm(
+        ('gemm_wide_kernel<PLAIN> 8 K ranges + split-K reduce, down (prefix)', lambda L: K.gemm(
             b['pre_h'], L['down_w'], out=b['pre_q'].view(M, -1)[:, :cfg.llm_hidden],
             residual=px, ss_out=ss_b), 2 * M * cfg.llm_hidden * cfg.llm_mlp),
-        ('attn_decode_t_kernel + merge (prefix)', lambda: K.mqa_attention(
+        ('attn_decode_t_kernel + merge (prefix)', lambda L: K.mqa_attention(
             b['pre_q'], kc0[:, :S], vc0, b['pre_ctx'], kgrp=b['kgrp'][:, :S],
             qgrp=b['qgrp_pre'], v_transposed=True), 4 * H * S * S * D),
     ]
-    V = model.vis['layers'][0]
+    pre = [(n, f, fl, model.llm['layers'][:cfg.llm_layers - 1])
+           for n, f, fl in pre]
     vx, vxn = b['vis_x'], b['vis_xn']
     Mv, vh = vx.shape
     nimg = Mv // cfg.num_patches
-    pre += [
-        ('gemm_tile_kernel<64,128,PLAIN> qkv+bias (SigLIP)', lambda: K.gemm(
+    vis = [
+        ('gemm_tile_kernel<64,128,PLAIN> qkv+bias (SigLIP)', lambda V: K.gemm(
             vxn, V['qkv_w'], out=b['vis_qkv'], bias=V['qkv_b']),
          2 * Mv * 3 * vh * vh),
         ('gemm_tile_kernel<64,64,PLAIN> o-proj+bias+res (SigLIP)',
-         lambda: K.gemm(b['vis_ctx'], V['o_w'], out=vxn, bias=V['o_b'],
+         lambda V: K.gemm(b['vis_ctx'], V['o_w'], out=vxn, bias=V['o_b'],
                         residual=vx), 2 * Mv * vh * vh),
-        ('gemm_tile_kernel<64,128,PLAIN> fc1+bias+gelu (SigLIP)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,128,PLAIN> fc1+bias+gelu (SigLIP)', lambda V: K.gemm(
             vxn, V['fc1_w'], out=b['vis_h'], bias=V['fc1_b'], act=2),
          2 * Mv * cfg.vit_mlp * vh),
-        ('gemm_tile_kernel<64,64,PLAIN> fc2+bias+res (SigLIP)', lambda: K.gemm(
+        ('gemm_tile_kernel<64,64,PLAIN> fc2+bias+res (SigLIP)', lambda V: K.gemm(
             b['vis_h'], V['fc2_w'], out=vxn, bias=V['fc2_b'], residual=vx),
          2 * Mv * vh * cfg.vit_mlp),
-        ('attn_kernel<96,80> (SigLIP)', lambda: K.mha_packed_qkv(
+        ('attn_kernel<96,80> (SigLIP)', lambda V: K.mha_packed_qkv(
             b['vis_qkv'], b['vis_ctx'], nimg, cfg.num_patches, cfg.vit_heads,
             cfg.vit_head_dim),
          4 * nimg * cfg.vit_heads * cfg.num_patches ** 2 * cfg.vit_head_dim),
     ]
-    for name, fn, flops in pre:
-        rows.append(_row(name, '', 'mfma', flops, _launch_time_us([fn], 10)))
+    pre += [(n, f, fl, model.vis['layers']) for n, f, fl in vis]
+    for name, fn, flops, layers in pre:
+        calls = [lambda L=L, fn=fn: fn(L) for L in layers]
+        rows.append(_row(name, '', 'mfma', flops,
+                         _launch_time_us(calls, 5, min_calls=len(calls))))
     return rows
 
 
@@ -752,8 +839,11 @@ def main():
     log(f'{ms:.3f} ms/chunk (wall), median event {per[len(per) // 2]:.3f} ms')
 
     roof = time_dominant_kernel(model) if B == 1 else None
+    roof_mfma = time_mfma_kernel(model) if B == 1 else None
     if roof:
-        log(f"dominant kernel {roof['avg_us']} us, {roof['achieved']} TFLOP/s")
+        log(f"dominant kernel {roof['avg_us']} us, {roof['achieved']} GB/s; "
+            f"MFMA kernel {roof_mfma['avg_us']} us, {roof_mfma['achieved']} "
+            f"TFLOP/s (library {roof_mfma['library_us']} us)")
 
     table, phases = None, None
     if B == 1 and not args.no_table:
@@ -812,6 +902,7 @@ def main():
             'median_event_ms': round(per[len(per) // 2], 3),
         },
         'roofline': roof,
+        'roofline_mfma': roof_mfma,
         'kernels': table,
         'phases': phases,
         'cpu_baseline': cpu,
