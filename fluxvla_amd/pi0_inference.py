@@ -347,11 +347,15 @@ class PI0Inference:
             mo = prepare_projector(sd, 'action_time_mlp_out', dev)
             # cat([action_emb, time_emb]) @ W^T = action_emb @ Wa^T +
             # time_emb @ Wt^T: the time half is a per-step fp32 bias.
-            self.mlp_in_a = mi['w'][:, :w].contiguous()
             wt = mi['w'][:, w:].contiguous()
             bias = K.gemm(temb, wt, bias=mi['b'], out_f32=True)
-            self.step_bias = bias[:-1].contiguous()
-            self.step_bias0 = bias[-1].contiguous()
+            # action_in_proj folded in: (x Wi^T + bi) Wa^T = x (Wa Wi)^T +
+            # Wa bi, one K = max_action_dim GEMM per step instead of two
+            wa = mi['w'][:, :w].float()
+            self.mlp_in_x = (wa @ self.act_in['w'].float()).to(BF16)
+            fold_b = wa @ self.act_in['b'].float()
+            self.step_bias = (bias[:-1] + fold_b).contiguous()
+            self.step_bias0 = (bias[-1] + fold_b).contiguous()
             self.mlp_out = mo
         self.rope = K.rope_table(cfg.prefix_len + cfg.suffix_len + 8,
                                  cfg.head_dim, cfg.rope_theta, device=dev)
@@ -395,8 +399,7 @@ class PI0Inference:
         if self.cfg.pi05:
             self.act_in_f = F(self.act_in['w'])
         else:
-            self.act_in_f = F(self.act_in['w'])
-            self.mlp_in_a_f = F(self.mlp_in_a)
+            self.mlp_in_x_f = F(self.mlp_in_x)
             self.mlp_out_f = F(self.mlp_out['w'])
 
     # -- the reference's module attributes with their prepare_triton hooks
@@ -530,10 +533,7 @@ class PI0Inference:
             'ex_xf': K.FragA.empty(cfg.exp_hidden, dev),
             'ex_ctxf': K.FragA.empty(cfg.heads * D, dev),
             'ex_hf': K.FragA.empty(cfg.exp_mlp, dev),
-            'act_h1': e(B * cfg.n_action_steps, cfg.proj_width),
-            'act_h2': e(B * cfg.n_action_steps, cfg.proj_width),
             'states': e(B, cfg.state_dim),
-            'state_emb': e(B, cfg.proj_width),
             'xt': e(B, cfg.n_action_steps, cfg.max_action_dim,
                     dt=torch.float32),
             'xt_bf16': e(B, cfg.n_action_steps, cfg.max_action_dim),
@@ -545,6 +545,15 @@ class PI0Inference:
             'rtc_cw': e(len(self.times), cfg.n_action_steps,
                         dt=torch.float32),
         }
+        if not cfg.pi05:
+            # PI0 suffix stream = [state_emb, mlp_out(silu(mlp_in(...)))]:
+            # the hidden rows of the action-time MLP sit at the suffix rows
+            # (the state row of each sample stays zero), and the mlp_out
+            # GEMM adds a constant residual that holds the state embedding
+            # in the state row and mlp_out's bias in the action rows
+            b['suf_h'] = e(B * Ss, cfg.proj_width)
+            b['suf_res'] = (self.mlp_out['b'][None]
+                            .expand(B * Ss, cfg.exp_hidden).contiguous())
         self._bufs[B] = b
         return b
 
@@ -781,12 +790,15 @@ class PI0Inference:
         x3 = b['ex_x']
         xt_b = b['xt_bf16'].view(B * na, -1)
         fr = self._frag_ok(B)
-        w_in = self.act_in_f if fr else self.act_in['w']
-        if not cfg.pi05:
-            K.gemm(b['states'], self.state['w'], out=b['state_emb'],
-                   bias=self.state['b'])
-            w_mi = self.mlp_in_a_f if fr else self.mlp_in_a
+        if cfg.pi05:
+            w_in = self.act_in_f if fr else self.act_in['w']
+        else:
+            # the state row of each sample's constant mlp_out residual
+            K.gemm(b['states'], self.state['w'], out=b['suf_res'],
+                   bias=self.state['b'], row_group=1, row_group_stride=Ss)
+            w_mi = self.mlp_in_x_f if fr else self.mlp_in_x
             w_mo = self.mlp_out_f if fr else self.mlp_out['w']
+            h = b['suf_h']  # row 0 of each sample (the state row) stays 0
         fused = self._fold_ok(B, rtc)
         for step in range(len(self.times)):
             if cfg.pi05:
@@ -794,20 +806,15 @@ class PI0Inference:
                        bias=self.act_in['b'],
                        c_frag=b['ex_xf'].rows(Ss) if fused else None)
             else:
-                K.gemm(xt_b, w_in, out=b['act_h1'], bias=self.act_in['b'])
                 # prefix RTC: locked positions take the time-0 embedding
                 lk = ({'rtc_lock': b['rtc_lock'], 'rtc_period': na,
                        'bias_f32_locked': self.step_bias0}
                       if rtc == 'prefix' else {})
-                K.gemm(b['act_h1'], w_mi, out=b['act_h2'],
-                       bias_f32=self.step_bias[step], act=ACT_SILU, **lk)
-                K.gemm(b['act_h2'], w_mo,
-                       out=x3.view(B * Ss, hid)[1:], bias=self.mlp_out['b'],
-                       row_group=na, row_group_stride=Ss)
-                K.copy_rows(b['state_emb'], x3.view(B * Ss, hid),
-                            row_group=1, dst_group_stride=Ss)
-                if fr:
-                    K.pack_frag(x3.view(Ss, hid), b['ex_xf'].rows(Ss))
+                K.gemm(xt_b, w_mi, out=h[1:], bias_f32=self.step_bias[step],
+                       act=ACT_SILU, row_group=na, row_group_stride=Ss, **lk)
+                K.gemm(h, w_mo, out=x3.view(B * Ss, hid),
+                       residual=b['suf_res'],
+                       c_frag=b['ex_xf'].rows(Ss) if fr else None)
             for i, L in enumerate(self.exp['layers']):
                 if fused:
                     self._expert_layer_pi05_fused(b, i, step)
