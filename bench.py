@@ -465,6 +465,294 @@ def table_only():
     print(json.dumps({'kernels': rows}), flush=True)
 
 
+# ---------------------------------------------------------------------------
+# rocprofv3 summaries: profiles/*.md from the CSVs of four profiler passes
+# ---------------------------------------------------------------------------
+# (output directory, -o prefix, profiler options, bench.py options)
+PROFILE_PASSES = (
+    ('ptab_kt', 'kt', '--kernel-trace --stats', '--table-only'),
+    ('ptab_fetch', 'fetch', '--pmc FETCH_SIZE', '--table-only'),
+    ('ptab_write', 'write', '--pmc WRITE_SIZE', '--table-only'),
+    ('pbench', 'bench', '--kernel-trace --stats', ''),
+)
+
+
+def profile_commands(out='$R/gpurun_out'):
+    """The profiler commands whose CSVs summarize_profiles reads (repo root
+    ``R``; TMPDIR=/tmp), one line each."""
+    cmds = []
+    for d, o, opts, args in PROFILE_PASSES:
+        cmds.append(f'rocprofv3 {opts} --output-format csv -d {out}/{d} -o {o} '
+                    f'-- python3 $R/bench.py{" " + args if args else ""}'
+                    f' > {out}/{d}.log 2>&1')
+    return cmds
+
+
+def _trace(path):
+    """Kernel-trace CSV rows in start order with name, workgroups, us."""
+    import csv
+    rows = sorted(csv.DictReader(open(path)),
+                  key=lambda r: int(r['Start_Timestamp']))
+    for r in rows:
+        r['name'] = r['Kernel_Name'].replace('void ', '').split('(')[0]
+        wg = 1
+        for ax in 'XYZ':
+            wg *= max(1, int(r.get(f'Grid_Size_{ax}', 1)) //
+                      max(1, int(r.get(f'Workgroup_Size_{ax}', 1))))
+        r['wgs'] = wg
+        r['us'] = (int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3
+    return rows
+
+
+def _counters(path):
+    """Counter-collection CSV rows in dispatch order: (name, wgs, KiB)."""
+    import csv
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r['Dispatch_Id']))
+    return [(r['Kernel_Name'].replace('void ', '').split('(')[0],
+             int(r['Grid_Size']) // max(1, int(r['Workgroup_Size'])),
+             float(r['Counter_Value'])) for r in rows]
+
+
+def _after_last(seq, name_of, sub):
+    """The entries after the last one whose name contains ``sub``."""
+    idx = [i for i, x in enumerate(seq) if sub in name_of(x)]
+    return seq[idx[-1] + 1:] if idx else seq
+
+
+def _json_line(path):
+    line = None
+    for s in open(path):
+        if s.startswith('{'):
+            line = s
+    return json.loads(line) if line else None
+
+
+# the per-kernel table's rows as dispatched by kernel_table (in order):
+# (row, [(kernel-name substring, workgroups, dispatches), ...]); dispatches =
+# one eager call + 3 warm-up + the timed graph replays, per operand set
+_E, _MP, _MV = 18 * 9, 17 * 9, 27 * 9
+TABLE_DISPATCHES = (
+    ('rms_norm_residual_kernel (C1)', [('rms_norm_residual_kernel', 256, 32 * 14)]),
+    ('rms_norm_residual_kernel (C1, cache-resident)',
+     [('rms_norm_residual_kernel', 256, 32 * 24)]),
+    ('copy_rows_kernel, same bytes (C1 floor: an 8.4 MB -> 8.4 MB copy)',
+     [('copy_rows_kernel', 2048, 32 * 14)]),
+    ('gemm_skinny_kernel<QKV_ROPE> (expert)', [('gemm_skinny_kernel<2', 160, _E)]),
+    ('gemm_skinny_kernel<PLAIN> o-proj (expert)', [('gemm_skinny_kernel<0', 256, _E)]),
+    ('gemm_skinny_kernel<GEGLU> (expert)', [('gemm_skinny_kernel<1', 256, _E)]),
+    ('gemm_skinny_kernel<PLAIN> down (expert)', [('gemm_skinny_kernel<0', 256, _E)]),
+    ('attn_decode_kernel + merge (expert)', [('attn_decode_kernel', 176, _E)]),
+    ('gemm_tile_kernel<64,128,QKV_ROPE> (prefix)',
+     [('gemm_tile_kernel<64, 128, 2, 2, 3, 2', 260, _MP)]),
+    ('gemm_tile_kernel<64,128,PLAIN> o-proj (prefix)',
+     [('gemm_tile_kernel<64, 128, 2, 2, 4, 0', 208, _MP)]),
+    ('gemm_wide_kernel<GEGLU> (prefix)', [('gemm_wide_kernel<1', 512, _MP)]),
+    ('gemm_wide_kernel<PLAIN> 8 K ranges + split-K reduce, down (prefix)',
+     [('gemm_wide_kernel<0', 256, _MP), ('gemm_partial_reduce_kernel<0', 816, _MP)]),
+    ('attn_decode_t_kernel + merge (prefix)',
+     [('attn_decode_t_kernel', 204, _MP), ('attn_decode_merge_kernel', 816, _MP)]),
+    ('gemm_tile_kernel<64,128,PLAIN> qkv+bias (SigLIP)',
+     [('gemm_tile_kernel<64, 128, 2, 2, 3, 0', 324, _MV)]),
+    ('gemm_tile_kernel<64,64,PLAIN> o-proj+bias+res (SigLIP)',
+     [('gemm_tile_kernel<64, 64, 2, 2, 4, 0', 216, _MV)]),
+    ('gemm_tile_kernel<64,128,PLAIN> fc1+bias+gelu (SigLIP)',
+     [('gemm_tile_kernel<64, 128, 2, 2, 3, 0', 408, _MV)]),
+    ('gemm_tile_kernel<64,64,PLAIN> fc2+bias+res (SigLIP)',
+     [('gemm_tile_kernel<64, 64, 2, 2, 4, 0', 216, _MV)]),
+    ('attn_kernel<96,80> (SigLIP)', [('attn_kernel<96, 80>', 192, _MV)]),
+)
+
+
+def _runs(rows, sub, min_len):
+    """Maximal runs of >= min_len consecutive dispatches of one kernel."""
+    runs, cur = [], []
+    for r in rows + [None]:
+        if r is not None and sub in r['name']:
+            cur.append(r)
+            continue
+        if len(cur) >= min_len:
+            runs.append(cur)
+        cur = []
+    return runs
+
+
+def _run_line(run):
+    import statistics
+    d = [r['us'] for r in run]
+    span = (int(run[-1]['End_Timestamp']) -
+            int(run[0]['Start_Timestamp'])) / 1e3 / len(run)
+    return (f'{len(run)} dispatches: mean {statistics.mean(d):.2f} us, median '
+            f'{statistics.median(d):.2f}, min {min(d):.2f}, max {max(d):.2f}, '
+            f'span/launch {span:.2f} us')
+
+
+def summarize_profiles(gdir, outdir):
+    """Write profiles/pi0_bs1_kernel_table_traffic.md,
+    pi0_bs1_chunk_kernel_stats.md and pi0_bs1_dominant_kernel_trace.md
+    into ``outdir`` from the CSVs the PROFILE_PASSES commands left under
+    ``gdir`` (and the JSON lines those runs printed to their logs)."""
+    import statistics
+    os.makedirs(outdir, exist_ok=True)
+    cmds = '\n'.join('    ' + c for c in profile_commands())
+    # ---- per-kernel table: durations and calibrated traffic ----
+    name0 = lambda x: x[0]  # noqa: E731
+    kt = [(r['name'], r['wgs'], r['us'])
+          for r in _trace(f'{gdir}/ptab_kt/kt_kernel_trace.csv')]
+    # the table's dispatches follow the chunk run first (its last Euler GEMM)
+    kt = _after_last(kt, name0, 'gemm_skinny_kernel<3')
+    fe = _after_last(_counters(f'{gdir}/ptab_fetch/fetch_counter_collection.csv'),
+                     name0, 'gemm_skinny_kernel<3')
+    wr = _after_last(_counters(f'{gdir}/ptab_write/write_counter_collection.csv'),
+                     name0, 'gemm_skinny_kernel<3')
+    # calibration: the three 256 MiB copies at the end of the program
+    cf = statistics.median([v for n, w, v in fe if 'copyBuffer' in n][-3:])
+    cw = statistics.median([v for n, w, v in wr if 'copyBuffer' in n][-3:])
+    sf, sw = 262144 / cf, 262144 / cw
+    bench_rows = {r['kernel']: r for r in
+                  (_json_line(f'{gdir}/ptab_kt.log') or {}).get('kernels', [])}
+    used = {}
+
+    def take(seq, tag, sub, wg, cnt):
+        idx = [i for i, x in enumerate(seq) if sub in x[0] and x[1] == wg]
+        start = used.get((tag, sub, wg), 0)
+        used[(tag, sub, wg)] = start + cnt
+        return [seq[i][2] for i in idx[start:start + cnt]]
+    lines = []
+    for row, parts in TABLE_DISPATCHES:
+        tt = tf = tw = 0.0
+        descr, nmin = [], None
+        for sub, wg, cnt in parts:
+            t = take(kt, 'kt', sub, wg, cnt)
+            f = take(fe, 'fe', sub, wg, cnt)
+            w = take(wr, 'wr', sub, wg, cnt)
+            if not (t and f and w):
+                continue
+            tt += statistics.median(t)
+            tf += statistics.median(f) * sf * 1024 / 1e6
+            tw += statistics.median(w) * sw * 1024 / 1e6
+            base = sub.split('<')[0]
+            descr.append(f'`{base}{"<..>" if "<" in sub else ""}` ({wg})')
+            nmin = len(t) if nmin is None else min(nmin, len(t))
+        b = bench_rows.get(row)
+        ratio = (f'{(tf + tw) * 1e6 / b["work"]:.2f}'
+                 if b and b['bound'] == 'hbm' else '')
+        lines.append(f'| {row} | {" + ".join(descr)} | {nmin} | {tt:.2f} | '
+                     f'{tf:.2f} | {tw:.2f} | {ratio} |')
+    with open(f'{outdir}/pi0_bs1_kernel_table_traffic.md', 'w') as fh:
+        fh.write(f"""# PI0 bs=1 per-kernel table -- rocprofv3 durations and HBM traffic
+
+Every row of bench.py's per-kernel table (each main kernel of the chunk at
+its chunk shape; every row cycles the layers' operands, as the chunk reads
+them), with its rocprofv3 kernel duration and its calibrated FETCH_SIZE /
+WRITE_SIZE bytes per dispatch.
+
+Commands (repo root `R` on the MI355X box, `export TMPDIR=/tmp`; the first
+three passes run the same program, one counter block each; this file is
+`python3 bench.py --summarize-profiles gpurun_out` over their CSVs):
+
+{cmds}
+
+`bench.py --table-only` runs one chunk, then the table, then three copies of
+256 MiB.  Calibration (a device copy fetches and writes exactly its size):
+the copy reads FETCH {cf:.0f} KiB and WRITE {cw:.0f} KiB per dispatch, so
+FETCH is scaled by {sf:.3f} and WRITE by {sw:.3f}.  The rows are the
+table's own dispatches (those after the chunk), matched to the table rows
+in order; durations are the kernel-trace pass's median per row (the counter
+passes serialize dispatches, so their durations are not used); bytes are
+the counter medians times the calibration factors.  "traffic /
+algorithmic" = (FETCH + WRITE) / the row's algorithmic bytes (bench.py's
+`work`) for the HBM-bound rows.
+
+| bench row | kernel (WGs) | dispatches | rocprof median us | FETCH MB | WRITE MB | traffic / algorithmic |
+|---|---|---:|---:|---:|---:|---:|
+""" + '\n'.join(lines) + '\n')
+
+    # ---- the default bench run: one chunk of its timed loop ----
+    rows = _trace(f'{gdir}/pbench/bench_kernel_trace.csv')
+    js = _json_line(f'{gdir}/pbench.log') or {}
+    att_runs = _runs(rows, 'attn_decode_kernel', 18)
+    # the timed loop ends where the roofline timing's launches start
+    stop = rows.index(att_runs[0][0]) if att_runs else len(rows)
+    starts = [i for i in range(stop) if 'im2col_kernel' in rows[i]['name']]
+    chunk = None
+    for j, s0 in enumerate(starts):
+        s1 = starts[j + 1] if j + 1 < len(starts) else stop
+        ends = [i for i in range(s0, s1)
+                if 'gemm_skinny_kernel<3' in rows[i]['name']]
+        if ends:
+            chunk = rows[s0:ends[-1] + 1]
+    agg = {}
+    for r in chunk:
+        a = agg.setdefault(r['name'], [0, 0.0])
+        a[0] += 1
+        a[1] += r['us']
+    tot = sum(a[1] for a in agg.values())
+    span = (int(chunk[-1]['End_Timestamp']) -
+            int(chunk[0]['Start_Timestamp'])) / 1e6
+    table = '\n'.join(f'| `{n}` | {c} | {d / 1e3:.3f} | {d / c:.2f} |'
+                      for n, (c, d) in sorted(agg.items(), key=lambda kv: -kv[1][1]))
+    with open(f'{outdir}/pi0_bs1_chunk_kernel_stats.md', 'w') as fh:
+        fh.write(f"""# PI0 bs=1 action chunk -- rocprofv3 kernel statistics
+
+Command (repo root `R` on the MI355X box, `export TMPDIR=/tmp`; the default
+bench run itself; this file is `python3 bench.py --summarize-profiles
+gpurun_out` over its CSV):
+
+    {profile_commands()[-1]}
+
+The last whole chunk of bench.py's timed loop (graph replay; from its
+im2col to its last Euler GEMM).  The same run printed value =
+{js.get('value')} ms per chunk (HIP events, no profiler in the way of its
+own figure; under the profiler the chunk spans longer).
+
+One chunk: {len(chunk)} dispatches, {tot / 1e3:.3f} ms of kernel time over a
+{span:.3f} ms span.
+
+| kernel | calls | ms | avg us |
+|---|---:|---:|---:|
+{table}
+""")
+
+    # ---- the roofline kernels' own launches in the same run ----
+    roof, mf = js.get('roofline') or {}, js.get('roofline_mfma') or {}
+    att = '\n'.join('    ' + _run_line(r) for r in att_runs)
+    geg = '\n'.join('    ' + _run_line(r)
+                    for r in _runs(rows, 'gemm_wide_kernel<1', 17))
+    with open(f'{outdir}/pi0_bs1_dominant_kernel_trace.md', 'w') as fh:
+        fh.write(f"""# Roofline kernels of the PI0 bs=1 chunk -- rocprofv3 kernel trace of bench.py
+
+`roofline`: the chunk's largest kernel by time, `attn_decode_kernel` (the
+bs=1 expert's decode attention: 408 query rows x 867 keys, 14 key ranges
+merged inside the launch, idle workgroups prefetching the next GEMMs'
+weights and the next layer's key / value cache; {roof.get('bytes_per_launch')}
+algorithmic bytes per launch, {roof.get('launches_per_chunk')} launches per
+chunk).  `roofline_mfma`: the prefix GeGLU GEMM (`gemm_wide_kernel<1, ...>`,
+M=816, N=16384 x 2, K=2048, {mf.get('flops_per_launch')} flops per launch).
+
+Command (repo root `R` on the MI355X box, `export TMPDIR=/tmp`; the default
+bench run; this file is `python3 bench.py --summarize-profiles gpurun_out`):
+
+    {profile_commands()[-1]}
+
+Runs of back-to-back dispatches in start order (durations End - Start;
+span/launch = first start to last end over the run, which keeps the kernel
+boundaries as bench.py's HIP-event figure does).  bench.py times the 18
+expert layers' launches in one graph (one eager pass, then 3 + 20
+replays): its run is the {18 * 23}-dispatch one.
+
+attn_decode_kernel (bench.py in the same run: avg_us {roof.get('avg_us')} per
+launch, frac {roof.get('frac')} of HBM peak):
+
+{att}
+
+gemm_wide_kernel<1> (bench.py: avg_us {mf.get('avg_us')}, {mf.get('achieved')}
+TFLOP/s, frac {mf.get('frac')}; hipBLASLt on the same flops
+{mf.get('library_us')} us):
+
+{geg}
+""")
+
+
 def cpu_model_name():
     """The host CPU's model string (/proc/cpuinfo), else platform's guess."""
     import platform
@@ -783,7 +1071,15 @@ def main():
                     help='run only the per-kernel table (every main kernel '
                     'of the chunk at its chunk shape) + a calibration copy '
                     '(for rocprofv3 --kernel-trace / --pmc passes)')
+    ap.add_argument('--summarize-profiles', metavar='DIR',
+                    help='write the profiles/*.md summaries into DIR/profiles '
+                    'from the CSVs of the rocprofv3 passes under DIR (see '
+                    'profile_commands)')
     args = ap.parse_args()
+    if args.summarize_profiles:
+        d = args.summarize_profiles
+        summarize_profiles(d, os.path.join(d, 'profiles'))
+        return
     if args.gpus != 1:
         print('bench.py: this build runs on one GPU; multi-GPU figures are '
               'not part of it (the path shards by request, see DESIGN.md)',

@@ -222,8 +222,13 @@ const char* fvx_last_error(void);
  * requests a range length of ceil(K / split_k) (still capped at 256). */
 int64_t fvx_gemm_workspace_bytes(const fvx_gemm_desc* d);
 
-/* General GEMM with fused epilogue (all matmul_* entry points below are thin
- * wrappers around it). */
+/* General GEMM with fused epilogue.  Replaces the reference's
+ * matmul_bias_cuda (fluxvla/ops/cuda/matmul_bias/matmul_bias.py:19-60,
+ * matmul_bias_forward.cpp:21-51) and the Triton GEMMs behind
+ * fluxvla/ops/atomic_ops.py:34-378 (matmul_bias_res, matmul_res,
+ * matmul_bias_silu, matmul_bias_small, rms_matmul_gate / matmul_gate,
+ * rms_matmul_qkv_rope / matmul_qkv_rope, matmul_res_gate, ...): one
+ * descriptor covers every epilogue those entry points fuse. */
 int fvx_gemm(const fvx_gemm_desc* d, void* stream);
 
 /*
