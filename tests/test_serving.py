@@ -123,3 +123,29 @@ def test_run_needs_pyzmq():
     except ImportError:
         with pytest.raises(ImportError):
             PolicyServer(bind=True)
+
+
+def test_msgpack_observation_bytes_and_order():
+    """The reference's map order (frames, then arrays, then strings, each
+    in the observation's order) and bytes; untagged values pass through."""
+    img = np.zeros((8, 8, 3), np.uint8)
+    st = np.arange(3, dtype=np.float32)
+    obs = {'prompt': 'go', 'state': st, 'cam_high': img}
+    raw = S.ObsSerializer.to_bytes(obs)
+    npy = io.BytesIO()
+    np.save(npy, st, allow_pickle=False)
+    want_tail = msgpack.packb({'state': {'__ndarray__': True,
+                                         'data': npy.getvalue()},
+                               'prompt': 'go'})
+    keys = list(msgpack.unpackb(raw, raw=False))
+    assert keys == ['cam_high', 'state', 'prompt']
+    # the map after its first entry is byte for byte the arrays and strings
+    assert raw.endswith(want_tail[1:])
+    extra = msgpack.packb({'meta': {'a': 1}, 'name': b'xy'})
+    assert S.ObsSerializer.from_bytes(extra) == {'meta': {'a': 1},
+                                                 'name': 'xy'}
+    back = S.ObsSerializer.from_bytes(raw)
+    assert list(back) == keys and back['prompt'] == 'go'
+    assert np.array_equal(back['state'], st) and back['cam_high'].shape == (8, 8, 3)
+    assert S.MsgSerializer.from_bytes(S.MsgSerializer.to_bytes(
+        {'x': [st, 1]}))['x'][0].tolist() == [0.0, 1.0, 2.0]
