@@ -680,6 +680,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   constexpr int HD = 256, KT = kDecKT;
   __shared__ __align__(16) unsigned char smem[kDecLDS];
   __shared__ float sL[4][64], sM[64];
+  warm_kernargs<sizeof(fvx_attn_desc) + 32>();
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int n_groups = (int)p.n_problems * n_rg;
   if (counters && (int)blockIdx.x >= n_items && (int)blockIdx.x < merge_first) {

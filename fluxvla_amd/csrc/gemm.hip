@@ -1602,6 +1602,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   __shared__ float sP[W][NB][RR][16 + 1];
   __shared__ float sS[W][RR];
   __shared__ int s_last;
+  warm_kernargs<sizeof(GemmArgs) + 24>();
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
