@@ -71,6 +71,7 @@ __global__ __launch_bounds__(256) void attn_kernel(fvx_attn_desc p,
   __shared__ __align__(16) bf16_t sK[kKeyTile * LDK];
   __shared__ __align__(16) bf16_t sVt[HDV * LDV];
   __shared__ int32_t sG[kKeyTile];
+  warm_kernargs<sizeof(fvx_attn_desc) + 32>();
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
@@ -1068,6 +1069,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
   __shared__ __align__(16) unsigned char smem[dt_lds<NW>()];
   __shared__ float sLq[RPW], sMq[RPW];
+  warm_kernargs<sizeof(fvx_attn_desc) + 32>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane & 31, h = lane >> 5;
@@ -1389,6 +1391,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
 // issued before the merge, which is applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
     fvx_attn_desc p, int n_rg, int splits, int hs) {
+  warm_kernargs<sizeof(fvx_attn_desc) + 32>();
   const int R = (int)(p.sq * p.heads);
   const int gid = blockIdx.x * 256 + threadIdx.x;
   if (gid >= (int)p.n_problems * R * 32) return;

@@ -545,6 +545,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   constexpr int AROWS = C::AROWS;
   __shared__ __align__(16) char smem[C::LDS_BYTES];
   __shared__ float sRow[BM];
+  warm_kernargs<sizeof(GemmArgs) + 24>();
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -936,6 +937,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
   static_assert(NWV == 4 || NWV == 8, "4 or 8 waves");
   __shared__ __align__(16) char smem[wide_lds_bytes<NWV>()];
   __shared__ float sRow[kGwBM];
+  warm_kernargs<sizeof(GemmArgs) + 24>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -1243,6 +1245,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   static_assert(!(F8A && SUM_A), "an e4m3 A has no bf16 squares to sum");
   __shared__ __align__(16) char smem[kGw8Stages * kGw8Stage];
   __shared__ float sRow[kGwBM];
+  warm_kernargs<sizeof(GemmArgs) + 24>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -1920,6 +1923,7 @@ template <int MODE>
 __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
                                                                   int splits,
                                                                   int vec_ok) {
+  warm_kernargs<sizeof(GemmArgs) + 24>();
   constexpr int NB = (MODE == FVX_GEMM_GEGLU) ? 2 : 1;
   constexpr int UN = 8;  // splits in flight per pass
   const int64_t N = p.n, K = p.k, M = p.m;
