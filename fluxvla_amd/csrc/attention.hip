@@ -443,20 +443,33 @@ constexpr int kDecLDS = kDecOffQG + 64 * 4;
 static_assert(64 * kDecOP * 4 <= 2 * kDecStage, "O rows fit the stages");
 constexpr int kDecLoads = 17;  // DMA instructions per wave per tile
 
-// Query row r of a problem is (token r / heads, head r % heads); `hs` is
-// log2(heads) when heads is a power of two (shifts instead of divisions).
-__device__ __forceinline__ int row_tok(int r, int heads, int hs) {
-  return hs >= 0 ? r >> hs : r / heads;
-}
+// Division by the small divisors of the decode kernels (heads, the problem
+// divisor zdiv, the row-group and split counts): x / d = umulhi(x, m) with
+// m = ceil(2^32 / d) (0 for d = 1), exact for x < 2^32 / d -- the host
+// checks every dividend's bound (dec_div_exact).  One multiply in
+// place of a ~20-instruction integer division: the decode prologues run
+// dozens of them before their first load is issued.
+struct FastDiv {
+  uint32_t m;
+  __device__ __forceinline__ int div(int x) const {
+    return m ? (int)__umulhi((uint32_t)x, m) : x;
+  }
+};
+struct DecDiv {
+  FastDiv heads, zdiv, rg, splits, rgw;  // rgw: the 128-row groups (NW = 4)
+};
+
+// Query row r of a problem is (token r / heads, head r % heads).
+__device__ __forceinline__ int row_tok(int r, const DecDiv& dv) { return dv.heads.div(r); }
 
 // One output chunk: `n` (4 or 8) dims d0.. of query row r of problem z,
 // row-major and, if requested, fragment-major for the o-projection.
 template <int NE>
 __device__ __forceinline__ void dec_store(const fvx_attn_desc& p, int z, int r,
-                                          int d0, int hs, const float* v) {
+                                          int d0, const DecDiv& dv, const float* v) {
   const int heads = (int)p.heads;
-  const int tok = row_tok(r, heads, hs), h = r - tok * heads;
-  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
+  const int tok = row_tok(r, dv), h = r - tok * heads;
+  const int64_t zb = dv.zdiv.div(z), zh = z - zb * p.zdiv;
   // o may be NULL on this path when o_frag is given (the row-major copy
   // has no reader then)
   bf16_t* dst = p.o ? (bf16_t*)p.o + zb * p.o_zs1 + zh * p.o_zs2 + (int64_t)tok * p.o_tok_stride +
@@ -501,7 +514,7 @@ __device__ void dec_prefetch(const fvx_attn_desc& p, int pw, int npw, int first,
 // no load is spent on splits that do not exist).
 template <int AUX, int NS>
 __device__ __forceinline__ void dec_merge8_ns(const fvx_attn_desc& p, int n_rg, int splits,
-                                              int hs, int z, int r, int d0) {
+                                              const DecDiv& dv, int z, int r, int d0) {
   const int rg = r >> 6, i = r & 63;
   const float* base = (const float*)p.workspace + (((int64_t)z * n_rg + rg) * splits) * kDecPF;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(base, (uint32_t)(splits * kDecPF * 4));
@@ -546,7 +559,7 @@ __device__ __forceinline__ void dec_merge8_ns(const fvx_attn_desc& p, int n_rg, 
   const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] *= inv;
-  dec_store<8>(p, z, r, d0, hs, acc);
+  dec_store<8>(p, z, r, d0, dv, acc);
 }
 
 // dec_merge8_ns for the in-launch merge (splits <= 16, partials of this
@@ -554,7 +567,7 @@ __device__ __forceinline__ void dec_merge8_ns(const fvx_attn_desc& p, int n_rg, 
 // references and sums from sML[split][8 rows] (staged in LDS by the merging
 // workgroup, one load per thread instead of two per split and thread).
 __device__ __forceinline__ void dec_merge8_staged(const fvx_attn_desc& p, int n_rg, int splits,
-                                                  int hs, int z, int r, int d0,
+                                                  const DecDiv& dv, int z, int r, int d0,
                                                   const float2* sML) {
   constexpr int NS = 16;
   const int rg = r >> 6, i = r & 63, rl = r & 7;
@@ -588,18 +601,18 @@ __device__ __forceinline__ void dec_merge8_staged(const fvx_attn_desc& p, int n_
   const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] *= inv;
-  dec_store<8>(p, z, r, d0, hs, acc);
+  dec_store<8>(p, z, r, d0, dv, acc);
 }
 
 template <int AUX>
 __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int splits,
-                                           int hs, int z, int r, int d0) {
+                                           const DecDiv& dv, int z, int r, int d0) {
   if (splits <= 4)
-    dec_merge8_ns<AUX, 4>(p, n_rg, splits, hs, z, r, d0);
+    dec_merge8_ns<AUX, 4>(p, n_rg, splits, dv, z, r, d0);
   else if (splits <= 8)
-    dec_merge8_ns<AUX, 8>(p, n_rg, splits, hs, z, r, d0);
+    dec_merge8_ns<AUX, 8>(p, n_rg, splits, dv, z, r, d0);
   else
-    dec_merge8_ns<AUX, 16>(p, n_rg, splits, hs, z, r, d0);
+    dec_merge8_ns<AUX, 16>(p, n_rg, splits, dv, z, r, d0);
 }
 
 // One merging workgroup of the in-launch merge: 8 rows (chunk) of 64-row
@@ -614,12 +627,12 @@ __device__ __forceinline__ void dec_merge8(const fvx_attn_desc& p, int n_rg, int
 // reset leaves a count behind, so fvx_attention_check reports the status
 // and clears every counter before the next call relies on them.  The
 // group's last merging workgroup resets both of its counters.
-__device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, int hs,
+__device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, const DecDiv& dv,
                              uint32_t* counters, int grp, int chunk, int polls,
                              unsigned char* smem) {
   const int tid = threadIdx.x;
   const int R = (int)(p.sq * p.heads);
-  const int z = grp / n_rg, rg = grp % n_rg;
+  const int z = dv.rg.div(grp), rg = grp - z * n_rg;
   const int r = rg * 64 + 8 * chunk + (tid >> 5), d0 = (tid & 31) * 8;
   uint32_t* ctr = counters + (int64_t)grp * 64;
   if (tid == 0) {
@@ -651,7 +664,7 @@ __device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, int h
     ((float*)sML)[2 * (s * 8 + rl) + which] = v;
   }
   __syncthreads();
-  dec_merge8_staged(p, n_rg, splits, hs, z, r, d0, sML);
+  dec_merge8_staged(p, n_rg, splits, dv, z, r, d0, sML);
   if (tid == 0) {
     const int rows = R - rg * 64 < 64 ? R - rg * 64 : 64;
     const uint32_t old =
@@ -674,7 +687,7 @@ __device__ void dec_merge_wg(const fvx_attn_desc& p, int n_rg, int splits, int h
 // R) do nothing.  n_items and merge_first are multiples of 8.
 __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
                                                           int n_rg, int splits,
-                                                          int kps, int hs,
+                                                          int kps, DecDiv dv,
                                                           int n_items,
                                                           uint32_t* counters,
                                                           int merge_first) {
@@ -686,8 +699,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   const int n_groups = (int)p.n_problems * n_rg;
   if (counters && (int)blockIdx.x >= n_items && (int)blockIdx.x < merge_first) {
     const int j = slot - n_items / 8, grp = xcd + 8 * (j / 8);
-    if (grp < n_groups && (grp % n_rg) * 64 + 8 * (j % 8) < (int)(p.sq * p.heads))
-      dec_merge_wg(p, n_rg, splits, hs, counters, grp, j % 8,
+    if (grp < n_groups && (grp - dv.rg.div(grp) * n_rg) * 64 + 8 * (j % 8) < (int)(p.sq * p.heads))
+      dec_merge_wg(p, n_rg, splits, dv, counters, grp, j % 8,
                    p.merge_no_wait ? 0 : kDecMergeSpin, smem);
     return;
   }
@@ -701,20 +714,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
   const int fr = lane & 15, g = lane >> 4;
   int item;
   if (counters) {
-    const int grp = xcd + 8 * (slot / splits);
+    const int sq = dv.splits.div(slot);
+    const int grp = xcd + 8 * sq;
     if (grp >= n_groups) return;  // an empty slot
-    item = ((grp / n_rg) * splits + slot % splits) * n_rg + grp % n_rg;
+    const int gz = dv.rg.div(grp);
+    item = (gz * splits + (slot - sq * splits)) * n_rg + (grp - gz * n_rg);
   } else {
     // XCD-aware order: consecutive items (the row groups of one key range)
     // land on one XCD and share its L2 copy of the range's K / V tiles.
     const int nb = n_items, q8 = nb >> 3, r8 = nb & 7;
     item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
   }
-  const int rg = item % n_rg;
-  const int split = (item / n_rg) % splits;
-  const int z = item / (n_rg * splits);
+  const int ir = dv.rg.div(item), rg = item - ir * n_rg;
+  const int z = dv.splits.div(ir), split = ir - z * splits;
   const int heads = (int)p.heads, R = (int)p.sq * heads;
-  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
+  const int64_t zb = dv.zdiv.div(z), zh = z - zb * p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
   const bf16_t* K = (const bf16_t*)p.k + zb * p.k_zs1 + zh * p.k_zs2;
   const bf16_t* Vt = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
@@ -775,7 +789,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     for (int i = 0; i < 8; ++i) {
       const int rl = 16 * w + 2 * i + (lane >> 5);
       const int r = rg * 64 + rl;
-      const int tok = row_tok(r, heads, hs);
+      const int tok = row_tok(r, dv);
       const int ch = (lane & 31) ^ (rl & 15);
       load_lds16(rq, qb + (16 * w + 2 * i) * 512,
                  r < R ? (uint32_t)(tok * qts + (r - tok * heads) * qhs + 8 * ch) * 2
@@ -783,7 +797,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
     }
     if (w == 0) {
       const int r = rg * 64 + lane;
-      load_lds4(rqg, lbase + kDecOffQG, r < R ? (uint32_t)row_tok(r, heads, hs) * 4 : kOOB);
+      load_lds4(rqg, lbase + kDecOffQG, r < R ? (uint32_t)row_tok(r, dv) * 4 : kOOB);
     }
   }
   issue(kbeg, 0);
@@ -957,7 +971,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(fvx_attn_desc p,
       const f32x4_t b = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
       float v[8] = {a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv,
                     b[0] * inv, b[1] * inv, b[2] * inv, b[3] * inv};
-      dec_store<8>(p, z, r, d0, hs, v);
+      dec_store<8>(p, z, r, d0, dv, v);
     }
     return;
   }
@@ -1064,7 +1078,7 @@ __device__ __forceinline__ float half_pair_sum(float v) {
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
                                                                 int n_rg, int splits,
-                                                                int kps, int hs) {
+                                                                int kps, DecDiv dv) {
   constexpr int HD = 256, KT = 64, RPW = 32 * NW, LPW = 32 / NW;
   static_assert(NW == 2 || NW == 4, "2 or 4 waves");
   __shared__ __align__(16) unsigned char smem[dt_lds<NW>()];
@@ -1077,11 +1091,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int item = xcd * q8 + (xcd < r8 ? xcd : r8) + slot;
   const int n_rgw = (n_rg * 64 + RPW - 1) / RPW;  // RPW-row groups
-  const int rg = item % n_rgw;
-  const int split = (item / n_rgw) % splits;
-  const int z = item / (n_rgw * splits);
+  const int ir = dv.rgw.div(item), rg = item - ir * n_rgw;
+  const int z = dv.splits.div(ir), split = ir - z * splits;
   const int heads = (int)p.heads, R = (int)p.sq * heads;
-  const int64_t zb = (uint32_t)z / (uint32_t)p.zdiv, zh = (uint32_t)z % (uint32_t)p.zdiv;
+  const int64_t zb = dv.zdiv.div(z), zh = z - zb * p.zdiv;
   const bf16_t* Q = (const bf16_t*)p.q + zb * p.q_zs1 + zh * p.q_zs2;
   const bf16_t* K = (const bf16_t*)p.k + zb * p.k_zs1 + zh * p.k_zs2;
   const bf16_t* Vt = (const bf16_t*)p.v + zb * p.v_zs1 + zh * p.v_zs2;
@@ -1134,7 +1147,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int L = 16 * w + i, rl = 2 * L + (lane >> 5), r = rg * RPW + rl;
-      const int tok = row_tok(r, heads, hs);
+      const int tok = row_tok(r, dv);
       const int ch = (lane & 31) ^ (rl & 15);
       load_lds16(rq, qb + 2 * L * 512,
                  r < R ? (uint32_t)(tok * qts + (r - tok * heads) * qhs + 8 * ch) * 2 : kOOB);
@@ -1142,7 +1155,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
     if (w < NW / 2) {  // 64 rows' groups per wave
       const int r = rg * RPW + 64 * w + lane;
       load_lds4(rqg, lbase + kDtOffQG + 256 * w,
-                r < R ? (uint32_t)row_tok(r, heads, hs) * 4 : kOOB);
+                r < R ? (uint32_t)row_tok(r, dv) * 4 : kOOB);
     }
   }
 #pragma unroll
@@ -1363,7 +1376,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
       const f32x4_t b = *(const f32x4_t*)&sO[i * kDecOP + d0 + 4];
       float v[8] = {a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv,
                     b[0] * inv, b[1] * inv, b[2] * inv, b[3] * inv};
-      dec_store<8>(p, z, r, d0, hs, v);
+      dec_store<8>(p, z, r, d0, dv, v);
     }
     return;
   }
@@ -1390,7 +1403,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_t_kernel(fvx_attn_desc p,
 // dims); the loads of up to 4, 8 or 16 splits (as many as there are) are
 // issued before the merge, which is applied in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
-    fvx_attn_desc p, int n_rg, int splits, int hs) {
+    fvx_attn_desc p, int n_rg, int splits, DecDiv dv) {
   warm_kernargs<sizeof(fvx_attn_desc) + 32>();
   const int R = (int)(p.sq * p.heads);
   const int gid = blockIdx.x * 256 + threadIdx.x;
@@ -1398,7 +1411,7 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(
   const int d0 = (gid & 31) * 8;
   const int zr = gid >> 5;
   const int z = zr / R, r = zr % R;
-  dec_merge8<0>(p, n_rg, splits, hs, z, r, d0);
+  dec_merge8<0>(p, n_rg, splits, dv, z, r, d0);
 }
 
 struct AttnPlan {
@@ -1486,10 +1499,34 @@ static DecodePlan plan_decode(const fvx_attn_desc& d) {
   return a;
 }
 
+// FastDiv of d: m = ceil(2^32 / d), 0 for d = 1 (d < 2^31).
+static FastDiv fast_div(int64_t d) {
+  return FastDiv{d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) / (uint64_t)d)};
+}
+static int64_t dt_groups(int n_rb) { return ((int64_t)n_rb * 64 + 32 * kDtNW - 1) / (32 * kDtNW); }
+static DecDiv dec_div(const fvx_attn_desc& d, const DecodePlan& a) {
+  return DecDiv{fast_div(d.heads), fast_div(d.zdiv), fast_div(a.n_rb), fast_div(a.splits),
+                fast_div(dt_groups(a.n_rb))};
+}
+// every dividend of a FastDiv stays below 2^32 / divisor
+static bool dec_div_exact(const fvx_attn_desc& d, const DecodePlan& a) {
+  const uint64_t lim = (uint64_t)1 << 32;
+  const uint64_t R = (uint64_t)(d.sq * d.heads), items = (uint64_t)a.n_items + 8 * 256;
+  const uint64_t wide = (uint64_t)d.n_problems * a.splits * dt_groups(a.n_rb) + 8 * 256;
+  return R * (uint64_t)d.heads < lim && (uint64_t)d.n_problems * (uint64_t)d.zdiv < lim &&
+         items * (uint64_t)a.n_rb < lim && items * (uint64_t)a.splits < lim &&
+         wide * (uint64_t)dt_groups(a.n_rb) < lim && wide * (uint64_t)a.splits < lim;
+}
+// the decode kernels serve d: head_dim 256 with the transposed value cache,
+// 32-bit operand offsets, exact fast divisions
+static bool decode_ok(const fvx_attn_desc& d) {
+  return use_decode(d) && dec_div_exact(d, plan_decode(d));
+}
+
 extern "C" int64_t fvx_attention_workspace_bytes(const fvx_attn_desc* d) {
   if (!d || d->sq <= 0 || d->sk <= 0 || d->heads <= 0 || d->n_problems <= 0)
     return 0;
-  if (use_decode(*d)) return plan_decode(*d).ws_bytes;
+  if (decode_ok(*d)) return plan_decode(*d).ws_bytes;
   return plan_attn(*d).ws_bytes;
 }
 
@@ -1574,7 +1611,7 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
               FVX_ERR_SHAPE,
               "attention: a transposed V needs head_dim 256, v_d_stride %% 8 "
               "== 0 and sk <= v_d_stride");
-  FVX_REQUIRE(!d.o_frag || (use_decode(d) && d.n_problems * d.sq <= 64 &&
+  FVX_REQUIRE(!d.o_frag || (decode_ok(d) && d.n_problems * d.sq <= 64 &&
                              d.o_head_stride % 8 == 0 && d.o_tok_stride % 8 == 0 &&
                              aligned16(d.o) && aligned16(d.o_frag)),
               FVX_ERR_ARG,
@@ -1593,7 +1630,7 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
   if (d.sq == 0 || d.n_problems == 0) return FVX_OK;
   FVX_REQUIRE(d.sk > 0, FVX_ERR_SHAPE, "attention: sk must be > 0");
   hipStream_t s = (hipStream_t)stream;
-  if (use_decode(d)) {
+  if (decode_ok(d)) {
     DecodePlan a = plan_decode(d);
     if (a.splits > 1 && (!d.workspace || d.workspace_bytes < a.ws_bytes))
       return set_error(FVX_ERR_WORKSPACE,
@@ -1602,7 +1639,7 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
                        (long long)d.workspace_bytes);
     FVX_REQUIRE(aligned16(d.workspace), FVX_ERR_ALIGN,
                 "attention: workspace must be 16B aligned");
-    const int hs = (d.heads & (d.heads - 1)) == 0 ? __builtin_ctzll((uint64_t)d.heads) : -1;
+    const DecDiv dv = dec_div(d, a);
     const fvx_attn_desc dk = past_counters(d);
     // the 4-wave kernel's in-launch merge: each 64-row group's ranges and
     // its 8 merging workgroups on one XCD, all of them resident at once
@@ -1629,11 +1666,11 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
       const int64_t groups = (a.n_rb * 64 + 32 * kDtNW - 1) / (32 * kDtNW);
       const int64_t wgs = d.n_problems * a.splits * groups;
       hipLaunchKernelGGL(attn_decode_t_kernel<kDtNW>, dim3((unsigned)wgs),
-                         dim3(64 * kDtNW), 0, s, dk, a.n_rb, a.splits, (int)a.kps, hs);
+                         dim3(64 * kDtNW), 0, s, dk, a.n_rb, a.splits, (int)a.kps, dv);
     } else
       hipLaunchKernelGGL(attn_decode_kernel,
                          dim3((unsigned)(item_blocks + merge_blocks + pf_wgs)), dim3(256), 0,
-                         s, dk, a.n_rb, a.splits, (int)a.kps, hs, item_blocks,
+                         s, dk, a.n_rb, a.splits, (int)a.kps, dv, item_blocks,
                          fused ? (uint32_t*)d.workspace : nullptr,
                          item_blocks + merge_blocks);
     int st = launch_status("attention(decode)");
@@ -1641,7 +1678,7 @@ extern "C" int fvx_attention(const fvx_attn_desc* dp, void* stream) {
     const int64_t threads = (int64_t)d.n_problems * d.sq * d.heads * 32;
     hipLaunchKernelGGL(attn_decode_merge_kernel,
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                       dk, a.n_rb, a.splits, hs);
+                       dk, a.n_rb, a.splits, dv);
     return launch_status("attention(decode merge)");
   }
   return run_generic(d, s);
