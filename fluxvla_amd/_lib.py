@@ -76,6 +76,7 @@ class GemmDesc(ctypes.Structure):
         ('rtc_cw', c_vp),
         ('rtc_omt', c_f32),
         ('a_scale', c_vp), ('bias2_f32', c_vp),
+        ('ln_csum', c_vp),
     ]
 
 

@@ -75,6 +75,17 @@ __device__ __forceinline__ float sumsq8(const bf16x8& v) {
   return s;
 }
 
+// sum of 8 bf16 values: four dot products with (1, 1) (exact products)
+__device__ __forceinline__ float sum8(const bf16x8& v) {
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  const bf16x2v one = {(__bf16)1.0f, (__bf16)1.0f};
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.w[i]), one, s, false);
+  return s;
+}
+
 // ---------------------------------------------------------------------------
 // Row-chunk epilogue: output columns n .. n + 7 of one row m.
 //
@@ -96,6 +107,7 @@ struct EpiIn {
   float xt[8];    // EULER state
   float prev[8];  // EULER with RTC: the previous chunk's actions
   float cw;       // EULER with RTC guidance: the row's correction weight
+  float cs[8];    // PLAIN with a folded LayerNorm: the weight's column sums
   bool locked;    // PLAIN, EULER: the row is in the RTC locked prefix
 };
 
@@ -160,7 +172,7 @@ __device__ __forceinline__ void bl_f8(__amdgpu_buffer_rsrc_t r, uint32_t off,
 // outside the item loops (an absent operand gets an empty view, whose reads
 // return zeros).
 struct EpiViews {
-  __amdgpu_buffer_rsrc_t bias, bf32, gate, res, pos, xt, prev, cw, rope, positions;
+  __amdgpu_buffer_rsrc_t bias, bf32, gate, res, pos, xt, prev, cw, rope, positions, csum;
 };
 
 template <int MODE>
@@ -168,7 +180,7 @@ __device__ __forceinline__ EpiViews epi_views(const GemmArgs& p) {
   EpiViews V;
   const int64_t N = p.n;
   V.bias = V.bf32 = V.gate = V.res = V.pos = V.xt = V.prev = V.cw = V.rope = V.positions =
-      make_rsrc(nullptr, 0u);
+      V.csum = make_rsrc(nullptr, 0u);
   if (MODE == FVX_GEMM_QKV_ROPE) {
     V.positions = make_rsrc(p.positions, rec_bytes(p.m * 4));
     V.rope = make_rsrc(p.rope, 0x7fffffffu);
@@ -183,6 +195,7 @@ __device__ __forceinline__ EpiViews epi_views(const GemmArgs& p) {
     V.cw = make_rsrc(p.rtc_cw, p.rtc_cw ? rec_bytes(p.rtc_period * 4) : 0u);
   }
   if (MODE == FVX_GEMM_PLAIN) {
+    V.csum = make_rsrc(p.ln_csum, p.ln_csum ? rec_bytes(N * 4) : 0u);
     const bool gdiv = p.gate_group > 1;
     const int64_t grows = gdiv ? udiv32(p.m + p.gate_group - 1, p.gate_group) : p.m;
     V.gate = make_rsrc(p.gate, p.gate ? rec_bytes(grows * p.ldg * 2) : 0u);
@@ -197,12 +210,14 @@ __device__ __forceinline__ EpiViews epi_views(const GemmArgs& p) {
 __device__ __align__(16) const float kZeros8[8] = {};
 
 // the column operands of columns n .. n + 7 (bias_f32: the unlocked rows')
-template <int MODE>
+// (LN: the kernel build with the folded LayerNorm, which reads ln_csum)
+template <int MODE, bool LN = false>
 __device__ __forceinline__ void epi_load_col(const EpiViews& V, int64_t n, bool vec,
                                              EpiIn& in) {
   if (MODE != FVX_GEMM_PLAIN && MODE != FVX_GEMM_EULER) return;
   in.bias = bl_b8(V.bias, (uint32_t)(n * 2), vec);
   bl_f8(V.bf32, (uint32_t)(n * 4), vec, in.f0);
+  if (MODE == FVX_GEMM_PLAIN && LN) bl_f8(V.csum, (uint32_t)(n * 4), vec, in.cs);
 }
 
 // the row operands of row m, columns n .. n + 7
@@ -263,18 +278,22 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, const EpiViews& V, i
   epi_load_row<MODE>(p, V, m, n, vec, cnt, in);
 }
 
-// v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m.
-// want_xo (PLAIN, GEGLU): xo receives the 8 values as stored (bf16-rounded
-// unless out_f32), for the hand-over outputs (epi_handoff).
-template <int MODE>
+// v: main accumulators, u: GEGLU up accumulators, r: RMS factor of row m
+// (LN build with a folded LayerNorm: its rsqrt(var + eps), with mr =
+// mean * r).  want_xo (PLAIN, GEGLU): xo receives the 8 values as stored
+// (bf16-rounded unless out_f32), for the hand-over outputs (epi_handoff).
+template <int MODE, bool LN = false>
 __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
                                           int64_t n, bool vec, int cnt,
                                           const float* v, const float* u,
                                           float r, const EpiIn& in,
-                                          bool want_xo, float* xo) {
+                                          bool want_xo, float* xo, float mr = 0.f) {
   float x[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = v[e] * r;
+  if (MODE == FVX_GEMM_PLAIN && LN && p.ln_csum)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = fmaf(-mr, in.cs[e], x[e]);
   if (MODE == FVX_GEMM_GEGLU) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = gelu_tanh(x[e]) * (u[e] * r);
@@ -376,13 +395,14 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
 }
 
 // Hand-over outputs of one row's 64-column block, held as 8-column chunks
-// by 8 consecutive lanes (every lane runs the shuffles; `valid`: this lane's
-// chunk exists, `lead`: its first lane): the row's sum of squares of the
-// stored values (ss_out) and the e4m3 copy with the block's E8M0 exponent
-// (a8_out), quantized exactly as quant_fp8x32 quantizes an A block.
-__device__ __forceinline__ void epi_handoff(const GemmArgs& p, bool valid, bool lead,
-                                            int64_t m, int64_t n, int cnt,
-                                            const float* xo) {
+// n .. n + 7 by 8 consecutive lanes (every lane runs the shuffles; `valid`:
+// this lane's chunk exists; the block's first lane stores): the row's sum of
+// squares of the stored values (ss_out) and the e4m3 copy with the block's
+// E8M0 exponent (a8_out), quantized exactly as quant_fp8x32 quantizes an A
+// block.
+__device__ __forceinline__ void epi_handoff(const GemmArgs& p, bool valid, int64_t m,
+                                            int64_t n, int cnt, const float* xo) {
+  const bool lead = ((n >> 3) & 7) == 0;
   if (p.ss_out) {
     float q = 0.f;
     if (valid)
@@ -437,23 +457,112 @@ __device__ __forceinline__ void epi_handoff(const GemmArgs& p, bool valid, bool 
   }
 }
 
-// Sum over the parts of a row's handed-over sums of squares (ss_in), all
-// loads in flight, added in part order; parts past the view read as zero.
-__device__ __forceinline__ float ss_in_row(const GemmArgs& p, int64_t m) {
-  const __amdgpu_buffer_rsrc_t r =
-      make_rsrc(p.ss_in, rec_bytes((int64_t)p.ss_parts * p.ss_ld * 4));
-  float s = 0.f;
-  for (int q0 = 0; q0 < p.ss_parts; q0 += 8) {
-    float t[8];
+// The handed-over sums of squares (`parts`: ss_in) of rows m0 .. m0 + R - 1,
+// with every thread of an NT-thread workgroup: thread t loads parts
+// t / R, t / R + NT / R, ... of row t % R, all loads in flight (up to 64
+// parts per row; more take a loop), and thread t < R receives its row's
+// total, added in a fixed order.  A loop over the parts in one thread per row
+// waited for a memory round trip per 8 parts before its wave could start
+// the K loop.  Every thread must call it (two barriers); sTmp: NT floats
+// of LDS.
+template <int R, int NT>
+__device__ float rows_parts_sum(const GemmArgs& p, const float* parts, int64_t m0, int64_t M,
+                                float* sTmp) {
+  static_assert(NT % R == 0, "whole rows per thread group");
+  constexpr int STEP = NT / R, MAXL = (64 + STEP - 1) / STEP;
+  const int tid = threadIdx.x, row = tid % R, j0 = tid / R;
+  const int64_t m = m0 + row;
+  const bool mv = m < M;
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(parts, rec_bytes((int64_t)p.ss_parts * p.ss_ld * 4));
+  float acc = 0.f;
+  if (p.ss_parts <= STEP * MAXL) {
+    float t[MAXL];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      t[u] = bload1f(r, q0 + u < p.ss_parts ? (uint32_t)(((int64_t)(q0 + u) * p.ss_ld + m) * 4)
-                                            : kOOB);
+    for (int u = 0; u < MAXL; ++u) {
+      const int q = j0 + STEP * u;
+      t[u] = bload1f(rs, (mv && q < p.ss_parts) ? (uint32_t)(((int64_t)q * p.ss_ld + m) * 4)
+                                                : kOOB);
+    }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s += t[u];
+    for (int u = 0; u < MAXL; ++u) acc += t[u];
+  } else {
+    for (int q = j0; q < p.ss_parts; q += STEP)
+      acc += bload1f(rs, mv ? (uint32_t)(((int64_t)q * p.ss_ld + m) * 4) : kOOB);
   }
-  return s;
+  sTmp[tid] = acc;
+  __syncthreads();
+  float tot = 0.f;
+  if (tid < R)
+#pragma unroll
+    for (int j = 0; j < STEP; ++j) tot += sTmp[j * R + tid];
+  __syncthreads();  // sTmp may be reused
+  return tot;
 }
+
+// The tile kernel's handed-over row sums of squares (ss_in) of rows m0 ..
+// m0 + R - 1, split in two so that no wait sits in front of the K loop:
+// issue() puts every load in flight ahead of the first slabs (thread t takes
+// parts t / R, t / R + NT / R, ... of row t % R, up to STEP * L parts per row
+// in registers), finish() adds them after the K loop, when they have long
+// landed; rows with more parts are loaded by finish() itself.  Thread t < R
+// receives its row's total, added in a fixed order.  Every thread calls
+// finish() (one barrier); sTmp: NT floats of LDS, not to be rewritten before
+// the caller's next barrier.
+template <int R, int NT>
+struct RowParts {
+  static_assert(NT % R == 0, "whole rows per thread group");
+  static constexpr int STEP = NT / R, L = STEP >= 4 ? (48 + STEP - 1) / STEP : 12;
+  float q[L];
+
+  __device__ __forceinline__ bool in_regs(const GemmArgs& p) const {
+    return p.ss_parts <= STEP * L;
+  }
+  // byte offset of part qi of row m (the host keeps the array below 2^31
+  // bytes); kOOB (a zero) past the parts or the rows
+  __device__ __forceinline__ static uint32_t off(uint32_t row4, uint32_t ld4, int qi, int parts,
+                                                 bool mv) {
+    const uint32_t o = row4 + (uint32_t)qi * ld4;
+    return (mv && qi < parts) ? o : kOOB;
+  }
+  __device__ __forceinline__ void issue(const GemmArgs& p, int64_t m0, int64_t M) {
+    const int tid = threadIdx.x, j0 = tid / R, parts = p.ss_parts;
+    const int64_t m = m0 + tid % R;
+    const bool mv = m < M && in_regs(p);
+    const uint32_t row4 = (uint32_t)m * 4u, ld4 = (uint32_t)p.ss_ld * 4u;
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(p.ss_in, rec_bytes((int64_t)parts * p.ss_ld * 4));
+#pragma unroll
+    for (int u = 0; u < L; ++u) q[u] = bload1f(rq, off(row4, ld4, j0 + STEP * u, parts, mv));
+  }
+  __device__ __forceinline__ float finish(const GemmArgs& p, int64_t m0, int64_t M,
+                                          float* sTmp) {
+    const int tid = threadIdx.x, j0 = tid / R, parts = p.ss_parts;
+    const int64_t m = m0 + tid % R;
+    float aq = 0.f;
+    if (in_regs(p)) {
+      // the sum starts here, after the K loop, not where the loads were
+      // issued (an add hoisted there would wait for them)
+#pragma unroll
+      for (int u = 0; u < L; ++u) {
+        asm volatile("" : "+v"(q[u]));
+        aq += q[u];
+      }
+    } else {
+      const uint32_t row4 = (uint32_t)m * 4u, ld4 = (uint32_t)p.ss_ld * 4u;
+      const __amdgpu_buffer_rsrc_t rq =
+          make_rsrc(p.ss_in, rec_bytes((int64_t)parts * p.ss_ld * 4));
+      for (int qi = j0; qi < parts; qi += STEP) aq += bload1f(rq, off(row4, ld4, qi, parts, m < M));
+    }
+    sTmp[tid] = aq;
+    __syncthreads();
+    float tq = 0.f;
+    if (tid < R)
+#pragma unroll
+      for (int j = 0; j < STEP; ++j) tq += sTmp[j * R + tid];
+    return tq;
+  }
+};
 
 // Host check: may the chunk epilogue use 16-byte accesses for full chunks?
 static bool epi_vec_ok(const GemmArgs& d) {
@@ -534,17 +643,32 @@ struct TileCfg {
 
 // F8 && A16 (W8A16): the F8 LDS layout (128-k slabs, e4m3 weight rows), but
 // A stays bf16 and each 8 weight bytes become one bf16 MFMA fragment.
-template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8, bool A16>
+// XF: the row-sum paths compiled in (bit 0: handed-over row sums of squares
+// read, ss_in; bit 1: hand-over outputs, ss_out / a8_out; bit 2, PLAIN, not
+// with bit 0: the folded LayerNorm, ln_csum, on sums of A's values and
+// squares taken in the K loop).  GEMMs without them run a build without their
+// code: compiled in but not taken, it cost such 20 us launches ~0.7 us.
+// bf16 bit-0 builds have no K-loop sum of squares: the host picks them only
+// for rownorm GEMMs with ss_in (fp8-weight tiles keep one build, XF = 3,
+// with every path).
+template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8, bool A16,
+          int XF = 3>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     GemmArgs p, int m_tiles, int n_tiles, int splits, int64_t kchunk,
     int vec_ok) {
   static_assert(!A16 || F8, "W8A16 is an fp8-weight variant");
+  constexpr bool RPX = (XF & 1) != 0, HOX = (XF & 2) != 0;
+  constexpr bool SUMX = !RPX || F8;  // builds with the K-loop sum of squares
+  // ... and of values, for the folded LayerNorm
+  constexpr bool LN = (XF & 4) != 0 && MODE == FVX_GEMM_PLAIN && !F8 && !RPX;
   typedef TileCfg<BM, BN, WGM, WGN, STAGES, MODE, F8> C;
   constexpr int NB = C::NB, WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
   constexpr int LPW = C::LPW, WNO = C::WNO, ELD = C::ELD, BK = C::BK;
   constexpr int AROWS = C::AROWS;
   __shared__ __align__(16) char smem[C::LDS_BYTES];
-  __shared__ float sRow[BM];
+  __shared__ float sRow[BM], sSum[BM], sTmp[64 * WGM * WGN];
+  // per-wave partial row sums (bf16, K-loop sums: squares, values)
+  __shared__ float sPart[LN ? 2 : 1][F8 || !SUMX ? 1 : WGN][F8 || !SUMX ? 1 : BM];
   warm_kernargs<sizeof(GemmArgs) + 24>();
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -630,12 +754,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  float ss[FM];
+  float ss[FM], sv[FM];
 #pragma unroll
-  for (int i = 0; i < FM; ++i) ss[i] = 0.f;
+  for (int i = 0; i < FM; ++i) ss[i] = sv[i] = 0.f;
   // the fused RMSNorm sums A's squares in the K loop unless they are handed
   // over (ss_in)
-  const bool sum_a = p.rownorm && !p.ss_in;
+  const bool sum_a = SUMX && p.rownorm && !p.ss_in;
+  const int wn_u = __builtin_amdgcn_readfirstlane(wn);
 
   // LDS row of B fragment j of this wave (GEGLU: gate blocks, then up)
   auto brow = [&](int j) {
@@ -731,7 +856,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        if (SS) ss[i] += sumsq8(af[b][i]);
+        // the waves of a row band share the sums: wave wn takes the steps
+        // ks = wn (mod WGN)
+        if (SS && (ks % WGN) == wn_u) {
+          ss[i] += sumsq8(af[b][i]);
+          if (LN) sv[i] += sum8(af[b][i]);
+        }
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32x32x16(af[b][i], bfr[b][j], acc[i][j]);
         issue_group(ks * FM + i, 4 * FM, tn, tst);
@@ -740,12 +870,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     }
   };
 
+  // handed-over row sums of squares: in flight ahead of the first slabs,
+  // added after the K loop
+  RowParts<BM, 64 * WGM * WGN> rparts;
+  const bool rp_on = RPX && p.rownorm && p.ss_in;
+  if constexpr (RPX)
+    if (rp_on) rparts.issue(p, m0, M);
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
-  // handed-over row sums: thread t < BM takes row m0 + t (these loads wait
-  // with the first slabs)
-  float ss_pre = 0.f;
-  if (p.rownorm && p.ss_in && tid < BM && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
   auto k_loop = [&](auto with_ss) {
     for (int t0 = 0; t0 < nk; t0 += STAGES) {
 #pragma unroll
@@ -758,23 +890,54 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
       }
     }
   };
-  if (sum_a)
-    k_loop(BoolC<true>{});
-  else
+  if constexpr (SUMX) {
+    if (sum_a)
+      k_loop(BoolC<true>{});
+    else
+      k_loop(BoolC<false>{});
+  } else {
     k_loop(BoolC<false>{});
+  }
   // Loads past the end may still be in flight into the ring: drain them
   // before the ring becomes epilogue scratch.
   wait_vmcnt<0>();
+  float ss_pre = 0.f;
+  if constexpr (RPX)
+    if (rp_on) ss_pre = rparts.finish(p, m0, M, sTmp);
 
-  // Row sums of squares: lanes l and l ^ 32 hold the two k halves of row
-  // l % 32 of block i (waves with wn > 0 computed the same sums).
+  // Row sums of squares (and of values): lanes l and l ^ 32 hold the two
+  // k halves of row l % 32 of block i; bf16: wave wn summed the k steps
+  // ks = wn (mod WGN), added across the waves in wn order (fp8: waves with
+  // wn > 0 computed the same sums).
   if (!sum_a) {
     if (tid < BM) sRow[tid] = ss_pre;
-  } else if (wn == 0) {
+  } else if constexpr (F8) {
+    if (wn == 0)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const float s2 = ss[i] + __shfl_xor(ss[i], 32, 64);
+        if (lane < 32) sRow[wm * WM + 32 * i + lane] = s2;
+      }
+  } else if constexpr (SUMX) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const float s2 = ss[i] + __shfl_xor(ss[i], 32, 64);
-      if (lane < 32) sRow[wm * WM + 32 * i + lane] = s2;
+      const float v2 = sv[i] + __shfl_xor(sv[i], 32, 64);
+      if (lane < 32) {
+        sPart[0][wn][wm * WM + 32 * i + lane] = s2;
+        if constexpr (LN) sPart[1][wn][wm * WM + 32 * i + lane] = v2;
+      }
+    }
+    __syncthreads();
+    if (tid < BM) {
+      float a = 0.f, c = 0.f;
+#pragma unroll
+      for (int w = 0; w < WGN; ++w) {
+        a += sPart[0][w][tid];
+        if constexpr (LN) c += sPart[1][w][tid];
+      }
+      sRow[tid] = a;
+      if constexpr (LN) sSum[tid] = c;
     }
   }
   __syncthreads();
@@ -802,14 +965,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   // hand-over outputs: the 8 lanes of a row (CH == 8: one 64-column block
   // per wave); the shuffles run in every lane
   constexpr bool HO = MODE == FVX_GEMM_PLAIN && WNO == 64;
-  const bool ho = HO && (p.ss_out || p.a8_out) && splits == 1;
+  const bool ho = HOX && HO && (p.ss_out || p.a8_out) && splits == 1;
   const EpiViews V = epi_views<MODE>(p);
   // VA: every operand is 16B-aligned and N % 8 == 0 (uniform), so every
   // chunk with columns left holds 8 and moves as whole vectors
   auto epilogue = [&](auto va) {
     const bool vec = decltype(va)::value || (vec_ok && cnt == 8);
     EpiIn col;
-    if (splits == 1) epi_load_col<MODE>(V, nn, vec, col);
+    if (splits == 1) epi_load_col<MODE, LN>(V, nn, vec, col);
     float w0[8], w1[8];  // fp8: per-output-channel weight scales
     if (F8) {
       bl_f8(make_rsrc(p.b_scale, rec_bytes(N * 4)), (uint32_t)(nn * 4), vec, w0);
@@ -863,11 +1026,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
                   if (x < cnt) dst[x] = b ? u[x] : v[x];
               }
             } else {
-              const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
-              epi_store<MODE>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo);
+              float r = 1.f, mr = 0.f;
+              if (p.rownorm) {
+                if (LN && p.ln_csum) {
+                  // LayerNorm: mean and variance from the handed-over sums
+                  const float mean = sSum[m - m0] / (float)K;
+                  const float var = fmaxf(sRow[m - m0] / (float)K - mean * mean, 0.f);
+                  r = rsqrtf(var + p.rownorm_eps);
+                  mr = mean * r;
+                } else {
+                  r = rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps);
+                }
+              }
+              epi_store<MODE, LN>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo, mr);
             }
           }
-          if (ho) epi_handoff(p, m < M && cnt > 0, ch == 0, m, nn, cnt, xo);
+          if (ho) epi_handoff(p, m < M && cnt > 0, m, nn, cnt, xo);
         }
       }
     }
@@ -936,7 +1110,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
   constexpr int BAND = 512 / NWV, LW = BAND / 8;          // DMA band rows, loads per slab
   static_assert(NWV == 4 || NWV == 8, "4 or 8 waves");
   __shared__ __align__(16) char smem[wide_lds_bytes<NWV>()];
-  __shared__ float sRow[kGwBM];
+  __shared__ float sRow[kGwBM], sTmp[64 * NWV];
   warm_kernargs<sizeof(GemmArgs) + 24>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1001,7 +1175,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
   issue(0, 0);
   // handed-over row sums: thread t < 256 takes row m0 + t (waits with slab 0)
   float ss_pre = 0.f;
-  if (!SUM_A && p.rownorm && tid < kGwBM && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
+  if (!SUM_A && p.rownorm) ss_pre = rows_parts_sum<kGwBM, 64 * NWV>(p, p.ss_in, m0, M, sTmp);
   bf16x8 af[2][RB], bfr[2][4];
   auto rd = [&](int stage, int ks, int b) {
     const char* s = smem + stage * kGwStage;
@@ -1198,7 +1372,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(GemmArgs p, int 
             epi_store<MODE>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo);
           }
           // the 8 lanes of a row's 64-column block
-          if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
+          if (ho) epi_handoff(p, m < M && cnt > 0, m, nn, cnt, xo);
         }
       }
     }
@@ -1244,7 +1418,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   constexpr int kGw8AStage = LY::A, kGw8Stage = LY::STAGE;
   static_assert(!(F8A && SUM_A), "an e4m3 A has no bf16 squares to sum");
   __shared__ __align__(16) char smem[kGw8Stages * kGw8Stage];
-  __shared__ float sRow[kGwBM];
+  __shared__ float sRow[kGwBM], sTmp[256];
   warm_kernargs<sizeof(GemmArgs) + 24>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1400,7 +1574,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
   issue(0, 0);
   issue(nk > 1 ? 1 : 0, 1);
   float ss_pre = 0.f;
-  if (!SUM_A && p.rownorm && m0 + tid < M) ss_pre = ss_in_row(p, m0 + tid);
+  if (!SUM_A && p.rownorm) ss_pre = rows_parts_sum<kGwBM, 256>(p, p.ss_in, m0, M, sTmp);
   for (int t = 0; t < nk; ++t) {
     // this wave's loads of slab t landed (slab t + 1's may still fly)
     if (F8A && wave == 0)
@@ -1503,7 +1677,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_f8_kernel(GemmArgs p, int m_
             const float r = p.rownorm ? rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps) : 1.f;
             epi_store<MODE>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo);
           }
-          if (ho) epi_handoff(p, m < M && cnt > 0, (ch & 7) == 0, m, nn, cnt, xo);
+          if (ho) epi_handoff(p, m < M && cnt > 0, m, nn, cnt, xo);
         }
       }
     }
@@ -1990,7 +2164,7 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
   const bool ho = MODE == FVX_GEMM_PLAIN && (p.ss_out || p.a8_out);
   float xo[8];
   epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in, ho, xo);
-  if (ho) epi_handoff(p, cnt > 0, ((nn / 8) & 7) == 0, m, nn, cnt, xo);
+  if (ho) epi_handoff(p, cnt > 0, m, nn, cnt, xo);
 }
 
 // ---------------------------------------------------------------------------
@@ -2089,6 +2263,21 @@ static int validate(const GemmArgs& d) {
               FVX_ERR_ARG, "gemm: ss_out needs mode PLAIN, m > 64 and ss_ld >= m");
   FVX_REQUIRE(!d.ss_in || (d.rownorm && d.ss_parts > 0 && d.ss_ld >= d.m), FVX_ERR_ARG,
               "gemm: ss_in needs rownorm, ss_parts > 0 and ss_ld >= m");
+  {
+    // the kernels address the row-sum arrays with 32-bit byte offsets
+    const int64_t parts_in = d.ss_in ? d.ss_parts : 0;
+    const int64_t parts_out = d.ss_out ? (d.n + 63) / 64 : 0;
+    const int64_t parts = parts_in > parts_out ? parts_in : parts_out;
+    FVX_REQUIRE(parts == 0 || parts * d.ss_ld < ((int64_t)1 << 29), FVX_ERR_ARG,
+                "gemm: row-sum arrays must hold fewer than 2^29 floats (parts %lld, ss_ld %lld)",
+                (long long)parts, (long long)d.ss_ld);
+  }
+  FVX_REQUIRE(!d.ln_csum || (d.mode == FVX_GEMM_PLAIN && d.rownorm && !d.ss_in && d.m > 64 &&
+                             d.split_k <= 1 && !d.b_fp8 && !d.a_scale && !d.ss_out &&
+                             !d.a8_out),
+              FVX_ERR_ARG,
+              "gemm: ln_csum needs mode PLAIN, rownorm without ss_in, m > 64, one K range, "
+              "bf16 weights and no hand-over outputs");
   FVX_REQUIRE(!d.a8_out || ((d.mode == FVX_GEMM_PLAIN || d.mode == FVX_GEMM_GEGLU) &&
                             !d.out_f32 && d.m > 64 && d.a8_out_scale &&
                             d.a8_out_ld >= d.n && d.a8_out_ld % 8 == 0 &&
@@ -2287,6 +2476,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   const int64_t tiles = ((d.m + 63) / 64) * ((d.n + bn - 1) / bn);
   const int64_t wtiles = ((d.m + 255) / 256) * ((d.n + 2 * bn - 1) / (2 * bn));
   const bool wide_ok = (!d.b_fp8 || FVX_WIDE_F8) && d.k % 64 == 0 && d.split_k <= 1 &&
+                       !d.ln_csum &&
                        (d.mode == FVX_GEMM_PLAIN || gg || d.mode == FVX_GEMM_QKV_ROPE);
   t.splits = 1;
   // PLAIN / QKV: one workgroup of 256 x 256 per CU at a time, so the tiles
@@ -2312,37 +2502,83 @@ static TilePlan plan_tile(const GemmArgs& d) {
   }
   if (gg && wtiles >= 256) t.cfg = 1;
   else t.cfg = tiles <= 256 ? 2 : 0;
-  if (d.ss_out || d.a8_out) return t;  // written by the one-pass epilogue
+  // hand-overs are written by the one-pass epilogue of 64-column waves
+  if (d.ss_out || d.a8_out) return t;
   if (FVX_SMALL_TILES && !gg && !d.b_fp8 && d.split_k == 0 && tiles < FVX_SMALL_MAX_TILES) {
     t.cfg = kSmallCfg;
     return t;
   }
+  if (d.ln_csum) return t;  // one K range
   if (d.split_k > 0) t.splits = d.split_k;
   else if (t.cfg != 1 && tiles < 128 && d.k >= 4096) t.splits = 2;
   return t;
 }
 
+// The tile kernel build for a launch: xf = the row-sum paths it needs
+// (gemm_tile_kernel's XF; bits 1 and 2 only matter for PLAIN, and a folded
+// LayerNorm hands nothing over).  fp8-weight tiles keep one build with the
+// paths but the LayerNorm.
+template <int BM, int BN, int WGM, int WGN, int ST, int MODE, bool F8, bool A16>
+static void launch_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int xf, int m_tiles,
+                        int n_tiles, int splits, int64_t kchunk, int vec_ok) {
+  auto go = [&](auto xc) {
+    constexpr int X = decltype(xc)::value;
+    hipLaunchKernelGGL((gemm_tile_kernel<BM, BN, WGM, WGN, ST, MODE, F8, A16, X>), grid,
+                       dim3(64 * WGM * WGN), 0, s, d, m_tiles, n_tiles, splits, kchunk,
+                       vec_ok);
+  };
+  if constexpr (F8) {
+    go(IntC<3>{});
+  } else if constexpr (MODE != FVX_GEMM_PLAIN) {
+    if (xf & 1) go(IntC<1>{});
+    else go(IntC<0>{});
+  } else {
+    switch (xf) {
+      case 0: go(IntC<0>{}); break;
+      case 1: go(IntC<1>{}); break;
+      case 2: go(IntC<2>{}); break;
+      case 3: go(IntC<3>{}); break;
+      default: go(IntC<4>{}); break;  // folded LayerNorm, alone
+    }
+  }
+}
+
+// bf16 256 x 256 tiles (config 1): GEGLU only (the planner's choice for
+// GeGLU projections with >= 256 wide tiles)
+template <int MODE>
+static void launch_big_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int xf, int m_tiles,
+                            int n_tiles, int splits, int64_t kchunk, int vec_ok) {
+  if constexpr (MODE == FVX_GEMM_GEGLU)
+    launch_tile<256, 256, 2, 4, 2, MODE, false, false>(grid, s, d, xf, m_tiles, n_tiles, splits,
+                                                       kchunk, vec_ok);
+}
+
 // 64 x 64 tiles (kSmallCfg): not instantiated for GEGLU, whose tiles hold
 // two weights' columns
 template <int MODE>
-static void launch_small_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int m_tiles,
+static void launch_small_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int xf, int m_tiles,
                               int n_tiles, int splits, int64_t kchunk, int vec_ok) {
   if constexpr (MODE != FVX_GEMM_GEGLU)
-    hipLaunchKernelGGL((gemm_tile_kernel<64, 64, 2, 2, 4, MODE, false, false>), grid,
-                       dim3(256), 0, s, d, m_tiles, n_tiles, splits, kchunk, vec_ok);
+    launch_tile<64, 64, 2, 2, 4, MODE, false, false>(grid, s, d, xf, m_tiles, n_tiles, splits,
+                                                     kchunk, vec_ok);
 }
 
 static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
   FVX_REQUIRE(cfg >= 0 && cfg < kTileCfgs, FVX_ERR_ARG, "gemm: bad tile config %d", cfg);
+  FVX_REQUIRE(cfg != 1 || d.mode == FVX_GEMM_GEGLU || d.b_fp8, FVX_ERR_ARG,
+              "gemm: the bf16 256 x 256 tile configuration is built for GEGLU only");
   FVX_REQUIRE(cfg != kSmallCfg || (d.mode != FVX_GEMM_GEGLU && !d.b_fp8), FVX_ERR_ARG,
               "gemm: the 64 x 64 tile configuration takes no GEGLU / fp8 weights");
+  FVX_REQUIRE(cfg != kSmallCfg || (!d.a8_out && !d.ss_out), FVX_ERR_ARG,
+              "gemm: the 64 x 64 tile configuration hands nothing over");
   const bool gg = d.mode == FVX_GEMM_GEGLU;
   const int bm = tile_bm(cfg, d.b_fp8), bn = kTileBN[cfg] / (gg ? 2 : 1);
   const int m_tiles = (int)((d.m + bm - 1) / bm);
   const int n_tiles = (int)((d.n + bn - 1) / bn);
   // hand-overs come from a one-pass epilogue, except through the reduce
   // kernel behind a split wide kernel
-  if (splits < 1 || (cfg == kWideCfg ? !wide_split_ok(d) : (d.ss_out || d.a8_out)))
+  if (splits < 1 ||
+      (cfg == kWideCfg ? !wide_split_ok(d) : (d.ss_out || d.a8_out || d.ln_csum)))
     splits = 1;
   const int64_t bk = d.b_fp8 ? 128 : 64;
   int64_t kchunk = (d.k + splits - 1) / splits;
@@ -2421,10 +2657,14 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     if (stw || splits == 1) return stw;
   } else {
     dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
+    // row-sum paths: handed-over sums read (the tile kernel's bit-0 build
+    // has no K-loop sum of squares), hand-over outputs (one-pass epilogue)
+    const int xf = ((d.rownorm && d.ss_in) ? 1 : 0) |
+                   ((splits == 1 && (d.ss_out || d.a8_out)) ? 2 : 0) |
+                   (d.ln_csum ? 4 : 0);
 #define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_)                                 \
-    hipLaunchKernelGGL((gemm_tile_kernel<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_>),  \
-                       grid, dim3(64 * WGM_ * WGN_), 0, s, d, m_tiles, n_tiles, splits, \
-                       kchunk, vec_ok)
+    launch_tile<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_>(grid, s, d, xf, m_tiles,    \
+                                                           n_tiles, splits, kchunk, vec_ok)
     // fp8 tiles hold 128-k slabs (bf16 A rows of 256 bytes): config 1 becomes
     // 128 x 256 to stay within the LDS
 #define LCFG8(MODE, A16_)                                                             \
@@ -2437,10 +2677,11 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     } else if (d.b_fp8) {                                                             \
       LCFG8(MODE, true)                                                               \
     } else {                                                                          \
-      if (cfg == 1) LT(256, 256, 2, 4, 2, MODE, false, false);                        \
+      if (cfg == 1)                                                                   \
+        launch_big_tile<MODE>(grid, s, d, xf, m_tiles, n_tiles, splits, kchunk, vec_ok); \
       else if (cfg == 2) LT(64, 128, 2, 2, 4, MODE, false, false);                    \
       else if (cfg == kSmallCfg)                                                      \
-        launch_small_tile<MODE>(grid, s, d, m_tiles, n_tiles, splits, kchunk, vec_ok); \
+        launch_small_tile<MODE>(grid, s, d, xf, m_tiles, n_tiles, splits, kchunk, vec_ok); \
       else LT(64, 128, 2, 2, 3, MODE, false, false);                                  \
     }
     FVX_MODE_DISPATCH(d.mode, LCFG)

@@ -385,11 +385,14 @@ def _set_a8(d, a8=None, a8_out=None):
         d.a8_scale, d.a8_sld = a8.scale.data_ptr(), a8.scale.stride(0)
 
 
-def _set_ss(d, rownorm_eps, ss_in=None, ss_out=None):
+def _set_ss(d, rownorm_eps, ss_in=None, ss_out=None, ln_csum=None):
     """Row sums of squares handed between GEMMs: ``ss_out`` (fp32 [parts,
     ld], parts = ss_parts(n)) receives the producer's per-block sums of its
     squared bf16 outputs; ``ss_in`` (same layout, from the GEMM that wrote
-    this GEMM's A) replaces the fused RMSNorm's pass over A."""
+    this GEMM's A) replaces the fused RMSNorm's pass over A.  ``ln_csum``
+    (fp32 [N], the weight's column sums): the fused norm is a LayerNorm on
+    row sums of A's values and squares taken in the K loop
+    (fvx_gemm_desc.ln_csum)."""
     if rownorm_eps is not None:
         d.rownorm, d.rownorm_eps = 1, float(rownorm_eps)
     if ss_in is not None:
@@ -404,18 +407,27 @@ def _set_ss(d, rownorm_eps, ss_in=None, ss_out=None):
         if (ss_out.dim() != 2 or ss_out.stride(1) != 1 or ss_out.shape[1] < d.m or
                 ss_out.shape[0] < ss_parts(d.n)):
             raise ValueError(f'ss_out must be [>= {ss_parts(d.n)}, >= m] with unit row stride')
+        if ss_in is not None and ss_out.stride(0) != d.ss_ld:
+            raise ValueError('ss_in and ss_out need the same row stride (one ss_ld)')
         d.ss_out, d.ss_ld = ss_out.data_ptr(), ss_out.stride(0)
+    if ln_csum is not None:
+        _check(ln_csum, 'ln_csum', dtype=torch.float32)
+        if ln_csum.numel() < d.n or rownorm_eps is None or ss_in is not None:
+            raise ValueError('ln_csum needs N values and rownorm_eps, and takes no ss_in')
+        d.ln_csum = ln_csum.data_ptr()
 
 
 def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
          gate=None, gate_group=1, pos=None, pos_period=0, act=_lib.ACT_NONE,
          rownorm_eps=None, out_f32=False, row_group=0, row_group_stride=0,
          split_k=0, c_frag=None, ss_in=None, ss_out=None, a8=None, a8_out=None,
-         noalloc=False, rtc_lock=None, rtc_period=0, bias_f32_locked=None):
+         noalloc=False, rtc_lock=None, rtc_period=0, bias_f32_locked=None,
+         ln_csum=None):
     """out = epilogue(a @ weight^T); see fvx_gemm_desc for the order.
     ``a`` may be a FragA and ``weight`` a FragB; ``c_frag`` (a FragA with
     k == n) also receives the output in the fragment-major layout;
-    ``ss_in`` / ``ss_out``: see _set_ss; ``a8`` / ``a8_out``: see Fp8Act.
+    ``ss_in`` / ``ss_out`` / ``ln_csum``: see _set_ss; ``a8`` / ``a8_out``:
+    see Fp8Act.
     ``noalloc``: run through fvx_gemm_noalloc (split-K scratch in the
     library's static device array, no workspace).  ``rtc_lock`` (device
     int32 [1]), ``rtc_period``, ``bias_f32_locked``: rows with
@@ -449,7 +461,7 @@ def gemm(a, weight, out=None, *, bias=None, bias_f32=None, residual=None,
         d.pos, d.pos_period = pos.data_ptr(), pos_period or pos.shape[0]
     d.act, d.mode, d.out_f32 = int(act), _lib.GEMM_PLAIN, int(bool(out_f32))
     _set_rtc(d, rtc_lock, rtc_period, bias_f32_locked)
-    _set_ss(d, rownorm_eps, ss_in, ss_out)
+    _set_ss(d, rownorm_eps, ss_in, ss_out, ln_csum)
     _set_a8(d, a8, a8_out)
     d.row_group, d.row_group_stride = row_group, row_group_stride
     d.split_k = split_k

@@ -274,6 +274,9 @@ class PI0Inference:
         # (A scaled by 1 + scale as it is loaded, the shift as a bias, the
         # gate read from the style row by the residual epilogues)
         self.fold_adarms = True
+        # SigLIP: the LayerNorms run inside the GEMMs after them (Q|K|V,
+        # fc1, the projector), on row sums taken in their K loops
+        self.fold_layernorm = True
         # predict_action ends with the attention merge status check (it
         # waits for the chunk); off, callers run kernels.attention_check
         self.check_merge = True
@@ -361,7 +364,25 @@ class PI0Inference:
                                  cfg.head_dim, cfg.rope_theta, device=dev)
         self._prepare_frag_weights()
         self._prepare_adarms_fold()
+        self._prepare_layernorm_fold()
         torch.cuda.synchronize(dev)
+
+    def _prepare_layernorm_fold(self):
+        """SigLIP's LayerNorms folded into the GEMMs after them: with g / beta
+        the norm's gain / shift, LN(x) @ W^T + b = rstd * (x @ (W g)^T -
+        mean * csum) + (b + W beta), csum[n] = sum_k (W g)[n, k] taken from
+        the bf16 weights the MFMAs multiply (fvx_gemm_desc.ln_csum); mean
+        and rstd come from row sums of x the GEMM takes in its K loop."""
+        def fold(w, bias, g, beta):
+            wg = (w.float() * g.float()[None]).to(BF16)
+            return {'w': wg, 'csum': wg.float().sum(1).contiguous(),
+                    'b': (bias.float() + w.float() @ beta.float()).contiguous()}
+        V = self.vis
+        self.vis_ln = [{'qkv': fold(L['qkv_w'], L['qkv_b'], L['ln1_w'], L['ln1_b']),
+                        'fc1': fold(L['fc1_w'], L['fc1_b'], L['ln2_w'], L['ln2_b'])}
+                       for L in V['layers']]
+        self.proj_ln = fold(self.proj['w'], self.proj['b'], V['post_ln_w'],
+                            V['post_ln_b'])
 
     def _prepare_adarms_fold(self):
         """Per (step, layer) fp32 biases shift @ W^T of the folded adaptive
@@ -566,6 +587,26 @@ class PI0Inference:
         imgs = b['images'].view(nimg, 3, cfg.image_size, cfg.image_size)
         K.im2col_patches(imgs, cfg.patch, cfg.patch_k_pad, out=b['patches'])
         x, xn = b['vis_x'], b['vis_xn']
+        n_img_tok = cfg.n_views * cfg.num_patches
+        pre = b['pre_x'].view(-1, cfg.llm_hidden)
+        if self.fold_layernorm:
+            # every LayerNorm inside the next GEMM, on row sums of x taken in
+            # that GEMM's K loop
+            ln = lambda f: {'rownorm_eps': cfg.vit_eps, 'ln_csum': f['csum'],  # noqa
+                            'bias_f32': f['b']}
+            K.gemm(b['patches'], V['patch_w'], out=x, bias=V['patch_b'],
+                   pos=V['pos_emb'], pos_period=cfg.num_patches)
+            for L, F in zip(V['layers'], self.vis_ln):
+                K.gemm(x, F['qkv']['w'], out=b['vis_qkv'], **ln(F['qkv']))
+                K.mha_packed_qkv(b['vis_qkv'], b['vis_ctx'], nimg,
+                                 cfg.num_patches, cfg.vit_heads, cfg.vit_head_dim)
+                K.gemm(b['vis_ctx'], L['o_w'], out=x, bias=L['o_b'], residual=x)
+                K.gemm(x, F['fc1']['w'], out=b['vis_h'], act=ACT_GELU_TANH,
+                       **ln(F['fc1']))
+                K.gemm(b['vis_h'], L['fc2_w'], out=x, bias=L['fc2_b'], residual=x)
+            K.gemm(x, self.proj_ln['w'], out=pre, row_group=n_img_tok,
+                   row_group_stride=cfg.prefix_len, **ln(self.proj_ln))
+            return
         K.gemm(b['patches'], V['patch_w'], out=x, bias=V['patch_b'],
                pos=V['pos_emb'], pos_period=cfg.num_patches)
         for L in V['layers']:
@@ -579,9 +620,7 @@ class PI0Inference:
                    act=ACT_GELU_TANH)
             K.gemm(b['vis_h'], L['fc2_w'], out=x, bias=L['fc2_b'], residual=x)
         K.layer_norm(x, V['post_ln_w'], V['post_ln_b'], cfg.vit_eps, out=xn)
-        n_img_tok = cfg.n_views * cfg.num_patches
-        K.gemm(xn, self.proj['w'], out=b['pre_x'].view(-1, cfg.llm_hidden),
-               bias=self.proj['b'], row_group=n_img_tok,
+        K.gemm(xn, self.proj['w'], out=pre, bias=self.proj['b'], row_group=n_img_tok,
                row_group_stride=cfg.prefix_len)
 
     def transformer_encoder(self, b, B):

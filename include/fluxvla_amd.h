@@ -212,6 +212,18 @@ typedef struct fvx_gemm_desc {
    * weights only; NULL: unused. */
   const void* a_scale;
   const float* bias2_f32;          /* [N] fp32, GEGLU up half */
+  /* LayerNorm folded into the GEMM (no counterpart in the reference; it
+   * replaces the LayerNorm launches in front of SigLIP's Q|K|V, fc1 and the
+   * projector, siglip_vit.py via HF SiglipEncoderLayer).  With ln_csum
+   * ([N] fp32) a rownorm GEMM sums A's values (sum_m) and squares (ss_m)
+   * per row in its K loop and computes, before bias and activation,
+   *   v = (acc - mean_m * ln_csum[n]) * rsqrt(var_m + rownorm_eps),
+   *   mean_m = sum_m / K,  var_m = max(ss_m / K - mean_m^2, 0),
+   * which is LayerNorm(A) @ B^T when B is the layer's weight scaled by the
+   * norm's gain along k and ln_csum[n] = sum_k B[n][k] (the norm's shift
+   * enters as bias_f32).  PLAIN, M > 64, one K range (the tile kernel),
+   * bf16 weights, no ss_in, no hand-over outputs; NULL: unused. */
+  const float* ln_csum;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */

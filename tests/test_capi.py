@@ -95,6 +95,25 @@ def test_gemm_rejects_periods_past_32_bits():
         assert '2^31' in _err(lib)
 
 
+def test_gemm_rejects_bad_layernorm_fold():
+    # ln_csum: PLAIN, rownorm, M > 64, sums taken in the K loop (no ss_in),
+    # bf16 weights, one K range, nothing handed over
+    lib = _lib.load()
+
+    def desc(**kw):
+        d = _lib.GemmDesc()
+        d.a, d.b, d.c = 4096, 8192, 16384
+        d.m, d.n, d.k, d.lda, d.ldb, d.ldc = 128, 64, 64, 64, 64, 64
+        d.rownorm, d.rownorm_eps, d.ln_csum = 1, 1e-6, 32768
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return d
+    for kw in ({'rownorm': 0}, {'m': 64, 'ldc': 64}, {'ss_in': 65536, 'ss_parts': 1, 'ss_ld': 128},
+               {'ss_out': 65536, 'ss_ld': 128}, {'split_k': 2}, {'mode': _lib.GEMM_QKV_ROPE}):
+        assert lib.fvx_gemm(ctypes.byref(desc(**kw)), None) == _lib.FVX_ERR_ARG, kw
+        assert 'ln_csum' in _err(lib), kw
+
+
 def test_gemm_explicit_split_without_workspace_is_an_error():
     lib = _lib.load()
     d = _lib.GemmDesc()

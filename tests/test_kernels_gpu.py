@@ -258,6 +258,50 @@ def test_gemm_pos_rowgroup_f32(K, cuda):
     assert big.view(3, 300, n)[:, 256:].abs().max().item() == 0.0
 
 
+@pytest.mark.parametrize('m,n,act,rg', [
+    (768, 3456, 'none', 0),      # SigLIP Q|K|V (64 x 128 tiles)
+    (1024, 4304, 'gelu', 0),     # fc1, tanh GELU
+    (130, 1152, 'none', 0),      # ragged rows, 64 x 64 tiles
+    (768, 2048, 'none', 256),    # projector: rows [256 g + r] -> [300 g + r]
+])
+def test_gemm_layernorm_fold(K, cuda, m, n, act, rg):
+    """LayerNorm folded into the following GEMM: the GEMM sums its A rows'
+    values and squares in the K loop and computes LayerNorm(x) @ W^T + b
+    with W scaled by the norm's gain, the weight's column sums and the
+    shift folded into an fp32 bias.  x has a mean offset (0.3) so the mean
+    term matters.  Reference: torch fp32 layer_norm of the same bf16 x, then
+    the fp32 GEMM with the unfolded weight (and tanh GELU)."""
+    announce(f'gemm layernorm fold m={m} n={n} act={act} row_group={rg}')
+    from fluxvla_amd._lib import ACT_GELU_TANH, ACT_NONE
+    h = 1152
+    x = randn((m, h), 62, mean=0.3)
+    g = randn((h,), 63, std=0.2, mean=1.0)
+    beta = randn((h,), 64, std=0.2)
+    w = randn((n, h), 65, std=0.03)
+    b = randn((n,), 66, std=0.2)
+    wf = (w.float() * g.float()).bfloat16()
+    csum = wf.float().sum(1)
+    bf = b.float() + w.float() @ beta.float()
+    ref = F.layer_norm(x.float(), (h,), g.float(), beta.float(), eps=1e-6) @ w.float().t() + b.float()
+    if act == 'gelu':
+        ref = F.gelu(ref, approximate='tanh')
+    kw = dict(rownorm_eps=1e-6, ln_csum=csum.to(cuda), bias_f32=bf.to(cuda),
+              act=ACT_GELU_TANH if act == 'gelu' else ACT_NONE)
+    xc = x.to(cuda)
+    if rg:
+        groups = m // rg
+        big = torch.zeros(groups * 300, n, dtype=torch.bfloat16, device=cuda)
+        K.gemm(xc, wf.to(cuda), out=big, row_group=rg, row_group_stride=300, **kw)
+        got = big.view(groups, 300, n)[:, :rg].reshape(m, n)
+        assert big.view(groups, 300, n)[:, rg:].abs().max().item() == 0.0
+    else:
+        got = K.gemm(xc, wf.to(cuda), **kw)
+    assert rel_err(got, ref) <= REL_TOL
+    # repeatable bit for bit (fixed summation order)
+    if not rg:
+        assert torch.equal(got, K.gemm(xc, wf.to(cuda), **kw))
+
+
 @pytest.mark.parametrize('m,n,k', [(51, 4096, 1024), (816, 16384, 2048),
                                    (100, 4096, 1024)])
 def test_gemm_geglu_rownorm(K, cuda, m, n, k):
