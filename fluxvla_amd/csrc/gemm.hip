@@ -690,11 +690,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   const int nk = (int)((ke - kb + BK - 1) / BK);
 
   // Buffer views of the tile's A rows and B rows: rows past M / N read zero.
+  // Grouped A rows (a_row_group > 0): a view of the whole of A, each row's
+  // offset from its group, rows past M kept out by kmax.
   const int64_t a_rows = (M - m0 < BM) ? M - m0 : BM;
   const int64_t b_rows = (N - n0 < BN / NB) ? N - n0 : BN / NB;
   const uint32_t lda2 = (uint32_t)p.lda * 2, ldb2 = (uint32_t)p.ldb * (F8 ? 1 : 2);
+  const bool agrp = p.a_row_group > 0;
+  auto a_phys = [&](int64_t m) -> int64_t {  // physical row of product row m
+    const uint32_t q = udiv32(m, p.a_row_group);
+    return (int64_t)q * p.a_row_group_stride + ((uint32_t)m - q * (uint32_t)p.a_row_group);
+  };
   const i32x4_t rA =
-      make_rsrc4((const bf16_t*)p.a + m0 * p.lda, (uint32_t)(a_rows * lda2));
+      agrp ? make_rsrc4((const bf16_t*)p.a, (uint32_t)((a_phys(M - 1) + 1) * lda2))
+           : make_rsrc4((const bf16_t*)p.a + m0 * p.lda, (uint32_t)(a_rows * lda2));
   const i32x4_t rB0 =
       make_rsrc4((const char*)p.b + n0 * ldb2, (uint32_t)(b_rows * ldb2));
   const i32x4_t rB1 =
@@ -717,9 +725,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
     isa[i] = R0 < AROWS;
     if (R0 < AROWS) {
       const int hk = R0 / BM;  // F8: which 64-k half of the slab
+      const int ar = R0 % BM + lr;
       rsel[i] = rA;
-      voff[i] = (uint32_t)(R0 % BM + lr) * lda2 + (uint32_t)(kb + hk * 64 + gc * 8) * 2;
-      kmax[i] = (int)(ke - kb) - hk * 64 - gc * 8;
+      voff[i] = (uint32_t)(agrp ? a_phys(m0 + ar) : ar) * lda2 +
+                (uint32_t)(kb + hk * 64 + gc * 8) * 2;
+      kmax[i] = (agrp && m0 + ar >= M) ? 0 : (int)(ke - kb) - hk * 64 - gc * 8;
     } else {
       // 8-row groups never straddle the two weights' regions (BN / NB % 8 == 0)
       const int br0 = R0 - AROWS;
@@ -2229,8 +2239,11 @@ static SkinnyPlan plan_skinny(const GemmArgs& d) {
 
 // The skinny kernel serves M <= 64 while its arrival counters fit the
 // counter area and its partial offsets fit 31 bits; anything else is tiled.
+// A's rows in groups with gaps between them (fvx_gemm_desc.a_row_group)
+static bool a_grouped(const GemmArgs& d) { return d.a_row_group > 0 && d.m > d.a_row_group; }
+
 static bool use_skinny(const GemmArgs& d) {
-  if (d.m > 64) return false;
+  if (d.m > 64 || a_grouped(d)) return false;
   if (d.b_fp8 && !d.b_frag) return false;  // fp8 skinny reads fragment-major B
   const SkinnyPlan s = plan_skinny(d);
   // operand byte offsets are 32-bit
@@ -2271,6 +2284,17 @@ static int validate(const GemmArgs& d) {
     FVX_REQUIRE(parts == 0 || parts * d.ss_ld < ((int64_t)1 << 29), FVX_ERR_ARG,
                 "gemm: row-sum arrays must hold fewer than 2^29 floats (parts %lld, ss_ld %lld)",
                 (long long)parts, (long long)d.ss_ld);
+  }
+  FVX_REQUIRE(d.a_row_group >= 0 && d.a_row_group < ((int64_t)1 << 31) &&
+                  (d.a_row_group == 0 ||
+                   (d.a_row_group_stride >= d.a_row_group &&
+                    d.a_row_group_stride < ((int64_t)1 << 31))),
+              FVX_ERR_SHAPE, "gemm: need 0 <= a_row_group <= a_row_group_stride < 2^31");
+  if (a_grouped(d)) {
+    const int64_t last = (d.m - 1) / d.a_row_group * d.a_row_group_stride +
+                         (d.m - 1) % d.a_row_group;
+    FVX_REQUIRE(!d.a_frag && !d.a8 && (last + 1) * d.lda * 2 < ((int64_t)1 << 31), FVX_ERR_ARG,
+                "gemm: grouped A rows take a row-major bf16 A below 2 GiB");
   }
   FVX_REQUIRE(!d.ln_csum || (d.mode == FVX_GEMM_PLAIN && d.rownorm && !d.ss_in && d.m > 64 &&
                              d.split_k <= 1 && !d.b_fp8 && !d.a_scale && !d.ss_out &&
@@ -2476,7 +2500,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   const int64_t tiles = ((d.m + 63) / 64) * ((d.n + bn - 1) / bn);
   const int64_t wtiles = ((d.m + 255) / 256) * ((d.n + 2 * bn - 1) / (2 * bn));
   const bool wide_ok = (!d.b_fp8 || FVX_WIDE_F8) && d.k % 64 == 0 && d.split_k <= 1 &&
-                       !d.ln_csum &&
+                       !d.ln_csum && !a_grouped(d) &&
                        (d.mode == FVX_GEMM_PLAIN || gg || d.mode == FVX_GEMM_QKV_ROPE);
   t.splits = 1;
   // PLAIN / QKV: one workgroup of 256 x 256 per CU at a time, so the tiles

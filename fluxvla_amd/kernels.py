@@ -60,13 +60,33 @@ def _check(t, name, dtype=BF16, contiguous=True, allow_none=False):
 
 
 def _rows_ld(t, name):
-    """(rows, leading dim) of a 2-D view with unit column stride."""
+    """(rows, leading dim) of a 2-D view with unit column stride (a tensor
+    of more dims must be viewable as its rows: evenly spaced)."""
     if t.dim() < 2:
         raise ValueError(f'{name} must be at least 2-D')
     if t.stride(-1) != 1:
         raise ValueError(f'{name} must have unit stride in its last dim')
-    t2 = t if t.dim() == 2 else t.reshape(-1, t.shape[-1])
+    if t.dim() == 2:
+        return t.shape[0], t.stride(0)
+    try:
+        t2 = t.view(-1, t.shape[-1])
+    except RuntimeError as e:
+        raise ValueError(f'{name}: rows are not evenly spaced ({e})') from None
     return t2.shape[0], t2.stride(0)
+
+
+def _grouped_rows(a):
+    """A 3-D ``a`` [groups, rows, k] whose groups are further apart than
+    their rows (the action rows behind each sample's state row): (rows,
+    group stride in rows) for fvx_gemm_desc.a_row_group, else None."""
+    if a.dim() != 3 or a.shape[0] < 2 or a.shape[1] < 1 or a.stride(-1) != 1:
+        return None
+    g, rs = a.shape[1], a.stride(1)
+    if a.stride(0) == g * rs:
+        return None
+    if rs < a.shape[2] or a.stride(0) % rs or a.stride(0) < g * rs:
+        raise ValueError('a: groups of rows must be whole rows apart')
+    return g, a.stride(0) // rs
 
 
 # ---------------------------------------------------------------------------
@@ -299,7 +319,12 @@ def _gemm_desc(a, w):
         d.a, d.a_frag, dev = a.buf.data_ptr(), 1, a.buf.device
     else:
         _check(a, 'a', contiguous=False)
-        m, lda = _rows_ld(a, 'a')
+        grp = _grouped_rows(a)
+        if grp is not None:
+            m, lda = a.shape[0] * a.shape[1], a.stride(1)
+            d.a_row_group, d.a_row_group_stride = grp
+        else:
+            m, lda = _rows_ld(a, 'a')
         k = a.shape[-1]
         d.a, dev = a.data_ptr(), a.device
     if isinstance(w, FragB):

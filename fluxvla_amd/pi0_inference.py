@@ -861,39 +861,40 @@ class PI0Inference:
                     self._expert_layer_pi05(b, B, i, L, step, rtc)
                 else:
                     self._expert_layer_pi0(b, B, i, L)
+            # one Euler GEMM for the batch: the action rows of every sample
+            # (behind its state row for PI0: A's rows in groups of na)
             lead = Ss - na
-            for s in range(B):
-                a = x3[s, lead:]
-                if fused:
-                    K.gemm_euler(a, self.act_out_f, self.act_out['b'],
-                                 b['xt'][s], self.dt, xt_bf16=b['xt_bf16'][s],
-                                 rownorm_eps=cfg.rms_eps,
-                                 bias_f32=self.fold_out[step],
-                                 a_scale=self.styles[step, -1, :hid],
-                                 **self._euler_rtc(b, s, step, rtc))
-                    continue
-                if cfg.pi05:
-                    xn = b['ex_xn'][s, lead:]
-                    st = self.styles[step, -1:]
-                    lk = ({'style_locked': self.styles0[-1],
-                           'lock': b['rtc_lock'], 'lock_period': na}
-                          if rtc == 'prefix' else {})
-                    K.adarms_norm(a, st, out=xn, eps=cfg.rms_eps, **lk)
-                    a, rn = xn, None
-                else:
-                    rn = cfg.rms_eps
-                K.gemm_euler(a, self.act_out_f, self.act_out['b'],
-                             b['xt'][s], self.dt, xt_bf16=b['xt_bf16'][s],
-                             rownorm_eps=rn, **self._euler_rtc(b, s, step, rtc))
+            a = x3[:, lead:]
+            xt, xtb = b['xt'].view(B * na, -1), b['xt_bf16'].view(B * na, -1)
+            w_out = self.act_out_f if fr else self.act_out['w']
+            if fused:
+                K.gemm_euler(a, w_out, self.act_out['b'], xt, self.dt, xt_bf16=xtb,
+                             rownorm_eps=cfg.rms_eps, bias_f32=self.fold_out[step],
+                             a_scale=self.styles[step, -1, :hid],
+                             **self._euler_rtc(b, B, step, rtc))
+                continue
+            if cfg.pi05:
+                xn = b['ex_xn'][:, lead:]
+                st = self.styles[step, -1:]
+                lk = ({'style_locked': self.styles0[-1],
+                       'lock': b['rtc_lock'], 'lock_period': na}
+                      if rtc == 'prefix' else {})
+                K.adarms_norm(a, st, out=xn, eps=cfg.rms_eps, **lk)
+                a, rn = xn, None
+            else:
+                rn = cfg.rms_eps
+            K.gemm_euler(a, w_out, self.act_out['b'], xt, self.dt, xt_bf16=xtb,
+                         rownorm_eps=rn, **self._euler_rtc(b, B, step, rtc))
 
-    def _euler_rtc(self, b, s, step, rtc):
-        """Real-time chunking arguments of sample s's Euler GEMM."""
+    def _euler_rtc(self, b, B, step, rtc):
+        """Real-time chunking arguments of the batch's Euler GEMM (row m is
+        action step m % n_action_steps of its sample)."""
         na = self.cfg.n_action_steps
+        prev = b['rtc_prev'].view(B * na, -1)
         if rtc == 'prefix':
-            return {'rtc_lock': b['rtc_lock'], 'rtc_period': na,
-                    'rtc_prev': b['rtc_prev'][s]}
+            return {'rtc_lock': b['rtc_lock'], 'rtc_period': na, 'rtc_prev': prev}
         if rtc == 'guidance':
-            return {'rtc_period': na, 'rtc_prev': b['rtc_prev'][s],
+            return {'rtc_period': na, 'rtc_prev': prev,
                     'rtc_cw': b['rtc_cw'][step],
                     'rtc_omt': self._rtc_omt[step]}
         return {}

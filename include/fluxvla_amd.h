@@ -224,6 +224,15 @@ typedef struct fvx_gemm_desc {
    * enters as bias_f32).  PLAIN, M > 64, one K range (the tile kernel),
    * bf16 weights, no ss_in, no hand-over outputs; NULL: unused. */
   const float* ln_csum;
+  /* A's rows in groups (no counterpart in the reference; one launch for the
+   * action rows of a whole batch, which sit behind each sample's state row
+   * in the suffix stream): with a_row_group > 0, row m of the product reads
+   * row (m / a_row_group) * a_row_group_stride + m % a_row_group of a, rows
+   * lda elements apart (a_row_group_stride >= a_row_group, both < 2^31).
+   * A call with m > a_row_group takes the tile kernel (not with a_frag or
+   * a8); 0: rows m of a. */
+  int64_t a_row_group;
+  int64_t a_row_group_stride;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */

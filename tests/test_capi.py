@@ -167,3 +167,40 @@ def test_python_layer_raises_value_error_on_status():
         d.a, d.b, d.c = 4096, 8192, 16384
         d.m, d.n, d.k, d.lda, d.ldb, d.ldc = 4, 4, 12, 12, 12, 4
         _lib.call('fvx_gemm', ctypes.byref(d), None)
+
+
+def test_gemm_rejects_bad_row_groups():
+    # a_row_group: 0 <= group <= stride < 2^31; grouped rows (m > group)
+    # take a row-major bf16 A (no fragment-major A, no e4m3 A)
+    lib = _lib.load()
+
+    def desc(**kw):
+        d = _lib.GemmDesc()
+        d.a, d.b, d.c = 4096, 8192, 16384
+        d.m, d.n, d.k, d.lda, d.ldb, d.ldc = 100, 64, 64, 64, 64, 64
+        d.a_row_group, d.a_row_group_stride = 50, 51
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return d
+    for kw in ({'a_row_group': -1}, {'a_row_group_stride': 49}, {'a_row_group_stride': 1 << 31}):
+        assert lib.fvx_gemm(ctypes.byref(desc(**kw)), None) == _lib.FVX_ERR_SHAPE, kw
+        assert 'a_row_group' in _err(lib), kw
+    assert lib.fvx_gemm(ctypes.byref(desc(a_frag=1)), None) == _lib.FVX_ERR_ARG
+    assert 'grouped A rows' in _err(lib)
+
+
+def test_grouped_rows_views():
+    # the Python layer reads a 3-D A with gaps between its groups as
+    # grouped rows, and refuses other unevenly spaced views
+    import torch
+
+    from fluxvla_amd import kernels as K
+    buf = torch.zeros(4, 51, 64)
+    assert K._grouped_rows(buf[:, 1:]) == (50, 51)
+    assert K._grouped_rows(buf[:, :]) is None
+    assert K._grouped_rows(buf[:1, 1:]) is None
+    with pytest.raises(ValueError):
+        K._rows_ld(buf[:, 1:], 'x')
+    assert K._rows_ld(buf[:1, 1:], 'x') == (50, 64)
+    with pytest.raises(ValueError):
+        K._grouped_rows(buf[:, 1:, :32].transpose(0, 1))

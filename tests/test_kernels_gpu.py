@@ -393,6 +393,44 @@ def test_gemm_euler(K, cuda, m):
     assert torch.equal(xtb.cpu(), xt.cpu().bfloat16())
 
 
+@pytest.mark.parametrize('groups,rows,stride', [(8, 50, 51), (2, 25, 51), (3, 50, 64),
+                                                (32, 50, 51)])
+def test_gemm_grouped_a_rows(K, cuda, groups, rows, stride):
+    """A read in row groups with gaps between them (the action rows behind
+    each sample's state row: fvx_gemm_desc.a_row_group), as a 3-D view
+    [groups, rows, k] of a taller buffer.  The Euler GEMM over the batch
+    against the same GEMM on the gathered rows, bit for bit (same
+    products, same tile order), and against an fp32 reference; a PLAIN
+    GEMM with bias on the same view; the gap rows are never read (NaN)."""
+    announce(f'gemm grouped A rows {groups}x{rows} stride {stride}')
+    k, n = 1024, 32
+    buf = randn((groups, stride, k), 74, std=2.0)
+    buf[:, :stride - rows] = float('nan')
+    xg = buf.to(cuda)[:, stride - rows:]
+    x = xg.contiguous()
+    w = randn((n, k), 75, std=0.02).to(cuda)
+    b = randn((n,), 76, std=0.1).to(cuda)
+    m = groups * rows
+    xt0 = torch.randn(m, n, generator=gen(77))
+    outs = []
+    for a in (xg, x):
+        xt = xt0.clone().to(cuda)
+        xtb = torch.empty(m, n, dtype=torch.bfloat16, device=cuda)
+        K.gemm_euler(a, w, b, xt, -0.1, xt_bf16=xtb, rownorm_eps=1e-6)
+        outs.append((xt.cpu(), xtb.cpu()))
+    if m > 64:  # both take the tile kernel (m <= 64 ungrouped: the skinny one)
+        assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    xf = x.view(m, k).float().cpu()
+    v = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)) @ w.float().cpu().t() \
+        + b.float().cpu()
+    assert (outs[0][0] - (xt0 - 0.1 * v)).abs().max().item() <= 2e-3
+    got = K.gemm(xg, w, bias=b)
+    assert got.shape == (groups, rows, n)
+    if m > 64:
+        assert torch.equal(got, K.gemm(x, w, bias=b))
+    assert rel_err(got.view(m, n), xf @ w.float().cpu().t() + b.float().cpu()) <= REL_TOL
+
+
 # ---------------------------------------------------------------------------
 # Attention
 # ---------------------------------------------------------------------------
