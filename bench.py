@@ -532,9 +532,10 @@ def _json_line(path):
 # one eager call + 3 warm-up + the timed graph replays, per operand set
 _E, _MP, _MV = 18 * 9, 17 * 9, 27 * 9
 TABLE_DISPATCHES = (
-    ('rms_norm_residual_kernel (C1)', [('rms_norm_residual_kernel', 256, 32 * 14)]),
+    # C1: 2048-column rows take one 4-wave workgroup each
+    ('rms_norm_residual_kernel (C1)', [('rms_norm_residual_kernel', 1024, 32 * 14)]),
     ('rms_norm_residual_kernel (C1, cache-resident)',
-     [('rms_norm_residual_kernel', 256, 32 * 24)]),
+     [('rms_norm_residual_kernel', 1024, 32 * 24)]),
     ('copy_rows_kernel, same bytes (C1 floor: an 8.4 MB -> 8.4 MB copy)',
      [('copy_rows_kernel', 2048, 32 * 14)]),
     ('gemm_skinny_kernel<QKV_ROPE> (expert)', [('gemm_skinny_kernel<2', 160, _E)]),

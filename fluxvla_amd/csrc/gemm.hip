@@ -2464,6 +2464,15 @@ constexpr int kSmallCfg = 4;
 #ifndef FVX_SMALL_TILES
 #define FVX_SMALL_TILES 1
 #endif
+#ifndef FVX_SMALL_STAGES
+#define FVX_SMALL_STAGES 4
+#endif
+#ifndef FVX_SMALL_SPLIT
+#define FVX_SMALL_SPLIT 1
+#endif
+#ifndef FVX_SMALL_SPLIT_MIN_K
+#define FVX_SMALL_SPLIT_MIN_K 4096
+#endif
 #ifndef FVX_SMALL_MAX_TILES
 #define FVX_SMALL_MAX_TILES 128
 #endif
@@ -2530,6 +2539,8 @@ static TilePlan plan_tile(const GemmArgs& d) {
   if (d.ss_out || d.a8_out) return t;
   if (FVX_SMALL_TILES && !gg && !d.b_fp8 && d.split_k == 0 && tiles < FVX_SMALL_MAX_TILES) {
     t.cfg = kSmallCfg;
+    if (FVX_SMALL_SPLIT > 1 && d.k >= FVX_SMALL_SPLIT_MIN_K && !d.ln_csum)
+      t.splits = FVX_SMALL_SPLIT;
     return t;
   }
   if (d.ln_csum) return t;  // one K range
@@ -2583,8 +2594,8 @@ template <int MODE>
 static void launch_small_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int xf, int m_tiles,
                               int n_tiles, int splits, int64_t kchunk, int vec_ok) {
   if constexpr (MODE != FVX_GEMM_GEGLU)
-    launch_tile<64, 64, 2, 2, 4, MODE, false, false>(grid, s, d, xf, m_tiles, n_tiles, splits,
-                                                     kchunk, vec_ok);
+    launch_tile<64, 64, 2, 2, FVX_SMALL_STAGES, MODE, false, false>(
+        grid, s, d, xf, m_tiles, n_tiles, splits, kchunk, vec_ok);
 }
 
 static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {

@@ -107,6 +107,32 @@ def test_padded_prompt_and_missing_view(models, cuda):
     assert err <= CHUNK_ATOL
 
 
+def test_layernorm_fold_chunk_matches_oracle(cuda):
+    """The opt-in SigLIP LayerNorm fold (fold_layernorm: the norms inside the
+    Q|K|V, fc1 and projector GEMMs) keeps the chunk within the bar, and
+    within 2e-2 of the unfolded chunk."""
+    announce('pi0 chunk with the SigLIP LayerNorm fold')
+    from fluxvla_amd.pi0_inference import PI0Inference
+    cfg = tiny()
+    sd = make_state_dict(cfg, seed=9)
+    inp = make_inputs(cfg, batch=1, seed=10)
+    ref = O.predict_action(sd, cfg, inp['images'], inp['lang_tokens'],
+                           inp['states'], inp['img_masks'], inp['lang_masks'],
+                           inp['noise'])
+    m = PI0Inference(cfg, sd, device='cuda', max_batch=1)
+    outs = []
+    for fold in (False, True):
+        m.fold_layernorm = fold
+        m._graphs.clear()
+        outs.append(m.predict_action(inp['images'].to(cuda), inp['lang_tokens'].to(cuda),
+                                     inp['states'].to(cuda),
+                                     noise=inp['noise'].to(cuda)).cpu())
+    err = (outs[1] - ref).abs().max().item()
+    print(f'folded chunk max abs err {err:.3e}')
+    assert err <= CHUNK_ATOL
+    assert (outs[1] - outs[0]).abs().max().item() <= CHUNK_ATOL
+
+
 def test_eager_equals_graph(cuda):
     announce('pi0 eager vs graph')
     from fluxvla_amd.pi0_inference import PI0Inference
