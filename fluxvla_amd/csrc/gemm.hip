@@ -175,12 +175,20 @@ struct EpiViews {
   __amdgpu_buffer_rsrc_t bias, bf32, gate, res, pos, xt, prev, cw, rope, positions, csum;
 };
 
-template <int MODE>
+// (SP: the plain-epilogue build -- PLAIN with bias, fp32 bias, activation
+// and residual only; the host checks that the call uses nothing else)
+template <int MODE, bool SP = false>
 __device__ __forceinline__ EpiViews epi_views(const GemmArgs& p) {
   EpiViews V;
   const int64_t N = p.n;
   V.bias = V.bf32 = V.gate = V.res = V.pos = V.xt = V.prev = V.cw = V.rope = V.positions =
       V.csum = make_rsrc(nullptr, 0u);
+  if constexpr (SP) {
+    V.bias = make_rsrc(p.bias, p.bias ? rec_bytes(N * 2) : 0u);
+    V.bf32 = make_rsrc(p.bias_f32, p.bias_f32 ? rec_bytes(N * 4) : 0u);
+    V.res = make_rsrc(p.residual, p.residual ? rec_bytes(p.m * p.ldr * 2) : 0u);
+    return V;
+  }
   if (MODE == FVX_GEMM_QKV_ROPE) {
     V.positions = make_rsrc(p.positions, rec_bytes(p.m * 4));
     V.rope = make_rsrc(p.rope, 0x7fffffffu);
@@ -221,10 +229,15 @@ __device__ __forceinline__ void epi_load_col(const EpiViews& V, int64_t n, bool 
 }
 
 // the row operands of row m, columns n .. n + 7
-template <int MODE>
+template <int MODE, bool SP = false>
 __device__ __forceinline__ void epi_load_row(const GemmArgs& p, const EpiViews& V, int64_t m,
                                              int64_t n, bool vec, int cnt, EpiIn& in) {
   if (MODE == FVX_GEMM_GEGLU) return;
+  if constexpr (SP) {
+    // 32-bit offsets: the host keeps m * ldr below 2^31
+    in.res = bl_b8(V.res, ((uint32_t)m * (uint32_t)p.ldr + (uint32_t)n) * 2u, vec);
+    return;
+  }
   if (MODE == FVX_GEMM_QKV_ROPE) {
     const int hd = p.head_dim;
     const bool rot = n < (int64_t)(p.n_q_heads + 1) * hd;
@@ -282,7 +295,7 @@ __device__ __forceinline__ void epi_load(const GemmArgs& p, const EpiViews& V, i
 // (LN build with a folded LayerNorm: its rsqrt(var + eps), with mr =
 // mean * r).  want_xo (PLAIN, GEGLU): xo receives the 8 values as stored
 // (bf16-rounded unless out_f32), for the hand-over outputs (epi_handoff).
-template <int MODE, bool LN = false>
+template <int MODE, bool LN = false, bool SP = false>
 __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
                                           int64_t n, bool vec, int cnt,
                                           const float* v, const float* u,
@@ -291,6 +304,29 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
   float x[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = v[e] * r;
+  if constexpr (SP && MODE == FVX_GEMM_PLAIN) {
+    // the same operations in the same order as below, with 32-bit row
+    // offsets (the host keeps m * ldc below 2^31)
+    float t[8];
+    unpack8(in.bias, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] += t[e] + in.f0[e];
+    if (p.act == FVX_ACT_SILU) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = silu(x[e]);
+    } else if (p.act == FVX_ACT_GELU_TANH) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = gelu_tanh(x[e]);
+    }
+    if (p.residual) {
+      unpack8(in.res, t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] += t[e];
+    }
+    st_b8((bf16_t*)p.c + ((uint32_t)m * (uint32_t)p.ldc + (uint32_t)n), x, vec, cnt);
+    if (want_xo) unpack8(pack8(x), xo);
+    return;
+  }
   if (MODE == FVX_GEMM_PLAIN && LN && p.ln_csum)
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = fmaf(-mr, in.cs[e], x[e]);
@@ -659,6 +695,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   static_assert(!A16 || F8, "W8A16 is an fp8-weight variant");
   constexpr bool RPX = (XF & 1) != 0, HOX = (XF & 2) != 0;
   constexpr bool SUMX = !RPX || F8;  // builds with the K-loop sum of squares
+  // bit 3: the plain epilogue (PLAIN with bias, fp32 bias, activation and
+  // residual only; 32-bit row offsets)
+  constexpr bool SP = (XF & 8) != 0 && MODE == FVX_GEMM_PLAIN && !F8;
   // ... and of values, for the folded LayerNorm
   constexpr bool LN = (XF & 4) != 0 && MODE == FVX_GEMM_PLAIN && !F8 && !RPX;
   typedef TileCfg<BM, BN, WGM, WGN, STAGES, MODE, F8> C;
@@ -976,7 +1015,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   // per wave); the shuffles run in every lane
   constexpr bool HO = MODE == FVX_GEMM_PLAIN && WNO == 64;
   const bool ho = HOX && HO && (p.ss_out || p.a8_out) && splits == 1;
-  const EpiViews V = epi_views<MODE>(p);
+  const EpiViews V = epi_views<MODE, SP>(p);
   // VA: every operand is 16B-aligned and N % 8 == 0 (uniform), so every
   // chunk with columns left holds 8 and moves as whole vectors
   auto epilogue = [&](auto va) {
@@ -1004,7 +1043,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
 #pragma unroll
           for (int e = 0; e < EB; ++e) {
             in[e] = col;
-            epi_load_row<MODE>(p, V, rb + RS * (e0 + e), nn, vec, cnt, in[e]);
+            epi_load_row<MODE, SP>(p, V, rb + RS * (e0 + e), nn, vec, cnt, in[e]);
           }
         }
 #pragma unroll
@@ -1048,7 +1087,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
                   r = rsqrtf(sRow[m - m0] / (float)K + p.rownorm_eps);
                 }
               }
-              epi_store<MODE, LN>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo, mr);
+              epi_store<MODE, LN, SP>(p, m, nn, vec, cnt, v, u, r, in[e], ho, xo, mr);
             }
           }
           if (ho) epi_handoff(p, m < M && cnt > 0, m, nn, cnt, xo);
@@ -2549,10 +2588,21 @@ static TilePlan plan_tile(const GemmArgs& d) {
   return t;
 }
 
+// May a one-pass PLAIN tile GEMM take the plain-epilogue build
+// (gemm_tile_kernel's XF bit 3)?  Bias, fp32 bias, activation, residual,
+// the fused RMSNorm and the hand-overs only, bf16 output rows below 2^31
+// elements from the start of c and of the residual.
+static bool plain_epilogue_ok(const GemmArgs& d, int splits) {
+  return d.mode == FVX_GEMM_PLAIN && !d.b_fp8 && splits == 1 && !d.gate && !d.pos &&
+         !d.out_f32 && !d.c_frag && d.row_group == 0 && !d.rtc_lock && !d.bias_f32_locked &&
+         !d.ln_csum && d.m * d.ldc < ((int64_t)1 << 31) &&
+         (!d.residual || d.m * d.ldr < ((int64_t)1 << 31));
+}
+
 // The tile kernel build for a launch: xf = the row-sum paths it needs
 // (gemm_tile_kernel's XF; bits 1 and 2 only matter for PLAIN, and a folded
-// LayerNorm hands nothing over).  fp8-weight tiles keep one build with the
-// paths but the LayerNorm.
+// LayerNorm hands nothing over) and bit 3 for the plain epilogue.  fp8-weight
+// tiles keep one build with the row-sum paths but the LayerNorm.
 template <int BM, int BN, int WGM, int WGN, int ST, int MODE, bool F8, bool A16>
 static void launch_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int xf, int m_tiles,
                         int n_tiles, int splits, int64_t kchunk, int vec_ok) {
@@ -2573,7 +2623,10 @@ static void launch_tile(dim3 grid, hipStream_t s, const GemmArgs& d, int xf, int
       case 1: go(IntC<1>{}); break;
       case 2: go(IntC<2>{}); break;
       case 3: go(IntC<3>{}); break;
-      default: go(IntC<4>{}); break;  // folded LayerNorm, alone
+      case 4: go(IntC<4>{}); break;  // folded LayerNorm, alone
+      case 8: go(IntC<8>{}); break;
+      case 10: go(IntC<10>{}); break;
+      default: go(IntC<3>{}); break;
     }
   }
 }
@@ -2694,9 +2747,9 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     dim3 grid((unsigned)(m_tiles * n_tiles), (unsigned)splits);
     // row-sum paths: handed-over sums read (the tile kernel's bit-0 build
     // has no K-loop sum of squares), hand-over outputs (one-pass epilogue)
-    const int xf = ((d.rownorm && d.ss_in) ? 1 : 0) |
-                   ((splits == 1 && (d.ss_out || d.a8_out)) ? 2 : 0) |
-                   (d.ln_csum ? 4 : 0);
+    int xf = ((d.rownorm && d.ss_in) ? 1 : 0) |
+             ((splits == 1 && (d.ss_out || d.a8_out)) ? 2 : 0) | (d.ln_csum ? 4 : 0);
+    if ((xf == 0 || xf == 2) && plain_epilogue_ok(d, splits)) xf |= 8;
 #define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_)                                 \
     launch_tile<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_>(grid, s, d, xf, m_tiles,    \
                                                            n_tiles, splits, kchunk, vec_ok)

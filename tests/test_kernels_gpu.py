@@ -659,3 +659,34 @@ def test_decode_attention_prefetch_changes_nothing(cuda, place):
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
     assert all(torch.equal(a, w.buf) for a, w in zip(before, ws))
+
+
+@pytest.mark.parametrize('m,n,k', [(768, 1152, 4304), (768, 3456, 1152), (816, 2048, 2048),
+                                   (130, 200, 72)])
+def test_plain_epilogue_build_is_bitwise_generic(K, cuda, m, n, k):
+    """The tile kernel's plain-epilogue build (PLAIN with bias, fp32 bias,
+    activation, residual) against the generic epilogue on the same call
+    (forced by an identity row group: out row m = m), bit for bit, and
+    against an fp32 reference."""
+    announce(f'plain epilogue build m={m} n={n} k={k}')
+    from fluxvla_amd._lib import ACT_GELU_TANH, ACT_NONE
+    a = randn((m, k), 80).to(cuda)
+    w = randn((n, k), 81, std=0.02).to(cuda)
+    b = randn((n,), 82, std=0.5).to(cuda)
+    bf = torch.randn(n, generator=gen(83)).to(cuda)
+    res = randn((m, n), 84).to(cuda)
+    for kw in (dict(bias=b, residual=res), dict(bias_f32=bf, act=ACT_GELU_TANH),
+               dict(bias=b, bias_f32=bf, act=ACT_NONE, residual=res)):
+        fast = K.gemm(a, w, **kw)
+        generic = K.gemm(a, w, row_group=m, row_group_stride=m, **kw)
+        assert torch.equal(fast, generic)
+        ref = a.float() @ w.float().t()
+        if 'bias' in kw:
+            ref = ref + b.float()
+        if 'bias_f32' in kw:
+            ref = ref + bf
+        if kw.get('act') == ACT_GELU_TANH:
+            ref = F.gelu(ref, approximate='tanh')
+        if 'residual' in kw:
+            ref = ref + res.float()
+        assert rel_err(fast, ref) <= REL_TOL
