@@ -2142,7 +2142,8 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
 // bytes at a time (N % 4 == 0) through a buffer view (past it: zeros),
 // the loads of up to 8 splits in flight before their adds, which follow
 // split order (deterministic).
-template <int MODE>
+// (SP: the plain-epilogue build, as the tile kernel's XF bit 3)
+template <int MODE, bool SP = false>
 __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
                                                                   int splits,
                                                                   int vec_ok) {
@@ -2162,7 +2163,11 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(ws, rec_bytes((NB * plane + (int64_t)splits * M) * 4));
   EpiIn in;
-  epi_load<MODE>(p, epi_views<MODE>(p), m, nn, vec_ok && cnt == 8, cnt, in);
+  {
+    const EpiViews V = epi_views<MODE, SP>(p);
+    epi_load_col<MODE>(V, nn, vec_ok && cnt == 8, in);
+    epi_load_row<MODE, SP>(p, V, m, nn, vec_ok && cnt == 8, cnt, in);
+  }
   float v[8], u[8], ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = u[e] = 0.f;
@@ -2212,7 +2217,7 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs p,
   // row's 64-column block
   const bool ho = MODE == FVX_GEMM_PLAIN && (p.ss_out || p.a8_out);
   float xo[8];
-  epi_store<MODE>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in, ho, xo);
+  epi_store<MODE, false, SP>(p, m, nn, vec_ok && cnt == 8, cnt, v, u, r, in, ho, xo);
   if (ho) epi_handoff(p, cnt > 0, m, nn, cnt, xo);
 }
 
@@ -2588,15 +2593,14 @@ static TilePlan plan_tile(const GemmArgs& d) {
   return t;
 }
 
-// May a one-pass PLAIN tile GEMM take the plain-epilogue build
-// (gemm_tile_kernel's XF bit 3)?  Bias, fp32 bias, activation, residual,
-// the fused RMSNorm and the hand-overs only, bf16 output rows below 2^31
-// elements from the start of c and of the residual.
-static bool plain_epilogue_ok(const GemmArgs& d, int splits) {
-  return d.mode == FVX_GEMM_PLAIN && !d.b_fp8 && splits == 1 && !d.gate && !d.pos &&
-         !d.out_f32 && !d.c_frag && d.row_group == 0 && !d.rtc_lock && !d.bias_f32_locked &&
-         !d.ln_csum && d.m * d.ldc < ((int64_t)1 << 31) &&
-         (!d.residual || d.m * d.ldr < ((int64_t)1 << 31));
+// May a PLAIN GEMM's epilogue take the plain-epilogue build (the tile
+// kernel's XF bit 3, the split-K reduce's SP)?  Bias, fp32 bias,
+// activation, residual, the fused RMSNorm and the hand-overs only, bf16
+// output rows below 2^31 elements from the start of c and of the residual.
+static bool plain_epilogue_ok(const GemmArgs& d) {
+  return d.mode == FVX_GEMM_PLAIN && !d.gate && !d.pos && !d.out_f32 && !d.c_frag &&
+         d.row_group == 0 && !d.rtc_lock && !d.bias_f32_locked && !d.ln_csum &&
+         d.m * d.ldc < ((int64_t)1 << 31) && (!d.residual || d.m * d.ldr < ((int64_t)1 << 31));
 }
 
 // The tile kernel build for a launch: xf = the row-sum paths it needs
@@ -2749,7 +2753,7 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     // has no K-loop sum of squares), hand-over outputs (one-pass epilogue)
     int xf = ((d.rownorm && d.ss_in) ? 1 : 0) |
              ((splits == 1 && (d.ss_out || d.a8_out)) ? 2 : 0) | (d.ln_csum ? 4 : 0);
-    if ((xf == 0 || xf == 2) && plain_epilogue_ok(d, splits)) xf |= 8;
+    if ((xf == 0 || xf == 2) && !d.b_fp8 && splits == 1 && plain_epilogue_ok(d)) xf |= 8;
 #define LT(BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_)                                 \
     launch_tile<BM_, BN_, WGM_, WGN_, ST_, MODE, F8_, A16_>(grid, s, d, xf, m_tiles,    \
                                                            n_tiles, splits, kchunk, vec_ok)
@@ -2780,10 +2784,15 @@ static int run_tile(GemmArgs d, int cfg, int splits, hipStream_t s) {
     if (st3 || splits == 1) return st3;
   }
   const int64_t chunks = d.m * ((d.n + 7) / 8);
-#define L(MODE)                                                                  \
-  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>,                           \
-                     dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s, d, \
-                     splits, vec_ok)
+  const dim3 rgrid((unsigned)((chunks + 255) / 256));
+  if (plain_epilogue_ok(d)) {
+    hipLaunchKernelGGL((gemm_partial_reduce_kernel<FVX_GEMM_PLAIN, true>), rgrid, dim3(256), 0,
+                       s, d, splits, vec_ok);
+    return launch_status("gemm(reduce)");
+  }
+#define L(MODE)                                                                           \
+  hipLaunchKernelGGL(gemm_partial_reduce_kernel<MODE>, rgrid, dim3(256), 0, s, d, splits, \
+                     vec_ok)
   FVX_MODE_DISPATCH(d.mode, L)
 #undef L
   return launch_status("gemm(reduce)");

@@ -690,3 +690,26 @@ def test_plain_epilogue_build_is_bitwise_generic(K, cuda, m, n, k):
         if 'residual' in kw:
             ref = ref + res.float()
         assert rel_err(fast, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize('m,n,k,split_k', [(816, 2048, 16384, 0), (200, 256, 4096, 2)])
+def test_plain_reduce_build_is_bitwise_generic(K, cuda, m, n, k, split_k):
+    """The split-K reduce's plain-epilogue build (behind the wide kernel over
+    8 K ranges: the prefix down projection; behind split tiles) against the
+    generic epilogue (forced by an identity row group), bit for bit, with
+    the row sums of squares handed over; and against an fp32 reference."""
+    announce(f'plain reduce build m={m} n={n} k={k} split_k={split_k}')
+    a = randn((m, k), 90).to(cuda)
+    w = randn((n, k), 91, std=0.01).to(cuda)
+    b = randn((n,), 92, std=0.5).to(cuda)
+    res = randn((m, n), 93).to(cuda)
+    outs = []
+    for kw in ({}, dict(row_group=m, row_group_stride=m)):
+        x = res.clone()
+        ss = torch.zeros(K.ss_parts(n), m, device=cuda)
+        K.gemm(a, w, out=x, bias=b, residual=x, ss_out=ss if split_k == 0 else None,
+               split_k=split_k, **kw)
+        outs.append((x, ss))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    ref = a.float() @ w.float().t() + b.float() + res.float()
+    assert rel_err(outs[0][0], ref) <= REL_TOL
