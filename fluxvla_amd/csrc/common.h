@@ -343,12 +343,15 @@ __device__ __forceinline__ float silu(float x) {
 }
 
 // Warm the scalar cache with the first BYTES of the kernel's argument block:
-// one scalar load per 64-byte line, all in flight, one wait.  The compiler
-// reads a large descriptor argument in several batches of scalar loads, each
-// behind a branch or a use and each waited for; cold (the caches start empty
-// in every launch) each batch is a memory round trip (~0.3-0.6 us measured)
-// before the first operand load can even issue.  After this call those
-// batches hit the scalar cache.
+// one scalar load per 64-byte line.  The compiler reads a large descriptor
+// argument in several batches of scalar loads, each behind a branch or a use
+// and each waited for; cold (the caches start empty in every launch) each
+// batch is a memory round trip (~0.3-0.6 us measured) before the first
+// operand load can even issue.  After this call those batches hit the
+// scalar cache.  The loads are plain ones that an empty asm statement
+// consumes: the compiler issues them together with its own first argument
+// loads, ahead of their one wait (loads inside the asm statement came after
+// that wait, a second round trip).
 template <int BYTES>
 __device__ __forceinline__ void warm_kernargs() {
   static_assert(BYTES > 0 && BYTES <= 640, "up to ten 64-byte lines");
@@ -359,27 +362,10 @@ __device__ __forceinline__ void warm_kernargs() {
                 o5 = 320 < BYTES ? 320 : last, o6 = 384 < BYTES ? 384 : last,
                 o7 = 448 < BYTES ? 448 : last, o8 = 512 < BYTES ? 512 : last,
                 o9 = 576 < BYTES ? 576 : last;
-  const auto* kp = __builtin_amdgcn_kernarg_segment_ptr();
-  uint32_t v0, v1, v2, v3, v4, v5, v6, v7, v8, v9;
-  // one statement: the destinations stay reserved until the wait, so no
-  // other instruction can write them while a load is still in flight
-  asm volatile(
-      "s_load_dword %0, %10, %11\n\t"
-      "s_load_dword %1, %10, %12\n\t"
-      "s_load_dword %2, %10, %13\n\t"
-      "s_load_dword %3, %10, %14\n\t"
-      "s_load_dword %4, %10, %15\n\t"
-      "s_load_dword %5, %10, %16\n\t"
-      "s_load_dword %6, %10, %17\n\t"
-      "s_load_dword %7, %10, %18\n\t"
-      "s_load_dword %8, %10, %19\n\t"
-      "s_load_dword %9, %10, %20\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&s"(v0), "=&s"(v1), "=&s"(v2), "=&s"(v3), "=&s"(v4), "=&s"(v5), "=&s"(v6),
-        "=&s"(v7), "=&s"(v8), "=&s"(v9)
-      : "s"(kp), "i"(o0), "i"(o1), "i"(o2), "i"(o3), "i"(o4), "i"(o5), "i"(o6), "i"(o7),
-        "i"(o8), "i"(o9)
-      : "memory");
+  const uint32_t* kp = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" ::"s"(kp[o0 / 4]), "s"(kp[o1 / 4]), "s"(kp[o2 / 4]), "s"(kp[o3 / 4]),
+               "s"(kp[o4 / 4]), "s"(kp[o5 / 4]), "s"(kp[o6 / 4]), "s"(kp[o7 / 4]),
+               "s"(kp[o8 / 4]), "s"(kp[o9 / 4]));
 }
 
 // Cache prefetch by the idle workgroups of a launch (no counterpart in the
