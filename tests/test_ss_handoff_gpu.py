@@ -148,3 +148,30 @@ def test_ss_args_rejected(K, cuda):
         K.gemm(a, w, ss_in=ss)
     with pytest.raises(Exception):
         K.gemm(a, w, ss_out=ss)
+
+
+@pytest.mark.parametrize('n', [1024, 2048])
+def test_ss_in_and_ss_out_in_one_gemm(K, cuda, n):
+    """A rownorm PLAIN GEMM that reads handed-over sums (ss_in) and hands its
+    own output's sums on (ss_out, with a residual): the tile build with both
+    row-sum paths.  Against the same call summing A's squares itself, and
+    the handed-on sums against the stored rows."""
+    announce(f'ss_in + ss_out plain n={n}')
+    m, hid = 816, 2048
+    x, ss, _ = produce(K, cuda, m, 256, hid, 50)
+    w = randn((n, hid), 53, std=0.02).to(cuda)
+    res = randn((m, n), 54).to(cuda)
+    outs = []
+    for s_in in (ss[:, :m], None):
+        y = res.clone()
+        # one row stride for both (ss_ld)
+        so = torch.full((K.ss_parts(n), m + 3), float('nan'), device=cuda)
+        K.gemm(x, w, out=y, residual=y, rownorm_eps=1e-6, ss_in=s_in, ss_out=so)
+        outs.append((y, so))
+    (y, so), (y_own, _) = outs
+    ref = (x.double().cpu() * rms(x)) @ w.double().cpu().t() + res.double().cpu()
+    assert rel_err(y, ref) <= REL_TOL
+    assert within_ulp(y, y_own)
+    want = block_sumsq(y, K.ss_parts(n))
+    got = so[:, :m].double().cpu()
+    assert ((got - want).abs() <= 1e-5 * want.abs() + 1e-6).all()
