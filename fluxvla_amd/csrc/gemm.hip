@@ -175,8 +175,9 @@ struct EpiViews {
   __amdgpu_buffer_rsrc_t bias, bf32, gate, res, pos, xt, prev, cw, rope, positions, csum;
 };
 
-// (SP: the plain-epilogue build -- PLAIN with bias, fp32 bias, activation
-// and residual only; the host checks that the call uses nothing else)
+// (SP: the plain-epilogue build -- PLAIN with bias, fp32 bias, activation,
+// a per-row gate, residual and the fragment-major copy only; the host
+// checks that the call uses nothing else)
 template <int MODE, bool SP = false>
 __device__ __forceinline__ EpiViews epi_views(const GemmArgs& p) {
   EpiViews V;
@@ -187,6 +188,7 @@ __device__ __forceinline__ EpiViews epi_views(const GemmArgs& p) {
     V.bias = make_rsrc(p.bias, p.bias ? rec_bytes(N * 2) : 0u);
     V.bf32 = make_rsrc(p.bias_f32, p.bias_f32 ? rec_bytes(N * 4) : 0u);
     V.res = make_rsrc(p.residual, p.residual ? rec_bytes(p.m * p.ldr * 2) : 0u);
+    V.gate = make_rsrc(p.gate, p.gate ? rec_bytes(p.m * p.ldg * 2) : 0u);
     return V;
   }
   if (MODE == FVX_GEMM_QKV_ROPE) {
@@ -234,8 +236,9 @@ __device__ __forceinline__ void epi_load_row(const GemmArgs& p, const EpiViews& 
                                              int64_t n, bool vec, int cnt, EpiIn& in) {
   if (MODE == FVX_GEMM_GEGLU) return;
   if constexpr (SP) {
-    // 32-bit offsets: the host keeps m * ldr below 2^31
+    // 32-bit offsets: the host keeps m * ldr and m * ldg below 2^31
     in.res = bl_b8(V.res, ((uint32_t)m * (uint32_t)p.ldr + (uint32_t)n) * 2u, vec);
+    in.gate = bl_b8(V.gate, ((uint32_t)m * (uint32_t)p.ldg + (uint32_t)n) * 2u, vec);
     return;
   }
   if (MODE == FVX_GEMM_QKV_ROPE) {
@@ -318,12 +321,18 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = gelu_tanh(x[e]);
     }
+    if (p.gate) {
+      unpack8(in.gate, t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= t[e];
+    }
     if (p.residual) {
       unpack8(in.res, t);
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] += t[e];
     }
     st_b8((bf16_t*)p.c + ((uint32_t)m * (uint32_t)p.ldc + (uint32_t)n), x, vec, cnt);
+    if (p.c_frag) st8((bf16_t*)p.c_frag + frag_offset(m, n), pack8(x));
     if (want_xo) unpack8(pack8(x), xo);
     return;
   }
@@ -1807,7 +1816,7 @@ __device__ __forceinline__ void sc1_load8(__amdgpu_buffer_rsrc_t r, int off,
   }
 }
 
-template <int MODE, bool F8, bool A16, int RB, bool ASC>
+template <int MODE, bool F8, bool A16, int RB, bool ASC, bool SP = false>
 __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(GemmArgs p,
                                                           int splits,
                                                           int64_t kc,
@@ -2000,7 +2009,11 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
   const bool mine = tid < 2 * RR && row < M && cnt > 0;
   const bool vec = vec_ok && cnt == 8;
   EpiIn in;
-  if (mine) epi_load<MODE>(p, epi_views<MODE>(p), row, ncol, vec, cnt, in);
+  if (mine) {
+    const EpiViews V = epi_views<MODE, SP>(p);
+    epi_load_col<MODE>(V, ncol, vec, in);
+    epi_load_row<MODE, SP>(p, V, row, ncol, vec, cnt, in);
+  }
   // ASC with QKV_ROPE / GEGLU: the folded shift's fp32 biases (gate, up)
   constexpr bool FB = ASC && (MODE == FVX_GEMM_QKV_ROPE || MODE == FVX_GEMM_GEGLU);
   float fb[8], fb2[8];
@@ -2132,7 +2145,7 @@ __global__ __launch_bounds__(64 * sk_waves(F8, A16)) void gemm_skinny_kernel(Gem
     }
     r = 1.f;
   }
-  epi_store<MODE>(p, row, ncol, vec, cnt, v, u, r, in, false, nullptr);
+  epi_store<MODE, false, SP>(p, row, ncol, vec, cnt, v, u, r, in, false, nullptr);
 }
 
 // Sum of the split partials of the tile or wide kernel + epilogue.  Thread t
@@ -2594,13 +2607,15 @@ static TilePlan plan_tile(const GemmArgs& d) {
 }
 
 // May a PLAIN GEMM's epilogue take the plain-epilogue build (the tile
-// kernel's XF bit 3, the split-K reduce's SP)?  Bias, fp32 bias,
-// activation, residual, the fused RMSNorm and the hand-overs only, bf16
-// output rows below 2^31 elements from the start of c and of the residual.
+// kernel's XF bit 3, the skinny kernel's and the split-K reduce's SP)?
+// Bias, fp32 bias, activation, a per-row gate, residual, the fragment-major
+// copy, the fused RMSNorm and the hand-overs only, bf16 output rows below
+// 2^31 elements from the start of c, of the residual and of the gate.
 static bool plain_epilogue_ok(const GemmArgs& d) {
-  return d.mode == FVX_GEMM_PLAIN && !d.gate && !d.pos && !d.out_f32 && !d.c_frag &&
-         d.row_group == 0 && !d.rtc_lock && !d.bias_f32_locked && !d.ln_csum &&
-         d.m * d.ldc < ((int64_t)1 << 31) && (!d.residual || d.m * d.ldr < ((int64_t)1 << 31));
+  return d.mode == FVX_GEMM_PLAIN && !d.pos && !d.out_f32 && d.row_group == 0 && !d.rtc_lock &&
+         !d.bias_f32_locked && !d.ln_csum && d.m * d.ldc < ((int64_t)1 << 31) &&
+         (!d.residual || d.m * d.ldr < ((int64_t)1 << 31)) &&
+         (!d.gate || (d.gate_group <= 1 && d.m * d.ldg < ((int64_t)1 << 31)));
 }
 
 // The tile kernel build for a launch: xf = the row-sum paths it needs
@@ -2854,6 +2869,17 @@ extern "C" int fvx_gemm(const fvx_gemm_desc* dp, void* stream) {
                 "gemm: workspace must be 16B aligned");
     dim3 grid((unsigned)sp.n_tiles, (unsigned)sp.splits, (unsigned)sp.row_groups);
     const int vec_ok = epi_vec_ok(d) ? 1 : 0;
+    // bf16 PLAIN calls that the plain epilogue covers take its build
+    if (d.mode == FVX_GEMM_PLAIN && !d.b_fp8 && !d.a_scale && plain_epilogue_ok(d)) {
+#define LS(RB_)                                                                          \
+  hipLaunchKernelGGL((gemm_skinny_kernel<FVX_GEMM_PLAIN, false, false, RB_, false, true>), \
+                     grid, dim3(64 * kSkWaves), 0, s, d, sp.splits, sp.kc, vec_ok)
+      if (sp.rb == 1) LS(1);
+      else if (sp.rb == 2) LS(2);
+      else LS(4);
+#undef LS
+      return launch_status("gemm(skinny)");
+    }
 #define L(MODE)                                                                 \
   if (d.b_fp8 && d.fp8_act)                                                      \
     hipLaunchKernelGGL((gemm_skinny_kernel<MODE, true, false, 4, false>), grid,  \

@@ -713,3 +713,28 @@ def test_plain_reduce_build_is_bitwise_generic(K, cuda, m, n, k, split_k):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     ref = a.float() @ w.float().t() + b.float() + res.float()
     assert rel_err(outs[0][0], ref) <= REL_TOL
+
+
+@pytest.mark.parametrize('m,n,k', [(51, 1024, 2048), (51, 1024, 4096), (17, 1000, 1000)])
+def test_plain_epilogue_build_skinny_gate_frag(K, cuda, m, n, k):
+    """The skinny kernel's plain-epilogue build (the bs=1 expert's O and
+    down projections: residual, per-row gate, fragment-major copy, bias)
+    against the generic epilogue on the same call (forced by an identity
+    row group), bit for bit in both outputs, and against fp32."""
+    announce(f'plain epilogue build skinny m={m} n={n} k={k}')
+    a = randn((m, k), 94).to(cuda)
+    w = randn((n, k), 95, std=0.02).to(cuda)
+    b = randn((n,), 96, std=0.5).to(cuda)
+    res = randn((m, n), 97).to(cuda)
+    gate = randn((m, n), 98, std=0.5).to(cuda)
+    outs = []
+    for kw in ({}, dict(row_group=m, row_group_stride=m)):
+        x = res.clone()
+        cf = K.FragA.empty(n, cuda).rows(m) if n % 32 == 0 else None
+        K.gemm(a, w, out=x, bias=b, residual=x, gate=gate, c_frag=cf, **kw)
+        outs.append((x, cf))
+    assert torch.equal(outs[0][0], outs[1][0])
+    if outs[0][1] is not None:
+        assert torch.equal(outs[0][1].buf, outs[1][1].buf)
+    ref = (a.float() @ w.float().t() + b.float()) * gate.float() + res.float()
+    assert rel_err(outs[0][0], ref) <= REL_TOL
