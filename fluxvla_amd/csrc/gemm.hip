@@ -688,14 +688,15 @@ struct TileCfg {
 
 // F8 && A16 (W8A16): the F8 LDS layout (128-k slabs, e4m3 weight rows), but
 // A stays bf16 and each 8 weight bytes become one bf16 MFMA fragment.
-// XF: the row-sum paths compiled in (bit 0: handed-over row sums of squares
-// read, ss_in; bit 1: hand-over outputs, ss_out / a8_out; bit 2, PLAIN, not
-// with bit 0: the folded LayerNorm, ln_csum, on sums of A's values and
-// squares taken in the K loop).  GEMMs without them run a build without their
-// code: compiled in but not taken, it cost such 20 us launches ~0.7 us.
-// bf16 bit-0 builds have no K-loop sum of squares: the host picks them only
-// for rownorm GEMMs with ss_in (fp8-weight tiles keep one build, XF = 3,
-// with every path).
+// XF: the optional paths compiled in (bit 0: handed-over row sums of
+// squares read, ss_in; bit 1: hand-over outputs, ss_out / a8_out; bit 2,
+// PLAIN, not with bit 0: the folded LayerNorm, ln_csum, on sums of A's
+// values and squares taken in the K loop; bit 3, PLAIN: the plain epilogue,
+// see plain_epilogue_ok).  GEMMs without a path run a build without its
+// code: compiled in but not taken, the row-sum paths cost such 20 us
+// launches ~0.7 us.  bf16 bit-0 builds have no K-loop sum of squares: the
+// host picks them only for rownorm GEMMs with ss_in (fp8-weight tiles keep
+// one build, XF = 3, with both row-sum paths).
 template <int BM, int BN, int WGM, int WGN, int STAGES, int MODE, bool F8, bool A16,
           int XF = 3>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
@@ -704,11 +705,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_tile_kernel(
   static_assert(!A16 || F8, "W8A16 is an fp8-weight variant");
   constexpr bool RPX = (XF & 1) != 0, HOX = (XF & 2) != 0;
   constexpr bool SUMX = !RPX || F8;  // builds with the K-loop sum of squares
-  // bit 3: the plain epilogue (PLAIN with bias, fp32 bias, activation and
-  // residual only; 32-bit row offsets)
-  constexpr bool SP = (XF & 8) != 0 && MODE == FVX_GEMM_PLAIN && !F8;
   // ... and of values, for the folded LayerNorm
   constexpr bool LN = (XF & 4) != 0 && MODE == FVX_GEMM_PLAIN && !F8 && !RPX;
+  // the plain epilogue (32-bit row offsets, no unused features)
+  constexpr bool SP = (XF & 8) != 0 && MODE == FVX_GEMM_PLAIN && !F8;
   typedef TileCfg<BM, BN, WGM, WGN, STAGES, MODE, F8> C;
   constexpr int NB = C::NB, WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
   constexpr int LPW = C::LPW, WNO = C::WNO, ELD = C::ELD, BK = C::BK;
