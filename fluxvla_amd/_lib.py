@@ -154,7 +154,31 @@ SIGNATURES = {
     'fvx_copy_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64,
                               c_i64, c_vp]),
     'fvx_resize_normalize': (c_i32, [ctypes.POINTER(ImageDesc), c_vp]),
+    # backward ops of guidance RTC with use_vjp
+    'fvx_rms_norm_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
+                                      c_vp, c_vp, c_vp, c_i64, c_vp, c_i64,
+                                      c_i64, c_i64, c_i64, c_i64, c_f32,
+                                      c_vp]),
+    'fvx_act_backward': (c_i32, [c_i32, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
+                                 c_i64, c_i64, c_vp]),
+    'fvx_attention_rows_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp,
+                                            c_vp, c_vp, c_i64, c_vp, c_vp,
+                                            c_i64, c_i64, c_i64, c_i64, c_i64,
+                                            c_i64, c_i64, c_f32, c_vp]),
+    'fvx_transpose_bf16': (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
+                                   c_i64, c_i64, c_i64, c_vp]),
+    'fvx_rope_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
+                                  c_vp, c_vp, c_i64, c_i64, c_i64, c_i64,
+                                  c_vp]),
+    'fvx_rtc_vjp_error': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
+                                  c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
+                                  c_vp]),
+    'fvx_rtc_vjp_update': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
+                                   c_vp, c_i64, c_vp, c_vp, c_i64, c_vp,
+                                   c_i64, c_i64, c_i64, c_f32, c_f32, c_vp]),
 }
+
+ACT_BWD_GEGLU, ACT_BWD_SILU = 0, 1
 
 _lib = None
 

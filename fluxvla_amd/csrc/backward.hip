@@ -1,0 +1,534 @@
+// Backward kernels of the action expert: the vector-Jacobian product J^T e
+// of one denoising step that guidance real-time chunking with use_vjp adds
+// to the velocity (fluxvla/engines/utils/rtc_guidance.py:142-150, which
+// takes it from torch autograd through the whole denoiser).
+//
+// The products with weights (dY @ W for every linear layer, and the
+// attention's Q K^T, dO V^T, dS K, dS^T Q, P^T dO) run through fvx_gemm on
+// transposed operand copies; this file holds what lies between them:
+//   rms_backward_kernel      RMSNorm (and adaRMS scale) backward + residual
+//   act_backward_kernel      GeGLU and SiLU backward, elementwise
+//   attn_rows_backward_kernel  masked softmax backward per query row
+//   transpose_kernel         bf16 [rows, cols] -> [cols, rows] (batched)
+//   rope_backward_kernel     RoPE backward of dq / dk, packed with dv
+//   rtc_vjp_*_kernel         the guidance error and the corrected update
+// Every kernel reads and writes in fp32 except where a bf16 operand of the
+// next GEMM is produced; one thread or one wavefront per independent item,
+// every access bounds-checked against the sizes the host validated.
+#include "capi_util.h"
+#include "common.h"
+
+namespace fvx {
+
+namespace {
+
+constexpr int kBwdRows = 4;  // rows (wavefronts) per 256-thread workgroup
+
+__device__ __forceinline__ void ld_f8(const float* p, float* f) {
+  const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p);
+  const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[e] = a[e];
+    f[4 + e] = b[e];
+  }
+}
+
+__device__ __forceinline__ void st_f8(float* p, const float* f) {
+  *reinterpret_cast<f32x4_t*>(p) = f32x4_t{f[0], f[1], f[2], f[3]};
+  *reinterpret_cast<f32x4_t*>(p + 4) = f32x4_t{f[4], f[5], f[6], f[7]};
+}
+
+__device__ __forceinline__ int64_t grouped_row(int64_t m, int64_t g, int64_t gs) {
+  return g > 0 ? (m / g) * gs + m % g : m;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm backward.  Forward (GemmaRMSNorm with the (1 + w) gain folded into
+// the next GEMM's weights, condition_gemma.py:75-80; adaRMS keeps its
+// per-style (1 + scale), :126-145):  y = x r (1 + scale),
+// r = rsqrt(mean(x^2) + eps).  With g = dy (1 + scale):
+//   dx = dres + r g - (r^3 / n) (x . g) x.
+// One wavefront per row; vector v (8 columns) of the row is lane v % 64's
+// (v / 64)-th.  x, dres, out and out_b rows follow the row-group map
+// (m / g) * gs + m % g (identity for g = 0); dy rows are compact.
+// out_b = bf16(dx * gate): the A operand of the next backward GEMM.
+// ---------------------------------------------------------------------------
+template <int NV>
+__global__ __launch_bounds__(256) void rms_backward_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const float* __restrict__ dy,
+    int64_t ldy, const float* __restrict__ dres, int64_t ldr,
+    const bf16_t* __restrict__ scale, const bf16_t* __restrict__ gate,
+    float* __restrict__ out, int64_t ldo, bf16_t* __restrict__ out_b,
+    int64_t ldob, int64_t rows, int cols, int64_t grp, int64_t grp_stride,
+    float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * kBwdRows + (threadIdx.x >> 6);
+  if (m >= rows) return;
+  const int64_t pr = grouped_row(m, grp, grp_stride);
+  const int nvec = cols >> 3;
+  float xv[NV][8], g[NV][8];
+  float ss = 0.f, dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v < nvec) {
+      unpack8(ld8(x + pr * ldx + v * 8), xv[i]);
+      ld_f8(dy + m * ldy + v * 8, g[i]);
+      if (scale) {
+        float sc[8];
+        unpack8(ld8(scale + v * 8), sc);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[i][e] *= 1.f + sc[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[i][e] = g[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ss += xv[i][e] * xv[i][e];
+      dot += xv[i][e] * g[i][e];
+    }
+  }
+  ss = wave_sum(ss);
+  dot = wave_sum(dot);
+  const float r = rsqrtf(ss / (float)cols + eps);
+  const float c = r * r * r * dot / (float)cols;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = lane + 64 * i;
+    if (v >= nvec) continue;
+    float d[8], rd[8];
+    if (dres) {
+      ld_f8(dres + pr * ldr + v * 8, rd);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rd[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = rd[e] + r * g[i][e] - c * xv[i][e];
+    if (out) st_f8(out + pr * ldo + v * 8, d);
+    if (out_b) {
+      if (gate) {
+        float gf[8];
+        unpack8(ld8(gate + v * 8), gf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gf[e] *= d[e];
+        st8(out_b + pr * ldob + v * 8, pack8(gf));
+      } else {
+        st8(out_b + pr * ldob + v * 8, pack8(d));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Activation backward, 8 columns per thread.
+//   GEGLU (GemmaMLP, condition_gemma.py:156-192: h = gelu_tanh(gg) * uu):
+//     in = [gg | uu] (cols each), dy = dh ->
+//     out = [dh uu gelu'(gg) | dh gelu(gg)]
+//   SILU (the PI0 action-time MLP, pi0_flowmatching.py:300-310): in = z,
+//     out = dy silu'(z)
+// gelu_tanh(x) = x s, s = 1 / (1 + exp(-2u)), u = sqrt(2/pi) (x + 0.044715
+// x^3) (the forward's own formula, common.h), so gelu' = s + x s (1 - s)
+// 2 sqrt(2/pi) (1 + 3 * 0.044715 x^2);  silu'(z) = sig (1 + z (1 - sig)).
+// ---------------------------------------------------------------------------
+constexpr int kActGeglu = 0, kActSilu = 1;
+
+template <int ACT>
+__global__ __launch_bounds__(256) void act_backward_kernel(
+    const bf16_t* __restrict__ in, int64_t ldi, const bf16_t* __restrict__ dy,
+    int64_t ldy, bf16_t* __restrict__ out, int64_t ldo, int64_t rows, int cols) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nv = cols >> 3;
+  if (t >= rows * nv) return;
+  const int64_t m = t / nv;
+  const int c = (int)(t - m * nv) * 8;
+  float a[8], d[8], o[8];
+  unpack8(ld8(in + m * ldi + c), a);
+  unpack8(ld8(dy + m * ldy + c), d);
+  if (ACT == kActGeglu) {
+    float u[8], o2[8];
+    unpack8(ld8(in + m * ldi + cols + c), u);
+    constexpr float k2 = 1.5957691216057308f;  // 2 sqrt(2 / pi)
+    constexpr float k1 = 0.044715f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = a[e];
+      const float s = 1.f / (1.f + expf(-k2 * (x + k1 * x * x * x)));
+      const float dg = s + x * s * (1.f - s) * k2 * (1.f + 3.f * k1 * x * x);
+      o[e] = d[e] * u[e] * dg;
+      o2[e] = d[e] * (x * s);
+    }
+    st8(out + m * ldo + c, pack8(o));
+    st8(out + m * ldo + cols + c, pack8(o2));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float z = a[e];
+      const float sg = 1.f / (1.f + expf(-z));
+      o[e] = d[e] * sg * (1.f + z * (1.f - sg));
+    }
+    st8(out + m * ldo + c, pack8(o));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Masked softmax backward of one attention problem, one wavefront per query
+// row (row r = query token r / heads, head r % heads).  s: raw scores q . k
+// (fp32), dp: dO . v (fp32), both [rows, ld]; key j is visible to the row
+// iff kgrp[j] <= qgrp[token] (the make_att_2d_masks rule,
+// model_utils.py:77-95).  With logits l = scale s and P = softmax over the
+// visible keys:
+//   D = sum_j P_j dp_j,  ds_j = scale P_j (dp_j - D)   (d of the raw score)
+// ds is written for columns [0, n_cols) (zero past n_keys and on masked
+// keys); for the n_suffix keys from key0 the row also goes into column r of
+// ds_t and p_t ([n_suffix, ldt], bf16): the A operands of dK = ds^T Q and
+// dV = P^T dO.  Four passes over the row (max, sum, D, write) re-read s and
+// dp from the cache instead of holding a row of any length in registers.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_rows_backward_kernel(
+    const float* __restrict__ s, int64_t lds, const float* __restrict__ dp,
+    int64_t lddp, const int32_t* __restrict__ kgrp,
+    const int32_t* __restrict__ qgrp, bf16_t* __restrict__ ds, int64_t ldds,
+    bf16_t* __restrict__ ds_t, bf16_t* __restrict__ p_t, int64_t ldt,
+    int64_t key0, int n_suffix, int64_t rows, int heads, int n_keys,
+    int n_cols, float scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * kBwdRows + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int32_t qg = qgrp ? qgrp[r / heads] : 0;
+  const float* sr = s + r * lds;
+  const float* dr = dp + r * lddp;
+  constexpr float kLog2e = 1.4426950408889634f;
+  float mx = -INFINITY;
+  for (int j = lane; j < n_keys; j += 64)
+    if (!kgrp || kgrp[j] <= qg) mx = fmaxf(mx, sr[j] * scale);
+  mx = wave_max(mx);
+  float l = 0.f;
+  if (mx != -INFINITY)
+    for (int j = lane; j < n_keys; j += 64)
+      if (!kgrp || kgrp[j] <= qg) l += exp2f((sr[j] * scale - mx) * kLog2e);
+  l = wave_sum(l);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  float dsum = 0.f;
+  for (int j = lane; j < n_keys; j += 64)
+    if (!kgrp || kgrp[j] <= qg)
+      dsum += exp2f((sr[j] * scale - mx) * kLog2e) * inv * dr[j];
+  dsum = wave_sum(dsum);
+  for (int j = lane; j < n_cols; j += 64) {
+    float p = 0.f, d = 0.f;
+    if (j < n_keys && (!kgrp || kgrp[j] <= qg) && l > 0.f) {
+      p = exp2f((sr[j] * scale - mx) * kLog2e) * inv;
+      d = scale * p * (dr[j] - dsum);
+    }
+    ds[r * ldds + j] = f2bf(d);
+    const int64_t js = j - key0;
+    if (js >= 0 && js < n_suffix) {
+      if (ds_t) ds_t[js * ldt + r] = f2bf(d);
+      if (p_t) p_t[js * ldt + r] = f2bf(p);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 transpose, 32 x 32 tiles through LDS (one padding column keeps the
+// column reads conflict-free): dst[b][c][r] = src[b][r][c].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void transpose_kernel(
+    const bf16_t* __restrict__ src, int64_t ld_src, int64_t src_bs,
+    bf16_t* __restrict__ dst, int64_t ld_dst, int64_t dst_bs, int64_t rows,
+    int64_t cols) {
+  __shared__ bf16_t tile[32][33];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  const bf16_t* sb = src + b * src_bs;
+  bf16_t* db = dst + b * dst_bs;
+#pragma unroll
+  for (int i = 0; i < 32; i += 8) {
+    const int64_t r = r0 + ty + i, c = c0 + tx;
+    if (r < rows && c < cols) tile[ty + i][tx] = sb[r * ld_src + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 32; i += 8) {
+    const int64_t c = c0 + ty + i, r = r0 + tx;
+    if (r < rows && c < cols) db[c * ld_dst + r] = tile[tx][ty + i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE backward, packed: row m of out = [dq rotated back (n_q_heads heads) |
+// dk rotated back | dv], bf16 -- the dY of the Q|K|V GEMM.  The forward
+// rotates pair (2i, 2i+1) of each head (pair-interleaved columns) by
+// (cos, sin) = rope[pos][i]: (a, b) -> (a c - b s, b c + a s); its
+// transpose takes (ga, gb) -> (ga c + gb s, gb c - ga s).  One thread per
+// column pair.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rope_backward_kernel(
+    const float* __restrict__ dq, int64_t ldq, const float* __restrict__ dk,
+    int64_t ldk, const float* __restrict__ dv, int64_t ldv,
+    const float* __restrict__ rope, const int32_t* __restrict__ positions,
+    bf16_t* __restrict__ out, int64_t ldo, int64_t rows, int n_q_heads,
+    int head_dim) {
+  const int half = head_dim >> 1;
+  const int pairs = (n_q_heads + 2) * half;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * pairs) return;
+  const int64_t m = t / pairs;
+  const int p = (int)(t - m * pairs);
+  const int qpairs = n_q_heads * half;
+  float a, b;
+  bool rot = true;
+  if (p < qpairs) {
+    a = dq[m * ldq + 2 * p];
+    b = dq[m * ldq + 2 * p + 1];
+  } else if (p < qpairs + half) {
+    const int i = p - qpairs;
+    a = dk[m * ldk + 2 * i];
+    b = dk[m * ldk + 2 * i + 1];
+  } else {
+    const int i = p - qpairs - half;
+    a = dv[m * ldv + 2 * i];
+    b = dv[m * ldv + 2 * i + 1];
+    rot = false;
+  }
+  if (rot) {
+    const int i = p % half;
+    const float* cs = rope + ((int64_t)positions[m] * half + i) * 2;
+    const float c = cs[0], s = cs[1];
+    const float ga = a * c + b * s, gb = b * c - a * s;
+    a = ga;
+    b = gb;
+  }
+  *reinterpret_cast<uint32_t*>(out + m * ldo + 2 * p) = f2bf2(a, b);
+}
+
+// ---------------------------------------------------------------------------
+// Guidance error and corrected Euler update (rtc_guidance.py:107-155 with
+// use_vjp, under _predict_action_guidance_rtc, pi0_flowmatching.py:671-700,
+// whose denoiser is -u for the model velocity u).  Row m is action step
+// m % period of its sample; w: per-step prefix weights (zero past the
+// previous chunk), omt = 1 - t of the step.
+//   e = w (prev - x + omt u)                  (the error at x_1 = x - omt u)
+//   x <- x + dt u - dt gw e + dt gw omt g      (g = J_u^T e)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rtc_vjp_error_kernel(
+    const float* __restrict__ x, int64_t ldx, const float* __restrict__ u,
+    int64_t ldu, const float* __restrict__ prev, int64_t ldp,
+    const float* __restrict__ w, bf16_t* __restrict__ e, int64_t lde,
+    int64_t rows, int cols, int64_t period, float omt) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * cols) return;
+  const int64_t m = t / cols;
+  const int c = (int)(t - m * cols);
+  const float ev = w[m % period] * (prev[m * ldp + c] - x[m * ldx + c] + omt * u[m * ldu + c]);
+  e[m * lde + c] = f2bf(ev);
+}
+
+__global__ __launch_bounds__(256) void rtc_vjp_update_kernel(
+    float* __restrict__ x, int64_t ldx, bf16_t* __restrict__ xb, int64_t ldxb,
+    const float* __restrict__ u, int64_t ldu, const float* __restrict__ prev,
+    int64_t ldp, const float* __restrict__ w, const float* __restrict__ g,
+    int64_t ldg, const float* __restrict__ gw, int64_t rows, int cols,
+    int64_t period, float omt, float dt) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * cols) return;
+  const int64_t m = t / cols;
+  const int c = (int)(t - m * cols);
+  const float xv = x[m * ldx + c], uv = u[m * ldu + c];
+  const float ev = w[m % period] * (prev[m * ldp + c] - xv + omt * uv);
+  const float k = dt * gw[0];
+  const float xn = xv + dt * uv - k * ev + k * omt * g[m * ldg + c];
+  x[m * ldx + c] = xn;
+  if (xb) xb[m * ldxb + c] = f2bf(xn);
+}
+
+inline unsigned blocks(int64_t items, int64_t per) {
+  return (unsigned)((items + per - 1) / per);
+}
+
+inline bool al16(const void* p) { return aligned16(p); }
+
+}  // namespace
+
+}  // namespace fvx
+
+using namespace fvx;
+
+extern "C" int fvx_rms_norm_backward(const void* x, int64_t ldx, const float* dy,
+                                     int64_t ldy, const float* dres, int64_t ldr,
+                                     const void* scale, const void* gate, float* out,
+                                     int64_t ldo, void* out_bf16, int64_t ldob,
+                                     int64_t rows, int64_t cols, int64_t row_group,
+                                     int64_t row_group_stride, float eps,
+                                     void* stream) {
+  clear_error();
+  FVX_REQUIRE(x && dy && (out || out_bf16), FVX_ERR_NULL,
+              "rms_norm_backward: x, dy and an output are required");
+  FVX_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 4096, FVX_ERR_SHAPE,
+              "rms_norm_backward: cols must be a positive multiple of 8 <= 4096");
+  FVX_REQUIRE(ldx >= cols && ldy >= cols && ldx % 8 == 0 && ldy % 8 == 0 &&
+                  (!dres || (ldr >= cols && ldr % 8 == 0)) &&
+                  (!out || (ldo >= cols && ldo % 8 == 0)) &&
+                  (!out_bf16 || (ldob >= cols && ldob % 8 == 0)),
+              FVX_ERR_SHAPE, "rms_norm_backward: leading dims must be >= cols, multiples of 8");
+  FVX_REQUIRE(al16(x) && al16(dy) && al16(dres) && al16(out) && al16(out_bf16) &&
+                  al16(scale) && al16(gate),
+              FVX_ERR_ALIGN, "rms_norm_backward: pointers must be 16-byte aligned");
+  FVX_REQUIRE(row_group >= 0 && (row_group == 0 || row_group_stride >= row_group),
+              FVX_ERR_ARG, "rms_norm_backward: bad row group");
+  FVX_REQUIRE(eps >= 0.f, FVX_ERR_ARG, "rms_norm_backward: eps must be >= 0");
+  if (rows == 0) return FVX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int nv = (int)((cols / 8 + 63) / 64);
+  const dim3 grid(blocks(rows, kBwdRows));
+#define L(NV)                                                                          \
+  hipLaunchKernelGGL(rms_backward_kernel<NV>, grid, dim3(256), 0, s, (const bf16_t*)x, \
+                     ldx, dy, ldy, dres, ldr, (const bf16_t*)scale,                    \
+                     (const bf16_t*)gate, out, ldo, (bf16_t*)out_bf16, ldob, rows,     \
+                     (int)cols, row_group, row_group_stride, eps)
+  switch (nv) {
+    case 1: L(1); break;
+    case 2: L(2); break;
+    case 3: L(3); break;
+    case 4: L(4); break;
+    case 5: L(5); break;
+    case 6: L(6); break;
+    case 7: L(7); break;
+    default: L(8); break;
+  }
+#undef L
+  return launch_status("rms_norm_backward");
+}
+
+extern "C" int fvx_act_backward(int act, const void* in, int64_t ldi, const void* dy,
+                                int64_t ldy, void* out, int64_t ldo, int64_t rows,
+                                int64_t cols, void* stream) {
+  clear_error();
+  FVX_REQUIRE(in && dy && out, FVX_ERR_NULL, "act_backward: in, dy, out are required");
+  FVX_REQUIRE(act == FVX_ACT_BWD_GEGLU || act == FVX_ACT_BWD_SILU, FVX_ERR_ARG,
+              "act_backward: bad act %d", act);
+  const int64_t w = act == FVX_ACT_BWD_GEGLU ? 2 * cols : cols;
+  FVX_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols < (1 << 30), FVX_ERR_SHAPE,
+              "act_backward: cols must be a positive multiple of 8");
+  FVX_REQUIRE(ldi >= w && ldo >= w && ldy >= cols && ldi % 8 == 0 && ldo % 8 == 0 &&
+                  ldy % 8 == 0,
+              FVX_ERR_SHAPE, "act_backward: leading dims too small or not multiples of 8");
+  FVX_REQUIRE(al16(in) && al16(dy) && al16(out), FVX_ERR_ALIGN,
+              "act_backward: pointers must be 16-byte aligned");
+  if (rows == 0) return FVX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(blocks(rows * (cols / 8), 256));
+  if (act == FVX_ACT_BWD_GEGLU)
+    hipLaunchKernelGGL(act_backward_kernel<kActGeglu>, grid, dim3(256), 0, s,
+                       (const bf16_t*)in, ldi, (const bf16_t*)dy, ldy, (bf16_t*)out, ldo,
+                       rows, (int)cols);
+  else
+    hipLaunchKernelGGL(act_backward_kernel<kActSilu>, grid, dim3(256), 0, s,
+                       (const bf16_t*)in, ldi, (const bf16_t*)dy, ldy, (bf16_t*)out, ldo,
+                       rows, (int)cols);
+  return launch_status("act_backward");
+}
+
+extern "C" int fvx_attention_rows_backward(
+    const float* s, int64_t lds, const float* dp, int64_t lddp, const int32_t* kgrp,
+    const int32_t* qgrp, void* ds, int64_t ldds, void* ds_t, void* p_t, int64_t ldt,
+    int64_t key0, int64_t n_suffix, int64_t rows, int64_t heads, int64_t n_keys,
+    int64_t n_cols, float scale, void* stream) {
+  clear_error();
+  FVX_REQUIRE(s && dp && ds, FVX_ERR_NULL, "attention_rows_backward: s, dp, ds are required");
+  FVX_REQUIRE((kgrp == nullptr) == (qgrp == nullptr), FVX_ERR_ARG,
+              "attention_rows_backward: kgrp and qgrp must both be given or both be NULL");
+  FVX_REQUIRE(rows >= 0 && heads > 0 && n_keys > 0 && n_cols >= n_keys &&
+                  n_cols < (1 << 30) && lds >= n_keys && lddp >= n_keys && ldds >= n_cols,
+              FVX_ERR_SHAPE, "attention_rows_backward: bad sizes");
+  FVX_REQUIRE((!ds_t && !p_t) ||
+                  (n_suffix > 0 && key0 >= 0 && key0 + n_suffix <= n_keys && ldt >= rows),
+              FVX_ERR_SHAPE, "attention_rows_backward: bad suffix columns");
+  if (rows == 0) return FVX_OK;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_rows_backward_kernel, dim3(blocks(rows, kBwdRows)), dim3(256), 0,
+                     st, s, lds, dp, lddp, kgrp, qgrp, (bf16_t*)ds, ldds, (bf16_t*)ds_t,
+                     (bf16_t*)p_t, ldt, key0, (int)n_suffix, rows, (int)heads,
+                     (int)n_keys, (int)n_cols, scale);
+  return launch_status("attention_rows_backward");
+}
+
+extern "C" int fvx_transpose_bf16(const void* src, int64_t ld_src, int64_t src_batch_stride,
+                                  void* dst, int64_t ld_dst, int64_t dst_batch_stride,
+                                  int64_t rows, int64_t cols, int64_t batch, void* stream) {
+  clear_error();
+  FVX_REQUIRE(src && dst, FVX_ERR_NULL, "transpose_bf16: src and dst are required");
+  FVX_REQUIRE(rows >= 0 && cols >= 0 && batch >= 0 && batch < 65536 && ld_src >= cols &&
+                  ld_dst >= rows && rows < ((int64_t)1 << 31) / 32 * 32 &&
+                  cols < ((int64_t)1 << 31) / 32 * 32,
+              FVX_ERR_SHAPE, "transpose_bf16: bad sizes");
+  if (rows == 0 || cols == 0 || batch == 0) return FVX_OK;
+  const dim3 grid(blocks(cols, 32), blocks(rows, 32), (unsigned)batch);
+  FVX_REQUIRE(grid.y < 65536, FVX_ERR_SHAPE, "transpose_bf16: too many rows");
+  hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+                     (const bf16_t*)src, ld_src, src_batch_stride, (bf16_t*)dst, ld_dst,
+                     dst_batch_stride, rows, cols);
+  return launch_status("transpose_bf16");
+}
+
+extern "C" int fvx_rope_backward(const float* dq, int64_t ldq, const float* dk, int64_t ldk,
+                                 const float* dv, int64_t ldv, const float* rope,
+                                 const int32_t* positions, void* out, int64_t ldo,
+                                 int64_t rows, int64_t n_q_heads, int64_t head_dim,
+                                 void* stream) {
+  clear_error();
+  FVX_REQUIRE(dq && dk && dv && rope && positions && out, FVX_ERR_NULL,
+              "rope_backward: every operand is required");
+  FVX_REQUIRE(rows >= 0 && n_q_heads > 0 && head_dim > 0 && head_dim % 2 == 0 &&
+                  ldq >= n_q_heads * head_dim && ldk >= head_dim && ldv >= head_dim &&
+                  ldq % 2 == 0 && ldk % 2 == 0 && ldv % 2 == 0 && ldo % 2 == 0 &&
+                  ldo >= (n_q_heads + 2) * head_dim,
+              FVX_ERR_SHAPE, "rope_backward: bad sizes");
+  FVX_REQUIRE(((uintptr_t)out & 3) == 0 && ((uintptr_t)dq & 7) == 0 &&
+                  ((uintptr_t)dk & 7) == 0 && ((uintptr_t)dv & 7) == 0,
+              FVX_ERR_ALIGN, "rope_backward: misaligned operand");
+  if (rows == 0) return FVX_OK;
+  const int64_t pairs = (n_q_heads + 2) * head_dim / 2;
+  hipLaunchKernelGGL(rope_backward_kernel, dim3(blocks(rows * pairs, 256)), dim3(256), 0,
+                     (hipStream_t)stream, dq, ldq, dk, ldk, dv, ldv, rope, positions,
+                     (bf16_t*)out, ldo, rows, (int)n_q_heads, (int)head_dim);
+  return launch_status("rope_backward");
+}
+
+extern "C" int fvx_rtc_vjp_error(const float* x, int64_t ldx, const float* u, int64_t ldu,
+                                 const float* prev, int64_t ldp, const float* w, void* e,
+                                 int64_t lde, int64_t rows, int64_t cols, int64_t period,
+                                 float omt, void* stream) {
+  clear_error();
+  FVX_REQUIRE(x && u && prev && w && e, FVX_ERR_NULL, "rtc_vjp_error: every operand is required");
+  FVX_REQUIRE(rows >= 0 && cols > 0 && period > 0 && ldx >= cols && ldu >= cols &&
+                  ldp >= cols && lde >= cols && cols < (1 << 30),
+              FVX_ERR_SHAPE, "rtc_vjp_error: bad sizes");
+  if (rows == 0) return FVX_OK;
+  hipLaunchKernelGGL(rtc_vjp_error_kernel, dim3(blocks(rows * cols, 256)), dim3(256), 0,
+                     (hipStream_t)stream, x, ldx, u, ldu, prev, ldp, w, (bf16_t*)e, lde,
+                     rows, (int)cols, period, omt);
+  return launch_status("rtc_vjp_error");
+}
+
+extern "C" int fvx_rtc_vjp_update(float* x, int64_t ldx, void* x_bf16, int64_t ldxb,
+                                  const float* u, int64_t ldu, const float* prev, int64_t ldp,
+                                  const float* w, const float* g, int64_t ldg,
+                                  const float* gw, int64_t rows, int64_t cols,
+                                  int64_t period, float omt, float dt, void* stream) {
+  clear_error();
+  FVX_REQUIRE(x && u && prev && w && g && gw, FVX_ERR_NULL,
+              "rtc_vjp_update: x, u, prev, w, g and gw are required");
+  FVX_REQUIRE(rows >= 0 && cols > 0 && period > 0 && ldx >= cols && ldu >= cols &&
+                  ldp >= cols && ldg >= cols && (!x_bf16 || ldxb >= cols) && cols < (1 << 30),
+              FVX_ERR_SHAPE, "rtc_vjp_update: bad sizes");
+  if (rows == 0) return FVX_OK;
+  hipLaunchKernelGGL(rtc_vjp_update_kernel, dim3(blocks(rows * cols, 256)), dim3(256), 0,
+                     (hipStream_t)stream, x, ldx, (bf16_t*)x_bf16, ldxb, u, ldu, prev, ldp, w,
+                     g, ldg, gw, rows, (int)cols, period, omt, dt);
+  return launch_status("rtc_vjp_update");
+}

@@ -14,7 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 OUT = os.path.join(PKG, 'libfluxvla_amd.so')
 OBJ_DIR = os.path.join(HERE, '_build')
-SOURCES = ['norm.hip', 'gemm.hip', 'attention.hip', 'misc.hip', 'preprocess.hip']
+SOURCES = ['norm.hip', 'gemm.hip', 'attention.hip', 'misc.hip', 'preprocess.hip',
+           'backward.hip']
 ARCH = 'gfx950'
 
 HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')

@@ -866,6 +866,183 @@ def rope_table(max_pos, head_dim, theta=10000.0, device=None):
     return t.to(device) if device is not None else t
 
 
+# ---------------------------------------------------------------------------
+# Backward ops (guidance real-time chunking with use_vjp)
+# ---------------------------------------------------------------------------
+def _mapped_rows(t, name, rows, row_group, row_group_stride):
+    """(leading dim) of a 2-D operand whose row m sits at
+    (m / row_group) * row_group_stride + m % row_group; checks it covers
+    the last mapped row."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f'{name} must be 2-D with unit column stride')
+    if rows:
+        last = rows - 1
+        if row_group:
+            last = (last // row_group) * row_group_stride + last % row_group
+        if last >= t.shape[0]:
+            raise ValueError(f'{name} has {t.shape[0]} rows, the map needs '
+                             f'{last + 1}')
+    return t.stride(0)
+
+
+def rms_norm_backward(x, dy, *, out=None, out_bf16=None, dres=None,
+                      scale=None, gate=None, eps=1e-6, row_group=0,
+                      row_group_stride=0):
+    """dx of y = x r (1 + scale) (fvx_rms_norm_backward): dy fp32 [rows,
+    cols] (compact); x bf16, dres / out fp32 and out_bf16 (= bf16(dx *
+    gate)) 2-D views whose row m is (m / row_group) * row_group_stride +
+    m % row_group.  scale / gate: bf16 [cols] or None."""
+    _check(dy, 'dy', dtype=torch.float32, contiguous=False)
+    rows, ldy = _rows_ld(dy, 'dy')
+    cols = dy.shape[-1]
+    if out is None and out_bf16 is None:
+        out = torch.empty(rows, cols, dtype=torch.float32, device=dy.device)
+    _check(x, 'x', contiguous=False)
+    ldx = _mapped_rows(x, 'x', rows, row_group, row_group_stride)
+    args = []
+    for t, nm, dt in ((dres, 'dres', torch.float32), (out, 'out', torch.float32),
+                      (out_bf16, 'out_bf16', BF16)):
+        if t is None:
+            args.append(0)
+            continue
+        _check(t, nm, dtype=dt, contiguous=False)
+        if t.shape[-1] != cols:
+            raise ValueError(f'{nm} must have {cols} columns')
+        args.append(_mapped_rows(t, nm, rows, row_group, row_group_stride))
+    for t, nm in ((scale, 'scale'), (gate, 'gate')):
+        _check(t, nm, contiguous=False, allow_none=True)
+        if t is not None and (t.numel() < cols or t.stride(-1) != 1):
+            raise ValueError(f'{nm} must hold {cols} contiguous values')
+    if x.shape[-1] != cols:
+        raise ValueError(f'x must have {cols} columns')
+    _lib.call('fvx_rms_norm_backward', _ptr(x), ldx, _ptr(dy), ldy,
+              _ptr(dres), args[0], _ptr(scale), _ptr(gate), _ptr(out),
+              args[1], _ptr(out_bf16), args[2], rows, cols, row_group,
+              row_group_stride, float(eps), _stream())
+    return out if out is not None else out_bf16
+
+
+def act_backward(act, inp, dy, out=None):
+    """GeGLU (act=ACT_BWD_GEGLU, inp = [gate | up] [rows, 2 cols]) or SiLU
+    (inp = z [rows, cols]) backward; dy bf16 [rows, cols]; out bf16 like
+    inp (fvx_act_backward)."""
+    _check(inp, 'inp', contiguous=False)
+    _check(dy, 'dy', contiguous=False)
+    rows, ldy = _rows_ld(dy, 'dy')
+    cols = dy.shape[-1]
+    width = 2 * cols if act == _lib.ACT_BWD_GEGLU else cols
+    if inp.shape[-1] != width:
+        raise ValueError(f'inp must have {width} columns')
+    if out is None:
+        out = torch.empty(rows, width, dtype=BF16, device=dy.device)
+    _check(out, 'out', contiguous=False)
+    _, ldi = _rows_ld(inp, 'inp')
+    _, ldo = _rows_ld(out, 'out')
+    _lib.call('fvx_act_backward', int(act), _ptr(inp), ldi, _ptr(dy), ldy,
+              _ptr(out), ldo, rows, cols, _stream())
+    return out
+
+
+def attention_rows_backward(s, dp, ds, *, heads, n_keys, scale, kgrp=None,
+                            qgrp=None, ds_t=None, p_t=None, key0=0,
+                            n_suffix=0):
+    """Masked softmax backward of one attention problem
+    (fvx_attention_rows_backward): s, dp fp32 [rows, >= n_keys]; ds bf16
+    [rows, n_cols]; ds_t / p_t bf16 [n_suffix, >= rows]."""
+    _check(s, 's', dtype=torch.float32, contiguous=False)
+    _check(dp, 'dp', dtype=torch.float32, contiguous=False)
+    _check(ds, 'ds', contiguous=False)
+    rows, lds = _rows_ld(s, 's')
+    _, lddp = _rows_ld(dp, 'dp')
+    _, ldds = _rows_ld(ds, 'ds')
+    if dp.shape[0] != rows or ds.shape[0] != rows:
+        raise ValueError('s, dp and ds must have the same rows')
+    if rows % heads:
+        raise ValueError('rows must be tokens * heads')
+    for t, nm in ((kgrp, 'kgrp'), (qgrp, 'qgrp')):
+        _check(t, nm, dtype=torch.int32, allow_none=True)
+    if kgrp is not None and (kgrp.numel() < n_keys or qgrp is None
+                             or qgrp.numel() < rows // heads):
+        raise ValueError('kgrp must cover n_keys and qgrp every token')
+    ldt = 0
+    for t, nm in ((ds_t, 'ds_t'), (p_t, 'p_t')):
+        if t is not None:
+            _check(t, nm, contiguous=False)
+            if t.shape[0] < n_suffix:
+                raise ValueError(f'{nm} must have n_suffix rows')
+            _, ld = _rows_ld(t, nm)
+            if ldt and ld != ldt:
+                raise ValueError('ds_t and p_t must share a leading dim')
+            ldt = ld
+    _lib.call('fvx_attention_rows_backward', _ptr(s), lds, _ptr(dp), lddp,
+              _ptr(kgrp), _ptr(qgrp), _ptr(ds), ldds, _ptr(ds_t), _ptr(p_t),
+              ldt, key0, n_suffix, rows, heads, n_keys, ds.shape[-1],
+              float(scale), _stream())
+    return ds
+
+
+def transpose(src, dst):
+    """dst[..., c, r] = src[..., r, c] for bf16 [rows, cols] or [batch, rows,
+    cols] views (unit column stride)."""
+    _check(src, 'src', contiguous=False)
+    _check(dst, 'dst', contiguous=False)
+    s3 = src if src.dim() == 3 else src[None]
+    d3 = dst if dst.dim() == 3 else dst[None]
+    if (s3.dim() != 3 or d3.dim() != 3 or s3.stride(-1) != 1 or d3.stride(-1) != 1
+            or d3.shape != (s3.shape[0], s3.shape[2], s3.shape[1])):
+        raise ValueError('transpose: dst must be src with its last two dims '
+                         'swapped, both with unit column stride')
+    _lib.call('fvx_transpose_bf16', _ptr(src), s3.stride(1), s3.stride(0),
+              _ptr(dst), d3.stride(1), d3.stride(0), s3.shape[1], s3.shape[2],
+              s3.shape[0], _stream())
+    return dst
+
+
+def rope_backward(dq, dk, dv, rope, positions, out, n_q_heads, head_dim):
+    """out bf16 [rows, (n_q_heads + 2) * head_dim] = [dq, dk rotated back |
+    dv] (fvx_rope_backward); dq / dk / dv fp32 2-D views."""
+    for t, nm in ((dq, 'dq'), (dk, 'dk'), (dv, 'dv'), (rope, 'rope')):
+        _check(t, nm, dtype=torch.float32, contiguous=(nm == 'rope'))
+    _check(positions, 'positions', dtype=torch.int32)
+    _check(out, 'out', contiguous=False)
+    rows, ldq = _rows_ld(dq, 'dq')
+    if positions.numel() < rows or dk.shape[0] != rows or dv.shape[0] != rows:
+        raise ValueError('dq, dk, dv and positions must cover the same rows')
+    _lib.call('fvx_rope_backward', _ptr(dq), ldq, _ptr(dk), dk.stride(0),
+              _ptr(dv), dv.stride(0), _ptr(rope), _ptr(positions), _ptr(out),
+              out.stride(0), rows, n_q_heads, head_dim, _stream())
+    return out
+
+
+def rtc_vjp_error(x, u, prev, w, e, omt):
+    """e = bf16(w[m % period] (prev - x + omt u)) (fvx_rtc_vjp_error); x, u,
+    prev fp32 [rows, cols]; w fp32 [period]."""
+    for t, nm in ((x, 'x'), (u, 'u'), (prev, 'prev'), (w, 'w')):
+        _check(t, nm, dtype=torch.float32, contiguous=False)
+    _check(e, 'e', contiguous=False)
+    rows, cols = x.shape
+    _lib.call('fvx_rtc_vjp_error', _ptr(x), x.stride(0), _ptr(u), u.stride(0),
+              _ptr(prev), prev.stride(0), _ptr(w), _ptr(e), e.stride(0), rows,
+              cols, w.numel(), float(omt), _stream())
+    return e
+
+
+def rtc_vjp_update(x, u, prev, w, g, gw, omt, dt, x_bf16=None):
+    """x <- x + dt u - dt gw e + dt gw omt g, e = w (prev - x + omt u)
+    (fvx_rtc_vjp_update); gw: device fp32 scalar (a 1-element view)."""
+    for t, nm in ((x, 'x'), (u, 'u'), (prev, 'prev'), (w, 'w'), (g, 'g'),
+                  (gw, 'gw')):
+        _check(t, nm, dtype=torch.float32, contiguous=False)
+    _check(x_bf16, 'x_bf16', contiguous=False, allow_none=True)
+    rows, cols = x.shape
+    _lib.call('fvx_rtc_vjp_update', _ptr(x), x.stride(0), _ptr(x_bf16),
+              x_bf16.stride(0) if x_bf16 is not None else 0, _ptr(u),
+              u.stride(0), _ptr(prev), prev.stride(0), _ptr(w), _ptr(g),
+              g.stride(0), _ptr(gw), rows, cols, w.numel(), float(omt),
+              float(dt), _stream())
+    return x
+
+
 
 # ---------------------------------------------------------------------------
 # Camera-frame preprocessing

@@ -488,6 +488,105 @@ typedef struct fvx_image_desc {
 
 int fvx_resize_normalize(const fvx_image_desc* desc, void* stream);
 
+/*
+ * Backward ops of the action expert for guidance real-time chunking with
+ * use_vjp: the correction J^T e that apply_rtc_guidance takes from torch
+ * autograd through the denoiser (fluxvla/engines/utils/rtc_guidance.py:
+ * 142-150).  The reference has no fused counterparts (autograd runs the
+ * backward of each torch op); the products with weights and attention
+ * operands go through fvx_gemm on transposed copies, these ops sit between
+ * them.  All fp32 arithmetic; bf16 outputs are the next GEMM's A operand.
+ */
+
+/* RMSNorm backward (GemmaRMSNorm, condition_gemma.py:75-80, with its
+ * (1 + w) gain folded into the next GEMM's weights; adaRMS (:126-145) with
+ * its (1 + scale) as `scale`):  g = dy * (1 + scale) (scale bf16 [cols] or
+ * NULL), r = rsqrt(mean(x^2) + eps),
+ *   dx = dres + r g - (r^3 / cols) (x . g) x.
+ * out (fp32, may be NULL) = dx; out_bf16 (may be NULL) = bf16(dx * gate)
+ * (gate bf16 [cols] or NULL: 1).  Rows of x, dres, out and out_bf16 follow
+ * the row-group map (m / row_group) * row_group_stride + m % row_group
+ * (identity for row_group 0); dy rows are compact.  cols % 8 == 0,
+ * cols <= 4096, leading dims multiples of 8, pointers 16-byte aligned. */
+int fvx_rms_norm_backward(const void* x, int64_t ldx, const float* dy,
+                          int64_t ldy, const float* dres, int64_t ldr,
+                          const void* scale, const void* gate, float* out,
+                          int64_t ldo, void* out_bf16, int64_t ldob,
+                          int64_t rows, int64_t cols, int64_t row_group,
+                          int64_t row_group_stride, float eps, void* stream);
+
+/* Activation backward, bf16 in and out (GemmaMLP's GeGLU,
+ * condition_gemma.py:156-192; the PI0 action-time MLP's SiLU,
+ * pi0_flowmatching.py:300-310):
+ *   FVX_ACT_BWD_GEGLU: in = [gate | up] ([rows, 2 cols]), dy = dh ->
+ *     out = [dh * up * gelu_tanh'(gate) | dh * gelu_tanh(gate)]
+ *   FVX_ACT_BWD_SILU: in = z ([rows, cols]) -> out = dy * silu'(z)
+ * cols % 8 == 0, leading dims multiples of 8, pointers 16-byte aligned. */
+#define FVX_ACT_BWD_GEGLU 0
+#define FVX_ACT_BWD_SILU 1
+int fvx_act_backward(int act, const void* in, int64_t ldi, const void* dy,
+                     int64_t ldy, void* out, int64_t ldo, int64_t rows,
+                     int64_t cols, void* stream);
+
+/* Masked-softmax backward of one attention problem
+ * (condition_gemma.py:340-535's eager attention, softmax over
+ * scale * q k^T with the make_att_2d_masks rule of model_utils.py:77-95):
+ * row r is query token r / heads; s = q . k and dp = dO . v (fp32
+ * [rows, lds / lddp]); key j visible iff kgrp[j] <= qgrp[r / heads] (both
+ * NULL: all visible).  P = softmax of the visible logits, D = sum P dp,
+ *   ds[r][j] = bf16(scale P (dp - D))  for j < n_cols (0 past n_keys and
+ *   on masked keys).
+ * ds_t / p_t (bf16 [n_suffix, ldt], may be NULL): column r receives ds and
+ * P of keys key0 .. key0 + n_suffix - 1 (the A operands of dK = ds^T Q and
+ * dV = P^T dO). */
+int fvx_attention_rows_backward(const float* s, int64_t lds, const float* dp,
+                                int64_t lddp, const int32_t* kgrp,
+                                const int32_t* qgrp, void* ds, int64_t ldds,
+                                void* ds_t, void* p_t, int64_t ldt,
+                                int64_t key0, int64_t n_suffix, int64_t rows,
+                                int64_t heads, int64_t n_keys, int64_t n_cols,
+                                float scale, void* stream);
+
+/* bf16 transpose: dst[b][c][r] = src[b][r][c] for b < batch, r < rows,
+ * c < cols (element offsets b * batch_stride + row * ld). */
+int fvx_transpose_bf16(const void* src, int64_t ld_src,
+                       int64_t src_batch_stride, void* dst, int64_t ld_dst,
+                       int64_t dst_batch_stride, int64_t rows, int64_t cols,
+                       int64_t batch, void* stream);
+
+/* RoPE backward packed into the Q|K|V GEMM's dY: row m of out (bf16) =
+ * [dq (n_q_heads heads) | dk | dv], each head's column pair (2i, 2i+1)
+ * of dq and dk rotated by the transpose of the forward rotation at
+ * rope[positions[m]][i] (fp32 (cos, sin) pairs, the fvx_gemm QKV_ROPE
+ * table): (ga, gb) -> (ga cos + gb sin, gb cos - ga sin). */
+int fvx_rope_backward(const float* dq, int64_t ldq, const float* dk,
+                      int64_t ldk, const float* dv, int64_t ldv,
+                      const float* rope, const int32_t* positions, void* out,
+                      int64_t ldo, int64_t rows, int64_t n_q_heads,
+                      int64_t head_dim, void* stream);
+
+/* Guidance error and corrected update of one Euler step with use_vjp
+ * (apply_rtc_guidance, rtc_guidance.py:107-155, under
+ * _predict_action_guidance_rtc, pi0_flowmatching.py:671-700, whose
+ * denoiser is -u for the model velocity u; omt = 1 - t of the step).
+ * Row m is action step m % period of its sample, w fp32 [period] the
+ * prefix weights (zero past the previous chunk):
+ *   fvx_rtc_vjp_error:  e = bf16(w (prev - x + omt u))
+ *   fvx_rtc_vjp_update: x <- x + dt u - dt gw e + dt gw omt g, with e in
+ *                       fp32 as above, g = J_u^T e, gw = *gw (device, the
+ *                       step's guidance weight); x_bf16 (may be NULL)
+ *                       receives the bf16 copy. */
+int fvx_rtc_vjp_error(const float* x, int64_t ldx, const float* u,
+                      int64_t ldu, const float* prev, int64_t ldp,
+                      const float* w, void* e, int64_t lde, int64_t rows,
+                      int64_t cols, int64_t period, float omt, void* stream);
+int fvx_rtc_vjp_update(float* x, int64_t ldx, void* x_bf16, int64_t ldxb,
+                       const float* u, int64_t ldu, const float* prev,
+                       int64_t ldp, const float* w, const float* g,
+                       int64_t ldg, const float* gw, int64_t rows,
+                       int64_t cols, int64_t period, float omt, float dt,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,237 @@
+"""Parity of the backward ops behind guidance RTC with use_vjp
+(csrc/backward.hip) against float64 torch autograd of the forward op on
+the same inputs (the CPU), each op at the action expert's shapes.
+
+Bars: fp32 outputs within 1e-4 relative (max|out - ref| / max|ref|; the
+kernels compute in fp32), bf16 outputs within 1e-2 (one bf16 rounding),
+index/byte work (transposes) bit-exact.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+BF16_TOL = 1e-2
+
+
+def rel_err(out, ref):
+    out = out.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return ((out - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+def randn(shape, seed, std=1.0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+@pytest.fixture(scope='module')
+def K():
+    from fluxvla_amd import kernels
+    kernels._lib.load()
+    return kernels
+
+
+def rms_ref(x, dy, scale=None, dres=None, eps=1e-6):
+    """float64 autograd of y = x rsqrt(mean(x^2) + eps) (1 + scale)."""
+    xd = x.double().cpu().requires_grad_(True)
+    y = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + eps)
+    if scale is not None:
+        y = y * (1.0 + scale.double().cpu())
+    (g,) = torch.autograd.grad(y, xd, dy.double().cpu())
+    return g + (dres.double().cpu() if dres is not None else 0.0)
+
+
+@pytest.mark.parametrize('cols', [1024, 2048, 32 * 8])
+@pytest.mark.parametrize('with_scale', [False, True])
+def test_rms_norm_backward(K, cuda, cols, with_scale):
+    announce(f'rms_norm_backward cols={cols} scale={with_scale}')
+    m = 51
+    x = randn((m, cols), 1, std=2.0)
+    dy = randn((m, cols), 2, dtype=torch.float32)
+    dres = randn((m, cols), 3, dtype=torch.float32)
+    scale = randn((cols,), 4, std=0.3) if with_scale else None
+    gate = randn((cols,), 5, std=0.5)
+    out = torch.empty(m, cols, dtype=torch.float32, device=cuda)
+    outb = torch.empty(m, cols, dtype=torch.bfloat16, device=cuda)
+    K.rms_norm_backward(x.to(cuda), dy.to(cuda), out=out, out_bf16=outb,
+                        dres=dres.to(cuda),
+                        scale=scale.to(cuda) if with_scale else None,
+                        gate=gate.to(cuda), eps=1e-6)
+    ref = rms_ref(x, dy, scale, dres)
+    assert rel_err(out, ref) <= F32_TOL
+    assert rel_err(outb, ref * gate.double()) <= BF16_TOL
+
+
+def test_rms_norm_backward_row_groups(K, cuda):
+    """Rows mapped through groups (the action rows behind each sample's
+    state row): x / out rows (m / 50) * 51 + 1 + m % 50; rows outside the
+    map stay untouched."""
+    announce('rms_norm_backward row groups')
+    B, Ss, na, cols = 3, 51, 50, 1024
+    x = randn((B * Ss, cols), 11)
+    dy = randn((B * na, cols), 12, dtype=torch.float32)
+    out = torch.full((B * Ss, cols), 7.0, device=cuda)
+    xg = x.to(cuda)
+    # the view starting at row 1 of sample 0
+    K.rms_norm_backward(xg[1:], dy.to(cuda), out=out[1:], row_group=na,
+                        row_group_stride=Ss)
+    xs = x.view(B, Ss, cols)[:, 1:].reshape(-1, cols)
+    ref = rms_ref(xs, dy)
+    got = out.view(B, Ss, cols)[:, 1:].reshape(-1, cols)
+    assert rel_err(got, ref) <= F32_TOL
+    assert (out.view(B, Ss, cols)[:, 0].cpu() == 7.0).all()
+
+
+def test_geglu_backward(K, cuda):
+    announce('act_backward geglu')
+    m, n = 51, 4096
+    gu = randn((m, 2 * n), 21, std=1.5)
+    dh = randn((m, n), 22)
+    out = K.act_backward(K._lib.ACT_BWD_GEGLU, gu.to(cuda), dh.to(cuda))
+    g = gu[:, :n].double().requires_grad_(True)
+    u = gu[:, n:].double().requires_grad_(True)
+    h = F.gelu(g, approximate='tanh') * u
+    dg, du = torch.autograd.grad(h, (g, u), dh.double())
+    assert rel_err(out[:, :n], dg) <= BF16_TOL
+    assert rel_err(out[:, n:], du) <= BF16_TOL
+
+
+def test_silu_backward(K, cuda):
+    announce('act_backward silu')
+    m, n = 50, 1024
+    z = randn((m, n), 31, std=3.0)
+    dy = randn((m, n), 32)
+    out = K.act_backward(K._lib.ACT_BWD_SILU, z.to(cuda), dy.to(cuda))
+    zd = z.double().requires_grad_(True)
+    (ref,) = torch.autograd.grad(F.silu(zd), zd, dy.double())
+    assert rel_err(out, ref) <= BF16_TOL
+
+
+def softmax_bwd_ref(s, dp, vis, scale):
+    sd = s.double().cpu().requires_grad_(True)
+    logits = (sd * scale).masked_fill(~vis, float('-inf'))
+    p = torch.softmax(logits, -1).nan_to_num(0.0)
+    (ds,) = torch.autograd.grad(p, sd, dp.double().cpu())
+    return p.detach(), ds
+
+
+def test_attention_rows_backward(K, cuda):
+    """The expert's suffix rows (51 tokens x 8 heads) over 816 prefix keys
+    with padding and the block-causal suffix pattern; ds matches autograd of
+    the masked softmax, ds_t / p_t hold the suffix columns transposed."""
+    announce('attention_rows_backward')
+    S, Ss, H, T = 816, 51, 8, 872
+    nk = S + Ss
+    rows = Ss * H
+    scale = 256 ** -0.5
+    s = randn((rows, T), 41, std=20.0, dtype=torch.float32)
+    dp = randn((rows, T), 42, dtype=torch.float32)
+    kgrp = torch.zeros(nk, dtype=torch.int32)
+    kgrp[700:S] = 2**31 - 1  # padded prefix keys
+    suf = torch.cumsum(torch.tensor([1, 1] + [0] * (Ss - 2)), 0).int()
+    kgrp[S:] = suf
+    qgrp = suf.clone()
+    ds = torch.full((rows, T), float('nan'), dtype=torch.bfloat16, device=cuda)
+    ds_t = torch.zeros(Ss, rows, dtype=torch.bfloat16, device=cuda)
+    p_t = torch.zeros(Ss, rows, dtype=torch.bfloat16, device=cuda)
+    K.attention_rows_backward(s.to(cuda), dp.to(cuda), ds, heads=H, n_keys=nk,
+                              scale=scale, kgrp=kgrp.to(cuda),
+                              qgrp=qgrp.to(cuda), ds_t=ds_t, p_t=p_t, key0=S,
+                              n_suffix=Ss)
+    tok = torch.arange(rows) // H
+    vis = kgrp[None, :].long() <= qgrp[tok][:, None].long()
+    p, ref = softmax_bwd_ref(s[:, :nk], dp[:, :nk], vis, scale)
+    got = ds.cpu()
+    assert torch.isfinite(got.float()).all()
+    assert rel_err(got[:, :nk], ref) <= BF16_TOL
+    assert (got[:, nk:].float() == 0).all()
+    assert (got[:, :nk].float()[~vis] == 0).all()
+    assert rel_err(ds_t.t(), ref[:, S:]) <= BF16_TOL
+    assert rel_err(p_t.t(), p[:, S:]) <= BF16_TOL
+
+
+@pytest.mark.parametrize('shape', [(3, 816, 256), (1, 51, 2048), (2, 37, 45)])
+def test_transpose(K, cuda, shape):
+    announce(f'transpose {shape}')
+    src = randn(shape, 51).to(cuda)
+    dst = torch.empty(shape[0], shape[2], shape[1], dtype=torch.bfloat16,
+                      device=cuda)
+    K.transpose(src, dst)
+    assert torch.equal(dst.cpu(), src.cpu().transpose(1, 2))
+
+
+def test_transpose_strided_views(K, cuda):
+    """Cache slices: a [B, rows, D] slab of a longer cache into columns of
+    a [B, D, T] one."""
+    announce('transpose strided views')
+    B, T, D, S, Ss = 2, 872, 256, 816, 51
+    kc = randn((B, T, D), 52).to(cuda)
+    kt = torch.zeros(B, D, T, dtype=torch.bfloat16, device=cuda)
+    K.transpose(kc[:, S:S + Ss], kt[:, :, S:S + Ss])
+    want = torch.zeros(B, D, T, dtype=torch.bfloat16)
+    want[:, :, S:S + Ss] = kc.cpu()[:, S:S + Ss].transpose(1, 2)
+    assert torch.equal(kt.cpu(), want)
+
+
+def test_rope_backward(K, cuda):
+    """Against float64 autograd of the forward rotation of pair (2i, 2i+1)
+    by the fp32 table entry at the row's position."""
+    announce('rope_backward')
+    m, H, D = 51, 8, 256
+    rope = K.rope_table(1024, D)
+    pos = torch.randint(0, 1024, (m,), generator=torch.Generator().manual_seed(3),
+                        dtype=torch.int32)
+    dq = randn((m, H * D), 61, dtype=torch.float32)
+    dk = randn((m, D), 62, dtype=torch.float32)
+    dv = randn((m, D), 63, dtype=torch.float32)
+    out = torch.empty(m, (H + 2) * D, dtype=torch.bfloat16, device=cuda)
+    K.rope_backward(dq.to(cuda), dk.to(cuda), dv.to(cuda), rope.to(cuda),
+                    pos.to(cuda), out, H, D)
+    cs = rope[pos.long()].double()  # [m, D/2, 2]
+    c, s = cs[..., 0], cs[..., 1]
+
+    def fwd(x, heads):
+        x = x.view(m, heads, D // 2, 2)
+        a, b = x[..., 0], x[..., 1]
+        return torch.stack([a * c[:, None] - b * s[:, None],
+                            b * c[:, None] + a * s[:, None]], -1).reshape(m, -1)
+
+    q = torch.zeros(m, H * D, dtype=torch.float64, requires_grad=True)
+    k = torch.zeros(m, D, dtype=torch.float64, requires_grad=True)
+    gq, gk = torch.autograd.grad((fwd(q, H), fwd(k, 1)), (q, k),
+                                 (dq.double(), dk.double()))
+    got = out.cpu()
+    assert rel_err(got[:, :H * D], gq) <= BF16_TOL
+    assert rel_err(got[:, H * D:(H + 1) * D], gk) <= BF16_TOL
+    assert torch.equal(got[:, (H + 1) * D:], dv.to(torch.bfloat16))
+
+
+def test_rtc_vjp_error_and_update(K, cuda):
+    announce('rtc_vjp error / update')
+    B, na, ad = 2, 50, 32
+    x = randn((B * na, ad), 71, dtype=torch.float32)
+    u = randn((B * na, ad), 72, dtype=torch.float32)
+    prev = randn((B * na, ad), 73, dtype=torch.float32)
+    g = randn((B * na, ad), 74, dtype=torch.float32)
+    w = torch.rand(na, generator=torch.Generator().manual_seed(75))
+    w[30:] = 0
+    omt, dt, gw = 0.7, -0.1, 3.25
+    e = torch.empty(B * na, ad, dtype=torch.bfloat16, device=cuda)
+    K.rtc_vjp_error(x.to(cuda), u.to(cuda), prev.to(cuda), w.to(cuda), e, omt)
+    wr = w.double().repeat(B)[:, None]
+    ref_e = wr * (prev.double() - x.double() + omt * u.double())
+    assert rel_err(e, ref_e) <= BF16_TOL
+    xg = x.to(cuda)
+    xb = torch.empty(B * na, ad, dtype=torch.bfloat16, device=cuda)
+    gwt = torch.tensor([gw], dtype=torch.float32, device=cuda)
+    K.rtc_vjp_update(xg, u.to(cuda), prev.to(cuda), w.to(cuda), g.to(cuda),
+                     gwt, omt, dt, x_bf16=xb)
+    ref = (x.double() + dt * u.double() - dt * gw * ref_e
+           + dt * gw * omt * g.double())
+    assert rel_err(xg, ref) <= F32_TOL
+    assert torch.equal(xb.cpu(), xg.cpu().to(torch.bfloat16))
