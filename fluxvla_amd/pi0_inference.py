@@ -298,6 +298,7 @@ class PI0Inference:
     @torch.no_grad()
     def prepare_triton_inference(self, sd):
         cfg, dev = self.cfg, self.device
+        self._vjp = None  # rebuilt from these weights on first use
         self.vis = prepare_siglip(sd, cfg, dev)
         self.llm = prepare_gemma(sd, cfg, 'llm', dev)
         self.exp = prepare_gemma(sd, cfg, 'expert', dev)
@@ -569,6 +570,10 @@ class PI0Inference:
                           dt=torch.float32),
             'rtc_cw': e(len(self.times), cfg.n_action_steps,
                         dt=torch.float32),
+            # guidance with use_vjp: the prefix weights (zero past the
+            # previous chunk) and each step's guidance weight
+            'rtc_w': e(cfg.n_action_steps, dt=torch.float32),
+            'rtc_gw': e(len(self.times), dt=torch.float32),
         }
         if not cfg.pi05:
             # PI0 suffix stream = [state_emb, mlp_out(silu(mlp_in(...)))]:
@@ -826,8 +831,11 @@ class PI0Inference:
         (pi05_flowmatching_inference.py:155-312 / pi0_flowmatching.py:
         642-649, 787-831): suffix embedding, expert layers against the
         cached prefix K/V, final norm + action_out_proj + Euler update fused
-        in one GEMM epilogue.  ``rtc``: None, 'prefix' or 'guidance' (real-
-        time chunking, pi0_flowmatching.py:651-700; see fluxvla_amd.rtc)."""
+        in one GEMM epilogue.  ``rtc``: None, 'prefix', 'guidance' or
+        'guidance_vjp' (real-time chunking, pi0_flowmatching.py:651-700; see
+        fluxvla_amd.rtc; the last runs fluxvla_amd.vjp's loop)."""
+        if rtc == 'guidance_vjp':
+            return self._vjp_engine().decoder(b, B)
         cfg = self.cfg
         Ss, na, hid = cfg.suffix_len, cfg.n_action_steps, cfg.exp_hidden
         x3 = b['ex_x']
@@ -902,6 +910,14 @@ class PI0Inference:
                     'rtc_cw': b['rtc_cw'][step],
                     'rtc_omt': self._rtc_omt[step]}
         return {}
+
+    def _vjp_engine(self):
+        """The VJP step of guidance with use_vjp (fluxvla_amd.vjp), built on
+        first use: transposed weights and saved-activation buffers."""
+        if self._vjp is None:
+            from .vjp import ExpertVJP
+            self._vjp = ExpertVJP(self)
+        return self._vjp
 
     def _run(self, B, rtc=None):
         b = self._buffers(B)
@@ -978,8 +994,14 @@ class PI0Inference:
                 raise ValueError(f'prev_actions has {L} rows, the chunk {na}')
             b['rtc_prev'].zero_()
             b['rtc_prev'][:, :L].copy_(prev)
-            b['rtc_cw'].copy_(R.guidance_cw(self.times, self.dt, na,
-                                            prefix_len, L, rtc_config))
+            if rtc == 'guidance_vjp':
+                w, gw = R.guidance_vjp_tables(self.times, na, prefix_len, L,
+                                              rtc_config)
+                b['rtc_w'].copy_(w)
+                b['rtc_gw'].copy_(gw)
+            else:
+                b['rtc_cw'].copy_(R.guidance_cw(self.times, self.dt, na,
+                                                prefix_len, L, rtc_config))
 
     def _capture(self, B, rtc=None):
         g = torch.cuda.CUDAGraph()
@@ -1002,7 +1024,8 @@ class PI0Inference:
                        rtc_config: dict = None, *args, **kwargs):
         """The reference signature (pi0_flowmatching.py:702-715), real-time
         chunking included: with prev_actions, prefix_len > 0 and rtc_config
-        the loop is the 'prefix' (default) or 'guidance' method."""
+        the loop is the 'prefix' (default) or 'guidance' method, the latter
+        with rtc_config['use_vjp'] pulled back through the expert."""
         cfg = self.cfg
         B = images.shape[0]
         if B > self.max_batch:

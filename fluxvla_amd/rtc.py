@@ -16,6 +16,10 @@ inside the captured chunk graph, folded into kernels that already run:
   update as x + dt v + cw_r (prev - x + time v) with cw_r = -dt * gw(step) *
   w_r, read from a per-step table that depends only on the request's RTC
   settings.
+* guidance with use_vjp ('guidance_vjp'): the error pulled back through the
+  expert's Jacobian, J^T e, by the backward pass of fluxvla_amd.vjp; the
+  update reads the prefix weights and per-step guidance weights from device
+  tables (guidance_vjp_tables).
 
 ``compute_prefix_weights`` and ``compute_guidance_weight`` keep the
 reference's names and arguments (rtc_guidance.py:28-104).
@@ -78,9 +82,9 @@ def select_method(prev_actions, prefix_len, rtc_config):
         # the reference falls through to the plain loop for other names
         return None
     if method == 'guidance' and rtc_config.get('use_vjp', False):
-        raise NotImplementedError(
-            'guidance RTC with use_vjp=True backpropagates through the action '
-            'expert; this inference path has no backward pass')
+        # the correction pulled back through the expert's Jacobian
+        # (fluxvla_amd.vjp)
+        return 'guidance_vjp'
     return method
 
 
@@ -117,3 +121,20 @@ def guidance_cw(times, dt, n_action_steps, prefix_len, prev_len, rtc_config):
     max_gw = rtc_config.get('max_guidance_weight', 5.0)
     return torch.stack([-dt * compute_guidance_weight(1.0 - time, max_gw) * w
                         for time in times]).float()
+
+
+def guidance_vjp_tables(times, n_action_steps, prefix_len, prev_len,
+                        rtc_config):
+    """Device tables of the guidance update with use_vjp: the prefix weights
+    w (fp32 [n_action_steps], zero from prev_len on: those positions have no
+    previous action) and each step's guidance weight gw (fp32 [steps])
+    (_predict_action_guidance_rtc, pi0_flowmatching.py:671-700;
+    rtc_guidance.py:28-104)."""
+    w = compute_prefix_weights(n_action_steps, prefix_len,
+                               rtc_config.get('decay_end', prefix_len * 2),
+                               rtc_config.get('schedule', 'exp'))
+    w[prev_len:] = 0.0
+    max_gw = rtc_config.get('max_guidance_weight', 5.0)
+    gw = torch.tensor([compute_guidance_weight(1.0 - time, max_gw)
+                       for time in times], dtype=torch.float32)
+    return w, gw

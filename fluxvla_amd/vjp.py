@@ -1,0 +1,298 @@
+"""Guidance real-time chunking with ``use_vjp``: the action expert's
+vector-Jacobian product on the GPU.
+
+apply_rtc_guidance (fluxvla/engines/utils/rtc_guidance.py:107-155, under
+_predict_action_guidance_rtc, pi0_flowmatching.py:671-700) takes, with
+use_vjp, the correction c = (d x_1 / d x_t)^T e from torch autograd through
+the whole denoiser, x_1 = x_t - (1 - t) u(x_t) for the model velocity u and
+e = w (prev - x_1) on the previous chunk's rows.  Here one Euler step is
+
+  forward   the expert as in the plain loop, keeping each layer's input
+            stream X[i], its post-attention stream X2[i] and its rotated
+            queries Q[i] (the key/value cache already holds the suffix
+            keys and values); u from a PLAIN fp32 GEMM of action_out_proj;
+  error     e = bf16(w (prev - x + (1 - t) u))                (one kernel);
+  backward  g = J_u^T e layer by layer, last to first:
+              down:       dh = (gate2 dX3) @ W_down
+              GeGLU:      [gg | uu] recomputed from X2 (two GEMMs), the
+                          activation backward, da = d[gg | uu] @ [Wg; Wu]
+              norm:       dX2 = dX3 + RMSNorm-backward(X2, da)
+              O:          dO = (gate1 dX2) @ W_o
+              attention:  S = Q K^T, dP = dO V^T (fp32), the masked softmax
+                          backward per row, dQ = dS K, dK = dS^T Q and
+                          dV = P^T dO on the suffix keys (the prefix cache
+                          is a constant of x_t), RoPE backward
+              QKV:        da = d[q | k | v] @ W_qkv
+              norm:       dX = dX2 + RMSNorm-backward(X, da)
+            and through the suffix embedding (PI0: action-time MLP with
+            its SiLU; PI0.5: action_in_proj) to g = dL/dx_t;
+  update    x <- x + dt u - dt gw e + dt gw (1 - t) g              (one kernel).
+
+Every product runs through fvx_gemm: the weights' products use [in, out]
+copies of the prepared [out, in] weights (fp8 weights dequantized to bf16),
+the attention's products transposed copies of the key cache, of the value
+cache (row-major), of Q and of dO.  All of it is part of the captured chunk
+graph: per-request values (previous chunk, weights, guidance weights) are
+device buffers.
+"""
+import torch
+
+from . import _lib
+from . import kernels as K
+
+BF16 = torch.bfloat16
+
+
+def _weight_t(w):
+    """bf16 [in, out] copy of a prepared [out, in] weight (bf16 or row-major
+    fp8, dequantized): the B operand of dX = dY @ W."""
+    if isinstance(w, K.Fp8Weight):
+        w = w.dequantize()
+    return w.t().contiguous().to(BF16)
+
+
+class ExpertVJP:
+    """Transposed weights, saved activations and scratch of the VJP step
+    for one model; buffers per batch size."""
+
+    def __init__(self, model):
+        self.m = m = model
+        cfg = m.cfg
+        self.wT = []
+        for L in m.exp['layers']:
+            gu = torch.cat([_weight_t(L['gate_w']), _weight_t(L['up_w'])], 1)
+            self.wT.append({'qkv': _weight_t(L['qkv_w']),
+                            'o': _weight_t(L['o_w']),
+                            'gu': gu.contiguous(),
+                            'down': _weight_t(L['down_w'])})
+        self.out_t = _weight_t(m.act_out['w'])       # [hid, action_dim]
+        if cfg.pi05:
+            self.in_t = _weight_t(m.act_in['w'])     # [action_dim, hid]
+        else:
+            self.mo_t = _weight_t(m.mlp_out['w'])    # [proj_width, hid]
+            self.mi_t = _weight_t(m.mlp_in_x)        # [action_dim, proj]
+        self.scale = cfg.head_dim ** -0.5
+        self._bufs = {}
+
+    # -- buffers -------------------------------------------------------------
+    def buffers(self, B):
+        if B in self._bufs:
+            return self._bufs[B]
+        m, cfg, dev = self.m, self.m.cfg, self.m.device
+        S, Ss, D, H = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.heads
+        na, hid, mlp = cfg.n_action_steps, cfg.exp_hidden, cfg.exp_mlp
+        T, nL, ad = m.kv_len, cfg.exp_layers, cfg.max_action_dim
+        R = Ss * H
+
+        def e(*shape, dt=BF16):
+            return torch.empty(*shape, dtype=dt, device=dev)
+
+        def z(*shape, dt=BF16):
+            return torch.zeros(*shape, dtype=dt, device=dev)
+        v = {
+            'X': e(nL + 1, B * Ss, hid), 'X2': e(nL, B * Ss, hid),
+            'Q': e(nL, B * Ss, H * D), 'ctx': e(B, Ss, H * D),
+            'h': e(B * Ss, mlp), 'xn': e(B * Ss, hid), 'gate': e(B * Ss, hid),
+            # key cache transposed [layer][batch][dim][token] and value cache
+            # row-major [layer][batch][token][dim]; the columns / rows past
+            # the keys stay zero (the dQ GEMM's K runs over them)
+            'kT': z(nL, B, D, T), 'vr': z(nL, B, T, D),
+            'u': e(B * na, ad, dt=torch.float32), 'e': e(B * na, ad),
+            'g': e(B * na, ad, dt=torch.float32),
+            'dx': [e(B * Ss, hid, dt=torch.float32) for _ in range(2)],
+            'da': e(B * Ss, hid, dt=torch.float32), 'a': e(B * Ss, hid),
+            'dh': e(B * Ss, mlp), 'gu': e(B * Ss, 2 * mlp),
+            'dgu': e(B * Ss, 2 * mlp), 'dctx': e(B, Ss, H * D),
+            's': e(R, T, dt=torch.float32), 'dp': e(R, T, dt=torch.float32),
+            'ds': e(R, T), 'ds_t': e(Ss, R), 'p_t': e(Ss, R),
+            'qT': e(B, D, R), 'dOT': e(B, D, R),
+            'dq': e(B * Ss, H * D, dt=torch.float32),
+            'dk': e(B * Ss, D, dt=torch.float32),
+            'dv': e(B * Ss, D, dt=torch.float32),
+            'dqkv': e(B * Ss, (H + 2) * D),
+        }
+        if not cfg.pi05:
+            v['z'] = e(B * na, cfg.proj_width)
+            v['dsh'] = e(B * na, cfg.proj_width)
+            v['dz'] = e(B * na, cfg.proj_width)
+        self._bufs[B] = v
+        return v
+
+    # -- the chunk -------------------------------------------------------------
+    def decoder(self, b, B):
+        """The Euler loop with the VJP-corrected guidance update (replaces
+        PI0Inference.transformer_decoder for this method)."""
+        m, cfg = self.m, self.m.cfg
+        v = self.buffers(B)
+        S, Ss, hid = cfg.prefix_len, cfg.suffix_len, cfg.exp_hidden
+        nL = cfg.exp_layers
+        # the prefix part of every layer's transposed key / row-major value
+        # cache, once per chunk
+        kc = b['kc'].view(nL * B, m.kv_len, cfg.head_dim)
+        vc = b['vc'].view(nL * B, cfg.head_dim, m.kv_len)
+        K.transpose(kc[:, :S], v['kT'].view(nL * B, cfg.head_dim, m.kv_len)[:, :, :S])
+        K.transpose(vc[:, :, :S], v['vr'].view(nL * B, m.kv_len, cfg.head_dim)[:, :S])
+        if not cfg.pi05:
+            K.gemm(b['states'], m.state['w'], out=b['suf_res'],
+                   bias=m.state['b'], row_group=1, row_group_stride=Ss)
+        for step in range(len(m.times)):
+            self.forward(b, B, step)
+            self.backward(b, B, step)
+
+    def forward(self, b, B, step):
+        """Suffix embedding, expert layers with saved streams, u and e."""
+        m, cfg, v = self.m, self.m.cfg, self._bufs[B]
+        S, Ss, D, H = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.heads
+        na, hid, T = cfg.n_action_steps, cfg.exp_hidden, m.kv_len
+        X, X2, Q = v['X'], v['X2'], v['Q']
+        xt_b = b['xt_bf16'].view(B * na, -1)
+        if cfg.pi05:
+            K.gemm(xt_b, m.act_in['w'], out=X[0], bias=m.act_in['b'])
+        else:
+            h = b['suf_h']  # the state rows stay zero
+            K.gemm(xt_b, m.mlp_in_x, out=h[1:], bias_f32=m.step_bias[step],
+                   act=_lib.ACT_SILU, row_group=na, row_group_stride=Ss)
+            K.gemm(xt_b, m.mlp_in_x, out=v['z'], bias_f32=m.step_bias[step])
+            K.gemm(h, m.mlp_out['w'], out=X[0], residual=b['suf_res'])
+        st = m.styles[step] if cfg.pi05 else None
+        for i, L in enumerate(m.exp['layers']):
+            kc, vc = b['kc'][i], b['vc'][i]
+            x = X[i]
+            if cfg.pi05:
+                K.adarms_norm(x, st[2 * i:2 * i + 1], out=v['xn'],
+                              gate_out=v['gate'], eps=cfg.rms_eps)
+                a, rn = v['xn'], None
+            else:
+                a, rn = x, cfg.rms_eps
+            K.gemm_qkv_rope(a, L['qkv_w'], m.rope, b['pos_suf'], Q[i],
+                            kc.view(B * T, D)[S:], vc[:, :, S:], H, D,
+                            rownorm_eps=rn, row_group=Ss, row_group_stride=T,
+                            v_ld=T)
+            K.mqa_attention(Q[i].view(B, Ss, H * D), kc[:, :S + Ss], vc,
+                            v['ctx'], kgrp=b['kgrp'], qgrp=b['qgrp_suf'],
+                            v_transposed=True)
+            gate = v['gate'] if cfg.pi05 else None
+            K.gemm(v['ctx'].view(B * Ss, -1), L['o_w'], out=X2[i], residual=x,
+                   gate=gate)
+            if cfg.pi05:
+                K.adarms_norm(X2[i], st[2 * i + 1:2 * i + 2], out=v['xn'],
+                              gate_out=v['gate'], eps=cfg.rms_eps)
+                K.gemm_geglu(v['xn'], L['gate_w'], L['up_w'], out=v['h'])
+            else:
+                K.gemm_geglu(X2[i], L['gate_w'], L['up_w'], out=v['h'],
+                             rownorm_eps=cfg.rms_eps)
+            K.gemm(v['h'], L['down_w'], out=X[i + 1], residual=X2[i],
+                   gate=gate)
+        lead = Ss - na
+        last = X[-1].view(B, Ss, hid)
+        if cfg.pi05:
+            K.adarms_norm(X[-1], st[-1:], out=v['xn'], eps=cfg.rms_eps)
+            K.gemm(v['xn'], m.act_out['w'], out=v['u'], bias=m.act_out['b'],
+                   out_f32=True)
+        else:
+            K.gemm(last[:, lead:], m.act_out['w'], out=v['u'],
+                   bias=m.act_out['b'], rownorm_eps=cfg.rms_eps, out_f32=True)
+        K.rtc_vjp_error(b['xt'].view(B * na, -1), v['u'],
+                        b['rtc_prev'].view(B * na, -1), b['rtc_w'], v['e'],
+                        m._rtc_omt[step])
+
+    def backward(self, b, B, step):
+        """g = J_u^T e through the expert and the suffix embedding, then the
+        corrected Euler update."""
+        m, cfg, v = self.m, self.m.cfg, self._bufs[B]
+        S, Ss, D, H = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.heads
+        na, hid, mlp, T = (cfg.n_action_steps, cfg.exp_hidden, cfg.exp_mlp,
+                           m.kv_len)
+        nk, R, eps = S + Ss, Ss * H, cfg.rms_eps
+        X, X2, Q = v['X'], v['X2'], v['Q']
+        lead = Ss - na
+        w = hid
+        st = m.styles[step] if cfg.pi05 else None
+
+        def gate2(i):  # the MLP branch's gate of layer i (PI0.5)
+            return st[2 * i + 1, 2 * w:] if (cfg.pi05 and i >= 0) else None
+
+        nL = len(m.exp['layers'])
+        dx, dx2 = v['dx']
+        # d(final norm output) = e @ W_out, then the final norm's backward
+        # onto the action rows (the state row of PI0 gets none)
+        dxn = v['da'][:B * na]
+        K.gemm(v['e'], self.out_t, out=dxn, out_f32=True)
+        if cfg.pi05:
+            K.rms_norm_backward(X[-1], dxn, out=dx, out_bf16=v['a'],
+                                scale=st[-1, :w], gate=gate2(nL - 1), eps=eps)
+        else:
+            dx.zero_()
+            v['a'].zero_()
+            K.rms_norm_backward(X[-1][lead:], dxn, out=dx[lead:],
+                                out_bf16=v['a'][lead:], eps=eps,
+                                row_group=na, row_group_stride=Ss)
+        for i in range(nL - 1, -1, -1):
+            L, wt = m.exp['layers'][i], self.wT[i]
+            # MLP: dh = (gate2 dX3) @ W_down, [gg | uu] recomputed from X2
+            K.gemm(v['a'], wt['down'], out=v['dh'])
+            gu = v['gu']
+            if cfg.pi05:
+                K.adarms_norm(X2[i], st[2 * i + 1:2 * i + 2], out=v['xn'],
+                              eps=eps)
+                a2, rn = v['xn'], None
+            else:
+                a2, rn = X2[i], eps
+            K.gemm(a2, L['gate_w'], out=gu[:, :mlp], rownorm_eps=rn)
+            K.gemm(a2, L['up_w'], out=gu[:, mlp:], rownorm_eps=rn)
+            K.act_backward(_lib.ACT_BWD_GEGLU, gu, v['dh'], out=v['dgu'])
+            K.gemm(v['dgu'], wt['gu'], out=v['da'], out_f32=True)
+            K.rms_norm_backward(
+                X2[i], v['da'], dres=dx, out=dx2, out_bf16=v['a'],
+                scale=st[2 * i + 1, :w] if cfg.pi05 else None,
+                gate=st[2 * i, 2 * w:] if cfg.pi05 else None, eps=eps)
+            # attention: dO = (gate1 dX2) @ W_o
+            K.gemm(v['a'], wt['o'], out=v['dctx'].view(B * Ss, -1))
+            self._attention_backward(b, B, i)
+            K.gemm(v['dqkv'], wt['qkv'], out=v['da'], out_f32=True)
+            K.rms_norm_backward(
+                X[i], v['da'], dres=dx2, out=dx, out_bf16=v['a'],
+                scale=st[2 * i, :w] if cfg.pi05 else None, gate=gate2(i - 1),
+                eps=eps)
+        # suffix embedding: g = dL/dx_t
+        if cfg.pi05:
+            K.gemm(v['a'], self.in_t, out=v['g'], out_f32=True)
+        else:
+            a = v['a'].view(B, Ss, hid)[:, lead:]
+            K.gemm(a, self.mo_t, out=v['dsh'])
+            K.act_backward(_lib.ACT_BWD_SILU, v['z'], v['dsh'], out=v['dz'])
+            K.gemm(v['dz'], self.mi_t, out=v['g'], out_f32=True)
+        K.rtc_vjp_update(b['xt'].view(B * na, -1), v['u'],
+                         b['rtc_prev'].view(B * na, -1), b['rtc_w'], v['g'],
+                         b['rtc_gw'][step:step + 1], m._rtc_omt[step], m.dt,
+                         x_bf16=b['xt_bf16'].view(B * na, -1))
+
+    def _attention_backward(self, b, B, i):
+        """dq, dk, dv of layer i's attention from dO (v['dctx']), packed with
+        the RoPE backward into v['dqkv']."""
+        m, cfg, v = self.m, self.m.cfg, self._bufs[B]
+        S, Ss, D, H = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.heads
+        nk, R = S + Ss, Ss * H
+        kc, vc = b['kc'][i], b['vc'][i]
+        kT, vr = v['kT'][i], v['vr'][i]
+        # this step's suffix keys / values into the transposed copies
+        K.transpose(kc[:, S:nk], kT[:, :, S:nk])
+        K.transpose(vc[:, :, S:nk], vr[:, S:nk])
+        q3 = v['Q'][i].view(B, R, D)
+        do3 = v['dctx'].view(B, R, D)
+        K.transpose(q3, v['qT'])
+        K.transpose(do3, v['dOT'])
+        dq3 = v['dq'].view(B, R, D)
+        for z in range(B):
+            K.gemm(q3[z], kc[z, :nk], out=v['s'][:, :nk], out_f32=True)
+            K.gemm(do3[z], vr[z, :nk], out=v['dp'][:, :nk], out_f32=True)
+            K.attention_rows_backward(
+                v['s'], v['dp'], v['ds'], heads=H, n_keys=nk,
+                scale=self.scale, kgrp=b['kgrp'][z], qgrp=b['qgrp_suf'][z],
+                ds_t=v['ds_t'], p_t=v['p_t'], key0=S, n_suffix=Ss)
+            K.gemm(v['ds'], kT[z], out=dq3[z], out_f32=True)
+            rows = slice(z * Ss, (z + 1) * Ss)
+            K.gemm(v['ds_t'], v['qT'][z], out=v['dk'][rows], out_f32=True)
+            K.gemm(v['p_t'], v['dOT'][z], out=v['dv'][rows], out_f32=True)
+        K.rope_backward(v['dq'], v['dk'], v['dv'], m.rope, b['pos_suf'],
+                        v['dqkv'], H, D)

@@ -11,7 +11,8 @@ uses as PI0's only inference path (BaseVLA -> PI0FlowMatching.predict_action):
 
   predict_action   fluxvla/models/vlas/pi0_flowmatching.py:702-785, 642-649
   RTC loops        pi0_flowmatching.py:651-700,
-                   fluxvla/engines/utils/rtc_guidance.py:28-155 (no VJP)
+                   fluxvla/engines/utils/rtc_guidance.py:28-155 (the VJP
+                   of use_vjp by torch autograd, as the reference)
   embed_prefix     pi0_flowmatching.py:204-250
   embed_suffix     pi0_flowmatching.py:252-321 (PI0),
                    fluxvla/models/vlas/pi05_flowmatching.py:68-127 (PI0.5)
@@ -434,39 +435,53 @@ def compute_guidance_weight(t, max_guidance_weight):
 
 
 def apply_rtc_guidance(x_t, denoise_fn, prev_actions, prefix_weights, t,
-                       max_guidance_weight):
-    """apply_rtc_guidance without VJP (rtc_guidance.py:107-155): v + gw *
-    w * (prev - x_1) on the first L_prev positions, x_1 = x_t + v (1 - t)."""
+                       max_guidance_weight, use_vjp=False):
+    """apply_rtc_guidance (rtc_guidance.py:107-155): v + gw * c with the
+    error e = w * (prev - x_1) on the first L_prev positions (zero after),
+    x_1 = x_t + v (1 - t).  Without VJP c = e; with use_vjp c is e pulled
+    back through x_1's Jacobian, (d x_1 / d x_t)^T e = e + (1 - t) J_v^T e,
+    by torch autograd through the denoiser (:142-150)."""
     eps = 1e-6
     one_minus_t = max(1.0 - t, eps)
     w = prefix_weights[None, :, None]
     gw = compute_guidance_weight(t, max_guidance_weight)
+
+    def full_error(x_1):
+        L_prev = prev_actions.shape[1]
+        error_full = torch.zeros_like(x_1)
+        if L_prev:
+            error_full[:, :L_prev] = ((prev_actions - x_1[:, :L_prev])
+                                      * w[:, :L_prev])
+        return error_full
+
+    if use_vjp:
+        with torch.enable_grad():
+            x_g = x_t.detach().requires_grad_(True)
+            v_t = denoise_fn(x_g)
+            x_1 = x_g + v_t * one_minus_t
+            (corr,) = torch.autograd.grad(x_1, x_g,
+                                          grad_outputs=full_error(x_1))
+        return v_t.detach() + gw * corr.detach()
     v_t = denoise_fn(x_t)
-    x_1 = x_t + v_t * one_minus_t
-    L_prev = prev_actions.shape[1]
-    error_full = torch.zeros_like(x_1)
-    if L_prev:
-        error_full[:, :L_prev] = (prev_actions - x_1[:, :L_prev]) * w[:, :L_prev]
-    return v_t + gw * error_full
+    return v_t + gw * full_error(x_t + v_t * one_minus_t)
 
 
 def euler_guidance_rtc(x_t, denoise, bsize, dt, prev_actions, prefix_len,
                        rtc_config, n_action_steps):
-    """_predict_action_guidance_rtc (pi0_flowmatching.py:671-700) with
-    use_vjp False: the guidance works in the 0 = noise time convention, so
-    the model velocity enters negated."""
-    if rtc_config.get('use_vjp', False):
-        raise NotImplementedError('guidance RTC with use_vjp')
+    """_predict_action_guidance_rtc (pi0_flowmatching.py:671-700), with or
+    without use_vjp: the guidance works in the 0 = noise time convention,
+    so the model velocity enters negated."""
     prefix_weights = compute_prefix_weights(
         n_action_steps, prefix_len, rtc_config.get('decay_end', prefix_len * 2),
         rtc_config.get('schedule', 'exp'))
     max_gw = rtc_config.get('max_guidance_weight', 5.0)
+    use_vjp = rtc_config.get('use_vjp', False)
     time = torch.tensor(1.0, dtype=torch.float32)
     while time >= -dt / 2:
         t_batch = time.expand(bsize)
         v_fm = apply_rtc_guidance(x_t, lambda x: -denoise(x, t_batch),
                                   prev_actions, prefix_weights,
-                                  1.0 - time.item(), max_gw)
+                                  1.0 - time.item(), max_gw, use_vjp=use_vjp)
         x_t += dt * (-v_fm)
         time += dt
     return x_t

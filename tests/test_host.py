@@ -215,10 +215,31 @@ def test_rtc_method_selection_and_padding():
     assert R.select_method(None, 3, {'method': 'prefix'}) is None
     assert R.select_method(prev, 3, None) is None
     assert R.select_method(prev, 3, {'method': 'other'}) is None
-    with pytest.raises(NotImplementedError):
-        R.select_method(prev, 3, {'method': 'guidance', 'use_vjp': True})
+    assert R.select_method(prev, 3, {'method': 'guidance',
+                                     'use_vjp': True}) == 'guidance_vjp'
+    assert R.select_method(prev, 3, {'method': 'guidance',
+                                     'use_vjp': False}) == 'guidance'
     p = R.pad_prev_actions(prev, 32, 14)
     assert p.shape == (1, 5, 32) and torch.equal(p[..., 14:],
                                                  torch.zeros(1, 5, 18))
     with pytest.raises(ValueError):
         R.pad_prev_actions(prev, 32, None)
+
+
+def test_rtc_guidance_vjp_tables_match_oracle():
+    """The VJP update's device tables: the oracle's prefix weights with the
+    rows past the previous chunk zeroed, and the oracle's guidance weight at
+    t = 1 - time of each step."""
+    from fluxvla_amd import rtc as R
+    from fluxvla_amd.pi0_inference import euler_times
+    from oracle import pi0_oracle as O
+    times, _ = euler_times(10)
+    rc = {'decay_end': 17, 'schedule': 'linear', 'max_guidance_weight': 3.0}
+    w, gw = R.guidance_vjp_tables(times, 50, 6, 24, rc)
+    want = O.compute_prefix_weights(50, 6, 17, 'linear')
+    want[24:] = 0
+    assert torch.allclose(w, want)
+    assert gw.shape == (10,)
+    for k, time in enumerate(times):
+        assert abs(gw[k].item() - O.compute_guidance_weight(1.0 - time, 3.0)) < 1e-6
+    assert gw[0].item() == 3.0  # capped at pure noise

@@ -854,3 +854,101 @@ def test_denoise_step_output_rows_closed_form():
     assert torch.allclose(got, want, atol=1e-5)
     bad = _planted_denoise(first_rows=True)(sd, cfg, states, ppad, kvs, x_t, t)
     assert not torch.allclose(bad, want, atol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# guidance with use_vjp (rtc_guidance.py:142-150)
+# ---------------------------------------------------------------------------
+def test_guidance_vjp_linear_denoiser_closed_form():
+    """A linear denoiser v(x) = x A^T + b (per action row) has J_v^T e =
+    e A, so the correction is e + (1 - t) e A with e = w (prev - x_1) on the
+    previous chunk's rows: the VJP's sign, its (1 - t) factor, the identity
+    term and the transposition of A each change the result (A is not
+    symmetric)."""
+    g = torch.Generator().manual_seed(61)
+    B, T, D, L = 2, 50, 32, 30
+    x = torch.randn(B, T, D, generator=g)
+    prev = torch.randn(B, L, D, generator=g)
+    A = torch.randn(D, D, generator=g) / math.sqrt(D)
+    b = torch.randn(D, generator=g)
+    w = O.compute_prefix_weights(T, 5, 20, 'exp')
+    t, gmax = 0.35, 5.0
+
+    def den(z):
+        return z @ A.t() + b
+
+    got = O.apply_rtc_guidance(x, den, prev, w, t, gmax, use_vjp=True)
+    v = den(x)
+    x1 = x + v * (1 - t)
+    e = torch.zeros_like(x)
+    e[:, :L] = (prev - x1[:, :L]) * w[None, :L, None]
+    gw = O.compute_guidance_weight(t, gmax)
+    want = v + gw * (e + (1 - t) * e @ A)
+    assert torch.allclose(got, want, atol=1e-5)
+    for bad in (v + gw * (e - (1 - t) * e @ A), v + gw * (e + e @ A),
+                v + gw * (1 - t) * e @ A, v + gw * (e + (1 - t) * e @ A.t())):
+        assert not torch.allclose(got, bad, atol=1e-3)
+    # without use_vjp the correction is e alone
+    plain = O.apply_rtc_guidance(x, den, prev, w, t, gmax)
+    assert torch.allclose(plain, v + gw * e, atol=1e-6)
+
+
+def test_guidance_vjp_constant_velocity_equals_plain_guidance():
+    """A denoiser that ignores x has a zero Jacobian: the VJP loop equals
+    the loop without it step for step."""
+    g = torch.Generator().manual_seed(62)
+    B, T, D = 1, 50, 32
+    noise = torch.randn(B, T, D, generator=g)
+    c = torch.randn(B, T, D, generator=g)
+    prev = torch.randn(B, 40, D, generator=g)
+    rc = {'method': 'guidance', 'decay_end': 12, 'schedule': 'exp'}
+    a = O.euler_guidance_rtc(noise.clone(), lambda x, t: c.clone(), B,
+                             torch.tensor(-0.1), prev, 4, rc, T)
+    b = O.euler_guidance_rtc(noise.clone(), lambda x, t: c.clone(), B,
+                             torch.tensor(-0.1), prev, 4, dict(rc, use_vjp=True),
+                             T)
+    assert torch.allclose(a, b, atol=1e-6)
+
+
+@pytest.mark.parametrize('pi05', [False, True])
+def test_guidance_vjp_through_denoise_step_finite_differences(pi05):
+    """Through the real denoiser (a one-layer expert against a random
+    cache): the VJP correction minus e, dotted with a direction d, equals
+    -(1 - t) e . J_u d with J_u d from central differences of denoise_step
+    (the guidance passes -u as its denoiser)."""
+    cfg = tiny(pi05=pi05, proj_width=64, exp_hidden=64, exp_mlp=96, heads=2,
+               head_dim=16, vit_layers=0, llm_layers=0, exp_layers=1)
+    sd = {k: v.float() for k, v in make_state_dict(cfg, seed=63).items()}
+    g = torch.Generator().manual_seed(64)
+    B, Sp = 2, 9
+    ppad = torch.ones(B, Sp, dtype=torch.bool)
+    ppad[1, 6:] = False
+    kvs = [(torch.randn(B, 1, Sp, cfg.head_dim, generator=g),
+            torch.randn(B, 1, Sp, cfg.head_dim, generator=g))]
+    states = torch.rand(B, cfg.state_dim, generator=g) * 2 - 1
+    x = torch.randn(B, cfg.n_action_steps, cfg.max_action_dim, generator=g)
+    prev = torch.randn(B, 30, cfg.max_action_dim, generator=g)
+    w = O.compute_prefix_weights(cfg.n_action_steps, 6, 18, 'linear')
+    time = torch.tensor(0.6)
+
+    def u(z):
+        return O.denoise_step(sd, cfg, states, ppad, kvs, z, time.expand(B))
+
+    t, gmax = 1.0 - 0.6, 5.0
+    with torch.no_grad():
+        got = O.apply_rtc_guidance(x, lambda z: -u(z), prev, w, t, gmax,
+                                   use_vjp=True)
+        plain = O.apply_rtc_guidance(x, lambda z: -u(z), prev, w, t, gmax)
+    gw = O.compute_guidance_weight(t, gmax)
+    jte_part = (got - plain) / gw  # = -(1 - t) J_u^T e
+    v = -u(x)
+    e = torch.zeros_like(x)
+    e[:, :30] = (prev - (x + v * (1 - t))[:, :30]) * w[None, :30, None]
+    for seed in (65, 66):
+        d = torch.randn(x.shape, generator=torch.Generator().manual_seed(seed))
+        eps = 1e-2
+        jd = (u(x + eps * d) - u(x - eps * d)) / (2 * eps)
+        lhs = (jte_part * d).sum().item()
+        rhs = -(1 - t) * (e * jd).sum().item()
+        assert abs(lhs - rhs) <= 2e-3 * abs(rhs) + 1e-5, (lhs, rhs)
+        assert abs(rhs) > 1e-2

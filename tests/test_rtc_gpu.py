@@ -3,7 +3,7 @@ adaRMS epilogues that carry it, against fp32 references of the same op, and
 whole chunks (PI0, PI0.5; prefix and guidance methods) against the CPU
 oracle's restatement of PI0FlowMatching._predict_action_prefix_rtc /
 _predict_action_guidance_rtc (fluxvla/models/vlas/pi0_flowmatching.py:
-651-700) and rtc_guidance.py:28-155.
+651-700) and rtc_guidance.py:28-155 (use_vjp by torch autograd).
 
 Bars as for the plain chunk: max abs error 2e-2 on the 50 x 32 chunk; the
 locked prefix rows are exactly the previous chunk; kernel outputs within
@@ -241,8 +241,92 @@ def test_rtc_falls_back_to_plain(models, cuda):
     prev = torch.randn(1, 30, 14, generator=gen(46))
     plain = m.predict_action(inp['images'].to(cuda), inp['lang_tokens'].to(cuda),
                              inp['states'].to(cuda), noise=inp['noise'].to(cuda)).cpu()
-    for p, rc in ((0, {'method': 'prefix'}), (5, None), (5, {'method': 'other'})):
+    for p, rc in ((0, {'method': 'prefix'}), (5, None), (5, {'method': 'other'}),
+                  (0, {'method': 'guidance', 'use_vjp': True})):
         got = _run(m, inp, cuda, prev, p, rc)
         assert torch.equal(got, plain)
-    with pytest.raises(NotImplementedError):
-        _run(m, inp, cuda, prev, 5, {'method': 'guidance', 'use_vjp': True})
+
+
+@pytest.mark.parametrize('pi05', [False, True])
+@pytest.mark.parametrize('batch', [1, 2])
+def test_guidance_vjp_rtc_chunk(models, cuda, pi05, batch):
+    """Guidance with use_vjp (rtc_guidance.py:142-150): the correction
+    pulled back through the expert's Jacobian by the backward kernels,
+    against the oracle's torch-autograd loop.  The VJP term moves the chunk
+    by far more than the bar (the oracle with and without it), so a product
+    that dropped or mis-signed it would fail."""
+    announce(f'pi0 guidance-vjp chunk pi05={pi05} batch={batch}')
+    cfg, sd, m = models(pi05)
+    inp = make_inputs(cfg, batch=batch, seed=47)
+    prev = torch.randn(batch, 40, 14, generator=gen(48)) * 0.5
+    rc = {'enabled': True, 'method': 'guidance', 'use_vjp': True,
+          'schedule': 'exp', 'max_guidance_weight': 5.0, 'decay_end': 20}
+    ref, kvs = _oracle(cfg, sd, inp, prev, 6, rc)
+    plain_ref, _ = _oracle(cfg, sd, inp, prev, 6, dict(rc, use_vjp=False), kvs)
+    got = _run(m, inp, cuda, prev, 6, rc)
+    plain = _run(m, inp, cuda, prev, 6, dict(rc, use_vjp=False))
+    err = (got - ref).abs().max().item()
+    moved, moved_got = ref - plain_ref, got - plain
+    d_err = rel_err(moved_got, moved)
+    print(f'chunk max abs err {err:.3e}; the VJP term moves the chunk by '
+          f'{moved.abs().max().item():.3e} (oracle), its move is off by '
+          f'{d_err:.3e} relative')
+    assert err <= CHUNK_ATOL
+    # the VJP term's own effect (with minus without it) matches the oracle's
+    assert d_err <= 0.2
+    # eager run of the same loop gives the graph's chunk
+    m.use_graph = False
+    try:
+        eager = _run(m, inp, cuda, prev, 6, rc)
+    finally:
+        m.use_graph = True
+    assert torch.equal(eager, got)
+
+
+@pytest.mark.parametrize('pi05', [False, True])
+@pytest.mark.parametrize('batch', [1, 2])
+def test_guidance_vjp_step_matches_autograd(models, cuda, pi05, batch):
+    """One VJP step on its own: after a chunk has filled the prefix cache,
+    the step's forward (u) and backward (g = J_u^T e) at a chosen x_t against
+    the oracle's denoise_step and torch autograd through it at the same
+    bf16 input, with e = w (prev - x + (1 - t) u) as the product forms it."""
+    announce(f'pi0 guidance-vjp one step pi05={pi05} batch={batch}')
+    cfg, sd, m = models(pi05)
+    inp = make_inputs(cfg, batch=batch, seed=49)
+    prev = torch.randn(batch, 40, 14, generator=gen(50)) * 0.5
+    rc = {'enabled': True, 'method': 'guidance', 'use_vjp': True,
+          'max_guidance_weight': 5.0, 'decay_end': 25}
+    m.use_graph = False
+    try:
+        _run(m, inp, cuda, prev, 8, rc)
+    finally:
+        m.use_graph = True
+    eng, b = m._vjp, m._bufs[batch]
+    na = cfg.n_action_steps
+    x = torch.randn(batch, na, cfg.max_action_dim, generator=gen(51))
+    b['xt'].copy_(x)
+    b['xt_bf16'].copy_(x)
+    step = 3
+    eng.forward(b, batch, step)
+    eng.backward(b, batch, step)
+    v = eng.buffers(batch)
+    u = v['u'].view(batch, na, -1).cpu()
+    g = v['g'].view(batch, na, -1).cpu()
+    cache, pad = O.prefix_forward(sd, cfg, inp['images'], inp['lang_tokens'],
+                                  inp['img_masks'], inp['lang_masks'])
+    xb = x.bfloat16().float()
+    time = torch.tensor(m.times[step])
+    with torch.enable_grad():
+        xg = xb.clone().requires_grad_(True)
+        u_ref = O.denoise_step(sd, cfg, inp['states'].float(), pad, cache, xg,
+                               time.expand(batch))
+        w = b['rtc_w'].cpu()
+        prev_p = b['rtc_prev'].cpu()
+        e = w[None, :, None] * (prev_p - x + m._rtc_omt[step] * u_ref.detach())
+        (g_ref,) = torch.autograd.grad(u_ref, xg, e)
+    eu, eg = rel_err(u, u_ref), rel_err(g, g_ref)
+    cos = torch.nn.functional.cosine_similarity(g.flatten(), g_ref.flatten(),
+                                                dim=0).item()
+    print(f'u rel err {eu:.3e}; g rel err {eg:.3e}, cosine {cos:.5f}')
+    assert eu <= 2e-2
+    assert eg <= 5e-2 and cos >= 0.995
