@@ -165,6 +165,10 @@ SIGNATURES = {
                                             c_vp, c_vp, c_i64, c_vp, c_vp,
                                             c_i64, c_i64, c_i64, c_i64, c_i64,
                                             c_i64, c_i64, c_f32, c_vp]),
+    'fvx_attention_suffix_kv_backward': (c_i32, [c_vp, c_vp, c_i64, c_vp,
+                                                 c_i64, c_vp, c_i64, c_vp,
+                                                 c_i64, c_vp, c_i64, c_i64,
+                                                 c_i64, c_i64, c_vp]),
     'fvx_transpose_bf16': (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
                                    c_i64, c_i64, c_i64, c_vp]),
     'fvx_rope_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,

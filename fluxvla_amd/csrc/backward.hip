@@ -232,6 +232,111 @@ __global__ __launch_bounds__(256) void attn_rows_backward_kernel(
   }
 }
 
+// The same with the row held in registers (NK keys per lane, up to 64 NK
+// keys): every load of the row is issued at once, one memory round trip
+// instead of four passes' worth.
+template <int NK>
+__global__ __launch_bounds__(256) void attn_rows_backward_reg_kernel(
+    const float* __restrict__ s, int64_t lds, const float* __restrict__ dp,
+    int64_t lddp, const int32_t* __restrict__ kgrp,
+    const int32_t* __restrict__ qgrp, bf16_t* __restrict__ ds, int64_t ldds,
+    bf16_t* __restrict__ ds_t, bf16_t* __restrict__ p_t, int64_t ldt,
+    int64_t key0, int n_suffix, int64_t rows, int heads, int n_keys,
+    int n_cols, float scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * kBwdRows + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int32_t qg = qgrp ? qgrp[r / heads] : 0;
+  const float* sr = s + r * lds;
+  const float* dr = dp + r * lddp;
+  constexpr float kLog2e = 1.4426950408889634f;
+  float lg[NK], dv[NK];
+  bool vis[NK];
+#pragma unroll
+  for (int c = 0; c < NK; ++c) {
+    const int j = lane + 64 * c;
+    const bool in = j < n_keys;
+    lg[c] = in ? sr[j] : 0.f;
+    dv[c] = in ? dr[j] : 0.f;
+    vis[c] = in && (!kgrp || kgrp[j] <= qg);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NK; ++c) {
+    lg[c] *= scale;
+    if (vis[c]) mx = fmaxf(mx, lg[c]);
+  }
+  mx = wave_max(mx);
+  float l = 0.f;
+#pragma unroll
+  for (int c = 0; c < NK; ++c) {
+    lg[c] = vis[c] ? exp2f((lg[c] - mx) * kLog2e) : 0.f;
+    l += lg[c];
+  }
+  l = wave_sum(l);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  float dsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < NK; ++c) {
+    lg[c] *= inv;  // P
+    dsum += lg[c] * dv[c];
+  }
+  dsum = wave_sum(dsum);
+#pragma unroll
+  for (int c = 0; c < NK; ++c) {
+    const int j = lane + 64 * c;
+    if (j < n_cols) {
+      const float d = scale * lg[c] * (dv[c] - dsum);  // 0 where P is 0
+      ds[r * ldds + j] = f2bf(d);
+      const int64_t js = j - key0;
+      if (js >= 0 && js < n_suffix) {
+        if (ds_t) ds_t[js * ldt + r] = f2bf(d);
+        if (p_t) p_t[js * ldt + r] = f2bf(lg[c]);
+      }
+    }
+  }
+  for (int j = lane + 64 * NK; j < n_cols; j += 64) ds[r * ldds + j] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Suffix keys' gradients of one attention problem: dk[j] = sum_r ds_t[j][r]
+// q[r] and dv[j] = sum_r p_t[j][r] dO[r] (ds already carries the softmax
+// scale), the sums over every query row r = (token, head) -- the heads
+// share the one key/value head.  Workgroup (j, 64-column block): lane =
+// column, each of the 4 waves sums a quarter of the rows, then the waves'
+// sums add through LDS in wave order.  fp32 out.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_suffix_kv_backward_kernel(
+    const bf16_t* __restrict__ ds_t, const bf16_t* __restrict__ p_t,
+    int64_t ldt, const bf16_t* __restrict__ q, int64_t ldq,
+    const bf16_t* __restrict__ dout, int64_t ldo, float* __restrict__ dk,
+    int64_t ldk, float* __restrict__ dv, int64_t ldv, int rows, int cols) {
+  __shared__ float red[2][4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t j = blockIdx.x;
+  const int c = blockIdx.y * 64 + lane;
+  const bool live = c < cols;
+  const int per = (rows + 3) / 4;
+  const int r0 = w * per, r1 = min(rows, r0 + per);
+  float ak = 0.f, av = 0.f;
+  const bf16_t* dsr = ds_t + j * ldt;
+  const bf16_t* ptr = p_t + j * ldt;
+  for (int r = r0; r < r1; ++r) {
+    const float a = bf2f(dsr[r]), b = bf2f(ptr[r]);
+    if (live) {
+      ak += a * bf2f(q[(int64_t)r * ldq + c]);
+      av += b * bf2f(dout[(int64_t)r * ldo + c]);
+    }
+  }
+  red[0][w][lane] = ak;
+  red[1][w][lane] = av;
+  __syncthreads();
+  if (w == 0 && live) {
+    dk[j * ldk + c] = ((red[0][0][lane] + red[0][1][lane]) + red[0][2][lane]) + red[0][3][lane];
+    dv[j * ldv + c] = ((red[1][0][lane] + red[1][1][lane]) + red[1][2][lane]) + red[1][3][lane];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // bf16 transpose, 32 x 32 tiles through LDS (one padding column keeps the
 // column reads conflict-free): dst[b][c][r] = src[b][r][c].
@@ -450,11 +555,41 @@ extern "C" int fvx_attention_rows_backward(
               FVX_ERR_SHAPE, "attention_rows_backward: bad suffix columns");
   if (rows == 0) return FVX_OK;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(attn_rows_backward_kernel, dim3(blocks(rows, kBwdRows)), dim3(256), 0,
-                     st, s, lds, dp, lddp, kgrp, qgrp, (bf16_t*)ds, ldds, (bf16_t*)ds_t,
-                     (bf16_t*)p_t, ldt, key0, (int)n_suffix, rows, (int)heads,
-                     (int)n_keys, (int)n_cols, scale);
+  const dim3 grid(blocks(rows, kBwdRows));
+  const int nk = (int)((n_keys + 63) / 64);
+#define L(KERNEL)                                                                         \
+  hipLaunchKernelGGL(KERNEL, grid, dim3(256), 0, st, s, lds, dp, lddp, kgrp, qgrp,        \
+                     (bf16_t*)ds, ldds, (bf16_t*)ds_t, (bf16_t*)p_t, ldt, key0,           \
+                     (int)n_suffix, rows, (int)heads, (int)n_keys, (int)n_cols, scale)
+  if (nk <= 4) L(attn_rows_backward_reg_kernel<4>);
+  else if (nk <= 8) L(attn_rows_backward_reg_kernel<8>);
+  else if (nk <= 12) L(attn_rows_backward_reg_kernel<12>);
+  else if (nk <= 16) L(attn_rows_backward_reg_kernel<16>);
+  else L(attn_rows_backward_kernel);
+#undef L
   return launch_status("attention_rows_backward");
+}
+
+extern "C" int fvx_attention_suffix_kv_backward(const void* ds_t, const void* p_t,
+                                                int64_t ldt, const void* q, int64_t ldq,
+                                                const void* dout, int64_t ldo, float* dk,
+                                                int64_t ldk, float* dv, int64_t ldv,
+                                                int64_t n_suffix, int64_t rows,
+                                                int64_t cols, void* stream) {
+  clear_error();
+  FVX_REQUIRE(ds_t && p_t && q && dout && dk && dv, FVX_ERR_NULL,
+              "attention_suffix_kv_backward: every operand is required");
+  FVX_REQUIRE(n_suffix >= 0 && n_suffix < 65536 && rows > 0 && rows < (1 << 30) &&
+                  cols > 0 && cols < (1 << 22) && ldt >= rows && ldq >= cols &&
+                  ldo >= cols && ldk >= cols && ldv >= cols,
+              FVX_ERR_SHAPE, "attention_suffix_kv_backward: bad sizes");
+  if (n_suffix == 0) return FVX_OK;
+  hipLaunchKernelGGL(attn_suffix_kv_backward_kernel,
+                     dim3((unsigned)n_suffix, blocks(cols, 64)), dim3(256), 0,
+                     (hipStream_t)stream, (const bf16_t*)ds_t, (const bf16_t*)p_t, ldt,
+                     (const bf16_t*)q, ldq, (const bf16_t*)dout, ldo, dk, ldk, dv, ldv,
+                     (int)rows, (int)cols);
+  return launch_status("attention_suffix_kv_backward");
 }
 
 extern "C" int fvx_transpose_bf16(const void* src, int64_t ld_src, int64_t src_batch_stride,

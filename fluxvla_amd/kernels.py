@@ -981,6 +981,27 @@ def attention_rows_backward(s, dp, ds, *, heads, n_keys, scale, kgrp=None,
     return ds
 
 
+def attention_suffix_kv_backward(ds_t, p_t, q, dout, dk, dv):
+    """dk = ds_t @ q, dv = p_t @ dout (fvx_attention_suffix_kv_backward):
+    ds_t / p_t bf16 [n_suffix, >= rows], q / dout bf16 [rows, cols], dk / dv
+    fp32 [n_suffix, cols]."""
+    for t, nm in ((ds_t, 'ds_t'), (p_t, 'p_t'), (q, 'q'), (dout, 'dout')):
+        _check(t, nm, contiguous=False)
+    for t, nm in ((dk, 'dk'), (dv, 'dv')):
+        _check(t, nm, dtype=torch.float32, contiguous=False)
+    rows, ldq = _rows_ld(q, 'q')
+    _, ldo = _rows_ld(dout, 'dout')
+    ns, ldt = _rows_ld(ds_t, 'ds_t')
+    if p_t.stride(0) != ldt or p_t.shape[0] != ns or dout.shape[0] != rows:
+        raise ValueError('p_t must match ds_t and dout must match q')
+    if dk.shape[0] < ns or dv.shape[0] < ns:
+        raise ValueError('dk / dv need n_suffix rows')
+    _lib.call('fvx_attention_suffix_kv_backward', _ptr(ds_t), _ptr(p_t), ldt,
+              _ptr(q), ldq, _ptr(dout), ldo, _ptr(dk), dk.stride(0), _ptr(dv),
+              dv.stride(0), ns, rows, q.shape[-1], _stream())
+    return dk, dv
+
+
 def transpose(src, dst):
     """dst[..., c, r] = src[..., r, c] for bf16 [rows, cols] or [batch, rows,
     cols] views (unit column stride)."""

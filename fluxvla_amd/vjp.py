@@ -19,19 +19,20 @@ e = w (prev - x_1) on the previous chunk's rows.  Here one Euler step is
               norm:       dX2 = dX3 + RMSNorm-backward(X2, da)
               O:          dO = (gate1 dX2) @ W_o
               attention:  S = Q K^T, dP = dO V^T (fp32), the masked softmax
-                          backward per row, dQ = dS K, dK = dS^T Q and
-                          dV = P^T dO on the suffix keys (the prefix cache
-                          is a constant of x_t), RoPE backward
+                          backward per row, dQ = dS K, and dK = dS^T Q,
+                          dV = P^T dO on the suffix keys in one kernel (the
+                          prefix cache is a constant of x_t), RoPE backward
               QKV:        da = d[q | k | v] @ W_qkv
               norm:       dX = dX2 + RMSNorm-backward(X, da)
             and through the suffix embedding (PI0: action-time MLP with
             its SiLU; PI0.5: action_in_proj) to g = dL/dx_t;
   update    x <- x + dt u - dt gw e + dt gw (1 - t) g              (one kernel).
 
-Every product runs through fvx_gemm: the weights' products use [in, out]
-copies of the prepared [out, in] weights (fp8 weights dequantized to bf16),
-the attention's products transposed copies of the key cache, of the value
-cache (row-major), of Q and of dO.  All of it is part of the captured chunk
+The weights' products and the attention's Q K^T, dO V^T and dS K run
+through fvx_gemm: on [in, out] copies of the prepared [out, in] weights (fp8
+weights dequantized to bf16; fragment-major for the M <= 64 GEMMs of bs=1),
+on a transposed copy of the key cache and a row-major copy of the value
+cache.  All of it is part of the captured chunk
 graph: per-request values (previous chunk, weights, guidance weights) are
 device buffers.
 """
@@ -71,8 +72,21 @@ class ExpertVJP:
         else:
             self.mo_t = _weight_t(m.mlp_out['w'])    # [proj_width, hid]
             self.mi_t = _weight_t(m.mlp_in_x)        # [action_dim, proj]
+        # fragment-major copies for the M <= 64 GEMMs (bs = 1)
+        F = K.FragB.pack
+        self.wT_f = [{nm: F(w) for nm, w in L.items()} for L in self.wT]
+        self.out_t_f = F(self.out_t)
+        if cfg.pi05:
+            self.in_t_f = F(self.in_t)
+        else:
+            self.mo_t_f, self.mi_t_f = F(self.mo_t), F(self.mi_t)
         self.scale = cfg.head_dim ** -0.5
         self._bufs = {}
+
+    def _frag(self, B):
+        """The expert's GEMMs have M = B * suffix_len rows: fragment-major
+        weights when that is <= 64."""
+        return B * self.m.cfg.suffix_len <= 64
 
     # -- buffers -------------------------------------------------------------
     def buffers(self, B):
@@ -105,7 +119,6 @@ class ExpertVJP:
             'dgu': e(B * Ss, 2 * mlp), 'dctx': e(B, Ss, H * D),
             's': e(R, T, dt=torch.float32), 'dp': e(R, T, dt=torch.float32),
             'ds': e(R, T), 'ds_t': e(Ss, R), 'p_t': e(Ss, R),
-            'qT': e(B, D, R), 'dOT': e(B, D, R),
             'dq': e(B * Ss, H * D, dt=torch.float32),
             'dk': e(B * Ss, D, dt=torch.float32),
             'dv': e(B * Ss, D, dt=torch.float32),
@@ -146,16 +159,21 @@ class ExpertVJP:
         na, hid, T = cfg.n_action_steps, cfg.exp_hidden, m.kv_len
         X, X2, Q = v['X'], v['X2'], v['Q']
         xt_b = b['xt_bf16'].view(B * na, -1)
+        fr = self._frag(B)
         if cfg.pi05:
-            K.gemm(xt_b, m.act_in['w'], out=X[0], bias=m.act_in['b'])
+            K.gemm(xt_b, m.act_in_f if fr else m.act_in['w'], out=X[0],
+                   bias=m.act_in['b'])
         else:
             h = b['suf_h']  # the state rows stay zero
-            K.gemm(xt_b, m.mlp_in_x, out=h[1:], bias_f32=m.step_bias[step],
+            w_mi = m.mlp_in_x_f if fr else m.mlp_in_x
+            K.gemm(xt_b, w_mi, out=h[1:], bias_f32=m.step_bias[step],
                    act=_lib.ACT_SILU, row_group=na, row_group_stride=Ss)
-            K.gemm(xt_b, m.mlp_in_x, out=v['z'], bias_f32=m.step_bias[step])
-            K.gemm(h, m.mlp_out['w'], out=X[0], residual=b['suf_res'])
+            K.gemm(xt_b, w_mi, out=v['z'], bias_f32=m.step_bias[step])
+            K.gemm(h, m.mlp_out_f if fr else m.mlp_out['w'], out=X[0],
+                   residual=b['suf_res'])
         st = m.styles[step] if cfg.pi05 else None
-        for i, L in enumerate(m.exp['layers']):
+        layers = m.exp_f if fr else m.exp['layers']
+        for i, L in enumerate(layers):
             kc, vc = b['kc'][i], b['vc'][i]
             x = X[i]
             if cfg.pi05:
@@ -185,13 +203,14 @@ class ExpertVJP:
                    gate=gate)
         lead = Ss - na
         last = X[-1].view(B, Ss, hid)
+        w_out = m.act_out_f if fr else m.act_out['w']
         if cfg.pi05:
             K.adarms_norm(X[-1], st[-1:], out=v['xn'], eps=cfg.rms_eps)
-            K.gemm(v['xn'], m.act_out['w'], out=v['u'], bias=m.act_out['b'],
+            K.gemm(v['xn'], w_out, out=v['u'], bias=m.act_out['b'],
                    out_f32=True)
         else:
-            K.gemm(last[:, lead:], m.act_out['w'], out=v['u'],
-                   bias=m.act_out['b'], rownorm_eps=cfg.rms_eps, out_f32=True)
+            K.gemm(last[:, lead:], w_out, out=v['u'], bias=m.act_out['b'],
+                   rownorm_eps=cfg.rms_eps, out_f32=True)
         K.rtc_vjp_error(b['xt'].view(B * na, -1), v['u'],
                         b['rtc_prev'].view(B * na, -1), b['rtc_w'], v['e'],
                         m._rtc_omt[step])
@@ -213,11 +232,14 @@ class ExpertVJP:
             return st[2 * i + 1, 2 * w:] if (cfg.pi05 and i >= 0) else None
 
         nL = len(m.exp['layers'])
+        fr = self._frag(B)
+        wts = self.wT_f if fr else self.wT
         dx, dx2 = v['dx']
         # d(final norm output) = e @ W_out, then the final norm's backward
         # onto the action rows (the state row of PI0 gets none)
         dxn = v['da'][:B * na]
-        K.gemm(v['e'], self.out_t, out=dxn, out_f32=True)
+        K.gemm(v['e'], self.out_t_f if fr else self.out_t, out=dxn,
+               out_f32=True)
         if cfg.pi05:
             K.rms_norm_backward(X[-1], dxn, out=dx, out_bf16=v['a'],
                                 scale=st[-1, :w], gate=gate2(nL - 1), eps=eps)
@@ -228,7 +250,8 @@ class ExpertVJP:
                                 out_bf16=v['a'][lead:], eps=eps,
                                 row_group=na, row_group_stride=Ss)
         for i in range(nL - 1, -1, -1):
-            L, wt = m.exp['layers'][i], self.wT[i]
+            wt = wts[i]
+            L = m.exp_f[i] if fr else m.exp['layers'][i]
             # MLP: dh = (gate2 dX3) @ W_down, [gg | uu] recomputed from X2
             K.gemm(v['a'], wt['down'], out=v['dh'])
             gu = v['gu']
@@ -256,12 +279,14 @@ class ExpertVJP:
                 eps=eps)
         # suffix embedding: g = dL/dx_t
         if cfg.pi05:
-            K.gemm(v['a'], self.in_t, out=v['g'], out_f32=True)
+            K.gemm(v['a'], self.in_t_f if fr else self.in_t, out=v['g'],
+                   out_f32=True)
         else:
             a = v['a'].view(B, Ss, hid)[:, lead:]
-            K.gemm(a, self.mo_t, out=v['dsh'])
+            K.gemm(a, self.mo_t_f if fr else self.mo_t, out=v['dsh'])
             K.act_backward(_lib.ACT_BWD_SILU, v['z'], v['dsh'], out=v['dz'])
-            K.gemm(v['dz'], self.mi_t, out=v['g'], out_f32=True)
+            K.gemm(v['dz'], self.mi_t_f if fr else self.mi_t, out=v['g'],
+                   out_f32=True)
         K.rtc_vjp_update(b['xt'].view(B * na, -1), v['u'],
                          b['rtc_prev'].view(B * na, -1), b['rtc_w'], v['g'],
                          b['rtc_gw'][step:step + 1], m._rtc_omt[step], m.dt,
@@ -280,8 +305,6 @@ class ExpertVJP:
         K.transpose(vc[:, :, S:nk], vr[:, S:nk])
         q3 = v['Q'][i].view(B, R, D)
         do3 = v['dctx'].view(B, R, D)
-        K.transpose(q3, v['qT'])
-        K.transpose(do3, v['dOT'])
         dq3 = v['dq'].view(B, R, D)
         for z in range(B):
             K.gemm(q3[z], kc[z, :nk], out=v['s'][:, :nk], out_f32=True)
@@ -292,7 +315,7 @@ class ExpertVJP:
                 ds_t=v['ds_t'], p_t=v['p_t'], key0=S, n_suffix=Ss)
             K.gemm(v['ds'], kT[z], out=dq3[z], out_f32=True)
             rows = slice(z * Ss, (z + 1) * Ss)
-            K.gemm(v['ds_t'], v['qT'][z], out=v['dk'][rows], out_f32=True)
-            K.gemm(v['p_t'], v['dOT'][z], out=v['dv'][rows], out_f32=True)
+            K.attention_suffix_kv_backward(v['ds_t'], v['p_t'], q3[z], do3[z],
+                                           v['dk'][rows], v['dv'][rows])
         K.rope_backward(v['dq'], v['dk'], v['dv'], m.rope, b['pos_suf'],
                         v['dqkv'], H, D)

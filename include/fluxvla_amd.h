@@ -547,6 +547,20 @@ int fvx_attention_rows_backward(const float* s, int64_t lds, const float* dp,
                                 int64_t heads, int64_t n_keys, int64_t n_cols,
                                 float scale, void* stream);
 
+/* Gradients of the suffix keys and values of one attention problem
+ * (the eager attention's backward, condition_gemma.py:340-535): with ds_t /
+ * p_t as fvx_attention_rows_backward writes them ([n_suffix, ldt] bf16,
+ * column r = query row r),
+ *   dk[j][c] = sum_r ds_t[j][r] q[r][c],  dv[j][c] = sum_r p_t[j][r] dout[r][c]
+ * for j < n_suffix, c < cols, r < rows (q, dout bf16 [rows, ld]; dk, dv
+ * fp32).  The heads of a key/value head are rows of the same sums. */
+int fvx_attention_suffix_kv_backward(const void* ds_t, const void* p_t,
+                                     int64_t ldt, const void* q, int64_t ldq,
+                                     const void* dout, int64_t ldo, float* dk,
+                                     int64_t ldk, float* dv, int64_t ldv,
+                                     int64_t n_suffix, int64_t rows,
+                                     int64_t cols, void* stream);
+
 /* bf16 transpose: dst[b][c][r] = src[b][r][c] for b < batch, r < rows,
  * c < cols (element offsets b * batch_stride + row * ld). */
 int fvx_transpose_bf16(const void* src, int64_t ld_src,

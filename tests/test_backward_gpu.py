@@ -120,12 +120,15 @@ def softmax_bwd_ref(s, dp, vis, scale):
     return p.detach(), ds
 
 
-def test_attention_rows_backward(K, cuda):
-    """The expert's suffix rows (51 tokens x 8 heads) over 816 prefix keys
+@pytest.mark.parametrize('S', [816, 1100])
+def test_attention_rows_backward(K, cuda, S):
+    """The expert's suffix rows (51 tokens x 8 heads) over S prefix keys
     with padding and the block-causal suffix pattern; ds matches autograd of
-    the masked softmax, ds_t / p_t hold the suffix columns transposed."""
-    announce('attention_rows_backward')
-    S, Ss, H, T = 816, 51, 8, 872
+    the masked softmax, ds_t / p_t hold the suffix columns transposed.  816:
+    the row held in registers; 1100 (> 1024 keys): the multi-pass kernel."""
+    announce(f'attention_rows_backward S={S}')
+    Ss, H = 51, 8
+    T = (S + Ss + 7) // 8 * 8
     nk = S + Ss
     rows = Ss * H
     scale = 256 ** -0.5
@@ -235,3 +238,20 @@ def test_rtc_vjp_error_and_update(K, cuda):
            + dt * gw * omt * g.double())
     assert rel_err(xg, ref) <= F32_TOL
     assert torch.equal(xb.cpu(), xg.cpu().to(torch.bfloat16))
+
+
+def test_attention_suffix_kv_backward(K, cuda):
+    """dk = ds_t @ q and dv = p_t @ dO over the 408 query rows, against
+    float64 products of the same bf16 operands."""
+    announce('attention_suffix_kv_backward')
+    Ss, R, D = 51, 408, 256
+    ds_t = randn((Ss, R), 81, std=0.1)
+    p_t = randn((Ss, R), 82, std=0.1)
+    q = randn((R, D), 83)
+    do = randn((R, D), 84)
+    dk = torch.full((Ss, D), float('nan'), device=cuda)
+    dv = torch.full((Ss, D), float('nan'), device=cuda)
+    K.attention_suffix_kv_backward(ds_t.to(cuda), p_t.to(cuda), q.to(cuda),
+                                   do.to(cuda), dk, dv)
+    assert rel_err(dk, ds_t.double() @ q.double()) <= F32_TOL
+    assert rel_err(dv, p_t.double() @ do.double()) <= F32_TOL
