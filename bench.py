@@ -25,7 +25,8 @@ Also reported on the same JSON line:
                 chunks, and config 1 alone (median of 20);
   configs       BASELINE configs 4 and 5 (ms/chunk, actions/s, accuracy);
   rtc           the same chunk with real-time chunking (prefix and guidance
-                methods, previous chunk of 30 rows, prefix 5);
+                methods, guidance also with use_vjp, previous chunk of 30
+                rows, prefix 5);
   serving       one predict_action request through the serving boundary
                 (three 480x640 JPEG frames, msgpack): host decode, device
                 preprocessing + chunk + device-to-host, reply encoding;
@@ -961,13 +962,16 @@ def other_configs(pi0_model, sd0, dev, parity=True):
 
 def rtc_times(model, dinp, steps=10):
     """ms/chunk of the prefix and guidance RTC loops at bs=1 (each its own
-    captured graph), and the locked rows' exactness."""
+    captured graph; guidance also with use_vjp: forward and backward through
+    the expert at every step), and the locked rows' exactness."""
     import torch
     g = torch.Generator().manual_seed(5)
     prev = (torch.randn(1, 30, 32, generator=g) * 0.5).to(dinp['images'].device)
     out = {}
-    for method in ('prefix', 'guidance'):
-        rc = {'enabled': True, 'method': method, 'max_guidance_weight': 5.0}
+    for method in ('prefix', 'guidance', 'guidance_vjp'):
+        rc = {'enabled': True, 'method': method.split('_')[0],
+              'max_guidance_weight': 5.0,
+              'use_vjp': method == 'guidance_vjp'}
 
         def step():
             return model.predict_action(dinp['images'], dinp['lang_tokens'],
