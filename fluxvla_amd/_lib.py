@@ -161,6 +161,7 @@ SIGNATURES = {
                                       c_vp]),
     'fvx_act_backward': (c_i32, [c_i32, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
                                  c_i64, c_i64, c_vp]),
+    'fvx_geglu_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp]),
     'fvx_attention_rows_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp,
                                             c_vp, c_vp, c_i64, c_vp, c_vp,
                                             c_i64, c_i64, c_i64, c_i64, c_i64,

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void rms_backward_kernel(
 // x^3) (the forward's own formula, common.h), so gelu' = s + x s (1 - s)
 // 2 sqrt(2/pi) (1 + 3 * 0.044715 x^2);  silu'(z) = sig (1 + z (1 - sig)).
 // ---------------------------------------------------------------------------
-constexpr int kActGeglu = 0, kActSilu = 1;
+constexpr int kActGeglu = 0, kActSilu = 1, kGegluFwd = 2;
 
 template <int ACT>
 __global__ __launch_bounds__(256) void act_backward_kernel(
@@ -147,6 +147,14 @@ __global__ __launch_bounds__(256) void act_backward_kernel(
   const int c = (int)(t - m * nv) * 8;
   float a[8], d[8], o[8];
   unpack8(ld8(in + m * ldi + c), a);
+  if (ACT == kGegluFwd) {
+    // the forward product itself: out = gelu_tanh(gate) * up (dy unused)
+    unpack8(ld8(in + m * ldi + cols + c), d);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = gelu_tanh(a[e]) * d[e];
+    st8(out + m * ldo + c, pack8(o));
+    return;
+  }
   unpack8(ld8(dy + m * ldy + c), d);
   if (ACT == kActGeglu) {
     float u[8], o2[8];
@@ -302,38 +310,79 @@ __global__ __launch_bounds__(256) void attn_rows_backward_reg_kernel(
 // Suffix keys' gradients of one attention problem: dk[j] = sum_r ds_t[j][r]
 // q[r] and dv[j] = sum_r p_t[j][r] dO[r] (ds already carries the softmax
 // scale), the sums over every query row r = (token, head) -- the heads
-// share the one key/value head.  Workgroup (j, 64-column block): lane =
-// column, each of the 4 waves sums a quarter of the rows, then the waves'
-// sums add through LDS in wave order.  fp32 out.
+// share the one key/value head.  Workgroup (j, 64-column block): thread t
+// owns 8 columns (t % 8) of every 32nd row from t / 8, loading 16 bytes of
+// q and dO per row, four rows in flight; the 32 row groups' sums then add
+// through LDS in row-group order.  fp32 out.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void attn_suffix_kv_backward_kernel(
     const bf16_t* __restrict__ ds_t, const bf16_t* __restrict__ p_t,
     int64_t ldt, const bf16_t* __restrict__ q, int64_t ldq,
     const bf16_t* __restrict__ dout, int64_t ldo, float* __restrict__ dk,
     int64_t ldk, float* __restrict__ dv, int64_t ldv, int rows, int cols) {
-  __shared__ float red[2][4][64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ float red[2][32][65];
+  const int t = threadIdx.x;
+  const int cg = t & 7, rg = t >> 3;
   const int64_t j = blockIdx.x;
-  const int c = blockIdx.y * 64 + lane;
-  const bool live = c < cols;
-  const int per = (rows + 3) / 4;
-  const int r0 = w * per, r1 = min(rows, r0 + per);
-  float ak = 0.f, av = 0.f;
+  const int c0 = blockIdx.y * 64 + cg * 8;
+  const bool live = c0 < cols;  // cols % 8 == 0
+  float ak[8], av[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ak[e] = av[e] = 0.f;
   const bf16_t* dsr = ds_t + j * ldt;
   const bf16_t* ptr = p_t + j * ldt;
-  for (int r = r0; r < r1; ++r) {
-    const float a = bf2f(dsr[r]), b = bf2f(ptr[r]);
-    if (live) {
-      ak += a * bf2f(q[(int64_t)r * ldq + c]);
-      av += b * bf2f(dout[(int64_t)r * ldo + c]);
+  int r = rg;
+  for (; r + 96 < rows; r += 128) {
+    float a[4], b[4];
+    bf16x8 qv[4], ov[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int rr = r + 32 * u;
+      a[u] = bf2f(dsr[rr]);
+      b[u] = bf2f(ptr[rr]);
+      qv[u] = live ? ld8(q + (int64_t)rr * ldq + c0) : zero8();
+      ov[u] = live ? ld8(dout + (int64_t)rr * ldo + c0) : zero8();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float qf[8], of[8];
+      unpack8(qv[u], qf);
+      unpack8(ov[u], of);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ak[e] += a[u] * qf[e];
+        av[e] += b[u] * of[e];
+      }
     }
   }
-  red[0][w][lane] = ak;
-  red[1][w][lane] = av;
+  for (; r < rows; r += 32) {
+    const float a = bf2f(dsr[r]), b = bf2f(ptr[r]);
+    if (live) {
+      float qf[8], of[8];
+      unpack8(ld8(q + (int64_t)r * ldq + c0), qf);
+      unpack8(ld8(dout + (int64_t)r * ldo + c0), of);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ak[e] += a * qf[e];
+        av[e] += b * of[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[0][rg][cg * 8 + e] = ak[e];
+    red[1][rg][cg * 8 + e] = av[e];
+  }
   __syncthreads();
-  if (w == 0 && live) {
-    dk[j * ldk + c] = ((red[0][0][lane] + red[0][1][lane]) + red[0][2][lane]) + red[0][3][lane];
-    dv[j * ldv + c] = ((red[1][0][lane] + red[1][1][lane]) + red[1][2][lane]) + red[1][3][lane];
+  if (t < 128) {
+    const int which = t >> 6, c = t & 63;
+    float sum = 0.f;
+    for (int g = 0; g < 32; ++g) sum += red[which][g][c];
+    const int col = blockIdx.y * 64 + c;
+    if (col < cols) {
+      if (which == 0) dk[j * ldk + col] = sum;
+      else dv[j * ldv + col] = sum;
+    }
   }
 }
 
@@ -538,6 +587,22 @@ extern "C" int fvx_act_backward(int act, const void* in, int64_t ldi, const void
   return launch_status("act_backward");
 }
 
+extern "C" int fvx_geglu_rows(const void* gu, int64_t ldgu, void* out, int64_t ldo,
+                              int64_t rows, int64_t cols, void* stream) {
+  clear_error();
+  FVX_REQUIRE(gu && out, FVX_ERR_NULL, "geglu_rows: gu and out are required");
+  FVX_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols < (1 << 30) &&
+                  ldgu >= 2 * cols && ldo >= cols && ldgu % 8 == 0 && ldo % 8 == 0,
+              FVX_ERR_SHAPE, "geglu_rows: bad sizes");
+  FVX_REQUIRE(al16(gu) && al16(out), FVX_ERR_ALIGN,
+              "geglu_rows: pointers must be 16-byte aligned");
+  if (rows == 0) return FVX_OK;
+  hipLaunchKernelGGL(act_backward_kernel<kGegluFwd>, dim3(blocks(rows * (cols / 8), 256)),
+                     dim3(256), 0, (hipStream_t)stream, (const bf16_t*)gu, ldgu,
+                     (const bf16_t*)gu, ldgu, (bf16_t*)out, ldo, rows, (int)cols);
+  return launch_status("geglu_rows");
+}
+
 extern "C" int fvx_attention_rows_backward(
     const float* s, int64_t lds, const float* dp, int64_t lddp, const int32_t* kgrp,
     const int32_t* qgrp, void* ds, int64_t ldds, void* ds_t, void* p_t, int64_t ldt,
@@ -580,9 +645,12 @@ extern "C" int fvx_attention_suffix_kv_backward(const void* ds_t, const void* p_
   FVX_REQUIRE(ds_t && p_t && q && dout && dk && dv, FVX_ERR_NULL,
               "attention_suffix_kv_backward: every operand is required");
   FVX_REQUIRE(n_suffix >= 0 && n_suffix < 65536 && rows > 0 && rows < (1 << 30) &&
-                  cols > 0 && cols < (1 << 22) && ldt >= rows && ldq >= cols &&
-                  ldo >= cols && ldk >= cols && ldv >= cols,
+                  cols > 0 && cols % 8 == 0 && cols < (1 << 22) && ldt >= rows &&
+                  ldq >= cols && ldo >= cols && ldq % 8 == 0 && ldo % 8 == 0 &&
+                  ldk >= cols && ldv >= cols,
               FVX_ERR_SHAPE, "attention_suffix_kv_backward: bad sizes");
+  FVX_REQUIRE(al16(q) && al16(dout), FVX_ERR_ALIGN,
+              "attention_suffix_kv_backward: q and dout must be 16-byte aligned");
   if (n_suffix == 0) return FVX_OK;
   hipLaunchKernelGGL(attn_suffix_kv_backward_kernel,
                      dim3((unsigned)n_suffix, blocks(cols, 64)), dim3(256), 0,

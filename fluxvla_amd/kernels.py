@@ -943,6 +943,20 @@ def act_backward(act, inp, dy, out=None):
     return out
 
 
+def geglu_rows(gu, out=None):
+    """out = gelu_tanh(gu[:, :n]) * gu[:, n:] (bf16; fvx_geglu_rows)."""
+    _check(gu, 'gu', contiguous=False)
+    rows, ldgu = _rows_ld(gu, 'gu')
+    n = gu.shape[-1] // 2
+    if out is None:
+        out = torch.empty(rows, n, dtype=BF16, device=gu.device)
+    _check(out, 'out', contiguous=False)
+    _, ldo = _rows_ld(out, 'out')
+    _lib.call('fvx_geglu_rows', _ptr(gu), ldgu, _ptr(out), ldo, rows, n,
+              _stream())
+    return out
+
+
 def attention_rows_backward(s, dp, ds, *, heads, n_keys, scale, kgrp=None,
                             qgrp=None, ds_t=None, p_t=None, key0=0,
                             n_suffix=0):

@@ -8,14 +8,16 @@ the whole denoiser, x_1 = x_t - (1 - t) u(x_t) for the model velocity u and
 e = w (prev - x_1) on the previous chunk's rows.  Here one Euler step is
 
   forward   the expert as in the plain loop, keeping each layer's input
-            stream X[i], its post-attention stream X2[i] and its rotated
+            stream X[i], its post-attention stream X2[i], its rotated
             queries Q[i] (the key/value cache already holds the suffix
-            keys and values); u from a PLAIN fp32 GEMM of action_out_proj;
+            keys and values) and its MLP's [gate | up] rows GU[i] (one GEMM
+            over the stacked weights, then the GeGLU product); u from a
+            PLAIN fp32 GEMM of action_out_proj;
   error     e = bf16(w (prev - x + (1 - t) u))                (one kernel);
   backward  g = J_u^T e layer by layer, last to first:
               down:       dh = (gate2 dX3) @ W_down
-              GeGLU:      [gg | uu] recomputed from X2 (two GEMMs), the
-                          activation backward, da = d[gg | uu] @ [Wg; Wu]
+              GeGLU:      the activation backward on GU[i],
+                          da = d[gate | up] @ [Wg; Wu]
               norm:       dX2 = dX3 + RMSNorm-backward(X2, da)
               O:          dO = (gate1 dX2) @ W_o
               attention:  S = Q K^T, dP = dO V^T (fp32), the masked softmax
@@ -60,6 +62,11 @@ class ExpertVJP:
         self.m = m = model
         cfg = m.cfg
         self.wT = []
+        # [gate; up] stacked: one forward GEMM whose output the backward
+        # keeps ([gate | up] per row)
+        self.gu_w = [torch.cat([_weight_t(L['gate_w']).t(),
+                                _weight_t(L['up_w']).t()], 0).contiguous()
+                     for L in m.exp['layers']]
         for L in m.exp['layers']:
             gu = torch.cat([_weight_t(L['gate_w']), _weight_t(L['up_w'])], 1)
             self.wT.append({'qkv': _weight_t(L['qkv_w']),
@@ -75,6 +82,7 @@ class ExpertVJP:
         # fragment-major copies for the M <= 64 GEMMs (bs = 1)
         F = K.FragB.pack
         self.wT_f = [{nm: F(w) for nm, w in L.items()} for L in self.wT]
+        self.gu_w_f = [F(w) for w in self.gu_w]
         self.out_t_f = F(self.out_t)
         if cfg.pi05:
             self.in_t_f = F(self.in_t)
@@ -115,7 +123,7 @@ class ExpertVJP:
             'g': e(B * na, ad, dt=torch.float32),
             'dx': [e(B * Ss, hid, dt=torch.float32) for _ in range(2)],
             'da': e(B * Ss, hid, dt=torch.float32), 'a': e(B * Ss, hid),
-            'dh': e(B * Ss, mlp), 'gu': e(B * Ss, 2 * mlp),
+            'dh': e(B * Ss, mlp), 'GU': e(nL, B * Ss, 2 * mlp),
             'dgu': e(B * Ss, 2 * mlp), 'dctx': e(B, Ss, H * D),
             's': e(R, T, dt=torch.float32), 'dp': e(R, T, dt=torch.float32),
             'ds': e(R, T), 'ds_t': e(Ss, R), 'p_t': e(Ss, R),
@@ -192,13 +200,15 @@ class ExpertVJP:
             gate = v['gate'] if cfg.pi05 else None
             K.gemm(v['ctx'].view(B * Ss, -1), L['o_w'], out=X2[i], residual=x,
                    gate=gate)
+            # [gate | up] kept for the backward, then the GeGLU product
+            w_gu = self.gu_w_f[i] if fr else self.gu_w[i]
             if cfg.pi05:
                 K.adarms_norm(X2[i], st[2 * i + 1:2 * i + 2], out=v['xn'],
                               gate_out=v['gate'], eps=cfg.rms_eps)
-                K.gemm_geglu(v['xn'], L['gate_w'], L['up_w'], out=v['h'])
+                K.gemm(v['xn'], w_gu, out=v['GU'][i])
             else:
-                K.gemm_geglu(X2[i], L['gate_w'], L['up_w'], out=v['h'],
-                             rownorm_eps=cfg.rms_eps)
+                K.gemm(X2[i], w_gu, out=v['GU'][i], rownorm_eps=cfg.rms_eps)
+            K.geglu_rows(v['GU'][i], out=v['h'])
             K.gemm(v['h'], L['down_w'], out=X[i + 1], residual=X2[i],
                    gate=gate)
         lead = Ss - na
@@ -251,19 +261,11 @@ class ExpertVJP:
                                 row_group=na, row_group_stride=Ss)
         for i in range(nL - 1, -1, -1):
             wt = wts[i]
-            L = m.exp_f[i] if fr else m.exp['layers'][i]
-            # MLP: dh = (gate2 dX3) @ W_down, [gg | uu] recomputed from X2
+            # MLP: dh = (gate2 dX3) @ W_down, then GeGLU's backward on the
+            # [gate | up] rows the forward kept
             K.gemm(v['a'], wt['down'], out=v['dh'])
-            gu = v['gu']
-            if cfg.pi05:
-                K.adarms_norm(X2[i], st[2 * i + 1:2 * i + 2], out=v['xn'],
-                              eps=eps)
-                a2, rn = v['xn'], None
-            else:
-                a2, rn = X2[i], eps
-            K.gemm(a2, L['gate_w'], out=gu[:, :mlp], rownorm_eps=rn)
-            K.gemm(a2, L['up_w'], out=gu[:, mlp:], rownorm_eps=rn)
-            K.act_backward(_lib.ACT_BWD_GEGLU, gu, v['dh'], out=v['dgu'])
+            K.act_backward(_lib.ACT_BWD_GEGLU, v['GU'][i], v['dh'],
+                           out=v['dgu'])
             K.gemm(v['dgu'], wt['gu'], out=v['da'], out_f32=True)
             K.rms_norm_backward(
                 X2[i], v['da'], dres=dx, out=dx2, out_bf16=v['a'],

@@ -528,6 +528,14 @@ int fvx_act_backward(int act, const void* in, int64_t ldi, const void* dy,
                      int64_t ldy, void* out, int64_t ldo, int64_t rows,
                      int64_t cols, void* stream);
 
+/* GeGLU product row by row: out[r][c] = bf16(gelu_tanh(gu[r][c]) *
+ * gu[r][cols + c]) -- GemmaMLP's act(gate) * up (condition_gemma.py:
+ * 156-192) from a stored [gate | up] GEMM output, which the backward then
+ * reuses (the fused GEGLU GEMM keeps neither).  Same layout rules as
+ * fvx_act_backward. */
+int fvx_geglu_rows(const void* gu, int64_t ldgu, void* out, int64_t ldo,
+                   int64_t rows, int64_t cols, void* stream);
+
 /* Masked-softmax backward of one attention problem
  * (condition_gemma.py:340-535's eager attention, softmax over
  * scale * q k^T with the make_att_2d_masks rule of model_utils.py:77-95):
@@ -552,8 +560,9 @@ int fvx_attention_rows_backward(const float* s, int64_t lds, const float* dp,
  * p_t as fvx_attention_rows_backward writes them ([n_suffix, ldt] bf16,
  * column r = query row r),
  *   dk[j][c] = sum_r ds_t[j][r] q[r][c],  dv[j][c] = sum_r p_t[j][r] dout[r][c]
- * for j < n_suffix, c < cols, r < rows (q, dout bf16 [rows, ld]; dk, dv
- * fp32).  The heads of a key/value head are rows of the same sums. */
+ * for j < n_suffix, c < cols, r < rows (q, dout bf16 [rows, ld], 16-byte
+ * aligned, cols and the leading dims multiples of 8; dk, dv fp32).  The
+ * heads of a key/value head are rows of the same sums. */
 int fvx_attention_suffix_kv_backward(const void* ds_t, const void* p_t,
                                      int64_t ldt, const void* q, int64_t ldq,
                                      const void* dout, int64_t ldo, float* dk,

@@ -255,3 +255,14 @@ def test_attention_suffix_kv_backward(K, cuda):
                                    do.to(cuda), dk, dv)
     assert rel_err(dk, ds_t.double() @ q.double()) <= F32_TOL
     assert rel_err(dv, p_t.double() @ do.double()) <= F32_TOL
+
+
+def test_geglu_rows(K, cuda):
+    """out = gelu_tanh(gate) * up from stored [gate | up] rows, against
+    float64 of the same bf16 inputs."""
+    announce('geglu_rows')
+    m, n = 51, 4096
+    gu = randn((m, 2 * n), 91, std=1.5)
+    out = K.geglu_rows(gu.to(cuda))
+    g, u = gu[:, :n].double(), gu[:, n:].double()
+    assert rel_err(out, F.gelu(g, approximate='tanh') * u) <= BF16_TOL
