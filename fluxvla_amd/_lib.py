@@ -127,6 +127,27 @@ class ImageDesc(ctypes.Structure):
 
 RESIZE_LINEAR, RESIZE_PIL_BILINEAR = 0, 1
 
+
+class AttnBwdDesc(ctypes.Structure):
+    """Mirror of ``fvx_attn_bwd_desc``."""
+    _fields_ = [
+        ('q', c_vp), ('q_zs', c_i64),
+        ('o', c_vp), ('o_zs', c_i64),
+        ('dout', c_vp), ('do_zs', c_i64),
+        ('k', c_vp), ('k_zs', c_i64),
+        ('v', c_vp), ('v_zs', c_i64),
+        ('kt', c_vp), ('kt_ld', c_i64), ('kt_zs', c_i64),
+        ('kgrp', c_vp), ('kgrp_zs', c_i64),
+        ('qgrp', c_vp), ('qgrp_zs', c_i64),
+        ('stats', c_vp),
+        ('dq', c_vp), ('dq_parts', c_i64),
+        ('ds_t', c_vp), ('p_t', c_vp), ('ldt', c_i64), ('t_zs', c_i64),
+        ('rows', c_i64), ('heads', c_i64), ('head_dim', c_i64),
+        ('n_keys', c_i64), ('key0', c_i64), ('n_suffix', c_i64),
+        ('n_problems', c_i64),
+        ('scale', c_f32),
+    ]
+
 # name -> (restype, argtypes); the exact set declared by include/fluxvla_amd.h
 SIGNATURES = {
     'fvx_version': (c_i32, []),
@@ -172,9 +193,11 @@ SIGNATURES = {
                                                  c_i64, c_i64, c_vp]),
     'fvx_transpose_bf16': (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
                                    c_i64, c_i64, c_i64, c_vp]),
-    'fvx_rope_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
-                                  c_vp, c_vp, c_i64, c_i64, c_i64, c_i64,
-                                  c_vp]),
+    'fvx_rope_backward': (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,
+                                  c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64,
+                                  c_i64, c_i64, c_vp]),
+    'fvx_attention_backward': (c_i32, [ctypes.POINTER(AttnBwdDesc), c_vp]),
+    'fvx_attention_backward_parts': (c_i64, [c_i64]),
     'fvx_rtc_vjp_error': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
                                   c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
                                   c_vp]),

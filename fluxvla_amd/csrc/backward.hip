@@ -387,6 +387,282 @@ __global__ __launch_bounds__(256) void attn_suffix_kv_backward_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Fused attention backward of the decode shape (rows r = (token, head) of
+// one problem against all its keys, head_dim 256, one key/value head), on
+// bf16 MFMA.  Tiles of 32 rows x 64 keys, one workgroup each (grid: row
+// block, key tile, problem):
+//   attn_bwd_stats_kernel  S = Q K^T for the tile, the masked row maximum
+//                          and sum of exp2 over its keys (log2 domain);
+//   attn_bwd_main_kernel   the row's log-sum-exp from every tile's pair,
+//                          D = dO . O per row, S again (bitwise the same
+//                          MFMA sequence), P, dP = dO V^T, dS = scale P (dP -
+//                          D), the suffix keys' dS and P transposed into
+//                          ds_t / p_t, and dQ's share of the tile, dS K, as
+//                          an fp32 partial per key tile (summed by the RoPE
+//                          backward).
+// MFMA 32x32x16 (common.h mfma32x32x16): lane l supplies row / column
+// l % 32 with the 8 k-values 8 (l / 32) .. of each 16-k step; accumulator i
+// of lane l is (row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32).
+// Operands come straight from global memory through buffer views whose
+// bounds make rows past R and keys past the problem's read as zero.
+// ---------------------------------------------------------------------------
+constexpr int kBwdD = 256;       // head_dim of this path
+constexpr int kBwdRB = 32;       // rows per tile
+constexpr int kBwdKT = 64;       // keys per tile
+
+struct AttnBwdArgs {
+  const bf16_t* q; int64_t q_zs;     // [R][256] per problem (rows contiguous)
+  const bf16_t* o; int64_t o_zs;     // attention output, same layout
+  const bf16_t* dout; int64_t do_zs; // its gradient, same layout
+  const bf16_t* k; int64_t k_zs;     // key rows [nk][256]
+  const bf16_t* v; int64_t v_zs;     // value rows [nk][256]
+  const bf16_t* kt; int64_t kt_ld, kt_zs;  // keys transposed [256][kt_ld]
+  const int32_t* kgrp; int64_t kgrp_zs;
+  const int32_t* qgrp; int64_t qgrp_zs;
+  float* pm; float* pl;              // [problem][key tile][R]
+  float* dq; int64_t dq_part_stride; // [key tile][problems * R][256]
+  bf16_t* ds_t; bf16_t* p_t; int64_t ldt, t_zs;  // [problem][n_suffix][ldt]
+  int rows, heads, n_keys, key0, n_suffix, n_kt;
+  float scale;
+};
+
+// Visibility inputs of a tile, read once: each lane's key group (INT_MAX
+// past the keys) and the tile rows' query groups in LDS (INT_MIN past the
+// rows, so that nothing is visible there).  A load per (row, key) behind
+// the mask test would make every test wait for its own round trip.
+__device__ __forceinline__ int32_t bwd_key_group(const AttnBwdArgs& a, const int32_t* kg,
+                                                 int j) {
+  return j < a.n_keys ? (kg ? kg[j] : 0) : INT32_MAX;
+}
+
+__device__ __forceinline__ void bwd_stage_qgrp(const AttnBwdArgs& a, const int32_t* qg,
+                                               int r0, int32_t* sQG) {
+  const int t = threadIdx.x;
+  if (t < kBwdRB) {
+    const int r = r0 + t;
+    sQG[t] = r < a.rows ? (qg ? qg[r / a.heads] : 0) : INT32_MIN;
+  }
+}
+
+// S (or dP) block of 32 rows x 32 keys: A rows from `ra` (row r0 + l % 32),
+// B rows from `rb` (key kb + l % 32), 16 steps over the 256 dims.  All 32
+// loads are issued before the first MFMA (the scheduling barrier keeps the
+// compiler from interleaving them with the MFMAs, which would make every
+// step wait for its own round trip).
+__device__ __forceinline__ f32x16_t bwd_block(__amdgpu_buffer_rsrc_t ra, int r0,
+                                              __amdgpu_buffer_rsrc_t rb, int kb, int lane) {
+  f32x16_t acc = {};
+  const uint32_t ao = (uint32_t)((r0 + (lane & 31)) * kBwdD + 8 * (lane >> 5)) * 2;
+  const uint32_t bo = (uint32_t)((kb + (lane & 31)) * kBwdD + 8 * (lane >> 5)) * 2;
+  bf16x8 av[16], bv[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    av[t] = bload8(ra, ao + (uint32_t)(16 * t) * 2);
+    bv[t] = bload8(rb, bo + (uint32_t)(16 * t) * 2);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < 16; ++t) acc = mfma32x32x16(av[t], bv[t], acc);
+  return acc;
+}
+
+__device__ __forceinline__ int acc_row(int i, int lane) {
+  return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+}
+
+__global__ __launch_bounds__(128) void attn_bwd_stats_kernel(AttnBwdArgs a) {
+  // the tile's masked logits (log2 domain), [row][key], then reduced per row
+  // by 4 threads of 16 keys each (LDS instead of 2 x 5 cross-lane steps per
+  // accumulator row)
+  __shared__ float sX[kBwdRB][kBwdKT + 1];
+  __shared__ int32_t sQG[kBwdRB];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int z = blockIdx.z, kt = blockIdx.y, r0 = blockIdx.x * kBwdRB;
+  const int kb = kt * kBwdKT + 32 * w;
+  const int32_t* kg = a.kgrp ? a.kgrp + z * a.kgrp_zs : nullptr;
+  const int32_t* qg = a.qgrp ? a.qgrp + z * a.qgrp_zs : nullptr;
+  const int j = kb + (lane & 31);
+  // the mask groups' loads go out first and are consumed after the MFMAs
+  const int32_t kgv = bwd_key_group(a, kg, j);
+  const int32_t qgv = (t < kBwdRB && r0 + t < a.rows) ? (qg ? qg[(r0 + t) / a.heads] : 0)
+                                                      : INT32_MIN;
+  const uint32_t rbytes = (uint32_t)a.rows * kBwdD * 2, kbytes = (uint32_t)a.n_keys * kBwdD * 2;
+  const f32x16_t s = bwd_block(make_rsrc(a.q + z * a.q_zs, rbytes), r0,
+                               make_rsrc(a.k + z * a.k_zs, kbytes), kb, lane);
+  if (t < kBwdRB) sQG[t] = qgv;
+  __syncthreads();
+  const float c = a.scale * 1.4426950408889634f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int rr = acc_row(i, lane);
+    sX[rr][32 * w + (lane & 31)] = kgv <= sQG[rr] ? s[i] * c : -INFINITY;
+  }
+  __syncthreads();
+  const int rr = t >> 2, part = t & 3;
+  float x[16], m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    x[u] = sX[rr][16 * part + u];
+    m = fmaxf(m, x[u]);
+  }
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  float e = 0.f;
+  if (m != -INFINITY)
+#pragma unroll
+    for (int u = 0; u < 16; ++u) e += x[u] == -INFINITY ? 0.f : exp2f(x[u] - m);
+  e += __shfl_xor(e, 1, 64);
+  e += __shfl_xor(e, 2, 64);
+  if (part == 0 && r0 + rr < a.rows) {
+    const int64_t at = ((int64_t)z * a.n_kt + kt) * a.rows + r0 + rr;
+    a.pm[at] = m;
+    a.pl[at] = e;
+  }
+}
+
+__global__ __launch_bounds__(256) void attn_bwd_main_kernel(AttnBwdArgs a) {
+  __shared__ float sD[kBwdRB], sLse[kBwdRB];
+  __shared__ int32_t sQG[kBwdRB];
+  __shared__ float sdP[2][16][64];
+  __shared__ __align__(16) bf16_t sDS[kBwdRB][kBwdKT + 8];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int z = blockIdx.z, kt = blockIdx.y, r0 = blockIdx.x * kBwdRB;
+  const int k0 = kt * kBwdKT;
+  const uint32_t rbytes = (uint32_t)a.rows * kBwdD * 2, kbytes = (uint32_t)a.n_keys * kBwdD * 2;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q + z * a.q_zs, rbytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc(a.dout + z * a.do_zs, rbytes);
+  // D = dO . O of the tile's rows: thread t takes 32 dims of row t / 8
+  {
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.o + z * a.o_zs, rbytes);
+    const int rr = t >> 3;
+    const uint32_t off = (uint32_t)((r0 + rr) * kBwdD + 32 * (t & 7)) * 2;
+    float d = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float fo[8], fd[8];
+      unpack8(bload8(ro, off + 16 * u), fo);
+      unpack8(bload8(rdo, off + 16 * u), fd);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d += fo[e] * fd[e];
+    }
+    d += __shfl_xor(d, 1, 64);
+    d += __shfl_xor(d, 2, 64);
+    d += __shfl_xor(d, 4, 64);
+    if ((t & 7) == 0) sD[rr] = d;
+  }
+  // log-sum-exp (log2 domain) of each row over every key tile's pair: 16
+  // tiles' pairs loaded at once per pass (unconditional buffer loads; the
+  // tiles past n_kt are masked after), a running rescale between passes
+  if (t < kBwdRB) {
+    float M = -INFINITY, L = 0.f;
+    if (r0 + t < a.rows) {
+      // views of this problem's pairs (workgroup-uniform: a per-lane view
+      // would make every load a loop over the lanes)
+      const int64_t base = (int64_t)z * a.n_kt * a.rows;
+      const uint32_t bytes = (uint32_t)((int64_t)a.n_kt * a.rows * 4);
+      const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.pm + base, bytes);
+      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.pl + base, bytes);
+      for (int u0 = 0; u0 < a.n_kt; u0 += 16) {
+        float mv[16], lv[16], mn = M;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const uint32_t off = (uint32_t)(((int64_t)(u0 + u) * a.rows + r0 + t) * 4);
+          mv[u] = bload1f(rm, off);
+          lv[u] = bload1f(rl, off);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (u0 + u >= a.n_kt) mv[u] = -INFINITY;
+          mn = fmaxf(mn, mv[u]);
+        }
+        if (mn != -INFINITY) {
+          L *= exp2f(M - mn);  // 0 on the first pass (M = -inf)
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            if (mv[u] != -INFINITY) L += lv[u] * exp2f(mv[u] - mn);
+          M = mn;
+        }
+      }
+    }
+    sLse[t] = L > 0.f ? M + log2f(L) : INFINITY;
+  }
+  const int32_t* kg = a.kgrp ? a.kgrp + z * a.kgrp_zs : nullptr;
+  const int32_t* qg = a.qgrp ? a.qgrp + z * a.qgrp_zs : nullptr;
+  const int kh = w & 1, kb = k0 + 32 * kh, j = kb + (lane & 31);
+  const int32_t kgv = bwd_key_group(a, kg, j);
+  // loaded now, stored after the MFMAs (no wait ahead of the operand loads)
+  const int rq_t = t - 128;
+  const int32_t qgv = (rq_t >= 0 && rq_t < kBwdRB && r0 + rq_t < a.rows)
+                          ? (qg ? qg[(r0 + rq_t) / a.heads] : 0)
+                          : INT32_MIN;
+  f32x16_t acc;
+  if (w < 2) {
+    acc = bwd_block(rq, r0, make_rsrc(a.k + z * a.k_zs, kbytes), kb, lane);
+  } else {
+    acc = bwd_block(rdo, r0, make_rsrc(a.v + z * a.v_zs, kbytes), kb, lane);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sdP[kh][i][lane] = acc[i];
+    if (rq_t >= 0 && rq_t < kBwdRB) sQG[rq_t] = qgv;
+  }
+  __syncthreads();
+  if (w < 2) {
+    const float c = a.scale * 1.4426950408889634f;
+    bf16_t* dst = a.ds_t ? a.ds_t + z * a.t_zs : nullptr;
+    bf16_t* pst = a.p_t ? a.p_t + z * a.t_zs : nullptr;
+    const int js = j - a.key0;
+    const bool suf = js >= 0 && js < a.n_suffix;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rr = acc_row(i, lane), r = r0 + rr;
+      float p = 0.f, ds = 0.f;
+      if (kgv <= sQG[rr]) {
+        p = exp2f(acc[i] * c - sLse[rr]);
+        ds = a.scale * p * (sdP[kh][i][lane] - sD[rr]);
+      }
+      sDS[rr][32 * kh + (lane & 31)] = f2bf(ds);
+      if (suf && r < a.rows) {
+        if (dst) dst[(int64_t)js * a.ldt + r] = f2bf(ds);
+        if (pst) pst[(int64_t)js * a.ldt + r] = f2bf(p);
+      }
+    }
+  }
+  __syncthreads();
+  // dQ share of this key tile: [32 rows][256 dims] = dS [32][64] K [64][256];
+  // wave w takes the dims 64 w .. 64 w + 63 (two 32-column blocks)
+  const __amdgpu_buffer_rsrc_t rkt =
+      make_rsrc(a.kt + z * a.kt_zs, (uint32_t)(kBwdD * a.kt_ld * 2));
+  f32x16_t dq[2] = {};
+  bf16x8 kv[4][2], av[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int key = k0 + 16 * ks + 8 * (lane >> 5);  // 8 keys wholly below kt_ld or not
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int d = 64 * w + 32 * nb + (lane & 31);
+      kv[ks][nb] = bload8(rkt, key < a.kt_ld ? (uint32_t)(d * a.kt_ld + key) * 2 : kOOB);
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    av[ks] = *reinterpret_cast<const bf16x8*>(&sDS[lane & 31][16 * ks + 8 * (lane >> 5)]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) dq[nb] = mfma32x32x16(av[ks], kv[ks][nb], dq[nb]);
+  float* out = a.dq + (int64_t)kt * a.dq_part_stride + ((int64_t)z * a.rows + r0) * kBwdD;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int d = 64 * w + 32 * nb + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rr = acc_row(i, lane);
+      if (r0 + rr < a.rows) out[(int64_t)rr * kBwdD + d] = dq[nb][i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // bf16 transpose, 32 x 32 tiles through LDS (one padding column keeps the
 // column reads conflict-free): dst[b][c][r] = src[b][r][c].
 // ---------------------------------------------------------------------------
@@ -422,7 +698,8 @@ __global__ __launch_bounds__(256) void transpose_kernel(
 // column pair.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rope_backward_kernel(
-    const float* __restrict__ dq, int64_t ldq, const float* __restrict__ dk,
+    const float* __restrict__ dq, int64_t ldq, int dq_parts, int64_t dq_part_stride,
+    const float* __restrict__ dk,
     int64_t ldk, const float* __restrict__ dv, int64_t ldv,
     const float* __restrict__ rope, const int32_t* __restrict__ positions,
     bf16_t* __restrict__ out, int64_t ldo, int64_t rows, int n_q_heads,
@@ -437,8 +714,13 @@ __global__ __launch_bounds__(256) void rope_backward_kernel(
   float a, b;
   bool rot = true;
   if (p < qpairs) {
-    a = dq[m * ldq + 2 * p];
-    b = dq[m * ldq + 2 * p + 1];
+    // dq: the sum of dq_parts partials (key tiles), in part order
+    a = b = 0.f;
+    for (int u = 0; u < dq_parts; ++u) {
+      const float2 v = *reinterpret_cast<const float2*>(dq + u * dq_part_stride + m * ldq + 2 * p);
+      a += v.x;
+      b += v.y;
+    }
   } else if (p < qpairs + half) {
     const int i = p - qpairs;
     a = dk[m * ldk + 2 * i];
@@ -678,12 +960,15 @@ extern "C" int fvx_transpose_bf16(const void* src, int64_t ld_src, int64_t src_b
   return launch_status("transpose_bf16");
 }
 
-extern "C" int fvx_rope_backward(const float* dq, int64_t ldq, const float* dk, int64_t ldk,
+extern "C" int fvx_rope_backward(const float* dq, int64_t ldq, int64_t dq_parts,
+                                 int64_t dq_part_stride, const float* dk, int64_t ldk,
                                  const float* dv, int64_t ldv, const float* rope,
                                  const int32_t* positions, void* out, int64_t ldo,
                                  int64_t rows, int64_t n_q_heads, int64_t head_dim,
                                  void* stream) {
   clear_error();
+  FVX_REQUIRE(dq_parts >= 1 && dq_parts < 4096 && (dq_parts == 1 || dq_part_stride % 2 == 0),
+              FVX_ERR_ARG, "rope_backward: bad dq parts");
   FVX_REQUIRE(dq && dk && dv && rope && positions && out, FVX_ERR_NULL,
               "rope_backward: every operand is required");
   FVX_REQUIRE(rows >= 0 && n_q_heads > 0 && head_dim > 0 && head_dim % 2 == 0 &&
@@ -697,8 +982,9 @@ extern "C" int fvx_rope_backward(const float* dq, int64_t ldq, const float* dk, 
   if (rows == 0) return FVX_OK;
   const int64_t pairs = (n_q_heads + 2) * head_dim / 2;
   hipLaunchKernelGGL(rope_backward_kernel, dim3(blocks(rows * pairs, 256)), dim3(256), 0,
-                     (hipStream_t)stream, dq, ldq, dk, ldk, dv, ldv, rope, positions,
-                     (bf16_t*)out, ldo, rows, (int)n_q_heads, (int)head_dim);
+                     (hipStream_t)stream, dq, ldq, (int)dq_parts, dq_part_stride, dk, ldk,
+                     dv, ldv, rope, positions, (bf16_t*)out, ldo, rows, (int)n_q_heads,
+                     (int)head_dim);
   return launch_status("rope_backward");
 }
 
@@ -734,4 +1020,58 @@ extern "C" int fvx_rtc_vjp_update(float* x, int64_t ldx, void* x_bf16, int64_t l
                      (hipStream_t)stream, x, ldx, (bf16_t*)x_bf16, ldxb, u, ldu, prev, ldp, w,
                      g, ldg, gw, rows, (int)cols, period, omt, dt);
   return launch_status("rtc_vjp_update");
+}
+
+extern "C" int fvx_attention_backward(const fvx_attn_bwd_desc* d, void* stream) {
+  clear_error();
+  FVX_REQUIRE(d, FVX_ERR_NULL, "attention_backward: descriptor is NULL");
+  FVX_REQUIRE(d->q && d->o && d->dout && d->k && d->v && d->kt && d->stats && d->dq,
+              FVX_ERR_NULL, "attention_backward: q, o, dout, k, v, kt, stats, dq required");
+  FVX_REQUIRE(d->head_dim == kBwdD, FVX_ERR_SHAPE,
+              "attention_backward: head_dim must be 256 (got %lld)", (long long)d->head_dim);
+  FVX_REQUIRE((d->kgrp == nullptr) == (d->qgrp == nullptr), FVX_ERR_ARG,
+              "attention_backward: kgrp and qgrp must both be given or both be NULL");
+  FVX_REQUIRE(d->n_problems > 0 && d->n_problems < 65536 && d->heads > 0 && d->rows > 0 &&
+                  d->rows % d->heads == 0 && d->n_keys > 0 && d->kt_ld >= d->n_keys &&
+                  d->kt_ld % 8 == 0 && (int64_t)d->rows * kBwdD * 2 < ((int64_t)1 << 31) &&
+                  (int64_t)d->kt_ld * kBwdD * 2 < ((int64_t)1 << 31),
+              FVX_ERR_SHAPE, "attention_backward: bad sizes");
+  FVX_REQUIRE((!d->ds_t && !d->p_t) ||
+                  (d->n_suffix > 0 && d->key0 >= 0 && d->key0 + d->n_suffix <= d->n_keys &&
+                   d->ldt >= d->rows),
+              FVX_ERR_SHAPE, "attention_backward: bad suffix columns");
+  FVX_REQUIRE(al16(d->q) && al16(d->o) && al16(d->dout) && al16(d->k) && al16(d->v) &&
+                  al16(d->kt) && d->q_zs % 8 == 0 && d->o_zs % 8 == 0 && d->do_zs % 8 == 0 &&
+                  d->k_zs % 8 == 0 && d->v_zs % 8 == 0 && d->kt_zs % 8 == 0,
+              FVX_ERR_ALIGN, "attention_backward: operands must be 16-byte aligned");
+  const int n_rb = (int)((d->rows + kBwdRB - 1) / kBwdRB);
+  const int n_kt = (int)((d->n_keys + kBwdKT - 1) / kBwdKT);
+  FVX_REQUIRE(d->dq_parts == n_kt, FVX_ERR_ARG,
+              "attention_backward: dq must hold %d key-tile partials (dq_parts = %lld)", n_kt,
+              (long long)d->dq_parts);
+  AttnBwdArgs a;
+  a.q = (const bf16_t*)d->q; a.q_zs = d->q_zs;
+  a.o = (const bf16_t*)d->o; a.o_zs = d->o_zs;
+  a.dout = (const bf16_t*)d->dout; a.do_zs = d->do_zs;
+  a.k = (const bf16_t*)d->k; a.k_zs = d->k_zs;
+  a.v = (const bf16_t*)d->v; a.v_zs = d->v_zs;
+  a.kt = (const bf16_t*)d->kt; a.kt_ld = d->kt_ld; a.kt_zs = d->kt_zs;
+  a.kgrp = d->kgrp; a.kgrp_zs = d->kgrp_zs;
+  a.qgrp = d->qgrp; a.qgrp_zs = d->qgrp_zs;
+  a.pm = d->stats;
+  a.pl = d->stats + d->n_problems * n_kt * d->rows;
+  a.dq = d->dq; a.dq_part_stride = d->n_problems * d->rows * kBwdD;
+  a.ds_t = (bf16_t*)d->ds_t; a.p_t = (bf16_t*)d->p_t; a.ldt = d->ldt; a.t_zs = d->t_zs;
+  a.rows = (int)d->rows; a.heads = (int)d->heads; a.n_keys = (int)d->n_keys;
+  a.key0 = (int)d->key0; a.n_suffix = (int)d->n_suffix; a.n_kt = n_kt;
+  a.scale = d->scale;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(n_rb, n_kt, (unsigned)d->n_problems);
+  hipLaunchKernelGGL(attn_bwd_stats_kernel, grid, dim3(128), 0, s, a);
+  hipLaunchKernelGGL(attn_bwd_main_kernel, grid, dim3(256), 0, s, a);
+  return launch_status("attention_backward");
+}
+
+extern "C" int64_t fvx_attention_backward_parts(int64_t n_keys) {
+  return n_keys > 0 ? (n_keys + kBwdKT - 1) / kBwdKT : 0;
 }

@@ -1035,18 +1035,88 @@ def transpose(src, dst):
 
 def rope_backward(dq, dk, dv, rope, positions, out, n_q_heads, head_dim):
     """out bf16 [rows, (n_q_heads + 2) * head_dim] = [dq, dk rotated back |
-    dv] (fvx_rope_backward); dq / dk / dv fp32 2-D views."""
+    dv] (fvx_rope_backward); dk / dv fp32 2-D views, dq one too or a 3-D
+    [parts, rows, cols] stack of partials (summed)."""
     for t, nm in ((dq, 'dq'), (dk, 'dk'), (dv, 'dv'), (rope, 'rope')):
         _check(t, nm, dtype=torch.float32, contiguous=(nm == 'rope'))
     _check(positions, 'positions', dtype=torch.int32)
     _check(out, 'out', contiguous=False)
+    parts, pstride = 1, 0
+    if dq.dim() == 3:
+        parts, pstride = dq.shape[0], dq.stride(0)
+        dq = dq[0]
     rows, ldq = _rows_ld(dq, 'dq')
     if positions.numel() < rows or dk.shape[0] != rows or dv.shape[0] != rows:
         raise ValueError('dq, dk, dv and positions must cover the same rows')
-    _lib.call('fvx_rope_backward', _ptr(dq), ldq, _ptr(dk), dk.stride(0),
-              _ptr(dv), dv.stride(0), _ptr(rope), _ptr(positions), _ptr(out),
-              out.stride(0), rows, n_q_heads, head_dim, _stream())
+    _lib.call('fvx_rope_backward', _ptr(dq), ldq, parts, pstride, _ptr(dk),
+              dk.stride(0), _ptr(dv), dv.stride(0), _ptr(rope), _ptr(positions),
+              _ptr(out), out.stride(0), rows, n_q_heads, head_dim, _stream())
     return out
+
+
+def attention_backward_parts(n_keys):
+    """Key-tile partials of fvx_attention_backward's dq."""
+    return int(_lib.load().fvx_attention_backward_parts(n_keys))
+
+
+def attention_backward(q, o, dout, k, v, kt, dq, stats, *, heads, scale,
+                       kgrp=None, qgrp=None, ds_t=None, p_t=None, key0=0,
+                       n_suffix=0):
+    """Fused decode-shape attention backward (fvx_attention_backward) for
+    n problems: q / o / dout bf16 [n, rows, 256]; k / v bf16 [n, >= n_keys,
+    256] rows with n_keys = k.shape[1]; kt bf16 [n, 256, kt_ld] (zero past
+    n_keys); dq fp32 [parts, n * rows, 256]; stats fp32 scratch of
+    2 * n * parts * rows; kgrp int32 [n, >= n_keys], qgrp [n, rows / heads];
+    ds_t / p_t bf16 [n, n_suffix, >= rows]."""
+    d = _lib.AttnBwdDesc()
+    n, rows, hd = q.shape
+    nk = k.shape[1]
+    for t, nm in ((q, 'q'), (o, 'o'), (dout, 'dout')):
+        _check(t, nm, contiguous=False)
+        if t.shape != q.shape or t.stride(1) != hd or t.stride(2) != 1:
+            raise ValueError(f'{nm} must be [n, rows, head_dim] with packed rows')
+    for t, nm in ((k, 'k'), (v, 'v')):
+        _check(t, nm, contiguous=False)
+        if t.shape[0] != n or t.shape[2] != hd or t.stride(1) != hd or t.stride(2) != 1:
+            raise ValueError(f'{nm} must be [n, keys, head_dim] with packed rows')
+    _check(kt, 'kt', contiguous=False)
+    if kt.shape[:2] != (n, hd) or kt.stride(2) != 1 or kt.stride(1) < nk:
+        raise ValueError('kt must be [n, head_dim, >= n_keys]')
+    parts = attention_backward_parts(nk)
+    _check(dq, 'dq', dtype=torch.float32)
+    if dq.shape != (parts, n * rows, hd):
+        raise ValueError(f'dq must be [{parts}, {n * rows}, {hd}]')
+    _check(stats, 'stats', dtype=torch.float32)
+    if stats.numel() < 2 * n * parts * rows:
+        raise ValueError('stats is too small')
+    d.q, d.q_zs = q.data_ptr(), q.stride(0)
+    d.o, d.o_zs = o.data_ptr(), o.stride(0)
+    d.dout, d.do_zs = dout.data_ptr(), dout.stride(0)
+    d.k, d.k_zs = k.data_ptr(), k.stride(0)
+    d.v, d.v_zs = v.data_ptr(), v.stride(0)
+    d.kt, d.kt_ld, d.kt_zs = kt.data_ptr(), kt.stride(1), kt.stride(0)
+    if kgrp is not None:
+        _check(kgrp, 'kgrp', dtype=torch.int32, contiguous=False)
+        _check(qgrp, 'qgrp', dtype=torch.int32, contiguous=False)
+        if (kgrp.shape[-1] < nk or qgrp.shape[-1] < rows // heads
+                or kgrp.stride(-1) != 1 or qgrp.stride(-1) != 1):
+            raise ValueError('kgrp must cover the keys and qgrp every token')
+        d.kgrp, d.kgrp_zs = kgrp.data_ptr(), kgrp.stride(0) if kgrp.dim() > 1 else 0
+        d.qgrp, d.qgrp_zs = qgrp.data_ptr(), qgrp.stride(0) if qgrp.dim() > 1 else 0
+    d.stats = stats.data_ptr()
+    d.dq, d.dq_parts = dq.data_ptr(), parts
+    if ds_t is not None or p_t is not None:
+        for t, nm in ((ds_t, 'ds_t'), (p_t, 'p_t')):
+            _check(t, nm)
+            if t.shape[:2] != (n, n_suffix) or t.shape[2] < rows:
+                raise ValueError(f'{nm} must be [n, n_suffix, >= rows]')
+        d.ds_t, d.p_t = _ptr(ds_t), _ptr(p_t)
+        d.ldt, d.t_zs = ds_t.stride(1), ds_t.stride(0)
+    d.rows, d.heads, d.head_dim = rows, heads, hd
+    d.n_keys, d.key0, d.n_suffix, d.n_problems = nk, key0, n_suffix, n
+    d.scale = float(scale)
+    _lib.call('fvx_attention_backward', ctypes.byref(d), _stream())
+    return dq
 
 
 def rtc_vjp_error(x, u, prev, w, e, omt):

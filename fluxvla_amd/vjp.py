@@ -20,21 +20,21 @@ e = w (prev - x_1) on the previous chunk's rows.  Here one Euler step is
                           da = d[gate | up] @ [Wg; Wu]
               norm:       dX2 = dX3 + RMSNorm-backward(X2, da)
               O:          dO = (gate1 dX2) @ W_o
-              attention:  S = Q K^T, dP = dO V^T (fp32), the masked softmax
-                          backward per row, dQ = dS K, and dK = dS^T Q,
-                          dV = P^T dO on the suffix keys in one kernel (the
-                          prefix cache is a constant of x_t), RoPE backward
+              attention:  one fused MFMA backward (S = Q K^T, P from the
+                          rows' log-sum-exp, dP = dO V^T, dS, dQ = dS K in
+                          key-tile partials), then dK = dS^T Q and dV = P^T
+                          dO on the suffix keys (the prefix cache is a
+                          constant of x_t), RoPE backward summing dQ
               QKV:        da = d[q | k | v] @ W_qkv
               norm:       dX = dX2 + RMSNorm-backward(X, da)
             and through the suffix embedding (PI0: action-time MLP with
             its SiLU; PI0.5: action_in_proj) to g = dL/dx_t;
   update    x <- x + dt u - dt gw e + dt gw (1 - t) g              (one kernel).
 
-The weights' products and the attention's Q K^T, dO V^T and dS K run
-through fvx_gemm: on [in, out] copies of the prepared [out, in] weights (fp8
-weights dequantized to bf16; fragment-major for the M <= 64 GEMMs of bs=1),
-on a transposed copy of the key cache and a row-major copy of the value
-cache.  All of it is part of the captured chunk
+The weights' products run through fvx_gemm on [in, out] copies of the
+prepared [out, in] weights (fp8 weights dequantized to bf16; fragment-major
+for the M <= 64 GEMMs of bs=1); the attention backward reads the key cache,
+a transposed copy of it and a row-major copy of the value cache.  All of it is part of the captured chunk
 graph: per-request values (previous chunk, weights, guidance weights) are
 device buffers.
 """
@@ -105,6 +105,7 @@ class ExpertVJP:
         na, hid, mlp = cfg.n_action_steps, cfg.exp_hidden, cfg.exp_mlp
         T, nL, ad = m.kv_len, cfg.exp_layers, cfg.max_action_dim
         R = Ss * H
+        parts = K.attention_backward_parts(S + Ss)
 
         def e(*shape, dt=BF16):
             return torch.empty(*shape, dtype=dt, device=dev)
@@ -113,7 +114,7 @@ class ExpertVJP:
             return torch.zeros(*shape, dtype=dt, device=dev)
         v = {
             'X': e(nL + 1, B * Ss, hid), 'X2': e(nL, B * Ss, hid),
-            'Q': e(nL, B * Ss, H * D), 'ctx': e(B, Ss, H * D),
+            'Q': e(nL, B * Ss, H * D), 'CTX': e(nL, B * Ss, H * D),
             'h': e(B * Ss, mlp), 'xn': e(B * Ss, hid), 'gate': e(B * Ss, hid),
             # key cache transposed [layer][batch][dim][token] and value cache
             # row-major [layer][batch][token][dim]; the columns / rows past
@@ -125,9 +126,9 @@ class ExpertVJP:
             'da': e(B * Ss, hid, dt=torch.float32), 'a': e(B * Ss, hid),
             'dh': e(B * Ss, mlp), 'GU': e(nL, B * Ss, 2 * mlp),
             'dgu': e(B * Ss, 2 * mlp), 'dctx': e(B, Ss, H * D),
-            's': e(R, T, dt=torch.float32), 'dp': e(R, T, dt=torch.float32),
-            'ds': e(R, T), 'ds_t': e(Ss, R), 'p_t': e(Ss, R),
-            'dq': e(B * Ss, H * D, dt=torch.float32),
+            'ds_t': e(B, Ss, R), 'p_t': e(B, Ss, R),
+            'dq': e(parts, B * R, D, dt=torch.float32),
+            'stats': e(2 * B * parts * R, dt=torch.float32),
             'dk': e(B * Ss, D, dt=torch.float32),
             'dv': e(B * Ss, D, dt=torch.float32),
             'dqkv': e(B * Ss, (H + 2) * D),
@@ -194,12 +195,12 @@ class ExpertVJP:
                             kc.view(B * T, D)[S:], vc[:, :, S:], H, D,
                             rownorm_eps=rn, row_group=Ss, row_group_stride=T,
                             v_ld=T)
+            ctx = v['CTX'][i]
             K.mqa_attention(Q[i].view(B, Ss, H * D), kc[:, :S + Ss], vc,
-                            v['ctx'], kgrp=b['kgrp'], qgrp=b['qgrp_suf'],
-                            v_transposed=True)
+                            ctx.view(B, Ss, H * D), kgrp=b['kgrp'],
+                            qgrp=b['qgrp_suf'], v_transposed=True)
             gate = v['gate'] if cfg.pi05 else None
-            K.gemm(v['ctx'].view(B * Ss, -1), L['o_w'], out=X2[i], residual=x,
-                   gate=gate)
+            K.gemm(ctx, L['o_w'], out=X2[i], residual=x, gate=gate)
             # [gate | up] kept for the backward, then the GeGLU product
             w_gu = self.gu_w_f[i] if fr else self.gu_w[i]
             if cfg.pi05:
@@ -296,7 +297,8 @@ class ExpertVJP:
 
     def _attention_backward(self, b, B, i):
         """dq, dk, dv of layer i's attention from dO (v['dctx']), packed with
-        the RoPE backward into v['dqkv']."""
+        the RoPE backward into v['dqkv']: the fused attention backward over
+        the batch's problems, then the suffix keys' dK / dV per sample."""
         m, cfg, v = self.m, self.m.cfg, self._bufs[B]
         S, Ss, D, H = cfg.prefix_len, cfg.suffix_len, cfg.head_dim, cfg.heads
         nk, R = S + Ss, Ss * H
@@ -307,17 +309,14 @@ class ExpertVJP:
         K.transpose(vc[:, :, S:nk], vr[:, S:nk])
         q3 = v['Q'][i].view(B, R, D)
         do3 = v['dctx'].view(B, R, D)
-        dq3 = v['dq'].view(B, R, D)
+        K.attention_backward(q3, v['CTX'][i].view(B, R, D), do3, kc[:, :nk],
+                             vr[:, :nk], kT, v['dq'], v['stats'], heads=H,
+                             scale=self.scale, kgrp=b['kgrp'],
+                             qgrp=b['qgrp_suf'], ds_t=v['ds_t'], p_t=v['p_t'],
+                             key0=S, n_suffix=Ss)
         for z in range(B):
-            K.gemm(q3[z], kc[z, :nk], out=v['s'][:, :nk], out_f32=True)
-            K.gemm(do3[z], vr[z, :nk], out=v['dp'][:, :nk], out_f32=True)
-            K.attention_rows_backward(
-                v['s'], v['dp'], v['ds'], heads=H, n_keys=nk,
-                scale=self.scale, kgrp=b['kgrp'][z], qgrp=b['qgrp_suf'][z],
-                ds_t=v['ds_t'], p_t=v['p_t'], key0=S, n_suffix=Ss)
-            K.gemm(v['ds'], kT[z], out=dq3[z], out_f32=True)
             rows = slice(z * Ss, (z + 1) * Ss)
-            K.attention_suffix_kv_backward(v['ds_t'], v['p_t'], q3[z], do3[z],
-                                           v['dk'][rows], v['dv'][rows])
-        K.rope_backward(v['dq'], v['dk'], v['dv'], m.rope, b['pos_suf'],
-                        v['dqkv'], H, D)
+            K.attention_suffix_kv_backward(v['ds_t'][z], v['p_t'][z], q3[z],
+                                           do3[z], v['dk'][rows], v['dv'][rows])
+        K.rope_backward(v['dq'].view(-1, B * Ss, H * D), v['dk'], v['dv'],
+                        m.rope, b['pos_suf'], v['dqkv'], H, D)

@@ -570,6 +570,42 @@ int fvx_attention_suffix_kv_backward(const void* ds_t, const void* p_t,
                                      int64_t n_suffix, int64_t rows,
                                      int64_t cols, void* stream);
 
+/* Fused attention backward of the decode shape (the action expert's
+ * suffix rows against its cached prefix and suffix keys; the eager
+ * attention's backward under autograd, condition_gemma.py:340-535), on bf16
+ * MFMA in 32-row x 64-key tiles.  Per problem z: rows r = token * heads +
+ * head of q / o / dout ([rows][256] bf16, o the attention output), keys j <
+ * n_keys of k and v ([n_keys][256] bf16 rows) and kt (the keys transposed,
+ * [256][kt_ld] bf16, zero past n_keys), visibility kgrp[j] <= qgrp[r /
+ * heads] (both NULL: all).  With P = softmax(scale q k^T) over the visible
+ * keys, D = dout . o per row and dS = scale P (dout v^T - D):
+ *   dq  (fp32 [dq_parts][n_problems * rows][256]): key tile t's share of
+ *       dS k (dq_parts = fvx_attention_backward_parts(n_keys); their sum is
+ *       dq, which fvx_rope_backward adds up);
+ *   ds_t / p_t (may be NULL; bf16 [n_problems][n_suffix][ldt], problem
+ *       stride t_zs): dS and P of keys key0 .. key0 + n_suffix - 1,
+ *       column r = row r (fvx_attention_suffix_kv_backward's operands);
+ *   stats: fp32 scratch of 2 * n_problems * dq_parts * rows floats.
+ * Strides (*_zs) in elements; head_dim must be 256. */
+typedef struct fvx_attn_bwd_desc {
+  const void* q; int64_t q_zs;
+  const void* o; int64_t o_zs;
+  const void* dout; int64_t do_zs;
+  const void* k; int64_t k_zs;
+  const void* v; int64_t v_zs;
+  const void* kt; int64_t kt_ld, kt_zs;
+  const int32_t* kgrp; int64_t kgrp_zs;
+  const int32_t* qgrp; int64_t qgrp_zs;
+  float* stats;
+  float* dq; int64_t dq_parts;
+  void* ds_t; void* p_t; int64_t ldt, t_zs;
+  int64_t rows, heads, head_dim, n_keys, key0, n_suffix, n_problems;
+  float scale;
+} fvx_attn_bwd_desc;
+
+int fvx_attention_backward(const fvx_attn_bwd_desc* d, void* stream);
+int64_t fvx_attention_backward_parts(int64_t n_keys);
+
 /* bf16 transpose: dst[b][c][r] = src[b][r][c] for b < batch, r < rows,
  * c < cols (element offsets b * batch_stride + row * ld). */
 int fvx_transpose_bf16(const void* src, int64_t ld_src,
@@ -581,8 +617,11 @@ int fvx_transpose_bf16(const void* src, int64_t ld_src,
  * [dq (n_q_heads heads) | dk | dv], each head's column pair (2i, 2i+1)
  * of dq and dk rotated by the transpose of the forward rotation at
  * rope[positions[m]][i] (fp32 (cos, sin) pairs, the fvx_gemm QKV_ROPE
- * table): (ga, gb) -> (ga cos + gb sin, gb cos - ga sin). */
-int fvx_rope_backward(const float* dq, int64_t ldq, const float* dk,
+ * table): (ga, gb) -> (ga cos + gb sin, gb cos - ga sin).  dq is the sum of
+ * dq_parts partials dq_part_stride elements apart (fvx_attention_backward's
+ * key tiles; 1 for a plain dq). */
+int fvx_rope_backward(const float* dq, int64_t ldq, int64_t dq_parts,
+                      int64_t dq_part_stride, const float* dk,
                       int64_t ldk, const float* dv, int64_t ldv,
                       const float* rope, const int32_t* positions, void* out,
                       int64_t ldo, int64_t rows, int64_t n_q_heads,

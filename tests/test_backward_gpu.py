@@ -266,3 +266,65 @@ def test_geglu_rows(K, cuda):
     out = K.geglu_rows(gu.to(cuda))
     g, u = gu[:, :n].double(), gu[:, n:].double()
     assert rel_err(out, F.gelu(g, approximate='tanh') * u) <= BF16_TOL
+
+
+@pytest.mark.parametrize('n,S', [(1, 816), (2, 816), (1, 100)])
+def test_attention_backward_fused(K, cuda, n, S):
+    """The fused decode-shape attention backward (and the suffix keys'
+    gradients from its ds_t / p_t) against float64 autograd of the masked
+    attention: rows = 51 tokens x 8 heads, S prefix keys (some padded) plus
+    the block-causal suffix; dq summed from the key-tile partials."""
+    announce(f'attention_backward fused n={n} S={S}')
+    Ss, H, D = 51, 8, 256
+    nk, R = S + Ss, Ss * H
+    T = (nk + 7) // 8 * 8
+    scale = D ** -0.5
+    q = randn((n, R, D), 101)
+    k = randn((n, T, D), 102)
+    v = randn((n, T, D), 103)
+    dout = randn((n, R, D), 104)
+    kgrp = torch.zeros(n, nk, dtype=torch.int32)
+    kgrp[:, S - 30:S] = 2**31 - 1
+    if n > 1:
+        kgrp[1, :20] = 2**31 - 1
+    suf = torch.cumsum(torch.tensor([1, 1] + [0] * (Ss - 2)), 0).int()
+    kgrp[:, S:] = suf
+    qgrp = suf[None].expand(n, Ss).contiguous()
+    tok = torch.arange(R) // H
+    vis = kgrp[:, None, :].long() <= qgrp[:, tok][:, :, None].long()  # [n, R, nk]
+    qd = q.double().requires_grad_(True)
+    kd = k[:, :nk].double().requires_grad_(True)
+    vd = v[:, :nk].double().requires_grad_(True)
+    logits = (qd @ kd.transpose(1, 2) * scale).masked_fill(~vis, float('-inf'))
+    p = torch.softmax(logits, -1)
+    o = p @ vd
+    dq_ref, dk_ref, dv_ref = torch.autograd.grad(o, (qd, kd, vd), dout.double())
+    kt = torch.zeros(n, D, T, dtype=torch.bfloat16)
+    kt[:, :, :nk] = k[:, :nk].transpose(1, 2)
+    parts = K.attention_backward_parts(nk)
+    dq = torch.full((parts, n * R, D), float('nan'), device=cuda)
+    stats = torch.empty(2 * n * parts * R, device=cuda)
+    ds_t = torch.zeros(n, Ss, R, dtype=torch.bfloat16, device=cuda)
+    p_t = torch.zeros(n, Ss, R, dtype=torch.bfloat16, device=cuda)
+    kc = k.to(cuda)
+    vc = v.to(cuda)
+    K.attention_backward(q.to(cuda), o.detach().to(torch.bfloat16).to(cuda),
+                         dout.to(cuda), kc[:, :nk], vc[:, :nk], kt.to(cuda), dq,
+                         stats, heads=H, scale=scale, kgrp=kgrp.to(cuda),
+                         qgrp=qgrp.to(cuda), ds_t=ds_t, p_t=p_t, key0=S,
+                         n_suffix=Ss)
+    got = dq.sum(0).view(n, R, D)
+    assert torch.isfinite(got).all()
+    assert rel_err(got, dq_ref) <= 2e-2
+    # P and dS of the suffix keys
+    ds_ref = p.detach() * (dout.double() @ vd.detach().transpose(1, 2)
+                           - (o.detach() * dout.double()).sum(-1, keepdim=True)) * scale
+    assert rel_err(p_t.transpose(1, 2), p.detach()[:, :, S:]) <= BF16_TOL
+    assert rel_err(ds_t.transpose(1, 2), ds_ref[:, :, S:]) <= 2e-2
+    for z in range(n):
+        dk = torch.empty(Ss, D, device=cuda)
+        dv = torch.empty(Ss, D, device=cuda)
+        K.attention_suffix_kv_backward(ds_t[z], p_t[z], q[z].to(cuda),
+                                       dout[z].to(cuda), dk, dv)
+        assert rel_err(dk, dk_ref[z, S:]) <= 2e-2
+        assert rel_err(dv, dv_ref[z, S:]) <= 2e-2

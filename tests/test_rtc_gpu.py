@@ -267,13 +267,15 @@ def test_guidance_vjp_rtc_chunk(models, cuda, pi05, batch):
     plain = _run(m, inp, cuda, prev, 6, dict(rc, use_vjp=False))
     err = (got - ref).abs().max().item()
     moved, moved_got = ref - plain_ref, got - plain
-    d_err = rel_err(moved_got, moved)
+    d_err = (moved_got - moved).abs().max().item()
     print(f'chunk max abs err {err:.3e}; the VJP term moves the chunk by '
           f'{moved.abs().max().item():.3e} (oracle), its move is off by '
-          f'{d_err:.3e} relative')
+          f'{d_err:.3e}')
     assert err <= CHUNK_ATOL
-    # the VJP term's own effect (with minus without it) matches the oracle's
-    assert d_err <= 0.2
+    # the VJP term's own effect (with minus without it) matches the
+    # oracle's; dropping it would miss by the whole move (> 3e-2 here)
+    assert moved.abs().max().item() > 3 * 0.5 * CHUNK_ATOL
+    assert d_err <= 0.5 * CHUNK_ATOL
     # eager run of the same loop gives the graph's chunk
     m.use_graph = False
     try:
