@@ -474,8 +474,15 @@ PROFILE_PASSES = (
     ('ptab_kt', 'kt', '--kernel-trace --stats', '--table-only'),
     ('ptab_fetch', 'fetch', '--pmc FETCH_SIZE', '--table-only'),
     ('ptab_write', 'write', '--pmc WRITE_SIZE', '--table-only'),
+    ('pvjp', 'vjp', '--kernel-trace --stats', '--vjp-only'),
     ('pbench', 'bench', '--kernel-trace --stats', ''),
 )
+
+
+def _profile_command(name):
+    """profile_commands()'s line of the pass writing into ``name``."""
+    names = [d for d, _, _, _ in PROFILE_PASSES]
+    return profile_commands()[names.index(name)]
 
 
 def profile_commands(out='$R/gpurun_out'):
@@ -489,13 +496,20 @@ def profile_commands(out='$R/gpurun_out'):
     return cmds
 
 
+def _kernel_name(full):
+    """A kernel's name without its argument list (and without the
+    '(anonymous namespace)::' scope, whose parenthesis is not one)."""
+    return (full.replace('void ', '').replace('(anonymous namespace)::', '')
+            .split('(')[0])
+
+
 def _trace(path):
     """Kernel-trace CSV rows in start order with name, workgroups, us."""
     import csv
     rows = sorted(csv.DictReader(open(path)),
                   key=lambda r: int(r['Start_Timestamp']))
     for r in rows:
-        r['name'] = r['Kernel_Name'].replace('void ', '').split('(')[0]
+        r['name'] = _kernel_name(r['Kernel_Name'])
         wg = 1
         for ax in 'XYZ':
             wg *= max(1, int(r.get(f'Grid_Size_{ax}', 1)) //
@@ -509,7 +523,7 @@ def _counters(path):
     """Counter-collection CSV rows in dispatch order: (name, wgs, KiB)."""
     import csv
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r['Dispatch_Id']))
-    return [(r['Kernel_Name'].replace('void ', '').split('(')[0],
+    return [(_kernel_name(r['Kernel_Name']),
              int(r['Grid_Size']) // max(1, int(r['Workgroup_Size'])),
              float(r['Counter_Value'])) for r in rows]
 
@@ -700,7 +714,7 @@ Command (repo root `R` on the MI355X box, `export TMPDIR=/tmp`; the default
 bench run itself; this file is `python3 bench.py --summarize-profiles
 gpurun_out` over its CSV):
 
-    {profile_commands()[-1]}
+    {_profile_command('pbench')}
 
 The last whole chunk of bench.py's timed loop (graph replay; from its
 im2col to its last Euler GEMM).  The same run printed value =
@@ -734,7 +748,7 @@ M=816, N=16384 x 2, K=2048, {mf.get('flops_per_launch')} flops per launch).
 Command (repo root `R` on the MI355X box, `export TMPDIR=/tmp`; the default
 bench run; this file is `python3 bench.py --summarize-profiles gpurun_out`):
 
-    {profile_commands()[-1]}
+    {_profile_command('pbench')}
 
 Runs of back-to-back dispatches in start order (durations End - Start;
 span/launch = first start to last end over the run, which keeps the kernel
@@ -753,6 +767,88 @@ TFLOP/s, frac {mf.get('frac')}; hipBLASLt on the same flops
 
 {geg}
 """)
+
+
+def summarize_vjp_profile(gdir, outdir):
+    """profiles/pi0_bs1_vjp_chunk_kernel_stats.md from the --vjp-only pass:
+    the kernels of its last whole guidance-with-VJP chunk."""
+    path = f'{gdir}/pvjp/vjp_kernel_trace.csv'
+    if not os.path.exists(path):
+        return
+    rows = _trace(path)
+    js = _json_line(f'{gdir}/pvjp.log') or {}
+    starts = [i for i, r in enumerate(rows) if 'im2col_kernel' in r['name']]
+    s0 = starts[-1]
+    ends = [i for i in range(s0, len(rows)) if 'rtc_vjp_update' in rows[i]['name']]
+    chunk = rows[s0:ends[-1] + 1]
+    agg = {}
+    for r in chunk:
+        a = agg.setdefault(r['name'], [0, 0.0])
+        a[0] += 1
+        a[1] += r['us']
+    tot = sum(a[1] for a in agg.values())
+    span = (int(chunk[-1]['End_Timestamp']) -
+            int(chunk[0]['Start_Timestamp'])) / 1e6
+    table = '\n'.join(f'| `{n}` | {c} | {d / 1e3:.3f} | {d / c:.2f} |'
+                      for n, (c, d) in sorted(agg.items(), key=lambda kv: -kv[1][1]))
+    with open(f'{outdir}/pi0_bs1_vjp_chunk_kernel_stats.md', 'w') as fh:
+        fh.write(f"""# PI0 bs=1 chunk with guidance RTC and use_vjp -- rocprofv3 kernel statistics
+
+Command (repo root `R` on the MI355X box, `export TMPDIR=/tmp`; this file
+is `python3 bench.py --summarize-profiles gpurun_out` over its CSV):
+
+    {_profile_command('pvjp')}
+
+`bench.py --vjp-only` builds the PI0 bs=1 model, then runs chunks with
+guidance real-time chunking and use_vjp (a previous chunk of 30 rows,
+prefix 5; each Euler step a forward with saved activations and a backward
+through the expert) through their captured graph.  The last whole chunk
+(from its im2col to its last guidance update).  The same run printed
+{js.get('ms_per_chunk')} ms per chunk (wall clock over its timed chunks,
+no profiler in the way).
+
+One chunk: {len(chunk)} dispatches, {tot / 1e3:.3f} ms of kernel time over a
+{span:.3f} ms span.
+
+| kernel | calls | ms | avg us |
+|---|---:|---:|---:|
+{table}
+""")
+
+
+def vjp_only(steps=5):
+    """Guidance-with-VJP chunks alone (PI0 bs=1): the program of the
+    rocprofv3 pass behind the VJP kernel statistics."""
+    import torch
+
+    from fluxvla_amd.config import PI0
+    from fluxvla_amd.pi0_inference import PI0Inference
+    from fluxvla_amd.weights import make_inputs, make_state_dict
+    dev = torch.device('cuda', 0)
+    sd = make_state_dict(PI0, seed=0, device=dev)
+    model = PI0Inference(PI0, sd, device=dev, max_batch=1)
+    dinp = {k: v.to(dev) for k, v in make_inputs(PI0, batch=1, seed=1).items()}
+    g = torch.Generator().manual_seed(5)
+    prev = (torch.randn(1, 30, 32, generator=g) * 0.5).to(dev)
+    rc = {'enabled': True, 'method': 'guidance', 'use_vjp': True,
+          'max_guidance_weight': 5.0}
+
+    def step():
+        return model.predict_action(dinp['images'], dinp['lang_tokens'],
+                                    dinp['states'], dinp['img_masks'],
+                                    dinp['lang_masks'], noise=dinp['noise'],
+                                    prev_actions=prev, prefix_len=5,
+                                    rtc_config=rc)
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    log(f'vjp-only: {ms:.3f} ms per chunk')
+    print(json.dumps({'ms_per_chunk': round(ms, 3)}), flush=True)
 
 
 def cpu_model_name():
@@ -1076,6 +1172,9 @@ def main():
                     help='run only the per-kernel table (every main kernel '
                     'of the chunk at its chunk shape) + a calibration copy '
                     '(for rocprofv3 --kernel-trace / --pmc passes)')
+    ap.add_argument('--vjp-only', action='store_true',
+                    help='run guidance-with-VJP chunks alone (the rocprofv3 '
+                    'pass of the VJP kernel statistics)')
     ap.add_argument('--summarize-profiles', metavar='DIR',
                     help='write the profiles/*.md summaries into DIR/profiles '
                     'from the CSVs of the rocprofv3 passes under DIR (see '
@@ -1084,6 +1183,7 @@ def main():
     if args.summarize_profiles:
         d = args.summarize_profiles
         summarize_profiles(d, os.path.join(d, 'profiles'))
+        summarize_vjp_profile(d, os.path.join(d, 'profiles'))
         return
     if args.gpus != 1:
         print('bench.py: this build runs on one GPU; multi-GPU figures are '
@@ -1096,6 +1196,9 @@ def main():
         return
     if args.table_only:
         table_only()
+        return
+    if args.vjp_only:
+        vjp_only()
         return
 
     import torch
