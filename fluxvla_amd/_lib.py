@@ -178,11 +178,12 @@ SIGNATURES = {
     # backward ops of guidance RTC with use_vjp
     'fvx_rms_norm_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
                                       c_vp, c_vp, c_vp, c_i64, c_vp, c_i64,
-                                      c_i64, c_i64, c_i64, c_i64, c_f32,
+                                      c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
                                       c_vp]),
     'fvx_act_backward': (c_i32, [c_i32, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
-                                 c_i64, c_i64, c_vp]),
-    'fvx_geglu_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp]),
+                                 c_vp, c_i64, c_i64, c_vp]),
+    'fvx_geglu_rows': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64,
+                               c_vp]),
     'fvx_attention_rows_backward': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp,
                                             c_vp, c_vp, c_i64, c_vp, c_vp,
                                             c_i64, c_i64, c_i64, c_i64, c_i64,
@@ -194,8 +195,8 @@ SIGNATURES = {
     'fvx_transpose_bf16': (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
                                    c_i64, c_i64, c_i64, c_vp]),
     'fvx_rope_backward': (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,
-                                  c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64,
-                                  c_i64, c_i64, c_vp]),
+                                  c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp,
+                                  c_i64, c_i64, c_i64, c_vp]),
     'fvx_attention_backward': (c_i32, [ctypes.POINTER(AttnBwdDesc), c_vp]),
     'fvx_attention_backward_parts': (c_i64, [c_i64]),
     'fvx_rtc_vjp_error': (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,

@@ -52,7 +52,8 @@ __device__ __forceinline__ int64_t grouped_row(int64_t m, int64_t g, int64_t gs)
 // One wavefront per row; vector v (8 columns) of the row is lane v % 64's
 // (v / 64)-th.  x, dres, out and out_b rows follow the row-group map
 // (m / g) * gs + m % g (identity for g = 0); dy rows are compact.
-// out_b = bf16(dx * gate): the A operand of the next backward GEMM.
+// out_b = bf16(dx * gate): the A operand of the next backward GEMM; out_f
+// the same values in the fragment-major A layout (row pr, M <= 64 GEMMs).
 // ---------------------------------------------------------------------------
 template <int NV>
 __global__ __launch_bounds__(256) void rms_backward_kernel(
@@ -60,8 +61,8 @@ __global__ __launch_bounds__(256) void rms_backward_kernel(
     int64_t ldy, const float* __restrict__ dres, int64_t ldr,
     const bf16_t* __restrict__ scale, const bf16_t* __restrict__ gate,
     float* __restrict__ out, int64_t ldo, bf16_t* __restrict__ out_b,
-    int64_t ldob, int64_t rows, int cols, int64_t grp, int64_t grp_stride,
-    float eps) {
+    int64_t ldob, bf16_t* __restrict__ out_f, int64_t rows, int cols,
+    int64_t grp, int64_t grp_stride, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * kBwdRows + (threadIdx.x >> 6);
   if (m >= rows) return;
@@ -109,16 +110,16 @@ __global__ __launch_bounds__(256) void rms_backward_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) d[e] = rd[e] + r * g[i][e] - c * xv[i][e];
     if (out) st_f8(out + pr * ldo + v * 8, d);
-    if (out_b) {
+    if (out_b || out_f) {
       if (gate) {
         float gf[8];
         unpack8(ld8(gate + v * 8), gf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) gf[e] *= d[e];
-        st8(out_b + pr * ldob + v * 8, pack8(gf));
-      } else {
-        st8(out_b + pr * ldob + v * 8, pack8(d));
+        for (int e = 0; e < 8; ++e) d[e] *= gf[e];
       }
+      const bf16x8 b = pack8(d);
+      if (out_b) st8(out_b + pr * ldob + v * 8, b);
+      if (out_f) st8(out_f + frag_offset(pr, v * 8), b);
     }
   }
 }
@@ -139,7 +140,8 @@ constexpr int kActGeglu = 0, kActSilu = 1, kGegluFwd = 2;
 template <int ACT>
 __global__ __launch_bounds__(256) void act_backward_kernel(
     const bf16_t* __restrict__ in, int64_t ldi, const bf16_t* __restrict__ dy,
-    int64_t ldy, bf16_t* __restrict__ out, int64_t ldo, int64_t rows, int cols) {
+    int64_t ldy, bf16_t* __restrict__ out, int64_t ldo, bf16_t* __restrict__ out_f,
+    int64_t rows, int cols) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int nv = cols >> 3;
   if (t >= rows * nv) return;
@@ -152,7 +154,9 @@ __global__ __launch_bounds__(256) void act_backward_kernel(
     unpack8(ld8(in + m * ldi + cols + c), d);
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = gelu_tanh(a[e]) * d[e];
-    st8(out + m * ldo + c, pack8(o));
+    const bf16x8 b = pack8(o);
+    if (out) st8(out + m * ldo + c, b);
+    if (out_f) st8(out_f + frag_offset(m, c), b);
     return;
   }
   unpack8(ld8(dy + m * ldy + c), d);
@@ -169,8 +173,15 @@ __global__ __launch_bounds__(256) void act_backward_kernel(
       o[e] = d[e] * u[e] * dg;
       o2[e] = d[e] * (x * s);
     }
-    st8(out + m * ldo + c, pack8(o));
-    st8(out + m * ldo + cols + c, pack8(o2));
+    const bf16x8 b = pack8(o), b2 = pack8(o2);
+    if (out) {
+      st8(out + m * ldo + c, b);
+      st8(out + m * ldo + cols + c, b2);
+    }
+    if (out_f) {
+      st8(out_f + frag_offset(m, c), b);
+      st8(out_f + frag_offset(m, cols + c), b2);
+    }
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -178,7 +189,9 @@ __global__ __launch_bounds__(256) void act_backward_kernel(
       const float sg = 1.f / (1.f + expf(-z));
       o[e] = d[e] * sg * (1.f + z * (1.f - sg));
     }
-    st8(out + m * ldo + c, pack8(o));
+    const bf16x8 b = pack8(o);
+    if (out) st8(out + m * ldo + c, b);
+    if (out_f) st8(out_f + frag_offset(m, c), b);
   }
 }
 
@@ -702,8 +715,8 @@ __global__ __launch_bounds__(256) void rope_backward_kernel(
     const float* __restrict__ dk,
     int64_t ldk, const float* __restrict__ dv, int64_t ldv,
     const float* __restrict__ rope, const int32_t* __restrict__ positions,
-    bf16_t* __restrict__ out, int64_t ldo, int64_t rows, int n_q_heads,
-    int head_dim) {
+    bf16_t* __restrict__ out, int64_t ldo, bf16_t* __restrict__ out_f, int64_t rows,
+    int n_q_heads, int head_dim) {
   const int half = head_dim >> 1;
   const int pairs = (n_q_heads + 2) * half;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -739,7 +752,9 @@ __global__ __launch_bounds__(256) void rope_backward_kernel(
     a = ga;
     b = gb;
   }
-  *reinterpret_cast<uint32_t*>(out + m * ldo + 2 * p) = f2bf2(a, b);
+  const uint32_t v = f2bf2(a, b);
+  if (out) *reinterpret_cast<uint32_t*>(out + m * ldo + 2 * p) = v;
+  if (out_f) *reinterpret_cast<uint32_t*>(out_f + frag_offset(m, 2 * p)) = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -794,16 +809,30 @@ inline bool al16(const void* p) { return aligned16(p); }
 
 using namespace fvx;
 
+// A fragment-major output holds rows < 64 and 32-column steps.
+static bool frag_fits(int64_t last_row, int64_t cols) {
+  return last_row < 64 && cols % 32 == 0 && cols < (1 << 24);
+}
+
 extern "C" int fvx_rms_norm_backward(const void* x, int64_t ldx, const float* dy,
                                      int64_t ldy, const float* dres, int64_t ldr,
                                      const void* scale, const void* gate, float* out,
                                      int64_t ldo, void* out_bf16, int64_t ldob,
-                                     int64_t rows, int64_t cols, int64_t row_group,
-                                     int64_t row_group_stride, float eps,
-                                     void* stream) {
+                                     void* out_frag, int64_t rows, int64_t cols,
+                                     int64_t row_group, int64_t row_group_stride,
+                                     float eps, void* stream) {
   clear_error();
-  FVX_REQUIRE(x && dy && (out || out_bf16), FVX_ERR_NULL,
+  FVX_REQUIRE(x && dy && (out || out_bf16 || out_frag), FVX_ERR_NULL,
               "rms_norm_backward: x, dy and an output are required");
+  {
+    const int64_t last = rows <= 0 ? 0
+                         : row_group > 0
+                             ? ((rows - 1) / row_group) * row_group_stride + (rows - 1) % row_group
+                             : rows - 1;
+    FVX_REQUIRE(!out_frag || (frag_fits(last, cols) && al16(out_frag)), FVX_ERR_ARG,
+                "rms_norm_backward: out_frag needs mapped rows < 64, cols %% 32 == 0 and a "
+                "16-byte aligned buffer");
+  }
   FVX_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 4096, FVX_ERR_SHAPE,
               "rms_norm_backward: cols must be a positive multiple of 8 <= 4096");
   FVX_REQUIRE(ldx >= cols && ldy >= cols && ldx % 8 == 0 && ldy % 8 == 0 &&
@@ -824,8 +853,8 @@ extern "C" int fvx_rms_norm_backward(const void* x, int64_t ldx, const float* dy
 #define L(NV)                                                                          \
   hipLaunchKernelGGL(rms_backward_kernel<NV>, grid, dim3(256), 0, s, (const bf16_t*)x, \
                      ldx, dy, ldy, dres, ldr, (const bf16_t*)scale,                    \
-                     (const bf16_t*)gate, out, ldo, (bf16_t*)out_bf16, ldob, rows,     \
-                     (int)cols, row_group, row_group_stride, eps)
+                     (const bf16_t*)gate, out, ldo, (bf16_t*)out_bf16, ldob,           \
+                     (bf16_t*)out_frag, rows, (int)cols, row_group, row_group_stride, eps)
   switch (nv) {
     case 1: L(1); break;
     case 2: L(2); break;
@@ -841,17 +870,22 @@ extern "C" int fvx_rms_norm_backward(const void* x, int64_t ldx, const float* dy
 }
 
 extern "C" int fvx_act_backward(int act, const void* in, int64_t ldi, const void* dy,
-                                int64_t ldy, void* out, int64_t ldo, int64_t rows,
-                                int64_t cols, void* stream) {
+                                int64_t ldy, void* out, int64_t ldo, void* out_frag,
+                                int64_t rows, int64_t cols, void* stream) {
   clear_error();
-  FVX_REQUIRE(in && dy && out, FVX_ERR_NULL, "act_backward: in, dy, out are required");
+  FVX_REQUIRE(in && dy && (out || out_frag), FVX_ERR_NULL,
+              "act_backward: in, dy and an output are required");
+  FVX_REQUIRE(!out_frag || (frag_fits(rows - 1, act == FVX_ACT_BWD_GEGLU ? 2 * cols : cols) &&
+                            al16(out_frag)),
+              FVX_ERR_ARG, "act_backward: out_frag needs rows <= 64, 32-column steps and a "
+                           "16-byte aligned buffer");
   FVX_REQUIRE(act == FVX_ACT_BWD_GEGLU || act == FVX_ACT_BWD_SILU, FVX_ERR_ARG,
               "act_backward: bad act %d", act);
   const int64_t w = act == FVX_ACT_BWD_GEGLU ? 2 * cols : cols;
   FVX_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols < (1 << 30), FVX_ERR_SHAPE,
               "act_backward: cols must be a positive multiple of 8");
-  FVX_REQUIRE(ldi >= w && ldo >= w && ldy >= cols && ldi % 8 == 0 && ldo % 8 == 0 &&
-                  ldy % 8 == 0,
+  FVX_REQUIRE(ldi >= w && (!out || ldo >= w) && ldy >= cols && ldi % 8 == 0 &&
+                  ldo % 8 == 0 && ldy % 8 == 0,
               FVX_ERR_SHAPE, "act_backward: leading dims too small or not multiples of 8");
   FVX_REQUIRE(al16(in) && al16(dy) && al16(out), FVX_ERR_ALIGN,
               "act_backward: pointers must be 16-byte aligned");
@@ -861,27 +895,31 @@ extern "C" int fvx_act_backward(int act, const void* in, int64_t ldi, const void
   if (act == FVX_ACT_BWD_GEGLU)
     hipLaunchKernelGGL(act_backward_kernel<kActGeglu>, grid, dim3(256), 0, s,
                        (const bf16_t*)in, ldi, (const bf16_t*)dy, ldy, (bf16_t*)out, ldo,
-                       rows, (int)cols);
+                       (bf16_t*)out_frag, rows, (int)cols);
   else
     hipLaunchKernelGGL(act_backward_kernel<kActSilu>, grid, dim3(256), 0, s,
                        (const bf16_t*)in, ldi, (const bf16_t*)dy, ldy, (bf16_t*)out, ldo,
-                       rows, (int)cols);
+                       (bf16_t*)out_frag, rows, (int)cols);
   return launch_status("act_backward");
 }
 
 extern "C" int fvx_geglu_rows(const void* gu, int64_t ldgu, void* out, int64_t ldo,
-                              int64_t rows, int64_t cols, void* stream) {
+                              void* out_frag, int64_t rows, int64_t cols, void* stream) {
   clear_error();
-  FVX_REQUIRE(gu && out, FVX_ERR_NULL, "geglu_rows: gu and out are required");
+  FVX_REQUIRE(gu && (out || out_frag), FVX_ERR_NULL,
+              "geglu_rows: gu and an output are required");
   FVX_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols < (1 << 30) &&
-                  ldgu >= 2 * cols && ldo >= cols && ldgu % 8 == 0 && ldo % 8 == 0,
+                  ldgu >= 2 * cols && (!out || ldo >= cols) && ldgu % 8 == 0 && ldo % 8 == 0,
               FVX_ERR_SHAPE, "geglu_rows: bad sizes");
-  FVX_REQUIRE(al16(gu) && al16(out), FVX_ERR_ALIGN,
+  FVX_REQUIRE(al16(gu) && al16(out) && al16(out_frag), FVX_ERR_ALIGN,
               "geglu_rows: pointers must be 16-byte aligned");
+  FVX_REQUIRE(!out_frag || frag_fits(rows - 1, cols), FVX_ERR_ARG,
+              "geglu_rows: out_frag needs rows <= 64 and cols %% 32 == 0");
   if (rows == 0) return FVX_OK;
   hipLaunchKernelGGL(act_backward_kernel<kGegluFwd>, dim3(blocks(rows * (cols / 8), 256)),
                      dim3(256), 0, (hipStream_t)stream, (const bf16_t*)gu, ldgu,
-                     (const bf16_t*)gu, ldgu, (bf16_t*)out, ldo, rows, (int)cols);
+                     (const bf16_t*)gu, ldgu, (bf16_t*)out, ldo, (bf16_t*)out_frag, rows,
+                     (int)cols);
   return launch_status("geglu_rows");
 }
 
@@ -964,17 +1002,20 @@ extern "C" int fvx_rope_backward(const float* dq, int64_t ldq, int64_t dq_parts,
                                  int64_t dq_part_stride, const float* dk, int64_t ldk,
                                  const float* dv, int64_t ldv, const float* rope,
                                  const int32_t* positions, void* out, int64_t ldo,
-                                 int64_t rows, int64_t n_q_heads, int64_t head_dim,
-                                 void* stream) {
+                                 void* out_frag, int64_t rows, int64_t n_q_heads,
+                                 int64_t head_dim, void* stream) {
   clear_error();
+  FVX_REQUIRE(!out_frag || (frag_fits(rows - 1, (n_q_heads + 2) * head_dim) &&
+                            ((uintptr_t)out_frag & 3) == 0),
+              FVX_ERR_ARG, "rope_backward: out_frag needs rows <= 64 and 32-column steps");
   FVX_REQUIRE(dq_parts >= 1 && dq_parts < 4096 && (dq_parts == 1 || dq_part_stride % 2 == 0),
               FVX_ERR_ARG, "rope_backward: bad dq parts");
-  FVX_REQUIRE(dq && dk && dv && rope && positions && out, FVX_ERR_NULL,
-              "rope_backward: every operand is required");
+  FVX_REQUIRE(dq && dk && dv && rope && positions && (out || out_frag), FVX_ERR_NULL,
+              "rope_backward: every operand and an output are required");
   FVX_REQUIRE(rows >= 0 && n_q_heads > 0 && head_dim > 0 && head_dim % 2 == 0 &&
                   ldq >= n_q_heads * head_dim && ldk >= head_dim && ldv >= head_dim &&
                   ldq % 2 == 0 && ldk % 2 == 0 && ldv % 2 == 0 && ldo % 2 == 0 &&
-                  ldo >= (n_q_heads + 2) * head_dim,
+                  (!out || ldo >= (n_q_heads + 2) * head_dim),
               FVX_ERR_SHAPE, "rope_backward: bad sizes");
   FVX_REQUIRE(((uintptr_t)out & 3) == 0 && ((uintptr_t)dq & 7) == 0 &&
                   ((uintptr_t)dk & 7) == 0 && ((uintptr_t)dv & 7) == 0,
@@ -983,8 +1024,8 @@ extern "C" int fvx_rope_backward(const float* dq, int64_t ldq, int64_t dq_parts,
   const int64_t pairs = (n_q_heads + 2) * head_dim / 2;
   hipLaunchKernelGGL(rope_backward_kernel, dim3(blocks(rows * pairs, 256)), dim3(256), 0,
                      (hipStream_t)stream, dq, ldq, (int)dq_parts, dq_part_stride, dk, ldk,
-                     dv, ldv, rope, positions, (bf16_t*)out, ldo, rows, (int)n_q_heads,
-                     (int)head_dim);
+                     dv, ldv, rope, positions, (bf16_t*)out, ldo, (bf16_t*)out_frag, rows,
+                     (int)n_q_heads, (int)head_dim);
   return launch_status("rope_backward");
 }
 

@@ -885,17 +885,19 @@ def _mapped_rows(t, name, rows, row_group, row_group_stride):
     return t.stride(0)
 
 
-def rms_norm_backward(x, dy, *, out=None, out_bf16=None, dres=None,
-                      scale=None, gate=None, eps=1e-6, row_group=0,
+def rms_norm_backward(x, dy, *, out=None, out_bf16=None, out_frag=None,
+                      dres=None, scale=None, gate=None, eps=1e-6, row_group=0,
                       row_group_stride=0):
     """dx of y = x r (1 + scale) (fvx_rms_norm_backward): dy fp32 [rows,
     cols] (compact); x bf16, dres / out fp32 and out_bf16 (= bf16(dx *
     gate)) 2-D views whose row m is (m / row_group) * row_group_stride +
-    m % row_group.  scale / gate: bf16 [cols] or None."""
+    m % row_group; out_frag: a FragA receiving out_bf16's values.
+    scale / gate: bf16 [cols] or None."""
     _check(dy, 'dy', dtype=torch.float32, contiguous=False)
     rows, ldy = _rows_ld(dy, 'dy')
     cols = dy.shape[-1]
-    if out is None and out_bf16 is None:
+    frag = _frag_out(out_frag, cols)
+    if out is None and out_bf16 is None and frag is None:
         out = torch.empty(rows, cols, dtype=torch.float32, device=dy.device)
     _check(x, 'x', contiguous=False)
     ldx = _mapped_rows(x, 'x', rows, row_group, row_group_stride)
@@ -917,15 +919,25 @@ def rms_norm_backward(x, dy, *, out=None, out_bf16=None, dres=None,
         raise ValueError(f'x must have {cols} columns')
     _lib.call('fvx_rms_norm_backward', _ptr(x), ldx, _ptr(dy), ldy,
               _ptr(dres), args[0], _ptr(scale), _ptr(gate), _ptr(out),
-              args[1], _ptr(out_bf16), args[2], rows, cols, row_group,
+              args[1], _ptr(out_bf16), args[2], frag, rows, cols, row_group,
               row_group_stride, float(eps), _stream())
     return out if out is not None else out_bf16
 
 
-def act_backward(act, inp, dy, out=None):
+def _frag_out(f, width):
+    """The buffer pointer of a FragA output of ``width`` columns, or None."""
+    if f is None:
+        return None
+    if not isinstance(f, FragA) or f.k != width:
+        raise ValueError(f'out_frag must be a FragA with k == {width}')
+    _check(f.buf, 'out_frag')
+    return f.buf.data_ptr()
+
+
+def act_backward(act, inp, dy, out=None, out_frag=None):
     """GeGLU (act=ACT_BWD_GEGLU, inp = [gate | up] [rows, 2 cols]) or SiLU
     (inp = z [rows, cols]) backward; dy bf16 [rows, cols]; out bf16 like
-    inp (fvx_act_backward)."""
+    inp and / or out_frag, a FragA of the same width (fvx_act_backward)."""
     _check(inp, 'inp', contiguous=False)
     _check(dy, 'dy', contiguous=False)
     rows, ldy = _rows_ld(dy, 'dy')
@@ -933,26 +945,33 @@ def act_backward(act, inp, dy, out=None):
     width = 2 * cols if act == _lib.ACT_BWD_GEGLU else cols
     if inp.shape[-1] != width:
         raise ValueError(f'inp must have {width} columns')
-    if out is None:
+    frag = _frag_out(out_frag, width)
+    if out is None and frag is None:
         out = torch.empty(rows, width, dtype=BF16, device=dy.device)
-    _check(out, 'out', contiguous=False)
+    ldo = 0
+    if out is not None:
+        _check(out, 'out', contiguous=False)
+        _, ldo = _rows_ld(out, 'out')
     _, ldi = _rows_ld(inp, 'inp')
-    _, ldo = _rows_ld(out, 'out')
     _lib.call('fvx_act_backward', int(act), _ptr(inp), ldi, _ptr(dy), ldy,
-              _ptr(out), ldo, rows, cols, _stream())
+              _ptr(out), ldo, frag, rows, cols, _stream())
     return out
 
 
-def geglu_rows(gu, out=None):
-    """out = gelu_tanh(gu[:, :n]) * gu[:, n:] (bf16; fvx_geglu_rows)."""
+def geglu_rows(gu, out=None, out_frag=None):
+    """out = gelu_tanh(gu[:, :n]) * gu[:, n:] (bf16; fvx_geglu_rows), and /
+    or the same into out_frag (a FragA with k == n)."""
     _check(gu, 'gu', contiguous=False)
     rows, ldgu = _rows_ld(gu, 'gu')
     n = gu.shape[-1] // 2
-    if out is None:
+    frag = _frag_out(out_frag, n)
+    if out is None and frag is None:
         out = torch.empty(rows, n, dtype=BF16, device=gu.device)
-    _check(out, 'out', contiguous=False)
-    _, ldo = _rows_ld(out, 'out')
-    _lib.call('fvx_geglu_rows', _ptr(gu), ldgu, _ptr(out), ldo, rows, n,
+    ldo = 0
+    if out is not None:
+        _check(out, 'out', contiguous=False)
+        _, ldo = _rows_ld(out, 'out')
+    _lib.call('fvx_geglu_rows', _ptr(gu), ldgu, _ptr(out), ldo, frag, rows, n,
               _stream())
     return out
 
@@ -1033,14 +1052,17 @@ def transpose(src, dst):
     return dst
 
 
-def rope_backward(dq, dk, dv, rope, positions, out, n_q_heads, head_dim):
+def rope_backward(dq, dk, dv, rope, positions, out, n_q_heads, head_dim,
+                  out_frag=None):
     """out bf16 [rows, (n_q_heads + 2) * head_dim] = [dq, dk rotated back |
     dv] (fvx_rope_backward); dk / dv fp32 2-D views, dq one too or a 3-D
     [parts, rows, cols] stack of partials (summed)."""
     for t, nm in ((dq, 'dq'), (dk, 'dk'), (dv, 'dv'), (rope, 'rope')):
         _check(t, nm, dtype=torch.float32, contiguous=(nm == 'rope'))
     _check(positions, 'positions', dtype=torch.int32)
-    _check(out, 'out', contiguous=False)
+    frag = _frag_out(out_frag, (n_q_heads + 2) * head_dim)
+    if out is not None:
+        _check(out, 'out', contiguous=False)
     parts, pstride = 1, 0
     if dq.dim() == 3:
         parts, pstride = dq.shape[0], dq.stride(0)
@@ -1050,7 +1072,8 @@ def rope_backward(dq, dk, dv, rope, positions, out, n_q_heads, head_dim):
         raise ValueError('dq, dk, dv and positions must cover the same rows')
     _lib.call('fvx_rope_backward', _ptr(dq), ldq, parts, pstride, _ptr(dk),
               dk.stride(0), _ptr(dv), dv.stride(0), _ptr(rope), _ptr(positions),
-              _ptr(out), out.stride(0), rows, n_q_heads, head_dim, _stream())
+              _ptr(out), out.stride(0) if out is not None else 0, frag, rows,
+              n_q_heads, head_dim, _stream())
     return out
 
 

@@ -133,6 +133,11 @@ class ExpertVJP:
             'dv': e(B * Ss, D, dt=torch.float32),
             'dqkv': e(B * Ss, (H + 2) * D),
         }
+        if self._frag(B):
+            # fragment-major copies of the M <= 64 GEMMs' A operands
+            F = lambda k: K.FragA.empty(k, dev).rows(B * Ss)  # noqa: E731
+            v['f'] = {'x': F(hid), 'x2': F(hid), 'ctx': F(H * D), 'h': F(mlp),
+                      'a': F(hid), 'dgu': F(2 * mlp), 'dqkv': F((H + 2) * D)}
         if not cfg.pi05:
             v['z'] = e(B * na, cfg.proj_width)
             v['dsh'] = e(B * na, cfg.proj_width)
@@ -169,6 +174,8 @@ class ExpertVJP:
         X, X2, Q = v['X'], v['X2'], v['Q']
         xt_b = b['xt_bf16'].view(B * na, -1)
         fr = self._frag(B)
+        f = v.get('f') if fr else None
+        fc = (lambda nm: f[nm] if f else None)  # noqa: E731
         if cfg.pi05:
             K.gemm(xt_b, m.act_in_f if fr else m.act_in['w'], out=X[0],
                    bias=m.act_in['b'])
@@ -179,7 +186,7 @@ class ExpertVJP:
                    act=_lib.ACT_SILU, row_group=na, row_group_stride=Ss)
             K.gemm(xt_b, w_mi, out=v['z'], bias_f32=m.step_bias[step])
             K.gemm(h, m.mlp_out_f if fr else m.mlp_out['w'], out=X[0],
-                   residual=b['suf_res'])
+                   residual=b['suf_res'], c_frag=fc('x'))
         st = m.styles[step] if cfg.pi05 else None
         layers = m.exp_f if fr else m.exp['layers']
         for i, L in enumerate(layers):
@@ -190,7 +197,7 @@ class ExpertVJP:
                               gate_out=v['gate'], eps=cfg.rms_eps)
                 a, rn = v['xn'], None
             else:
-                a, rn = x, cfg.rms_eps
+                a, rn = (f['x'] if f else x), cfg.rms_eps
             K.gemm_qkv_rope(a, L['qkv_w'], m.rope, b['pos_suf'], Q[i],
                             kc.view(B * T, D)[S:], vc[:, :, S:], H, D,
                             rownorm_eps=rn, row_group=Ss, row_group_stride=T,
@@ -198,9 +205,11 @@ class ExpertVJP:
             ctx = v['CTX'][i]
             K.mqa_attention(Q[i].view(B, Ss, H * D), kc[:, :S + Ss], vc,
                             ctx.view(B, Ss, H * D), kgrp=b['kgrp'],
-                            qgrp=b['qgrp_suf'], v_transposed=True)
+                            qgrp=b['qgrp_suf'], v_transposed=True,
+                            o_frag=fc('ctx'))
             gate = v['gate'] if cfg.pi05 else None
-            K.gemm(ctx, L['o_w'], out=X2[i], residual=x, gate=gate)
+            K.gemm(f['ctx'] if f else ctx, L['o_w'], out=X2[i], residual=x,
+                   gate=gate, c_frag=None if cfg.pi05 else fc('x2'))
             # [gate | up] kept for the backward, then the GeGLU product
             w_gu = self.gu_w_f[i] if fr else self.gu_w[i]
             if cfg.pi05:
@@ -208,10 +217,15 @@ class ExpertVJP:
                               gate_out=v['gate'], eps=cfg.rms_eps)
                 K.gemm(v['xn'], w_gu, out=v['GU'][i])
             else:
-                K.gemm(X2[i], w_gu, out=v['GU'][i], rownorm_eps=cfg.rms_eps)
-            K.geglu_rows(v['GU'][i], out=v['h'])
-            K.gemm(v['h'], L['down_w'], out=X[i + 1], residual=X2[i],
-                   gate=gate)
+                K.gemm(f['x2'] if f else X2[i], w_gu, out=v['GU'][i],
+                       rownorm_eps=cfg.rms_eps)
+            if f:
+                K.geglu_rows(v['GU'][i], out_frag=f['h'])
+            else:
+                K.geglu_rows(v['GU'][i], out=v['h'])
+            K.gemm(f['h'] if f else v['h'], L['down_w'], out=X[i + 1],
+                   residual=X2[i], gate=gate,
+                   c_frag=None if cfg.pi05 else fc('x'))
         lead = Ss - na
         last = X[-1].view(B, Ss, hid)
         w_out = m.act_out_f if fr else m.act_out['w']
@@ -245,6 +259,9 @@ class ExpertVJP:
         nL = len(m.exp['layers'])
         fr = self._frag(B)
         wts = self.wT_f if fr else self.wT
+        f = v.get('f') if fr else None
+        af = f['a'] if f else None
+        a_in = af if f else v['a']  # the A operand of the backward GEMMs
         dx, dx2 = v['dx']
         # d(final norm output) = e @ W_out, then the final norm's backward
         # onto the action rows (the state row of PI0 gets none)
@@ -253,36 +270,49 @@ class ExpertVJP:
                out_f32=True)
         if cfg.pi05:
             K.rms_norm_backward(X[-1], dxn, out=dx, out_bf16=v['a'],
-                                scale=st[-1, :w], gate=gate2(nL - 1), eps=eps)
+                                out_frag=af, scale=st[-1, :w],
+                                gate=gate2(nL - 1), eps=eps)
         else:
             dx.zero_()
             v['a'].zero_()
             K.rms_norm_backward(X[-1][lead:], dxn, out=dx[lead:],
                                 out_bf16=v['a'][lead:], eps=eps,
                                 row_group=na, row_group_stride=Ss)
+            if af is not None:  # all rows, the zero state rows included
+                K.pack_frag(v['a'], af)
         for i in range(nL - 1, -1, -1):
             wt = wts[i]
             # MLP: dh = (gate2 dX3) @ W_down, then GeGLU's backward on the
             # [gate | up] rows the forward kept
-            K.gemm(v['a'], wt['down'], out=v['dh'])
-            K.act_backward(_lib.ACT_BWD_GEGLU, v['GU'][i], v['dh'],
-                           out=v['dgu'])
-            K.gemm(v['dgu'], wt['gu'], out=v['da'], out_f32=True)
+            K.gemm(a_in, wt['down'], out=v['dh'])
+            if f:
+                K.act_backward(_lib.ACT_BWD_GEGLU, v['GU'][i], v['dh'],
+                               out_frag=f['dgu'])
+            else:
+                K.act_backward(_lib.ACT_BWD_GEGLU, v['GU'][i], v['dh'],
+                               out=v['dgu'])
+            K.gemm(f['dgu'] if f else v['dgu'], wt['gu'], out=v['da'],
+                   out_f32=True)
             K.rms_norm_backward(
-                X2[i], v['da'], dres=dx, out=dx2, out_bf16=v['a'],
+                X2[i], v['da'], dres=dx, out=dx2,
+                out_bf16=None if f else v['a'], out_frag=af,
                 scale=st[2 * i + 1, :w] if cfg.pi05 else None,
                 gate=st[2 * i, 2 * w:] if cfg.pi05 else None, eps=eps)
             # attention: dO = (gate1 dX2) @ W_o
-            K.gemm(v['a'], wt['o'], out=v['dctx'].view(B * Ss, -1))
+            K.gemm(a_in, wt['o'], out=v['dctx'].view(B * Ss, -1))
             self._attention_backward(b, B, i)
-            K.gemm(v['dqkv'], wt['qkv'], out=v['da'], out_f32=True)
+            K.gemm(f['dqkv'] if f else v['dqkv'], wt['qkv'], out=v['da'],
+                   out_f32=True)
+            # the last one (layer 0) also row-major: the suffix embedding's
+            # backward reads the action rows
             K.rms_norm_backward(
-                X[i], v['da'], dres=dx2, out=dx, out_bf16=v['a'],
+                X[i], v['da'], dres=dx2, out=dx,
+                out_bf16=v['a'] if (i == 0 or not f) else None, out_frag=af,
                 scale=st[2 * i, :w] if cfg.pi05 else None, gate=gate2(i - 1),
                 eps=eps)
         # suffix embedding: g = dL/dx_t
         if cfg.pi05:
-            K.gemm(v['a'], self.in_t_f if fr else self.in_t, out=v['g'],
+            K.gemm(a_in, self.in_t_f if fr else self.in_t, out=v['g'],
                    out_f32=True)
         else:
             a = v['a'].view(B, Ss, hid)[:, lead:]
@@ -318,5 +348,7 @@ class ExpertVJP:
             rows = slice(z * Ss, (z + 1) * Ss)
             K.attention_suffix_kv_backward(v['ds_t'][z], v['p_t'][z], q3[z],
                                            do3[z], v['dk'][rows], v['dv'][rows])
+        f = v.get('f') if self._frag(B) else None
         K.rope_backward(v['dq'].view(-1, B * Ss, H * D), v['dk'], v['dv'],
-                        m.rope, b['pos_suf'], v['dqkv'], H, D)
+                        m.rope, b['pos_suf'], None if f else v['dqkv'], H, D,
+                        out_frag=f['dqkv'] if f else None)

@@ -507,13 +507,17 @@ int fvx_resize_normalize(const fvx_image_desc* desc, void* stream);
  * (gate bf16 [cols] or NULL: 1).  Rows of x, dres, out and out_bf16 follow
  * the row-group map (m / row_group) * row_group_stride + m % row_group
  * (identity for row_group 0); dy rows are compact.  cols % 8 == 0,
- * cols <= 4096, leading dims multiples of 8, pointers 16-byte aligned. */
+ * cols <= 4096, leading dims multiples of 8, pointers 16-byte aligned.
+ * out_frag (may be NULL): out_bf16's values in the fragment-major A layout
+ * of fvx_gemm_desc.a_frag (mapped rows < 64, cols % 32 == 0), for the
+ * M <= 64 GEMM that reads them. */
 int fvx_rms_norm_backward(const void* x, int64_t ldx, const float* dy,
                           int64_t ldy, const float* dres, int64_t ldr,
                           const void* scale, const void* gate, float* out,
                           int64_t ldo, void* out_bf16, int64_t ldob,
-                          int64_t rows, int64_t cols, int64_t row_group,
-                          int64_t row_group_stride, float eps, void* stream);
+                          void* out_frag, int64_t rows, int64_t cols,
+                          int64_t row_group, int64_t row_group_stride,
+                          float eps, void* stream);
 
 /* Activation backward, bf16 in and out (GemmaMLP's GeGLU,
  * condition_gemma.py:156-192; the PI0 action-time MLP's SiLU,
@@ -521,12 +525,14 @@ int fvx_rms_norm_backward(const void* x, int64_t ldx, const float* dy,
  *   FVX_ACT_BWD_GEGLU: in = [gate | up] ([rows, 2 cols]), dy = dh ->
  *     out = [dh * up * gelu_tanh'(gate) | dh * gelu_tanh(gate)]
  *   FVX_ACT_BWD_SILU: in = z ([rows, cols]) -> out = dy * silu'(z)
- * cols % 8 == 0, leading dims multiples of 8, pointers 16-byte aligned. */
+ * cols % 8 == 0, leading dims multiples of 8, pointers 16-byte aligned.
+ * out and out_frag (the fragment-major A layout, rows <= 64, widths % 32
+ * == 0) may each be NULL, not both. */
 #define FVX_ACT_BWD_GEGLU 0
 #define FVX_ACT_BWD_SILU 1
 int fvx_act_backward(int act, const void* in, int64_t ldi, const void* dy,
-                     int64_t ldy, void* out, int64_t ldo, int64_t rows,
-                     int64_t cols, void* stream);
+                     int64_t ldy, void* out, int64_t ldo, void* out_frag,
+                     int64_t rows, int64_t cols, void* stream);
 
 /* GeGLU product row by row: out[r][c] = bf16(gelu_tanh(gu[r][c]) *
  * gu[r][cols + c]) -- GemmaMLP's act(gate) * up (condition_gemma.py:
@@ -534,7 +540,7 @@ int fvx_act_backward(int act, const void* in, int64_t ldi, const void* dy,
  * reuses (the fused GEGLU GEMM keeps neither).  Same layout rules as
  * fvx_act_backward. */
 int fvx_geglu_rows(const void* gu, int64_t ldgu, void* out, int64_t ldo,
-                   int64_t rows, int64_t cols, void* stream);
+                   void* out_frag, int64_t rows, int64_t cols, void* stream);
 
 /* Masked-softmax backward of one attention problem
  * (condition_gemma.py:340-535's eager attention, softmax over
@@ -619,13 +625,14 @@ int fvx_transpose_bf16(const void* src, int64_t ld_src,
  * rope[positions[m]][i] (fp32 (cos, sin) pairs, the fvx_gemm QKV_ROPE
  * table): (ga, gb) -> (ga cos + gb sin, gb cos - ga sin).  dq is the sum of
  * dq_parts partials dq_part_stride elements apart (fvx_attention_backward's
- * key tiles; 1 for a plain dq). */
+ * key tiles; 1 for a plain dq).  out_frag (may be NULL; out may be NULL
+ * with it): the same rows in the fragment-major A layout (rows <= 64). */
 int fvx_rope_backward(const float* dq, int64_t ldq, int64_t dq_parts,
                       int64_t dq_part_stride, const float* dk,
                       int64_t ldk, const float* dv, int64_t ldv,
                       const float* rope, const int32_t* positions, void* out,
-                      int64_t ldo, int64_t rows, int64_t n_q_heads,
-                      int64_t head_dim, void* stream);
+                      int64_t ldo, void* out_frag, int64_t rows,
+                      int64_t n_q_heads, int64_t head_dim, void* stream);
 
 /* Guidance error and corrected update of one Euler step with use_vjp
  * (apply_rtc_guidance, rtc_guidance.py:107-155, under

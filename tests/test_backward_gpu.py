@@ -328,3 +328,37 @@ def test_attention_backward_fused(K, cuda, n, S):
                                        dout[z].to(cuda), dk, dv)
         assert rel_err(dk, dk_ref[z, S:]) <= 2e-2
         assert rel_err(dv, dv_ref[z, S:]) <= 2e-2
+
+
+def test_fragment_major_outputs(K, cuda):
+    """The fragment-major copies (the A operands of the bs=1 backward GEMMs)
+    hold exactly the row-major outputs' values, laid out as FragA."""
+    announce('backward fragment-major outputs')
+    m, hid, mlp, H, D = 51, 1024, 4096, 8, 256
+    x = randn((m, hid), 111).to(cuda)
+    dy = randn((m, hid), 112, dtype=torch.float32).to(cuda)
+    gate = randn((hid,), 113).to(cuda)
+    outb = torch.empty(m, hid, dtype=torch.bfloat16, device=cuda)
+    fa = K.FragA.empty(hid, cuda).rows(m)
+    K.rms_norm_backward(x, dy, out_bf16=outb, out_frag=fa, gate=gate)
+    assert torch.equal(fa.buf, K.pack_frag_a_ref(outb))
+    gu = randn((m, 2 * mlp), 114).to(cuda)
+    dh = randn((m, mlp), 115).to(cuda)
+    row = K.act_backward(K._lib.ACT_BWD_GEGLU, gu, dh)
+    fg = K.FragA.empty(2 * mlp, cuda).rows(m)
+    K.act_backward(K._lib.ACT_BWD_GEGLU, gu, dh, out_frag=fg)
+    assert torch.equal(fg.buf, K.pack_frag_a_ref(row))
+    h = K.geglu_rows(gu)
+    fh = K.FragA.empty(mlp, cuda).rows(m)
+    K.geglu_rows(gu, out_frag=fh)
+    assert torch.equal(fh.buf, K.pack_frag_a_ref(h))
+    rope = K.rope_table(1024, D).to(cuda)
+    pos = torch.arange(m, dtype=torch.int32, device=cuda) * 7
+    dq = randn((m, H * D), 116, dtype=torch.float32).to(cuda)
+    dk = randn((m, D), 117, dtype=torch.float32).to(cuda)
+    dv = randn((m, D), 118, dtype=torch.float32).to(cuda)
+    out = torch.empty(m, (H + 2) * D, dtype=torch.bfloat16, device=cuda)
+    K.rope_backward(dq, dk, dv, rope, pos, out, H, D)
+    fq = K.FragA.empty((H + 2) * D, cuda).rows(m)
+    K.rope_backward(dq, dk, dv, rope, pos, None, H, D, out_frag=fq)
+    assert torch.equal(fq.buf, K.pack_frag_a_ref(out))
