@@ -137,6 +137,8 @@ class AttnBwdDesc(ctypes.Structure):
         ('k', c_vp), ('k_zs', c_i64),
         ('v', c_vp), ('v_zs', c_i64),
         ('kt', c_vp), ('kt_ld', c_i64), ('kt_zs', c_i64),
+        ('vt', c_vp), ('vt_ld', c_i64), ('vt_zs', c_i64),
+        ('refresh_key0', c_i64), ('refresh_n', c_i64),
         ('kgrp', c_vp), ('kgrp_zs', c_i64),
         ('qgrp', c_vp), ('qgrp_zs', c_i64),
         ('stats', c_vp),

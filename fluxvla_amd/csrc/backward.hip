@@ -430,6 +430,8 @@ struct AttnBwdArgs {
   const bf16_t* k; int64_t k_zs;     // key rows [nk][256]
   const bf16_t* v; int64_t v_zs;     // value rows [nk][256]
   const bf16_t* kt; int64_t kt_ld, kt_zs;  // keys transposed [256][kt_ld]
+  const bf16_t* vt; int64_t vt_ld, vt_zs;  // values transposed [256][vt_ld] (refresh)
+  int rk0, rn;                        // keys whose kt columns / v rows are refreshed
   const int32_t* kgrp; int64_t kgrp_zs;
   const int32_t* qgrp; int64_t qgrp_zs;
   float* pm; float* pl;              // [problem][key tile][R]
@@ -530,6 +532,32 @@ __global__ __launch_bounds__(128) void attn_bwd_stats_kernel(AttnBwdArgs a) {
     const int64_t at = ((int64_t)z * a.n_kt + kt) * a.rows + r0 + rr;
     a.pm[at] = m;
     a.pl[at] = e;
+  }
+  // Refresh of the main pass's operand copies for keys [rk0, rk0 + rn) of
+  // this tile (the keys this step wrote into the caches): kt's columns from
+  // the key rows and v's rows from the transposed values.  The tile's row
+  // blocks split the 256 dims between them (8 at a time), so the few
+  // elements each writes cost no more than a short tail.  Only the main
+  // pass reads kt and v.
+  if (a.vt) {
+    const int j0 = max(kt * kBwdKT, a.rk0), j1 = min(kt * kBwdKT + kBwdKT, a.rk0 + a.rn);
+    const int dch = ((kBwdD / 8 + (int)gridDim.x - 1) / (int)gridDim.x) * 8;
+    const int d0 = blockIdx.x * dch, d1 = min(kBwdD, d0 + dch);
+    if (j0 < j1 && d0 < d1) {
+      const int nj = j1 - j0, nd = d1 - d0;
+      const bf16_t* kz = a.k + z * a.k_zs;
+      const bf16_t* vtz = a.vt + z * a.vt_zs;
+      bf16_t* ktz = const_cast<bf16_t*>(a.kt) + z * a.kt_zs;
+      bf16_t* vz = const_cast<bf16_t*>(a.v) + z * a.v_zs;
+      for (int idx = t; idx < nj * nd; idx += 128) {  // writes along keys
+        const int d = d0 + idx / nj, jj = idx % nj;
+        ktz[(int64_t)d * a.kt_ld + j0 + jj] = kz[(int64_t)(j0 + jj) * kBwdD + d];
+      }
+      for (int idx = t; idx < nj * nd; idx += 128) {  // writes along dims
+        const int jj = idx / nd, d = d0 + idx % nd;
+        vz[(int64_t)(j0 + jj) * kBwdD + d] = vtz[(int64_t)d * a.vt_ld + j0 + jj];
+      }
+    }
   }
 }
 
@@ -1077,6 +1105,10 @@ extern "C" int fvx_attention_backward(const fvx_attn_bwd_desc* d, void* stream) 
                   d->kt_ld % 8 == 0 && (int64_t)d->rows * kBwdD * 2 < ((int64_t)1 << 31) &&
                   (int64_t)d->kt_ld * kBwdD * 2 < ((int64_t)1 << 31),
               FVX_ERR_SHAPE, "attention_backward: bad sizes");
+  FVX_REQUIRE(!d->vt || (d->refresh_key0 >= 0 && d->refresh_n >= 0 &&
+                          d->refresh_key0 + d->refresh_n <= d->n_keys &&
+                          d->vt_ld >= d->n_keys && al16(d->vt)),
+              FVX_ERR_SHAPE, "attention_backward: bad refresh range or vt");
   FVX_REQUIRE((!d->ds_t && !d->p_t) ||
                   (d->n_suffix > 0 && d->key0 >= 0 && d->key0 + d->n_suffix <= d->n_keys &&
                    d->ldt >= d->rows),
@@ -1097,6 +1129,8 @@ extern "C" int fvx_attention_backward(const fvx_attn_bwd_desc* d, void* stream) 
   a.k = (const bf16_t*)d->k; a.k_zs = d->k_zs;
   a.v = (const bf16_t*)d->v; a.v_zs = d->v_zs;
   a.kt = (const bf16_t*)d->kt; a.kt_ld = d->kt_ld; a.kt_zs = d->kt_zs;
+  a.vt = (const bf16_t*)d->vt; a.vt_ld = d->vt_ld; a.vt_zs = d->vt_zs;
+  a.rk0 = (int)d->refresh_key0; a.rn = (int)d->refresh_n;
   a.kgrp = d->kgrp; a.kgrp_zs = d->kgrp_zs;
   a.qgrp = d->qgrp; a.qgrp_zs = d->qgrp_zs;
   a.pm = d->stats;

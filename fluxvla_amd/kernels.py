@@ -1084,13 +1084,15 @@ def attention_backward_parts(n_keys):
 
 def attention_backward(q, o, dout, k, v, kt, dq, stats, *, heads, scale,
                        kgrp=None, qgrp=None, ds_t=None, p_t=None, key0=0,
-                       n_suffix=0):
+                       n_suffix=0, vt=None, refresh=(0, 0)):
     """Fused decode-shape attention backward (fvx_attention_backward) for
     n problems: q / o / dout bf16 [n, rows, 256]; k / v bf16 [n, >= n_keys,
     256] rows with n_keys = k.shape[1]; kt bf16 [n, 256, kt_ld] (zero past
     n_keys); dq fp32 [parts, n * rows, 256]; stats fp32 scratch of
     2 * n * parts * rows; kgrp int32 [n, >= n_keys], qgrp [n, rows / heads];
-    ds_t / p_t bf16 [n, n_suffix, >= rows]."""
+    ds_t / p_t bf16 [n, n_suffix, >= rows]; vt bf16 [n, 256, >= n_keys] (the
+    value cache) with ``refresh`` = (first key, count): those keys' kt
+    columns and v rows are first rewritten from k and vt."""
     d = _lib.AttnBwdDesc()
     n, rows, hd = q.shape
     nk = k.shape[1]
@@ -1118,6 +1120,12 @@ def attention_backward(q, o, dout, k, v, kt, dq, stats, *, heads, scale,
     d.k, d.k_zs = k.data_ptr(), k.stride(0)
     d.v, d.v_zs = v.data_ptr(), v.stride(0)
     d.kt, d.kt_ld, d.kt_zs = kt.data_ptr(), kt.stride(1), kt.stride(0)
+    if vt is not None:
+        _check(vt, 'vt', contiguous=False)
+        if vt.shape[:2] != (n, hd) or vt.stride(2) != 1 or vt.shape[2] < nk:
+            raise ValueError('vt must be [n, head_dim, >= n_keys]')
+        d.vt, d.vt_ld, d.vt_zs = vt.data_ptr(), vt.stride(1), vt.stride(0)
+        d.refresh_key0, d.refresh_n = refresh
     if kgrp is not None:
         _check(kgrp, 'kgrp', dtype=torch.int32, contiguous=False)
         _check(qgrp, 'qgrp', dtype=torch.int32, contiguous=False)

@@ -334,16 +334,15 @@ class ExpertVJP:
         nk, R = S + Ss, Ss * H
         kc, vc = b['kc'][i], b['vc'][i]
         kT, vr = v['kT'][i], v['vr'][i]
-        # this step's suffix keys / values into the transposed copies
-        K.transpose(kc[:, S:nk], kT[:, :, S:nk])
-        K.transpose(vc[:, :, S:nk], vr[:, S:nk])
         q3 = v['Q'][i].view(B, R, D)
         do3 = v['dctx'].view(B, R, D)
         K.attention_backward(q3, v['CTX'][i].view(B, R, D), do3, kc[:, :nk],
                              vr[:, :nk], kT, v['dq'], v['stats'], heads=H,
                              scale=self.scale, kgrp=b['kgrp'],
                              qgrp=b['qgrp_suf'], ds_t=v['ds_t'], p_t=v['p_t'],
-                             key0=S, n_suffix=Ss)
+                             key0=S, n_suffix=Ss,
+                             # this step's suffix keys / values into the copies
+                             vt=vc, refresh=(S, Ss))
         for z in range(B):
             rows = slice(z * Ss, (z + 1) * Ss)
             K.attention_suffix_kv_backward(v['ds_t'][z], v['p_t'][z], q3[z],

@@ -592,6 +592,11 @@ int fvx_attention_suffix_kv_backward(const void* ds_t, const void* p_t,
  *       stride t_zs): dS and P of keys key0 .. key0 + n_suffix - 1,
  *       column r = row r (fvx_attention_suffix_kv_backward's operands);
  *   stats: fp32 scratch of 2 * n_problems * dq_parts * rows floats.
+ * vt (may be NULL): the values transposed ([256][vt_ld] bf16 per problem,
+ * the value cache); with it the call first rewrites, for keys
+ * refresh_key0 .. refresh_key0 + refresh_n - 1, kt's columns from k and
+ * v's rows from vt (the keys a step has just written into the caches), so
+ * kt and v are then written as well as read.
  * Strides (*_zs) in elements; head_dim must be 256. */
 typedef struct fvx_attn_bwd_desc {
   const void* q; int64_t q_zs;
@@ -600,6 +605,8 @@ typedef struct fvx_attn_bwd_desc {
   const void* k; int64_t k_zs;
   const void* v; int64_t v_zs;
   const void* kt; int64_t kt_ld, kt_zs;
+  const void* vt; int64_t vt_ld, vt_zs;
+  int64_t refresh_key0, refresh_n;
   const int32_t* kgrp; int64_t kgrp_zs;
   const int32_t* qgrp; int64_t qgrp_zs;
   float* stats;

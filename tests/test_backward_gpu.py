@@ -299,20 +299,29 @@ def test_attention_backward_fused(K, cuda, n, S):
     p = torch.softmax(logits, -1)
     o = p @ vd
     dq_ref, dk_ref, dv_ref = torch.autograd.grad(o, (qd, kd, vd), dout.double())
+    # the copies the kernel reads hold the prefix keys only: the suffix
+    # keys' kt columns and v rows come from the refresh (k, and vt = v^T)
     kt = torch.zeros(n, D, T, dtype=torch.bfloat16)
-    kt[:, :, :nk] = k[:, :nk].transpose(1, 2)
+    kt[:, :, :S] = k[:, :S].transpose(1, 2)
+    vrow = v.clone()
+    vrow[:, S:] = 0
+    vt = v.transpose(1, 2).contiguous()
     parts = K.attention_backward_parts(nk)
     dq = torch.full((parts, n * R, D), float('nan'), device=cuda)
     stats = torch.empty(2 * n * parts * R, device=cuda)
     ds_t = torch.zeros(n, Ss, R, dtype=torch.bfloat16, device=cuda)
     p_t = torch.zeros(n, Ss, R, dtype=torch.bfloat16, device=cuda)
     kc = k.to(cuda)
-    vc = v.to(cuda)
+    vc, ktc = vrow.to(cuda), kt.to(cuda)
     K.attention_backward(q.to(cuda), o.detach().to(torch.bfloat16).to(cuda),
-                         dout.to(cuda), kc[:, :nk], vc[:, :nk], kt.to(cuda), dq,
+                         dout.to(cuda), kc[:, :nk], vc[:, :nk], ktc, dq,
                          stats, heads=H, scale=scale, kgrp=kgrp.to(cuda),
                          qgrp=qgrp.to(cuda), ds_t=ds_t, p_t=p_t, key0=S,
-                         n_suffix=Ss)
+                         n_suffix=Ss, vt=vt.to(cuda), refresh=(S, Ss))
+    want_kt = torch.zeros(n, D, T, dtype=torch.bfloat16)
+    want_kt[:, :, :nk] = k[:, :nk].transpose(1, 2)
+    assert torch.equal(ktc.cpu(), want_kt)
+    assert torch.equal(vc.cpu()[:, :nk], v[:, :nk])
     got = dq.sum(0).view(n, R, D)
     assert torch.isfinite(got).all()
     assert rel_err(got, dq_ref) <= 2e-2
