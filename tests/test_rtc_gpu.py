@@ -332,3 +332,29 @@ def test_guidance_vjp_step_matches_autograd(models, cuda, pi05, batch):
     print(f'u rel err {eu:.3e}; g rel err {eg:.3e}, cosine {cos:.5f}')
     assert eu <= 2e-2
     assert eg <= 5e-2 and cos >= 0.995
+
+
+@pytest.mark.parametrize('weight_dtype', ['fp8', 'fp8_w8a8'])
+def test_guidance_vjp_fp8_chunk(cuda, weight_dtype):
+    """Guidance with use_vjp on fp8 weights (PI0.5, config 5): the backward
+    runs on the dequantized weights, the forward on the fp8 GEMMs; against
+    the oracle's VJP loop on the dequantized state dict, bs 1 and 2, within
+    the bar of the plain fp8 chunk (2e-2 W8A16, 5e-2 W8A8)."""
+    from fluxvla_amd.pi0_inference import PI0Inference
+    cfg = tiny(pi05=True, ori_action_dim=14)
+    sd = make_state_dict(cfg, seed=60)
+    m = PI0Inference(cfg, sd, device='cuda', max_batch=2,
+                     weight_dtype=weight_dtype)
+    sdq = m.dequantized_state_dict(sd)
+    bar = CHUNK_ATOL if weight_dtype == 'fp8' else 5e-2
+    rc = {'enabled': True, 'method': 'guidance', 'use_vjp': True,
+          'max_guidance_weight': 5.0, 'decay_end': 20}
+    for batch in (1, 2):
+        announce(f'guidance-vjp {weight_dtype} chunk batch={batch}')
+        inp = make_inputs(cfg, batch=batch, seed=61)
+        prev = torch.randn(batch, 40, 14, generator=gen(62)) * 0.5
+        ref, _ = _oracle(cfg, sdq, inp, prev, 6, rc)
+        got = _run(m, inp, cuda, prev, 6, rc)
+        err = (got - ref).abs().max().item()
+        print(f'{weight_dtype} guidance-vjp chunk max abs err {err:.3e}')
+        assert err <= bar
