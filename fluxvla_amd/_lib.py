@@ -78,6 +78,7 @@ class GemmDesc(ctypes.Structure):
         ('a_scale', c_vp), ('bias2_f32', c_vp),
         ('ln_csum', c_vp),
         ('a_row_group', c_i64), ('a_row_group_stride', c_i64),
+        ('gu_out', c_vp), ('ld_gu', c_i64),
     ]
 
 

@@ -340,6 +340,15 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = fmaf(-mr, in.cs[e], x[e]);
   if (MODE == FVX_GEMM_GEGLU) {
+    if (p.gu_out) {
+      // the pre-activations the product is taken from (gate | up)
+      float uu[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) uu[e] = u[e] * r;
+      bf16_t* g = (bf16_t*)p.gu_out + out_row(p, m) * p.ld_gu + n;
+      st_b8(g, x, vec, cnt);
+      st_b8(g + p.n, uu, vec, cnt);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = gelu_tanh(x[e]) * (u[e] * r);
     st_b8((bf16_t*)p.c + out_row(p, m) * p.ldc + n, x, vec, cnt);
@@ -2429,6 +2438,10 @@ static int validate(const GemmArgs& d) {
               "gemm: QKV_ROPE / GEGLU take fp32 biases only with a_scale, no bf16 bias");
   FVX_REQUIRE(!d.bias2_f32 || d.mode == FVX_GEMM_GEGLU, FVX_ERR_ARG,
               "gemm: bias2_f32 is the GEGLU up half's bias");
+  FVX_REQUIRE(!d.gu_out || (d.mode == FVX_GEMM_GEGLU && d.ld_gu >= 2 * d.n &&
+                            d.ld_gu % 8 == 0 && aligned16(d.gu_out)),
+              FVX_ERR_ARG, "gemm: gu_out needs GEGLU mode, ld_gu >= 2 n (a multiple of 8) "
+                           "and a 16-byte aligned buffer");
   FVX_REQUIRE(((uintptr_t)d.bias2_f32 & 15) == 0, FVX_ERR_ALIGN,
               "gemm: bias2_f32 must be 16B aligned");
   FVX_REQUIRE(!d.rtc_prev || (d.ld_prev >= d.n && (d.rtc_lock || d.rtc_cw)), FVX_ERR_ARG,
@@ -2566,7 +2579,7 @@ static TilePlan plan_tile(const GemmArgs& d) {
   const int64_t tiles = ((d.m + 63) / 64) * ((d.n + bn - 1) / bn);
   const int64_t wtiles = ((d.m + 255) / 256) * ((d.n + 2 * bn - 1) / (2 * bn));
   const bool wide_ok = (!d.b_fp8 || FVX_WIDE_F8) && d.k % 64 == 0 && d.split_k <= 1 &&
-                       !d.ln_csum && !a_grouped(d) &&
+                       !d.ln_csum && !a_grouped(d) && !d.gu_out &&
                        (d.mode == FVX_GEMM_PLAIN || gg || d.mode == FVX_GEMM_QKV_ROPE);
   t.splits = 1;
   // PLAIN / QKV: one workgroup of 256 x 256 per CU at a time, so the tiles

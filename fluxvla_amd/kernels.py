@@ -515,11 +515,12 @@ def _set_a_scale(d, a_scale=None, bias_f32=None, bias2_f32=None):
 
 def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
                c_frag=None, ss_in=None, a8=None, a8_out=None, a_scale=None,
-               bias_f32=None, bias2_f32=None):
+               bias_f32=None, bias2_f32=None, gu_out=None):
     """out = gelu_tanh(a @ gate_w^T) * (a @ up_w^T); with ``a_scale`` (the
     folded adaptive RMSNorm, M <= 64): gelu_tanh(r a' @ gate_w^T + bias_f32)
     * (r a' @ up_w^T + bias2_f32), a' = a * (1 + a_scale), r the RMS factor
-    of a."""
+    of a.  ``gu_out`` (bf16 [M, 2N] view): the gate and up values the
+    product is taken from (fvx_gemm_desc.gu_out)."""
     d = _gemm_desc(a, gate_w)
     if isinstance(gate_w, Fp8Weight):
         if (not isinstance(up_w, Fp8Weight) or up_w.frag != gate_w.frag or
@@ -549,6 +550,12 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
     _set_a8(d, a8, a8_out)
     d.split_k = split_k
     _set_c_frag(d, c_frag)
+    if gu_out is not None:
+        _check(gu_out, 'gu_out', contiguous=False)
+        rows, d.ld_gu = _rows_ld(gu_out, 'gu_out')
+        if gu_out.shape[-1] != 2 * d.n or rows != d.m:
+            raise ValueError(f'gu_out must be [{d.m}, {2 * d.n}]')
+        d.gu_out = gu_out.data_ptr()
     _run_gemm(d)
     return out
 

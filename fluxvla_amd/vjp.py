@@ -10,9 +10,9 @@ e = w (prev - x_1) on the previous chunk's rows.  Here one Euler step is
   forward   the expert as in the plain loop, keeping each layer's input
             stream X[i], its post-attention stream X2[i], its rotated
             queries Q[i] (the key/value cache already holds the suffix
-            keys and values) and its MLP's [gate | up] rows GU[i] (one GEMM
-            over the stacked weights, then the GeGLU product); u from a
-            PLAIN fp32 GEMM of action_out_proj;
+            keys and values), its attention output and its MLP's [gate |
+            up] rows GU[i] (written by the GeGLU GEMM beside its product);
+            u from a PLAIN fp32 GEMM of action_out_proj;
   error     e = bf16(w (prev - x + (1 - t) u))                (one kernel);
   backward  g = J_u^T e layer by layer, last to first:
               down:       dh = (gate2 dX3) @ W_down
@@ -62,11 +62,6 @@ class ExpertVJP:
         self.m = m = model
         cfg = m.cfg
         self.wT = []
-        # [gate; up] stacked: one forward GEMM whose output the backward
-        # keeps ([gate | up] per row)
-        self.gu_w = [torch.cat([_weight_t(L['gate_w']).t(),
-                                _weight_t(L['up_w']).t()], 0).contiguous()
-                     for L in m.exp['layers']]
         for L in m.exp['layers']:
             gu = torch.cat([_weight_t(L['gate_w']), _weight_t(L['up_w'])], 1)
             self.wT.append({'qkv': _weight_t(L['qkv_w']),
@@ -82,7 +77,6 @@ class ExpertVJP:
         # fragment-major copies for the M <= 64 GEMMs (bs = 1)
         F = K.FragB.pack
         self.wT_f = [{nm: F(w) for nm, w in L.items()} for L in self.wT]
-        self.gu_w_f = [F(w) for w in self.gu_w]
         self.out_t_f = F(self.out_t)
         if cfg.pi05:
             self.in_t_f = F(self.in_t)
@@ -210,19 +204,15 @@ class ExpertVJP:
             gate = v['gate'] if cfg.pi05 else None
             K.gemm(f['ctx'] if f else ctx, L['o_w'], out=X2[i], residual=x,
                    gate=gate, c_frag=None if cfg.pi05 else fc('x2'))
-            # [gate | up] kept for the backward, then the GeGLU product
-            w_gu = self.gu_w_f[i] if fr else self.gu_w[i]
+            # the GeGLU GEMM, keeping its [gate | up] values for the backward
             if cfg.pi05:
                 K.adarms_norm(X2[i], st[2 * i + 1:2 * i + 2], out=v['xn'],
                               gate_out=v['gate'], eps=cfg.rms_eps)
-                K.gemm(v['xn'], w_gu, out=v['GU'][i])
+                a2, rn = v['xn'], None
             else:
-                K.gemm(f['x2'] if f else X2[i], w_gu, out=v['GU'][i],
-                       rownorm_eps=cfg.rms_eps)
-            if f:
-                K.geglu_rows(v['GU'][i], out_frag=f['h'])
-            else:
-                K.geglu_rows(v['GU'][i], out=v['h'])
+                a2, rn = (f['x2'] if f else X2[i]), cfg.rms_eps
+            K.gemm_geglu(a2, L['gate_w'], L['up_w'], out=v['h'],
+                         rownorm_eps=rn, c_frag=fc('h'), gu_out=v['GU'][i])
             K.gemm(f['h'] if f else v['h'], L['down_w'], out=X[i + 1],
                    residual=X2[i], gate=gate,
                    c_frag=None if cfg.pi05 else fc('x'))

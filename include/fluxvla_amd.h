@@ -233,6 +233,15 @@ typedef struct fvx_gemm_desc {
    * a8); 0: rows m of a. */
   int64_t a_row_group;
   int64_t a_row_group_stride;
+  /* GEGLU pre-activations (no counterpart in the reference; for the
+   * GeGLU backward of guidance RTC with use_vjp, which autograd feeds from
+   * the same two values): gu_out (may be NULL) receives per output row the
+   * bf16 gate values (columns n) and up values (columns N + n) that the
+   * product gelu_tanh(gate) * up is taken from, row stride ld_gu >= 2 N.
+   * GEGLU mode on the skinny and tile kernels (the wide kernel is not used
+   * with it). */
+  void* gu_out;
+  int64_t ld_gu;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */

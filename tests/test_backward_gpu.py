@@ -371,3 +371,23 @@ def test_fragment_major_outputs(K, cuda):
     fq = K.FragA.empty((H + 2) * D, cuda).rows(m)
     K.rope_backward(dq, dk, dv, rope, pos, None, H, D, out_frag=fq)
     assert torch.equal(fq.buf, K.pack_frag_a_ref(out))
+
+
+@pytest.mark.parametrize('m', [51, 102])
+def test_geglu_gemm_keeps_pre_activations(K, cuda, m):
+    """fvx_gemm_desc.gu_out: the GeGLU GEMM (skinny at M = 51, tiled at
+    102; rownorm) also stores the gate and up values its product is taken
+    from -- against float64, and its product bitwise the same as without."""
+    announce(f'geglu gu_out m={m}')
+    k, n = 1024, 4096
+    a = randn((m, k), 121, std=2.0).to(cuda)
+    wg = randn((n, k), 122, std=0.03).to(cuda)
+    wu = randn((n, k), 123, std=0.03).to(cuda)
+    gu = torch.full((m, 2 * n), float('nan'), dtype=torch.bfloat16, device=cuda)
+    h = K.gemm_geglu(a, wg, wu, rownorm_eps=1e-6, gu_out=gu)
+    h0 = K.gemm_geglu(a, wg, wu, rownorm_eps=1e-6)
+    assert torch.equal(h, h0)
+    ad = a.double().cpu()
+    xn = ad * torch.rsqrt(ad.pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert rel_err(gu[:, :n], xn @ wg.double().cpu().t()) <= BF16_TOL
+    assert rel_err(gu[:, n:], xn @ wu.double().cpu().t()) <= BF16_TOL
