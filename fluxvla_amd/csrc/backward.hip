@@ -755,12 +755,22 @@ __global__ __launch_bounds__(256) void rope_backward_kernel(
   float a, b;
   bool rot = true;
   if (p < qpairs) {
-    // dq: the sum of dq_parts partials (key tiles), in part order
+    // dq: the sum of dq_parts partials (key tiles), in part order, eight
+    // partials' loads in flight at a time (one round trip per eight)
     a = b = 0.f;
-    for (int u = 0; u < dq_parts; ++u) {
-      const float2 v = *reinterpret_cast<const float2*>(dq + u * dq_part_stride + m * ldq + 2 * p);
-      a += v.x;
-      b += v.y;
+    const float* src = dq + m * ldq + 2 * p;
+    for (int u0 = 0; u0 < dq_parts; u0 += 8) {
+      float2 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = u0 + u < dq_parts
+                   ? *reinterpret_cast<const float2*>(src + (int64_t)(u0 + u) * dq_part_stride)
+                   : float2{0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        a += v[u].x;
+        b += v[u].y;
+      }
     }
   } else if (p < qpairs + half) {
     const int i = p - qpairs;
