@@ -718,8 +718,9 @@ gpurun_out` over its CSV):
 
 The last whole chunk of bench.py's timed loop (graph replay; from its
 im2col to its last Euler GEMM).  The same run printed value =
-{js.get('value')} ms per chunk (HIP events, no profiler in the way of its
-own figure; under the profiler the chunk spans longer).
+{js.get('value')} ms per chunk (its own HIP events around the graph
+replays, slowed by the profiler tracing every dispatch; the kernel times
+below are the trace's own).
 
 One chunk: {len(chunk)} dispatches, {tot / 1e3:.3f} ms of kernel time over a
 {span:.3f} ms span.
@@ -805,7 +806,8 @@ prefix 5; each Euler step a forward with saved activations and a backward
 through the expert) through their captured graph.  The last whole chunk
 (from its im2col to its last guidance update).  The same run printed
 {js.get('ms_per_chunk')} ms per chunk (wall clock over its timed chunks,
-no profiler in the way).
+slowed by the profiler tracing every dispatch; the kernel times below are
+the trace's own).
 
 One chunk: {len(chunk)} dispatches, {tot / 1e3:.3f} ms of kernel time over a
 {span:.3f} ms span.
