@@ -163,16 +163,8 @@ __global__ __launch_bounds__(256) void act_backward_kernel(
   if (ACT == kActGeglu) {
     float u[8], o2[8];
     unpack8(ld8(in + m * ldi + cols + c), u);
-    constexpr float k2 = 1.5957691216057308f;  // 2 sqrt(2 / pi)
-    constexpr float k1 = 0.044715f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = a[e];
-      const float s = 1.f / (1.f + expf(-k2 * (x + k1 * x * x * x)));
-      const float dg = s + x * s * (1.f - s) * k2 * (1.f + 3.f * k1 * x * x);
-      o[e] = d[e] * u[e] * dg;
-      o2[e] = d[e] * (x * s);
-    }
+    for (int e = 0; e < 8; ++e) geglu_grad(d[e], a[e], u[e], o[e], o2[e]);
     const bf16x8 b = pack8(o), b2 = pack8(o2);
     if (out) {
       st8(out + m * ldo + c, b);

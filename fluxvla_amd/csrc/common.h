@@ -325,6 +325,19 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// GeGLU's backward at one element: with h = gelu_tanh(g) * u and the
+// incoming dh, dg = dh u gelu'(g) and du = dh gelu(g), where gelu_tanh(g) =
+// g s, s = 1 / (1 + exp(-2v)), v = sqrt(2/pi) (g + 0.044715 g^3), so
+// gelu' = s + g s (1 - s) 2 sqrt(2/pi) (1 + 3 * 0.044715 g^2).
+__device__ __forceinline__ void geglu_grad(float dh, float g, float u, float& dg,
+                                           float& du) {
+  constexpr float k2 = 1.5957691216057308f;  // 2 sqrt(2 / pi)
+  constexpr float k1 = 0.044715f;
+  const float s = 1.f / (1.f + expf(-k2 * (g + k1 * g * g * g)));
+  dg = dh * u * (s + g * s * (1.f - s) * k2 * (1.f + 3.f * k1 * g * g));
+  du = dh * (g * s);
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), written through the
   // identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)) with the exponent in
