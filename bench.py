@@ -1189,7 +1189,8 @@ def main():
         return
     if args.gpus != 1:
         print('bench.py: this build runs on one GPU; multi-GPU figures are '
-              'not part of it (the path shards by request, see DESIGN.md)',
+              'not part of it (the path shards by request: each GPU serves '
+              'whole requests)',
               file=sys.stderr)
         sys.exit(2)
 
