@@ -541,13 +541,40 @@ __global__ __launch_bounds__(128) void attn_bwd_stats_kernel(AttnBwdArgs a) {
       const bf16_t* vtz = a.vt + z * a.vt_zs;
       bf16_t* ktz = const_cast<bf16_t*>(a.kt) + z * a.kt_zs;
       bf16_t* vz = const_cast<bf16_t*>(a.v) + z * a.v_zs;
-      for (int idx = t; idx < nj * nd; idx += 128) {  // writes along keys
-        const int d = d0 + idx / nj, jj = idx % nj;
-        ktz[(int64_t)d * a.kt_ld + j0 + jj] = kz[(int64_t)(j0 + jj) * kBwdD + d];
+      // 16 elements per thread and pass: all loads first, then the stores
+      // (a store ahead of the next load would make every element wait for
+      // its own round trip: the compiler cannot move a load above a store
+      // that may alias it)
+      const int total = nj * nd;
+      for (int base = t; base < total; base += 128 * 16) {  // writes along keys
+        bf16_t vals[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int idx = base + 128 * u;
+          const int d = d0 + idx / nj, jj = idx % nj;
+          vals[u] = idx < total ? kz[(int64_t)(j0 + jj) * kBwdD + d] : (bf16_t)0;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int idx = base + 128 * u;
+          const int d = d0 + idx / nj, jj = idx % nj;
+          if (idx < total) ktz[(int64_t)d * a.kt_ld + j0 + jj] = vals[u];
+        }
       }
-      for (int idx = t; idx < nj * nd; idx += 128) {  // writes along dims
-        const int jj = idx / nd, d = d0 + idx % nd;
-        vz[(int64_t)(j0 + jj) * kBwdD + d] = vtz[(int64_t)d * a.vt_ld + j0 + jj];
+      for (int base = t; base < total; base += 128 * 16) {  // writes along dims
+        bf16_t vals[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int idx = base + 128 * u;
+          const int jj = idx / nd, d = d0 + idx % nd;
+          vals[u] = idx < total ? vtz[(int64_t)d * a.vt_ld + j0 + jj] : (bf16_t)0;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int idx = base + 128 * u;
+          const int jj = idx / nd, d = d0 + idx % nd;
+          if (idx < total) vz[(int64_t)(j0 + jj) * kBwdD + d] = vals[u];
+        }
       }
     }
   }
