@@ -660,6 +660,23 @@ __global__ __launch_bounds__(256) void attn_bwd_main_kernel(AttnBwdArgs a) {
     acc = bwd_block(rq, r0, make_rsrc(a.k + z * a.k_zs, kbytes), kb, lane);
   } else {
     acc = bwd_block(rdo, r0, make_rsrc(a.v + z * a.v_zs, kbytes), kb, lane);
+  }
+  // the dQ product's K^T fragments (wave w: dims 64 w .. 64 w + 63), loaded
+  // now so that they are in flight during the softmax and ahead of the
+  // stores below (a load after a possibly aliasing store waits for it)
+  const __amdgpu_buffer_rsrc_t rkt =
+      make_rsrc(a.kt + z * a.kt_zs, (uint32_t)(kBwdD * a.kt_ld * 2));
+  bf16x8 kv[4][2];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int key = k0 + 16 * ks + 8 * (lane >> 5);  // 8 keys wholly below kt_ld or not
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int d = 64 * w + 32 * nb + (lane & 31);
+      kv[ks][nb] = bload8(rkt, key < a.kt_ld ? (uint32_t)(d * a.kt_ld + key) * 2 : kOOB);
+    }
+  }
+  if (w >= 2) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) sdP[kh][i][lane] = acc[i];
     if (rq_t >= 0 && rq_t < kBwdRB) sQG[rq_t] = qgv;
@@ -689,19 +706,8 @@ __global__ __launch_bounds__(256) void attn_bwd_main_kernel(AttnBwdArgs a) {
   __syncthreads();
   // dQ share of this key tile: [32 rows][256 dims] = dS [32][64] K [64][256];
   // wave w takes the dims 64 w .. 64 w + 63 (two 32-column blocks)
-  const __amdgpu_buffer_rsrc_t rkt =
-      make_rsrc(a.kt + z * a.kt_zs, (uint32_t)(kBwdD * a.kt_ld * 2));
   f32x16_t dq[2] = {};
-  bf16x8 kv[4][2], av[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int key = k0 + 16 * ks + 8 * (lane >> 5);  // 8 keys wholly below kt_ld or not
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int d = 64 * w + 32 * nb + (lane & 31);
-      kv[ks][nb] = bload8(rkt, key < a.kt_ld ? (uint32_t)(d * a.kt_ld + key) * 2 : kOOB);
-    }
-  }
+  bf16x8 av[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
     av[ks] = *reinterpret_cast<const bf16x8*>(&sDS[lane & 31][16 * ks + 8 * (lane >> 5)]);
