@@ -79,6 +79,8 @@ class GemmDesc(ctypes.Structure):
         ('ln_csum', c_vp),
         ('a_row_group', c_i64), ('a_row_group_stride', c_i64),
         ('gu_out', c_vp), ('ld_gu', c_i64),
+        ('k_t_out', c_vp), ('ld_kt', c_i64),
+        ('v_rows_out', c_vp), ('ld_vr', c_i64),
     ]
 
 

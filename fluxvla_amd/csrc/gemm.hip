@@ -368,11 +368,21 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
         x[2 * i] = a * c - b * s;
         x[2 * i + 1] = b * c + a * s;
       }
-      if (n < qcols)
+      if (n < qcols) {
         st_b8((bf16_t*)p.q_out + m * p.ldq + n, x, vec, cnt);
-      else
+      } else {
         st_b8((bf16_t*)p.k_out + out_row(p, m) * p.ldk + (n - qcols), x, vec,
               cnt);
+        if (p.k_t_out) {
+          // the keys transposed as well ([group][head_dim][ld_kt])
+          const int64_t b = p.row_group > 0 ? udiv32(m, p.row_group) : 0;
+          const int64_t t = p.row_group > 0 ? umod32(m, p.row_group) : m;
+          bf16_t* dst = (bf16_t*)p.k_t_out + (b * hd + (n - qcols)) * p.ld_kt + t;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (e < cnt) dst[e * p.ld_kt] = f2bf(x[e]);
+        }
+      }
     } else if (p.v_transposed) {
       // V^T cache: [group][head_dim][ldv], tokens contiguous
       const int64_t b = p.row_group > 0 ? udiv32(m, p.row_group) : 0;
@@ -381,6 +391,9 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int64_t m,
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (e < cnt) dst[e * p.ldv] = f2bf(x[e]);
+      if (p.v_rows_out)  // the values row-major as well
+        st_b8((bf16_t*)p.v_rows_out + out_row(p, m) * p.ld_vr + (n - qcols - hd), x, vec,
+              cnt);
     } else {
       st_b8((bf16_t*)p.v_out + out_row(p, m) * p.ldv + (n - qcols - hd), x,
             vec, cnt);
@@ -2438,6 +2451,13 @@ static int validate(const GemmArgs& d) {
               "gemm: QKV_ROPE / GEGLU take fp32 biases only with a_scale, no bf16 bias");
   FVX_REQUIRE(!d.bias2_f32 || d.mode == FVX_GEMM_GEGLU, FVX_ERR_ARG,
               "gemm: bias2_f32 is the GEGLU up half's bias");
+  FVX_REQUIRE((!d.k_t_out && !d.v_rows_out) ||
+                  (d.mode == FVX_GEMM_QKV_ROPE && d.v_transposed &&
+                   (!d.k_t_out || d.ld_kt > 0) &&
+                   (!d.v_rows_out || (d.ld_vr >= d.head_dim && d.ld_vr % 8 == 0 &&
+                                      aligned16(d.v_rows_out)))),
+              FVX_ERR_ARG, "gemm: k_t_out / v_rows_out need QKV_ROPE with a transposed "
+                           "v_out (and ld_vr >= head_dim, a multiple of 8)");
   FVX_REQUIRE(!d.gu_out || (d.mode == FVX_GEMM_GEGLU && d.ld_gu >= 2 * d.n &&
                             d.ld_gu % 8 == 0 && aligned16(d.gu_out)),
               FVX_ERR_ARG, "gemm: gu_out needs GEGLU mode, ld_gu >= 2 n (a multiple of 8) "

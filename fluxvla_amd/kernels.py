@@ -563,14 +563,17 @@ def gemm_geglu(a, gate_w, up_w, out=None, rownorm_eps=None, split_k=0,
 def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
                   head_dim, rownorm_eps=None, row_group=0, row_group_stride=0,
                   split_k=0, v_ld=None, ss_in=None, a8=None, a_scale=None,
-                  bias_f32=None):
+                  bias_f32=None, k_t_out=None, kt_ld=None, v_rows_out=None):
     """[q|k|v] = a @ w_qkv^T with pair-interleaved RoPE on q and k.
 
     rope: fp32 [max_pos, head_dim/2, 2] (cos, sin); positions: int32 [M].
     k_out rows are remapped with (row_group, row_group_stride).  v_out is
     row-major like k_out, or -- with ``v_ld`` given -- the transposed value
     cache: element (m, d) at v_out[(m // row_group * head_dim + d) * v_ld +
-    m % row_group] (v_out may be a view offset to the first token column)."""
+    m % row_group] (v_out may be a view offset to the first token column).
+    With a transposed v_out, ``k_t_out`` (+ ``kt_ld``) also receives the
+    keys transposed the same way and ``v_rows_out`` the values row-major
+    with k_out's rows (fvx_gemm_desc.k_t_out / v_rows_out)."""
     d = _gemm_desc(a, w_qkv)
     _check(rope, 'rope', dtype=torch.float32)
     _check(positions, 'positions', dtype=torch.int32)
@@ -586,6 +589,12 @@ def gemm_qkv_rope(a, w_qkv, rope, positions, q_out, k_out, v_out, n_q_heads,
         d.v_out, d.ldv = v_out.data_ptr(), _rows_ld(v_out, 'v_out')[1]
     else:
         d.v_out, d.ldv, d.v_transposed = v_out.data_ptr(), int(v_ld), 1
+    if k_t_out is not None:
+        _check(k_t_out, 'k_t_out', contiguous=False)
+        d.k_t_out, d.ld_kt = k_t_out.data_ptr(), int(kt_ld)
+    if v_rows_out is not None:
+        _check(v_rows_out, 'v_rows_out', contiguous=False)
+        d.v_rows_out, d.ld_vr = v_rows_out.data_ptr(), _rows_ld(v_rows_out, 'v_rows_out')[1]
     d.n_q_heads, d.head_dim = n_q_heads, head_dim
     _set_a_scale(d, a_scale, bias_f32)
     _set_ss(d, rownorm_eps, ss_in)

@@ -192,10 +192,13 @@ class ExpertVJP:
                 a, rn = v['xn'], None
             else:
                 a, rn = (f['x'] if f else x), cfg.rms_eps
+            # the suffix keys / values also into the attention backward's
+            # transposed-key and row-major value copies
             K.gemm_qkv_rope(a, L['qkv_w'], m.rope, b['pos_suf'], Q[i],
                             kc.view(B * T, D)[S:], vc[:, :, S:], H, D,
                             rownorm_eps=rn, row_group=Ss, row_group_stride=T,
-                            v_ld=T)
+                            v_ld=T, k_t_out=v['kT'][i][:, :, S:], kt_ld=T,
+                            v_rows_out=v['vr'][i].view(B * T, D)[S:])
             ctx = v['CTX'][i]
             K.mqa_attention(Q[i].view(B, Ss, H * D), kc[:, :S + Ss], vc,
                             ctx.view(B, Ss, H * D), kgrp=b['kgrp'],
@@ -330,9 +333,7 @@ class ExpertVJP:
                              vr[:, :nk], kT, v['dq'], v['stats'], heads=H,
                              scale=self.scale, kgrp=b['kgrp'],
                              qgrp=b['qgrp_suf'], ds_t=v['ds_t'], p_t=v['p_t'],
-                             key0=S, n_suffix=Ss,
-                             # this step's suffix keys / values into the copies
-                             vt=vc, refresh=(S, Ss))
+                             key0=S, n_suffix=Ss)
         for z in range(B):
             rows = slice(z * Ss, (z + 1) * Ss)
             K.attention_suffix_kv_backward(v['ds_t'][z], v['p_t'][z], q3[z],

@@ -242,6 +242,16 @@ typedef struct fvx_gemm_desc {
    * with it). */
   void* gu_out;
   int64_t ld_gu;
+  /* QKV_ROPE with v_transposed, copies in the other layouts (no
+   * counterpart in the reference; the operands of the attention backward of
+   * guidance RTC with use_vjp): k_t_out (may be NULL) receives the rotated
+   * keys transposed like v_out, element (m, d) at k_t_out[((m / row_group)
+   * * head_dim + d) * ld_kt + m % row_group]; v_rows_out (may be NULL) the
+   * values row-major with k_out's row map and row stride ld_vr. */
+  void* k_t_out;
+  int64_t ld_kt;
+  void* v_rows_out;
+  int64_t ld_vr;
 } fvx_gemm_desc;
 
 /* Library identity / diagnostics. */

@@ -391,3 +391,33 @@ def test_geglu_gemm_keeps_pre_activations(K, cuda, m):
     xn = ad * torch.rsqrt(ad.pow(2).mean(-1, keepdim=True) + 1e-6)
     assert rel_err(gu[:, :n], xn @ wg.double().cpu().t()) <= BF16_TOL
     assert rel_err(gu[:, n:], xn @ wu.double().cpu().t()) <= BF16_TOL
+
+
+@pytest.mark.parametrize('groups', [1, 2])
+def test_qkv_rope_writes_backward_copies(K, cuda, groups):
+    """fvx_gemm_desc.k_t_out / v_rows_out: the QKV + RoPE GEMM with a
+    transposed value cache also writes the keys transposed and the values
+    row-major (the attention backward's operands) -- bitwise the transposes
+    of what it writes to k_out / v_out, at the cache's row groups and gaps,
+    and nothing outside the suffix columns / rows."""
+    announce(f'qkv_rope backward copies groups={groups}')
+    ss, pre, hd, nq, k = 51, 816, 256, 8, 1024
+    T, m = pre + ss, groups * ss
+    a = randn((m, k), 131, std=2.0).to(cuda)
+    w = randn(((nq + 2) * hd, k), 132, std=0.03).to(cuda)
+    pos = torch.arange(pre, pre + ss, dtype=torch.int32).repeat(groups).to(cuda)
+    rope = K.rope_table(T + 8, hd, device=cuda)
+    q = torch.empty(m, nq * hd, dtype=torch.bfloat16, device=cuda)
+    kc = torch.zeros(groups, T, hd, dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros(groups, hd, T, dtype=torch.bfloat16, device=cuda)
+    kt = torch.zeros(groups, hd, T, dtype=torch.bfloat16, device=cuda)
+    vr = torch.zeros(groups, T, hd, dtype=torch.bfloat16, device=cuda)
+    K.gemm_qkv_rope(a, w, rope, pos, q, kc.view(groups * T, hd)[pre:],
+                    vc[:, :, pre:], nq, hd, rownorm_eps=1e-6, row_group=ss,
+                    row_group_stride=T, v_ld=T, k_t_out=kt[:, :, pre:], kt_ld=T,
+                    v_rows_out=vr.view(groups * T, hd)[pre:])
+    assert torch.equal(kt, kc.transpose(1, 2))
+    assert torch.equal(vr, vc.transpose(1, 2))
+    assert kc[:, pre:].abs().max().item() > 0
+    assert kc[:, :pre].abs().max().item() == 0.0
+    assert vc[:, :, :pre].abs().max().item() == 0.0
